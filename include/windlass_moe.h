@@ -1,0 +1,180 @@
+/*
+ * windlass_moe.h — C ABI of the MI355X (gfx950) MoE-layer hot path.
+ *
+ * This is the drop-in boundary for windlass's MoE layer: the functions below
+ * replace, one for one, the C++ entry points the reference binds for this
+ * path. Every pointer argument named d_* is a device pointer; sizes are in
+ * elements unless stated. No torch or HIP C++ types appear in the signatures:
+ * the stream is passed as an opaque `void*` holding a hipStream_t (NULL = the
+ * null stream).
+ *
+ * Error model: every call returns a wl_status. WL_OK is 0. On failure the
+ * context keeps a human-readable message, read with wl_last_error(). Nothing
+ * in this library calls exit() or abort() (the reference exits on CUDA and
+ * I/O errors: src/glm_expert_cache.cuh:91-95, src/glm_loader.cuh:24-26).
+ *
+ * Threading: one host thread per context. All device work of a call is
+ * enqueued on the stream passed to that call, in call order.
+ */
+#ifndef WINDLASS_MOE_H
+#define WINDLASS_MOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum wl_status {
+    WL_OK = 0,
+    WL_ERR_INVALID = 1,      /* bad argument or unsupported shape */
+    WL_ERR_HIP = 2,          /* a HIP runtime call failed */
+    WL_ERR_OOM = 3,          /* device or pinned-host allocation failed */
+    WL_ERR_NOT_RESIDENT = 4, /* a routed expert has no HBM slot bound */
+    WL_ERR_STATE = 5,        /* call made in the wrong state (e.g. layer not set) */
+    WL_ERR_DEVICE = 6,       /* the device kernel reported an error (see wl_check_error) */
+    WL_ERR_IO = 7            /* host backing store read failed */
+} wl_status;
+
+/* MoE fields of glm::Config (reference src/glm_loader.cuh:35-47). */
+typedef struct wl_moe_config {
+    uint32_t hidden;             /* hidden_size                 6144 */
+    uint32_t moe_inter;          /* moe_intermediate_size       2048 */
+    uint32_t n_routed_experts;   /* n_routed_experts             256 */
+    uint32_t n_experts_per_tok;  /* num_experts_per_tok            8 (<= WL_MAX_TOPK) */
+    uint32_t n_shared;           /* n_shared_experts               1 */
+    uint32_t n_layers;           /* MoE layers served by the context  */
+    float    routed_scaling;     /* routed_scaling_factor        2.5 */
+    int32_t  norm_topk_prob;     /* 1: renormalise the top-k weights */
+    float    rms_eps;            /* rms_norm_eps                1e-5 */
+} wl_moe_config;
+
+#define WL_MAX_TOPK 32           /* reference MAX_TOPK, src/glm_loader.cuh:86 */
+
+/* Sub-offsets inside one packed expert block (reference ExpertLayout,
+ * src/glm_layer_runner.cuh:52-72; tools/repack_experts_glm.py:46-55):
+ * gate_w | gate_s | up_w | up_s | down_w | down_s, MXFP4 nibbles (low nibble =
+ * even column) with one E8M0 scale byte per 32 values. */
+typedef struct wl_expert_layout {
+    size_t gw_off, gw_len, gs_off, gs_len;
+    size_t uw_off, uw_len, us_off, us_len;
+    size_t dw_off, dw_len, ds_off, ds_len;
+    size_t total;                /* 20,054,016 at hidden 6144 / inter 2048 */
+} wl_expert_layout;
+
+/* Replaces ExpertLayout::from(Config) (src/glm_layer_runner.cuh:60-72). */
+wl_status wl_expert_layout_of(const wl_moe_config* cfg, uint32_t inter, wl_expert_layout* out);
+
+typedef struct wl_ctx wl_ctx;
+
+/* Creates a context on the current HIP device. Replaces the MoE part of
+ * glm::alloc_scratch (src/glm_loader.cuh:363-450): all per-layer scratch
+ * (norm, logits, top-k, SwiGLU intermediates, partial sums, counters) is owned
+ * by the context. */
+wl_status wl_create(const wl_moe_config* cfg, wl_ctx** out);
+void      wl_destroy(wl_ctx* ctx);
+const char* wl_last_error(const wl_ctx* ctx);
+
+/* Shared-expert storage formats for wl_set_layer. */
+#define WL_SHARED_BF16  0   /* [gate SI*H | up SI*H | down H*SI] bf16, row-major */
+#define WL_SHARED_MXFP4 1   /* one packed block in wl_expert_layout order, inter = SI */
+
+/* Binds the non-expert weights of MoE layer `layer` (0-based within the
+ * context). Pointers are caller-owned and must stay valid while the layer is
+ * run. Replaces the MoE fields of glm::LayerWeights (src/glm_loader.cuh:
+ * 259-339): router_w [E,H] bf16, router_bias [E] f32 (e_score_correction_bias,
+ * kept f32 on purpose), post_attn_ln [H] bf16 (NULL = all ones), shared expert
+ * block as above. */
+wl_status wl_set_layer(wl_ctx* ctx, uint32_t layer, const uint16_t* d_router_w,
+                       const float* d_router_bias, const uint16_t* d_post_attn_ln,
+                       const void* d_shared, int32_t shared_dtype);
+
+/* ---- HBM slot table (replaces the pointer-returning ExpertSource::get of a
+ * fully resident model, src/glm_layer_runner.cuh:34-48) ---------------------
+ * The device keeps a table slot_of[layer][expert] -> block pointer, and the
+ * decode kernel resolves routed ids through it on the device, so no host
+ * round-trip (src/glm_layer_runner.cuh:393-396) is needed when every expert
+ * of the layer is bound. */
+wl_status wl_slot_bind(wl_ctx* ctx, uint32_t layer, uint32_t expert, const uint8_t* d_block);
+wl_status wl_slot_unbind(wl_ctx* ctx, uint32_t layer, uint32_t expert);
+/* Allocates a context-owned pool of n_slots expert blocks (one hipMalloc, like
+ * ExpertCache's pool, src/glm_expert_cache.cuh:150-156). */
+wl_status wl_slot_pool_create(wl_ctx* ctx, uint32_t n_slots);
+wl_status wl_slot_pool_ptr(wl_ctx* ctx, uint32_t slot, uint8_t** d_block);
+
+/* ---- the MoE layer ------------------------------------------------------
+ * Replaces glm::run_moe (src/glm_layer_runner.cuh:352-443) for a resident
+ * layer: post-attention RMSNorm -> router GEMV -> sigmoid + bias -> top-k ->
+ * renorm -> x routed_scaling -> K MXFP4 SwiGLU experts -> shared expert ->
+ * out = sum_k w_k e_k + shared. d_hidden [H] f32 is the pre-norm residual
+ * stream; d_out [H] f32 receives the block output WITHOUT the residual and must
+ * not alias d_hidden. Returns WL_ERR_NOT_RESIDENT if any expert of the layer
+ * is unbound. */
+wl_status wl_run_moe(wl_ctx* ctx, uint32_t layer, const float* d_hidden, float* d_out,
+                     void* stream);
+
+/* Same layer with the residual fused: d_out = d_resid + moe(d_hidden). Used
+ * by the decode chain (reference run_layer's residual_add,
+ * src/glm_layer_runner.cuh:675). d_out must alias neither input. */
+wl_status wl_run_moe_residual(wl_ctx* ctx, uint32_t layer, const float* d_hidden,
+                              const float* d_resid, float* d_out, void* stream);
+
+/* n_layers consecutive layers starting at first_layer, h <- h + moe(h) per
+ * layer (the MoE half of run_chain's per-layer loop, src/glm_layer_runner.cuh:
+ * 1065-1068). d_h [H] is updated in place; d_tmp [H] is caller scratch. */
+wl_status wl_run_chain(wl_ctx* ctx, uint32_t first_layer, uint32_t n_layers, float* d_h,
+                       float* d_tmp, void* stream);
+
+/* Device pointers to the last layer's intermediates (the substeps
+ * test_glm_chain reads through SubstepHook, src/test_glm_chain.cu:434-441). */
+typedef struct wl_taps_out {
+    const float*   norm;     /* [H]  post_attention_layernorm output */
+    const float*   logits;   /* [E]  router logits */
+    const int32_t* topk_idx; /* [K]  selected experts, descending biased score */
+    const float*   topk_w;   /* [K]  routing weights */
+    const float*   mid;      /* [K, I] routed SwiGLU outputs */
+    const float*   shared;   /* [H]  shared expert output */
+} wl_taps_out;
+wl_status wl_taps(wl_ctx* ctx, wl_taps_out* out);
+
+/* Synchronises `stream`, then returns WL_ERR_DEVICE (and clears the flag) if a
+ * kernel of this context reported an error since the last check. */
+wl_status wl_check_error(wl_ctx* ctx, void* stream);
+
+/* Execution schedule of wl_run_moe: WL_SCHED_FUSED runs one persistent
+ * task-queue kernel per layer; WL_SCHED_PHASED runs the same tasks as three
+ * stream-ordered launches. Both compute identical results. */
+#define WL_SCHED_FUSED  0
+#define WL_SCHED_PHASED 1
+wl_status wl_set_schedule(wl_ctx* ctx, int32_t sched);
+
+/* ---- single-expert building blocks ---------------------------------------
+ * y[N] = W . x for MXFP4 W ([N,K/2] packed nibbles + [N,K/32] E8M0 scales) and
+ * f32 x [K]. Replaces launch_dequant_matvec_mxfp4 (src/glm_kernels.cuh:104-110).
+ * Requires N % 16 == 0, K % 128 == 0, K <= 16384. */
+wl_status wl_dequant_matvec_mxfp4(const uint8_t* d_W, const uint8_t* d_S, const float* d_x, float* d_y,
+                                  uint32_t N, uint32_t K, void* stream);
+
+/* One routed expert applied to one position, without the routing weight:
+ * y = down(silu(gate x) * up x), d_block in wl_expert_layout order, x f32 [H],
+ * y f32 [H] and, if d_y_bf16 is not NULL, its bf16 (round-to-nearest-even)
+ * copy. The per-expert sequence of run_moe (3 x dequant_matvec_mxfp4 +
+ * silu_mul, src/glm_layer_runner.cuh:424-427) and expert_slot
+ * (tools/ref_glm_chain.py:679-685). Uses the context's scratch. */
+wl_status wl_expert_ffn(wl_ctx* ctx, const uint8_t* d_block, const float* d_x, float* d_y,
+                        uint16_t* d_y_bf16, void* stream);
+
+/* ---- synthetic weights (test and benchmark inputs; no reference
+ * counterpart: the reference loads real checkpoints) -----------------------
+ * Fills one expert block with the counter-based generator: packed weight
+ * bytes = bytes of mix32(mix32(i ^ salt_r) ^ key), scale bytes = 118 +
+ * (mix32(...) % 9), key = f(seed, layer, expert). The CPU oracle regenerates
+ * the same bytes. */
+wl_status wl_synth_expert(const wl_moe_config* cfg, uint32_t inter, uint32_t seed,
+                          uint32_t layer, uint32_t expert, uint8_t* d_block, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* WINDLASS_MOE_H */

@@ -1,0 +1,51 @@
+"""Builds a synthetic MoE model on the device through the C ABI (test and
+benchmark helper). Routed experts are filled on the device by
+wl_synth_expert; dense tensors come from oracle/synth.py (numpy) so the
+oracle sees the same values."""
+import numpy as np
+
+from oracle import synth
+from windlass_amd import hip, moe
+
+
+class DeviceModel:
+    def __init__(self, cfg, seed, n_layers=1, ln_weights=None, bias_offset=None, layer_seeds=None):
+        self.c = dict(cfg)
+        self.seed = seed
+        self.L = n_layers
+        H, I, E = cfg["hidden"], cfg["moe_inter"], cfg["n_routed_experts"]
+        self.SI = I * cfg.get("n_shared", 1)
+        self.cfg = moe.make_config(hidden=H, moe_inter=I, n_routed_experts=E,
+                                   n_experts_per_tok=cfg["n_experts_per_tok"],
+                                   n_shared=cfg.get("n_shared", 1), n_layers=n_layers,
+                                   routed_scaling=cfg.get("routed_scaling", 2.5),
+                                   norm_topk_prob=cfg.get("norm_topk_prob", True),
+                                   rms_eps=cfg.get("rms_eps", 1e-5))
+        self.ctx = moe.Context(self.cfg)
+        self.ctx.slot_pool_create(n_layers * E)
+        self.dense, self.bufs = [], []
+        for l in range(n_layers):
+            for e in range(E):
+                p = self.ctx.slot_pool_ptr(l * E + e)
+                moe.synth_expert(self.cfg, seed, l, e, p)
+                self.ctx.slot_bind(l, e, p)
+            d = synth.dense_layer(H, E, self.SI, seed, l)
+            if bias_offset is not None:
+                d["bias"] = (d["bias"] + bias_offset).astype(np.float32)
+            self.dense.append(d)
+            rw = hip.DeviceBuffer.from_array(d["router_w"])
+            bb = hip.DeviceBuffer.from_array(d["bias"])
+            sb = hip.DeviceBuffer.from_array(d["shared_block"])
+            lw = None
+            if ln_weights is not None:
+                lw = hip.DeviceBuffer.from_array(ln_weights[l])
+            self.bufs.append((rw, bb, sb, lw))
+            self.ctx.set_layer(l, rw.ptr, bb.ptr, lw.ptr if lw else None, sb.ptr)
+        hip.synchronize()
+
+    def oracle_cfg(self):
+        return self.c
+
+
+def make_io(H):
+    return hip.DeviceBuffer(4 * H), hip.DeviceBuffer(4 * H)

@@ -1,0 +1,445 @@
+// moe_host.cpp — the C ABI of include/windlass_moe.h: context, layer binding,
+// the HBM slot table and the launch schedule of the decode layer.
+//
+// Reference call surface this replaces: glm::run_moe + glm::ExpertSource +
+// glm::ExpertLayout (src/glm_layer_runner.cuh:34-72,352-443) and the MoE part of
+// glm::alloc_scratch (src/glm_loader.cuh:363-450).
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "../../include/windlass_moe.h"
+#include "internal.h"
+
+struct LayerState {
+    const uint16_t* router_w = nullptr;
+    const float* bias = nullptr;
+    const uint16_t* ln = nullptr;
+    const void* shared = nullptr;
+    int32_t shared_dtype = WL_SHARED_BF16;
+    bool set = false;
+};
+
+struct wl_ctx {
+    wl_moe_config cfg{};
+    wl_expert_layout lay{};
+    uint32_t SI = 0;
+    int device = 0;
+    int n_cu = 0;
+    int occ = 1;
+    int32_t sched = WL_SCHED_FUSED;
+    std::vector<LayerState> layers;
+    std::vector<const uint8_t*> h_slot;   // [L*E]
+    std::vector<uint32_t> n_bound;        // bound experts per layer
+    const uint8_t** d_slot = nullptr;     // [L*E]
+    wl::DecodeArgs* d_largs = nullptr;    // [L] per-layer kernel records
+    // scratch
+    float* norm = nullptr;
+    float* logits = nullptr;
+    int32_t* idx = nullptr;
+    float* topw = nullptr;
+    const uint8_t** sel = nullptr;
+    float* rmid = nullptr;
+    uint16_t* rmid_p = nullptr;
+    float* smid = nullptr;
+    uint16_t* smid_p = nullptr;
+    float* shared_out = nullptr;
+    float* edown = nullptr;
+    float* part_r = nullptr;
+    float* part_s = nullptr;
+    uint32_t* ctr = nullptr;
+    size_t n_ctr = 0;
+    // context-owned slot pool
+    uint8_t* pool = nullptr;
+    uint32_t pool_slots = 0;
+    std::vector<void*> allocs;
+    std::string err;
+};
+
+namespace {
+
+wl_status fail(wl_ctx* c, wl_status s, const char* fmt, ...) __attribute__((format(printf, 3, 4)));
+wl_status fail(wl_ctx* c, wl_status s, const char* fmt, ...) {
+    if (c) {
+        char buf[512];
+        va_list ap;
+        va_start(ap, fmt);
+        vsnprintf(buf, sizeof(buf), fmt, ap);
+        va_end(ap);
+        c->err = buf;
+    }
+    return s;
+}
+
+wl_status hip_fail(wl_ctx* c, hipError_t e, const char* what) {
+    return fail(c, WL_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+template <typename T>
+wl_status dalloc(wl_ctx* c, T** p, size_t bytes) {
+    void* q = nullptr;
+    hipError_t e = hipMalloc(&q, bytes ? bytes : 16);
+    if (e != hipSuccess) return fail(c, WL_ERR_OOM, "hipMalloc(%zu): %s", bytes, hipGetErrorString(e));
+    c->allocs.push_back(q);
+    *p = (T*)q;
+    return WL_OK;
+}
+
+wl_status validate_cfg(const wl_moe_config* cfg, wl_ctx* c) {
+    if (!cfg) return fail(c, WL_ERR_INVALID, "config is null");
+    const uint32_t H = cfg->hidden, I = cfg->moe_inter, E = cfg->n_routed_experts,
+                   K = cfg->n_experts_per_tok;
+    if (H == 0 || H % 128) return fail(c, WL_ERR_INVALID, "hidden=%u must be a positive multiple of 128", H);
+    if (I == 0 || I % 128) return fail(c, WL_ERR_INVALID, "moe_inter=%u must be a positive multiple of 128", I);
+    if (E == 0 || E % 16 || E > 4096) return fail(c, WL_ERR_INVALID, "n_routed_experts=%u must be a multiple of 16 in [16,4096]", E);
+    if (K == 0 || K > WL_MAX_TOPK || K > E) return fail(c, WL_ERR_INVALID, "n_experts_per_tok=%u must be in [1,min(%d,E)]", K, WL_MAX_TOPK);
+    if (cfg->n_shared == 0 || cfg->n_shared > 16) return fail(c, WL_ERR_INVALID, "n_shared=%u must be in [1,16]", cfg->n_shared);
+    if (cfg->n_layers == 0 || cfg->n_layers > 4096) return fail(c, WL_ERR_INVALID, "n_layers=%u must be in [1,4096]", cfg->n_layers);
+    if (H > 16384) return fail(c, WL_ERR_INVALID, "hidden=%u exceeds 16384", H);
+    return WL_OK;
+}
+
+// The device-side launch record of one layer: its weights, its slot table
+// row, the context scratch and the shapes.
+wl::DecodeArgs layer_record(const wl_ctx* c, uint32_t layer) {
+    const LayerState& L = c->layers[layer];
+    const uint32_t H = c->cfg.hidden, E = c->cfg.n_routed_experts, SI = c->SI;
+    wl::DecodeArgs a{};
+    a.ln_w = L.ln;
+    a.router_w = L.router_w;
+    a.bias = L.bias;
+    const uint16_t* sh = (const uint16_t*)L.shared;
+    a.sh_gate = sh;
+    a.sh_up = sh + (size_t)SI * H;
+    a.sh_down = sh + (size_t)2 * SI * H;
+    a.slot_tab = c->d_slot + (size_t)layer * E;
+    a.norm = c->norm;
+    a.logits = c->logits;
+    a.idx = c->idx;
+    a.topw = c->topw;
+    a.sel = c->sel;
+    a.rmid = c->rmid;
+    a.rmid_p = c->rmid_p;
+    a.smid = c->smid;
+    a.smid_p = c->smid_p;
+    a.shared_out = c->shared_out;
+    a.edown = c->edown;
+    a.part_r = c->part_r;
+    a.part_s = c->part_s;
+    a.ctr = c->ctr;
+    a.gw_off = c->lay.gw_off;
+    a.gs_off = c->lay.gs_off;
+    a.uw_off = c->lay.uw_off;
+    a.us_off = c->lay.us_off;
+    a.dw_off = c->lay.dw_off;
+    a.ds_off = c->lay.ds_off;
+    a.H = H;
+    a.I = c->cfg.moe_inter;
+    a.E = E;
+    a.K = c->cfg.n_experts_per_tok;
+    a.SI = SI;
+    a.eps = c->cfg.rms_eps;
+    a.scaling = c->cfg.routed_scaling;
+    a.norm_topk = c->cfg.norm_topk_prob ? 1 : 0;
+    return a;
+}
+
+}  // namespace
+
+extern "C" {
+
+wl_status wl_expert_layout_of(const wl_moe_config* cfg, uint32_t inter, wl_expert_layout* out) {
+    if (!cfg || !out) return WL_ERR_INVALID;
+    const size_t H = cfg->hidden, I = inter ? inter : cfg->moe_inter;
+    if (H % 32 || I % 32) return WL_ERR_INVALID;
+    wl_expert_layout l{};
+    size_t o = 0;
+    l.gw_off = o; l.gw_len = I * H / 2;  o += l.gw_len;
+    l.gs_off = o; l.gs_len = I * H / 32; o += l.gs_len;
+    l.uw_off = o; l.uw_len = I * H / 2;  o += l.uw_len;
+    l.us_off = o; l.us_len = I * H / 32; o += l.us_len;
+    l.dw_off = o; l.dw_len = H * I / 2;  o += l.dw_len;
+    l.ds_off = o; l.ds_len = H * I / 32; o += l.ds_len;
+    l.total = o;
+    *out = l;
+    return WL_OK;
+}
+
+wl_status wl_create(const wl_moe_config* cfg, wl_ctx** out) {
+    if (!out) return WL_ERR_INVALID;
+    *out = nullptr;
+    wl_status s = validate_cfg(cfg, nullptr);
+    if (s != WL_OK) return s;
+    wl_ctx* c = new wl_ctx();
+    c->cfg = *cfg;
+    c->SI = cfg->moe_inter * cfg->n_shared;
+    wl_expert_layout_of(cfg, 0, &c->lay);
+    hipError_t e = hipGetDevice(&c->device);
+    if (e != hipSuccess) { delete c; return WL_ERR_HIP; }
+    hipDeviceProp_t prop;
+    e = hipGetDeviceProperties(&prop, c->device);
+    if (e != hipSuccess) { delete c; return WL_ERR_HIP; }
+    c->n_cu = prop.multiProcessorCount;
+    const uint32_t H = cfg->hidden, I = cfg->moe_inter, E = cfg->n_routed_experts,
+                   K = cfg->n_experts_per_tok, L = cfg->n_layers, SI = c->SI;
+    int occ = 0;
+    if (wl::decode_occupancy(H, E, &occ) != 0 || occ < 1) occ = 1;
+    const char* env = getenv("WL_DECODE_WG_PER_CU");
+    if (env && atoi(env) > 0) occ = atoi(env) < occ ? atoi(env) : occ;
+    else if (occ > 2) occ = 2;
+    c->occ = occ;
+
+    c->layers.resize(L);
+    c->h_slot.assign((size_t)L * E, nullptr);
+    c->n_bound.assign(L, 0);
+    c->n_ctr = wl::C_FIXED + E / 16 + SI / 16 + H / 64;
+    if ((s = dalloc(c, &c->d_slot, sizeof(void*) * (size_t)L * E)) != WL_OK ||
+        (s = dalloc(c, &c->d_largs, sizeof(wl::DecodeArgs) * (size_t)L)) != WL_OK ||
+        (s = dalloc(c, &c->norm, 4 * (size_t)H)) != WL_OK ||
+        (s = dalloc(c, &c->logits, 4 * (size_t)E)) != WL_OK ||
+        (s = dalloc(c, &c->idx, 4 * (size_t)WL_MAX_TOPK)) != WL_OK ||
+        (s = dalloc(c, &c->topw, 4 * (size_t)WL_MAX_TOPK)) != WL_OK ||
+        (s = dalloc(c, &c->sel, sizeof(void*) * (size_t)WL_MAX_TOPK)) != WL_OK ||
+        (s = dalloc(c, &c->rmid, 4 * (size_t)K * I)) != WL_OK ||
+        (s = dalloc(c, &c->rmid_p, 2 * 3 * (size_t)K * I)) != WL_OK ||
+        (s = dalloc(c, &c->smid, 4 * (size_t)SI)) != WL_OK ||
+        (s = dalloc(c, &c->smid_p, 2 * 3 * (size_t)SI)) != WL_OK ||
+        (s = dalloc(c, &c->shared_out, 4 * (size_t)H)) != WL_OK ||
+        (s = dalloc(c, &c->edown, 4 * (size_t)K * H)) != WL_OK ||
+        (s = dalloc(c, &c->part_r, 4 * (size_t)(E / 16) * 4 * 16)) != WL_OK ||
+        (s = dalloc(c, &c->part_s, 4 * (size_t)(SI / 16) * 4 * 32)) != WL_OK ||
+        (s = dalloc(c, &c->ctr, 4 * c->n_ctr)) != WL_OK) {
+        wl_destroy(c);
+        return s;
+    }
+    e = hipMemset(c->d_slot, 0, sizeof(void*) * (size_t)L * E);
+    if (e == hipSuccess) e = hipMemset(c->ctr, 0, 4 * c->n_ctr);
+    if (e == hipSuccess) e = hipMemset(c->sel, 0, sizeof(void*) * WL_MAX_TOPK);
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (e != hipSuccess) { wl_destroy(c); return WL_ERR_HIP; }
+    *out = c;
+    return WL_OK;
+}
+
+void wl_destroy(wl_ctx* c) {
+    if (!c) return;
+    for (void* p : c->allocs) hipFree(p);
+    delete c;
+}
+
+const char* wl_last_error(const wl_ctx* c) { return c ? c->err.c_str() : "null context"; }
+
+wl_status wl_set_layer(wl_ctx* c, uint32_t layer, const uint16_t* d_router_w, const float* d_router_bias,
+                       const uint16_t* d_post_attn_ln, const void* d_shared, int32_t shared_dtype) {
+    if (!c) return WL_ERR_INVALID;
+    if (layer >= c->cfg.n_layers) return fail(c, WL_ERR_INVALID, "layer %u >= n_layers %u", layer, c->cfg.n_layers);
+    if (!d_router_w || !d_router_bias || !d_shared)
+        return fail(c, WL_ERR_INVALID, "router weight, router bias and shared expert are required");
+    if (shared_dtype != WL_SHARED_BF16)
+        return fail(c, WL_ERR_INVALID, "shared_dtype %d not supported by this build (bf16 only)", shared_dtype);
+    LayerState& L = c->layers[layer];
+    L.router_w = d_router_w;
+    L.bias = d_router_bias;
+    L.ln = d_post_attn_ln;
+    L.shared = d_shared;
+    L.shared_dtype = shared_dtype;
+    const wl::DecodeArgs a = layer_record(c, layer);
+    hipError_t e = hipMemcpy(c->d_largs + layer, &a, sizeof(a), hipMemcpyHostToDevice);
+    if (e != hipSuccess) return hip_fail(c, e, "layer record upload");
+    L.set = true;
+    return WL_OK;
+}
+
+wl_status wl_slot_bind(wl_ctx* c, uint32_t layer, uint32_t expert, const uint8_t* d_block) {
+    if (!c) return WL_ERR_INVALID;
+    if (layer >= c->cfg.n_layers || expert >= c->cfg.n_routed_experts)
+        return fail(c, WL_ERR_INVALID, "slot (%u,%u) out of range", layer, expert);
+    if (!d_block) return fail(c, WL_ERR_INVALID, "null block for (%u,%u)", layer, expert);
+    const size_t i = (size_t)layer * c->cfg.n_routed_experts + expert;
+    if (!c->h_slot[i]) c->n_bound[layer]++;
+    c->h_slot[i] = d_block;
+    hipError_t e = hipMemcpy(c->d_slot + i, &c->h_slot[i], sizeof(void*), hipMemcpyHostToDevice);
+    if (e != hipSuccess) return hip_fail(c, e, "slot table update");
+    return WL_OK;
+}
+
+wl_status wl_slot_unbind(wl_ctx* c, uint32_t layer, uint32_t expert) {
+    if (!c) return WL_ERR_INVALID;
+    if (layer >= c->cfg.n_layers || expert >= c->cfg.n_routed_experts)
+        return fail(c, WL_ERR_INVALID, "slot (%u,%u) out of range", layer, expert);
+    const size_t i = (size_t)layer * c->cfg.n_routed_experts + expert;
+    if (c->h_slot[i]) c->n_bound[layer]--;
+    c->h_slot[i] = nullptr;
+    hipError_t e = hipMemcpy(c->d_slot + i, &c->h_slot[i], sizeof(void*), hipMemcpyHostToDevice);
+    if (e != hipSuccess) return hip_fail(c, e, "slot table update");
+    return WL_OK;
+}
+
+wl_status wl_slot_pool_create(wl_ctx* c, uint32_t n_slots) {
+    if (!c) return WL_ERR_INVALID;
+    if (c->pool) return fail(c, WL_ERR_STATE, "slot pool already created");
+    if (n_slots == 0) return fail(c, WL_ERR_INVALID, "n_slots must be positive");
+    const size_t bytes = (size_t)n_slots * c->lay.total;
+    void* p = nullptr;
+    hipError_t e = hipMalloc(&p, bytes);
+    if (e != hipSuccess) return fail(c, WL_ERR_OOM, "slot pool of %u x %zu B: %s", n_slots, c->lay.total, hipGetErrorString(e));
+    c->allocs.push_back(p);
+    c->pool = (uint8_t*)p;
+    c->pool_slots = n_slots;
+    return WL_OK;
+}
+
+wl_status wl_slot_pool_ptr(wl_ctx* c, uint32_t slot, uint8_t** d_block) {
+    if (!c || !d_block) return WL_ERR_INVALID;
+    if (!c->pool) return fail(c, WL_ERR_STATE, "no slot pool");
+    if (slot >= c->pool_slots) return fail(c, WL_ERR_INVALID, "slot %u >= %u", slot, c->pool_slots);
+    *d_block = c->pool + (size_t)slot * c->lay.total;
+    return WL_OK;
+}
+
+static wl_status run_layer(wl_ctx* c, uint32_t layer, const float* d_hidden, const float* d_resid,
+                           float* d_out, void* stream) {
+    if (!c) return WL_ERR_INVALID;
+    if (layer >= c->cfg.n_layers) return fail(c, WL_ERR_INVALID, "layer %u >= n_layers %u", layer, c->cfg.n_layers);
+    const LayerState& L = c->layers[layer];
+    if (!L.set) return fail(c, WL_ERR_STATE, "layer %u has no weights (wl_set_layer)", layer);
+    if (!d_hidden || !d_out) return fail(c, WL_ERR_INVALID, "null hidden/out");
+    if (d_out == d_hidden || (d_resid && d_out == d_resid))
+        return fail(c, WL_ERR_INVALID, "d_out must not alias the inputs");
+    const uint32_t H = c->cfg.hidden, I = c->cfg.moe_inter, E = c->cfg.n_routed_experts,
+                   K = c->cfg.n_experts_per_tok, SI = c->SI;
+    if (c->n_bound[layer] != E)
+        return fail(c, WL_ERR_NOT_RESIDENT, "layer %u has %u of %u experts bound", layer, c->n_bound[layer], E);
+
+    wl::DecodeDyn dyn{};
+    dyn.hidden = d_hidden;
+    dyn.resid = d_resid;
+    dyn.out = d_out;
+
+    const wl::TaskMap tm = wl::TaskMap::make(H, I, E, K, SI);
+    const uint32_t slots = (uint32_t)(c->n_cu * c->occ);
+    auto launch = [&](uint32_t lo, uint32_t hi, int wait, int tap) -> wl_status {
+        dyn.task_lo = lo;
+        dyn.task_hi = hi;
+        dyn.wait_deps = wait;
+        dyn.write_norm_tap = tap;
+        const uint32_t n = hi - lo;
+        const uint32_t grid = n < slots ? n : slots;
+        int e = wl::launch_decode(c->d_largs + layer, dyn, H, E, grid, stream);
+        if (e != 0) return hip_fail(c, (hipError_t)e, "decode launch");
+        return WL_OK;
+    };
+    if (c->sched == WL_SCHED_FUSED) return launch(0, tm.total, 1, 1);
+    wl_status s;
+    if ((s = launch(0, tm.oRG, 0, 1)) != WL_OK) return s;
+    if ((s = launch(tm.oRG, tm.oRD, 0, 0)) != WL_OK) return s;
+    return launch(tm.oRD, tm.total, 0, 0);
+}
+
+wl_status wl_run_moe(wl_ctx* c, uint32_t layer, const float* d_hidden, float* d_out, void* stream) {
+    return run_layer(c, layer, d_hidden, nullptr, d_out, stream);
+}
+
+wl_status wl_run_moe_residual(wl_ctx* c, uint32_t layer, const float* d_hidden, const float* d_resid,
+                              float* d_out, void* stream) {
+    if (!d_resid) return fail(c, WL_ERR_INVALID, "null residual");
+    return run_layer(c, layer, d_hidden, d_resid, d_out, stream);
+}
+
+wl_status wl_run_chain(wl_ctx* c, uint32_t first_layer, uint32_t n_layers, float* d_h, float* d_tmp,
+                       void* stream) {
+    if (!c) return WL_ERR_INVALID;
+    if (!d_h || !d_tmp || d_h == d_tmp) return fail(c, WL_ERR_INVALID, "chain needs two distinct buffers");
+    if (first_layer + (uint64_t)n_layers > c->cfg.n_layers)
+        return fail(c, WL_ERR_INVALID, "layers [%u,%u) exceed n_layers %u", first_layer,
+                    first_layer + n_layers, c->cfg.n_layers);
+    float* cur = d_h;
+    float* nxt = d_tmp;
+    for (uint32_t l = 0; l < n_layers; l++) {
+        wl_status s = run_layer(c, first_layer + l, cur, cur, nxt, stream);
+        if (s != WL_OK) return s;
+        float* t = cur;
+        cur = nxt;
+        nxt = t;
+    }
+    if (cur != d_h) {
+        hipError_t e = hipMemcpyAsync(d_h, cur, 4 * (size_t)c->cfg.hidden, hipMemcpyDeviceToDevice,
+                                      (hipStream_t)stream);
+        if (e != hipSuccess) return hip_fail(c, e, "chain copy-back");
+    }
+    return WL_OK;
+}
+
+wl_status wl_taps(wl_ctx* c, wl_taps_out* out) {
+    if (!c || !out) return WL_ERR_INVALID;
+    out->norm = c->norm;
+    out->logits = c->logits;
+    out->topk_idx = c->idx;
+    out->topk_w = c->topw;
+    out->mid = c->rmid;
+    out->shared = c->shared_out;
+    return WL_OK;
+}
+
+wl_status wl_check_error(wl_ctx* c, void* stream) {
+    if (!c) return WL_ERR_INVALID;
+    hipError_t e = hipStreamSynchronize((hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(c, e, "stream synchronize");
+    uint32_t flag = 0;
+    e = hipMemcpy(&flag, c->ctr + wl::C_ERROR, 4, hipMemcpyDeviceToHost);
+    if (e != hipSuccess) return hip_fail(c, e, "error flag read");
+    if (flag) {
+        const uint32_t zero = 0;
+        hipMemcpy(c->ctr + wl::C_ERROR, &zero, 4, hipMemcpyHostToDevice);
+        return fail(c, WL_ERR_DEVICE, "device error bits 0x%x%s%s", flag,
+                    (flag & wl::E_SPIN) ? " [dependency wait expired]" : "",
+                    (flag & wl::E_NOT_RESIDENT) ? " [routed expert not resident]" : "");
+    }
+    return WL_OK;
+}
+
+wl_status wl_set_schedule(wl_ctx* c, int32_t sched) {
+    if (!c) return WL_ERR_INVALID;
+    if (sched != WL_SCHED_FUSED && sched != WL_SCHED_PHASED)
+        return fail(c, WL_ERR_INVALID, "unknown schedule %d", sched);
+    c->sched = sched;
+    return WL_OK;
+}
+
+wl_status wl_dequant_matvec_mxfp4(const uint8_t* d_W, const uint8_t* d_S, const float* d_x, float* d_y,
+                                  uint32_t N, uint32_t K, void* stream) {
+    if (!d_W || !d_S || !d_x || !d_y) return WL_ERR_INVALID;
+    if (N == 0 || N % 16 || K == 0 || K % 128 || K > 16384) return WL_ERR_INVALID;
+    return wl::launch_dequant_matvec(d_W, d_S, d_x, d_y, N, K, stream) == 0 ? WL_OK : WL_ERR_HIP;
+}
+
+wl_status wl_expert_ffn(wl_ctx* c, const uint8_t* d_block, const float* d_x, float* d_y, uint16_t* d_y_bf16,
+                        void* stream) {
+    if (!c) return WL_ERR_INVALID;
+    if (!d_block || !d_x || !d_y) return fail(c, WL_ERR_INVALID, "null block/x/y");
+    int e = wl::launch_expert_ffn(d_block, c->lay.gw_off, c->lay.gs_off, c->lay.uw_off, c->lay.us_off,
+                                  c->lay.dw_off, c->lay.ds_off, d_x, c->cfg.hidden, c->cfg.moe_inter,
+                                  c->rmid, c->rmid_p, d_y, d_y_bf16, stream);
+    if (e != 0) return hip_fail(c, (hipError_t)e, "expert ffn launch");
+    return WL_OK;
+}
+
+wl_status wl_synth_expert(const wl_moe_config* cfg, uint32_t inter, uint32_t seed, uint32_t layer,
+                          uint32_t expert, uint8_t* d_block, void* stream) {
+    if (!cfg || !d_block) return WL_ERR_INVALID;
+    wl_expert_layout l;
+    if (wl_expert_layout_of(cfg, inter, &l) != WL_OK) return WL_ERR_INVALID;
+    if ((cfg->hidden % 128) || ((inter ? inter : cfg->moe_inter) % 128)) return WL_ERR_INVALID;
+    const uint32_t key = wl::synth_key(seed, layer, expert);
+    int e = wl::launch_synth_expert(d_block, l.gw_off, l.gw_len, l.gs_off, l.gs_len, l.uw_off, l.uw_len,
+                                    l.us_off, l.us_len, l.dw_off, l.dw_len, l.ds_off, l.ds_len, key,
+                                    stream);
+    return e == 0 ? WL_OK : WL_ERR_HIP;
+}
+
+}  // extern "C"

@@ -1,0 +1,194 @@
+"""ctypes binding of include/windlass_moe.h.
+
+The MoE path itself is the native library libwindlass_moe.so (gfx950 HIP
+kernels behind a C ABI). This module only marshals arguments; it has no compute
+of its own and no fallback: if the library is missing, loading fails loudly.
+"""
+import ctypes
+import os
+import re
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libwindlass_moe.so")
+HEADER = os.path.join(os.path.dirname(HERE), "include", "windlass_moe.h")
+
+WL_OK = 0
+STATUS = {0: "WL_OK", 1: "WL_ERR_INVALID", 2: "WL_ERR_HIP", 3: "WL_ERR_OOM", 4: "WL_ERR_NOT_RESIDENT",
+          5: "WL_ERR_STATE", 6: "WL_ERR_DEVICE", 7: "WL_ERR_IO"}
+SHARED_BF16, SHARED_MXFP4 = 0, 1
+SCHED_FUSED, SCHED_PHASED = 0, 1
+MAX_TOPK = 32
+
+
+class NativeLibraryMissing(ImportError):
+    pass
+
+
+class WindlassError(RuntimeError):
+    def __init__(self, status, msg):
+        super().__init__(f"{STATUS.get(status, status)}: {msg}")
+        self.status = status
+
+
+class MoeConfig(ctypes.Structure):
+    _fields_ = [("hidden", ctypes.c_uint32), ("moe_inter", ctypes.c_uint32),
+                ("n_routed_experts", ctypes.c_uint32), ("n_experts_per_tok", ctypes.c_uint32),
+                ("n_shared", ctypes.c_uint32), ("n_layers", ctypes.c_uint32),
+                ("routed_scaling", ctypes.c_float), ("norm_topk_prob", ctypes.c_int32),
+                ("rms_eps", ctypes.c_float)]
+
+
+class ExpertLayout(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_size_t) for n in
+                ["gw_off", "gw_len", "gs_off", "gs_len", "uw_off", "uw_len", "us_off", "us_len",
+                 "dw_off", "dw_len", "ds_off", "ds_len", "total"]]
+
+
+class Taps(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_void_p) for n in ["norm", "logits", "topk_idx", "topk_w", "mid", "shared"]]
+
+
+_lib = None
+
+
+def load():
+    """Loads libwindlass_moe.so (raises NativeLibraryMissing if it was not built)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise NativeLibraryMissing(
+            f"{LIB_PATH} is missing: build it with `python -m windlass_amd.build` (there is no fallback path)")
+    lib = ctypes.CDLL(LIB_PATH)
+    vp, u32, i32 = ctypes.c_void_p, ctypes.c_uint32, ctypes.c_int32
+    sig = {
+        "wl_expert_layout_of": [ctypes.POINTER(MoeConfig), u32, ctypes.POINTER(ExpertLayout)],
+        "wl_create": [ctypes.POINTER(MoeConfig), ctypes.POINTER(vp)],
+        "wl_set_layer": [vp, u32, vp, vp, vp, vp, i32],
+        "wl_slot_bind": [vp, u32, u32, vp],
+        "wl_slot_unbind": [vp, u32, u32],
+        "wl_slot_pool_create": [vp, u32],
+        "wl_slot_pool_ptr": [vp, u32, ctypes.POINTER(vp)],
+        "wl_run_moe": [vp, u32, vp, vp, vp],
+        "wl_run_moe_residual": [vp, u32, vp, vp, vp, vp],
+        "wl_run_chain": [vp, u32, u32, vp, vp, vp],
+        "wl_taps": [vp, ctypes.POINTER(Taps)],
+        "wl_check_error": [vp, vp],
+        "wl_set_schedule": [vp, i32],
+        "wl_synth_expert": [ctypes.POINTER(MoeConfig), u32, u32, u32, u32, vp, vp],
+        "wl_dequant_matvec_mxfp4": [vp, vp, vp, vp, u32, u32, vp],
+        "wl_expert_ffn": [vp, vp, vp, vp, vp, vp],
+    }
+    for name, args in sig.items():
+        fn = getattr(lib, name)
+        fn.argtypes = args
+        fn.restype = ctypes.c_int
+    lib.wl_destroy.argtypes = [vp]
+    lib.wl_destroy.restype = None
+    lib.wl_last_error.argtypes = [vp]
+    lib.wl_last_error.restype = ctypes.c_char_p
+    _lib = lib
+    return lib
+
+
+def header_functions(path=HEADER):
+    """Names of every function declared in the public header."""
+    text = open(path).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(wl_[a-z0-9_]+)\s*\(", text)))
+
+
+def make_config(hidden=6144, moe_inter=2048, n_routed_experts=256, n_experts_per_tok=8, n_shared=1,
+                n_layers=1, routed_scaling=2.5, norm_topk_prob=True, rms_eps=1e-5):
+    return MoeConfig(hidden, moe_inter, n_routed_experts, n_experts_per_tok, n_shared, n_layers,
+                     routed_scaling, 1 if norm_topk_prob else 0, rms_eps)
+
+
+def expert_layout(cfg, inter=0):
+    lay = ExpertLayout()
+    rc = load().wl_expert_layout_of(ctypes.byref(cfg), inter, ctypes.byref(lay))
+    if rc != WL_OK:
+        raise WindlassError(rc, "wl_expert_layout_of")
+    return lay
+
+
+def synth_expert(cfg, seed, layer, expert, d_block, stream=0, inter=0):
+    rc = load().wl_synth_expert(ctypes.byref(cfg), inter, seed, layer, expert, d_block, stream)
+    if rc != WL_OK:
+        raise WindlassError(rc, "wl_synth_expert")
+
+
+def dequant_matvec_mxfp4(d_W, d_S, d_x, d_y, N, K, stream=0):
+    rc = load().wl_dequant_matvec_mxfp4(d_W, d_S, d_x, d_y, N, K, stream)
+    if rc != WL_OK:
+        raise WindlassError(rc, "wl_dequant_matvec_mxfp4")
+
+
+class Context:
+    """One wl_ctx: the MoE layers of a model on the current device."""
+
+    def __init__(self, cfg):
+        self.lib = load()
+        self.cfg = cfg
+        h = ctypes.c_void_p()
+        rc = self.lib.wl_create(ctypes.byref(cfg), ctypes.byref(h))
+        if rc != WL_OK:
+            raise WindlassError(rc, "wl_create")
+        self.h = h.value
+
+    def _ck(self, rc, what):
+        if rc != WL_OK:
+            raise WindlassError(rc, f"{what}: {self.lib.wl_last_error(self.h).decode()}")
+
+    def close(self):
+        if self.h:
+            self.lib.wl_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def set_layer(self, layer, router_w, bias, ln_w, shared, shared_dtype=SHARED_BF16):
+        self._ck(self.lib.wl_set_layer(self.h, layer, router_w, bias, ln_w, shared, shared_dtype),
+                 "wl_set_layer")
+
+    def slot_bind(self, layer, expert, d_block):
+        self._ck(self.lib.wl_slot_bind(self.h, layer, expert, d_block), "wl_slot_bind")
+
+    def slot_unbind(self, layer, expert):
+        self._ck(self.lib.wl_slot_unbind(self.h, layer, expert), "wl_slot_unbind")
+
+    def slot_pool_create(self, n_slots):
+        self._ck(self.lib.wl_slot_pool_create(self.h, n_slots), "wl_slot_pool_create")
+
+    def slot_pool_ptr(self, slot):
+        p = ctypes.c_void_p()
+        self._ck(self.lib.wl_slot_pool_ptr(self.h, slot, ctypes.byref(p)), "wl_slot_pool_ptr")
+        return p.value
+
+    def run_moe(self, layer, d_hidden, d_out, stream=0):
+        self._ck(self.lib.wl_run_moe(self.h, layer, d_hidden, d_out, stream), "wl_run_moe")
+
+    def run_moe_residual(self, layer, d_hidden, d_resid, d_out, stream=0):
+        self._ck(self.lib.wl_run_moe_residual(self.h, layer, d_hidden, d_resid, d_out, stream),
+                 "wl_run_moe_residual")
+
+    def run_chain(self, first_layer, n_layers, d_h, d_tmp, stream=0):
+        self._ck(self.lib.wl_run_chain(self.h, first_layer, n_layers, d_h, d_tmp, stream), "wl_run_chain")
+
+    def taps(self):
+        t = Taps()
+        self._ck(self.lib.wl_taps(self.h, ctypes.byref(t)), "wl_taps")
+        return {n: getattr(t, n) for n, _ in Taps._fields_}
+
+    def check_error(self, stream=0):
+        self._ck(self.lib.wl_check_error(self.h, stream), "wl_check_error")
+
+    def expert_ffn(self, d_block, d_x, d_y, d_y_bf16=None, stream=0):
+        self._ck(self.lib.wl_expert_ffn(self.h, d_block, d_x, d_y, d_y_bf16, stream), "wl_expert_ffn")
+
+    def set_schedule(self, sched):
+        self._ck(self.lib.wl_set_schedule(self.h, sched), "wl_set_schedule")
