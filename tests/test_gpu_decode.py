@@ -14,7 +14,7 @@ from oracle import moe_oracle as O
 from oracle import native, synth
 from windlass_amd import moe
 
-from .devmodel import DeviceModel, make_io
+from windlass_amd.model import DeviceModel, make_io
 
 pytestmark = pytest.mark.gpu
 GOLD = os.path.join(os.path.dirname(__file__), "golden")

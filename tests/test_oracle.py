@@ -190,3 +190,14 @@ def test_moe_layer_negative_controls():
             return G[:, ::-1].copy(), U, D  # column order scrambled
 
     assert O.rel_to_scale(ref, O.moe_layer(h, dense, Swapped(H, I, seed), 0, c)["out"]) > 1e-2
+
+
+def test_product_and_oracle_input_recipes_agree():
+    # the product's input generator and the oracle's restatement of it
+    from windlass_amd import synthdata
+    a = synthdata.dense_layer(256, 32, 128, 5, 2)
+    b = synth.dense_layer(256, 32, 128, 5, 2)
+    for k in a:
+        assert np.array_equal(a[k], b[k]), k
+    assert np.array_equal(synthdata.hidden_state(256, 3, 1), synth.hidden_state(256, 3, 1))
+    assert np.array_equal(synthdata.zipf_bias_offset(64, 4), synth.zipf_bias_offset(64, 4))

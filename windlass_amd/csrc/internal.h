@@ -11,29 +11,53 @@ namespace wl {
 constexpr int kWaves = 8;
 constexpr int kThreads = kWaves * 64;
 
-// Counter words (device, zero at rest; the last work-group to leave a launch
-// puts them back to zero). Per-tile arrival counters follow the fixed words.
-enum CounterWord : uint32_t {
-    C_CLAIM = 0,      // task queue head
-    C_EXIT = 1,       // work-groups that have left the launch
-    C_ROUTER = 2,     // router row tiles complete
-    C_TOPK = 3,       // 1 once top-k ids/weights/block pointers are published
-    C_SGU = 4,        // shared gate/up row tiles complete
-    C_RGU = 5,        // routed gate/up row tiles complete
-    C_SDOWN = 6,      // shared down row tiles complete
-    C_ERROR = 7,      // sticky error bits, cleared by the host
-    C_FIXED = 16      // first per-tile counter
-};
+// Cross-work-group state of one decode layer lives in uncached device memory
+// (MTYPE UC: loads and stores go to the memory side, never into a per-XCD L2),
+// so a producer never needs an L2 write-back fence — measured on MI355X, one
+// agent-scope release per task cut streaming from 5.2 to 0.9 TB/s — and a
+// consumer's polling load always sees the latest value.
+//
+// Arrival counters (read-modify-write) each own a 128-byte line: RMWs on one
+// line serialise at ~33 ns each. Completion flags hold the epoch of the call
+// that set them, so they never need resetting.
+constexpr uint32_t kLineWords = 32;
 
-// Error bits reported in C_ERROR.
+// Error bits reported in the error word.
 enum : uint32_t {
     E_SPIN = 1u,          // a dependency wait exceeded its bound
     E_NOT_RESIDENT = 2u,  // a routed expert resolved to a null block
 };
 
-// Per-layer launch arguments; lives in device memory (one record per layer) so
-// the kernel reads it through the scalar cache instead of holding ~60 kernel
-// argument registers for its whole lifetime.
+// Word offsets inside the uncached synchronisation block.
+struct SyncMap {
+    uint32_t c_rtile;   // [E/16] router tile arrivals (one line each)
+    uint32_t c_sgtile;  // [SI/16] shared gate/up tile arrivals (one line each)
+    uint32_t c_router;  // router tiles complete (one line)
+    uint32_t c_rdblk;   // [H/64] routed-down block arrivals (one line each)
+    uint32_t f_topk;    // epoch once top-k is published
+    uint32_t f_sgu;     // [SI/16] epoch once shared SwiGLU tile t is published
+    uint32_t f_rgu;     // [K][I/16] epoch once routed SwiGLU tile is published
+    uint32_t f_sdown;   // [H/16] epoch once shared-down tile is published
+    uint32_t error;     // sticky error bits
+    uint32_t words;
+    __host__ __device__ static SyncMap make(uint32_t H, uint32_t I, uint32_t E, uint32_t K, uint32_t SI) {
+        SyncMap m;
+        uint32_t o = 0;
+        m.c_rtile = o;  o += (E / 16) * kLineWords;
+        m.c_sgtile = o; o += (SI / 16) * kLineWords;
+        m.c_router = o; o += kLineWords;
+        m.c_rdblk = o;  o += (H / 64) * kLineWords;
+        m.f_topk = o;   o += kLineWords;
+        m.f_sgu = o;    o += SI / 16;
+        m.f_rgu = o;    o += K * (I / 16);
+        m.f_sdown = o;  o += H / 16;
+        o = (o + kLineWords - 1) / kLineWords * kLineWords;
+        m.error = o;    o += kLineWords;
+        m.words = o;
+        return m;
+    }
+};
+
 struct DecodeArgs {
     const uint16_t* ln_w;       // [H] bf16 or null (= ones)
     const uint16_t* router_w;   // [E][H] bf16
@@ -42,21 +66,21 @@ struct DecodeArgs {
     const uint16_t* sh_up;      // [SI][H] bf16
     const uint16_t* sh_down;    // [H][SI] bf16
     const uint8_t* const* slot_tab;  // [E] block pointers of this layer
-    // context scratch
+    // context scratch; the arrays marked (UC) are in uncached memory
     float* norm;                // [H]
-    float* logits;              // [E]
-    int32_t* idx;               // [K]
-    float* topw;                // [K]
-    const uint8_t** sel;        // [K] block pointers of the selected experts
+    float* logits;              // [E] (UC)
+    int32_t* idx;               // [K] (UC)
+    float* topw;                // [K] (UC)
+    const uint8_t** sel;        // [K] block pointers of the selected experts (UC)
     float* rmid;                // [K][I]
-    uint16_t* rmid_p;           // [K][3][I] bf16 pieces of rmid
+    uint16_t* rmid_p;           // [K][3][I] bf16 pieces of rmid (UC)
     float* smid;                // [SI]
-    uint16_t* smid_p;           // [3][SI]
-    float* shared_out;          // [H]
-    float* edown;               // [K][H] routed down outputs before weighting
-    float* part_r;              // [E/16][4][16]
-    float* part_s;              // [SI/16][4][32]
-    uint32_t* ctr;              // counters
+    uint16_t* smid_p;           // [3][SI] (UC)
+    float* shared_out;          // [H] (UC)
+    float* edown;               // [K][H] routed down outputs before weighting (UC)
+    float* part_r;              // [E/16][4][16] (UC)
+    float* part_s;              // [SI/16][4][32] (UC)
+    uint32_t* sync;             // uncached synchronisation block (SyncMap)
     // expert block layout (byte offsets)
     uint64_t gw_off, gs_off, uw_off, us_off, dw_off, ds_off;
     uint32_t H, I, E, K, SI;
@@ -72,6 +96,7 @@ struct DecodeDyn {
     uint32_t task_lo, task_hi;  // task range of this launch
     int32_t wait_deps;          // 0 when stream order already satisfies dependencies
     int32_t write_norm_tap;     // 1 in the launch that owns task 0
+    uint32_t epoch;             // non-zero, different for every call of the context
 };
 
 // Row tiles (16 rows each) per routed-down task: one expert x 64 output rows.

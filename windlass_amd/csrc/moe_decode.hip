@@ -73,11 +73,27 @@ WL_DEV f32x4 mma(bf16x8 a, bf16x8 b, f32x4 d) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, d, 0, 0, 0);
 }
 WL_DEV bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
-WL_DEV u32x4 ld16(const void* p) { return *(const u32x4*)p; }
-// A operand: piece row r (< 3) of a [3][stride] bf16 array, 8 values at col.
-WL_DEV bf16x8 a_piece(const uint16_t* base, uint32_t stride, uint32_t r, uint32_t col) {
+typedef __attribute__((address_space(1))) const u32x4 g_u32x4;
+typedef __attribute__((address_space(1))) const uint8_t g_u8;
+typedef __attribute__((address_space(3))) const u32x4 l_u32x4;
+// 16-byte and 1-byte loads from global memory (never through the flat path).
+WL_DEV u32x4 gld16(const void* p) { return *(g_u32x4*)p; }
+WL_DEV uint32_t gld1(const uint8_t* p) { return *(g_u8*)p; }
+// A operand: piece row r (< 3) of a [3][stride] bf16 array, 8 values at col;
+// zero for the other rows and for k tiles past the end (valid == false).
+WL_DEV bf16x8 a_lds(const uint16_t* base, uint32_t stride, uint32_t r, uint32_t col, bool valid) {
     u32x4 v = {0u, 0u, 0u, 0u};
-    if (r < 3u) v = ld16(base + r * stride + col);
+    if (r < 3u && valid) v = *(const u32x4*)(base + r * stride + col);
+    return as_bf16x8(v);
+}
+WL_DEV bf16x8 a_glb(const uint16_t* base, uint32_t stride, uint32_t r, uint32_t col, bool valid) {
+    u32x4 v = {0u, 0u, 0u, 0u};
+    if (r < 3u && valid) v = gld16(base + r * stride + col);
+    return as_bf16x8(v);
+}
+WL_DEV bf16x8 a_any(const uint16_t* base, uint32_t stride, uint32_t r, uint32_t col, bool valid) {
+    u32x4 v = {0u, 0u, 0u, 0u};
+    if (r < 3u && valid) v = *(const u32x4*)(base + r * stride + col);
     return as_bf16x8(v);
 }
 WL_DEV float sum3(f32x4 d) { return d[0] + d[1] + d[2]; }
@@ -97,44 +113,63 @@ WL_DEV float silu_mul(float g, float u) {
 }
 
 // ---- device-wide synchronisation -----------------------------------------
-WL_DEV uint32_t ld_relaxed(uint32_t* p) {
+// All words touched here are in uncached memory (see SyncMap). A barrier
+// (which waits for every wave's outstanding stores) orders a work-group's
+// results before the single store or RMW that announces them.
+WL_DEV uint32_t ld_sync(uint32_t* p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-// All threads: publish this work-group's global writes, then bump *c by one.
-// Returns the counter value before the increment (same in every thread).
-WL_DEV uint32_t publish_add(uint32_t* c, uint32_t* s_bcast) {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+WL_DEV void st_sync(uint32_t* p, uint32_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Arrival: returns the counter value before this work-group's increment.
+WL_DEV uint32_t arrive(uint32_t* c, uint32_t* s_bcast) {
     __syncthreads();
-    if (threadIdx.x == 0)
-        *s_bcast = __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (threadIdx.x == 0) *s_bcast = __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
     const uint32_t v = *s_bcast;
     __syncthreads();
     return v;
 }
-WL_DEV void acquire_all() { __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent"); }
+// Completion flag: set to this call's epoch once the work-group's stores are done.
+WL_DEV void signal(uint32_t* flag, uint32_t epoch) {
+    __syncthreads();
+    if (threadIdx.x == 0) st_sync(flag, epoch);
+}
+// Invalidate the caches this work-group reads through (cheap on gfx950), so
+// data read after a wait cannot come from a stale line.
+WL_DEV void acquire_all() {
+    if (threadIdx.x < 64) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    __syncthreads();
+}
+WL_DEV void raise_error(uint32_t* sync, const SyncMap& m, uint32_t bits) {
+    __hip_atomic_fetch_or(sync + m.error, bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
-// Bounded wait until *c >= target. Returns false (and E_SPIN is set) on expiry
-// or if another work-group already reported an error.
-WL_DEV bool wait_ge(uint32_t* ctr, uint32_t w, uint32_t target, uint32_t* s_bcast) {
-    if (threadIdx.x == 0) {
-        uint32_t ok = 1u, spins = 0u;
-        while (ld_relaxed(ctr + w) < target) {
-            if (ld_relaxed(ctr + C_ERROR) != 0u) { ok = 0u; break; }
-            __builtin_amdgcn_s_sleep(8);
-            if (++spins > (1u << 21)) {
-                __hip_atomic_fetch_or(ctr + C_ERROR, E_SPIN, __ATOMIC_RELAXED,
-                                      __HIP_MEMORY_SCOPE_AGENT);
+// Bounded wait until flags[0..n) all equal `epoch` (wave 0 polls, one flag per
+// lane). Returns false, with E_SPIN raised, if the bound expires or another
+// work-group already raised an error.
+WL_DEV bool wait_flags(uint32_t* sync, const SyncMap& m, uint32_t first, uint32_t n, uint32_t epoch,
+                       uint32_t* s_bcast) {
+    if (threadIdx.x < 64) {
+        const uint32_t lane = threadIdx.x;
+        uint32_t ok = 1u;
+        for (uint32_t spins = 0;; spins++) {
+            bool mine = true;
+            for (uint32_t f = lane; f < n; f += 64) mine = mine && (ld_sync(sync + first + f) == epoch);
+            if (__all(mine)) break;
+            if (ld_sync(sync + m.error) != 0u || spins > (1u << 20)) {
+                if (lane == 0 && spins > (1u << 20)) raise_error(sync, m, E_SPIN);
                 ok = 0u;
                 break;
             }
+            __builtin_amdgcn_s_sleep(4);
         }
-        *s_bcast = ok;
+        if (lane == 0) *s_bcast = ok;
     }
-    __syncthreads();
+    acquire_all();
     const bool ok = *s_bcast != 0u;
     __syncthreads();
-    acquire_all();
     return ok;
 }
 
@@ -178,13 +213,17 @@ WL_DEV void norm_prologue(const DecodeArgs& a, const float* hidden, uint16_t* xp
 }
 
 // ---- tile kernels -----------------------------------------------------------
-// Rows [0,16) of NM bf16 matrices (row stride ld elements, pointers already at
-// the tile's first row), k in 32-wide tiles [kt0, kt0+nkt), against the LDS
-// norm pieces. Leaves per-wave row sums in red[wave][mat*16 + row].
-template <int NM>
+// All weight loads go through explicit global-address-space pointers and are
+// issued unconditionally (k tiles past the end are clamped to the last valid
+// tile and their A operand is zeroed), so a wave keeps its whole batch of
+// loads in flight instead of waiting on each one.
+
+// Rows [0,16) of NM bf16 matrices (row stride ld elements, pointers at the
+// tile's first row), k in 32-wide tiles [kt0, kt0+nkt), against the LDS norm
+// pieces. Leaves per-wave row sums in red[wave][mat*16 + row].
+template <int NM, int MAXT>
 WL_DEV void bf16_tile(const uint16_t* const (&W)[NM], uint32_t ld, uint32_t kt0, uint32_t nkt,
                       const uint16_t* xp, uint32_t xps, float* red) {
-    constexpr int MAXT = 6;
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t n = lane & 15, g = lane >> 4;
     f32x4 d[NM];
@@ -194,21 +233,18 @@ WL_DEV void bf16_tile(const uint16_t* const (&W)[NM], uint32_t ld, uint32_t kt0,
         u32x4 wv[NM][MAXT];
 #pragma unroll
         for (int i = 0; i < MAXT; i++) {
-            const uint32_t kt = base + wave + kWaves * i;
-            if (kt < nkt) {
+            const uint32_t kt = min(base + wave + kWaves * i, nkt - 1);
 #pragma unroll
-                for (int mt = 0; mt < NM; mt++)
-                    wv[mt][i] = ld16(W[mt] + (size_t)n * ld + (kt0 + kt) * 32 + g * 8);
-            }
+            for (int mt = 0; mt < NM; mt++)
+                wv[mt][i] = gld16(W[mt] + (size_t)n * ld + (kt0 + kt) * 32 + g * 8);
         }
 #pragma unroll
         for (int i = 0; i < MAXT; i++) {
-            const uint32_t kt = base + wave + kWaves * i;
-            if (kt < nkt) {
-                const bf16x8 av = a_piece(xp, xps, n, (kt0 + kt) * 32 + g * 8);
+            const uint32_t ktr = base + wave + kWaves * i;
+            const uint32_t kt = min(ktr, nkt - 1);
+            const bf16x8 av = a_lds(xp, xps, n, (kt0 + kt) * 32 + g * 8, ktr < nkt);
 #pragma unroll
-                for (int mt = 0; mt < NM; mt++) d[mt] = mma(av, as_bf16x8(wv[mt][i]), d[mt]);
-            }
+            for (int mt = 0; mt < NM; mt++) d[mt] = mma(av, as_bf16x8(wv[mt][i]), d[mt]);
         }
     }
     if (lane < 16) {
@@ -221,10 +257,10 @@ WL_DEV void bf16_tile(const uint16_t* const (&W)[NM], uint32_t ld, uint32_t kt0,
 // Routed gate/up rows [0,16) of one MXFP4 expert (pointers at the tile's first
 // row), full K = H, against the LDS norm pieces. Leaves red[wave][0..15] = gate,
 // red[wave][16..31] = up.
+template <int MAXT>
 WL_DEV void fp4_gu_tile(const uint8_t* gw, const uint8_t* gs, const uint8_t* uw,
                         const uint8_t* us, uint32_t H, const uint16_t* xp, uint32_t xps,
                         float* red) {
-    constexpr int MAXT = 3;
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t n = lane & 15, g = lane >> 4;
     const uint32_t rb = H / 2, rs = H / 32, nkt = H / 128;
@@ -234,25 +270,22 @@ WL_DEV void fp4_gu_tile(const uint8_t* gw, const uint8_t* gs, const uint8_t* uw,
         uint32_t sg[MAXT], su[MAXT];
 #pragma unroll
         for (int i = 0; i < MAXT; i++) {
-            const uint32_t kt = base + wave + kWaves * i;
-            if (kt < nkt) {
-                wg[i] = ld16(gw + (size_t)n * rb + kt * 64 + g * 16);
-                wu[i] = ld16(uw + (size_t)n * rb + kt * 64 + g * 16);
-                sg[i] = gs[(size_t)n * rs + kt * 4 + g];
-                su[i] = us[(size_t)n * rs + kt * 4 + g];
-            }
+            const uint32_t kt = min(base + wave + kWaves * i, nkt - 1);
+            wg[i] = gld16(gw + (size_t)n * rb + kt * 64 + g * 16);
+            wu[i] = gld16(uw + (size_t)n * rb + kt * 64 + g * 16);
+            sg[i] = gld1(gs + (size_t)n * rs + kt * 4 + g);
+            su[i] = gld1(us + (size_t)n * rs + kt * 4 + g);
         }
 #pragma unroll
         for (int i = 0; i < MAXT; i++) {
-            const uint32_t kt = base + wave + kWaves * i;
-            if (kt < nkt) {
-                const float scg = e8m0f(sg[i]), scu = e8m0f(su[i]);
+            const uint32_t ktr = base + wave + kWaves * i;
+            const uint32_t kt = min(ktr, nkt - 1);
+            const float scg = e8m0f(sg[i]), scu = e8m0f(su[i]);
 #pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    const bf16x8 av = a_piece(xp, xps, n, kt * 128 + g * 32 + j * 8);
-                    dg = mma(av, fp4x8_bf16(wg[i][j], scg), dg);
-                    du = mma(av, fp4x8_bf16(wu[i][j], scu), du);
-                }
+            for (int j = 0; j < 4; j++) {
+                const bf16x8 av = a_lds(xp, xps, n, kt * 128 + g * 32 + j * 8, ktr < nkt);
+                dg = mma(av, fp4x8_bf16(wg[i][j], scg), dg);
+                du = mma(av, fp4x8_bf16(wu[i][j], scu), du);
             }
         }
     }
@@ -264,9 +297,9 @@ WL_DEV void fp4_gu_tile(const uint8_t* gw, const uint8_t* gs, const uint8_t* uw,
 }
 
 // Shared-expert down rows [0,16) (bf16, row stride SI, pointer at the first
-// row), against the global SwiGLU pieces smid_p [3][SI]. red[wave][0..15].
+// row), against the global SwiGLU pieces ap [3][SI]. red[wave][0..15].
+template <int MAXT>
 WL_DEV void bf16_down_tile(const uint16_t* W, uint32_t SI, const uint16_t* ap, float* red) {
-    constexpr int MAXT = 8;
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t n = lane & 15, g = lane >> 4;
     const uint32_t nkt = SI / 32;
@@ -276,29 +309,24 @@ WL_DEV void bf16_down_tile(const uint16_t* W, uint32_t SI, const uint16_t* ap, f
         bf16x8 av[MAXT];
 #pragma unroll
         for (int i = 0; i < MAXT; i++) {
-            const uint32_t kt = base + wave + kWaves * i;
-            if (kt < nkt) {
-                wv[i] = ld16(W + (size_t)n * SI + kt * 32 + g * 8);
-                av[i] = a_piece(ap, SI, n, kt * 32 + g * 8);
-            }
+            const uint32_t ktr = base + wave + kWaves * i;
+            const uint32_t kt = min(ktr, nkt - 1);
+            wv[i] = gld16(W + (size_t)n * SI + kt * 32 + g * 8);
+            av[i] = a_glb(ap, SI, n, kt * 32 + g * 8, ktr < nkt);
         }
 #pragma unroll
-        for (int i = 0; i < MAXT; i++) {
-            const uint32_t kt = base + wave + kWaves * i;
-            if (kt < nkt) d = mma(av[i], as_bf16x8(wv[i]), d);
-        }
+        for (int i = 0; i < MAXT; i++) d = mma(av[i], as_bf16x8(wv[i]), d);
     }
     if (lane < 16) red[wave * 64 + lane] = sum3(d);
     __syncthreads();
 }
 
 // Routed down: RT row tiles (16 rows each, pointers at the block's first row)
-// of one MXFP4 expert over K = I, against that expert's global SwiGLU pieces
-// ap [3][I]. red[wave][t*16 + row].
-template <int RT>
+// of one MXFP4 expert over K = I, against that expert's SwiGLU pieces ap
+// [3][aps] (global or LDS). red[wave][t*16 + row].
+template <int RT, int MAXT>
 WL_DEV void fp4_down_block(const uint8_t* dw, const uint8_t* ds, uint32_t I, const uint16_t* ap,
                            uint32_t aps, float* red) {
-    constexpr int MAXT = 1;
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t n = lane & 15, g = lane >> 4;
     const uint32_t rb = I / 2, rs = I / 32, nkt = I / 128;
@@ -310,29 +338,26 @@ WL_DEV void fp4_down_block(const uint8_t* dw, const uint8_t* ds, uint32_t I, con
         uint32_t sv[RT][MAXT];
 #pragma unroll
         for (int i = 0; i < MAXT; i++) {
-            const uint32_t kt = base + wave + kWaves * i;
-            if (kt < nkt) {
+            const uint32_t kt = min(base + wave + kWaves * i, nkt - 1);
 #pragma unroll
-                for (int t = 0; t < RT; t++) {
-                    const size_t row = (size_t)t * 16 + n;
-                    wv[t][i] = ld16(dw + row * rb + kt * 64 + g * 16);
-                    sv[t][i] = ds[row * rs + kt * 4 + g];
-                }
+            for (int t = 0; t < RT; t++) {
+                const size_t row = (size_t)t * 16 + n;
+                wv[t][i] = gld16(dw + row * rb + kt * 64 + g * 16);
+                sv[t][i] = gld1(ds + row * rs + kt * 4 + g);
             }
         }
 #pragma unroll
         for (int i = 0; i < MAXT; i++) {
-            const uint32_t kt = base + wave + kWaves * i;
-            if (kt < nkt) {
-                bf16x8 av[4];
+            const uint32_t ktr = base + wave + kWaves * i;
+            const uint32_t kt = min(ktr, nkt - 1);
+            bf16x8 av[4];
 #pragma unroll
-                for (int j = 0; j < 4; j++) av[j] = a_piece(ap, aps, n, kt * 128 + g * 32 + j * 8);
+            for (int j = 0; j < 4; j++) av[j] = a_any(ap, aps, n, kt * 128 + g * 32 + j * 8, ktr < nkt);
 #pragma unroll
-                for (int t = 0; t < RT; t++) {
-                    const float sc = e8m0f(sv[t][i]);
+            for (int t = 0; t < RT; t++) {
+                const float sc = e8m0f(sv[t][i]);
 #pragma unroll
-                    for (int j = 0; j < 4; j++) d[t] = mma(av[j], fp4x8_bf16(wv[t][i][j], sc), d[t]);
-                }
+                for (int j = 0; j < 4; j++) d[t] = mma(av[j], fp4x8_bf16(wv[t][i][j], sc), d[t]);
             }
         }
     }
@@ -393,14 +418,17 @@ WL_DEV void topk_publish(const DecodeArgs& a, float* sc, float* ch, float* wsel)
             if (!blk) bad = 1;
             a.sel[k] = blk;
         }
-        if (bad)
-            __hip_atomic_fetch_or(a.ctr + C_ERROR, E_NOT_RESIDENT, __ATOMIC_RELAXED,
-                                  __HIP_MEMORY_SCOPE_AGENT);
+        if (bad) raise_error(a.sync, SyncMap::make(a.H, a.I, a.E, a.K, a.SI), E_NOT_RESIDENT);
     }
     __syncthreads();
 }
 
 // ---- the persistent task kernel ----------------------------------------------
+// Work-group b runs tasks b, b + G, b + 2G, ... (G = gridDim.x); tasks are
+// numbered in dependency order, so each work-group meets its waits in the order
+// the producers finish. With the fused schedule G is the number of work-groups
+// the device holds at once, so every producer is resident; the waits are bounded
+// regardless and report E_SPIN instead of hanging.
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 4)))
 moe_decode_kernel(const DecodeArgs* __restrict__ pa, const DecodeDyn d) {
     const DecodeArgs& a = *pa;
@@ -411,61 +439,44 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const DecodeDyn d) {
     float* ebuf = red + kWaves * 64;          // [32][16]
     float* tks = ebuf + 32 * 16;              // [2E + 32] top-k staging
     __shared__ uint32_t s_bcast;
-    __shared__ uint32_t s_next;
-    __shared__ uint32_t s_fail;
+    __shared__ const uint8_t* s_sel[32];
+    __shared__ float s_w[32];
 
     const TaskMap tm = TaskMap::make(a.H, a.I, a.E, a.K, a.SI);
-    uint32_t* ctr = a.ctr;
+    const SyncMap sm = SyncMap::make(a.H, a.I, a.E, a.K, a.SI);
+    uint32_t* sync = a.sync;
+    const uint32_t ep = d.epoch;
     const uint32_t tid = threadIdx.x;
-    bool have_norm = false;
+    bool have_norm = false, have_topk = false, have_sgu = false, ok_all = true;
+    uint32_t have_rgu_k = 0xFFFFFFFFu;
 
-    if (tid == 0) {
-        s_next = __hip_atomic_fetch_add(ctr + C_CLAIM, 1u, __ATOMIC_RELAXED,
-                                        __HIP_MEMORY_SCOPE_AGENT);
-        s_fail = ld_relaxed(ctr + C_ERROR);
-    }
-
-    for (;;) {
-        __syncthreads();
-        const uint32_t t = d.task_lo + s_next;
-        const bool failed = s_fail != 0u;
-        __syncthreads();
-        if (t >= d.task_hi) break;
-        // claim the next task now; its latency hides behind this task's loads
-        uint32_t next_claim = 0;
-        if (tid == 0)
-            next_claim = __hip_atomic_fetch_add(ctr + C_CLAIM, 1u, __ATOMIC_RELAXED,
-                                                __HIP_MEMORY_SCOPE_AGENT);
-
-        if (!failed && t < tm.oSG) {
+    for (uint32_t t = d.task_lo + blockIdx.x; t < d.task_hi; t += gridDim.x) {
+        if (t < tm.oSG) {
             // ---------------- router partial (16 rows, one k-quarter) -------------
             const uint32_t tile = t >> 2, q = t & 3u;
             const uint32_t nkt = a.H / 32 / 4;
             if (!have_norm) { norm_prologue(a, d.hidden, xp, xps, red, d.write_norm_tap && t == 0); have_norm = true; }
             const uint16_t* W[1] = {a.router_w + (size_t)tile * 16 * a.H};
-            bf16_tile<1>(W, a.H, q * nkt, nkt, xp, xps, red);
+            bf16_tile<1, 6>(W, a.H, q * nkt, nkt, xp, xps, red);
             if (tid < 16) a.part_r[(tile * 4 + q) * 16 + tid] = wave_total(red, tid);
-            const uint32_t arrived = publish_add(ctr + C_FIXED + tile, &s_bcast);
-            if (arrived == 3u) {
+            uint32_t* cnt = sync + sm.c_rtile + tile * kLineWords;
+            if (arrive(cnt, &s_bcast) == 3u) {
                 acquire_all();
                 if (tid < 16) {
-                    float s = 0.f;
-                    for (int qq = 0; qq < 4; qq++) s += a.part_r[(tile * 4 + qq) * 16 + tid];
-                    a.logits[tile * 16 + tid] = s;
+                    float sum = 0.f;
+                    for (int qq = 0; qq < 4; qq++) sum += a.part_r[(tile * 4 + qq) * 16 + tid];
+                    a.logits[tile * 16 + tid] = sum;
                 }
-                if (tid == 0) ctr[C_FIXED + tile] = 0u;
-                const uint32_t done = publish_add(ctr + C_ROUTER, &s_bcast);
-                if (done == a.E / 16 - 1) {
+                if (tid == 0) st_sync(cnt, 0u);
+                uint32_t* done = sync + sm.c_router;
+                if (arrive(done, &s_bcast) == a.E / 16 - 1) {
                     acquire_all();
                     topk_publish(a, tks, tks + a.E, tks + 2 * a.E);
-                    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-                    __syncthreads();
-                    if (tid == 0)
-                        __hip_atomic_store(ctr + C_TOPK, 1u, __ATOMIC_RELAXED,
-                                           __HIP_MEMORY_SCOPE_AGENT);
+                    if (tid == 0) st_sync(done, 0u);
+                    signal(sync + sm.f_topk, ep);
                 }
             }
-        } else if (!failed && t < tm.oRG) {
+        } else if (t < tm.oRG) {
             // ---------------- shared gate/up partial ------------------------------
             const uint32_t u = t - tm.oSG;
             const uint32_t tile = u >> 2, q = u & 3u;
@@ -473,10 +484,10 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const DecodeDyn d) {
             if (!have_norm) { norm_prologue(a, d.hidden, xp, xps, red, false); have_norm = true; }
             const uint16_t* W[2] = {a.sh_gate + (size_t)tile * 16 * a.H,
                                     a.sh_up + (size_t)tile * 16 * a.H};
-            bf16_tile<2>(W, a.H, q * nkt, nkt, xp, xps, red);
+            bf16_tile<2, 6>(W, a.H, q * nkt, nkt, xp, xps, red);
             if (tid < 32) a.part_s[(tile * 4 + q) * 32 + tid] = wave_total(red, tid);
-            const uint32_t arrived = publish_add(ctr + C_FIXED + a.E / 16 + tile, &s_bcast);
-            if (arrived == 3u) {
+            uint32_t* cnt = sync + sm.c_sgtile + tile * kLineWords;
+            if (arrive(cnt, &s_bcast) == 3u) {
                 acquire_all();
                 if (tid < 16) {
                     float gs = 0.f, us = 0.f;
@@ -493,23 +504,27 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const DecodeDyn d) {
                     a.smid_p[a.SI + r] = (uint16_t)m;
                     a.smid_p[2 * a.SI + r] = (uint16_t)l;
                 }
-                if (tid == 0) ctr[C_FIXED + a.E / 16 + tile] = 0u;
-                publish_add(ctr + C_SGU, &s_bcast);
+                if (tid == 0) st_sync(cnt, 0u);
+                signal(sync + sm.f_sgu + tile, ep);
             }
-        } else if (!failed && t < tm.oSD) {
+        } else if (t < tm.oSD) {
             // ---------------- routed gate/up + SwiGLU -----------------------------
             const uint32_t u = t - tm.oRG;
             const uint32_t tiles = a.I / 16;
             const uint32_t k = u / tiles, tile = u % tiles;
             if (!have_norm) { norm_prologue(a, d.hidden, xp, xps, red, false); have_norm = true; }
-            bool ok = true;
-            if (d.wait_deps) ok = wait_ge(ctr, C_TOPK, 1u, &s_bcast);
-            const uint8_t* blk = ok ? a.sel[k] : nullptr;
+            if (!have_topk) {
+                if (d.wait_deps) ok_all = wait_flags(sync, sm, sm.f_topk, 1, ep, &s_bcast) && ok_all;
+                if (tid < a.K) { s_sel[tid] = a.sel[tid]; s_w[tid] = a.topw[tid]; }
+                __syncthreads();
+                have_topk = true;
+            }
+            const uint8_t* blk = ok_all ? s_sel[k] : nullptr;
             if (blk) {
                 const size_t r0 = (size_t)tile * 16;
-                fp4_gu_tile(blk + a.gw_off + r0 * (a.H / 2), blk + a.gs_off + r0 * (a.H / 32),
-                            blk + a.uw_off + r0 * (a.H / 2), blk + a.us_off + r0 * (a.H / 32), a.H,
-                            xp, xps, red);
+                fp4_gu_tile<3>(blk + a.gw_off + r0 * (a.H / 2), blk + a.gs_off + r0 * (a.H / 32),
+                               blk + a.uw_off + r0 * (a.H / 2), blk + a.us_off + r0 * (a.H / 32), a.H,
+                               xp, xps, red);
                 if (tid < 16) {
                     const float mid = silu_mul(wave_total(red, tid), wave_total(red, 16 + tid));
                     const uint32_t r = tile * 16 + tid;
@@ -521,64 +536,60 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const DecodeDyn d) {
                     p[a.I + r] = (uint16_t)m;
                     p[2 * a.I + r] = (uint16_t)l;
                 }
-                publish_add(ctr + C_RGU, &s_bcast);
+                signal(sync + sm.f_rgu + k * tiles + tile, ep);
             }
-        } else if (!failed && t < tm.oRD) {
+        } else if (t < tm.oRD) {
             // ---------------- shared down -----------------------------------------
             const uint32_t tile = t - tm.oSD;
-            bool ok = true;
-            if (d.wait_deps) ok = wait_ge(ctr, C_SGU, a.SI / 16, &s_bcast);
-            if (ok) {
-                bf16_down_tile(a.sh_down + (size_t)tile * 16 * a.SI, a.SI, a.smid_p, red);
-                if (tid < 16) a.shared_out[tile * 16 + tid] = wave_total(red, tid);
-                publish_add(ctr + C_SDOWN, &s_bcast);
+            if (!have_sgu) {
+                if (d.wait_deps) ok_all = wait_flags(sync, sm, sm.f_sgu, a.SI / 16, ep, &s_bcast) && ok_all;
+                have_sgu = true;
             }
-        } else if (!failed) {
+            if (ok_all) {
+                bf16_down_tile<8>(a.sh_down + (size_t)tile * 16 * a.SI, a.SI, a.smid_p, red);
+                if (tid < 16) a.shared_out[tile * 16 + tid] = wave_total(red, tid);
+                signal(sync + sm.f_sdown + tile, ep);
+            }
+        } else {
             // ---------------- routed down + combine -------------------------------
             const uint32_t u = t - tm.oRD;
             const uint32_t blocks = a.H / (16 * kDownRT);
             const uint32_t k = u / blocks, blkrow = u % blocks;
-            bool ok = true;
-            if (d.wait_deps) ok = wait_ge(ctr, C_RGU, a.K * (a.I / 16), &s_bcast);
-            const uint8_t* blk = ok ? a.sel[k] : nullptr;
+            if (!have_topk) {
+                if (d.wait_deps) ok_all = wait_flags(sync, sm, sm.f_topk, 1, ep, &s_bcast) && ok_all;
+                if (tid < a.K) { s_sel[tid] = a.sel[tid]; s_w[tid] = a.topw[tid]; }
+                __syncthreads();
+                have_topk = true;
+            }
+            if (have_rgu_k != k) {
+                // this expert's SwiGLU output must be complete
+                if (d.wait_deps)
+                    ok_all = wait_flags(sync, sm, sm.f_rgu + k * (a.I / 16), a.I / 16, ep, &s_bcast) && ok_all;
+                have_rgu_k = k;
+            }
+            const uint8_t* blk = ok_all ? s_sel[k] : nullptr;
             if (blk) {
                 const size_t r0 = (size_t)blkrow * 16 * kDownRT;
-                fp4_down_block<kDownRT>(blk + a.dw_off + r0 * (a.I / 2), blk + a.ds_off + r0 * (a.I / 32),
-                                        a.I, a.rmid_p + (size_t)k * 3 * a.I, a.I, red);
+                fp4_down_block<kDownRT, 1>(blk + a.dw_off + r0 * (a.I / 2), blk + a.ds_off + r0 * (a.I / 32),
+                                           a.I, a.rmid_p + (size_t)k * 3 * a.I, a.I, red);
                 if (tid < 16 * kDownRT) a.edown[(size_t)k * a.H + r0 + tid] = wave_total(red, tid);
-                const uint32_t cnt_word = C_FIXED + a.E / 16 + a.SI / 16 + blkrow;
-                const uint32_t arrived = publish_add(ctr + cnt_word, &s_bcast);
-                if (arrived == a.K - 1) {
+                uint32_t* cnt = sync + sm.c_rdblk + blkrow * kLineWords;
+                if (arrive(cnt, &s_bcast) == a.K - 1) {
                     acquire_all();
                     bool ok2 = true;
-                    if (d.wait_deps) ok2 = wait_ge(ctr, C_SDOWN, a.H / 16, &s_bcast);
+                    if (d.wait_deps)
+                        ok2 = wait_flags(sync, sm, sm.f_sdown + blkrow * kDownRT, kDownRT, ep, &s_bcast);
                     if (ok2 && tid < 16 * kDownRT) {
                         const size_t r = r0 + tid;
                         float acc = 0.f;
                         for (uint32_t kk = 0; kk < a.K; kk++)
-                            acc = __fadd_rn(acc, __fmul_rn(a.topw[kk], a.edown[(size_t)kk * a.H + r]));
+                            acc = __fadd_rn(acc, __fmul_rn(s_w[kk], a.edown[(size_t)kk * a.H + r]));
                         acc = __fadd_rn(acc, a.shared_out[r]);
                         d.out[r] = d.resid ? __fadd_rn(d.resid[r], acc) : acc;
                     }
-                    if (tid == 0) ctr[cnt_word] = 0u;
+                    if (tid == 0) st_sync(cnt, 0u);
                 }
             }
-        }
-
-        if (tid == 0) {
-            s_next = next_claim;
-            s_fail = ld_relaxed(ctr + C_ERROR);
-        }
-    }
-
-    // leave the launch; the last work-group out resets the counters
-    __syncthreads();
-    if (tid == 0) {
-        const uint32_t old = __hip_atomic_fetch_add(ctr + C_EXIT, 1u, __ATOMIC_ACQ_REL,
-                                                    __HIP_MEMORY_SCOPE_AGENT);
-        if (old == gridDim.x - 1) {
-            for (uint32_t w = 0; w < C_ERROR; w++)
-                __hip_atomic_store(ctr + w, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     }
 }
@@ -607,7 +618,7 @@ dequant_matvec_kernel(const uint8_t* __restrict__ W, const uint8_t* __restrict__
     float* red = (float*)(lds_raw + (size_t)3 * xps * 2);
     pieces_to_lds(x, K, xp, xps);
     const size_t r0 = (size_t)blockIdx.x * 16;
-    fp4_down_block<1>(W + r0 * (K / 2), S + r0 * (K / 32), K, xp, xps, red);
+    fp4_down_block<1, 1>(W + r0 * (K / 2), S + r0 * (K / 32), K, xp, xps, red);
     if (threadIdx.x < 16 && r0 + threadIdx.x < N) y[r0 + threadIdx.x] = wave_total(red, threadIdx.x);
 }
 
@@ -622,7 +633,7 @@ ffn_gu_kernel(const uint8_t* __restrict__ blk, uint64_t gw_off, uint64_t gs_off,
     float* red = (float*)(lds_raw + (size_t)3 * xps * 2);
     pieces_to_lds(x, H, xp, xps);
     const size_t r0 = (size_t)blockIdx.x * 16;
-    fp4_gu_tile(blk + gw_off + r0 * (H / 2), blk + gs_off + r0 * (H / 32), blk + uw_off + r0 * (H / 2),
+    fp4_gu_tile<3>(blk + gw_off + r0 * (H / 2), blk + gs_off + r0 * (H / 32), blk + uw_off + r0 * (H / 2),
                 blk + us_off + r0 * (H / 32), H, xp, xps, red);
     if (threadIdx.x < 16) {
         const float m = silu_mul(wave_total(red, threadIdx.x), wave_total(red, 16 + threadIdx.x));
@@ -643,7 +654,7 @@ ffn_down_kernel(const uint8_t* __restrict__ blk, uint64_t dw_off, uint64_t ds_of
                 uint16_t* __restrict__ y_bf16) {
     __shared__ float red[kWaves * 64];
     const size_t r0 = (size_t)blockIdx.x * 16 * kDownRT;
-    fp4_down_block<kDownRT>(blk + dw_off + r0 * (I / 2), blk + ds_off + r0 * (I / 32), I, mid_p, I, red);
+    fp4_down_block<kDownRT, 1>(blk + dw_off + r0 * (I / 2), blk + ds_off + r0 * (I / 32), I, mid_p, I, red);
     if (threadIdx.x < 16 * kDownRT) {
         const float v = wave_total(red, threadIdx.x);
         y[r0 + threadIdx.x] = v;

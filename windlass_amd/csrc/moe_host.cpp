@@ -10,6 +10,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -52,8 +53,11 @@ struct wl_ctx {
     float* edown = nullptr;
     float* part_r = nullptr;
     float* part_s = nullptr;
-    uint32_t* ctr = nullptr;
-    size_t n_ctr = 0;
+    uint32_t* sync = nullptr;
+    wl::SyncMap sm{};
+    uint32_t epoch = 0;
+    void* uc_block = nullptr;   // uncached scratch (returned to the process pool on destroy)
+    size_t uc_bytes = 0;
     // context-owned slot pool
     uint8_t* pool = nullptr;
     uint32_t pool_slots = 0;
@@ -88,6 +92,35 @@ wl_status dalloc(wl_ctx* c, T** p, size_t bytes) {
     c->allocs.push_back(q);
     *p = (T*)q;
     return WL_OK;
+}
+
+// Uncached device memory is never returned to the runtime while the process
+// lives (freeing it after a kernel has read it has corrupted later allocations
+// on this platform); blocks of destroyed contexts are kept here for reuse.
+struct UcBlock { int device; size_t bytes; void* ptr; };
+std::mutex g_uc_mu;
+std::vector<UcBlock> g_uc_free;
+
+void* uc_acquire(int device, size_t bytes) {
+    {
+        std::lock_guard<std::mutex> lk(g_uc_mu);
+        for (size_t i = 0; i < g_uc_free.size(); i++) {
+            if (g_uc_free[i].device == device && g_uc_free[i].bytes >= bytes) {
+                void* p = g_uc_free[i].ptr;
+                g_uc_free.erase(g_uc_free.begin() + i);
+                return p;
+            }
+        }
+    }
+    void* p = nullptr;
+    if (hipExtMallocWithFlags(&p, bytes, hipDeviceMallocUncached) != hipSuccess) return nullptr;
+    return p;
+}
+
+void uc_release(int device, size_t bytes, void* p) {
+    if (!p) return;
+    std::lock_guard<std::mutex> lk(g_uc_mu);
+    g_uc_free.push_back({device, bytes, p});
 }
 
 wl_status validate_cfg(const wl_moe_config* cfg, wl_ctx* c) {
@@ -131,7 +164,7 @@ wl::DecodeArgs layer_record(const wl_ctx* c, uint32_t layer) {
     a.edown = c->edown;
     a.part_r = c->part_r;
     a.part_s = c->part_s;
-    a.ctr = c->ctr;
+    a.sync = c->sync;
     a.gw_off = c->lay.gw_off;
     a.gs_off = c->lay.gs_off;
     a.uw_off = c->lay.uw_off;
@@ -197,29 +230,52 @@ wl_status wl_create(const wl_moe_config* cfg, wl_ctx** out) {
     c->layers.resize(L);
     c->h_slot.assign((size_t)L * E, nullptr);
     c->n_bound.assign(L, 0);
-    c->n_ctr = wl::C_FIXED + E / 16 + SI / 16 + H / 64;
+    c->sm = wl::SyncMap::make(H, I, E, K, SI);
     if ((s = dalloc(c, &c->d_slot, sizeof(void*) * (size_t)L * E)) != WL_OK ||
         (s = dalloc(c, &c->d_largs, sizeof(wl::DecodeArgs) * (size_t)L)) != WL_OK ||
         (s = dalloc(c, &c->norm, 4 * (size_t)H)) != WL_OK ||
-        (s = dalloc(c, &c->logits, 4 * (size_t)E)) != WL_OK ||
-        (s = dalloc(c, &c->idx, 4 * (size_t)WL_MAX_TOPK)) != WL_OK ||
-        (s = dalloc(c, &c->topw, 4 * (size_t)WL_MAX_TOPK)) != WL_OK ||
-        (s = dalloc(c, &c->sel, sizeof(void*) * (size_t)WL_MAX_TOPK)) != WL_OK ||
         (s = dalloc(c, &c->rmid, 4 * (size_t)K * I)) != WL_OK ||
-        (s = dalloc(c, &c->rmid_p, 2 * 3 * (size_t)K * I)) != WL_OK ||
-        (s = dalloc(c, &c->smid, 4 * (size_t)SI)) != WL_OK ||
-        (s = dalloc(c, &c->smid_p, 2 * 3 * (size_t)SI)) != WL_OK ||
-        (s = dalloc(c, &c->shared_out, 4 * (size_t)H)) != WL_OK ||
-        (s = dalloc(c, &c->edown, 4 * (size_t)K * H)) != WL_OK ||
-        (s = dalloc(c, &c->part_r, 4 * (size_t)(E / 16) * 4 * 16)) != WL_OK ||
-        (s = dalloc(c, &c->part_s, 4 * (size_t)(SI / 16) * 4 * 32)) != WL_OK ||
-        (s = dalloc(c, &c->ctr, 4 * c->n_ctr)) != WL_OK) {
+        (s = dalloc(c, &c->smid, 4 * (size_t)SI)) != WL_OK) {
         wl_destroy(c);
         return s;
     }
+    // the uncached block: sync words, then every array one work-group writes
+    // and another reads
+    {
+        size_t off = 0;
+        auto carve = [&](size_t bytes) { size_t o = off; off += (bytes + 255) / 256 * 256; return o; };
+        const size_t o_sync = carve(4 * (size_t)c->sm.words);
+        const size_t o_logits = carve(4 * (size_t)E);
+        const size_t o_idx = carve(4 * (size_t)WL_MAX_TOPK);
+        const size_t o_topw = carve(4 * (size_t)WL_MAX_TOPK);
+        const size_t o_sel = carve(sizeof(void*) * (size_t)WL_MAX_TOPK);
+        const size_t o_part_r = carve(4 * (size_t)(E / 16) * 4 * 16);
+        const size_t o_part_s = carve(4 * (size_t)(SI / 16) * 4 * 32);
+        const size_t o_rmid_p = carve(2 * 3 * (size_t)K * I);
+        const size_t o_smid_p = carve(2 * 3 * (size_t)SI);
+        const size_t o_shared = carve(4 * (size_t)H);
+        const size_t o_edown = carve(4 * (size_t)K * H);
+        c->uc_bytes = off;
+        c->uc_block = uc_acquire(c->device, off);
+        if (!c->uc_block) {
+            wl_destroy(c);
+            return WL_ERR_OOM;
+        }
+        uint8_t* b = (uint8_t*)c->uc_block;
+        c->sync = (uint32_t*)(b + o_sync);
+        c->logits = (float*)(b + o_logits);
+        c->idx = (int32_t*)(b + o_idx);
+        c->topw = (float*)(b + o_topw);
+        c->sel = (const uint8_t**)(b + o_sel);
+        c->part_r = (float*)(b + o_part_r);
+        c->part_s = (float*)(b + o_part_s);
+        c->rmid_p = (uint16_t*)(b + o_rmid_p);
+        c->smid_p = (uint16_t*)(b + o_smid_p);
+        c->shared_out = (float*)(b + o_shared);
+        c->edown = (float*)(b + o_edown);
+    }
     e = hipMemset(c->d_slot, 0, sizeof(void*) * (size_t)L * E);
-    if (e == hipSuccess) e = hipMemset(c->ctr, 0, 4 * c->n_ctr);
-    if (e == hipSuccess) e = hipMemset(c->sel, 0, sizeof(void*) * WL_MAX_TOPK);
+    if (e == hipSuccess) e = hipMemset(c->uc_block, 0, c->uc_bytes);
     if (e == hipSuccess) e = hipDeviceSynchronize();
     if (e != hipSuccess) { wl_destroy(c); return WL_ERR_HIP; }
     *out = c;
@@ -228,7 +284,9 @@ wl_status wl_create(const wl_moe_config* cfg, wl_ctx** out) {
 
 void wl_destroy(wl_ctx* c) {
     if (!c) return;
+    if (c->uc_block) hipDeviceSynchronize();
     for (void* p : c->allocs) hipFree(p);
+    uc_release(c->device, c->uc_bytes, c->uc_block);
     delete c;
 }
 
@@ -317,6 +375,8 @@ static wl_status run_layer(wl_ctx* c, uint32_t layer, const float* d_hidden, con
         return fail(c, WL_ERR_NOT_RESIDENT, "layer %u has %u of %u experts bound", layer, c->n_bound[layer], E);
 
     wl::DecodeDyn dyn{};
+    if (++c->epoch == 0) c->epoch = 1;
+    dyn.epoch = c->epoch;
     dyn.hidden = d_hidden;
     dyn.resid = d_resid;
     dyn.out = d_out;
@@ -391,11 +451,11 @@ wl_status wl_check_error(wl_ctx* c, void* stream) {
     hipError_t e = hipStreamSynchronize((hipStream_t)stream);
     if (e != hipSuccess) return hip_fail(c, e, "stream synchronize");
     uint32_t flag = 0;
-    e = hipMemcpy(&flag, c->ctr + wl::C_ERROR, 4, hipMemcpyDeviceToHost);
+    e = hipMemcpy(&flag, c->sync + c->sm.error, 4, hipMemcpyDeviceToHost);
     if (e != hipSuccess) return hip_fail(c, e, "error flag read");
     if (flag) {
         const uint32_t zero = 0;
-        hipMemcpy(c->ctr + wl::C_ERROR, &zero, 4, hipMemcpyHostToDevice);
+        hipMemcpy(c->sync + c->sm.error, &zero, 4, hipMemcpyHostToDevice);
         return fail(c, WL_ERR_DEVICE, "device error bits 0x%x%s%s", flag,
                     (flag & wl::E_SPIN) ? " [dependency wait expired]" : "",
                     (flag & wl::E_NOT_RESIDENT) ? " [routed expert not resident]" : "");

@@ -1,15 +1,14 @@
-"""Builds a synthetic MoE model on the device through the C ABI (test and
-benchmark helper). Routed experts are filled on the device by
-wl_synth_expert; dense tensors come from oracle/synth.py (numpy) so the
-oracle sees the same values."""
+"""A resident synthetic MoE model built through the C ABI: every routed
+expert of every layer in one context-owned HBM slot pool (filled on the device
+by wl_synth_expert), dense tensors from windlass_amd.synthdata uploaded once.
+Used by the benchmark and the GPU tests."""
 import numpy as np
 
-from oracle import synth
-from windlass_amd import hip, moe
+from . import hip, moe, synthdata
 
 
 class DeviceModel:
-    def __init__(self, cfg, seed, n_layers=1, ln_weights=None, bias_offset=None, layer_seeds=None):
+    def __init__(self, cfg, seed, n_layers=1, ln_weights=None, bias_offset=None):
         self.c = dict(cfg)
         self.seed = seed
         self.L = n_layers
@@ -29,22 +28,21 @@ class DeviceModel:
                 p = self.ctx.slot_pool_ptr(l * E + e)
                 moe.synth_expert(self.cfg, seed, l, e, p)
                 self.ctx.slot_bind(l, e, p)
-            d = synth.dense_layer(H, E, self.SI, seed, l)
+            d = synthdata.dense_layer(H, E, self.SI, seed, l)
             if bias_offset is not None:
                 d["bias"] = (d["bias"] + bias_offset).astype(np.float32)
             self.dense.append(d)
             rw = hip.DeviceBuffer.from_array(d["router_w"])
             bb = hip.DeviceBuffer.from_array(d["bias"])
             sb = hip.DeviceBuffer.from_array(d["shared_block"])
-            lw = None
-            if ln_weights is not None:
-                lw = hip.DeviceBuffer.from_array(ln_weights[l])
+            lw = hip.DeviceBuffer.from_array(ln_weights[l]) if ln_weights is not None else None
             self.bufs.append((rw, bb, sb, lw))
             self.ctx.set_layer(l, rw.ptr, bb.ptr, lw.ptr if lw else None, sb.ptr)
         hip.synchronize()
 
-    def oracle_cfg(self):
-        return self.c
+    def close(self):
+        self.ctx.close()
+        self.bufs = []
 
 
 def make_io(H):

@@ -9,7 +9,7 @@ import os
 import re
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libwindlass_moe.so")
+LIB_PATH = os.environ.get("WINDLASS_MOE_LIB") or os.path.join(HERE, "libwindlass_moe.so")
 HEADER = os.path.join(os.path.dirname(HERE), "include", "windlass_moe.h")
 
 WL_OK = 0
