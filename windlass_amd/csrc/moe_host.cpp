@@ -32,29 +32,30 @@ struct wl_ctx {
     uint32_t SI = 0;
     int device = 0;
     int n_cu = 0;
-    int occ = 1;
     int32_t sched = WL_SCHED_FUSED;
     std::vector<LayerState> layers;
     std::vector<const uint8_t*> h_slot;   // [L*E]
     std::vector<uint32_t> n_bound;        // bound experts per layer
     const uint8_t** d_slot = nullptr;     // [L*E]
     wl::DecodeArgs* d_largs = nullptr;    // [L] per-layer kernel records
-    // scratch
+    // intermediates kept for inspection (ordinary device memory)
     float* norm = nullptr;
-    float* logits = nullptr;
+    float* smid = nullptr;
+    float* rmid = nullptr;
     int32_t* idx = nullptr;
     float* topw = nullptr;
-    const uint8_t** sel = nullptr;
-    float* rmid = nullptr;
-    uint16_t* rmid_p = nullptr;
-    float* smid = nullptr;
-    uint16_t* smid_p = nullptr;
     float* shared_out = nullptr;
     float* edown = nullptr;
-    float* part_r = nullptr;
-    float* part_s = nullptr;
+    uint16_t* ffn_mid_p = nullptr;  // wl_expert_ffn's SwiGLU pieces
+    // cross-work-group arrays (uncached)
+    float* logits = nullptr;
+    uint16_t* smid_p = nullptr;
+    float* part = nullptr;
+    float* sdpart = nullptr;
     uint32_t* sync = nullptr;
     wl::SyncMap sm{};
+    wl::Plan plan{};
+    uint32_t grid = 0;
     uint32_t epoch = 0;
     void* uc_block = nullptr;   // uncached scratch (returned to the process pool on destroy)
     size_t uc_bytes = 0;
@@ -129,11 +130,12 @@ wl_status validate_cfg(const wl_moe_config* cfg, wl_ctx* c) {
                    K = cfg->n_experts_per_tok;
     if (H == 0 || H % 128) return fail(c, WL_ERR_INVALID, "hidden=%u must be a positive multiple of 128", H);
     if (I == 0 || I % 128) return fail(c, WL_ERR_INVALID, "moe_inter=%u must be a positive multiple of 128", I);
+    if ((uint64_t)I * cfg->n_shared > 65536) return fail(c, WL_ERR_INVALID, "shared inter %u too large", I * cfg->n_shared);
     if (E == 0 || E % 16 || E > 4096) return fail(c, WL_ERR_INVALID, "n_routed_experts=%u must be a multiple of 16 in [16,4096]", E);
     if (K == 0 || K > WL_MAX_TOPK || K > E) return fail(c, WL_ERR_INVALID, "n_experts_per_tok=%u must be in [1,min(%d,E)]", K, WL_MAX_TOPK);
     if (cfg->n_shared == 0 || cfg->n_shared > 16) return fail(c, WL_ERR_INVALID, "n_shared=%u must be in [1,16]", cfg->n_shared);
     if (cfg->n_layers == 0 || cfg->n_layers > 4096) return fail(c, WL_ERR_INVALID, "n_layers=%u must be in [1,4096]", cfg->n_layers);
-    if (H > 16384) return fail(c, WL_ERR_INVALID, "hidden=%u exceeds 16384", H);
+    if (H > 8192) return fail(c, WL_ERR_INVALID, "hidden=%u exceeds 8192", H);
     return WL_OK;
 }
 
@@ -152,18 +154,16 @@ wl::DecodeArgs layer_record(const wl_ctx* c, uint32_t layer) {
     a.sh_down = sh + (size_t)2 * SI * H;
     a.slot_tab = c->d_slot + (size_t)layer * E;
     a.norm = c->norm;
-    a.logits = c->logits;
+    a.smid = c->smid;
+    a.rmid = c->rmid;
     a.idx = c->idx;
     a.topw = c->topw;
-    a.sel = c->sel;
-    a.rmid = c->rmid;
-    a.rmid_p = c->rmid_p;
-    a.smid = c->smid;
-    a.smid_p = c->smid_p;
     a.shared_out = c->shared_out;
     a.edown = c->edown;
-    a.part_r = c->part_r;
-    a.part_s = c->part_s;
+    a.logits = c->logits;
+    a.smid_p = c->smid_p;
+    a.part = c->part;
+    a.sdpart = c->sdpart;
     a.sync = c->sync;
     a.gw_off = c->lay.gw_off;
     a.gs_off = c->lay.gs_off;
@@ -171,6 +171,7 @@ wl::DecodeArgs layer_record(const wl_ctx* c, uint32_t layer) {
     a.us_off = c->lay.us_off;
     a.dw_off = c->lay.dw_off;
     a.ds_off = c->lay.ds_off;
+    a.blk_bytes = c->lay.total;
     a.H = H;
     a.I = c->cfg.moe_inter;
     a.E = E;
@@ -220,22 +221,37 @@ wl_status wl_create(const wl_moe_config* cfg, wl_ctx** out) {
     c->n_cu = prop.multiProcessorCount;
     const uint32_t H = cfg->hidden, I = cfg->moe_inter, E = cfg->n_routed_experts,
                    K = cfg->n_experts_per_tok, L = cfg->n_layers, SI = c->SI;
-    int occ = 0;
-    if (wl::decode_occupancy(H, E, &occ) != 0 || occ < 1) occ = 1;
-    const char* env = getenv("WL_DECODE_WG_PER_CU");
-    if (env && atoi(env) > 0) occ = atoi(env) < occ ? atoi(env) : occ;
-    else if (occ > 2) occ = 2;
-    c->occ = occ;
+    // one work-group per CU (all resident at once: the fused launch has grid
+    // barriers), a multiple of 8 so every XCD holds the same number
+    uint32_t grid = (uint32_t)c->n_cu;
+    if (const char* env = getenv("WL_DECODE_GRID")) {
+        const int gv = atoi(env);
+        if (gv > 0 && gv < (int)grid) grid = (uint32_t)gv;
+    }
+    if (grid > wl::kMaxGrid) grid = wl::kMaxGrid;
+    if (grid >= 16) grid &= ~7u;
+    c->grid = grid;
+    c->plan = wl::Plan::make(H, I, SI, K, grid);
+    const wl::LdsMap lm = wl::LdsMap::make(H, SI, E, K, c->plan);
+    if ((int)lm.bytes > wl::decode_max_lds()) {
+        delete c;
+        return WL_ERR_INVALID;
+    }
 
     c->layers.resize(L);
     c->h_slot.assign((size_t)L * E, nullptr);
     c->n_bound.assign(L, 0);
-    c->sm = wl::SyncMap::make(H, I, E, K, SI);
+    c->sm = wl::SyncMap::make();
     if ((s = dalloc(c, &c->d_slot, sizeof(void*) * (size_t)L * E)) != WL_OK ||
         (s = dalloc(c, &c->d_largs, sizeof(wl::DecodeArgs) * (size_t)L)) != WL_OK ||
         (s = dalloc(c, &c->norm, 4 * (size_t)H)) != WL_OK ||
+        (s = dalloc(c, &c->smid, 4 * (size_t)SI)) != WL_OK ||
         (s = dalloc(c, &c->rmid, 4 * (size_t)K * I)) != WL_OK ||
-        (s = dalloc(c, &c->smid, 4 * (size_t)SI)) != WL_OK) {
+        (s = dalloc(c, &c->idx, 4 * (size_t)WL_MAX_TOPK)) != WL_OK ||
+        (s = dalloc(c, &c->topw, 4 * (size_t)WL_MAX_TOPK)) != WL_OK ||
+        (s = dalloc(c, &c->shared_out, 4 * (size_t)H)) != WL_OK ||
+        (s = dalloc(c, &c->edown, 4 * (size_t)K * H)) != WL_OK ||
+        (s = dalloc(c, &c->ffn_mid_p, 2 * 3 * (size_t)I)) != WL_OK) {
         wl_destroy(c);
         return s;
     }
@@ -246,15 +262,9 @@ wl_status wl_create(const wl_moe_config* cfg, wl_ctx** out) {
         auto carve = [&](size_t bytes) { size_t o = off; off += (bytes + 255) / 256 * 256; return o; };
         const size_t o_sync = carve(4 * (size_t)c->sm.words);
         const size_t o_logits = carve(4 * (size_t)E);
-        const size_t o_idx = carve(4 * (size_t)WL_MAX_TOPK);
-        const size_t o_topw = carve(4 * (size_t)WL_MAX_TOPK);
-        const size_t o_sel = carve(sizeof(void*) * (size_t)WL_MAX_TOPK);
-        const size_t o_part_r = carve(4 * (size_t)(E / 16) * 4 * 16);
-        const size_t o_part_s = carve(4 * (size_t)(SI / 16) * 4 * 32);
-        const size_t o_rmid_p = carve(2 * 3 * (size_t)K * I);
         const size_t o_smid_p = carve(2 * 3 * (size_t)SI);
-        const size_t o_shared = carve(4 * (size_t)H);
-        const size_t o_edown = carve(4 * (size_t)K * H);
+        const size_t o_part = carve(4 * (size_t)c->plan.U * H);
+        const size_t o_sdpart = carve(4 * (size_t)c->plan.KS * H);
         c->uc_bytes = off;
         c->uc_block = uc_acquire(c->device, off);
         if (!c->uc_block) {
@@ -264,15 +274,9 @@ wl_status wl_create(const wl_moe_config* cfg, wl_ctx** out) {
         uint8_t* b = (uint8_t*)c->uc_block;
         c->sync = (uint32_t*)(b + o_sync);
         c->logits = (float*)(b + o_logits);
-        c->idx = (int32_t*)(b + o_idx);
-        c->topw = (float*)(b + o_topw);
-        c->sel = (const uint8_t**)(b + o_sel);
-        c->part_r = (float*)(b + o_part_r);
-        c->part_s = (float*)(b + o_part_s);
-        c->rmid_p = (uint16_t*)(b + o_rmid_p);
         c->smid_p = (uint16_t*)(b + o_smid_p);
-        c->shared_out = (float*)(b + o_shared);
-        c->edown = (float*)(b + o_edown);
+        c->part = (float*)(b + o_part);
+        c->sdpart = (float*)(b + o_sdpart);
     }
     e = hipMemset(c->d_slot, 0, sizeof(void*) * (size_t)L * E);
     if (e == hipSuccess) e = hipMemset(c->uc_block, 0, c->uc_bytes);
@@ -375,30 +379,23 @@ static wl_status run_layer(wl_ctx* c, uint32_t layer, const float* d_hidden, con
         return fail(c, WL_ERR_NOT_RESIDENT, "layer %u has %u of %u experts bound", layer, c->n_bound[layer], E);
 
     wl::DecodeDyn dyn{};
-    if (++c->epoch == 0) c->epoch = 1;
+    if (++c->epoch >= 0x7FFFFFFFu) c->epoch = 1;
     dyn.epoch = c->epoch;
     dyn.hidden = d_hidden;
     dyn.resid = d_resid;
     dyn.out = d_out;
-
-    const wl::TaskMap tm = wl::TaskMap::make(H, I, E, K, SI);
-    const uint32_t slots = (uint32_t)(c->n_cu * c->occ);
-    auto launch = [&](uint32_t lo, uint32_t hi, int wait, int tap) -> wl_status {
-        dyn.task_lo = lo;
-        dyn.task_hi = hi;
-        dyn.wait_deps = wait;
-        dyn.write_norm_tap = tap;
-        const uint32_t n = hi - lo;
-        const uint32_t grid = n < slots ? n : slots;
-        int e = wl::launch_decode(c->d_largs + layer, dyn, H, E, grid, stream);
+    auto launch = [&](uint32_t lo, uint32_t hi) -> wl_status {
+        dyn.seg_lo = lo;
+        dyn.seg_hi = hi;
+        int e = wl::launch_decode(c->d_largs + layer, dyn, H, I, SI, E, K, c->grid, stream);
         if (e != 0) return hip_fail(c, (hipError_t)e, "decode launch");
         return WL_OK;
     };
-    if (c->sched == WL_SCHED_FUSED) return launch(0, tm.total, 1, 1);
+    if (c->sched == WL_SCHED_FUSED) return launch(0, 2);
     wl_status s;
-    if ((s = launch(0, tm.oRG, 0, 1)) != WL_OK) return s;
-    if ((s = launch(tm.oRG, tm.oRD, 0, 0)) != WL_OK) return s;
-    return launch(tm.oRD, tm.total, 0, 0);
+    if ((s = launch(0, 0)) != WL_OK) return s;
+    if ((s = launch(1, 1)) != WL_OK) return s;
+    return launch(2, 2);
 }
 
 wl_status wl_run_moe(wl_ctx* c, uint32_t layer, const float* d_hidden, float* d_out, void* stream) {
@@ -454,8 +451,9 @@ wl_status wl_check_error(wl_ctx* c, void* stream) {
     e = hipMemcpy(&flag, c->sync + c->sm.error, 4, hipMemcpyDeviceToHost);
     if (e != hipSuccess) return hip_fail(c, e, "error flag read");
     if (flag) {
-        const uint32_t zero = 0;
-        hipMemcpy(c->sync + c->sm.error, &zero, 4, hipMemcpyHostToDevice);
+        // a launch that gave up may have left barrier counters mid-count
+        hipMemset(c->sync, 0, 4 * (size_t)c->sm.words);
+        hipDeviceSynchronize();
         return fail(c, WL_ERR_DEVICE, "device error bits 0x%x%s%s", flag,
                     (flag & wl::E_SPIN) ? " [dependency wait expired]" : "",
                     (flag & wl::E_NOT_RESIDENT) ? " [routed expert not resident]" : "");
@@ -484,7 +482,7 @@ wl_status wl_expert_ffn(wl_ctx* c, const uint8_t* d_block, const float* d_x, flo
     if (!d_block || !d_x || !d_y) return fail(c, WL_ERR_INVALID, "null block/x/y");
     int e = wl::launch_expert_ffn(d_block, c->lay.gw_off, c->lay.gs_off, c->lay.uw_off, c->lay.us_off,
                                   c->lay.dw_off, c->lay.ds_off, d_x, c->cfg.hidden, c->cfg.moe_inter,
-                                  c->rmid, c->rmid_p, d_y, d_y_bf16, stream);
+                                  c->rmid, c->ffn_mid_p, d_y, d_y_bf16, stream);
     if (e != 0) return hip_fail(c, (hipError_t)e, "expert ffn launch");
     return WL_OK;
 }
