@@ -107,6 +107,7 @@ def main():
     t_build = time.time()
     dm = DeviceModel(c, seed=args.seed, n_layers=args.layers)
     dm.ctx.set_schedule(moe.SCHED_FUSED if args.sched == "fused" else moe.SCHED_PHASED)
+    dm.ctx.set_taps(False)  # the shared-expert output tap is a test hook
     n_h = 64
     hs = np.stack([synthdata.hidden_state(H, 5000 + i) for i in range(n_h)])
     d_hs = hip.DeviceBuffer.from_array(hs)

@@ -81,8 +81,10 @@ const char* wl_last_error(const wl_ctx* ctx);
 #define WL_SHARED_MXFP4 1   /* one packed block in wl_expert_layout order, inter = SI */
 
 /* Binds the non-expert weights of MoE layer `layer` (0-based within the
- * context). Pointers are caller-owned and must stay valid while the layer is
- * run. Replaces the MoE fields of glm::LayerWeights (src/glm_loader.cuh:
+ * context). Router, bias and norm pointers are caller-owned and must stay
+ * valid while the layer is run; the shared expert is copied (into the native
+ * layout, in context-owned memory) during the call, which synchronises the
+ * device. Replaces the MoE fields of glm::LayerWeights (src/glm_loader.cuh:
  * 259-339): router_w [E,H] bf16, router_bias [E] f32 (e_score_correction_bias,
  * kept f32 on purpose), post_attn_ln [H] bf16 (NULL = all ones), shared expert
  * block as above. */
@@ -95,11 +97,22 @@ wl_status wl_set_layer(wl_ctx* ctx, uint32_t layer, const uint16_t* d_router_w,
  * The device keeps a table slot_of[layer][expert] -> block pointer, and the
  * decode kernel resolves routed ids through it on the device, so no host
  * round-trip (src/glm_layer_runner.cuh:393-396) is needed when every expert
- * of the layer is bound. */
-wl_status wl_slot_bind(wl_ctx* ctx, uint32_t layer, uint32_t expert, const uint8_t* d_block);
+ * of the layer is bound.
+ *
+ * Bound blocks are in the NATIVE layout (wl_native_block_bytes bytes): the
+ * same bytes as the reference's packed block, reordered so that each 16-byte
+ * load of a GPU wave is one lane of a contiguous 1 KB chunk and the E8M0
+ * scales of 16 k tiles of one lane are one 16-byte chunk. Convert a
+ * reference-layout block with wl_expert_to_native (the conversion the
+ * reference's loader would run when it fills a VRAM slot,
+ * src/glm_expert_cache.cuh:394-433). */
+size_t    wl_native_block_bytes(const wl_moe_config* cfg);
+wl_status wl_expert_to_native(const wl_moe_config* cfg, const uint8_t* d_ref_block, uint8_t* d_native_block,
+                              void* stream);
+wl_status wl_slot_bind(wl_ctx* ctx, uint32_t layer, uint32_t expert, const uint8_t* d_native_block);
 wl_status wl_slot_unbind(wl_ctx* ctx, uint32_t layer, uint32_t expert);
-/* Allocates a context-owned pool of n_slots expert blocks (one hipMalloc, like
- * ExpertCache's pool, src/glm_expert_cache.cuh:150-156). */
+/* Allocates a context-owned pool of n_slots native expert blocks (one
+ * hipMalloc, like ExpertCache's pool, src/glm_expert_cache.cuh:150-156). */
 wl_status wl_slot_pool_create(wl_ctx* ctx, uint32_t n_slots);
 wl_status wl_slot_pool_ptr(wl_ctx* ctx, uint32_t slot, uint8_t** d_block);
 
@@ -134,7 +147,7 @@ typedef struct wl_taps_out {
     const int32_t* topk_idx; /* [K]  selected experts, descending biased score */
     const float*   topk_w;   /* [K]  routing weights */
     const float*   mid;      /* [K, I] routed SwiGLU outputs */
-    const float*   shared;   /* [H]  shared expert output */
+    const float*   shared;   /* [H]  shared expert output (when taps are on) */
 } wl_taps_out;
 wl_status wl_taps(wl_ctx* ctx, wl_taps_out* out);
 
@@ -143,11 +156,20 @@ wl_status wl_taps(wl_ctx* ctx, wl_taps_out* out);
 wl_status wl_check_error(wl_ctx* ctx, void* stream);
 
 /* Execution schedule of wl_run_moe: WL_SCHED_FUSED runs one persistent
- * task-queue kernel per layer; WL_SCHED_PHASED runs the same tasks as three
- * stream-ordered launches. Both compute identical results. */
+ * kernel per layer (a grid barrier before the final combine); WL_SCHED_PHASED
+ * runs the combine as a second stream-ordered launch. Both compute identical
+ * results. */
 #define WL_SCHED_FUSED  0
 #define WL_SCHED_PHASED 1
 wl_status wl_set_schedule(wl_ctx* ctx, int32_t sched);
+
+/* Whether wl_run_moe also produces the shared-expert output tap (wl_taps_out.
+ * shared). The other taps are always written. The shared expert's
+ * contribution is otherwise only kept summed into the layer output, so the tap
+ * costs one extra H-vector per work-group; off for benchmarking. Default: on
+ * (the reference's run_moe leaves every intermediate in its scratch,
+ * src/glm_layer_runner.cuh:431-436). */
+wl_status wl_set_taps(wl_ctx* ctx, int32_t enable);
 
 /* ---- single-expert building blocks ---------------------------------------
  * y[N] = W . x for MXFP4 W ([N,K/2] packed nibbles + [N,K/32] E8M0 scales) and
@@ -173,6 +195,10 @@ wl_status wl_expert_ffn(wl_ctx* ctx, const uint8_t* d_block, const float* d_x, f
  * the same bytes. */
 wl_status wl_synth_expert(const wl_moe_config* cfg, uint32_t inter, uint32_t seed,
                           uint32_t layer, uint32_t expert, uint8_t* d_block, void* stream);
+/* The same synthetic expert written directly in the native layout (equal to
+ * wl_expert_to_native of wl_synth_expert's block). */
+wl_status wl_synth_expert_native(const wl_moe_config* cfg, uint32_t seed, uint32_t layer, uint32_t expert,
+                                 uint8_t* d_native_block, void* stream);
 
 #ifdef __cplusplus
 }

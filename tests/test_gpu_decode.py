@@ -230,3 +230,26 @@ def test_not_resident_is_an_error(gpu):
         dm.ctx.run_moe(0, dh.ptr, dout.ptr)
     assert ei.value.status == 4
     dm.ctx.close()
+
+
+@pytest.mark.parametrize("shape", [(256, 128), (384, 256), (6144, 2048)])
+def test_native_layout(gpu, shape):
+    """wl_synth_expert_native == wl_expert_to_native(wl_synth_expert block) ==
+    the numpy restatement of the native layout (oracle/native_layout.py)."""
+    from oracle import native_layout
+    hip = gpu
+    H, I = shape
+    cfg = moe.make_config(hidden=H, moe_inter=I)
+    lay = moe.expert_layout(cfg)
+    nbytes = moe.native_block_bytes(cfg)
+    assert nbytes == sum(native_layout.native_sizes(H, I))
+    ref = hip.DeviceBuffer(lay.total)
+    nat1, nat2 = hip.DeviceBuffer(nbytes), hip.DeviceBuffer(nbytes)
+    moe.synth_expert(cfg, 5, 1, 7, ref.ptr)
+    moe.expert_to_native(cfg, ref.ptr, nat1.ptr)
+    moe.synth_expert_native(cfg, 5, 1, 7, nat2.ptr)
+    hip.synchronize()
+    a, b = nat1.download(np.uint8), nat2.download(np.uint8)
+    assert np.array_equal(a, b)
+    want = native_layout.to_native(synth.expert_block(H, I, 5, 1, 7), H, I)
+    assert np.array_equal(a, want)

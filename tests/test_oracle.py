@@ -201,3 +201,24 @@ def test_product_and_oracle_input_recipes_agree():
         assert np.array_equal(a[k], b[k]), k
     assert np.array_equal(synthdata.hidden_state(256, 3, 1), synth.hidden_state(256, 3, 1))
     assert np.array_equal(synthdata.zipf_bias_offset(64, 4), synth.zipf_bias_offset(64, 4))
+
+
+@pytest.mark.parametrize("shape", [(256, 128), (384, 256), (6144, 2048)])
+def test_native_layout_is_a_reordering(shape):
+    """The native layout restatement moves every weight byte exactly once and
+    puts every real scale byte of a lane's row where the kernel reads it."""
+    from oracle import native_layout
+    H, I = shape
+    parts = synth.expert_block(H, I, 5, 1, 7)
+    nat = native_layout.to_native(parts, H, I)
+    gu, gus, dn, dns = native_layout.native_sizes(H, I)
+    assert nat.size == gu + gus + dn + dns
+    assert np.array_equal(np.sort(nat[:gu]), np.sort(np.concatenate([parts[0].ravel(), parts[2].ravel()])))
+    assert np.array_equal(np.sort(nat[gu + gus:gu + gus + dn]), np.sort(parts[4].ravel()))
+    # lane (n=3, g=2) of tile 1, k tile 1: gate row 11, bytes [64 + 32, +16)
+    nkt = H // 128
+    chunk = nat[(1 * nkt + 1) * 1024:(1 * nkt + 2) * 1024].reshape(64, 16)
+    assert np.array_equal(chunk[2 * 16 + 3], parts[0][11, 96:112])
+    # its scale: byte 1 of lane 35's chunk in tile 1's first scale chunk = gate_s[11, 4*1 + 2]
+    sc = nat[gu + 1 * ((nkt + 15) // 16) * 1024:][:1024].reshape(64, 16)
+    assert sc[35, 1] == parts[1][11, 6]

@@ -19,14 +19,19 @@ constexpr uint32_t kSlice = 64;
 // Largest grid the synchronisation block is sized for.
 constexpr uint32_t kMaxGrid = 2048;
 
-// Cross-work-group data of one decode layer lives in uncached device memory
-// (MTYPE UC: loads and stores go to the memory side, never into a per-XCD L2),
-// so a producer never needs an L2 write-back fence — measured on MI355X, one
-// agent-scope release per work-group cut streaming from 5.2 to 0.9 TB/s — and
-// a consumer's load always sees the latest value.
+// Cross-work-group data of one layer (logits, shared SwiGLU values, partial
+// sums) is ordinary device memory written with agent-scope (sc1) stores, which
+// write through the writer's L2, and read with agent-scope (sc1) loads, which
+// never return a line cached in a per-CU L1 or per-XCD L2 — measured on
+// MI355X: plain loads after a grid barrier return stale data for the other
+// XCDs, sc1 loads never did, and an L2 invalidate per work-group costs ~14 us.
+// A release fence (L2 write-back) is never needed; one per work-group cut
+// streaming from 5.2 to 0.9 TB/s.
 //
-// Counters and release words each own a 128-byte line: read-modify-writes on
-// one line serialise (about 15 ns each).
+// The barrier words (counters, release words, error bits) live in uncached
+// memory so that read-modify-writes from all XCDs meet at one point. Counters
+// and release words each own a 128-byte line: read-modify-writes on one line
+// serialise (about 15 ns each).
 constexpr uint32_t kLineWords = 32;
 
 // Error bits reported in the error word.
@@ -57,23 +62,25 @@ struct SyncMap {
 // Work decomposition of one layer over G work-groups (identical on host and
 // device).
 //   router rows      E rows, row r on work-group r mod G
-//   shared gate/up   SI/8 tiles of 8 gate + 8 up rows, tile t on t mod G
-//   shared down      (H/16 row tiles) x KS k-splits, unit v on v mod G
+//   shared expert    SI/8 tiles of 8 gate + 8 up rows; the work-group of tile t
+//                    also applies columns [8t, 8t+8) of the down projection
 //   routed units     K experts x S = I/64 slices, unit u = (k = u mod K,
 //                    j = u / K) on u mod G: rows [64j, 64j+64) of gate/up and
-//                    columns [64j, 64j+64) of down; the partial down product
-//                    of every unit is an H-vector in `part`
-//   reduction        rows [RB*w, RB*w + RB) on work-group w
+//                    columns [64j, 64j+64) of down
+//   partials         every work-group's w_k-weighted routed and shared
+//                    contributions, summed per output row in LDS, published as
+//                    one H-vector per work-group
+//   combine          H/32 blocks of 32 rows, block b on b mod G
+constexpr uint32_t kRowBlock = 32;  // rows per combine block (= rows per down item)
 struct Plan {
-    uint32_t G, S, U, KS, NSD, RB;
+    uint32_t G, S, U, NB;
     __host__ __device__ static Plan make(uint32_t H, uint32_t I, uint32_t SI, uint32_t K, uint32_t G) {
+        (void)SI;
         Plan p;
         p.G = G;
         p.S = I / kSlice;
         p.U = K * p.S;
-        p.KS = (SI % 64u == 0u) ? 2u : 1u;
-        p.NSD = (H / 16u) * p.KS;
-        p.RB = (H + G - 1u) / G;
+        p.NB = H / kRowBlock;
         return p;
     }
 };
@@ -82,61 +89,113 @@ struct DecodeArgs {
     const uint16_t* ln_w;       // [H] bf16 or null (= ones)
     const uint16_t* router_w;   // [E][H] bf16
     const float* bias;          // [E] f32
-    const uint16_t* sh_gate;    // [SI][H] bf16
-    const uint16_t* sh_up;      // [SI][H] bf16
-    const uint16_t* sh_down;    // [H][SI] bf16
+    const uint8_t* sh_native;   // shared expert, NativeShared layout
     const uint8_t* const* slot_tab;  // [E] block pointers of this layer
-    // intermediates kept for inspection (ordinary device memory)
+    // intermediates kept for inspection (ordinary stores, read after the launch)
     float* norm;                // [H]
+    float* logits;              // [E]
     float* smid;                // [SI] shared SwiGLU output
     float* rmid;                // [K][I] routed SwiGLU outputs, slot order
     int32_t* idx;               // [K]
     float* topw;                // [K]
-    float* shared_out;          // [H]
-    float* edown;               // [K][H] routed down outputs before weighting
-    // cross-work-group arrays (uncached)
-    float* logits;              // [E]
-    uint16_t* smid_p;           // [3][SI] bf16 pieces of smid
-    float* part;                // [U][H] routed partial down products
-    float* sdpart;              // [KS][H] shared-down partial sums
-    uint32_t* sync;             // synchronisation block (SyncMap)
-    // expert block layout (byte offsets)
-    uint64_t gw_off, gs_off, uw_off, us_off, dw_off, ds_off, blk_bytes;
+    float* shared_out;          // [H] (written when taps are on)
+    // cross-work-group arrays (agent-scope stores and loads)
+    uint64_t* lslot;            // [E] logit of this call: epoch << 32 | f32 bits
+    float* part;                // [H/32][G][32] partials, block-major
+    float* tsh;                 // [H/32][G][32] shared-expert partials (taps on)
+    uint32_t* sync;             // synchronisation block (SyncMap), uncached
     uint32_t H, I, E, K, SI;
     float eps, scaling;
     int32_t norm_topk;
 };
 
 // Per-call launch arguments (kernel arguments by value). A layer runs as
-// segments 0 (norm, router, shared gate/up), 1 (top-k, shared down, routed
-// experts) and 2 (combine); a fused launch runs [0, 2] with grid barriers
-// between segments, a phased schedule runs each segment as its own launch.
+// segment 0 (everything up to the published partials) and segment 1 (the
+// combine); a fused launch runs both with a grid barrier between them, the
+// phased schedule runs each as its own launch.
 struct DecodeDyn {
     const float* hidden;        // [H] pre-norm residual stream
     const float* resid;         // [H] or null: out = resid + moe
     float* out;                 // [H]
     uint32_t seg_lo, seg_hi;
-    uint32_t epoch;             // different for every call of the context
+    uint32_t epoch;             // different for every call of the context, never 0
+    int32_t taps;               // 1: also produce the shared-expert output tap
 };
 
 // Dynamic LDS layout of the decode kernel (byte offsets).
 struct LdsMap {
-    uint32_t xp, xn, smp, rmp, red, topk, slots, misc, bytes;
+    uint32_t xp, pv, rmp, red, topk, slots, misc, bytes;
     __host__ __device__ static LdsMap make(uint32_t H, uint32_t SI, uint32_t E, uint32_t K, const Plan& p) {
+        (void)SI;
+        (void)K;
         LdsMap m;
         auto al = [](uint32_t x) { return (x + 15u) & ~15u; };
         uint32_t o = 0;
         m.xp = o;   o += al(3u * (H + 8u) * 2u);
-        m.xn = o;   // normalised input (f32); later the combine's staging
-        const uint32_t fin = (p.U + p.KS + K) * p.RB * 4u;
-        o += al(H * 4u > fin ? H * 4u : fin);
-        m.smp = o;  o += al(3u * (SI + 8u) * 2u);
+        m.pv = o;   // normalised input; this work-group's partial; combine staging
+        uint32_t f32n = (p.G + 16u) * kRowBlock;
+        if (f32n < H) f32n = H;
+        o += al(f32n * 4u);
         m.rmp = o;  o += al(3u * (kSlice + 8u) * 2u);
         m.red = o;  o += kWaves * 64u * 4u;
         m.topk = o; o += al((2u * E + 64u) * 4u);
         m.slots = o; o += al(E * 8u);
-        m.misc = o; o += 64u;
+        m.misc = o; o += 128u;
         m.bytes = o;
+        return m;
+    }
+};
+
+// lowbias32 integer hash of the synthetic-weight generator (synth.hip).
+__host__ __device__ inline uint32_t mix32(uint32_t x) {
+    x ^= x >> 16;
+    x *= 0x7FEB352Du;
+    x ^= x >> 15;
+    x *= 0x846CA68Bu;
+    x ^= x >> 16;
+    return x;
+}
+
+// ---- native (HBM) layouts ----------------------------------------------------
+// Expert blocks bound to the decode kernel are stored so that every 16-byte
+// load of a wave is one lane of a 1 KB contiguous chunk, in the lane order the
+// MFMA operands want (lane l = (n, g) = (l % 16, l / 16)), and the E8M0 scales
+// of 16 consecutive k tiles (or row pairs) of one lane are one 16-byte chunk.
+// The reference layout (gate_w | gate_s | up_w | up_s | down_w | down_s, rows
+// of packed nibbles) is what callers provide; wl_expert_to_native converts.
+//
+//   gu   [I/8 tiles][H/128 k tiles] 1 KB: lane (n,g) = row n<8 ? gate 8T+n :
+//        up 8T+n-8, bytes [64kt + 16g, +16) of that row
+//   gus  [I/8 tiles][ceil(H/2048)] 1 KB: lane byte i = scale of the lane's
+//        row at k tile 16c + i, block 4kt + g (0 past the end)
+//   dn   [I/64 slices][H/32 row pairs] 1 KB: lane (n,g) = down row
+//        32q + n + 16(g>>1), bytes [32j + 16(g&1), +16)
+//   dns  [I/64 slices][ceil(H/512)] 1 KB: lane byte i = scale of the lane's
+//        row at pair 16c + i, block 2j + (g&1)
+struct NativeLayout {
+    uint64_t gu, gus, dn, dns, total;
+    __host__ __device__ static NativeLayout make(uint32_t H, uint32_t I) {
+        NativeLayout m;
+        uint64_t o = 0;
+        m.gu = o;  o += (uint64_t)(I / 8) * (H / 128) * 1024;
+        m.gus = o; o += (uint64_t)(I / 8) * ((H / 128 + 15) / 16) * 1024;
+        m.dn = o;  o += (uint64_t)(I / 64) * (H / 32) * 1024;
+        m.dns = o; o += (uint64_t)(I / 64) * ((H / 32 + 15) / 16) * 1024;
+        m.total = o;
+        return m;
+    }
+};
+// The shared expert (bf16) per layer:
+//   sgu  [SI/8 tiles][H/32 k tiles] 1 KB: lane (n,g) = row n<8 ? gate 8T+n :
+//        up 8T+n-8, columns [32kt + 8g, +8)
+//   sdn  [SI/8 tiles][H rows] 16 B: columns [8T, 8T+8) of down row r
+struct NativeShared {
+    uint64_t sgu, sdn, total;
+    __host__ __device__ static NativeShared make(uint32_t H, uint32_t SI) {
+        NativeShared m;
+        m.sgu = 0;
+        m.sdn = (uint64_t)(SI / 8) * (H / 32) * 1024;
+        m.total = m.sdn + (uint64_t)(SI / 8) * H * 16;
         return m;
     }
 };
@@ -151,6 +210,10 @@ int launch_expert_ffn(const uint8_t* blk, uint64_t gw_off, uint64_t gs_off, uint
                       uint64_t us_off, uint64_t dw_off, uint64_t ds_off, const float* x, uint32_t H,
                       uint32_t I, float* mid, uint16_t* mid_p, float* y, uint16_t* y_bf16,
                       void* stream);
+// Reference-layout block -> native block (src null: synthesise the native
+// block directly from the counter-based generator with `key`).
+int launch_expert_to_native(const uint8_t* src, uint8_t* dst, uint32_t H, uint32_t I, uint32_t key, void* stream);
+int launch_shared_to_native(const uint16_t* src, uint16_t* dst, uint32_t H, uint32_t SI, void* stream);
 int launch_synth_expert(uint8_t* d_block, uint64_t gw_off, uint64_t gw_len, uint64_t gs_off,
                         uint64_t gs_len, uint64_t uw_off, uint64_t uw_len, uint64_t us_off,
                         uint64_t us_len, uint64_t dw_off, uint64_t dw_len, uint64_t ds_off,

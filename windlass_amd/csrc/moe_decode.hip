@@ -19,7 +19,7 @@
 //          split-K partial of expert k's output over all H rows.
 //      reference: dequant_matvec_mxfp4 x3 + silu_mul, src/glm_kernels.cuh:63-110,
 //      src/glm_layer_runner.cuh:338-341,424-427
-//   2  every work-group combines RB output rows: e_k = sum_j partial(k, j),
+//   2  work-groups combine blocks of 32 output rows: e_k = sum_j partial(k, j),
 //      out = sum_k w_k e_k (slot order) + shared (src/glm_layer_runner.cuh:
 //      403,428,436).
 //
@@ -49,6 +49,20 @@
 #include "internal.h"
 
 namespace wl {
+
+// Diagnostic builds (-DWL_TIMELINE) record a 100 MHz timestamp per work-group
+// at each phase boundary; product builds compile WL_TL to nothing.
+#ifdef WL_TIMELINE
+__device__ uint64_t g_tl[kMaxGrid * 16];
+#define WL_TL(i)                                                                                  \
+    do {                                                                                          \
+        if (threadIdx.x == 0) g_tl[(size_t)blockIdx.x * 16 + (i)] = __builtin_amdgcn_s_memrealtime(); \
+    } while (0)
+#else
+#define WL_TL(i) \
+    do {         \
+    } while (0)
+#endif
 
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
 typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
@@ -108,6 +122,20 @@ WL_DEV u32x4 bld16(rsrc_t r, uint32_t voff, uint32_t soff) {
 }
 WL_DEV uint32_t bld1(rsrc_t r, uint32_t voff, uint32_t soff) {
     return __builtin_amdgcn_raw_buffer_load_b8(r, (int)voff, (int)soff, 0);
+}
+// Agent-scope (sc1) accesses for data one work-group writes and others read:
+// the store writes through the writer's L2, the load bypasses the reader's L1
+// and L2 (aux bit 4 of the buffer instructions is sc1).
+constexpr int kSC1 = 16;
+WL_DEV void st_ag(float* p, float v) {
+    __hip_atomic_store((__attribute__((address_space(1))) uint32_t*)p, __float_as_uint(v), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+}
+WL_DEV uint32_t bld4_ag(rsrc_t r, uint32_t voff, uint32_t soff) {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, kSC1);
+}
+WL_DEV u32x4 bld16_ag(rsrc_t r, uint32_t voff, uint32_t soff) {
+    return __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, kSC1);
 }
 // A value the compiler must treat as uniform across the wave (it is).
 WL_DEV uint32_t uni(uint32_t x) { return __builtin_amdgcn_readfirstlane(x); }
@@ -252,10 +280,18 @@ WL_DEV float block_sum(float v, float* red) {
 
 // ---- batches ------------------------------------------------------------
 constexpr int kNB = 8;
+static_assert(16 % kNB == 0, "a batch's scales must lie in one 16-byte chunk");
 struct Batch {
     u32x4 w[kNB];
-    uint32_t s[kNB];
+    u32x4 sv;  // the 16-byte scale chunk holding this batch's scales (MXFP4 streams)
 };
+// Scale byte of slot i of a batch whose first item is item0 (scale chunks hold
+// 16 consecutive items).
+WL_DEV uint32_t batch_scale(const Batch& B, uint32_t item0, int i) {
+    const uint32_t o = item0 % 16u + (uint32_t)i;
+    const uint32_t w = (o / 4u == 0u) ? B.sv.x : (o / 4u == 1u) ? B.sv.y : (o / 4u == 2u) ? B.sv.z : B.sv.w;
+    return (w >> (8u * (o % 4u))) & 0xFFu;
+}
 // Shared-down batch: kSPU k tiles of each of 3 units.
 constexpr uint32_t kSPU = 4;
 struct SdBatch {
@@ -301,16 +337,19 @@ WL_DEV void topk_score(float logit, float bias, uint32_t e, float* sc, float* ch
     sc[e] = s;
     ch[e] = c;
 }
+// Rank of every expert among the E choices (one thread per expert, the
+// choices read as broadcast 16-byte LDS loads, 16 in flight at a time).
 WL_DEV void topk_rank(uint32_t E, uint32_t K, const float* sc, const float* ch, uint32_t* sidx, float* sw) {
     for (uint32_t e = threadIdx.x; e < E; e += kThreads) {
         const float c = ch[e];
         uint32_t rank = 0;
+#pragma unroll 16
         for (uint32_t j = 0; j < E; j += 4) {
-            const float4 v = *(const float4*)(ch + j);
-            rank += (v.x > c || (v.x == c && j + 0 < e)) ? 1u : 0u;
-            rank += (v.y > c || (v.y == c && j + 1 < e)) ? 1u : 0u;
-            rank += (v.z > c || (v.z == c && j + 2 < e)) ? 1u : 0u;
-            rank += (v.w > c || (v.w == c && j + 3 < e)) ? 1u : 0u;
+            const float4 q = *(const float4*)(ch + j);
+            rank += (q.x > c || (q.x == c && j + 0 < e)) ? 1u : 0u;
+            rank += (q.y > c || (q.y == c && j + 1 < e)) ? 1u : 0u;
+            rank += (q.z > c || (q.z == c && j + 2 < e)) ? 1u : 0u;
+            rank += (q.w > c || (q.w == c && j + 3 < e)) ? 1u : 0u;
         }
         if (rank < K) {
             sidx[rank] = e;
@@ -319,6 +358,67 @@ WL_DEV void topk_rank(uint32_t E, uint32_t K, const float* sc, const float* ch, 
     }
     lds_barrier();
 }
+// Largest 64-bit key (hi, lo) over the 64 lanes, returned uniform. DPP row
+// shifts and row broadcasts (VALU only) leave the maximum in lane 63.
+WL_DEV bool key_gt(uint32_t ah, uint32_t al, uint32_t bh, uint32_t bl) { return ah > bh || (ah == bh && al > bl); }
+template <int CTRL, int ROWS>
+WL_DEV void key_step(uint32_t& h, uint32_t& l) {
+    const uint32_t oh = (uint32_t)__builtin_amdgcn_update_dpp((int)h, (int)h, CTRL, ROWS, 0xF, false);
+    const uint32_t ol = (uint32_t)__builtin_amdgcn_update_dpp((int)l, (int)l, CTRL, ROWS, 0xF, false);
+    const bool t = key_gt(oh, ol, h, l);
+    h = t ? oh : h;
+    l = t ? ol : l;
+}
+WL_DEV void wave_max_key(uint32_t& h, uint32_t& l) {
+    key_step<0xB1, 0xF>(h, l);   // quad_perm [1,0,3,2]
+    key_step<0x4E, 0xF>(h, l);   // quad_perm [2,3,0,1]
+    key_step<0x114, 0xF>(h, l);  // row_shr:4
+    key_step<0x118, 0xF>(h, l);  // row_shr:8
+    key_step<0x142, 0xA>(h, l);  // row_bcast:15
+    key_step<0x143, 0xC>(h, l);  // row_bcast:31
+    h = __builtin_amdgcn_readlane(h, 63);
+    l = __builtin_amdgcn_readlane(l, 63);
+}
+// Order-preserving map of a float to uint32 (NaN never reaches it).
+WL_DEV uint32_t fkey(float f) {
+    const uint32_t u = __float_as_uint(f);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+// E <= 256: K rounds of a wave-wide argmax (wave 0, 4 candidates per lane)
+// over keys (fkey(choice), ~e): the largest choice, ties to the lowest index,
+// i.e. the reference's K serial argmax passes (src/glm_layer_runner.cuh:318-330).
+WL_DEV void topk_argmax(uint32_t E, uint32_t K, const float* sc, const float* ch, uint32_t* sidx, float* sw) {
+    if (threadIdx.x < 64) {
+        const uint32_t lane = threadIdx.x;
+        uint32_t kh[4], kl[4];
+#pragma unroll
+        for (int m = 0; m < 4; m++) {
+            const uint32_t e = lane + 64u * m;
+            kh[m] = e < E ? fkey(ch[e]) : 0u;  // 0: below every real key (fkey(-inf) > 0)
+            kl[m] = ~e;
+        }
+        for (uint32_t k = 0; k < K; k++) {
+            uint32_t bh = kh[0], bl = kl[0];
+#pragma unroll
+            for (int m = 1; m < 4; m++) {
+                const bool t = key_gt(kh[m], kl[m], bh, bl);
+                bh = t ? kh[m] : bh;
+                bl = t ? kl[m] : bl;
+            }
+            wave_max_key(bh, bl);
+            const uint32_t e = ~bl;
+#pragma unroll
+            for (int m = 0; m < 4; m++)
+                if (lane + 64u * m == e) kh[m] = 0u;
+            if (lane == 0) {
+                sidx[k] = e;
+                sw[k] = sc[e];
+            }
+        }
+    }
+    lds_barrier();
+}
+
 // Routing weight of slot k: score / (sum of the K scores + 1e-20) x scaling.
 WL_DEV float topk_weight(const DecodeArgs& a, uint32_t K, const float* sw, uint32_t k) {
     float sum = 0.f;
@@ -328,30 +428,15 @@ WL_DEV float topk_weight(const DecodeArgs& a, uint32_t K, const float* sw, uint3
     return w * a.scaling;
 }
 
-// Shared down projection, any shape: units vu = w + G*i, one at a time, k
-// tiles spread over the waves, then a cross-wave sum (fixed order) per row.
-// Not on the GLM path (kept out of line so it does not add to the decode
-// kernel's register pressure).
-__device__ __noinline__ void sd_general(const DecodeArgs& a, const Plan& P, const uint16_t* smp, uint32_t sps,
-                                        float* red, uint32_t H, uint32_t SI, uint32_t w, uint32_t G) {
-    const uint32_t lane = threadIdx.x & 63, v = threadIdx.x >> 6, n = lane & 15, g = lane >> 4;
-    const uint32_t SIh = SI / P.KS, nkts = SIh / 32;
-    for (uint32_t vu = w; vu < P.NSD; vu += G) {
-        const uint32_t tr = vu / P.KS, h = vu % P.KS;
-        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-        for (uint32_t kt = v; kt < nkts; kt += kWaves) {
-            const u32x4 b = gld16(a.sh_down + (size_t)(16u * tr + n) * SI + h * SIh + kt * 32u + 8u * g);
-            acc = mma(a_lds(smp, sps, n, h * SIh + kt * 32u + 8u * g, true), as_bf16x8(b), acc);
-        }
-        if (lane < 16) red[v * 64 + n] = sum3(acc);
-        lds_barrier();
-        if (threadIdx.x < 16) {
-            float s = 0.f;
-            for (int wv = 0; wv < kWaves; wv++) s += red[wv * 64 + threadIdx.x];
-            gst(a.sdpart + (size_t)h * H + 16u * tr + threadIdx.x, s);
-        }
-        lds_barrier();
-    }
+// AND of a per-thread predicate over the work-group (LDS only).
+WL_DEV bool block_all(bool p, uint32_t* flags) {
+    const bool wv = __all(p);
+    if ((threadIdx.x & 63) == 0) flags[threadIdx.x >> 6] = wv ? 1u : 0u;
+    lds_barrier();
+    const uint4 f0 = *(const uint4*)flags, f1 = *(const uint4*)(flags + 4);
+    const bool r = (f0.x & f0.y & f0.z & f0.w & f1.x & f1.y & f1.z & f1.w) != 0u;
+    lds_barrier();
+    return r;
 }
 
 // ---- the decode kernel -------------------------------------------------------
@@ -372,10 +457,7 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const DecodeDyn d) {
     extern __shared__ __align__(16) uint8_t lds[];
     uint16_t* xp = (uint16_t*)(lds + L.xp);
     const uint32_t xps = H + 8;
-    float* xn = (float*)(lds + L.xn);
-    float* fin = xn;
-    uint16_t* smp = (uint16_t*)(lds + L.smp);
-    const uint32_t sps = SI + 8;
+    float* pv = (float*)(lds + L.pv);  // normalised input, then this work-group's partial, then combine staging
     uint16_t* rmp = (uint16_t*)(lds + L.rmp);
     constexpr uint32_t rps = kSlice + 8;
     float* red = (float*)(lds + L.red);
@@ -384,70 +466,19 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const DecodeDyn d) {
     uint32_t* tk_idx = (uint32_t*)(tk_ch + E);
     float* tk_w = (float*)(tk_idx + 32);
     const uint8_t** tk_blk = (const uint8_t**)(lds + L.slots);
-    uint32_t* misc = (uint32_t*)(lds + L.misc);
+    uint32_t* misc = (uint32_t*)(lds + L.misc);  // [0..8) vote flags, [8] barrier flag
+    float* smf = (float*)(misc + 16);           // [8] this tile's shared SwiGLU values
 
     Batch bA, bB;
-    SdBatch bP;
 
-    // ---- shared down: units vu = w + G*i ((16-row tile, k half) pairs).
-    // Fast path (at most 3 units per work-group and SI/KS <= 8*kSPU*32): one
-    // batch holds kSPU 32-wide k tiles of each unit for every wave (slot
-    // lu*kSPU + i: unit lu, k tile kSPU*v + i). Anything else runs sd_general.
-    const uint32_t SIh = SI / P.KS;        // k columns per unit
-    const uint32_t nkts = SIh / 32;        // k tiles per unit
-    const uint32_t sd_units = w < P.NSD ? cdiv(P.NSD - w, G) : 0u;
-    const bool sd_fast = sd_units <= 3u && nkts <= 8u * kSPU;
-    const rsrc_t sd_rs = make_rsrc(a.sh_down, H * SI * 2u);
-    const uint32_t sd_voff = (n * SI + 8u * g) * 2u;
-    uint32_t sd_s[3], sd_a[3];
-#pragma unroll
-    for (int lu = 0; lu < 3; lu++) {
-        const uint32_t vc = min(w + G * lu, P.NSD - 1u);
-        const uint32_t tr = vc / P.KS, h = vc % P.KS;
-        sd_s[lu] = uni((16u * tr * SI + h * SIh + kSPU * v * 32u) * 2u);
-        sd_a[lu] = uni(h * SIh + kSPU * v * 32u);
-    }
-    auto sd_issue = [&](SdBatch& B) {
-#pragma unroll
-        for (int lu = 0; lu < 3; lu++) {
-#pragma unroll
-            for (int i = 0; i < (int)kSPU; i++) B.w[lu * kSPU + i] = bld16(sd_rs, sd_voff + i * 64u, sd_s[lu]);
-        }
-    };
-    auto sd_consume_store = [&](const SdBatch& B) {
-        f32x4 sacc[3];
-#pragma unroll
-        for (int lu = 0; lu < 3; lu++) {
-            sacc[lu] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int i = 0; i < (int)kSPU; i++) {
-                const bool valid = (uint32_t)lu < sd_units && kSPU * v + i < nkts;
-                const u32x4 z = {0u, 0u, 0u, 0u};
-                sacc[lu] = mma(a_lds(smp, sps, n, sd_a[lu] + i * 32u + 8u * g, valid),
-                               as_bf16x8(valid ? B.w[lu * kSPU + i] : z), sacc[lu]);
-            }
-        }
-        if (lane < 16) {
-#pragma unroll
-            for (int lu = 0; lu < 3; lu++) red[v * 64 + lu * 16 + n] = sum3(sacc[lu]);
-        }
-        lds_barrier();
-        if (tid < 48) {
-            const uint32_t lu = tid / 16, row = tid % 16;
-            const uint32_t vu = w + G * lu;
-            if (lu < sd_units) {
-                float s = 0.f;
-#pragma unroll
-                for (int wv = 0; wv < kWaves; wv++) s += red[wv * 64 + tid];
-                const uint32_t tr = vu / P.KS, h = vu % P.KS;
-                gst(a.sdpart + (size_t)h * H + 16u * tr + row, s);
-            }
-        }
-        lds_barrier();
-    };
-
-    // ================= segment 0: norm, router row, shared gate/up ==============
+    // ================= segment 0: everything but the combine ====================
     if (d.seg_lo == 0u) {
+        WL_TL(0);
+        // routing inputs that do not depend on this call's data, for experts
+        // e = tid (E <= 512; the rest later): consumed long after they land
+        const rsrc_t bs_rs = make_rsrc(a.bias, E * 4u), sl_rs = make_rsrc(a.slot_tab, E * 8u);
+        const uint32_t bias0 = __builtin_amdgcn_raw_buffer_load_b32(bs_rs, (int)(4u * tid), 0, 0);
+        const uint64_t slot0 = __builtin_bit_cast(uint64_t, __builtin_amdgcn_raw_buffer_load_b64(sl_rs, (int)(8u * tid), 0, 0));
         // hidden state and norm weight first: they are consumed first
         constexpr int HV = 4;  // float4 per thread: H <= 8192
         float4 hv[HV];
@@ -463,23 +494,30 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const DecodeDyn d) {
         // the first router row of this work-group
         constexpr int RCH = 2;  // 16-byte chunks per thread: H <= 8192
         const uint32_t nch = H / 8;
-        const uint32_t r0 = min(w, E - 1u);
         const rsrc_t rt_rs = make_rsrc(a.router_w, E * H * 2u);
         u32x4 rw[RCH];
 #pragma unroll
-        for (int m = 0; m < RCH; m++) rw[m] = bld16(rt_rs, 16u * min(tid + kThreads * m, nch - 1u), r0 * H * 2u);
-        // shared gate/up: tiles t = w + G*i of SI/8; items are 32-wide k tiles
+        for (int m = 0; m < RCH; m++) rw[m] = bld16(rt_rs, 16u * min(tid + kThreads * m, nch - 1u), min(w, E - 1u) * H * 2u);
+
+        // shared gate/up tiles (8 gate + 8 up rows). At G = SI/8 (GLM) the
+        // tiles are mapped so that the 32 work-groups of one XCD hold 32
+        // consecutive tiles: their down-projection columns share lines.
         const uint32_t nsg = SI / 8, nkt = H / 32;
+        const bool xcd_map = nsg == G && (G & 7u) == 0u;
+        auto tile_of = [&](uint32_t i) {  // i-th tile of this work-group
+            const uint32_t t = w + G * i;
+            return xcd_map ? (w & 7u) * (G / 8u) + (w >> 3) : t;
+        };
         const uint32_t sg_per = cdiv(nkt, 8u);  // k tiles per wave: [v*sg_per, +sg_per)
         const uint32_t sg_nb = at_least2(cdiv(sg_per, (uint32_t)kNB));
-        // gate and up are adjacent in the shared block: one resource covers both
-        const rsrc_t sg_rs = make_rsrc(a.sh_gate, 2u * SI * H * 2u);
+        // native shared expert: tile T, k tile kt is the 1 KB chunk T*(H/32)+kt
+        const NativeShared NS = NativeShared::make(H, SI);
+        const rsrc_t sg_rs = make_rsrc(a.sh_native + NS.sgu, (uint32_t)(NS.sdn - NS.sgu));
         auto sg_issue = [&](uint32_t tile, uint32_t b, Batch& B) {
-            const uint32_t row = min(tile, nsg - 1u) * 8u + (n & 7u);
-            const uint32_t voff = ((n < 8 ? 0u : SI * H) + row * H + 8u * g) * 2u;
+            const uint32_t voff = min(tile, nsg - 1u) * nkt * 1024u + 16u * lane;
             const uint32_t kt0 = v * sg_per + b * kNB;
 #pragma unroll
-            for (int i = 0; i < kNB; i++) B.w[i] = bld16(sg_rs, voff + i * 64u, kt0 * 64u);
+            for (int i = 0; i < kNB; i++) B.w[i] = bld16(sg_rs, voff, (kt0 + i) * 1024u);
         };
         f32x4 gacc;
         auto sg_consume = [&](uint32_t b, const Batch& B) {
@@ -491,8 +529,32 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const DecodeDyn d) {
                 gacc = mma(a_lds(xp, xps, n, kt * 32u + 8u * g, valid), as_bf16x8(valid ? B.w[i] : z), gacc);
             }
         };
-        sg_issue(w, 0, bA);
-        sg_issue(w, 1, bB);
+        // shared down, columns [8t, 8t+8) of every row: thread tid takes rows
+        // tid + 512*i, 16 bytes each (zero past the end)
+        constexpr int SDV = 16;  // rows per thread: H <= 8192
+        const rsrc_t sd_rs = make_rsrc(a.sh_native + NS.sdn, (uint32_t)(NS.total - NS.sdn));
+        u32x4 sdw[SDV];
+        // logit slots of experts e = tid, loaded behind the last weights of the
+        // shared expert: by then the router rows are long published
+        uint64_t lsl = 0;
+        auto lsl_load = [&]() {
+            if (tid < E)
+                lsl = __hip_atomic_load((__attribute__((address_space(1))) uint64_t*)(a.lslot + tid), __ATOMIC_RELAXED,
+                                        __HIP_MEMORY_SCOPE_AGENT);
+        };
+        bool lsl_sent = false;
+        auto sd_issue = [&](uint32_t tile) {
+#pragma unroll
+            for (int i = 0; i < SDV; i++)  // row tid + 512 i of the tile: 16 bytes, rows past H read zeros
+                sdw[i] = bld16(sd_rs, (tile * H + tid) * 16u, kThreads * i * 16u);
+            if (!lsl_sent) {
+                lsl_load();
+                lsl_sent = true;
+            }
+        };
+        const uint32_t tile0 = tile_of(0);
+        sg_issue(tile0, 0, bA);
+        sg_issue(tile0, 1, bB);
 
         // RMSNorm: w * (x * (1/sqrt(mean(x^2) + eps))) in fp32
         // (tools/ref_glm_chain.py:63-80; src/glm_primitives.cuh:35-62)
@@ -506,6 +568,7 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const DecodeDyn d) {
         }
         const float tot = block_sum(ss, red);
         const float rinv = 1.0f / sqrtf(tot / (float)H + a.eps);
+        float* xn = pv;
 #pragma unroll
         for (int i = 0; i < HV; i++) {
             const uint32_t j = tid + kThreads * i;
@@ -527,9 +590,20 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const DecodeDyn d) {
                 }
             }
         }
+        if (tid < E) {
+            tk_ch[tid] = __uint_as_float(bias0);  // the bias until topk_score replaces it
+            tk_blk[tid] = (const uint8_t*)slot0;
+        }
+        for (uint32_t e = tid + kThreads; e < E; e += kThreads) {
+            tk_ch[e] = gld(a.bias + e);
+            tk_blk[e] = gld(a.slot_tab + e);
+        }
         lds_barrier();
+        WL_TL(1);
 
-        // router rows r = w + G*i (bf16 x f32, fp32 accumulate)
+        // router rows r = w + G*i (bf16 x f32, fp32 accumulate); each logit
+        // is published as one 64-bit word (epoch << 32 | bits) with an
+        // agent-scope store: a reader that sees this call's epoch has the value
         for (uint32_t r = w, first = 1; r < E; r += G, first = 0) {
             if (!first) {
 #pragma unroll
@@ -556,22 +630,39 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const DecodeDyn d) {
             if (lane == 0) red[v * 64 + 48] = pd;
             lds_barrier();
             if (tid == 0) {
-                float s = 0.f;
+                float sum = 0.f;
 #pragma unroll
-                for (int wv = 0; wv < kWaves; wv++) s += red[wv * 64 + 48];
-                gst(a.logits + r, s);
+                for (int wv = 0; wv < kWaves; wv++) sum += red[wv * 64 + 48];
+                __hip_atomic_store((__attribute__((address_space(1))) uint64_t*)(a.lslot + r),
+                                   ((uint64_t)d.epoch << 32) | __float_as_uint(sum), __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
             }
             lds_barrier();
         }
+        WL_TL(2);
 
-        // shared gate/up tiles, SwiGLU of 8 rows each
-        for (uint32_t tile = w; tile < nsg; tile += G) {
-            if (tile != w) {
+        // shared expert: SwiGLU of each tile's 8 rows, then those 8 columns of
+        // the down projection applied to every output row, into pv
+        const uint32_t ntiles = w < nsg ? cdiv(nsg - w, G) : 0u;
+        for (uint32_t i = tid; i < H; i += kThreads) pv[i] = 0.f;  // xn is no longer needed
+        for (uint32_t ti = 0; ti < ntiles; ti++) {
+            const uint32_t tile = tile_of(ti);
+            if (ti != 0) {
                 sg_issue(tile, 0, bA);
                 sg_issue(tile, 1, bB);
             }
             gacc = f32x4{0.f, 0.f, 0.f, 0.f};
-            pingpong(sg_nb, bA, bB, [&](uint32_t b, Batch& B) { sg_issue(tile, b, B); }, sg_consume);
+            bool sd_sent = false;
+            pingpong(sg_nb, bA, bB,
+                     [&](uint32_t b, Batch& B) {
+                         sg_issue(tile, b, B);
+                         if (b + 1 >= sg_nb && !sd_sent) {  // the last issue: shared-down rows follow it
+                             sd_issue(tile);
+                             sd_sent = true;
+                         }
+                     },
+                     sg_consume);
+            if (!sd_sent) sd_issue(tile);
             if (lane < 16) red[v * 64 + n] = sum3(gacc);
             lds_barrier();
             if (tid < 8) {
@@ -582,95 +673,111 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const DecodeDyn d) {
                     us += red[wv * 64 + 8 + tid];
                 }
                 const float mid = silu_mul(gs, us);
-                const uint32_t r = tile * 8 + tid;
-                gst(a.smid + r, mid);
-                uint32_t ph, pm, pl;
-                split3(mid, ph, pm, pl);
-                gst(a.smid_p + r, (uint16_t)ph);
-                gst(a.smid_p + SI + r, (uint16_t)pm);
-                gst(a.smid_p + 2 * SI + r, (uint16_t)pl);
+                smf[tid] = mid;
+                gst(a.smid + tile * 8 + tid, mid);
+            }
+            lds_barrier();
+            const float4 m0 = *(const float4*)smf, m1 = *(const float4*)(smf + 4);
+#pragma unroll
+            for (int i = 0; i < SDV; i++) {
+                const uint32_t r = tid + kThreads * i;
+                if (r < H) {
+                    float x = 0.f;
+                    x = fmaf(bf2f(sdw[i].x & 0xFFFFu), m0.x, x);
+                    x = fmaf(bf2f(sdw[i].x >> 16), m0.y, x);
+                    x = fmaf(bf2f(sdw[i].y & 0xFFFFu), m0.z, x);
+                    x = fmaf(bf2f(sdw[i].y >> 16), m0.w, x);
+                    x = fmaf(bf2f(sdw[i].z & 0xFFFFu), m1.x, x);
+                    x = fmaf(bf2f(sdw[i].z >> 16), m1.y, x);
+                    x = fmaf(bf2f(sdw[i].w & 0xFFFFu), m1.z, x);
+                    x = fmaf(bf2f(sdw[i].w >> 16), m1.w, x);
+                    pv[r] += x;
+                }
             }
             lds_barrier();
         }
+        // pv -> rows [32b, 32b+32) into block b, slot w of dst ([H/32][G][32]),
+        // agent-scope 16-byte stores
+        auto publish = [&](float* dst) {
+            const rsrc_t rs = make_rsrc(dst, P.NB * G * kRowBlock * 4u);
+            for (uint32_t c = tid; c < H / 4u; c += kThreads) {
+                const uint32_t r = 4u * c, b = r / kRowBlock;
+                const u32x4 x = *(const u32x4*)(pv + r);
+                __builtin_amdgcn_raw_buffer_store_b128(x, rs, (int)(4u * ((b * G + w) * kRowBlock + r % kRowBlock)), 0,
+                                                       kSC1);
+            }
+        };
+        if (d.taps) publish(a.tsh);  // the shared-expert contribution alone, for the tap
+        WL_TL(3);
 
-        if (d.seg_hi >= 1u) {
-            if (!grid_barrier(a.sync, SM, 2u * d.epoch, w, G, misc, false)) return;
+        // ---- top-k: every logit of this call must be published (a slot that
+        // still holds an older epoch is re-read)
+        if (!lsl_sent) lsl_load();
+        {
+            bool ok = true;
+            uint32_t done = 0;  // bit i: expert tid + 512*i scored (tk_ch[e] then holds its choice, no longer the bias)
+            for (uint32_t spins = 0;; spins++) {
+                bool mine = true;
+                for (uint32_t i = 0, e = tid; e < E; i++, e += kThreads) {
+                    if ((done >> i) & 1u) continue;
+                    const uint64_t x = i == 0 ? lsl
+                                              : __hip_atomic_load((__attribute__((address_space(1))) uint64_t*)(a.lslot + e),
+                                                                  __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    if ((uint32_t)(x >> 32) == d.epoch) {
+                        topk_score(__uint_as_float((uint32_t)x), tk_ch[e], e, tk_sc, tk_ch);
+                        if (w == 0) gst(a.logits + e, __uint_as_float((uint32_t)x));
+                        done |= 1u << i;
+                    } else {
+                        mine = false;
+                    }
+                }
+                if (block_all(mine, misc)) break;
+                if (spins > (1u << 20) || ld_sync(a.sync + SM.error) != 0u) {
+                    if (tid == 0 && spins > (1u << 20)) raise_error(a.sync, SM, E_SPIN);
+                    ok = false;
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(2);
+                lsl_load();
+            }
+            if (!ok) return;
         }
-    }
-
-    // ================= segment 1: top-k, shared down, routed units ==============
-    if (d.seg_lo <= 1u && d.seg_hi >= 1u) {
-        // The top-k inputs, the slot table and the shared SwiGLU pieces are
-        // loaded first and the first shared-down batch right after them, so
-        // those weights stream while the top-k is computed.
-        constexpr int TKV = 2, SMV = 2;  // per thread: E <= 1024, 3*SI/8 <= 1024 in registers
-        const rsrc_t lg_rs = make_rsrc(a.logits, E * 4u), bs_rs = make_rsrc(a.bias, E * 4u);
-        const rsrc_t sl_rs = make_rsrc(a.slot_tab, E * 8u), sm_rs = make_rsrc(a.smid_p, 3u * SI * 2u);
-        uint32_t lgv[TKV], bsv[TKV];
-        uint64_t slv[TKV];
-        u32x4 smv[SMV];
-#pragma unroll
-        for (int i = 0; i < TKV; i++) {
-            const uint32_t e = tid + kThreads * i;
-            lgv[i] = __builtin_amdgcn_raw_buffer_load_b32(lg_rs, (int)(4u * e), 0, 0);
-            bsv[i] = __builtin_amdgcn_raw_buffer_load_b32(bs_rs, (int)(4u * e), 0, 0);
-            slv[i] = __builtin_bit_cast(uint64_t, __builtin_amdgcn_raw_buffer_load_b64(sl_rs, (int)(8u * e), 0, 0));
-        }
-#pragma unroll
-        for (int i = 0; i < SMV; i++) smv[i] = bld16(sm_rs, 16u * (tid + kThreads * i), 0u);
-        if (sd_fast && sd_units) sd_issue(bP);
-#pragma unroll
-        for (int i = 0; i < TKV; i++) {
-            const uint32_t e = tid + kThreads * i;
-            if (e < E) topk_score(__uint_as_float(lgv[i]), __uint_as_float(bsv[i]), e, tk_sc, tk_ch);
-            if (e < E) tk_blk[e] = (const uint8_t*)slv[i];
-        }
-        for (uint32_t e = tid + kThreads * TKV; e < E; e += kThreads) {
-            topk_score(gld(a.logits + e), gld(a.bias + e), e, tk_sc, tk_ch);
-            tk_blk[e] = gld(a.slot_tab + e);
-        }
-#pragma unroll
-        for (int i = 0; i < SMV; i++) {
-            const uint32_t c = tid + kThreads * i;
-            if (c < 3u * SI / 8u) *(u32x4*)(smp + (c / (SI / 8u)) * sps + (c % (SI / 8u)) * 8u) = smv[i];
-        }
-        for (uint32_t c = tid + kThreads * SMV; c < 3u * SI / 8u; c += kThreads)
-            *(u32x4*)(smp + (c / (SI / 8u)) * sps + (c % (SI / 8u)) * 8u) = gld16(a.smid_p + 8u * c);
-        lds_barrier();
-        topk_rank(E, K, tk_sc, tk_ch, tk_idx, tk_w);
+        if (E <= 256u) topk_argmax(E, K, tk_sc, tk_ch, tk_idx, tk_w);
+        else topk_rank(E, K, tk_sc, tk_ch, tk_idx, tk_w);
+        WL_TL(5);
         if (w == 0 && tid < K) {
             gst(a.idx + tid, (int32_t)tk_idx[tid]);
             gst(a.topw + tid, topk_weight(a, K, tk_w, tid));
         }
 
-        // routed units u = w + G*i: items are gate/up k tiles (128 wide, this
-        // wave's 8+8 row tile), then down row pairs (32 rows x the slice's 64
-        // columns), each wave a contiguous range of them
+        // ---- routed units u = w + G*i: items are gate/up k tiles (128 wide,
+        // this wave's 8+8 row tile), then down row pairs (32 rows x the
+        // slice's 64 columns), each wave a contiguous range of them
         const uint32_t nkg = H / 128, nq = H / 32;
-        const uint32_t dq_per = cdiv(nq, 8u);  // down row pairs per wave: [v*dq_per, +dq_per)
+        const uint32_t dq_per = cdiv(cdiv(nq, 8u), (uint32_t)kNB) * kNB;  // row pairs per wave: [v*dq_per, +dq_per)
         const uint32_t nbg = cdiv(nkg, (uint32_t)kNB);
         const uint32_t nbd = cdiv(dq_per, (uint32_t)kNB);
         const uint32_t nbr = nbg + nbd;  // >= 2
         const uint8_t* blk = nullptr;
-        uint32_t uk = 0, uj = 0, uu = 0;
+        uint32_t uk = 0, uj = 0;
+        float wk = 0.f;
+        // at most one routed unit per work-group (GLM: exactly one): its down
+        // items publish the partial rows directly
+        const bool direct = P.U <= G && w < P.U;
         rsrc_t r_rs = make_rsrc(a.router_w, 16u);  // rebound per unit
-        uint32_t gu_voff = 0, gu_soff = 0, dn_voff = 0, dn_soff = 0;
-        // Branch-free: per-slot offsets are selected, then one block of loads
-        // (loads on two paths would be joined by register copies that wait
-        // for them).
+        uint32_t gu_voff = 0, gus_voff = 0, dn_voff = 0, dns_voff = 0;
+        // Native block: the gate/up items of this wave are 1 KB chunks
+        // [tile*(H/128) + kt], the down items [slice*(H/32) + q]; one 16-byte
+        // scale chunk per batch. Branch-free: offsets are selected, then one
+        // block of loads (loads on two paths would be joined by register copies
+        // that wait for them).
         auto r_issue = [&](uint32_t b, Batch& B) {
             const bool gu = b < nbg;
-            const uint32_t kt0 = b * kNB;
-            const uint32_t q0 = v * dq_per + (b - nbg) * kNB;
+            const uint32_t i0 = gu ? b * kNB : v * dq_per + (b - nbg) * kNB;
+            const uint32_t wv = gu ? gu_voff : dn_voff;
 #pragma unroll
-            for (int i = 0; i < kNB; i++) {
-                const uint32_t wv = gu ? gu_voff + i * 64u : dn_voff;
-                const uint32_t ws = gu ? kt0 * 64u : (q0 + i) * 32u * (I / 2);
-                const uint32_t sv = gu ? gu_soff + i * 4u : dn_soff;
-                const uint32_t ss = gu ? kt0 * 4u : (q0 + i) * 32u * (I / 32);
-                B.w[i] = bld16(r_rs, wv, ws);
-                B.s[i] = bld1(r_rs, sv, ss);
-            }
+            for (int i = 0; i < kNB; i++) B.w[i] = bld16(r_rs, wv, (i0 + i) * 1024u);
+            B.sv = bld16(r_rs, gu ? gus_voff : dns_voff, (i0 / 16u) * 1024u);
         };
         f32x4 racc;
         bf16x8 A0, A1;
@@ -680,9 +787,9 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const DecodeDyn d) {
                 for (int i = 0; i < kNB; i++) {
                     const uint32_t kt = b * kNB + i;
                     const bool valid = kt < nkg;
-                    // a masked item reads the next row (or zeros past the
+                    // a masked item reads another tile (or zeros past the
                     // block): scale 0 makes its B operand exactly zero
-                    const float sc = valid ? e8m0f(B.s[i]) : 0.f;
+                    const float sc = valid ? e8m0f(batch_scale(B, b * kNB, i)) : 0.f;
 #pragma unroll
                     for (int jj = 0; jj < 4; jj++)
                         racc = mma(a_lds(xp, xps, n, kt * 128u + 32u * g + 8u * jj, valid),
@@ -704,6 +811,7 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const DecodeDyn d) {
                         rmp[2 * rps + col] = (uint16_t)pl;
                     }
                     lds_barrier();
+                    WL_TL(7);
                     // down A operands: k groups of lane g hold slice columns
                     // {0,32,8,40}[g] (+16 for the second), matching the
                     // lane order the row-pair swap below produces
@@ -715,6 +823,7 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const DecodeDyn d) {
                 const uint32_t m0 = (b - nbg) * kNB;
 #pragma unroll
                 for (int i = 0; i < kNB; i++) {
+                    const uint32_t sbyte = batch_scale(B, v * dq_per + m0, i);
                     // lane (n, g) holds 16 bytes of row n + 16*(g>>1): columns
                     // [32*(g&1), +32) of the slice, and that block's scale.
                     // One swap of lane halves turns dwords (0,1) into the B
@@ -723,7 +832,7 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const DecodeDyn d) {
                     const uint32_t m = m0 + i, q = v * dq_per + m;
                     const bool valid = m < dq_per && q < nq;
                     uint32_t sx, sy, x01, y01, x23, y23;
-                    swap32(B.s[i], B.s[i], sx, sy);
+                    swap32(sbyte, sbyte, sx, sy);
                     swap32(B.w[i][0], B.w[i][1], x01, y01);
                     swap32(B.w[i][2], B.w[i][3], x23, y23);
                     const float scx = e8m0f(sx), scy = e8m0f(sy);
@@ -733,92 +842,101 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const DecodeDyn d) {
                     d1 = mma(A1, fp4x8_bf16(y23, scy), d1);
                     const float s0 = sum3(d0);
                     const float s1 = __shfl(sum3(d1), (lane - 16u) & 63u, 64);
-                    if (valid && lane < 32) gst(a.part + (size_t)uu * H + q * 32u + lane, lane < 16 ? s0 : s1);
+                    // rows [32q, 32q+32): this unit's weighted contribution; with
+                    // one unit per work-group the rows are final and go straight
+                    // to block q of the partials
+                    if (valid && lane < 32) {
+                        const float x = pv[q * 32u + lane] + wk * (lane < 16 ? s0 : s1);
+                        if (direct) st_ag(a.part + ((size_t)q * G + w) * kRowBlock + lane, x);
+                        else pv[q * 32u + lane] = x;
+                    }
                 }
             }
         };
 
         bool first_unit = true;
         for (uint32_t u = w; u < P.U; u += G) {
-            uu = u;
             uk = u % K;
             uj = u / K;
             blk = uni_ptr(tk_blk[tk_idx[uk]]);
+            wk = topk_weight(a, K, tk_w, uk);
             if (blk == nullptr) {
                 if (tid == 0) raise_error(a.sync, SM, E_NOT_RESIDENT);
                 continue;
             }
             if (!first_unit) lds_barrier();  // rmp of the previous unit fully read
+            first_unit = false;
             {
-                const uint32_t row = uj * kSlice + v * 8u + (n & 7u);
-                const uint32_t drow = n + 16u * (g >> 1);
-                // packed block: gate_w | gate_s | up_w | up_s | down_w | down_s
-                // (reference ExpertLayout, src/glm_layer_runner.cuh:60-72)
-                const uint32_t gw = 0, gs = gw + I * H / 2, uw = gs + I * H / 32, us = uw + I * H / 2;
-                const uint32_t dw = us + I * H / 32, ds = dw + H * I / 2, total = ds + H * I / 32;
-                r_rs = make_rsrc(blk, total);
-                gu_voff = (n < 8 ? gw : uw) + row * (H / 2) + 16u * g;
-                gu_soff = (n < 8 ? gs : us) + row * (H / 32) + g;
-                dn_voff = dw + drow * (I / 2) + 32u * uj + 16u * (g & 1u);
-                dn_soff = ds + drow * (I / 32) + 2u * uj + (g & 1u);
+                const NativeLayout NL = NativeLayout::make(H, I);
+                const uint32_t tile = uj * (kSlice / 8u) + v;  // this wave's 8+8 row tile
+                r_rs = make_rsrc(blk, (uint32_t)NL.total);
+                gu_voff = (uint32_t)NL.gu + tile * nkg * 1024u + 16u * lane;
+                gus_voff = (uint32_t)NL.gus + tile * cdiv(nkg, 16u) * 1024u + 16u * lane;
+                dn_voff = (uint32_t)NL.dn + uj * nq * 1024u + 16u * lane;
+                dns_voff = (uint32_t)NL.dns + uj * cdiv(nq, 16u) * 1024u + 16u * lane;
             }
             r_issue(0, bA);
-            if (first_unit) {
-                // shared down (its batch is in bP) while batch 0 flies
-                if (sd_fast && sd_units) sd_consume_store(bP);
-                first_unit = false;
-            }
             r_issue(1, bB);
             racc = f32x4{0.f, 0.f, 0.f, 0.f};
             pingpong(nbr, bA, bB, r_issue, r_consume);
+            WL_TL(8);
         }
-        if (first_unit && sd_fast && sd_units) sd_consume_store(bP);  // no routed unit here
-        if (!sd_fast) sd_general(a, P, smp, sps, red, H, SI, w, G);
+        lds_barrier();
 
-        if (d.seg_hi >= 2u) {
-            if (!grid_barrier(a.sync, SM, 2u * d.epoch + 1u, w, G, misc, true)) return;
+        // ---- publish this work-group's partial (the combine of block b reads
+        // its G slots contiguously), unless the down items already did
+        if (!direct) publish(a.part);
+        if (d.seg_hi >= 1u) {
+            if (!grid_barrier(a.sync, SM, d.epoch, w, G, misc + 8, true)) return;
         }
+        WL_TL(9);
     }
 
-    // ================= segment 2: combine ========================================
-    if (d.seg_hi >= 2u) {
-        if (d.seg_lo == 2u) {
-            for (uint32_t e = tid; e < E; e += kThreads) topk_score(gld(a.logits + e), gld(a.bias + e), e, tk_sc, tk_ch);
+    // ================= segment 1: combine ========================================
+    // out[r] = sum over work-groups of their partials (fixed order), + resid.
+    if (d.seg_hi >= 1u) {
+        constexpr uint32_t RB = kRowBlock;
+        float* fin = pv;                   // [G][32]
+        float* f2 = fin + (size_t)G * RB;  // [16][32]
+        // sum of the G slots of block blkr of src; the result is in threads 0..31
+        auto block_total = [&](const float* src, uint32_t blkr) -> float {
+            const rsrc_t rs = make_rsrc(src + (size_t)blkr * G * RB, G * RB * 4u);
+            for (uint32_t base = 0; base < G * RB; base += kThreads * 16u) {
+                u32x4 pq[4];
+#pragma unroll
+                for (int i = 0; i < 4; i++) pq[i] = bld16_ag(rs, 4u * (base + 4u * (tid + kThreads * i)), 0u);
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const uint32_t idx = base + 4u * (tid + kThreads * i);
+                    if (idx < G * RB) *(u32x4*)(fin + idx) = pq[i];
+                }
+            }
             lds_barrier();
-            topk_rank(E, K, tk_sc, tk_ch, tk_idx, tk_w);
-        }
-        const uint32_t RB = P.RB, r0 = w * RB;
-        if (r0 >= H) return;
-        const uint32_t nr = min(RB, H - r0);
-        float* fsd = fin + P.U * RB;
-        float* fe = fsd + P.KS * RB;
-        for (uint32_t i = tid; i < P.U * RB; i += kThreads) {
-            const uint32_t u = i / RB, rr = i % RB;
-            fin[i] = rr < nr ? gld(a.part + (size_t)u * H + r0 + rr) : 0.f;
-        }
-        for (uint32_t i = tid; i < P.KS * RB; i += kThreads) {
-            const uint32_t h = i / RB, rr = i % RB;
-            fsd[i] = rr < nr ? gld(a.sdpart + (size_t)h * H + r0 + rr) : 0.f;
-        }
-        lds_barrier();
-        for (uint32_t i = tid; i < K * RB; i += kThreads) {
-            const uint32_t k = i / RB, rr = i % RB;
-            float e = 0.f;
-            for (uint32_t j = 0; j < P.S; j++) e += fin[(j * K + k) * RB + rr];
-            fe[i] = e;
-            if (rr < nr) gst(a.edown + (size_t)k * H + r0 + rr, e);
-        }
-        lds_barrier();
-        for (uint32_t rr = tid; rr < nr; rr += kThreads) {
-            float sh = 0.f;
-            for (uint32_t h = 0; h < P.KS; h++) sh += fsd[h * RB + rr];
+            {  // 16 groups of work-groups, then the 16 group sums
+                const uint32_t rr = tid % RB, grp = tid / RB;
+                float sum = 0.f;
+                for (uint32_t ww = grp; ww < G; ww += 16u) sum += fin[ww * RB + rr];
+                f2[grp * RB + rr] = sum;
+            }
+            lds_barrier();
             float o = 0.f;
-            for (uint32_t k = 0; k < K; k++) o = __fadd_rn(o, __fmul_rn(topk_weight(a, K, tk_w, k), fe[k * RB + rr]));
-            o = __fadd_rn(o, sh);
-            const uint32_t r = r0 + rr;
-            gst(a.shared_out + r, sh);
-            gst(d.out + r, d.resid ? __fadd_rn(gld(d.resid + r), o) : o);
+            if (tid < RB) {
+#pragma unroll
+                for (int gi = 0; gi < 16; gi++) o += f2[gi * RB + tid];
+            }
+            lds_barrier();
+            return o;
+        };
+        for (uint32_t blkr = w; blkr < P.NB; blkr += G) {
+            const uint32_t r = blkr * RB + tid;
+            const float o = block_total(a.part, blkr);
+            if (tid < RB) gst(d.out + r, d.resid ? __fadd_rn(gld(d.resid + r), o) : o);
+            if (d.taps) {
+                const float sh = block_total(a.tsh, blkr);
+                if (tid < RB) gst(a.shared_out + r, sh);
+            }
         }
+        WL_TL(10);
     }
 }
 
@@ -1040,5 +1158,11 @@ int launch_decode(const DecodeArgs* d_args, const DecodeDyn& dyn, uint32_t H, ui
                            dyn);
     return (int)hipGetLastError();
 }
+
+#ifdef WL_TIMELINE
+extern "C" int wl_dbg_timeline(void* host, size_t bytes) {
+    return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(g_tl), bytes, 0, hipMemcpyDeviceToHost);
+}
+#endif
 
 }  // namespace wl

@@ -21,7 +21,7 @@ struct LayerState {
     const uint16_t* router_w = nullptr;
     const float* bias = nullptr;
     const uint16_t* ln = nullptr;
-    const void* shared = nullptr;
+    uint8_t* shared = nullptr;  // context-owned native copy of the shared expert
     int32_t shared_dtype = WL_SHARED_BF16;
     bool set = false;
 };
@@ -29,6 +29,7 @@ struct LayerState {
 struct wl_ctx {
     wl_moe_config cfg{};
     wl_expert_layout lay{};
+    size_t native_bytes = 0;
     uint32_t SI = 0;
     int device = 0;
     int n_cu = 0;
@@ -40,19 +41,19 @@ struct wl_ctx {
     wl::DecodeArgs* d_largs = nullptr;    // [L] per-layer kernel records
     // intermediates kept for inspection (ordinary device memory)
     float* norm = nullptr;
+    float* logits = nullptr;
     float* smid = nullptr;
     float* rmid = nullptr;
     int32_t* idx = nullptr;
     float* topw = nullptr;
     float* shared_out = nullptr;
-    float* edown = nullptr;
     uint16_t* ffn_mid_p = nullptr;  // wl_expert_ffn's SwiGLU pieces
-    // cross-work-group arrays (uncached)
-    float* logits = nullptr;
-    uint16_t* smid_p = nullptr;
+    int32_t taps = 1;
+    // cross-work-group arrays (agent-scope stores and loads)
+    uint64_t* lslot = nullptr;
     float* part = nullptr;
-    float* sdpart = nullptr;
-    uint32_t* sync = nullptr;
+    float* tsh = nullptr;
+    uint32_t* sync = nullptr;   // barrier words (uncached)
     wl::SyncMap sm{};
     wl::Plan plan{};
     uint32_t grid = 0;
@@ -148,30 +149,19 @@ wl::DecodeArgs layer_record(const wl_ctx* c, uint32_t layer) {
     a.ln_w = L.ln;
     a.router_w = L.router_w;
     a.bias = L.bias;
-    const uint16_t* sh = (const uint16_t*)L.shared;
-    a.sh_gate = sh;
-    a.sh_up = sh + (size_t)SI * H;
-    a.sh_down = sh + (size_t)2 * SI * H;
+    a.sh_native = L.shared;
     a.slot_tab = c->d_slot + (size_t)layer * E;
     a.norm = c->norm;
+    a.logits = c->logits;
     a.smid = c->smid;
     a.rmid = c->rmid;
     a.idx = c->idx;
     a.topw = c->topw;
     a.shared_out = c->shared_out;
-    a.edown = c->edown;
-    a.logits = c->logits;
-    a.smid_p = c->smid_p;
+    a.lslot = c->lslot;
     a.part = c->part;
-    a.sdpart = c->sdpart;
+    a.tsh = c->tsh;
     a.sync = c->sync;
-    a.gw_off = c->lay.gw_off;
-    a.gs_off = c->lay.gs_off;
-    a.uw_off = c->lay.uw_off;
-    a.us_off = c->lay.us_off;
-    a.dw_off = c->lay.dw_off;
-    a.ds_off = c->lay.ds_off;
-    a.blk_bytes = c->lay.total;
     a.H = H;
     a.I = c->cfg.moe_inter;
     a.E = E;
@@ -213,6 +203,7 @@ wl_status wl_create(const wl_moe_config* cfg, wl_ctx** out) {
     c->cfg = *cfg;
     c->SI = cfg->moe_inter * cfg->n_shared;
     wl_expert_layout_of(cfg, 0, &c->lay);
+    c->native_bytes = wl::NativeLayout::make(cfg->hidden, cfg->moe_inter).total;
     hipError_t e = hipGetDevice(&c->device);
     if (e != hipSuccess) { delete c; return WL_ERR_HIP; }
     hipDeviceProp_t prop;
@@ -250,35 +241,24 @@ wl_status wl_create(const wl_moe_config* cfg, wl_ctx** out) {
         (s = dalloc(c, &c->idx, 4 * (size_t)WL_MAX_TOPK)) != WL_OK ||
         (s = dalloc(c, &c->topw, 4 * (size_t)WL_MAX_TOPK)) != WL_OK ||
         (s = dalloc(c, &c->shared_out, 4 * (size_t)H)) != WL_OK ||
-        (s = dalloc(c, &c->edown, 4 * (size_t)K * H)) != WL_OK ||
-        (s = dalloc(c, &c->ffn_mid_p, 2 * 3 * (size_t)I)) != WL_OK) {
+        (s = dalloc(c, &c->ffn_mid_p, 2 * 3 * (size_t)I)) != WL_OK ||
+        (s = dalloc(c, &c->logits, 4 * (size_t)E)) != WL_OK ||
+        (s = dalloc(c, &c->lslot, 8 * (size_t)E)) != WL_OK ||
+        (s = dalloc(c, &c->part, 4 * (size_t)H * grid)) != WL_OK ||
+        (s = dalloc(c, &c->tsh, 4 * (size_t)H * grid)) != WL_OK) {
         wl_destroy(c);
         return s;
     }
-    // the uncached block: sync words, then every array one work-group writes
-    // and another reads
-    {
-        size_t off = 0;
-        auto carve = [&](size_t bytes) { size_t o = off; off += (bytes + 255) / 256 * 256; return o; };
-        const size_t o_sync = carve(4 * (size_t)c->sm.words);
-        const size_t o_logits = carve(4 * (size_t)E);
-        const size_t o_smid_p = carve(2 * 3 * (size_t)SI);
-        const size_t o_part = carve(4 * (size_t)c->plan.U * H);
-        const size_t o_sdpart = carve(4 * (size_t)c->plan.KS * H);
-        c->uc_bytes = off;
-        c->uc_block = uc_acquire(c->device, off);
-        if (!c->uc_block) {
-            wl_destroy(c);
-            return WL_ERR_OOM;
-        }
-        uint8_t* b = (uint8_t*)c->uc_block;
-        c->sync = (uint32_t*)(b + o_sync);
-        c->logits = (float*)(b + o_logits);
-        c->smid_p = (uint16_t*)(b + o_smid_p);
-        c->part = (float*)(b + o_part);
-        c->sdpart = (float*)(b + o_sdpart);
+    // the uncached block holds only the barrier words
+    c->uc_bytes = 4 * (size_t)c->sm.words;
+    c->uc_block = uc_acquire(c->device, c->uc_bytes);
+    if (!c->uc_block) {
+        wl_destroy(c);
+        return WL_ERR_OOM;
     }
+    c->sync = (uint32_t*)c->uc_block;
     e = hipMemset(c->d_slot, 0, sizeof(void*) * (size_t)L * E);
+    if (e == hipSuccess) e = hipMemset(c->lslot, 0, 8 * (size_t)E);  // epoch 0: never a call's
     if (e == hipSuccess) e = hipMemset(c->uc_block, 0, c->uc_bytes);
     if (e == hipSuccess) e = hipDeviceSynchronize();
     if (e != hipSuccess) { wl_destroy(c); return WL_ERR_HIP; }
@@ -288,8 +268,8 @@ wl_status wl_create(const wl_moe_config* cfg, wl_ctx** out) {
 
 void wl_destroy(wl_ctx* c) {
     if (!c) return;
-    if (c->uc_block) hipDeviceSynchronize();
-    for (void* p : c->allocs) hipFree(p);
+    if (c->uc_block) (void)hipDeviceSynchronize();
+    for (void* p : c->allocs) (void)hipFree(p);
     uc_release(c->device, c->uc_bytes, c->uc_block);
     delete c;
 }
@@ -308,7 +288,14 @@ wl_status wl_set_layer(wl_ctx* c, uint32_t layer, const uint16_t* d_router_w, co
     L.router_w = d_router_w;
     L.bias = d_router_bias;
     L.ln = d_post_attn_ln;
-    L.shared = d_shared;
+    if (!L.shared) {
+        wl_status st = dalloc(c, &L.shared, wl::NativeShared::make(c->cfg.hidden, c->SI).total);
+        if (st != WL_OK) return st;
+    }
+    if (wl::launch_shared_to_native((const uint16_t*)d_shared, (uint16_t*)L.shared, c->cfg.hidden, c->SI, nullptr) != 0)
+        return fail(c, WL_ERR_HIP, "shared expert conversion launch failed");
+    hipError_t se = hipDeviceSynchronize();
+    if (se != hipSuccess) return hip_fail(c, se, "shared expert conversion");
     L.shared_dtype = shared_dtype;
     const wl::DecodeArgs a = layer_record(c, layer);
     hipError_t e = hipMemcpy(c->d_largs + layer, &a, sizeof(a), hipMemcpyHostToDevice);
@@ -346,10 +333,10 @@ wl_status wl_slot_pool_create(wl_ctx* c, uint32_t n_slots) {
     if (!c) return WL_ERR_INVALID;
     if (c->pool) return fail(c, WL_ERR_STATE, "slot pool already created");
     if (n_slots == 0) return fail(c, WL_ERR_INVALID, "n_slots must be positive");
-    const size_t bytes = (size_t)n_slots * c->lay.total;
+    const size_t bytes = (size_t)n_slots * c->native_bytes;
     void* p = nullptr;
     hipError_t e = hipMalloc(&p, bytes);
-    if (e != hipSuccess) return fail(c, WL_ERR_OOM, "slot pool of %u x %zu B: %s", n_slots, c->lay.total, hipGetErrorString(e));
+    if (e != hipSuccess) return fail(c, WL_ERR_OOM, "slot pool of %u x %zu B: %s", n_slots, c->native_bytes, hipGetErrorString(e));
     c->allocs.push_back(p);
     c->pool = (uint8_t*)p;
     c->pool_slots = n_slots;
@@ -360,7 +347,7 @@ wl_status wl_slot_pool_ptr(wl_ctx* c, uint32_t slot, uint8_t** d_block) {
     if (!c || !d_block) return WL_ERR_INVALID;
     if (!c->pool) return fail(c, WL_ERR_STATE, "no slot pool");
     if (slot >= c->pool_slots) return fail(c, WL_ERR_INVALID, "slot %u >= %u", slot, c->pool_slots);
-    *d_block = c->pool + (size_t)slot * c->lay.total;
+    *d_block = c->pool + (size_t)slot * c->native_bytes;
     return WL_OK;
 }
 
@@ -384,6 +371,7 @@ static wl_status run_layer(wl_ctx* c, uint32_t layer, const float* d_hidden, con
     dyn.hidden = d_hidden;
     dyn.resid = d_resid;
     dyn.out = d_out;
+    dyn.taps = c->taps;
     auto launch = [&](uint32_t lo, uint32_t hi) -> wl_status {
         dyn.seg_lo = lo;
         dyn.seg_hi = hi;
@@ -391,11 +379,10 @@ static wl_status run_layer(wl_ctx* c, uint32_t layer, const float* d_hidden, con
         if (e != 0) return hip_fail(c, (hipError_t)e, "decode launch");
         return WL_OK;
     };
-    if (c->sched == WL_SCHED_FUSED) return launch(0, 2);
+    if (c->sched == WL_SCHED_FUSED) return launch(0, 1);
     wl_status s;
     if ((s = launch(0, 0)) != WL_OK) return s;
-    if ((s = launch(1, 1)) != WL_OK) return s;
-    return launch(2, 2);
+    return launch(1, 1);
 }
 
 wl_status wl_run_moe(wl_ctx* c, uint32_t layer, const float* d_hidden, float* d_out, void* stream) {
@@ -452,12 +439,18 @@ wl_status wl_check_error(wl_ctx* c, void* stream) {
     if (e != hipSuccess) return hip_fail(c, e, "error flag read");
     if (flag) {
         // a launch that gave up may have left barrier counters mid-count
-        hipMemset(c->sync, 0, 4 * (size_t)c->sm.words);
-        hipDeviceSynchronize();
+        (void)hipMemset(c->sync, 0, 4 * (size_t)c->sm.words);
+        (void)hipDeviceSynchronize();
         return fail(c, WL_ERR_DEVICE, "device error bits 0x%x%s%s", flag,
                     (flag & wl::E_SPIN) ? " [dependency wait expired]" : "",
                     (flag & wl::E_NOT_RESIDENT) ? " [routed expert not resident]" : "");
     }
+    return WL_OK;
+}
+
+wl_status wl_set_taps(wl_ctx* c, int32_t enable) {
+    if (!c) return WL_ERR_INVALID;
+    c->taps = enable ? 1 : 0;
     return WL_OK;
 }
 
@@ -485,6 +478,30 @@ wl_status wl_expert_ffn(wl_ctx* c, const uint8_t* d_block, const float* d_x, flo
                                   c->rmid, c->ffn_mid_p, d_y, d_y_bf16, stream);
     if (e != 0) return hip_fail(c, (hipError_t)e, "expert ffn launch");
     return WL_OK;
+}
+
+size_t wl_native_block_bytes(const wl_moe_config* cfg) {
+    if (!cfg) return 0;
+    return (size_t)wl::NativeLayout::make(cfg->hidden, cfg->moe_inter).total;
+}
+
+wl_status wl_expert_to_native(const wl_moe_config* cfg, const uint8_t* d_ref_block, uint8_t* d_native_block,
+                              void* stream) {
+    if (!cfg || !d_ref_block || !d_native_block) return WL_ERR_INVALID;
+    if (validate_cfg(cfg, nullptr) != WL_OK) return WL_ERR_INVALID;
+    return wl::launch_expert_to_native(d_ref_block, d_native_block, cfg->hidden, cfg->moe_inter, 0, stream) == 0
+               ? WL_OK
+               : WL_ERR_HIP;
+}
+
+wl_status wl_synth_expert_native(const wl_moe_config* cfg, uint32_t seed, uint32_t layer, uint32_t expert,
+                                 uint8_t* d_native_block, void* stream) {
+    if (!cfg || !d_native_block) return WL_ERR_INVALID;
+    if (validate_cfg(cfg, nullptr) != WL_OK) return WL_ERR_INVALID;
+    return wl::launch_expert_to_native(nullptr, d_native_block, cfg->hidden, cfg->moe_inter,
+                                       wl::synth_key(seed, layer, expert), stream) == 0
+               ? WL_OK
+               : WL_ERR_HIP;
 }
 
 wl_status wl_synth_expert(const wl_moe_config* cfg, uint32_t inter, uint32_t seed, uint32_t layer,

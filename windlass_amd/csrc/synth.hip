@@ -20,15 +20,6 @@
 
 namespace wl {
 
-__host__ __device__ static inline uint32_t mix32(uint32_t x) {
-    x ^= x >> 16;
-    x *= 0x7FEB352Du;
-    x ^= x >> 15;
-    x *= 0x846CA68Bu;
-    x ^= x >> 16;
-    return x;
-}
-
 uint32_t synth_key(uint32_t seed, uint32_t layer, uint32_t expert) {
     return mix32(mix32(seed ^ 0x9E3779B9u) ^
                  (layer * 0x85EBCA6Bu + expert * 0xC2B2AE35u + 0x27D4EB2Fu));

@@ -1,6 +1,7 @@
 """A resident synthetic MoE model built through the C ABI: every routed
-expert of every layer in one context-owned HBM slot pool (filled on the device
-by wl_synth_expert), dense tensors from windlass_amd.synthdata uploaded once.
+expert of every layer in one context-owned HBM slot pool (written on the device
+in the native layout by wl_synth_expert_native), dense tensors from
+windlass_amd.synthdata uploaded once.
 Used by the benchmark and the GPU tests."""
 import numpy as np
 
@@ -26,7 +27,7 @@ class DeviceModel:
         for l in range(n_layers):
             for e in range(E):
                 p = self.ctx.slot_pool_ptr(l * E + e)
-                moe.synth_expert(self.cfg, seed, l, e, p)
+                moe.synth_expert_native(self.cfg, seed, l, e, p)  # = wl_expert_to_native(synth block)
                 self.ctx.slot_bind(l, e, p)
             d = synthdata.dense_layer(H, E, self.SI, seed, l)
             if bias_offset is not None:

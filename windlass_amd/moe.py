@@ -75,7 +75,10 @@ def load():
         "wl_taps": [vp, ctypes.POINTER(Taps)],
         "wl_check_error": [vp, vp],
         "wl_set_schedule": [vp, i32],
+        "wl_set_taps": [vp, i32],
         "wl_synth_expert": [ctypes.POINTER(MoeConfig), u32, u32, u32, u32, vp, vp],
+        "wl_synth_expert_native": [ctypes.POINTER(MoeConfig), u32, u32, u32, vp, vp],
+        "wl_expert_to_native": [ctypes.POINTER(MoeConfig), vp, vp, vp],
         "wl_dequant_matvec_mxfp4": [vp, vp, vp, vp, u32, u32, vp],
         "wl_expert_ffn": [vp, vp, vp, vp, vp, vp],
     }
@@ -83,6 +86,8 @@ def load():
         fn = getattr(lib, name)
         fn.argtypes = args
         fn.restype = ctypes.c_int
+    lib.wl_native_block_bytes.argtypes = [ctypes.POINTER(MoeConfig)]
+    lib.wl_native_block_bytes.restype = ctypes.c_size_t
     lib.wl_destroy.argtypes = [vp]
     lib.wl_destroy.restype = None
     lib.wl_last_error.argtypes = [vp]
@@ -116,6 +121,22 @@ def synth_expert(cfg, seed, layer, expert, d_block, stream=0, inter=0):
     rc = load().wl_synth_expert(ctypes.byref(cfg), inter, seed, layer, expert, d_block, stream)
     if rc != WL_OK:
         raise WindlassError(rc, "wl_synth_expert")
+
+
+def synth_expert_native(cfg, seed, layer, expert, d_native, stream=0):
+    rc = load().wl_synth_expert_native(ctypes.byref(cfg), seed, layer, expert, d_native, stream)
+    if rc != WL_OK:
+        raise WindlassError(rc, "wl_synth_expert_native")
+
+
+def expert_to_native(cfg, d_ref, d_native, stream=0):
+    rc = load().wl_expert_to_native(ctypes.byref(cfg), d_ref, d_native, stream)
+    if rc != WL_OK:
+        raise WindlassError(rc, "wl_expert_to_native")
+
+
+def native_block_bytes(cfg):
+    return int(load().wl_native_block_bytes(ctypes.byref(cfg)))
 
 
 def dequant_matvec_mxfp4(d_W, d_S, d_x, d_y, N, K, stream=0):
@@ -192,3 +213,6 @@ class Context:
 
     def set_schedule(self, sched):
         self._ck(self.lib.wl_set_schedule(self.h, sched), "wl_set_schedule")
+
+    def set_taps(self, enable):
+        self._ck(self.lib.wl_set_taps(self.h, 1 if enable else 0), "wl_set_taps")
