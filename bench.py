@@ -87,6 +87,9 @@ def main():
     ap.add_argument("--seed", type=int, default=1)
     ap.add_argument("--cpu-sample", type=int, default=3, help="layers timed for the CPU baseline (0: skip)")
     ap.add_argument("--traffic-json", default=os.path.join(ROOT, "profiles", "decode_layer_traffic.json"))
+    ap.add_argument("--calib-copy-mb", type=int, default=0,
+                    help="after the timed steps, one device-to-device copy of this many MiB (the reference "
+                         "transfer for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE counters)")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -132,6 +135,14 @@ def main():
     ms = e0.elapsed_ms(e1)
     dm.ctx.check_error(stream.handle)
     us_per_layer = ms * 1e3 / args.steps
+
+    if args.calib_copy_mb > 0:
+        nb = args.calib_copy_mb << 20
+        src, dst = hip.DeviceBuffer(nb), hip.DeviceBuffer(nb)
+        hip.copy_d2d(dst.ptr, src.ptr, nb, stream.handle)
+        stream.synchronize()
+        src.free()
+        dst.free()
 
     nbytes = algorithmic_bytes(c)
     achieved = nbytes / (us_per_layer * 1e-6) / 1e9
