@@ -120,6 +120,13 @@ WL_DEV rsrc_t make_rsrc(const void* base, uint32_t bytes) {
 WL_DEV u32x4 bld16(rsrc_t r, uint32_t voff, uint32_t soff) {
     return __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0);
 }
+// Weight streams (read once per call): the non-temporal hint (aux bit 1).
+// Measured on MI355X: a 240 MB one-launch stream takes 38.6 us with it and
+// 43.3 us without.
+constexpr int kNT = 2;
+WL_DEV u32x4 bld16_nt(rsrc_t r, uint32_t voff, uint32_t soff) {
+    return __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, kNT);
+}
 WL_DEV uint32_t bld1(rsrc_t r, uint32_t voff, uint32_t soff) {
     return __builtin_amdgcn_raw_buffer_load_b8(r, (int)voff, (int)soff, 0);
 }
@@ -292,11 +299,6 @@ WL_DEV uint32_t batch_scale(const Batch& B, uint32_t item0, int i) {
     const uint32_t w = (o / 4u == 0u) ? B.sv.x : (o / 4u == 1u) ? B.sv.y : (o / 4u == 2u) ? B.sv.z : B.sv.w;
     return (w >> (8u * (o % 4u))) & 0xFFu;
 }
-// Shared-down batch: kSPU k tiles of each of 3 units.
-constexpr uint32_t kSPU = 4;
-struct SdBatch {
-    u32x4 w[3 * kSPU];
-};
 
 // Two-deep software pipeline over nb >= 2 batches: A holds batch 0 and B
 // batch 1 on entry, both already issued. Batch b+2 is issued right after
@@ -358,63 +360,61 @@ WL_DEV void topk_rank(uint32_t E, uint32_t K, const float* sc, const float* ch, 
     }
     lds_barrier();
 }
-// Largest 64-bit key (hi, lo) over the 64 lanes, returned uniform. DPP row
+// Largest value over the 64 lanes, returned uniform. DPP quad permutes, row
 // shifts and row broadcasts (VALU only) leave the maximum in lane 63.
-WL_DEV bool key_gt(uint32_t ah, uint32_t al, uint32_t bh, uint32_t bl) { return ah > bh || (ah == bh && al > bl); }
 template <int CTRL, int ROWS>
-WL_DEV void key_step(uint32_t& h, uint32_t& l) {
-    const uint32_t oh = (uint32_t)__builtin_amdgcn_update_dpp((int)h, (int)h, CTRL, ROWS, 0xF, false);
-    const uint32_t ol = (uint32_t)__builtin_amdgcn_update_dpp((int)l, (int)l, CTRL, ROWS, 0xF, false);
-    const bool t = key_gt(oh, ol, h, l);
-    h = t ? oh : h;
-    l = t ? ol : l;
+WL_DEV uint32_t max_step(uint32_t x) {
+    const uint32_t o = (uint32_t)__builtin_amdgcn_update_dpp((int)x, (int)x, CTRL, ROWS, 0xF, false);
+    return o > x ? o : x;
 }
-WL_DEV void wave_max_key(uint32_t& h, uint32_t& l) {
-    key_step<0xB1, 0xF>(h, l);   // quad_perm [1,0,3,2]
-    key_step<0x4E, 0xF>(h, l);   // quad_perm [2,3,0,1]
-    key_step<0x114, 0xF>(h, l);  // row_shr:4
-    key_step<0x118, 0xF>(h, l);  // row_shr:8
-    key_step<0x142, 0xA>(h, l);  // row_bcast:15
-    key_step<0x143, 0xC>(h, l);  // row_bcast:31
-    h = __builtin_amdgcn_readlane(h, 63);
-    l = __builtin_amdgcn_readlane(l, 63);
+WL_DEV uint32_t wave_max_u32(uint32_t x) {
+    x = max_step<0xB1, 0xF>(x);   // quad_perm [1,0,3,2]
+    x = max_step<0x4E, 0xF>(x);   // quad_perm [2,3,0,1]
+    x = max_step<0x114, 0xF>(x);  // row_shr:4
+    x = max_step<0x118, 0xF>(x);  // row_shr:8
+    x = max_step<0x142, 0xA>(x);  // row_bcast:15
+    x = max_step<0x143, 0xC>(x);  // row_bcast:31
+    return __builtin_amdgcn_readlane(x, 63);
 }
 // Order-preserving map of a float to uint32 (NaN never reaches it).
 WL_DEV uint32_t fkey(float f) {
     const uint32_t u = __float_as_uint(f);
     return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
-// E <= 256: K rounds of a wave-wide argmax (wave 0, 4 candidates per lane)
-// over keys (fkey(choice), ~e): the largest choice, ties to the lowest index,
-// i.e. the reference's K serial argmax passes (src/glm_layer_runner.cuh:318-330).
+// E <= 256: K rounds of a wave-wide argmax (wave 0, expert lane + 64m in
+// slot m of each lane) over fkey(choice): the largest choice, ties to the
+// lowest index (the first set bit of the first slot that holds the maximum),
+// i.e. the reference's K serial argmax passes (src/glm_layer_runner.cuh:
+// 318-330). Keys of real experts are > 0 (fkey(-inf) > 0); 0 marks an empty
+// slot or a taken expert.
 WL_DEV void topk_argmax(uint32_t E, uint32_t K, const float* sc, const float* ch, uint32_t* sidx, float* sw) {
     if (threadIdx.x < 64) {
         const uint32_t lane = threadIdx.x;
-        uint32_t kh[4], kl[4];
+        uint32_t key[4];
 #pragma unroll
         for (int m = 0; m < 4; m++) {
             const uint32_t e = lane + 64u * m;
-            kh[m] = e < E ? fkey(ch[e]) : 0u;  // 0: below every real key (fkey(-inf) > 0)
-            kl[m] = ~e;
+            key[m] = e < E ? fkey(ch[e]) : 0u;
         }
         for (uint32_t k = 0; k < K; k++) {
-            uint32_t bh = kh[0], bl = kl[0];
-#pragma unroll
-            for (int m = 1; m < 4; m++) {
-                const bool t = key_gt(kh[m], kl[m], bh, bl);
-                bh = t ? kh[m] : bh;
-                bl = t ? kl[m] : bl;
-            }
-            wave_max_key(bh, bl);
-            const uint32_t e = ~bl;
+            const uint32_t a01 = key[0] > key[1] ? key[0] : key[1];
+            const uint32_t a23 = key[2] > key[3] ? key[2] : key[3];
+            const uint32_t mx = wave_max_u32(a01 > a23 ? a01 : a23);
+            const uint64_t b0 = __builtin_amdgcn_ballot_w64(key[0] == mx);
+            const uint64_t b1 = __builtin_amdgcn_ballot_w64(key[1] == mx);
+            const uint64_t b2 = __builtin_amdgcn_ballot_w64(key[2] == mx);
+            const uint64_t b3 = __builtin_amdgcn_ballot_w64(key[3] == mx);
+            const uint32_t e = b0 ? (uint32_t)__builtin_ctzll(b0)
+                             : b1 ? 64u + (uint32_t)__builtin_ctzll(b1)
+                             : b2 ? 128u + (uint32_t)__builtin_ctzll(b2)
+                                  : 192u + (uint32_t)__builtin_ctzll(b3);
 #pragma unroll
             for (int m = 0; m < 4; m++)
-                if (lane + 64u * m == e) kh[m] = 0u;
-            if (lane == 0) {
-                sidx[k] = e;
-                sw[k] = sc[e];
-            }
+                if (lane + 64u * m == e) key[m] = 0u;
+            if (lane == 0) sidx[k] = e;
         }
+        // one wave: its LDS accesses complete in program order
+        if (lane < K) sw[lane] = sc[sidx[lane]];
     }
     lds_barrier();
 }
@@ -497,7 +497,7 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const DecodeDyn d) {
         const rsrc_t rt_rs = make_rsrc(a.router_w, E * H * 2u);
         u32x4 rw[RCH];
 #pragma unroll
-        for (int m = 0; m < RCH; m++) rw[m] = bld16(rt_rs, 16u * min(tid + kThreads * m, nch - 1u), min(w, E - 1u) * H * 2u);
+        for (int m = 0; m < RCH; m++) rw[m] = bld16_nt(rt_rs, 16u * min(tid + kThreads * m, nch - 1u), min(w, E - 1u) * H * 2u);
 
         // shared gate/up tiles (8 gate + 8 up rows). At G = SI/8 (GLM) the
         // tiles are mapped so that the 32 work-groups of one XCD hold 32
@@ -517,7 +517,7 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const DecodeDyn d) {
             const uint32_t voff = min(tile, nsg - 1u) * nkt * 1024u + 16u * lane;
             const uint32_t kt0 = v * sg_per + b * kNB;
 #pragma unroll
-            for (int i = 0; i < kNB; i++) B.w[i] = bld16(sg_rs, voff, (kt0 + i) * 1024u);
+            for (int i = 0; i < kNB; i++) B.w[i] = bld16_nt(sg_rs, voff, (kt0 + i) * 1024u);
         };
         f32x4 gacc;
         auto sg_consume = [&](uint32_t b, const Batch& B) {
@@ -544,13 +544,15 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const DecodeDyn d) {
         };
         bool lsl_sent = false;
         auto sd_issue = [&](uint32_t tile) {
-#pragma unroll
-            for (int i = 0; i < SDV; i++)  // row tid + 512 i of the tile: 16 bytes, rows past H read zeros
-                sdw[i] = bld16(sd_rs, (tile * H + tid) * 16u, kThreads * i * 16u);
+            // the logit slots go first: the top-k reads them before it needs
+            // these rows, and loads complete in issue order
             if (!lsl_sent) {
                 lsl_load();
                 lsl_sent = true;
             }
+#pragma unroll
+            for (int i = 0; i < SDV; i++)  // row tid + 512 i of the tile: 16 bytes, rows past H read zeros
+                sdw[i] = bld16_nt(sd_rs, (tile * H + tid) * 16u, kThreads * i * 16u);
         };
         const uint32_t tile0 = tile_of(0);
         sg_issue(tile0, 0, bA);
@@ -607,7 +609,7 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const DecodeDyn d) {
         for (uint32_t r = w, first = 1; r < E; r += G, first = 0) {
             if (!first) {
 #pragma unroll
-                for (int m = 0; m < RCH; m++) rw[m] = bld16(rt_rs, 16u * min(tid + kThreads * m, nch - 1u), r * H * 2u);
+                for (int m = 0; m < RCH; m++) rw[m] = bld16_nt(rt_rs, 16u * min(tid + kThreads * m, nch - 1u), r * H * 2u);
             }
             float pd = 0.f;
 #pragma unroll
@@ -645,6 +647,30 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const DecodeDyn d) {
         // the down projection applied to every output row, into pv
         const uint32_t ntiles = w < nsg ? cdiv(nsg - w, G) : 0u;
         for (uint32_t i = tid; i < H; i += kThreads) pv[i] = 0.f;  // xn is no longer needed
+        // the down columns of a tile: pv[r] += sum_c sdw[r][c] * smf[c]
+        auto sd_compute = [&]() {
+            const float4 m0 = *(const float4*)smf, m1 = *(const float4*)(smf + 4);
+#pragma unroll
+            for (int i = 0; i < SDV; i++) {
+                const uint32_t r = tid + kThreads * i;
+                if (r < H) {
+                    float x = 0.f;
+                    x = fmaf(bf2f(sdw[i].x & 0xFFFFu), m0.x, x);
+                    x = fmaf(bf2f(sdw[i].x >> 16), m0.y, x);
+                    x = fmaf(bf2f(sdw[i].y & 0xFFFFu), m0.z, x);
+                    x = fmaf(bf2f(sdw[i].y >> 16), m0.w, x);
+                    x = fmaf(bf2f(sdw[i].z & 0xFFFFu), m1.x, x);
+                    x = fmaf(bf2f(sdw[i].z >> 16), m1.y, x);
+                    x = fmaf(bf2f(sdw[i].w & 0xFFFFu), m1.z, x);
+                    x = fmaf(bf2f(sdw[i].w >> 16), m1.w, x);
+                    pv[r] += x;
+                }
+            }
+        };
+        // The last tile's down columns are applied after the top-k and the
+        // first routed loads are issued: its rows stay in flight meanwhile, so
+        // HBM keeps streaming through the top-k.
+        bool sd_pending = false;
         for (uint32_t ti = 0; ti < ntiles; ti++) {
             const uint32_t tile = tile_of(ti);
             if (ti != 0) {
@@ -677,24 +703,12 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const DecodeDyn d) {
                 gst(a.smid + tile * 8 + tid, mid);
             }
             lds_barrier();
-            const float4 m0 = *(const float4*)smf, m1 = *(const float4*)(smf + 4);
-#pragma unroll
-            for (int i = 0; i < SDV; i++) {
-                const uint32_t r = tid + kThreads * i;
-                if (r < H) {
-                    float x = 0.f;
-                    x = fmaf(bf2f(sdw[i].x & 0xFFFFu), m0.x, x);
-                    x = fmaf(bf2f(sdw[i].x >> 16), m0.y, x);
-                    x = fmaf(bf2f(sdw[i].y & 0xFFFFu), m0.z, x);
-                    x = fmaf(bf2f(sdw[i].y >> 16), m0.w, x);
-                    x = fmaf(bf2f(sdw[i].z & 0xFFFFu), m1.x, x);
-                    x = fmaf(bf2f(sdw[i].z >> 16), m1.y, x);
-                    x = fmaf(bf2f(sdw[i].w & 0xFFFFu), m1.z, x);
-                    x = fmaf(bf2f(sdw[i].w >> 16), m1.w, x);
-                    pv[r] += x;
-                }
+            if (ti + 1u < ntiles) {
+                sd_compute();
+                lds_barrier();
+            } else {
+                sd_pending = true;
             }
-            lds_barrier();
         }
         // pv -> rows [32b, 32b+32) into block b, slot w of dst ([H/32][G][32]),
         // agent-scope 16-byte stores
@@ -707,7 +721,20 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const DecodeDyn d) {
                                                        kSC1);
             }
         };
-        if (d.taps) publish(a.tsh);  // the shared-expert contribution alone, for the tap
+        // the deferred down columns, then (taps on) the shared-expert
+        // contribution alone, published for the tap
+        bool tsh_pending = d.taps != 0;
+        auto finish_shared = [&]() {
+            if (sd_pending) {
+                sd_compute();
+                sd_pending = false;
+            }
+            if (tsh_pending) {
+                lds_barrier();
+                publish(a.tsh);
+                tsh_pending = false;
+            }
+        };
         WL_TL(3);
 
         // ---- top-k: every logit of this call must be published (a slot that
@@ -742,6 +769,7 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const DecodeDyn d) {
             }
             if (!ok) return;
         }
+        WL_TL(4);
         if (E <= 256u) topk_argmax(E, K, tk_sc, tk_ch, tk_idx, tk_w);
         else topk_rank(E, K, tk_sc, tk_ch, tk_idx, tk_w);
         WL_TL(5);
@@ -776,8 +804,8 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const DecodeDyn d) {
             const uint32_t i0 = gu ? b * kNB : v * dq_per + (b - nbg) * kNB;
             const uint32_t wv = gu ? gu_voff : dn_voff;
 #pragma unroll
-            for (int i = 0; i < kNB; i++) B.w[i] = bld16(r_rs, wv, (i0 + i) * 1024u);
-            B.sv = bld16(r_rs, gu ? gus_voff : dns_voff, (i0 / 16u) * 1024u);
+            for (int i = 0; i < kNB; i++) B.w[i] = bld16_nt(r_rs, wv, (i0 + i) * 1024u);
+            B.sv = bld16_nt(r_rs, gu ? gus_voff : dns_voff, (i0 / 16u) * 1024u);
         };
         f32x4 racc;
         bf16x8 A0, A1;
@@ -856,8 +884,16 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const DecodeDyn d) {
 
         bool first_unit = true;
         for (uint32_t u = w; u < P.U; u += G) {
-            uk = u % K;
-            uj = u / K;
+#ifdef WL_UNIT_MAP
+            if (GLM) {  // XCD x = u % 8 takes slices x, x+8, x+16, x+24 of every expert
+                uk = (u / 8u) % 8u;
+                uj = (u % 8u) + 8u * (u / 64u);
+            } else
+#endif
+            {
+                uk = u % K;
+                uj = u / K;
+            }
             blk = uni_ptr(tk_blk[tk_idx[uk]]);
             wk = topk_weight(a, K, tk_w, uk);
             if (blk == nullptr) {
@@ -877,10 +913,12 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const DecodeDyn d) {
             }
             r_issue(0, bA);
             r_issue(1, bB);
+            finish_shared();  // pv is read by the down items, after the gate/up barrier
             racc = f32x4{0.f, 0.f, 0.f, 0.f};
             pingpong(nbr, bA, bB, r_issue, r_consume);
             WL_TL(8);
         }
+        finish_shared();
         lds_barrier();
 
         // ---- publish this work-group's partial (the combine of block b reads
