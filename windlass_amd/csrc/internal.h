@@ -119,6 +119,7 @@ struct DecodeDyn {
     float* out;                 // [H]
     uint32_t seg_lo, seg_hi;
     uint32_t epoch;             // different for every call of the context, never 0
+    uint32_t bar_seq;           // fused launches: this launch's grid-barrier number (>= 1)
     int32_t taps;               // 1: also produce the shared-expert output tap
 };
 

@@ -213,21 +213,24 @@ WL_DEV void raise_error(uint32_t* sync, const SyncMap& m, uint32_t bits) {
     __hip_atomic_fetch_or((g_u32*)(sync + m.error), bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Grid barrier `seq` (a value no earlier barrier of the context used). All
-// cross-work-group data is in uncached memory, so completing a work-group's
-// stores before its arrival is the whole release, and nothing is needed to
-// acquire. Arrival: one counter per group of work-groups (w mod 8, i.e. one
-// per XCD) and one counter of complete groups; the work-group that completes
-// the last group zeroes the counters and then writes `seq` to every
-// work-group's release word, which each work-group polls. Bounded: returns
-// false, with E_SPIN raised, if the release does not come, and false if
-// another work-group raised an error meanwhile.
+// Grid barrier number `seq` (1, 2, ... over the life of the sync block).
+// Arrival: one counter per group of work-groups (w mod 8, i.e. one per XCD)
+// and one counter of complete groups. The counters only grow: after barrier
+// n a group counter holds n x members and the group counter n x groups, so
+// the arrival that completes a group (and then the grid) is recognised from
+// the value its increment returns, with no reset. The work-group that
+// completes the grid writes `seq` to every work-group's release word, which
+// each work-group polls. Completing a work-group's cross-work-group stores
+// before its arrival is the whole release; the readers use agent-scope loads.
+// Bounded: returns false, with E_SPIN raised, if the release does not come,
+// and false if another work-group raised an error meanwhile.
 WL_DEV bool grid_barrier(uint32_t* sync, const SyncMap& m, uint32_t seq, uint32_t w, uint32_t G,
                          uint32_t* s_flag, bool all_waves_stored) {
     // Only wave 0 wrote cross-work-group data unless all_waves_stored; the
     // other waves then keep whatever loads they have in flight.
     if (all_waves_stored || threadIdx.x < 64) vm_drain();
     lds_barrier();
+    WL_TL(11);
     if (threadIdx.x < 64) {
         const uint32_t lane = threadIdx.x;
         const uint32_t grp = w & 7u;
@@ -236,18 +239,14 @@ WL_DEV bool grid_barrier(uint32_t* sync, const SyncMap& m, uint32_t seq, uint32_
         uint32_t old = 0;
         if (lane == 0) old = rmw_inc(sync + m.bar_grp + grp * kLineWords);
         old = __shfl(old, 0, 64);
-        if (old == members - 1u) {
+        if (old + 1u == members * seq) {
             uint32_t old2 = 0;
             if (lane == 0) old2 = rmw_inc(sync + m.bar_all);
             old2 = __shfl(old2, 0, 64);
-            if (old2 == groups - 1u) {
-                if (lane < 8) st_sync(sync + m.bar_grp + lane * kLineWords, 0u);
-                if (lane == 0) st_sync(sync + m.bar_all, 0u);
-                vm_drain();
+            if (old2 + 1u == groups * seq)
                 for (uint32_t f = lane; f < G; f += 64) st_sync(sync + m.bar_rel + f * kLineWords, seq);
-            }
         }
-        uint32_t ok = 1u;
+    uint32_t ok = 1u;
         for (uint32_t spins = 0;; spins++) {
             uint32_t r = 0, e = 0;
             if (lane == 0) {
@@ -267,6 +266,7 @@ WL_DEV bool grid_barrier(uint32_t* sync, const SyncMap& m, uint32_t seq, uint32_
         }
         if (lane == 0) *s_flag = ok;
     }
+    WL_TL(12);
     lds_barrier();
     const bool ok = *s_flag != 0u;
     lds_barrier();
@@ -884,16 +884,8 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const DecodeDyn d) {
 
         bool first_unit = true;
         for (uint32_t u = w; u < P.U; u += G) {
-#ifdef WL_UNIT_MAP
-            if (GLM) {  // XCD x = u % 8 takes slices x, x+8, x+16, x+24 of every expert
-                uk = (u / 8u) % 8u;
-                uj = (u % 8u) + 8u * (u / 64u);
-            } else
-#endif
-            {
-                uk = u % K;
-                uj = u / K;
-            }
+            uk = u % K;
+            uj = u / K;
             blk = uni_ptr(tk_blk[tk_idx[uk]]);
             wk = topk_weight(a, K, tk_w, uk);
             if (blk == nullptr) {
@@ -925,7 +917,7 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const DecodeDyn d) {
         // its G slots contiguously), unless the down items already did
         if (!direct) publish(a.part);
         if (d.seg_hi >= 1u) {
-            if (!grid_barrier(a.sync, SM, d.epoch, w, G, misc + 8, true)) return;
+            if (!grid_barrier(a.sync, SM, d.bar_seq, w, G, misc + 8, true)) return;
         }
         WL_TL(9);
     }

@@ -58,6 +58,7 @@ struct wl_ctx {
     wl::Plan plan{};
     uint32_t grid = 0;
     uint32_t epoch = 0;
+    uint32_t bar_seq = 0;  // grid barriers run since the sync block was last zeroed
     void* uc_block = nullptr;   // uncached scratch (returned to the process pool on destroy)
     size_t uc_bytes = 0;
     // context-owned slot pool
@@ -379,7 +380,15 @@ static wl_status run_layer(wl_ctx* c, uint32_t layer, const float* d_hidden, con
         if (e != 0) return hip_fail(c, (hipError_t)e, "decode launch");
         return WL_OK;
     };
-    if (c->sched == WL_SCHED_FUSED) return launch(0, 1);
+    if (c->sched == WL_SCHED_FUSED) {
+        if (++c->bar_seq == 0u) {  // after 2^32 barriers: zero the counters, start again at 1
+            hipError_t e = hipMemsetAsync(c->sync, 0, 4 * (size_t)c->sm.words, (hipStream_t)stream);
+            if (e != hipSuccess) return hip_fail(c, e, "sync block reset");
+            c->bar_seq = 1u;
+        }
+        dyn.bar_seq = c->bar_seq;
+        return launch(0, 1);
+    }
     wl_status s;
     if ((s = launch(0, 0)) != WL_OK) return s;
     return launch(1, 1);
@@ -441,6 +450,7 @@ wl_status wl_check_error(wl_ctx* c, void* stream) {
         // a launch that gave up may have left barrier counters mid-count
         (void)hipMemset(c->sync, 0, 4 * (size_t)c->sm.words);
         (void)hipDeviceSynchronize();
+        c->bar_seq = 0;
         return fail(c, WL_ERR_DEVICE, "device error bits 0x%x%s%s", flag,
                     (flag & wl::E_SPIN) ? " [dependency wait expired]" : "",
                     (flag & wl::E_NOT_RESIDENT) ? " [routed expert not resident]" : "");
