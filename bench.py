@@ -12,6 +12,12 @@ previous step; every step also has its own hidden state, so routing differs.
 Prints ONE JSON line. `value` is microseconds per layer (lower is better),
 measured with HIP events on the launch stream over the timed steps; the
 roofline block divides the layer's algorithmic bytes by that time.
+
+--workload chain measures BASELINE.json configs[2] instead: 24 resident GLM
+MoE layers (6144 expert blocks, 123 GB of HBM), h <- h + moe(h) layer by
+layer; a step is one decode token through all 24 layers, starting from its own
+seeded N(0,1) hidden state. `value` is then microseconds per layer within the
+chain (step time / 24) and tokens_per_s is reported beside it.
 """
 import argparse
 import json
@@ -84,6 +90,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--layers", type=int, default=8, help="distinct resident layer copies to rotate over")
     ap.add_argument("--sched", choices=["fused", "phased"], default="fused")
+    ap.add_argument("--workload", choices=["layer", "chain"], default="layer",
+                    help="layer: config 1 (default); chain: config 2, 24 layers per step")
+    ap.add_argument("--chain-layers", type=int, default=24)
     ap.add_argument("--seed", type=int, default=1)
     ap.add_argument("--cpu-sample", type=int, default=3, help="layers timed for the CPU baseline (0: skip)")
     ap.add_argument("--traffic-json", default=os.path.join(ROOT, "profiles", "decode_layer_traffic.json"))
@@ -107,6 +116,13 @@ def main():
 
     c = dict(GLM)
     H = c["hidden"]
+    chain = args.workload == "chain"
+    if chain:
+        args.layers = args.chain_layers
+        if "--steps" not in sys.argv:
+            args.steps = 64
+        if "--warmup" not in sys.argv:
+            args.warmup = 4
     t_build = time.time()
     dm = DeviceModel(c, seed=args.seed, n_layers=args.layers)
     dm.ctx.set_schedule(moe.SCHED_FUSED if args.sched == "fused" else moe.SCHED_PHASED)
@@ -118,7 +134,13 @@ def main():
     stream = hip.Stream()
     build_s = time.time() - t_build
 
+    d_h, d_tmp = hip.DeviceBuffer(4 * H), hip.DeviceBuffer(4 * H)
+
     def step(i):
+        if chain:  # one token: its own start state, then h <- h + moe(h) through every layer
+            hip.copy_d2d(d_h.ptr, d_hs.ptr + 4 * H * (i % n_h), 4 * H, stream.handle)
+            dm.ctx.run_chain(0, args.layers, d_h.ptr, d_tmp.ptr, stream.handle)
+            return
         l = i % args.layers
         dm.ctx.run_moe(l, d_hs.ptr + 4 * H * (i % n_h), d_out.ptr + 4 * H * l, stream.handle)
 
@@ -134,7 +156,8 @@ def main():
     e1.synchronize()
     ms = e0.elapsed_ms(e1)
     dm.ctx.check_error(stream.handle)
-    us_per_layer = ms * 1e3 / args.steps
+    layers_per_step = args.layers if chain else 1
+    us_per_layer = ms * 1e3 / args.steps / layers_per_step
 
     if args.calib_copy_mb > 0:
         nb = args.calib_copy_mb << 20
@@ -161,7 +184,8 @@ def main():
         us_one, n_one = cpu_baseline(c, args.seed, max(1, args.cpu_sample - 1), 1)
         cpu = {"value": round(us_all, 1), "unit": "us/layer", "cores": ncores, "kind": "port",
                "sample": f"numpy oracle (dequant to f32 + OpenBLAS matvecs) on {n_all} config-1 layers, median; "
-                         f"router+8 experts+shared; expert bytes pre-generated",
+                         f"router+8 experts+shared; expert bytes pre-generated"
+                         + ("; a chain token is 24 such layers (extrapolated x24)" if chain else ""),
                "value_1thread": round(us_one, 1), "gpu_speedup": round(us_all / us_per_layer, 1)}
 
     line = {
@@ -171,16 +195,19 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(us_per_layer / 1e3, 6),
+        "ms_per_step": round(us_per_layer * layers_per_step / 1e3, 6),
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "mxfp4/bf16 weights, f32 activations and accumulation",
         "data": "synthetic",
-        "config": {"workload": "config1: one GLM MoE decode layer, bs=1", "hidden": H,
-                   "moe_inter": c["moe_inter"], "n_routed_experts": c["n_routed_experts"],
+        "config": {"workload": (f"config2: chain of {args.layers} resident GLM MoE decode layers, bs=1, "
+                                f"h <- h + moe(h)" if chain else "config1: one GLM MoE decode layer, bs=1"),
+                   "hidden": H, "moe_inter": c["moe_inter"], "n_routed_experts": c["n_routed_experts"],
                    "n_experts_per_tok": c["n_experts_per_tok"], "shared": "bf16 inter 2048",
-                   "rotating_layers": args.layers, "schedule": args.sched, "global_batch": 1},
+                   ("chain_layers" if chain else "rotating_layers"): args.layers, "schedule": args.sched,
+                   "global_batch": 1},
+        "tokens_per_s": round(1e6 / (us_per_layer * layers_per_step), 2),
         "tokens_per_s_per_layer": round(1e6 / us_per_layer, 1),
         "achieved_GBps": round(achieved, 1),
         "pct_of_hbm_peak": round(100 * achieved / PEAK_HBM_GBPS, 2),

@@ -53,8 +53,10 @@ def rms_norm(x, w, eps):
 
 
 def silu(x):
-    """x / (1 + exp(-x)) (tools/ref_glm_chain.py:123-124)."""
-    return x / (np.float32(1.0) + np.exp(-x))
+    """x / (1 + exp(-x)) (tools/ref_glm_chain.py:123-124). exp(-x) overflows
+    to inf for x < -88, which gives the correct limit -0."""
+    with np.errstate(over="ignore"):
+        return x / (np.float32(1.0) + np.exp(-x))
 
 
 def route(x_norm, gate_w, bias, top_k, routed_scaling, norm_topk_prob):
