@@ -171,6 +171,57 @@ wl_status wl_set_schedule(wl_ctx* ctx, int32_t sched);
  * src/glm_layer_runner.cuh:431-436). */
 wl_status wl_set_taps(wl_ctx* ctx, int32_t enable);
 
+/* ---- HBM expert cache (config 4: more experts than HBM holds) -------------
+ * Replaces the reference's ExpertCache (src/glm_expert_cache.cuh:99-509): an
+ * LRU pool of `capacity` native expert blocks in HBM, keyed by (layer,
+ * expert), filled from host memory on a miss. Where the reference reads
+ * packed files with pread into pinned staging, this cache copies directly
+ * from pinned host blocks that the caller provides through `host_block`
+ * (native layout, wl_native_block_bytes bytes each, allocated with
+ * hipHostMalloc; NULL for an unknown expert fails the call with WL_ERR_IO).
+ *
+ * A layer with no experts bound through wl_slot_bind runs through the cache:
+ * wl_run_moe routes it (norm, router, top-k on the device), waits for the
+ * ids on the host (the reference's one host round trip per layer,
+ * src/glm_layer_runner.cuh:391-396), resolves them (hits bump the LRU,
+ * misses evict the least-recent key and start a host-to-device copy on a
+ * side stream), orders the caller's stream after those copies and runs the
+ * layer. Requires capacity >= 2 x n_experts_per_tok.
+ *
+ * With speculation on, wl_run_chain also applies layer l+1's router to layer
+ * l's input while layer l runs and starts the copies of the predicted
+ * misses then (cross-layer prefetch); those requests update the LRU order but
+ * are counted in spec_* only. */
+typedef const uint8_t* (*wl_host_block_fn)(void* user, uint32_t layer, uint32_t expert);
+wl_status wl_cache_create(wl_ctx* ctx, uint32_t capacity, wl_host_block_fn host_block, void* user);
+wl_status wl_cache_set_speculation(wl_ctx* ctx, int32_t enable);
+
+typedef struct wl_cache_stats {
+    uint64_t hits, misses, evictions;  /* reference ExpertCache counters (:334-336) */
+    uint64_t spec_requests;            /* speculative (predicted) requests */
+    uint64_t spec_copies;              /* speculative requests that started a copy */
+    uint64_t spec_hits;                /* real requests served by a speculative copy */
+    uint64_t bytes_h2d;                /* bytes copied host -> device */
+    uint32_t used, capacity;           /* occupied / total slots */
+} wl_cache_stats;
+wl_status wl_cache_get_stats(wl_ctx* ctx, wl_cache_stats* out);
+wl_status wl_cache_reset_stats(wl_ctx* ctx);
+
+/* ExpertCache::prefetch + get_async (src/glm_expert_cache.cuh:186-275):
+ * resolve n experts of `layer` at once (hits and misses counted), starting
+ * the copies of the misses; wl_cache_get then returns the device block of one
+ * resolved expert and orders `stream` after its copy. wl_cache_get on an
+ * expert that was not resolved resolves it alone. */
+wl_status wl_cache_prefetch(wl_ctx* ctx, uint32_t layer, const int32_t* experts, uint32_t n, void* stream);
+wl_status wl_cache_get(wl_ctx* ctx, uint32_t layer, uint32_t expert, void* stream, uint8_t** d_block);
+
+/* Test hook (no device use): replays `n_keys` requests through the cache's
+ * LRU bookkeeping with `capacity` slots, in batches of `batch` keys (keys
+ * repeated within a batch are skipped, as in a prefetch batch). hit_out[i]
+ * (optional) is 1 for a hit, 0 for a miss, 2 for a skipped duplicate. */
+wl_status wl_lru_replay(uint32_t capacity, const uint32_t* keys, uint32_t n_keys, uint32_t batch,
+                        uint8_t* hit_out, uint64_t* hits, uint64_t* misses, uint64_t* evictions);
+
 /* ---- single-expert building blocks ---------------------------------------
  * y[N] = W . x for MXFP4 W ([N,K/2] packed nibbles + [N,K/32] E8M0 scales) and
  * f32 x [K]. Replaces launch_dequant_matvec_mxfp4 (src/glm_kernels.cuh:104-110).

@@ -205,6 +205,13 @@ struct NativeShared {
 int launch_decode(const DecodeArgs* d_args, const DecodeDyn& dyn, uint32_t H, uint32_t I, uint32_t SI,
                   uint32_t E, uint32_t K, uint32_t grid, void* stream);
 int decode_max_lds();
+// Routing only (cache-backed layers): norm, router, top-k -> idx/topw/logits.
+size_t route_lds_bytes(uint32_t H, uint32_t E);
+int launch_route(const DecodeArgs* d_args, const float* hidden, uint32_t epoch, uint32_t H, uint32_t E,
+                 uint32_t grid, void* stream);
+// table[e] = ptrs[k] where ids[k] == e, null elsewhere (n <= 32).
+int launch_slot_fill(const uint8_t** table, uint32_t E, const int32_t* ids, const uint8_t* const* ptrs, uint32_t n,
+                     void* stream);
 int launch_dequant_matvec(const uint8_t* W, const uint8_t* S, const float* x, float* y, uint32_t N,
                           uint32_t K, void* stream);
 int launch_expert_ffn(const uint8_t* blk, uint64_t gw_off, uint64_t gs_off, uint64_t uw_off,

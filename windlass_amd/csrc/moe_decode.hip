@@ -439,6 +439,71 @@ WL_DEV bool block_all(bool p, uint32_t* flags) {
     return r;
 }
 
+// ---- routing prologue pieces shared by the decode and route kernels ---------
+// Both kernels must produce bit-identical logits (a cache-backed layer is
+// routed by route_kernel, its experts resolved by the host, and then run by
+// the decode kernel, which routes again and must select the same ids), so the
+// arithmetic lives here once.
+constexpr int kHV = 4;   // float4 of the hidden state per thread: H <= 8192
+constexpr int kRCH = 2;  // 16-byte router chunks per thread: H <= 8192
+// 1 / sqrt(mean(x^2) + eps) over the work-group's hidden-state registers.
+WL_DEV float norm_rinv(const float4 (&hv)[kHV], float* red, uint32_t H, float eps) {
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < kHV; i++) {
+        ss = __fadd_rn(ss, __fmul_rn(hv[i].x, hv[i].x));
+        ss = __fadd_rn(ss, __fmul_rn(hv[i].y, hv[i].y));
+        ss = __fadd_rn(ss, __fmul_rn(hv[i].z, hv[i].z));
+        ss = __fadd_rn(ss, __fmul_rn(hv[i].w, hv[i].w));
+    }
+    const float tot = block_sum(ss, red);
+    return 1.0f / sqrtf(tot / (float)H + eps);
+}
+// w * (x * rinv) (tools/ref_glm_chain.py:63-80; src/glm_primitives.cuh:35-62)
+WL_DEV float norm_value(float x, float rinv, bool has_ln, uint32_t ln_bits) {
+    float y = __fmul_rn(x, rinv);
+    if (has_ln) y = __fmul_rn(y, bf2f(ln_bits));
+    return y;
+}
+// This thread's share of one router row (bf16 x f32, fp32 accumulate),
+// reduced over the wave.
+WL_DEV float router_partial(const u32x4 (&rw)[kRCH], const float* xn, uint32_t nch) {
+    float pd = 0.f;
+#pragma unroll
+    for (int m = 0; m < kRCH; m++) {
+        const uint32_t c = threadIdx.x + kThreads * m;
+        if (c < nch) {
+            const float4 x0 = *(const float4*)(xn + 8 * c);
+            const float4 x1 = *(const float4*)(xn + 8 * c + 4);
+            pd = fmaf(bf2f(rw[m].x & 0xFFFFu), x0.x, pd);
+            pd = fmaf(bf2f(rw[m].x >> 16), x0.y, pd);
+            pd = fmaf(bf2f(rw[m].y & 0xFFFFu), x0.z, pd);
+            pd = fmaf(bf2f(rw[m].y >> 16), x0.w, pd);
+            pd = fmaf(bf2f(rw[m].z & 0xFFFFu), x1.x, pd);
+            pd = fmaf(bf2f(rw[m].z >> 16), x1.y, pd);
+            pd = fmaf(bf2f(rw[m].w & 0xFFFFu), x1.z, pd);
+            pd = fmaf(bf2f(rw[m].w >> 16), x1.w, pd);
+        }
+    }
+    for (int o = 32; o > 0; o >>= 1) pd += __shfl_xor(pd, o, 64);
+    return pd;
+}
+// Sum of the 8 wave partials of router row r (slot 48 of each wave's red
+// line), published as one 64-bit word (epoch << 32 | bits) with an
+// agent-scope store: a reader that sees this call's epoch has the value.
+WL_DEV void router_publish(float pd, float* red, uint64_t* lslot, uint32_t r, uint32_t epoch) {
+    if ((threadIdx.x & 63) == 0) red[(threadIdx.x >> 6) * 64 + 48] = pd;
+    lds_barrier();
+    if (threadIdx.x == 0) {
+        float sum = 0.f;
+#pragma unroll
+        for (int wv = 0; wv < kWaves; wv++) sum += red[wv * 64 + 48];
+        __hip_atomic_store((__attribute__((address_space(1))) uint64_t*)(lslot + r),
+                           ((uint64_t)epoch << 32) | __float_as_uint(sum), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    lds_barrier();
+}
+
 // ---- the decode kernel -------------------------------------------------------
 // GLM = true compiles the GLM shape (H 6144, I 2048, SI 2048, E 256, K 8) with
 // every shape constant known; GLM = false reads the shapes from the record.
@@ -480,7 +545,7 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const DecodeDyn d) {
         const uint32_t bias0 = __builtin_amdgcn_raw_buffer_load_b32(bs_rs, (int)(4u * tid), 0, 0);
         const uint64_t slot0 = __builtin_bit_cast(uint64_t, __builtin_amdgcn_raw_buffer_load_b64(sl_rs, (int)(8u * tid), 0, 0));
         // hidden state and norm weight first: they are consumed first
-        constexpr int HV = 4;  // float4 per thread: H <= 8192
+        constexpr int HV = kHV;
         float4 hv[HV];
         uint2 lv[HV];
         const rsrc_t hid_rs = make_rsrc(d.hidden, H * 4u);
@@ -492,7 +557,7 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const DecodeDyn d) {
             lv[i] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(ln_rs, (int)(8u * j), 0, 0));
         }
         // the first router row of this work-group
-        constexpr int RCH = 2;  // 16-byte chunks per thread: H <= 8192
+        constexpr int RCH = kRCH;
         const uint32_t nch = H / 8;
         const rsrc_t rt_rs = make_rsrc(a.router_w, E * H * 2u);
         u32x4 rw[RCH];
@@ -560,16 +625,7 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const DecodeDyn d) {
 
         // RMSNorm: w * (x * (1/sqrt(mean(x^2) + eps))) in fp32
         // (tools/ref_glm_chain.py:63-80; src/glm_primitives.cuh:35-62)
-        float ss = 0.f;
-#pragma unroll
-        for (int i = 0; i < HV; i++) {
-            ss = __fadd_rn(ss, __fmul_rn(hv[i].x, hv[i].x));
-            ss = __fadd_rn(ss, __fmul_rn(hv[i].y, hv[i].y));
-            ss = __fadd_rn(ss, __fmul_rn(hv[i].z, hv[i].z));
-            ss = __fadd_rn(ss, __fmul_rn(hv[i].w, hv[i].w));
-        }
-        const float tot = block_sum(ss, red);
-        const float rinv = 1.0f / sqrtf(tot / (float)H + a.eps);
+        const float rinv = norm_rinv(hv, red, H, a.eps);
         float* xn = pv;
 #pragma unroll
         for (int i = 0; i < HV; i++) {
@@ -579,8 +635,7 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const DecodeDyn d) {
                 const uint32_t ls[4] = {lv[i].x & 0xFFFFu, lv[i].x >> 16, lv[i].y & 0xFFFFu, lv[i].y >> 16};
 #pragma unroll
                 for (int c = 0; c < 4; c++) {
-                    float x = __fmul_rn(xs[c], rinv);
-                    if (a.ln_w) x = __fmul_rn(x, bf2f(ls[c]));
+                    const float x = norm_value(xs[c], rinv, a.ln_w != nullptr, ls[c]);
                     const uint32_t col = 4 * j + c;
                     xn[col] = x;
                     uint32_t ph, pm, pl;
@@ -611,35 +666,7 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const DecodeDyn d) {
 #pragma unroll
                 for (int m = 0; m < RCH; m++) rw[m] = bld16_nt(rt_rs, 16u * min(tid + kThreads * m, nch - 1u), r * H * 2u);
             }
-            float pd = 0.f;
-#pragma unroll
-            for (int m = 0; m < RCH; m++) {
-                const uint32_t c = tid + kThreads * m;
-                if (c < nch) {
-                    const float4 x0 = *(const float4*)(xn + 8 * c);
-                    const float4 x1 = *(const float4*)(xn + 8 * c + 4);
-                    pd = fmaf(bf2f(rw[m].x & 0xFFFFu), x0.x, pd);
-                    pd = fmaf(bf2f(rw[m].x >> 16), x0.y, pd);
-                    pd = fmaf(bf2f(rw[m].y & 0xFFFFu), x0.z, pd);
-                    pd = fmaf(bf2f(rw[m].y >> 16), x0.w, pd);
-                    pd = fmaf(bf2f(rw[m].z & 0xFFFFu), x1.x, pd);
-                    pd = fmaf(bf2f(rw[m].z >> 16), x1.y, pd);
-                    pd = fmaf(bf2f(rw[m].w & 0xFFFFu), x1.z, pd);
-                    pd = fmaf(bf2f(rw[m].w >> 16), x1.w, pd);
-                }
-            }
-            for (int o = 32; o > 0; o >>= 1) pd += __shfl_xor(pd, o, 64);
-            if (lane == 0) red[v * 64 + 48] = pd;
-            lds_barrier();
-            if (tid == 0) {
-                float sum = 0.f;
-#pragma unroll
-                for (int wv = 0; wv < kWaves; wv++) sum += red[wv * 64 + 48];
-                __hip_atomic_store((__attribute__((address_space(1))) uint64_t*)(a.lslot + r),
-                                   ((uint64_t)d.epoch << 32) | __float_as_uint(sum), __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
-            }
-            lds_barrier();
+            router_publish(router_partial(rw, xn, nch), red, a.lslot, r, d.epoch);
         }
         WL_TL(2);
 
@@ -970,6 +997,110 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const DecodeDyn d) {
     }
 }
 
+// ---- routing only (cache-backed layers) ------------------------------------
+// RMSNorm, the router rows of this work-group (r = w + G*i, epoch-tagged
+// logits, the same arithmetic as the decode kernel), then work-group 0 gathers
+// every logit and writes the top-k ids and weights (idx, topw) and the logits.
+// The host reads the ids, resolves the experts through its LRU slot pool, and
+// only then runs the layer (reference run_moe's router + D2H staging,
+// src/glm_layer_runner.cuh:386-396). LDS: xn [H] | red [8 x 64] | topk.
+__global__ void __launch_bounds__(kThreads) route_kernel(const DecodeArgs* __restrict__ pa, const float* hidden,
+                                                         uint32_t epoch) {
+    const DecodeArgs& a = *pa;
+    const uint32_t H = a.H, E = a.E, K = a.K;
+    const uint32_t G = gridDim.x, w = blockIdx.x, tid = threadIdx.x;
+    extern __shared__ __align__(16) uint8_t lds[];
+    float* xn = (float*)lds;
+    float* red = xn + ((H + 3u) & ~3u);
+    float* tk_sc = red + kWaves * 64;
+    float* tk_ch = tk_sc + E;
+    uint32_t* tk_idx = (uint32_t*)(tk_ch + E);
+    float* tk_w = (float*)(tk_idx + 32);
+    uint32_t* flags = (uint32_t*)(tk_w + 32);
+    const SyncMap SM = SyncMap::make();
+
+    float4 hv[kHV];
+    uint2 lv[kHV];
+    const rsrc_t hid_rs = make_rsrc(hidden, H * 4u);
+    const rsrc_t ln_rs = make_rsrc(a.ln_w ? (const void*)a.ln_w : (const void*)hidden, H * 2u);
+#pragma unroll
+    for (int i = 0; i < kHV; i++) {
+        const uint32_t j = tid + kThreads * i;
+        hv[i] = __builtin_bit_cast(float4, bld16(hid_rs, 16u * j, 0u));
+        lv[i] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(ln_rs, (int)(8u * j), 0, 0));
+    }
+    const uint32_t nch = H / 8;
+    const rsrc_t rt_rs = make_rsrc(a.router_w, E * H * 2u);
+    const float rinv = norm_rinv(hv, red, H, a.eps);
+#pragma unroll
+    for (int i = 0; i < kHV; i++) {
+        const uint32_t j = tid + kThreads * i;
+        if (j < H / 4) {
+            const float xs[4] = {hv[i].x, hv[i].y, hv[i].z, hv[i].w};
+            const uint32_t ls[4] = {lv[i].x & 0xFFFFu, lv[i].x >> 16, lv[i].y & 0xFFFFu, lv[i].y >> 16};
+#pragma unroll
+            for (int c = 0; c < 4; c++) xn[4 * j + c] = norm_value(xs[c], rinv, a.ln_w != nullptr, ls[c]);
+        }
+    }
+    lds_barrier();
+    for (uint32_t r = w; r < E; r += G) {
+        u32x4 rw[kRCH];
+#pragma unroll
+        for (int m = 0; m < kRCH; m++) rw[m] = bld16_nt(rt_rs, 16u * min(tid + kThreads * m, nch - 1u), r * H * 2u);
+        router_publish(router_partial(rw, xn, nch), red, a.lslot, r, epoch);
+    }
+    if (w != 0) return;
+
+    // work-group 0: every logit of this call (bounded poll), then the top-k
+    for (uint32_t e = tid; e < E; e += kThreads) tk_ch[e] = gld(a.bias + e);
+    lds_barrier();
+    uint32_t done = 0;  // bit i: expert tid + 512 i scored
+    for (uint32_t spins = 0;; spins++) {
+        bool mine = true;
+        for (uint32_t i = 0, e = tid; e < E; i++, e += kThreads) {
+            if ((done >> i) & 1u) continue;
+            const uint64_t x = __hip_atomic_load((__attribute__((address_space(1))) uint64_t*)(a.lslot + e),
+                                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if ((uint32_t)(x >> 32) == epoch) {
+                topk_score(__uint_as_float((uint32_t)x), tk_ch[e], e, tk_sc, tk_ch);
+                gst(a.logits + e, __uint_as_float((uint32_t)x));
+                done |= 1u << i;
+            } else {
+                mine = false;
+            }
+        }
+        if (block_all(mine, flags)) break;
+        if (spins > (1u << 20)) {
+            if (tid == 0) raise_error(a.sync, SM, E_SPIN);
+            return;
+        }
+        __builtin_amdgcn_s_sleep(2);
+    }
+    if (E <= 256u) topk_argmax(E, K, tk_sc, tk_ch, tk_idx, tk_w);
+    else topk_rank(E, K, tk_sc, tk_ch, tk_idx, tk_w);
+    if (tid < K) {
+        gst(a.idx + tid, (int32_t)tk_idx[tid]);
+        gst(a.topw + tid, topk_weight(a, K, tk_w, tid));
+    }
+}
+
+// Slot table of one layer: table[e] = the block of expert e if e is one of the
+// n resolved ids, else null (an id the host did not resolve then raises
+// E_NOT_RESIDENT instead of reading a stale slot).
+struct SlotFill {
+    int32_t ids[32];
+    const uint8_t* ptrs[32];
+    uint32_t n;
+};
+__global__ void __launch_bounds__(256) slot_fill_kernel(const uint8_t** table, uint32_t E, const SlotFill f) {
+    for (uint32_t e = blockIdx.x * blockDim.x + threadIdx.x; e < E; e += gridDim.x * blockDim.x) {
+        const uint8_t* p = nullptr;
+        for (uint32_t k = 0; k < f.n; k++)
+            if ((uint32_t)f.ids[k] == e) p = f.ptrs[k];
+        table[e] = p;
+    }
+}
+
 // ---- standalone kernels: one MXFP4 matvec, one MXFP4 expert FFN -------------
 // x (fp32) split into bf16 pieces in LDS by the whole work-group.
 WL_DEV void pieces_to_lds(const float* x, uint32_t K, uint16_t* xp, uint32_t xps) {
@@ -1171,6 +1302,32 @@ static bool glm_shape(uint32_t H, uint32_t I, uint32_t SI, uint32_t E, uint32_t 
 }
 
 int decode_max_lds() { return 160 * 1024; }
+
+size_t route_lds_bytes(uint32_t H, uint32_t E) {
+    return 4u * (((H + 3u) & ~3u) + kWaves * 64u + 2u * E + 64u + 8u);
+}
+
+int launch_route(const DecodeArgs* d_args, const float* hidden, uint32_t epoch, uint32_t H, uint32_t E,
+                 uint32_t grid, void* stream) {
+    const size_t lds = route_lds_bytes(H, E);
+    hipError_t e = hipFuncSetAttribute((const void*)route_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return (int)e;
+    hipLaunchKernelGGL(route_kernel, dim3(grid), dim3(kThreads), lds, (hipStream_t)stream, d_args, hidden, epoch);
+    return (int)hipGetLastError();
+}
+
+int launch_slot_fill(const uint8_t** table, uint32_t E, const int32_t* ids, const uint8_t* const* ptrs, uint32_t n,
+                     void* stream) {
+    if (n > 32) return (int)hipErrorInvalidValue;
+    SlotFill f{};
+    for (uint32_t k = 0; k < n; k++) {
+        f.ids[k] = ids[k];
+        f.ptrs[k] = ptrs[k];
+    }
+    f.n = n;
+    hipLaunchKernelGGL(slot_fill_kernel, dim3((E + 255) / 256), dim3(256), 0, (hipStream_t)stream, table, E, f);
+    return (int)hipGetLastError();
+}
 
 int launch_decode(const DecodeArgs* d_args, const DecodeDyn& dyn, uint32_t H, uint32_t I, uint32_t SI, uint32_t E,
                   uint32_t K, uint32_t grid, void* stream) {

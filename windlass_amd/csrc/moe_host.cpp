@@ -16,6 +16,7 @@
 
 #include "../../include/windlass_moe.h"
 #include "internal.h"
+#include "lru.h"
 
 struct LayerState {
     const uint16_t* router_w = nullptr;
@@ -24,6 +25,29 @@ struct LayerState {
     uint8_t* shared = nullptr;  // context-owned native copy of the shared expert
     int32_t shared_dtype = WL_SHARED_BF16;
     bool set = false;
+};
+
+// HBM expert cache (config 4): LRU slot pool filled from pinned host blocks.
+struct CacheState {
+    wl::SlotLru* lru = nullptr;
+    uint8_t* pool = nullptr;
+    uint32_t capacity = 0;
+    wl_host_block_fn fn = nullptr;
+    void* user = nullptr;
+    hipStream_t copy[2] = {nullptr, nullptr};  // side streams for host-to-device copies
+    uint32_t next_copy = 0;
+    std::vector<hipEvent_t> slot_ev;  // per slot: the last copy into it
+    std::vector<uint8_t> has_ev;      // slot_ev recorded at least once
+    std::vector<uint8_t> spec;        // filled by a speculative copy, not yet requested
+    hipEvent_t gate = nullptr;        // compute-stream point that copies into reused slots wait for
+    bool gate_recorded = false;
+    hipEvent_t ids_ev = nullptr, pred_ev = nullptr;
+    int32_t* h_ids = nullptr;         // pinned: [0,32) ids, [32] error word, [40,72) predicted ids
+    bool speculate = false;
+    bool spec_pending = false;
+    uint32_t spec_layer = 0;
+    uint64_t spec_requests = 0, spec_copies = 0, spec_hits = 0, bytes_h2d = 0;
+    std::vector<std::pair<uint32_t, uint8_t*>> resolved;  // last wl_cache_prefetch: key -> block
 };
 
 struct wl_ctx {
@@ -66,6 +90,7 @@ struct wl_ctx {
     uint32_t pool_slots = 0;
     std::vector<void*> allocs;
     std::string err;
+    CacheState cache;
 };
 
 namespace {
@@ -269,7 +294,17 @@ wl_status wl_create(const wl_moe_config* cfg, wl_ctx** out) {
 
 void wl_destroy(wl_ctx* c) {
     if (!c) return;
-    if (c->uc_block) (void)hipDeviceSynchronize();
+    if (c->uc_block || c->cache.lru) (void)hipDeviceSynchronize();
+    {
+        CacheState& C = c->cache;
+        for (hipEvent_t e : C.slot_ev) (void)hipEventDestroy(e);
+        for (hipEvent_t e : {C.gate, C.ids_ev, C.pred_ev})
+            if (e) (void)hipEventDestroy(e);
+        for (hipStream_t st : C.copy)
+            if (st) (void)hipStreamDestroy(st);
+        if (C.h_ids) (void)hipHostFree(C.h_ids);
+        delete C.lru;
+    }
     for (void* p : c->allocs) (void)hipFree(p);
     uc_release(c->device, c->uc_bytes, c->uc_block);
     delete c;
@@ -352,8 +387,115 @@ wl_status wl_slot_pool_ptr(wl_ctx* c, uint32_t slot, uint8_t** d_block) {
     return WL_OK;
 }
 
+// ---- expert cache ------------------------------------------------------------
+// Resolves n ids of `layer`: hits bump the LRU, misses take a slot (evicting
+// the least-recent key) and start a host-to-device copy on a side stream that
+// waits for the last gate (so no kernel enqueued before it still reads the
+// reused slot) and for the slot's previous copy. Real requests order `s`
+// after the copy of their slot; speculative ones only start copies (their
+// victims are never among the last real batch's experts: capacity >= 2K).
+static wl_status cache_resolve(wl_ctx* c, uint32_t layer, const int32_t* ids, uint32_t n, hipStream_t s,
+                               bool speculative, uint8_t** ptrs) {
+    CacheState& C = c->cache;
+    const uint32_t E = c->cfg.n_routed_experts;
+    const size_t nb = c->native_bytes;
+    hipError_t e;
+    if (!speculative) {
+        if ((e = hipEventRecord(C.gate, s)) != hipSuccess) return hip_fail(c, e, "cache gate");
+        C.gate_recorded = true;
+    }
+    for (uint32_t k = 0; k < n; k++) {
+        if (ids[k] < 0 || (uint32_t)ids[k] >= E)
+            return fail(c, WL_ERR_INVALID, "expert id %d of layer %u out of range", ids[k], layer);
+        bool dup = false;
+        for (uint32_t j = 0; j < k; j++)
+            if (ids[j] == ids[k]) {
+                dup = true;
+                if (ptrs) ptrs[k] = ptrs[j];
+            }
+        if (dup) continue;
+        const uint32_t key = layer * E + (uint32_t)ids[k];
+        const wl::SlotLru::Result r = C.lru->request(key, !speculative);
+        uint8_t* dst = C.pool + (size_t)r.slot * nb;
+        if (speculative) C.spec_requests++;
+        if (r.hit) {
+            if (!speculative && C.spec[r.slot]) {
+                C.spec_hits++;
+                C.spec[r.slot] = 0;
+            }
+        } else {
+            const uint8_t* src = C.fn(C.user, layer, (uint32_t)ids[k]);
+            if (!src) {
+                C.lru->forget(key);
+                return fail(c, WL_ERR_IO, "no host block for layer %u expert %d", layer, ids[k]);
+            }
+            hipStream_t cs = C.copy[C.next_copy++ & 1u];
+            if (C.gate_recorded && (e = hipStreamWaitEvent(cs, C.gate, 0)) != hipSuccess) return hip_fail(c, e, "copy gate");
+            if (C.has_ev[r.slot] && (e = hipStreamWaitEvent(cs, C.slot_ev[r.slot], 0)) != hipSuccess)
+                return hip_fail(c, e, "slot order");
+            if ((e = hipMemcpyAsync(dst, src, nb, hipMemcpyHostToDevice, cs)) != hipSuccess)
+                return hip_fail(c, e, "expert copy");
+            if ((e = hipEventRecord(C.slot_ev[r.slot], cs)) != hipSuccess) return hip_fail(c, e, "copy event");
+            C.has_ev[r.slot] = 1;
+            C.spec[r.slot] = speculative ? 1 : 0;
+            C.bytes_h2d += nb;
+            if (speculative) C.spec_copies++;
+        }
+        if (!speculative && C.has_ev[r.slot] && (e = hipStreamWaitEvent(s, C.slot_ev[r.slot], 0)) != hipSuccess)
+            return hip_fail(c, e, "wait for expert copy");
+        if (ptrs) ptrs[k] = dst;
+    }
+    return WL_OK;
+}
+
+// Routes `layer` on the device, resolves its ids on the host and fills its
+// slot table; with speculation and a next layer, also routes `next` on the
+// same input and copies the predicted ids back (resolved after the layer's
+// launch, by cache_speculate).
+static wl_status cache_prepare(wl_ctx* c, uint32_t layer, const float* d_hidden, uint32_t next, hipStream_t s) {
+    CacheState& C = c->cache;
+    const uint32_t H = c->cfg.hidden, E = c->cfg.n_routed_experts, K = c->cfg.n_experts_per_tok;
+    hipError_t e;
+    if (++c->epoch >= 0x7FFFFFFFu) c->epoch = 1;
+    int le = wl::launch_route(c->d_largs + layer, d_hidden, c->epoch, H, E, c->grid, s);
+    if (le != 0) return hip_fail(c, (hipError_t)le, "route launch");
+    if ((e = hipMemcpyAsync(C.h_ids, c->idx, 4 * (size_t)K, hipMemcpyDeviceToHost, s)) != hipSuccess ||
+        (e = hipMemcpyAsync(C.h_ids + 32, c->sync + c->sm.error, 4, hipMemcpyDeviceToHost, s)) != hipSuccess ||
+        (e = hipEventRecord(C.ids_ev, s)) != hipSuccess || (e = hipEventSynchronize(C.ids_ev)) != hipSuccess)
+        return hip_fail(c, e, "routing read-back");
+    if (C.h_ids[32] != 0)
+        return fail(c, WL_ERR_DEVICE, "device error bits 0x%x while routing layer %u (see wl_check_error)",
+                    (uint32_t)C.h_ids[32], layer);
+    uint8_t* ptrs[WL_MAX_TOPK];
+    wl_status st = cache_resolve(c, layer, C.h_ids, K, s, false, ptrs);
+    if (st != WL_OK) return st;
+    le = wl::launch_slot_fill(c->d_slot + (size_t)layer * E, E, C.h_ids, ptrs, K, s);
+    if (le != 0) return hip_fail(c, (hipError_t)le, "slot table fill");
+    C.spec_pending = false;
+    if (C.speculate && next < c->cfg.n_layers && c->n_bound[next] == 0 && c->layers[next].set) {
+        if (++c->epoch >= 0x7FFFFFFFu) c->epoch = 1;
+        le = wl::launch_route(c->d_largs + next, d_hidden, c->epoch, H, E, c->grid, s);
+        if (le != 0) return hip_fail(c, (hipError_t)le, "speculative route launch");
+        if ((e = hipMemcpyAsync(C.h_ids + 40, c->idx, 4 * (size_t)K, hipMemcpyDeviceToHost, s)) != hipSuccess ||
+            (e = hipEventRecord(C.pred_ev, s)) != hipSuccess)
+            return hip_fail(c, e, "prediction read-back");
+        C.spec_pending = true;
+        C.spec_layer = next;
+    }
+    return WL_OK;
+}
+
+static wl_status cache_speculate(wl_ctx* c, hipStream_t s) {
+    CacheState& C = c->cache;
+    if (!C.spec_pending) return WL_OK;
+    C.spec_pending = false;
+    hipError_t e = hipEventSynchronize(C.pred_ev);
+    if (e != hipSuccess) return hip_fail(c, e, "prediction wait");
+    return cache_resolve(c, C.spec_layer, C.h_ids + 40, c->cfg.n_experts_per_tok, s, true, nullptr);
+}
+
 static wl_status run_layer(wl_ctx* c, uint32_t layer, const float* d_hidden, const float* d_resid,
-                           float* d_out, void* stream) {
+                           float* d_out, void* stream, uint32_t next = 0xFFFFFFFFu) {
     if (!c) return WL_ERR_INVALID;
     if (layer >= c->cfg.n_layers) return fail(c, WL_ERR_INVALID, "layer %u >= n_layers %u", layer, c->cfg.n_layers);
     const LayerState& L = c->layers[layer];
@@ -363,8 +505,13 @@ static wl_status run_layer(wl_ctx* c, uint32_t layer, const float* d_hidden, con
         return fail(c, WL_ERR_INVALID, "d_out must not alias the inputs");
     const uint32_t H = c->cfg.hidden, I = c->cfg.moe_inter, E = c->cfg.n_routed_experts,
                    K = c->cfg.n_experts_per_tok, SI = c->SI;
-    if (c->n_bound[layer] != E)
+    const bool cached = c->n_bound[layer] == 0 && c->cache.lru != nullptr;
+    if (!cached && c->n_bound[layer] != E)
         return fail(c, WL_ERR_NOT_RESIDENT, "layer %u has %u of %u experts bound", layer, c->n_bound[layer], E);
+    if (cached) {
+        wl_status s = cache_prepare(c, layer, d_hidden, next, (hipStream_t)stream);
+        if (s != WL_OK) return s;
+    }
 
     wl::DecodeDyn dyn{};
     if (++c->epoch >= 0x7FFFFFFFu) c->epoch = 1;
@@ -387,11 +534,14 @@ static wl_status run_layer(wl_ctx* c, uint32_t layer, const float* d_hidden, con
             c->bar_seq = 1u;
         }
         dyn.bar_seq = c->bar_seq;
-        return launch(0, 1);
+        wl_status s = launch(0, 1);
+        if (s != WL_OK || !cached) return s;
+        return cache_speculate(c, (hipStream_t)stream);
     }
     wl_status s;
     if ((s = launch(0, 0)) != WL_OK) return s;
-    return launch(1, 1);
+    if ((s = launch(1, 1)) != WL_OK || !cached) return s;
+    return cache_speculate(c, (hipStream_t)stream);
 }
 
 wl_status wl_run_moe(wl_ctx* c, uint32_t layer, const float* d_hidden, float* d_out, void* stream) {
@@ -414,7 +564,8 @@ wl_status wl_run_chain(wl_ctx* c, uint32_t first_layer, uint32_t n_layers, float
     float* cur = d_h;
     float* nxt = d_tmp;
     for (uint32_t l = 0; l < n_layers; l++) {
-        wl_status s = run_layer(c, first_layer + l, cur, cur, nxt, stream);
+        const uint32_t next = l + 1 < n_layers ? first_layer + l + 1 : 0xFFFFFFFFu;
+        wl_status s = run_layer(c, first_layer + l, cur, cur, nxt, stream, next);
         if (s != WL_OK) return s;
         float* t = cur;
         cur = nxt;
@@ -436,6 +587,125 @@ wl_status wl_taps(wl_ctx* c, wl_taps_out* out) {
     out->topk_w = c->topw;
     out->mid = c->rmid;
     out->shared = c->shared_out;
+    return WL_OK;
+}
+
+wl_status wl_cache_create(wl_ctx* c, uint32_t capacity, wl_host_block_fn host_block, void* user) {
+    if (!c) return WL_ERR_INVALID;
+    CacheState& C = c->cache;
+    if (C.lru) return fail(c, WL_ERR_STATE, "the context already has a cache");
+    if (!host_block) return fail(c, WL_ERR_INVALID, "host_block is null");
+    if (capacity < 2u * c->cfg.n_experts_per_tok)
+        return fail(c, WL_ERR_INVALID, "capacity %u < 2 x n_experts_per_tok", capacity);
+    void* p = nullptr;
+    hipError_t e = hipMalloc(&p, (size_t)capacity * c->native_bytes);
+    if (e != hipSuccess)
+        return fail(c, WL_ERR_OOM, "cache pool of %u x %zu B: %s", capacity, c->native_bytes, hipGetErrorString(e));
+    c->allocs.push_back(p);
+    C.pool = (uint8_t*)p;
+    C.capacity = capacity;
+    C.fn = host_block;
+    C.user = user;
+    if ((e = hipHostMalloc((void**)&C.h_ids, 4 * 80, hipHostMallocDefault)) != hipSuccess)
+        return fail(c, WL_ERR_OOM, "pinned id buffer: %s", hipGetErrorString(e));
+    for (hipStream_t& st : C.copy)
+        if ((e = hipStreamCreateWithFlags(&st, hipStreamNonBlocking)) != hipSuccess) return hip_fail(c, e, "copy stream");
+    for (hipEvent_t* ev : {&C.gate, &C.ids_ev, &C.pred_ev})
+        if ((e = hipEventCreateWithFlags(ev, hipEventDisableTiming)) != hipSuccess) return hip_fail(c, e, "cache event");
+    C.slot_ev.assign(capacity, nullptr);
+    for (hipEvent_t& ev : C.slot_ev)
+        if ((e = hipEventCreateWithFlags(&ev, hipEventDisableTiming)) != hipSuccess) return hip_fail(c, e, "slot event");
+    C.has_ev.assign(capacity, 0);
+    C.spec.assign(capacity, 0);
+    C.lru = new wl::SlotLru(capacity);
+    return WL_OK;
+}
+
+wl_status wl_cache_set_speculation(wl_ctx* c, int32_t enable) {
+    if (!c) return WL_ERR_INVALID;
+    if (!c->cache.lru) return fail(c, WL_ERR_STATE, "no cache (wl_cache_create)");
+    c->cache.speculate = enable != 0;
+    return WL_OK;
+}
+
+wl_status wl_cache_get_stats(wl_ctx* c, wl_cache_stats* out) {
+    if (!c || !out) return WL_ERR_INVALID;
+    const CacheState& C = c->cache;
+    if (!C.lru) return fail(c, WL_ERR_STATE, "no cache (wl_cache_create)");
+    out->hits = C.lru->hits();
+    out->misses = C.lru->misses();
+    out->evictions = C.lru->evictions();
+    out->spec_requests = C.spec_requests;
+    out->spec_copies = C.spec_copies;
+    out->spec_hits = C.spec_hits;
+    out->bytes_h2d = C.bytes_h2d;
+    out->used = C.lru->used();
+    out->capacity = C.capacity;
+    return WL_OK;
+}
+
+wl_status wl_cache_reset_stats(wl_ctx* c) {
+    if (!c) return WL_ERR_INVALID;
+    CacheState& C = c->cache;
+    if (!C.lru) return fail(c, WL_ERR_STATE, "no cache (wl_cache_create)");
+    C.lru->reset_stats();
+    C.spec_requests = C.spec_copies = C.spec_hits = C.bytes_h2d = 0;
+    return WL_OK;
+}
+
+wl_status wl_cache_prefetch(wl_ctx* c, uint32_t layer, const int32_t* experts, uint32_t n, void* stream) {
+    if (!c) return WL_ERR_INVALID;
+    CacheState& C = c->cache;
+    if (!C.lru) return fail(c, WL_ERR_STATE, "no cache (wl_cache_create)");
+    if (layer >= c->cfg.n_layers || (n && !experts) || n > WL_MAX_TOPK || n > C.capacity / 2u)
+        return fail(c, WL_ERR_INVALID, "bad prefetch request (layer %u, n %u)", layer, n);
+    uint8_t* ptrs[WL_MAX_TOPK];
+    wl_status s = cache_resolve(c, layer, experts, n, (hipStream_t)stream, false, ptrs);
+    if (s != WL_OK) return s;
+    C.resolved.clear();
+    for (uint32_t k = 0; k < n; k++) C.resolved.push_back({layer * c->cfg.n_routed_experts + (uint32_t)experts[k], ptrs[k]});
+    return WL_OK;
+}
+
+wl_status wl_cache_get(wl_ctx* c, uint32_t layer, uint32_t expert, void* stream, uint8_t** d_block) {
+    if (!c || !d_block) return WL_ERR_INVALID;
+    CacheState& C = c->cache;
+    if (!C.lru) return fail(c, WL_ERR_STATE, "no cache (wl_cache_create)");
+    if (layer >= c->cfg.n_layers || expert >= c->cfg.n_routed_experts)
+        return fail(c, WL_ERR_INVALID, "(%u,%u) out of range", layer, expert);
+    const uint32_t key = layer * c->cfg.n_routed_experts + expert;
+    for (const auto& r : C.resolved)
+        if (r.first == key) {
+            *d_block = r.second;  // the prefetch already ordered the stream after its copy
+            return WL_OK;
+        }
+    const int32_t id = (int32_t)expert;
+    uint8_t* p = nullptr;
+    wl_status s = cache_resolve(c, layer, &id, 1, (hipStream_t)stream, false, &p);
+    if (s == WL_OK) *d_block = p;
+    return s;
+}
+
+wl_status wl_lru_replay(uint32_t capacity, const uint32_t* keys, uint32_t n_keys, uint32_t batch, uint8_t* hit_out,
+                        uint64_t* hits, uint64_t* misses, uint64_t* evictions) {
+    if (capacity == 0 || (n_keys && !keys) || batch == 0) return WL_ERR_INVALID;
+    wl::SlotLru lru(capacity);
+    for (uint32_t b0 = 0; b0 < n_keys; b0 += batch) {
+        const uint32_t b1 = b0 + batch < n_keys ? b0 + batch : n_keys;
+        for (uint32_t i = b0; i < b1; i++) {
+            bool dup = false;
+            for (uint32_t j = b0; j < i; j++) dup = dup || keys[j] == keys[i];
+            if (dup) {
+                if (hit_out) hit_out[i] = 2;
+                continue;
+            }
+            const wl::SlotLru::Result r = lru.request(keys[i]);
+            if (hit_out) hit_out[i] = r.hit ? 1 : 0;
+        }
+    }
+    if (hits) *hits = lru.hits();
+    if (misses) *misses = lru.misses();
+    if (evictions) *evictions = lru.evictions();
     return WL_OK;
 }
 

@@ -112,6 +112,38 @@ class DeviceBuffer:
             pass
 
 
+class HostBuffer:
+    """An owned pinned host allocation (hipHostMalloc) of `nbytes`."""
+
+    def __init__(self, nbytes):
+        self.nbytes = int(nbytes)
+        p = _vp()
+        check(_hip.hipHostMalloc(ctypes.byref(p), max(self.nbytes, 16), 0), f"hipHostMalloc({self.nbytes})")
+        self.ptr = p.value
+
+    def view(self, dtype=np.uint8, count=None, offset=0):
+        dtype = np.dtype(dtype)
+        if count is None:
+            count = (self.nbytes - offset) // dtype.itemsize
+        buf = (ctypes.c_uint8 * (count * dtype.itemsize)).from_address(self.ptr + offset)
+        return np.frombuffer(buf, dtype=dtype, count=count)
+
+    def free(self):
+        if self.ptr:
+            _hip.hipHostFree(_vp(self.ptr))
+            self.ptr = 0
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+def copy_d2h_ptr(dst_host, src_dev, nbytes):
+    check(_hip.hipMemcpy(_vp(dst_host), _vp(src_dev), nbytes, D2H), "D2H")
+
+
 def download_ptr(ptr, dtype, count):
     out = np.empty(count, dtype=np.dtype(dtype))
     check(_hip.hipMemcpy(out.ctypes.data_as(_vp), _vp(ptr), out.nbytes, D2H), "D2H")

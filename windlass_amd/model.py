@@ -1,19 +1,34 @@
-"""A resident synthetic MoE model built through the C ABI: every routed
-expert of every layer in one context-owned HBM slot pool (written on the device
-in the native layout by wl_synth_expert_native), dense tensors from
-windlass_amd.synthdata uploaded once.
-Used by the benchmark and the GPU tests."""
+"""Synthetic MoE models built through the C ABI, used by the benchmark and the
+GPU tests.
+
+DeviceModel: every routed expert of every layer resident in one context-owned
+HBM slot pool (written on the device in the native layout by
+wl_synth_expert_native).
+
+CachedModel: the same layers with their experts behind the HBM expert cache:
+a pinned host pool of `n_host` native blocks is the backing store, and
+(layer, expert) reads host block (layer * E + expert) mod n_host, whose bytes
+are the synthetic expert (hb // E, hb % E) — so `expert_source_key` maps every
+(layer, expert) to the synthetic key the oracle regenerates.
+
+Dense tensors come from windlass_amd.synthdata and are uploaded once. With
+shared_alias, every layer uses layer 0's shared expert (it is not behind the
+cache, so aliasing it changes nothing the cache does and saves generating one
+75 MB expert per layer)."""
+import ctypes
+
 import numpy as np
 
 from . import hip, moe, synthdata
 
 
-class DeviceModel:
-    def __init__(self, cfg, seed, n_layers=1, ln_weights=None, bias_offset=None):
+class _Layers:
+    def __init__(self, cfg, seed, n_layers, ln_weights=None, bias_offset=None, shared_alias=False):
         self.c = dict(cfg)
         self.seed = seed
         self.L = n_layers
         H, I, E = cfg["hidden"], cfg["moe_inter"], cfg["n_routed_experts"]
+        self.E = E
         self.SI = I * cfg.get("n_shared", 1)
         self.cfg = moe.make_config(hidden=H, moe_inter=I, n_routed_experts=E,
                                    n_experts_per_tok=cfg["n_experts_per_tok"],
@@ -22,28 +37,90 @@ class DeviceModel:
                                    norm_topk_prob=cfg.get("norm_topk_prob", True),
                                    rms_eps=cfg.get("rms_eps", 1e-5))
         self.ctx = moe.Context(self.cfg)
-        self.ctx.slot_pool_create(n_layers * E)
+        self._ln_weights = ln_weights
+        self._bias_offset = bias_offset
+        self._shared_alias = shared_alias
         self.dense, self.bufs = [], []
-        for l in range(n_layers):
-            for e in range(E):
-                p = self.ctx.slot_pool_ptr(l * E + e)
-                moe.synth_expert_native(self.cfg, seed, l, e, p)  # = wl_expert_to_native(synth block)
-                self.ctx.slot_bind(l, e, p)
-            d = synthdata.dense_layer(H, E, self.SI, seed, l)
-            if bias_offset is not None:
-                d["bias"] = (d["bias"] + bias_offset).astype(np.float32)
+
+    def _bind_dense(self):
+        H, E = self.c["hidden"], self.E
+        shared0 = None
+        for l in range(self.L):
+            if self._shared_alias and l > 0:
+                d = dict(synthdata.router_only(H, E, self.seed, l))
+                d.update({k: self.dense[0][k] for k in ("sh_gate", "sh_up", "sh_down", "shared_block")})
+            else:
+                d = synthdata.dense_layer(H, E, self.SI, self.seed, l)
+            if self._bias_offset is not None:
+                d["bias"] = (d["bias"] + self._bias_offset).astype(np.float32)
             self.dense.append(d)
             rw = hip.DeviceBuffer.from_array(d["router_w"])
             bb = hip.DeviceBuffer.from_array(d["bias"])
-            sb = hip.DeviceBuffer.from_array(d["shared_block"])
-            lw = hip.DeviceBuffer.from_array(ln_weights[l]) if ln_weights is not None else None
+            if shared0 is None or not self._shared_alias:
+                shared0 = hip.DeviceBuffer.from_array(d["shared_block"])
+            sb = shared0
+            lw = hip.DeviceBuffer.from_array(self._ln_weights[l]) if self._ln_weights is not None else None
             self.bufs.append((rw, bb, sb, lw))
             self.ctx.set_layer(l, rw.ptr, bb.ptr, lw.ptr if lw else None, sb.ptr)
-        hip.synchronize()
+
+    def expert_source_key(self, layer, expert):
+        return layer, expert
 
     def close(self):
         self.ctx.close()
         self.bufs = []
+
+
+class DeviceModel(_Layers):
+    """expert_key(layer, expert) -> (layer', expert') chooses which synthetic
+    expert fills each slot (default: its own)."""
+
+    def __init__(self, cfg, seed, n_layers=1, ln_weights=None, bias_offset=None, expert_key=None,
+                 shared_alias=False):
+        super().__init__(cfg, seed, n_layers, ln_weights, bias_offset, shared_alias)
+        self._key = expert_key or (lambda l, e: (l, e))
+        E = self.E
+        self.ctx.slot_pool_create(n_layers * E)
+        for l in range(n_layers):
+            for e in range(E):
+                p = self.ctx.slot_pool_ptr(l * E + e)
+                kl, ke = self._key(l, e)
+                moe.synth_expert_native(self.cfg, seed, kl, ke, p)  # = wl_expert_to_native(synth block)
+                self.ctx.slot_bind(l, e, p)
+        self._bind_dense()
+        hip.synchronize()
+
+    def expert_source_key(self, layer, expert):
+        return self._key(layer, expert)
+
+
+class CachedModel(_Layers):
+    def __init__(self, cfg, seed, n_layers, capacity, n_host, ln_weights=None, bias_offset=None,
+                 shared_alias=False):
+        super().__init__(cfg, seed, n_layers, ln_weights, bias_offset, shared_alias)
+        self.n_host = n_host
+        self.nb = moe.native_block_bytes(self.cfg)
+        self.host = hip.HostBuffer(n_host * self.nb)
+        tmp = hip.DeviceBuffer(self.nb)
+        for hb in range(n_host):
+            kl, ke = divmod(hb, self.E)
+            moe.synth_expert_native(self.cfg, seed, kl, ke, tmp.ptr)
+            hip.copy_d2h_ptr(self.host.ptr + hb * self.nb, tmp.ptr, self.nb)
+        tmp.free()
+        base, nb, E, nh = self.host.ptr, self.nb, self.E, n_host
+        self.ctx.cache_create(capacity, lambda l, e: base + ((l * E + e) % nh) * nb)
+        self._bind_dense()
+        hip.synchronize()
+
+    def host_block_index(self, layer, expert):
+        return (layer * self.E + expert) % self.n_host
+
+    def expert_source_key(self, layer, expert):
+        return divmod(self.host_block_index(layer, expert), self.E)
+
+    def close(self):
+        super().close()
+        self.host.free()
 
 
 def make_io(H):

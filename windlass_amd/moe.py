@@ -44,6 +44,16 @@ class ExpertLayout(ctypes.Structure):
                  "dw_off", "dw_len", "ds_off", "ds_len", "total"]]
 
 
+class CacheStats(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_uint64) for n in ["hits", "misses", "evictions", "spec_requests", "spec_copies",
+                                               "spec_hits", "bytes_h2d"]] + \
+               [("used", ctypes.c_uint32), ("capacity", ctypes.c_uint32)]
+
+
+# const uint8_t* host_block(void* user, uint32_t layer, uint32_t expert)
+HOST_BLOCK_FN = ctypes.CFUNCTYPE(ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint32)
+
+
 class Taps(ctypes.Structure):
     _fields_ = [(n, ctypes.c_void_p) for n in ["norm", "logits", "topk_idx", "topk_w", "mid", "shared"]]
 
@@ -81,6 +91,15 @@ def load():
         "wl_expert_to_native": [ctypes.POINTER(MoeConfig), vp, vp, vp],
         "wl_dequant_matvec_mxfp4": [vp, vp, vp, vp, u32, u32, vp],
         "wl_expert_ffn": [vp, vp, vp, vp, vp, vp],
+        "wl_cache_create": [vp, u32, HOST_BLOCK_FN, vp],
+        "wl_cache_set_speculation": [vp, i32],
+        "wl_cache_get_stats": [vp, ctypes.POINTER(CacheStats)],
+        "wl_cache_reset_stats": [vp],
+        "wl_cache_prefetch": [vp, u32, ctypes.POINTER(i32), u32, vp],
+        "wl_cache_get": [vp, u32, u32, vp, ctypes.POINTER(vp)],
+        "wl_lru_replay": [u32, ctypes.POINTER(u32), u32, u32, ctypes.POINTER(ctypes.c_uint8),
+                          ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_uint64),
+                          ctypes.POINTER(ctypes.c_uint64)],
     }
     for name, args in sig.items():
         fn = getattr(lib, name)
@@ -137,6 +156,21 @@ def expert_to_native(cfg, d_ref, d_native, stream=0):
 
 def native_block_bytes(cfg):
     return int(load().wl_native_block_bytes(ctypes.byref(cfg)))
+
+
+def lru_replay(capacity, keys, batch):
+    """The cache's LRU bookkeeping over a key sequence (no device use):
+    returns (per-key 1 hit / 0 miss / 2 skipped duplicate, hits, misses, evictions)."""
+    import numpy as np
+    k = np.ascontiguousarray(keys, dtype=np.uint32)
+    out = np.zeros(len(k), dtype=np.uint8)
+    h, m, e = ctypes.c_uint64(), ctypes.c_uint64(), ctypes.c_uint64()
+    rc = load().wl_lru_replay(capacity, k.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)), len(k), batch,
+                              out.ctypes.data_as(ctypes.POINTER(ctypes.c_uint8)), ctypes.byref(h), ctypes.byref(m),
+                              ctypes.byref(e))
+    if rc != WL_OK:
+        raise WindlassError(rc, "wl_lru_replay")
+    return out, h.value, m.value, e.value
 
 
 def dequant_matvec_mxfp4(d_W, d_S, d_x, d_y, N, K, stream=0):
@@ -216,3 +250,29 @@ class Context:
 
     def set_taps(self, enable):
         self._ck(self.lib.wl_set_taps(self.h, 1 if enable else 0), "wl_set_taps")
+
+    # ---- HBM expert cache -------------------------------------------------
+    def cache_create(self, capacity, host_block):
+        """host_block(layer, expert) -> address of a pinned native block (int)."""
+        self._host_block_cb = HOST_BLOCK_FN(lambda user, layer, expert: host_block(layer, expert))
+        self._ck(self.lib.wl_cache_create(self.h, capacity, self._host_block_cb, None), "wl_cache_create")
+
+    def cache_set_speculation(self, enable):
+        self._ck(self.lib.wl_cache_set_speculation(self.h, 1 if enable else 0), "wl_cache_set_speculation")
+
+    def cache_stats(self):
+        st = CacheStats()
+        self._ck(self.lib.wl_cache_get_stats(self.h, ctypes.byref(st)), "wl_cache_get_stats")
+        return {n: getattr(st, n) for n, _ in CacheStats._fields_}
+
+    def cache_reset_stats(self):
+        self._ck(self.lib.wl_cache_reset_stats(self.h), "wl_cache_reset_stats")
+
+    def cache_prefetch(self, layer, experts, stream=0):
+        arr = (ctypes.c_int32 * len(experts))(*[int(e) for e in experts])
+        self._ck(self.lib.wl_cache_prefetch(self.h, layer, arr, len(experts), stream), "wl_cache_prefetch")
+
+    def cache_get(self, layer, expert, stream=0):
+        p = ctypes.c_void_p()
+        self._ck(self.lib.wl_cache_get(self.h, layer, expert, stream, ctypes.byref(p)), "wl_cache_get")
+        return p.value

@@ -38,10 +38,17 @@ def normal_bf16(seed, layer, tag, shape, std):
     return f32_to_bf16(x).reshape(shape)
 
 
-def dense_layer(H, E, SI, seed, layer):
+def router_only(H, E, seed, layer):
+    """The router weight and bias of dense_layer (same draws)."""
     router_w = normal_bf16(seed, layer, TAG_ROUTER, (E, H), 0.02)
     bias = (_rng(seed, layer, TAG_BIAS).standard_normal(size=E, dtype=np.float32)
             * np.float32(0.01)).astype(np.float32)
+    return {"router_w": router_w, "bias": bias}
+
+
+def dense_layer(H, E, SI, seed, layer):
+    r = router_only(H, E, seed, layer)
+    router_w, bias = r["router_w"], r["bias"]
     sg = normal_bf16(seed, layer, TAG_SH_GATE, (SI, H), 0.02)
     su = normal_bf16(seed, layer, TAG_SH_UP, (SI, H), 0.02)
     sd = normal_bf16(seed, layer, TAG_SH_DOWN, (H, SI), 0.02)
