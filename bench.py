@@ -18,6 +18,15 @@ MoE layers (6144 expert blocks, 123 GB of HBM), h <- h + moe(h) layer by
 layer; a step is one decode token through all 24 layers, starting from its own
 seeded N(0,1) hidden state. `value` is then microseconds per layer within the
 chain (step time / 24) and tokens_per_s is reported beside it.
+
+--workload cache measures configs[4]: 75 MoE layers whose 19,200 experts sit
+behind the HBM expert cache (3,094 slots, 62 GB) and are copied from pinned
+host memory on a miss; router bias shaped by Zipf(1.1) popularity; a step is
+one token through the 75 layers; --spec adds cross-layer speculative prefetch. The host backing store is --host-blocks pinned native blocks
+(default 512, 10.3 GB): (layer, expert) reads block (layer*256 + expert) mod
+512, because 385 GB of distinct blocks exceed the host memory of the box. The
+key, the LRU and every copy are per (layer, expert) as in the reference; only
+the bytes repeat. The line adds hit_rate and the host-link rate.
 """
 import argparse
 import json
@@ -90,9 +99,17 @@ def main():
     ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--layers", type=int, default=8, help="distinct resident layer copies to rotate over")
     ap.add_argument("--sched", choices=["fused", "phased"], default="fused")
-    ap.add_argument("--workload", choices=["layer", "chain"], default="layer",
-                    help="layer: config 1 (default); chain: config 2, 24 layers per step")
+    ap.add_argument("--workload", choices=["layer", "chain", "cache"], default="layer",
+                    help="layer: config 1 (default); chain: config 2, 24 layers per step; "
+                         "cache: config 4, 75 cache-backed layers per step")
     ap.add_argument("--chain-layers", type=int, default=24)
+    ap.add_argument("--cache-layers", type=int, default=75)
+    ap.add_argument("--cache-slots", type=int, default=3094)
+    ap.add_argument("--host-blocks", type=int, default=512)
+    ap.add_argument("--spec", action="store_true",
+                    help="cache workload: cross-layer speculative prefetch (layer l+1's router on layer l's input)")
+    ap.add_argument("--zipf-amp", type=float, default=0.25,
+                    help="cache workload: bias offset of the most popular expert (rank r gets amp * r^-1.1)")
     ap.add_argument("--seed", type=int, default=1)
     ap.add_argument("--cpu-sample", type=int, default=3, help="layers timed for the CPU baseline (0: skip)")
     ap.add_argument("--traffic-json", default=os.path.join(ROOT, "profiles", "decode_layer_traffic.json"))
@@ -108,7 +125,7 @@ def main():
         sys.exit(2)
 
     from windlass_amd import hip, moe, synthdata
-    from windlass_amd.model import DeviceModel
+    from windlass_amd.model import CachedModel, DeviceModel
 
     if hip.device_count() < 1:
         print("bench.py: no GPU visible", file=sys.stderr)
@@ -116,15 +133,23 @@ def main():
 
     c = dict(GLM)
     H = c["hidden"]
-    chain = args.workload == "chain"
+    cache = args.workload == "cache"
+    chain = args.workload == "chain" or cache
     if chain:
-        args.layers = args.chain_layers
+        args.layers = args.cache_layers if cache else args.chain_layers
         if "--steps" not in sys.argv:
-            args.steps = 64
+            args.steps = 16 if cache else 64
         if "--warmup" not in sys.argv:
-            args.warmup = 4
+            args.warmup = 8 if cache else 4
     t_build = time.time()
-    dm = DeviceModel(c, seed=args.seed, n_layers=args.layers)
+    if cache:
+        dm = CachedModel(c, seed=args.seed, n_layers=args.layers, capacity=args.cache_slots,
+                         n_host=args.host_blocks, shared_alias=True,
+                         bias_offset=synthdata.zipf_bias_offset(c["n_routed_experts"], args.seed,
+                                                                amplitude=args.zipf_amp))
+        dm.ctx.cache_set_speculation(args.spec)
+    else:
+        dm = DeviceModel(c, seed=args.seed, n_layers=args.layers)
     dm.ctx.set_schedule(moe.SCHED_FUSED if args.sched == "fused" else moe.SCHED_PHASED)
     dm.ctx.set_taps(False)  # the shared-expert output tap is a test hook
     n_h = 64
@@ -148,6 +173,8 @@ def main():
         step(i)
     dm.ctx.check_error(stream.handle)
     hip.synchronize()
+    if cache:
+        dm.ctx.cache_reset_stats()
     e0, e1 = hip.Event(), hip.Event()
     e0.record(stream)
     for i in range(args.steps):
@@ -156,6 +183,7 @@ def main():
     e1.synchronize()
     ms = e0.elapsed_ms(e1)
     dm.ctx.check_error(stream.handle)
+    cstats = dm.ctx.cache_stats() if cache else None
     layers_per_step = args.layers if chain else 1
     us_per_layer = ms * 1e3 / args.steps / layers_per_step
 
@@ -201,7 +229,9 @@ def main():
         "vs_baseline": None,
         "dtype": "mxfp4/bf16 weights, f32 activations and accumulation",
         "data": "synthetic",
-        "config": {"workload": (f"config2: chain of {args.layers} resident GLM MoE decode layers, bs=1, "
+        "config": {"workload": (f"config4: {args.layers} GLM MoE layers behind a {args.cache_slots}-slot HBM expert "
+                                f"cache, misses from pinned host memory, bs=1" if cache else
+                                f"config2: chain of {args.layers} resident GLM MoE decode layers, bs=1, "
                                 f"h <- h + moe(h)" if chain else "config1: one GLM MoE decode layer, bs=1"),
                    "hidden": H, "moe_inter": c["moe_inter"], "n_routed_experts": c["n_routed_experts"],
                    "n_experts_per_tok": c["n_experts_per_tok"], "shared": "bf16 inter 2048",
@@ -215,6 +245,14 @@ def main():
                      "frac": round(achieved / PEAK_HBM_GBPS, 4), "traffic": traffic,
                      "algorithmic_bytes": nbytes, "kernel": "moe_decode_kernel"},
         "cpu_baseline": cpu,
+        **({"cache": {"hit_rate": round(cstats["hits"] / max(1, cstats["hits"] + cstats["misses"]), 4),
+                      "hits": cstats["hits"], "misses": cstats["misses"], "evictions": cstats["evictions"],
+                      "speculation": args.spec, "spec_requests": cstats["spec_requests"],
+                      "spec_copies": cstats["spec_copies"], "spec_hits": cstats["spec_hits"],
+                      "h2d_GB": round(cstats["bytes_h2d"] / 1e9, 3),
+                      "h2d_GBps": round(cstats["bytes_h2d"] / (ms * 1e-3) / 1e9, 2),
+                      "host_blocks": args.host_blocks, "slots": args.cache_slots,
+                      "zipf": {"s": 1.1, "amplitude": args.zipf_amp}}} if cache else {}),
         "build_s": round(build_s, 1),
     }
     print(json.dumps(line), flush=True)
