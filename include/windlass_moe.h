@@ -139,6 +139,19 @@ wl_status wl_run_moe_residual(wl_ctx* ctx, uint32_t layer, const float* d_hidden
 wl_status wl_run_chain(wl_ctx* ctx, uint32_t first_layer, uint32_t n_layers, float* d_h,
                        float* d_tmp, void* stream);
 
+/* The layer for n_tokens positions at once (prefill; reference
+ * run_moe_batched, src/glm_layer_runner.cuh:818-928). d_hidden [n_tokens][H]
+ * f32 pre-norm residual stream; d_out [n_tokens][H] = d_resid + moe(d_hidden)
+ * row by row (d_resid may be NULL: moe only; d_out must alias neither). Each
+ * token is routed exactly as wl_run_moe routes it (same ids); tokens are then
+ * grouped by expert (stable, (token, slot) order) and every selected expert's
+ * weights are streamed once per 32 of its tokens; the per-token combine sums
+ * the slots in slot order, then the shared expert (the reference's pass 3).
+ * Requires every expert of the layer bound (resident); n_tokens <= 65535.
+ * Scratch grows to the largest n_tokens seen (context-owned; growing synchronises the device). */
+wl_status wl_run_moe_batched(wl_ctx* ctx, uint32_t layer, uint32_t n_tokens, const float* d_hidden,
+                             const float* d_resid, float* d_out, void* stream);
+
 /* Device pointers to the last layer's intermediates (the substeps
  * test_glm_chain reads through SubstepHook, src/test_glm_chain.cu:434-441). */
 typedef struct wl_taps_out {

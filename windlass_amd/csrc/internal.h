@@ -201,6 +201,30 @@ struct NativeShared {
     }
 };
 
+// Batched (multi-token) layer, reference run_moe_batched
+// (src/glm_layer_runner.cuh:818-928): per-token routing, tokens grouped by
+// expert (stable: (token, slot) order), grouped GEMMs, per-token combine in
+// slot order. Scratch is context-owned and sized for T tokens.
+struct BatchArgs {
+    uint32_t T;
+    const float* hidden;   // [T][H] pre-norm residual stream
+    const float* resid;    // [T][H] or null
+    float* out;            // [T][H]
+    float* norm;           // [T][H]
+    float* logits;         // [T][E]
+    int32_t* idx;          // [T][K]
+    float* wts;            // [T][K]
+    uint32_t* counts;      // [E]
+    uint32_t* offsets;     // [E+1]
+    uint32_t* lists;       // [E][T] entries (token*K + slot) of expert e, ascending
+    uint32_t* ent;         // [T*K] compact index -> token*K + slot (expert-major)
+    uint32_t* pos;         // [T*K] token*K + slot -> compact index
+    float* mid;            // [T*K][I] routed SwiGLU outputs, compact rows
+    float* expout;         // [T*K][H] routed expert outputs, compact rows
+    float* smid;           // [T][SI]
+    float* shout;          // [T][H]
+};
+
 // Launchers (moe_decode.hip).
 int launch_decode(const DecodeArgs* d_args, const DecodeDyn& dyn, uint32_t H, uint32_t I, uint32_t SI,
                   uint32_t E, uint32_t K, uint32_t grid, void* stream);
@@ -218,6 +242,9 @@ int launch_expert_ffn(const uint8_t* blk, uint64_t gw_off, uint64_t gs_off, uint
                       uint64_t us_off, uint64_t dw_off, uint64_t ds_off, const float* x, uint32_t H,
                       uint32_t I, float* mid, uint16_t* mid_p, float* y, uint16_t* y_bf16,
                       void* stream);
+// Batched layer (moe_batched.hip): every stage on `stream`.
+int launch_batched(const DecodeArgs* d_args, const BatchArgs& b, uint32_t H, uint32_t I, uint32_t SI, uint32_t E,
+                   uint32_t K, uint32_t n_cu, void* stream);
 // Reference-layout block -> native block (src null: synthesise the native
 // block directly from the counter-based generator with `key`).
 int launch_expert_to_native(const uint8_t* src, uint8_t* dst, uint32_t H, uint32_t I, uint32_t key, void* stream);

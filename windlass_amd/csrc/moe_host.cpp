@@ -12,6 +12,7 @@
 #include <cstring>
 #include <mutex>
 #include <string>
+#include <type_traits>
 #include <vector>
 
 #include "../../include/windlass_moe.h"
@@ -48,6 +49,13 @@ struct CacheState {
     uint32_t spec_layer = 0;
     uint64_t spec_requests = 0, spec_copies = 0, spec_hits = 0, bytes_h2d = 0;
     std::vector<std::pair<uint32_t, uint8_t*>> resolved;  // last wl_cache_prefetch: key -> block
+};
+
+// Scratch of the batched layer, sized for `cap` tokens.
+struct BatchScratch {
+    uint32_t cap = 0;
+    std::vector<void*> bufs;
+    wl::BatchArgs b{};
 };
 
 struct wl_ctx {
@@ -91,6 +99,7 @@ struct wl_ctx {
     std::vector<void*> allocs;
     std::string err;
     CacheState cache;
+    BatchScratch batch;
 };
 
 namespace {
@@ -305,6 +314,7 @@ void wl_destroy(wl_ctx* c) {
         if (C.h_ids) (void)hipHostFree(C.h_ids);
         delete C.lru;
     }
+    for (void* p : c->batch.bufs) (void)hipFree(p);
     for (void* p : c->allocs) (void)hipFree(p);
     uc_release(c->device, c->uc_bytes, c->uc_block);
     delete c;
@@ -587,6 +597,61 @@ wl_status wl_taps(wl_ctx* c, wl_taps_out* out) {
     out->topk_w = c->topw;
     out->mid = c->rmid;
     out->shared = c->shared_out;
+    return WL_OK;
+}
+
+static wl_status batch_reserve(wl_ctx* c, uint32_t T) {
+    BatchScratch& B = c->batch;
+    if (T <= B.cap) return WL_OK;
+    hipError_t e = hipDeviceSynchronize();  // launches in flight may still use the old buffers
+    if (e != hipSuccess) return hip_fail(c, e, "batched scratch resize");
+    for (void* p : B.bufs) (void)hipFree(p);
+    B.bufs.clear();
+    B.cap = 0;
+    const size_t H = c->cfg.hidden, I = c->cfg.moe_inter, E = c->cfg.n_routed_experts, K = c->cfg.n_experts_per_tok,
+                 SI = c->SI, t = T;
+    wl::BatchArgs& b = B.b;
+    auto get = [&](auto** p, size_t bytes) -> bool {
+        void* q = nullptr;
+        if (hipMalloc(&q, bytes ? bytes : 16) != hipSuccess) return false;
+        B.bufs.push_back(q);
+        *p = (std::remove_reference_t<decltype(*p)>)q;
+        return true;
+    };
+    if (!get(&b.norm, 4 * t * H) || !get(&b.logits, 4 * t * E) || !get(&b.idx, 4 * t * K) || !get(&b.wts, 4 * t * K) ||
+        !get(&b.counts, 4 * E) || !get(&b.offsets, 4 * (E + 1)) || !get(&b.lists, 4 * E * t) ||
+        !get(&b.ent, 4 * t * K) || !get(&b.pos, 4 * t * K) || !get(&b.mid, 4 * t * K * I) ||
+        !get(&b.expout, 4 * t * K * H) || !get(&b.smid, 4 * t * SI) || !get(&b.shout, 4 * t * H)) {
+        for (void* p : B.bufs) (void)hipFree(p);
+        B.bufs.clear();
+        return fail(c, WL_ERR_OOM, "batched scratch for %u tokens", T);
+    }
+    B.cap = T;
+    return WL_OK;
+}
+
+wl_status wl_run_moe_batched(wl_ctx* c, uint32_t layer, uint32_t n_tokens, const float* d_hidden,
+                             const float* d_resid, float* d_out, void* stream) {
+    if (!c) return WL_ERR_INVALID;
+    if (layer >= c->cfg.n_layers) return fail(c, WL_ERR_INVALID, "layer %u >= n_layers %u", layer, c->cfg.n_layers);
+    if (!c->layers[layer].set) return fail(c, WL_ERR_STATE, "layer %u has no weights (wl_set_layer)", layer);
+    if (n_tokens == 0 || n_tokens > 65535) return fail(c, WL_ERR_INVALID, "n_tokens=%u must be in [1,65535]", n_tokens);
+    if (!d_hidden || !d_out || d_out == d_hidden || (d_resid && d_out == d_resid))
+        return fail(c, WL_ERR_INVALID, "null or aliasing batched buffers");
+    const uint32_t E = c->cfg.n_routed_experts;
+    if (c->n_bound[layer] != E)
+        return fail(c, WL_ERR_NOT_RESIDENT, "batched layer %u needs every expert bound (%u of %u)", layer,
+                    c->n_bound[layer], E);
+    wl_status s = batch_reserve(c, n_tokens);
+    if (s != WL_OK) return s;
+    wl::BatchArgs b = c->batch.b;
+    b.T = n_tokens;
+    b.hidden = d_hidden;
+    b.resid = d_resid;
+    b.out = d_out;
+    int e = wl::launch_batched(c->d_largs + layer, b, c->cfg.hidden, c->cfg.moe_inter, c->SI, E,
+                               c->cfg.n_experts_per_tok, (uint32_t)c->n_cu, stream);
+    if (e != 0) return hip_fail(c, (hipError_t)e, "batched launch");
     return WL_OK;
 }
 

@@ -82,6 +82,7 @@ def load():
         "wl_run_moe": [vp, u32, vp, vp, vp],
         "wl_run_moe_residual": [vp, u32, vp, vp, vp, vp],
         "wl_run_chain": [vp, u32, u32, vp, vp, vp],
+        "wl_run_moe_batched": [vp, u32, u32, vp, vp, vp, vp],
         "wl_taps": [vp, ctypes.POINTER(Taps)],
         "wl_check_error": [vp, vp],
         "wl_set_schedule": [vp, i32],
@@ -230,6 +231,10 @@ class Context:
     def run_moe_residual(self, layer, d_hidden, d_resid, d_out, stream=0):
         self._ck(self.lib.wl_run_moe_residual(self.h, layer, d_hidden, d_resid, d_out, stream),
                  "wl_run_moe_residual")
+
+    def run_moe_batched(self, layer, n_tokens, d_hidden, d_resid, d_out, stream=0):
+        self._ck(self.lib.wl_run_moe_batched(self.h, layer, n_tokens, d_hidden, d_resid, d_out, stream),
+                 "wl_run_moe_batched")
 
     def run_chain(self, first_layer, n_layers, d_h, d_tmp, stream=0):
         self._ck(self.lib.wl_run_chain(self.h, first_layer, n_layers, d_h, d_tmp, stream), "wl_run_chain")
