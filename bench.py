@@ -19,6 +19,11 @@ layer; a step is one decode token through all 24 layers, starting from its own
 seeded N(0,1) hidden state. `value` is then microseconds per layer within the
 chain (step time / 24) and tokens_per_s is reported beside it.
 
+--workload batched measures configs[3]: one GLM MoE layer applied to
+--tokens T positions at once (wl_run_moe_batched), router bias with the Zipf
+offset; `value` is microseconds per layer call (all T tokens), with
+tokens_per_s and the achieved bytes of the experts actually used.
+
 --workload cache measures configs[4]: 75 MoE layers whose 19,200 experts sit
 behind the HBM expert cache (3,094 slots, 62 GB) and are copied from pinned
 host memory on a miss; router bias shaped by Zipf(1.1) popularity; a step is
@@ -99,9 +104,10 @@ def main():
     ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--layers", type=int, default=8, help="distinct resident layer copies to rotate over")
     ap.add_argument("--sched", choices=["fused", "phased"], default="fused")
-    ap.add_argument("--workload", choices=["layer", "chain", "cache"], default="layer",
+    ap.add_argument("--workload", choices=["layer", "chain", "batched", "cache"], default="layer",
                     help="layer: config 1 (default); chain: config 2, 24 layers per step; "
-                         "cache: config 4, 75 cache-backed layers per step")
+                         "batched: config 3, --tokens positions per step; cache: config 4, 75 cache-backed layers per step")
+    ap.add_argument("--tokens", type=int, default=256, help="batched workload: positions per layer call")
     ap.add_argument("--chain-layers", type=int, default=24)
     ap.add_argument("--cache-layers", type=int, default=75)
     ap.add_argument("--cache-slots", type=int, default=3094)
@@ -134,6 +140,7 @@ def main():
     c = dict(GLM)
     H = c["hidden"]
     cache = args.workload == "cache"
+    batched = args.workload == "batched"
     chain = args.workload == "chain" or cache
     if chain:
         args.layers = args.cache_layers if cache else args.chain_layers
@@ -148,6 +155,15 @@ def main():
                          bias_offset=synthdata.zipf_bias_offset(c["n_routed_experts"], args.seed,
                                                                 amplitude=args.zipf_amp))
         dm.ctx.cache_set_speculation(args.spec)
+    elif batched:
+        args.layers = 1
+        if "--steps" not in sys.argv:
+            args.steps = 20
+        if "--warmup" not in sys.argv:
+            args.warmup = 3
+        dm = DeviceModel(c, seed=args.seed, n_layers=1,
+                         bias_offset=synthdata.zipf_bias_offset(c["n_routed_experts"], args.seed,
+                                                                amplitude=args.zipf_amp))
     else:
         dm = DeviceModel(c, seed=args.seed, n_layers=args.layers)
     dm.ctx.set_schedule(moe.SCHED_FUSED if args.sched == "fused" else moe.SCHED_PHASED)
@@ -161,7 +177,16 @@ def main():
 
     d_h, d_tmp = hip.DeviceBuffer(4 * H), hip.DeviceBuffer(4 * H)
 
+    if batched:
+        T = args.tokens
+        hb = np.stack([synthdata.hidden_state(H, 7000 + (t % 256)) for t in range(T)])
+        d_hb = hip.DeviceBuffer.from_array(hb)
+        d_ob = hip.DeviceBuffer(4 * H * T)
+
     def step(i):
+        if batched:
+            dm.ctx.run_moe_batched(0, T, d_hb.ptr, None, d_ob.ptr, stream.handle)
+            return
         if chain:  # one token: its own start state, then h <- h + moe(h) through every layer
             hip.copy_d2d(d_h.ptr, d_hs.ptr + 4 * H * (i % n_h), 4 * H, stream.handle)
             dm.ctx.run_chain(0, args.layers, d_h.ptr, d_tmp.ptr, stream.handle)
@@ -196,9 +221,16 @@ def main():
         dst.free()
 
     nbytes = algorithmic_bytes(c)
+    if batched:  # the experts this batch used (each read once), shared, router, T input/output rows
+        cnt = dm.ctx.batched_counts()
+        H_, I_ = c["hidden"], c["moe_inter"]
+        expert = 3 * I_ * H_ // 2 + 3 * I_ * H_ // 32
+        uniq = int((cnt > 0).sum())
+        nbytes = uniq * expert + 3 * I_ * c["n_shared"] * H_ * 2 + c["n_routed_experts"] * H_ * 2 + \
+            c["n_routed_experts"] * 4 + 2 * H_ * 4 * args.tokens
     achieved = nbytes / (us_per_layer * 1e-6) / 1e9
     traffic = None
-    if os.path.exists(args.traffic_json):
+    if args.workload in ("layer", "chain") and os.path.exists(args.traffic_json):
         try:
             traffic = json.load(open(args.traffic_json)).get("hbm_bytes_per_layer")
         except Exception:
@@ -229,7 +261,8 @@ def main():
         "vs_baseline": None,
         "dtype": "mxfp4/bf16 weights, f32 activations and accumulation",
         "data": "synthetic",
-        "config": {"workload": (f"config4: {args.layers} GLM MoE layers behind a {args.cache_slots}-slot HBM expert "
+        "config": {"workload": (f"config3: one GLM MoE layer over {args.tokens} tokens (batched)" if batched else
+                                f"config4: {args.layers} GLM MoE layers behind a {args.cache_slots}-slot HBM expert "
                                 f"cache, misses from pinned host memory, bs=1" if cache else
                                 f"config2: chain of {args.layers} resident GLM MoE decode layers, bs=1, "
                                 f"h <- h + moe(h)" if chain else "config1: one GLM MoE decode layer, bs=1"),
@@ -237,7 +270,7 @@ def main():
                    "n_experts_per_tok": c["n_experts_per_tok"], "shared": "bf16 inter 2048",
                    ("chain_layers" if chain else "rotating_layers"): args.layers, "schedule": args.sched,
                    "global_batch": 1},
-        "tokens_per_s": round(1e6 / (us_per_layer * layers_per_step), 2),
+        "tokens_per_s": round(1e6 / (us_per_layer * layers_per_step) * (args.tokens if batched else 1), 2),
         "tokens_per_s_per_layer": round(1e6 / us_per_layer, 1),
         "achieved_GBps": round(achieved, 1),
         "pct_of_hbm_peak": round(100 * achieved / PEAK_HBM_GBPS, 2),
@@ -245,6 +278,8 @@ def main():
                      "frac": round(achieved / PEAK_HBM_GBPS, 4), "traffic": traffic,
                      "algorithmic_bytes": nbytes, "kernel": "moe_decode_kernel"},
         "cpu_baseline": cpu,
+        **({"batched": {"tokens": args.tokens, "unique_experts": uniq, "max_tokens_per_expert": int(cnt.max()),
+                        "zipf": {"s": 1.1, "amplitude": args.zipf_amp}}} if batched else {}),
         **({"cache": {"hit_rate": round(cstats["hits"] / max(1, cstats["hits"] + cstats["misses"]), 4),
                       "hits": cstats["hits"], "misses": cstats["misses"], "evictions": cstats["evictions"],
                       "speculation": args.spec, "spec_requests": cstats["spec_requests"],

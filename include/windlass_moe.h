@@ -152,6 +152,12 @@ wl_status wl_run_chain(wl_ctx* ctx, uint32_t first_layer, uint32_t n_layers, flo
 wl_status wl_run_moe_batched(wl_ctx* ctx, uint32_t layer, uint32_t n_tokens, const float* d_hidden,
                              const float* d_resid, float* d_out, void* stream);
 
+/* Tokens routed to each expert by the last wl_run_moe_batched call (h_counts:
+ * host array of n_routed_experts; synchronises the device). The grouping the
+ * reference keeps in run_moe_batched's where[] (src/glm_layer_runner.cuh:
+ * 855-868). */
+wl_status wl_batched_counts(wl_ctx* ctx, uint32_t* h_counts);
+
 /* Device pointers to the last layer's intermediates (the substeps
  * test_glm_chain reads through SubstepHook, src/test_glm_chain.cu:434-441). */
 typedef struct wl_taps_out {

@@ -655,6 +655,16 @@ wl_status wl_run_moe_batched(wl_ctx* c, uint32_t layer, uint32_t n_tokens, const
     return WL_OK;
 }
 
+wl_status wl_batched_counts(wl_ctx* c, uint32_t* h_counts) {
+    if (!c || !h_counts) return WL_ERR_INVALID;
+    if (!c->batch.cap) return fail(c, WL_ERR_STATE, "no batched call yet");
+    hipError_t e = hipDeviceSynchronize();
+    if (e == hipSuccess)
+        e = hipMemcpy(h_counts, c->batch.b.counts, 4 * (size_t)c->cfg.n_routed_experts, hipMemcpyDeviceToHost);
+    if (e != hipSuccess) return hip_fail(c, e, "batched counts");
+    return WL_OK;
+}
+
 wl_status wl_cache_create(wl_ctx* c, uint32_t capacity, wl_host_block_fn host_block, void* user) {
     if (!c) return WL_ERR_INVALID;
     CacheState& C = c->cache;

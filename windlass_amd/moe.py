@@ -83,6 +83,7 @@ def load():
         "wl_run_moe_residual": [vp, u32, vp, vp, vp, vp],
         "wl_run_chain": [vp, u32, u32, vp, vp, vp],
         "wl_run_moe_batched": [vp, u32, u32, vp, vp, vp, vp],
+        "wl_batched_counts": [vp, ctypes.POINTER(u32)],
         "wl_taps": [vp, ctypes.POINTER(Taps)],
         "wl_check_error": [vp, vp],
         "wl_set_schedule": [vp, i32],
@@ -235,6 +236,13 @@ class Context:
     def run_moe_batched(self, layer, n_tokens, d_hidden, d_resid, d_out, stream=0):
         self._ck(self.lib.wl_run_moe_batched(self.h, layer, n_tokens, d_hidden, d_resid, d_out, stream),
                  "wl_run_moe_batched")
+
+    def batched_counts(self):
+        import numpy as np
+        out = np.zeros(self.cfg.n_routed_experts, dtype=np.uint32)
+        self._ck(self.lib.wl_batched_counts(self.h, out.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32))),
+                 "wl_batched_counts")
+        return out
 
     def run_chain(self, first_layer, n_layers, d_h, d_tmp, stream=0):
         self._ck(self.lib.wl_run_chain(self.h, first_layer, n_layers, d_h, d_tmp, stream), "wl_run_chain")
