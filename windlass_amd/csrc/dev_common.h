@@ -353,15 +353,17 @@ WL_DEV float norm_value(float x, float rinv, bool has_ln, uint32_t ln_bits) {
     return y;
 }
 // This thread's share of one router row (bf16 x f32, fp32 accumulate),
-// reduced over the wave.
-WL_DEV float router_partial(const u32x4 (&rw)[kRCH], const float* xn, uint32_t nch) {
+// reduced over the wave. x(m, h) returns xn[8c + 4h .. 8c + 4h + 4) for the
+// thread's chunk c = threadIdx.x + kThreads * m (from LDS or registers: the
+// arithmetic is the same either way).
+template <class XF>
+WL_DEV float router_partial_x(const u32x4 (&rw)[kRCH], XF x, uint32_t nch) {
     float pd = 0.f;
 #pragma unroll
     for (int m = 0; m < kRCH; m++) {
         const uint32_t c = threadIdx.x + kThreads * m;
         if (c < nch) {
-            const float4 x0 = *(const float4*)(xn + 8 * c);
-            const float4 x1 = *(const float4*)(xn + 8 * c + 4);
+            const float4 x0 = x(m, 0), x1 = x(m, 1);
             pd = fmaf(bf2f(rw[m].x & 0xFFFFu), x0.x, pd);
             pd = fmaf(bf2f(rw[m].x >> 16), x0.y, pd);
             pd = fmaf(bf2f(rw[m].y & 0xFFFFu), x0.z, pd);
@@ -374,6 +376,10 @@ WL_DEV float router_partial(const u32x4 (&rw)[kRCH], const float* xn, uint32_t n
     }
     for (int o = 32; o > 0; o >>= 1) pd += __shfl_xor(pd, o, 64);
     return pd;
+}
+WL_DEV float router_partial(const u32x4 (&rw)[kRCH], const float* xn, uint32_t nch) {
+    return router_partial_x(
+        rw, [&](int m, int h) { return *(const float4*)(xn + 8u * (threadIdx.x + kThreads * m) + 4u * h); }, nch);
 }
 // Sum of the 8 wave partials of router row r (slot 48 of each wave's red
 // line), published as one 64-bit word (epoch << 32 | bits) with an
