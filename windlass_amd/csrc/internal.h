@@ -28,33 +28,24 @@ constexpr uint32_t kMaxGrid = 2048;
 // A release fence (L2 write-back) is never needed; one per work-group cut
 // streaming from 5.2 to 0.9 TB/s.
 //
-// The barrier words (counters, release words, error bits) live in uncached
-// memory so that read-modify-writes from all XCDs meet at one point. Counters
-// and release words each own a 128-byte line: read-modify-writes on one line
-// serialise (about 15 ns each).
+// The error word lives in uncached memory so that read-modify-writes from
+// all XCDs meet at one point; it owns a 128-byte line.
 constexpr uint32_t kLineWords = 32;
 
 // Error bits reported in the error word.
 enum : uint32_t {
-    E_SPIN = 1u,          // a grid barrier wait exceeded its bound
+    E_SPIN = 1u,          // a wait for another work-group's data exceeded its bound
     E_NOT_RESIDENT = 2u,  // a routed expert resolved to a null block
 };
 
 // Word offsets inside the uncached synchronisation block.
 struct SyncMap {
-    uint32_t bar_grp;   // [8] arrival counters, one per group of work-groups (w % 8)
-    uint32_t bar_all;   // arrivals of complete groups
-    uint32_t bar_rel;   // [kMaxGrid] release words, one line per work-group
     uint32_t error;     // sticky error bits
     uint32_t words;
     __host__ __device__ static SyncMap make() {
         SyncMap m;
-        uint32_t o = 0;
-        m.bar_grp = o; o += 8 * kLineWords;
-        m.bar_all = o; o += kLineWords;
-        m.bar_rel = o; o += kMaxGrid * kLineWords;
-        m.error = o;   o += kLineWords;
-        m.words = o;
+        m.error = 0;
+        m.words = kLineWords;
         return m;
     }
 };
@@ -69,7 +60,7 @@ struct SyncMap {
 //                    columns [64j, 64j+64) of down
 //   partials         every work-group's w_k-weighted routed and shared
 //                    contributions, summed per output row in LDS, published as
-//                    one H-vector per work-group
+//                    one H-vector per work-group of epoch-tagged words
 //   combine          H/32 blocks of 32 rows, block b on b mod G
 constexpr uint32_t kRowBlock = 32;  // rows per combine block (= rows per down item)
 struct Plan {
@@ -101,8 +92,8 @@ struct DecodeArgs {
     float* shared_out;          // [H] (written when taps are on)
     // cross-work-group arrays (agent-scope stores and loads)
     uint64_t* lslot;            // [E] logit of this call: epoch << 32 | f32 bits
-    float* part;                // [H/32][G][32] partials, block-major
-    float* tsh;                 // [H/32][G][32] shared-expert partials (taps on)
+    uint64_t* part;             // [H/32][G][32] partials, block-major, epoch << 32 | f32 bits
+    uint64_t* tsh;              // [H/32][G][32] shared-expert partials (taps on), tagged likewise
     uint32_t* sync;             // synchronisation block (SyncMap), uncached
     uint32_t H, I, E, K, SI;
     float eps, scaling;
@@ -111,15 +102,14 @@ struct DecodeArgs {
 
 // Per-call launch arguments (kernel arguments by value). A layer runs as
 // segment 0 (everything up to the published partials) and segment 1 (the
-// combine); a fused launch runs both with a grid barrier between them, the
-// phased schedule runs each as its own launch.
+// combine); a fused launch runs both (the combine waits for the epoch tags of
+// the partials it reads), the phased schedule runs each as its own launch.
 struct DecodeDyn {
     const float* hidden;        // [H] pre-norm residual stream
     const float* resid;         // [H] or null: out = resid + moe
     float* out;                 // [H]
     uint32_t seg_lo, seg_hi;
     uint32_t epoch;             // different for every call of the context, never 0
-    uint32_t bar_seq;           // fused launches: this launch's grid-barrier number (>= 1)
     int32_t taps;               // 1: also produce the shared-expert output tap
 };
 

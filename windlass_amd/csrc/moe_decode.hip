@@ -65,64 +65,12 @@ __device__ uint64_t g_tl[kMaxGrid * 16];
     } while (0)
 #endif
 
-// Grid barrier number `seq` (1, 2, ... over the life of the sync block).
-// Arrival: one counter per group of work-groups (w mod 8, i.e. one per XCD)
-// and one counter of complete groups. The counters only grow: after barrier
-// n a group counter holds n x members and the group counter n x groups, so
-// the arrival that completes a group (and then the grid) is recognised from
-// the value its increment returns, with no reset. The work-group that
-// completes the grid writes `seq` to every work-group's release word, which
-// each work-group polls. Completing a work-group's cross-work-group stores
-// before its arrival is the whole release; the readers use agent-scope loads.
-// Bounded: returns false, with E_SPIN raised, if the release does not come,
-// and false if another work-group raised an error meanwhile.
-WL_DEV bool grid_barrier(uint32_t* sync, const SyncMap& m, uint32_t seq, uint32_t w, uint32_t G,
-                         uint32_t* s_flag, bool all_waves_stored) {
-    // Only wave 0 wrote cross-work-group data unless all_waves_stored; the
-    // other waves then keep whatever loads they have in flight.
-    if (all_waves_stored || threadIdx.x < 64) vm_drain();
-    lds_barrier();
-    WL_TL(11);
-    if (threadIdx.x < 64) {
-        const uint32_t lane = threadIdx.x;
-        const uint32_t grp = w & 7u;
-        const uint32_t members = (G - grp + 7u) / 8u;
-        const uint32_t groups = G < 8u ? G : 8u;
-        uint32_t old = 0;
-        if (lane == 0) old = rmw_inc(sync + m.bar_grp + grp * kLineWords);
-        old = __shfl(old, 0, 64);
-        if (old + 1u == members * seq) {
-            uint32_t old2 = 0;
-            if (lane == 0) old2 = rmw_inc(sync + m.bar_all);
-            old2 = __shfl(old2, 0, 64);
-            if (old2 + 1u == groups * seq)
-                for (uint32_t f = lane; f < G; f += 64) st_sync(sync + m.bar_rel + f * kLineWords, seq);
-        }
-    uint32_t ok = 1u;
-        for (uint32_t spins = 0;; spins++) {
-            uint32_t r = 0, e = 0;
-            if (lane == 0) {
-                r = ld_sync(sync + m.bar_rel + w * kLineWords);
-                if ((spins & 255u) == 255u) e = ld_sync(sync + m.error);
-            }
-            r = __shfl(r, 0, 64);
-            e = __shfl(e, 0, 64);
-            if (r == seq) break;
-            if (e != 0u) { ok = 0u; break; }
-            if (spins > (1u << 22)) {
-                if (lane == 0) raise_error(sync, m, E_SPIN);
-                ok = 0u;
-                break;
-            }
-            __builtin_amdgcn_s_sleep(1);
-        }
-        if (lane == 0) *s_flag = ok;
-    }
-    WL_TL(12);
-    lds_barrier();
-    const bool ok = *s_flag != 0u;
-    lds_barrier();
-    return ok;
+
+// A cross-work-group value with this call's epoch: one 8-byte agent-scope
+// store, so a reader that sees the epoch sees the value.
+WL_DEV void st_tag(uint64_t* p, uint32_t epoch, float x) {
+    __hip_atomic_store((__attribute__((address_space(1))) uint64_t*)p, ((uint64_t)epoch << 32) | __float_as_uint(x),
+                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ---- the decode kernel -------------------------------------------------------
@@ -359,15 +307,10 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const DecodeDyn d) {
             }
         }
         // pv -> rows [32b, 32b+32) into block b, slot w of dst ([H/32][G][32]),
-        // agent-scope 16-byte stores
-        auto publish = [&](float* dst) {
-            const rsrc_t rs = make_rsrc(dst, P.NB * G * kRowBlock * 4u);
-            for (uint32_t c = tid; c < H / 4u; c += kThreads) {
-                const uint32_t r = 4u * c, b = r / kRowBlock;
-                const u32x4 x = *(const u32x4*)(pv + r);
-                __builtin_amdgcn_raw_buffer_store_b128(x, rs, (int)(4u * ((b * G + w) * kRowBlock + r % kRowBlock)), 0,
-                                                       kSC1);
-            }
+        // tagged with this call's epoch
+        auto publish = [&](uint64_t* dst) {
+            for (uint32_t r = tid; r < H; r += kThreads)
+                st_tag(dst + ((size_t)(r / kRowBlock) * G + w) * kRowBlock + r % kRowBlock, d.epoch, pv[r]);
         };
         // the deferred down columns, then (taps on) the shared-expert
         // contribution alone, published for the tap
@@ -523,7 +466,7 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const DecodeDyn d) {
                     // to block q of the partials
                     if (valid && lane < 32) {
                         const float x = pv[q * 32u + lane] + wk * (lane < 16 ? s0 : s1);
-                        if (direct) st_ag(a.part + ((size_t)q * G + w) * kRowBlock + lane, x);
+                        if (direct) st_tag(a.part + ((size_t)q * G + w) * kRowBlock + lane, d.epoch, x);
                         else pv[q * 32u + lane] = x;
                     }
                 }
@@ -531,6 +474,7 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const DecodeDyn d) {
         };
 
         bool first_unit = true;
+        bool ran = false;  // a unit's down items published this work-group's rows
         for (uint32_t u = w; u < P.U; u += G) {
             uk = u % K;
             uj = u / K;
@@ -542,6 +486,7 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const DecodeDyn d) {
             }
             if (!first_unit) lds_barrier();  // rmp of the previous unit fully read
             first_unit = false;
+            ran = true;
             {
                 const NativeLayout NL = NativeLayout::make(H, I);
                 const uint32_t tile = uj * (kSlice / 8u) + v;  // this wave's 8+8 row tile
@@ -562,11 +507,11 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const DecodeDyn d) {
         lds_barrier();
 
         // ---- publish this work-group's partial (the combine of block b reads
-        // its G slots contiguously), unless the down items already did
-        if (!direct) publish(a.part);
-        if (d.seg_hi >= 1u) {
-            if (!grid_barrier(a.sync, SM, d.bar_seq, w, G, misc + 8, true)) return;
-        }
+        // its G slots contiguously), unless the down items already did. No
+        // barrier follows: the combine waits for the epoch tags of the words
+        // it reads.
+        if (!(direct && ran)) publish(a.part);
+        lds_barrier();  // pv is the combine's staging area
         WL_TL(9);
     }
 
@@ -576,17 +521,44 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const DecodeDyn d) {
         constexpr uint32_t RB = kRowBlock;
         float* fin = pv;                   // [G][32]
         float* f2 = fin + (size_t)G * RB;  // [16][32]
-        // sum of the G slots of block blkr of src; the result is in threads 0..31
-        auto block_total = [&](const float* src, uint32_t blkr) -> float {
-            const rsrc_t rs = make_rsrc(src + (size_t)blkr * G * RB, G * RB * 4u);
-            for (uint32_t base = 0; base < G * RB; base += kThreads * 16u) {
-                u32x4 pq[4];
+        // sum of the G slots of block blkr of src; the result is in threads
+        // 0..31. Each thread reads 16-byte chunks (two tagged words) of the
+        // block with agent-scope loads: all at once first, then, for chunks
+        // whose writer has not finished (an older epoch), again until this
+        // call's epoch shows (bounded; the error word ends the wait too).
+        auto block_total = [&](const uint64_t* src, uint32_t blkr) -> float {
+            const uint32_t nchunk = G * RB / 2u;
+            const rsrc_t rs = make_rsrc(src + (size_t)blkr * G * RB, G * RB * 8u);
+            constexpr uint32_t kGrp = 8;
+            for (uint32_t c0 = 0; c0 < nchunk; c0 += kThreads * kGrp) {
+                u32x4 q[kGrp];
 #pragma unroll
-                for (int i = 0; i < 4; i++) pq[i] = bld16_ag(rs, 4u * (base + 4u * (tid + kThreads * i)), 0u);
+                for (uint32_t i = 0; i < kGrp; i++) q[i] = bld16_ag(rs, 16u * (c0 + tid + kThreads * i), 0u);
+                uint32_t stale = 0;  // bit i: chunk i still holds an older epoch
+                for (uint32_t spins = 0;; spins++) {
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const uint32_t idx = base + 4u * (tid + kThreads * i);
-                    if (idx < G * RB) *(u32x4*)(fin + idx) = pq[i];
+                    for (uint32_t i = 0; i < kGrp; i++) {
+                        const uint32_t ch = c0 + tid + kThreads * i;
+                        const bool mine = ch < nchunk && (spins == 0 || ((stale >> i) & 1u));
+                        if (!mine) continue;
+                        if (q[i].y == d.epoch && q[i].w == d.epoch) {
+                            fin[2u * ch] = __uint_as_float(q[i].x);
+                            fin[2u * ch + 1u] = __uint_as_float(q[i].z);
+                            stale &= ~(1u << i);
+                        } else {
+                            stale |= 1u << i;
+                        }
+                    }
+                    if (stale == 0u) break;
+                    if (spins >= (1u << 20)) {
+                        raise_error(a.sync, SM, E_SPIN);
+                        break;
+                    }
+                    if ((spins & 63u) == 63u && ld_sync(a.sync + SM.error) != 0u) break;
+                    __builtin_amdgcn_s_sleep(2);
+#pragma unroll
+                    for (uint32_t i = 0; i < kGrp; i++)  // every stale chunk again, all in flight together
+                        if ((stale >> i) & 1u) q[i] = bld16_ag(rs, 16u * (c0 + tid + kThreads * i), 0u);
                 }
             }
             lds_barrier();

@@ -83,14 +83,13 @@ struct wl_ctx {
     int32_t taps = 1;
     // cross-work-group arrays (agent-scope stores and loads)
     uint64_t* lslot = nullptr;
-    float* part = nullptr;
-    float* tsh = nullptr;
+    uint64_t* part = nullptr;
+    uint64_t* tsh = nullptr;
     uint32_t* sync = nullptr;   // barrier words (uncached)
     wl::SyncMap sm{};
     wl::Plan plan{};
     uint32_t grid = 0;
     uint32_t epoch = 0;
-    uint32_t bar_seq = 0;  // grid barriers run since the sync block was last zeroed
     void* uc_block = nullptr;   // uncached scratch (returned to the process pool on destroy)
     size_t uc_bytes = 0;
     // context-owned slot pool
@@ -279,8 +278,8 @@ wl_status wl_create(const wl_moe_config* cfg, wl_ctx** out) {
         (s = dalloc(c, &c->ffn_mid_p, 2 * 3 * (size_t)I)) != WL_OK ||
         (s = dalloc(c, &c->logits, 4 * (size_t)E)) != WL_OK ||
         (s = dalloc(c, &c->lslot, 8 * (size_t)E)) != WL_OK ||
-        (s = dalloc(c, &c->part, 4 * (size_t)H * grid)) != WL_OK ||
-        (s = dalloc(c, &c->tsh, 4 * (size_t)H * grid)) != WL_OK) {
+        (s = dalloc(c, &c->part, 8 * (size_t)H * grid)) != WL_OK ||
+        (s = dalloc(c, &c->tsh, 8 * (size_t)H * grid)) != WL_OK) {
         wl_destroy(c);
         return s;
     }
@@ -293,7 +292,11 @@ wl_status wl_create(const wl_moe_config* cfg, wl_ctx** out) {
     }
     c->sync = (uint32_t*)c->uc_block;
     e = hipMemset(c->d_slot, 0, sizeof(void*) * (size_t)L * E);
-    if (e == hipSuccess) e = hipMemset(c->lslot, 0, 8 * (size_t)E);  // epoch 0: never a call's
+    // epoch 0 is never a call's: zeroed tagged arrays hold no valid word (a
+    // reused allocation could otherwise carry another context's tags)
+    if (e == hipSuccess) e = hipMemset(c->lslot, 0, 8 * (size_t)E);
+    if (e == hipSuccess) e = hipMemset(c->part, 0, 8 * (size_t)H * grid);
+    if (e == hipSuccess) e = hipMemset(c->tsh, 0, 8 * (size_t)H * grid);
     if (e == hipSuccess) e = hipMemset(c->uc_block, 0, c->uc_bytes);
     if (e == hipSuccess) e = hipDeviceSynchronize();
     if (e != hipSuccess) { wl_destroy(c); return WL_ERR_HIP; }
@@ -538,12 +541,6 @@ static wl_status run_layer(wl_ctx* c, uint32_t layer, const float* d_hidden, con
         return WL_OK;
     };
     if (c->sched == WL_SCHED_FUSED) {
-        if (++c->bar_seq == 0u) {  // after 2^32 barriers: zero the counters, start again at 1
-            hipError_t e = hipMemsetAsync(c->sync, 0, 4 * (size_t)c->sm.words, (hipStream_t)stream);
-            if (e != hipSuccess) return hip_fail(c, e, "sync block reset");
-            c->bar_seq = 1u;
-        }
-        dyn.bar_seq = c->bar_seq;
         wl_status s = launch(0, 1);
         if (s != WL_OK || !cached) return s;
         return cache_speculate(c, (hipStream_t)stream);
@@ -795,7 +792,6 @@ wl_status wl_check_error(wl_ctx* c, void* stream) {
         // a launch that gave up may have left barrier counters mid-count
         (void)hipMemset(c->sync, 0, 4 * (size_t)c->sm.words);
         (void)hipDeviceSynchronize();
-        c->bar_seq = 0;
         return fail(c, WL_ERR_DEVICE, "device error bits 0x%x%s%s", flag,
                     (flag & wl::E_SPIN) ? " [dependency wait expired]" : "",
                     (flag & wl::E_NOT_RESIDENT) ? " [routed expert not resident]" : "");
