@@ -268,41 +268,44 @@ WL_DEV uint32_t fkey(float f) {
     const uint32_t u = __float_as_uint(f);
     return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
-// E <= 256: K rounds of a wave-wide argmax (wave 0, expert lane + 64m in
-// slot m of each lane) over fkey(choice): the largest choice, ties to the
-// lowest index (the first set bit of the first slot that holds the maximum),
-// i.e. the reference's K serial argmax passes (src/glm_layer_runner.cuh:
-// 318-330). Keys of real experts are > 0 (fkey(-inf) > 0); 0 marks an empty
-// slot or a taken expert.
-WL_DEV void topk_argmax(uint32_t E, uint32_t K, const float* sc, const float* ch, uint32_t* sidx, float* sw) {
-    if (threadIdx.x < 64) {
-        const uint32_t lane = threadIdx.x;
-        uint32_t key[4];
+// E <= 256: K rounds of a wave-wide argmax (one whole wave, expert lane +
+// 64m in slot m of each lane) over fkey(choice): the largest choice, ties to
+// the lowest index (the first set bit of the first slot that holds the
+// maximum), i.e. the reference's K serial argmax passes
+// (src/glm_layer_runner.cuh:318-330). Keys of real experts are > 0
+// (fkey(-inf) > 0); 0 marks an empty slot or a taken expert. No barrier: the
+// caller orders sidx/sw for the other waves.
+WL_DEV void topk_argmax_wave(uint32_t E, uint32_t K, const float* sc, const float* ch, uint32_t* sidx, float* sw) {
+    const uint32_t lane = threadIdx.x & 63u;
+    uint32_t key[4];
 #pragma unroll
-        for (int m = 0; m < 4; m++) {
-            const uint32_t e = lane + 64u * m;
-            key[m] = e < E ? fkey(ch[e]) : 0u;
-        }
-        for (uint32_t k = 0; k < K; k++) {
-            const uint32_t a01 = key[0] > key[1] ? key[0] : key[1];
-            const uint32_t a23 = key[2] > key[3] ? key[2] : key[3];
-            const uint32_t mx = wave_max_u32(a01 > a23 ? a01 : a23);
-            const uint64_t b0 = __builtin_amdgcn_ballot_w64(key[0] == mx);
-            const uint64_t b1 = __builtin_amdgcn_ballot_w64(key[1] == mx);
-            const uint64_t b2 = __builtin_amdgcn_ballot_w64(key[2] == mx);
-            const uint64_t b3 = __builtin_amdgcn_ballot_w64(key[3] == mx);
-            const uint32_t e = b0 ? (uint32_t)__builtin_ctzll(b0)
-                             : b1 ? 64u + (uint32_t)__builtin_ctzll(b1)
-                             : b2 ? 128u + (uint32_t)__builtin_ctzll(b2)
-                                  : 192u + (uint32_t)__builtin_ctzll(b3);
-#pragma unroll
-            for (int m = 0; m < 4; m++)
-                if (lane + 64u * m == e) key[m] = 0u;
-            if (lane == 0) sidx[k] = e;
-        }
-        // one wave: its LDS accesses complete in program order
-        if (lane < K) sw[lane] = sc[sidx[lane]];
+    for (int m = 0; m < 4; m++) {
+        const uint32_t e = lane + 64u * m;
+        key[m] = e < E ? fkey(ch[e]) : 0u;
     }
+    for (uint32_t k = 0; k < K; k++) {
+        const uint32_t a01 = key[0] > key[1] ? key[0] : key[1];
+        const uint32_t a23 = key[2] > key[3] ? key[2] : key[3];
+        const uint32_t mx = wave_max_u32(a01 > a23 ? a01 : a23);
+        const uint64_t b0 = __builtin_amdgcn_ballot_w64(key[0] == mx);
+        const uint64_t b1 = __builtin_amdgcn_ballot_w64(key[1] == mx);
+        const uint64_t b2 = __builtin_amdgcn_ballot_w64(key[2] == mx);
+        const uint64_t b3 = __builtin_amdgcn_ballot_w64(key[3] == mx);
+        const uint32_t e = b0 ? (uint32_t)__builtin_ctzll(b0)
+                         : b1 ? 64u + (uint32_t)__builtin_ctzll(b1)
+                         : b2 ? 128u + (uint32_t)__builtin_ctzll(b2)
+                              : 192u + (uint32_t)__builtin_ctzll(b3);
+#pragma unroll
+        for (int m = 0; m < 4; m++)
+            if (lane + 64u * m == e) key[m] = 0u;
+        if (lane == 0) sidx[k] = e;
+    }
+    // one wave: its LDS accesses complete in program order
+    if (lane < K) sw[lane] = sc[sidx[lane]];
+}
+// The same by wave 0 of the work-group, then a barrier.
+WL_DEV void topk_argmax(uint32_t E, uint32_t K, const float* sc, const float* ch, uint32_t* sidx, float* sw) {
+    if (threadIdx.x < 64) topk_argmax_wave(E, K, sc, ch, sidx, sw);
     lds_barrier();
 }
 
