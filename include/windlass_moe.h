@@ -147,12 +147,14 @@ wl_status wl_run_chain(wl_ctx* ctx, uint32_t first_layer, uint32_t n_layers, flo
  * grouped by expert (stable, (token, slot) order) and every selected expert's
  * weights are streamed once per 32 of its tokens; the per-token combine sums
  * the slots in slot order, then the shared expert (the reference's pass 3).
- * Requires every expert of the layer bound (resident); n_tokens <= 65535.
- * Scratch grows to the largest n_tokens seen (context-owned; growing synchronises the device). */
+ * Requires every expert of the layer bound (resident); n_tokens <= 65535, run
+ * in chunks of up to 4096 tokens. Scratch grows to the largest chunk seen
+ * (context-owned; growing synchronises the device). */
 wl_status wl_run_moe_batched(wl_ctx* ctx, uint32_t layer, uint32_t n_tokens, const float* d_hidden,
                              const float* d_resid, float* d_out, void* stream);
 
-/* Tokens routed to each expert by the last wl_run_moe_batched call (h_counts:
+/* Tokens routed to each expert by the last chunk of the last wl_run_moe_batched
+ * call (all of it when n_tokens <= 4096) (h_counts:
  * host array of n_routed_experts; synchronises the device). The grouping the
  * reference keeps in run_moe_batched's where[] (src/glm_layer_runner.cuh:
  * 855-868). */

@@ -201,6 +201,8 @@ struct BatchArgs {
     const float* resid;    // [T][H] or null
     float* out;            // [T][H]
     float* norm;           // [T][H]
+    uint16_t* norm3;       // [T][3][H] bf16 pieces of norm
+    uint16_t* xperm3;      // [T*K][3][H] norm3 rows in compact (expert-major) entry order
     float* logits;         // [T][E]
     int32_t* idx;          // [T][K]
     float* wts;            // [T][K]
@@ -209,9 +211,9 @@ struct BatchArgs {
     uint32_t* lists;       // [E][T] entries (token*K + slot) of expert e, ascending
     uint32_t* ent;         // [T*K] compact index -> token*K + slot (expert-major)
     uint32_t* pos;         // [T*K] token*K + slot -> compact index
-    float* mid;            // [T*K][I] routed SwiGLU outputs, compact rows
+    uint16_t* mid3;        // [T*K][3][I] routed SwiGLU outputs (pieces), compact rows
     float* expout;         // [T*K][H] routed expert outputs, compact rows
-    float* smid;           // [T][SI]
+    uint16_t* smid3;       // [T][3][SI] shared SwiGLU outputs (pieces)
     float* shout;          // [T][H]
 };
 

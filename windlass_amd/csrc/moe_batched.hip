@@ -3,7 +3,8 @@
 // prefill): every expert's weights are streamed once per pass of up to kMT of
 // its tokens instead of once per token.
 //
-//   bnorm    RMSNorm per token
+//   bnorm    RMSNorm per token -> norm (f32, for the router) and norm3 (the
+//            three bf16 pieces the GEMMs read)
 //   broute   router logits, kTB tokens per work-group; norm and logits use the
 //            arithmetic of the decode and routing kernels, so a token's ids
 //            equal the ones wl_run_moe selects for it
@@ -11,69 +12,112 @@
 //   bcount   per expert: its entries (token*K + slot) in ascending order
 //            (wave ballots, deterministic) and their count
 //   bscatter per expert: its compact range (prefix of the counts), ent/pos
-//   bgu      routed gate/up + SwiGLU: unit = (token pass, expert, 4 slices of 64 rows)
-//   bdn      routed down: unit = (token pass, expert, 256 output rows)
-//   bsgu     shared gate/up + SwiGLU: unit = (token pass, 64-row slice)
-//   bsdn     shared down: unit = (token pass, 128 output rows)
+//   bpermute norm3 rows gathered into expert-major order (xperm3)
+//   bup      gate/up + SwiGLU: shared expert (unit = token pass x 64 rows),
+//            routed experts (unit = expert pass x 4 x 64 rows)
+//   bdown    down: shared expert (unit = token pass x 128 rows), routed
+//            experts (unit = expert pass x 512 rows)
 //   bcomb    out[t] = (resid[t] +) sum_k w[t][k] e_k[t] (slot order) + shared[t]
 //
-// The GEMMs put tokens on the MFMA's 16 rows (v_mfma_f32_16x16x32_bf16) and
-// each activation as three bf16 pieces (x = p0 + p1 + p2 to f32 precision)
-// accumulated by three MFMAs; MXFP4 weights are converted exactly to bf16
-// (v_cvt_scalef32_pk_bf16_fp4), bf16 weights are used as they are. The
-// activations of a pass are staged in LDS kKC columns at a time.
+// The GEMMs run each activation as three bf16 pieces (x = p0 + p1 + p2 to f32
+// precision) through v_mfma_f32_16x16x32_bf16; MXFP4 weights are converted
+// exactly to bf16 (v_cvt_scalef32_pk_bf16_fp4), bf16 weights are used as they
+// are. bup and bdown are persistent (one work-group per CU) and share one step
+// pipeline: activations arrive in LDS by DMA, weights two steps ahead in
+// registers.
 #include <hip/hip_runtime.h>
+
+#include <algorithm>
 
 #include "dev_common.h"
 #include "internal.h"
 
 namespace wl {
 
+#define WL_MEM __device__ __forceinline__  // member functions
+
 constexpr uint32_t kMT = 32;         // tokens per pass: two MFMA row blocks of 16
 constexpr uint32_t kKC = 256;        // activation columns staged per step
-constexpr uint32_t kAS = kKC + 8;    // LDS row stride (bf16) of a staged piece
-constexpr uint32_t kALds = 3u * kMT * kAS * 2u;
 constexpr uint32_t kTB = 8;          // tokens per routing work-group
 constexpr uint32_t kRouteGX = 16;    // routing work-groups per token block (router rows r = x + 16 i)
 
-// A operand of token block tb, piece pc: lane (m, g) holds the 8 columns
-// [col, col + 8) of token tb*16 + m (col already includes the lane group's
-// offset).
-WL_DEV bf16x8 afrag(const uint16_t* A, uint32_t pc, uint32_t tb, uint32_t col) {
-    const uint32_t m = threadIdx.x & 15u;
-    return as_bf16x8(*(const u32x4*)(A + (pc * kMT + tb * 16u + m) * kAS + col));
+// Row layout of a pass's staged activations, chosen per pass from its token
+// count nt (wave-uniform):
+//   pieces in rows (nt <= kPR): plane 0, row 4m + pc holds piece pc of token
+//     m (row 4m + 3 unused), so one MFMA covers 4 tokens; the three pieces of
+//     token 4tb + g come out as elements 0..2 of lane group g of block tb and
+//     are summed like the decode kernel's (sum3);
+//   tokens in rows (nt > kPR): plane pc, row m holds piece pc of token m; the
+//     three pieces accumulate into one tile by three MFMAs per 16 tokens.
+// MFMA rows are independent, so rows of absent tokens may hold anything.
+constexpr uint32_t kPR = 8;
+struct PassShape {
+    uint32_t nblk;  // 16-row blocks
+    uint32_t npc;   // planes (MFMAs per block)
+    bool pr;        // pieces in rows
+};
+WL_DEV PassShape pass_shape(uint32_t nt) {
+    return nt <= kPR ? PassShape{cdiv(nt, 4u), 1u, true} : PassShape{cdiv(nt, 16u), 3u, false};
 }
-// acc[tb] += x[tokens of block tb] . b for every live block (3 pieces).
-WL_DEV void mma_blocks(f32x4 (&acc)[2], const uint16_t* A, uint32_t nblk, uint32_t col, bf16x8 b) {
+// The outputs of a tile: lane (n, g) calls f(m, value) for each live token m
+// whose column-n value it holds. The epilogues pass the lane through
+// opaque_lane, so the compiler cannot hoist their per-row addresses out of
+// the step loop (where they would hold registers for the whole kernel).
+WL_DEV uint32_t opaque_lane() {
+    uint32_t l = threadIdx.x & 63u;
+    asm volatile("" : "+v"(l));
+    return l;
+}
+template <class F>
+WL_DEV void tile_each(const f32x4 (&acc)[2], uint32_t nt, bool pr, uint32_t lane, F f) {
+    const uint32_t g = lane >> 4;
 #pragma unroll
     for (uint32_t tb = 0; tb < 2; tb++) {
-        if (tb < nblk) {
+        if (pr) {
+            const uint32_t m = 4u * tb + g;
+            if (m < nt) f(m, sum3(acc[tb]));
+        } else {
 #pragma unroll
-            for (uint32_t pc = 0; pc < 3; pc++) acc[tb] = mma(afrag(A, pc, tb, col), b, acc[tb]);
+            for (uint32_t i = 0; i < 4; i++) {
+                const uint32_t m = tb * 16u + 4u * g + i;
+                if (m < nt) f(m, acc[tb][i]);
+            }
         }
     }
 }
-// SwiGLU epilogue of a gate/up tile: lane (n, g), element i of acc[tb] is
-// token tb*16 + 4g + i; columns n < 8 are gate rows, n + 8 the matching up
-// rows. Calls put(m, n, value) for n < 8 and live tokens.
+// SwiGLU epilogue of a gate/up tile: columns n < 8 are gate rows, n + 8 the
+// matching up rows. Calls put(m, n, value) for n < 8 and live tokens.
 template <class PutF>
-WL_DEV void swiglu_store(const f32x4 (&acc)[2], uint32_t nt, PutF put) {
-    const uint32_t lane = threadIdx.x & 63u, n = lane & 15u, g = lane >> 4;
+WL_DEV void swiglu_store(const f32x4 (&acc)[2], uint32_t nt, bool pr, uint32_t lane, PutF put) {
+    const uint32_t n = lane & 15u, g = lane >> 4;
 #pragma unroll
     for (uint32_t tb = 0; tb < 2; tb++) {
 #pragma unroll
         for (uint32_t i = 0; i < 4; i++) {
-            const float v = acc[tb][i];
+            if (pr && i > 0) continue;
+            const float v = pr ? sum3(acc[tb]) : acc[tb][i];
             const float up = __shfl(v, (lane + 8u) & 63u, 64);
-            const uint32_t m = tb * 16u + 4u * g + i;
+            const uint32_t m = pr ? 4u * tb + g : tb * 16u + 4u * g + i;
             if (n < 8u && m < nt) put(m, n, silu_mul(v, up));
         }
     }
 }
+// The three bf16 pieces of 4 consecutive values at p, p + stride, p + 2 stride.
+WL_DEV void store_pieces4(uint16_t* p, uint32_t stride, const float (&x)[4]) {
+    uint32_t h[4], md[4], l[4];
+#pragma unroll
+    for (int q = 0; q < 4; q++) split3(x[q], h[q], md[q], l[q]);
+    auto pack = [](const uint32_t (&x)[4]) {
+        return (uint64_t)(x[0] | (x[1] << 16)) | ((uint64_t)(x[2] | (x[3] << 16)) << 32);
+    };
+    gst((uint64_t*)p, pack(h));
+    gst((uint64_t*)(p + stride), pack(md));
+    gst((uint64_t*)(p + 2u * stride), pack(l));
+}
 
 // ---- routing ------------------------------------------------------------------
 // RMSNorm of token t = blockIdx.x (norm_rinv / norm_value: the decode kernel's
-// arithmetic) into b.norm.
+// arithmetic) into b.norm, and its three bf16 pieces into b.norm3.
 __global__ void __launch_bounds__(kThreads) bnorm_kernel(const DecodeArgs* __restrict__ pa, const BatchArgs b) {
     const DecodeArgs& a = *pa;
     const uint32_t H = a.H, tid = threadIdx.x, t = blockIdx.x;
@@ -101,6 +145,8 @@ __global__ void __launch_bounds__(kThreads) bnorm_kernel(const DecodeArgs* __res
             o.z = norm_value(xs[2], rinv, a.ln_w != nullptr, ls[2]);
             o.w = norm_value(xs[3], rinv, a.ln_w != nullptr, ls[3]);
             *(__attribute__((address_space(1))) u32x4*)(b.norm + (size_t)t * H + 4 * j) = __builtin_bit_cast(u32x4, o);
+            const float os[4] = {o.x, o.y, o.z, o.w};
+            store_pieces4(b.norm3 + (size_t)t * 3u * H + 4 * j, H, os);
         }
     }
 }
@@ -213,397 +259,681 @@ __global__ void __launch_bounds__(256) bscatter_kernel(const BatchArgs b, uint32
     }
 }
 
-// ---- grouped GEMMs ------------------------------------------------------------
-// Loads complete in issue order, so a wave cannot wait for its activation
-// loads of one step without also waiting for every weight load issued before
-// them. Each step therefore issues, in order: the activations of this step,
-// then the weights of the NEXT step, then consumes the activations (split
-// into LDS) and computes with the weights loaded one step earlier. A step
-// carries many weight tiles per activation stage (kSG slices per unit), so
-// the weights in flight during the wait are large.
-constexpr uint32_t kSG = 4;  // gate/up slices (64 rows each) per unit
+// Permute: the pieces of entry c's token into row c of b.xperm3, so each
+// expert's rows are contiguous for the grouped GEMM (the reference's permute
+// step). Grid-stride over (entry, 16-byte chunk).
+__global__ void __launch_bounds__(256) bpermute_kernel(const BatchArgs b, uint32_t H, uint32_t K) {
+    const uint32_t per = 3u * H / 8u;  // 16-byte chunks per row
+    const uint32_t n = b.T * K;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < (uint64_t)n * per;
+         i += (uint64_t)gridDim.x * blockDim.x) {
+        const uint32_t c = (uint32_t)(i / per), q = (uint32_t)(i % per);
+        const uint32_t t = gld(b.ent + c) / K;
+        const u32x4 v = gld16((const uint8_t*)(b.norm3 + (size_t)t * 3u * H) + 16u * q);
+        *(__attribute__((address_space(1))) u32x4*)((uint8_t*)(b.xperm3 + (size_t)c * 3u * H) + 16u * q) = v;
+    }
+}
 
-// Activation loads of one step (issued before the next step's weights).
-struct AStage {
-    float4 x[kMT * kKC / 4u / kThreads];
+// ---- pass table ----------------------------------------------------------------
+// Pass table of the routed GEMMs, in LDS: the experts' counts and offsets and
+// the exclusive prefix pp of their passes (cdiv(count, kMT)), pp[E] = all
+// passes. Units are numbered densely over the passes that exist (unit u =
+// pass j * parts + part), so the grid-stride loop visits live units only and
+// the passes of one expert sit next to each other.
+struct PassTab {
+    const uint32_t* cnt;
+    const uint32_t* off;
+    const uint32_t* pp;
+    uint32_t n;  // passes
 };
-template <class RowF>
-WL_DEV void a_load(AStage& S, RowF row, uint32_t nt, uint32_t k0, uint32_t kmax) {
-    constexpr uint32_t kPer = kMT * kKC / 4u / kThreads;
-#pragma unroll
-    for (uint32_t i = 0; i < kPer; i++) {
-        const uint32_t it = threadIdx.x + kThreads * i;
-        const uint32_t m = it / (kKC / 4u), c = (it % (kKC / 4u)) * 4u;
-        S.x[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (m < nt && k0 + c < kmax) S.x[i] = __builtin_bit_cast(float4, gld16(row(m) + k0 + c));
-    }
-}
-WL_DEV void a_store(uint16_t* A, const AStage& S) {
-    constexpr uint32_t kPer = kMT * kKC / 4u / kThreads;
-#pragma unroll
-    for (uint32_t i = 0; i < kPer; i++) {
-        const uint32_t it = threadIdx.x + kThreads * i;
-        const uint32_t m = it / (kKC / 4u), c = (it % (kKC / 4u)) * 4u;
-        const float xs[4] = {S.x[i].x, S.x[i].y, S.x[i].z, S.x[i].w};
-        uint32_t h[4], md[4], l[4];
-#pragma unroll
-        for (int q = 0; q < 4; q++) split3(xs[q], h[q], md[q], l[q]);
-        *(uint2*)(A + (0u * kMT + m) * kAS + c) = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
-        *(uint2*)(A + (1u * kMT + m) * kAS + c) = make_uint2(md[0] | (md[1] << 16), md[2] | (md[3] << 16));
-        *(uint2*)(A + (2u * kMT + m) * kAS + c) = make_uint2(l[0] | (l[1] << 16), l[2] | (l[3] << 16));
-    }
-}
-// Two-deep step pipeline over nst steps with weight buffers W0/W1: W0 holds
-// step 0 on entry. step(s, cur, nxt) must issue the activations of step s,
-// then issue(s + 1, nxt), then consume.
-template <class W, class StepF>
-WL_DEV void steps2(uint32_t nst, W& W0, W& W1, StepF step) {
-    uint32_t s = 0;
-#pragma unroll 1
-    for (; s + 2 <= nst; s += 2) {
-        step(s, W0, W1);
-        step(s + 1, W1, W0);
-    }
-    if (s < nst) step(s, W0, W1);
-}
-// An offset no buffer reaches: loads of steps past the end return zeros
-// without a memory access.
-constexpr uint32_t kOOB = 0x7FFFFFF0u;
-
-// Routed gate/up + SwiGLU. Unit u = (pass p, expert e, slice group sg):
-// tokens [p*kMT, +kMT) of expert e, rows of kSG slices [64(kSG sg + i), +64)
-// of gate and up (wave v: tiles 8(kSG sg + i) + v, native gu chunks), K = H in
-// steps of kKC columns (2 k tiles).
-struct GuW {
-    u32x4 w[kSG][2];
-    u32x4 sv[kSG];
-};
-__global__ void __launch_bounds__(kThreads) bgu_kernel(const DecodeArgs* __restrict__ pa, const BatchArgs b) {
-    const DecodeArgs& a = *pa;
-    const uint32_t H = a.H, I = a.I, E = a.E, K = a.K;
-    const uint32_t tid = threadIdx.x, lane = tid & 63u, g = lane >> 4;
-    const uint32_t v = uni(tid >> 6) & 7u;
-    extern __shared__ __align__(16) uint8_t lds[];
-    uint16_t* A = (uint16_t*)lds;
-    uint32_t* tok = (uint32_t*)(lds + kALds);
-    uint32_t* s_cnt = tok + kMT;  // [E] counts, then [E] offsets
-    const NativeLayout NL = NativeLayout::make(H, I);
-    const uint32_t S = I / kSlice, NSG = cdiv(S, kSG), nkg = H / 128, P = cdiv(b.T, kMT);
-    const uint32_t nst = cdiv(H, kKC);
-    const SyncMap SM = SyncMap::make();
+WL_DEV PassTab load_pass_tab(const BatchArgs& b, uint32_t E, uint32_t* s) {
+    const uint32_t tid = threadIdx.x;
+    uint32_t *cnt = s, *off = s + E, *pp = s + 2u * E;
     for (uint32_t f = tid; f < E; f += kThreads) {
-        s_cnt[f] = gld(b.counts + f);
-        s_cnt[E + f] = gld(b.offsets + f);
+        cnt[f] = gld(b.counts + f);
+        off[f] = gld(b.offsets + f);
     }
     lds_barrier();
-    for (uint32_t u = blockIdx.x; u < P * E * NSG; u += gridDim.x) {
-        const uint32_t p = u / (E * NSG), e = (u / NSG) % E, sg = u % NSG;
-        const uint32_t ne = uni(s_cnt[e]);
-        if (p * kMT >= ne) continue;
-        const uint32_t nt = min(kMT, ne - p * kMT), c0 = uni(s_cnt[E + e]) + p * kMT;
-        const uint8_t* blk = uni_ptr(gld(a.slot_tab + e));
-        if (blk == nullptr) {
-            if (tid == 0) raise_error(a.sync, SM, E_NOT_RESIDENT);
-            continue;
+    if (tid < 64u) {
+        const uint32_t per = cdiv(E, 64u), e0 = tid * per;
+        uint32_t mine = 0;
+        for (uint32_t i = 0; i < per; i++)
+            if (e0 + i < E) mine += cdiv(cnt[e0 + i], kMT);
+        uint32_t inc = mine;  // inclusive scan over the wave
+#pragma unroll
+        for (uint32_t o = 1; o < 64u; o <<= 1) {
+            const uint32_t t = __shfl_up(inc, o, 64);
+            if (tid >= o) inc += t;
         }
-        lds_barrier();  // the previous unit's readers of tok are done
-        if (tid < nt) tok[tid] = gld(b.ent + c0 + tid) / K;
-        lds_barrier();
-        const rsrc_t rs = make_rsrc(blk, (uint32_t)NL.total);
-        uint32_t gu_voff[kSG], gus_voff[kSG];
-        bool sl_ok[kSG];
+        uint32_t run = inc - mine;
+        for (uint32_t i = 0; i < per; i++)
+            if (e0 + i < E) {
+                pp[e0 + i] = run;
+                run += cdiv(cnt[e0 + i], kMT);
+            }
+        if (tid == 63u) pp[E] = inc;
+    }
+    lds_barrier();
+    return PassTab{cnt, off, pp, uni(pp[E])};
+}
+// Pass j (< n): its expert (the largest e with pp[e] <= j, which has a pass
+// since pp[e + 1] > j), the pass within the expert, its token count and its
+// first compact entry.
+struct Pass {
+    uint32_t e, nt, c0;
+};
+WL_DEV Pass pass_at(const PassTab& pt, uint32_t E, uint32_t j) {
+    uint32_t lo = 0, hi = E;  // pp[lo] <= j < pp[hi]
+    while (hi - lo > 1u) {
+        const uint32_t mid = (lo + hi) >> 1;
+        if (uni(pt.pp[mid]) <= j) lo = mid;
+        else hi = mid;
+    }
+    const uint32_t p = j - uni(pt.pp[lo]);
+    return Pass{lo, min(kMT, uni(pt.cnt[lo]) - p * kMT), uni(pt.off[lo]) + p * kMT};
+}
+
+// ---- grouped GEMMs ------------------------------------------------------------
+// A unit is one token pass (up to kMT tokens: rows [row0, row0 + nt) of a
+// [rows][3][kdim] bf16 piece array) times a block of weight rows, run in nst
+// steps of kKC columns. A work-group walks its units u = blockIdx.x + G i as
+// one flat sequence of steps z, so the pipeline runs across unit boundaries.
+// Step z:
+//   1. barrier: every wave is done with step z - 1, so LDS slot (z + 2) % 3
+//      (last read in step z - 1) is free;
+//   2. DMA the activations of step z + 2 into that slot (buffer_load ... lds,
+//      no registers), then load the weights of step z + 2 into register
+//      buffer (z + 2) % 3;
+//   3. wait until this wave's loads of step z (issued two steps ago) have
+//      landed, barrier (so every wave's DMAs have);
+//   4. compute step z from slot z % 3 and buffer z % 3; after a unit's last
+//      step, its epilogue.
+// Loads complete in issue order, so 3 is "at most kAfter loads outstanding":
+// the loads of steps z + 1 and z + 2 stay in flight, activations and weights
+// alike (a load under full load takes several microseconds, a step less). The
+// slots are separate LDS objects, so the compiler's own waits for DMA-written
+// LDS stay per slot.
+constexpr uint32_t kRows = 3u * kMT;            // LDS rows of a step
+constexpr uint32_t kRowB = kKC * 2u;            // bytes of a staged row
+constexpr uint32_t kSlotB = kRows * kRowB;      // 48 KB
+constexpr uint32_t kDma = kRows / 2u / kWaves;  // DMA instructions per wave per step (1 KB = 2 rows each)
+constexpr uint32_t kWL = 8;                     // 16-byte weight loads per step
+constexpr uint32_t kSL = 4;                     // 4-byte scale loads per step
+constexpr uint32_t kAfter = 2u * (kDma + kWL + kSL);
+constexpr uint32_t kOOBV = 0x80000000u;  // a lane offset past every piece array (they stay below 2 GB)
+static_assert(kRows % (2u * kWaves) == 0u, "DMA rows must split evenly over the waves");
+static_assert(kAfter < 64u, "vmcnt is 6 bits");
+
+// Slot layout: row R (512 bytes); its 16-byte group p holds columns
+// [k0 + 8 (p ^ (R & 15)), +8) of the step, so the 16 rows an A fragment reads
+// at one column fall in 16 different bank groups. Row R is (token m, piece
+// pc): R = 4m + pc with pieces in rows, R = 32 pc + m with tokens in rows.
+__shared__ __align__(16) uint8_t g_slot0[kSlotB];
+__shared__ __align__(16) uint8_t g_slot1[kSlotB];
+__shared__ __align__(16) uint8_t g_slot2[kSlotB];
+template <int S>
+WL_DEV uint8_t* slot() {
+    return S == 0 ? g_slot0 : S == 1 ? g_slot1 : g_slot2;
+}
+// Lane (m, g) A fragment of row 32 pc + 16 tb + m at 16-byte column group
+// cg = 16 hi + lo: the byte address splits into a uniform part and the lane
+// part m * kRowB + 16 (lo ^ m) (lane_off), which the kernels precompute for
+// the few lo they use.
+WL_DEV uint32_t a_lane_off(uint32_t lo) {
+    const uint32_t m = threadIdx.x & 15u;
+    return m * kRowB + 16u * (lo ^ m);
+}
+WL_DEV bf16x8 afrag(const uint8_t* sl, uint32_t pc, uint32_t tb, uint32_t hi, uint32_t lane_off) {
+    return as_bf16x8(*(const u32x4*)(sl + (pc * 32u + tb * 16u) * kRowB + 256u * hi + lane_off));
+}
+
+// Activation side of a unit: rows [row0, row0 + nt) of a piece array with
+// kdim columns (uniform values; dead: nt = 0).
+struct AStream {
+    rsrc_t rs;
+    uint32_t row0, nt, kdim;
+    bool pr;
+};
+WL_DEV void a_bind(AStream& A, const uint16_t* base, uint64_t bytes, uint32_t row0, uint32_t nt, bool pr,
+                   uint32_t kdim) {
+    A.rs = make_rsrc(base, (uint32_t)bytes);
+    A.row0 = row0;
+    A.nt = nt;
+    A.kdim = kdim;
+    A.pr = pr;
+}
+WL_DEV void a_none(AStream& A) { a_bind(A, nullptr, 0u, 0u, 0u, true, 0u); }
+// DMA instruction k of this wave writes slot rows 2j and 2j + 1 (j = v +
+// kWaves k; lanes 0-31 the first row), each lane 16 bytes: its byte offset in
+// the piece array (kOOBV: row absent, lands as zeros) is computed here rather
+// than kept in registers across the loop.
+template <int S>
+WL_DEV void a_issue(const AStream& A, uint32_t k0) {
+    const uint32_t lane = threadIdx.x & 63u, v = uni(threadIdx.x >> 6);
+#pragma unroll
+    for (uint32_t k = 0; k < kDma; k++) {
+        const uint32_t R = 2u * (v + kWaves * k) + (lane >> 5), cg = (lane & 31u) ^ (R & 15u);
+        const uint32_t m = A.pr ? R >> 2 : R & 31u, pc = A.pr ? R & 3u : R >> 5;
+        const uint32_t voff = (m < A.nt && pc < 3u) ? (((A.row0 + m) * 3u + pc) * A.kdim + 8u * cg) * 2u : kOOBV;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            A.rs, (__attribute__((address_space(3))) void*)(slot<S>() + (v + kWaves * k) * 2u * kRowB), 16u, voff,
+            2u * k0, 0, 0);
+    }
+}
+
+struct WBuf {
+    u32x4 w[kWL];
+    uint32_t s[kSL];
+};
+WL_DEV uint32_t bld4(rsrc_t r, uint32_t voff, uint32_t soff) {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, 0);
+}
+
+// Step 1: this wave's LDS reads are done (lgkmcnt(0)), barrier.
+WL_DEV void free_barrier() {
+    __builtin_amdgcn_s_waitcnt(0xC07Fu);  // lgkmcnt(0); vmcnt, expcnt not waited on
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+}
+// Step 3: s_waitcnt vmcnt(kAfter) (expcnt, lgkmcnt not waited on), barrier.
+WL_DEV void step_barrier() {
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt((kAfter & 15u) | ((kAfter >> 4) << 14) | 0x0F70u);
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Position of a stream in the flat step sequence: my unit i, its step s.
+struct Cursor {
+    uint32_t i, s;
+};
+WL_DEV bool advance(Cursor& c, uint32_t nst) {
+    if (++c.s < nst) return false;
+    c.s = 0;
+    c.i++;
+    return true;
+}
+template <int S, class Kn>
+WL_DEV void pipe_step(Kn& k, AStream& A, const WBuf& cur, WBuf& nxt) {
+    free_barrier();
+    if (advance(k.ca, k.nst)) k.bind_a(k.ca.i, A);
+    a_issue<(S + 2) % 3>(A, k.ca.s * kKC);
+    __builtin_amdgcn_sched_barrier(0);
+    if (advance(k.cw, k.nst)) k.bind_w(k.cw.i);
+    k.issue_w(k.cw.s, nxt);
+    step_barrier();
+    if (k.cc.i < k.nu) {
+        if (k.cc.s == 0u) k.begin(k.cc.i);
+        k.compute(k.cc.s, slot<S>(), cur);
+        if (k.cc.s == k.nst - 1u) k.finish();
+    }
+    advance(k.cc, k.nst);
+}
+// Runs the pipeline over this work-group's nu units. Kn provides nst, nu, the
+// cursors ca/cw/cc and bind_a(i, A) / bind_w(i) (unit i >= nu: nothing to
+// load), issue_w(s, W), begin(i), compute(s, slot, W), finish().
+template <class Kn>
+WL_DEV void run_steps(Kn& k) {
+    if (k.nu == 0u) return;
+    const uint32_t Z = k.nu * k.nst;
+    AStream A;
+    WBuf B0, B1, B2;
+    k.ca = k.cw = k.cc = Cursor{0u, 0u};
+    k.bind_a(0u, A);
+    a_issue<0>(A, 0u);
+    k.bind_w(0u);
+    k.issue_w(0u, B0);
+    if (advance(k.ca, k.nst)) k.bind_a(k.ca.i, A);
+    a_issue<1>(A, k.ca.s * kKC);
+    if (advance(k.cw, k.nst)) k.bind_w(k.cw.i);
+    k.issue_w(k.cw.s, B1);
+#pragma unroll 1
+    for (uint32_t z = 0; z < Z; z += 3u) {
+        pipe_step<0>(k, A, B0, B2);
+        pipe_step<1>(k, A, B1, B0);
+        pipe_step<2>(k, A, B2, B1);
+    }
+}
+
+// Tables every GEMM work-group loads into LDS: the pass table and the
+// layer's expert block pointers.
+WL_DEV const uint8_t* const* load_slot_tab(const DecodeArgs& a, uint32_t E, const uint8_t** s) {
+    for (uint32_t f = threadIdx.x; f < E; f += kThreads) s[f] = gld(a.slot_tab + f);
+    return s;  // visible after the barrier in load_pass_tab
+}
+__host__ __device__ inline size_t gemm_tab_bytes(uint32_t E) { return 8u * E + 4u * (3u * E + 1u); }
+
+// Splits x into its three bf16 pieces at p[0], p[stride], p[2 stride].
+WL_DEV void store3(uint16_t* p, uint32_t stride, float x) {
+    uint32_t h, md, l;
+    split3(x, h, md, l);
+    gst(p, (uint16_t)h);
+    gst(p + stride, (uint16_t)md);
+    gst(p + 2u * stride, (uint16_t)l);
+}
+
+// A unit of a GEMM kernel: shared-expert units first (token passes of the
+// batch), then the routed ones (expert passes of the pass table).
+struct UnitInfo {
+    bool live, sh;
+    uint32_t e, part, nt, row0;
+};
+
+// ---- gate/up + SwiGLU ---------------------------------------------------------
+// Shared unit (pass p, slice j): rows [64j, +64) of the shared gate and up
+// (wave v: tile 8j + v, 8 bf16 per lane per 32-column k tile), K = H.
+// Routed unit (expert pass, slice group sg): rows of kSG slices
+// [64(kSG sg + i), +64) (wave v: tiles 8(kSG sg + i) + v, native gu chunks:
+// 1 KB per 128-column k tile, one scale byte per k tile), K = H.
+// Output: the SwiGLU values as pieces, smid3 / mid3 rows.
+constexpr uint32_t kSG = 4;
+static_assert(kWL == 2u * kSG && kSL == kSG, "gate/up step = 2 k tiles x kSG slices");
+struct UpK {
+    const DecodeArgs& a;
+    const BatchArgs& b;
+    uint32_t H, I, SI, E, K, nkg, nkt, S, NSG, Ssh, Us, nst, nu, v, lane, g;
+    PassTab pt;
+    const uint8_t* const* stab;
+    NativeLayout NL;
+    Cursor ca, cw, cc;
+    // weight stream
+    rsrc_t wrs, srs;
+    bool wsh;
+    uint32_t wpart, wvoff, vgu, vgus, vsh;
+    // A fragment lane offsets: routed k step jj (cg = 16 q + 4 g + jj), shared
+    // k tile k (cg = 4 k + g)
+    uint32_t lo_r[4], lo_s[4];
+    // compute unit
+    UnitInfo cu;
+    PassShape cps;
+    uint32_t cvar;  // compute variant: 0/1 pieces in rows, 1/2 blocks; 2/3 tokens in rows, 1/2 blocks
+    f32x4 acc[kSG][2];
+
+    WL_MEM UnitInfo unit(uint32_t i) const {
+        UnitInfo x{false, false, 0u, 0u, 0u, 0u};
+        if (i >= nu) return x;
+        const uint32_t u = blockIdx.x + gridDim.x * i;
+        x.live = true;
+        if (u < Us) {
+            const uint32_t p = u / Ssh;
+            x.sh = true;
+            x.part = u % Ssh;
+            x.nt = min(kMT, b.T - p * kMT);
+            x.row0 = p * kMT;
+        } else {
+            const Pass ps = pass_at(pt, E, (u - Us) / NSG);
+            x.part = (u - Us) % NSG;
+            x.e = ps.e;
+            x.nt = ps.nt;
+            x.row0 = ps.c0;
+        }
+        return x;
+    }
+    WL_MEM void bind_a(uint32_t i, AStream& A) const {
+        const UnitInfo x = unit(i);
+        if (!x.live) return a_none(A);
+        const bool pr = pass_shape(x.nt).pr;
+        if (x.sh) a_bind(A, b.norm3, (uint64_t)b.T * 6u * H, x.row0, x.nt, pr, H);
+        else a_bind(A, b.xperm3, (uint64_t)b.T * K * 6u * H, x.row0, x.nt, pr, H);
+    }
+    WL_MEM void bind_w(uint32_t i) {
+        const UnitInfo x = unit(i);
+        wsh = x.sh;
+        wpart = x.part;
+        const NativeShared NS = NativeShared::make(H, SI);
+        const uint8_t* blk = x.live && !x.sh ? uni_ptr(stab[x.e]) : nullptr;
+        wrs = !x.live ? make_rsrc(nullptr, 0u)
+              : x.sh  ? make_rsrc(a.sh_native + NS.sgu, (uint32_t)(NS.sdn - NS.sgu))
+                      : make_rsrc(blk, blk ? (uint32_t)NL.total : 0u);
+        srs = x.live && !x.sh ? wrs : make_rsrc(nullptr, 0u);
+        wvoff = x.sh ? vsh : vgu;  // chosen here, not per load (see DownK::bind_w)
+    }
+    WL_MEM void issue_w(uint32_t s, WBuf& W) const {
+#pragma unroll
+        for (uint32_t k = 0; k < kWL; k++) {
+            const uint32_t sl = min(wpart * kSG + k / 2u, S - 1u);
+            const uint32_t ro = sl * 8u * nkg * 1024u + min(2u * s + k % 2u, nkg - 1u) * 1024u;
+            const uint32_t so = wpart * 8u * nkt * 1024u + min(8u * s + k, nkt - 1u) * 1024u;
+            W.w[k] = bld16_nt(wrs, wvoff, wsh ? so : ro);
+        }
+        const uint32_t kt = min(2u * s, nkg - 1u);
+#pragma unroll
+        for (uint32_t i = 0; i < kSL; i++) {
+            const uint32_t sl = min(wpart * kSG + i, S - 1u);
+            W.s[i] = bld4(srs, vgus, sl * 8u * cdiv(nkg, 16u) * 1024u + (kt / 16u) * 1024u + 4u * ((kt % 16u) / 4u));
+        }
+    }
+    WL_MEM void begin(uint32_t i) {
+        cu = unit(i);
+        cps = pass_shape(cu.nt);
+        cvar = (cps.pr ? 0u : 2u) + cps.nblk - 1u;
+        if (!cu.sh && stab[cu.e] == nullptr && threadIdx.x == 0) raise_error(a.sync, SyncMap::make(), E_NOT_RESIDENT);
+#pragma unroll
+        for (uint32_t j = 0; j < kSG; j++) acc[j][0] = acc[j][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    // One step for a pass of NB row blocks and NP planes (shape-specialised
+    // so the inner loops carry no branches).
+    template <uint32_t NB, uint32_t NP>
+    WL_MEM void comp_shared(uint32_t s, const uint8_t* sl, const WBuf& W) {
+#pragma unroll
+        for (uint32_t k = 0; k < 8u; k++) {
+            const u32x4 z = {0u, 0u, 0u, 0u};
+            const bf16x8 bw = as_bf16x8(8u * s + k < nkt ? W.w[k] : z);
+#pragma unroll
+            for (uint32_t tb = 0; tb < NB; tb++)
+#pragma unroll
+                for (uint32_t pc = 0; pc < NP; pc++)
+                    acc[0][tb] = mma(afrag(sl, pc, tb, k / 4u, lo_s[k % 4u]), bw, acc[0][tb]);
+        }
+    }
+    template <uint32_t NB, uint32_t NP>
+    WL_MEM void comp_routed(uint32_t s, const uint8_t* sl, const WBuf& W) {
+#pragma unroll
+        for (uint32_t q = 0; q < 2; q++) {
+            const uint32_t kt = 2u * s + q;
+            float sc[kSG];
+#pragma unroll
+            for (uint32_t i = 0; i < kSG; i++) sc[i] = kt < nkg ? e8m0f((W.s[i] >> (8u * (kt % 4u))) & 0xFFu) : 0.f;
+#pragma unroll
+            for (uint32_t jj = 0; jj < 4; jj++) {
+                bf16x8 bw[kSG];
+#pragma unroll
+                for (uint32_t i = 0; i < kSG; i++) bw[i] = fp4x8_bf16(W.w[2u * i + q][jj], sc[i]);
+                // the activation fragments of this k step (columns q * 128 +
+                // 32 g + 8 jj), one plane at a time, shared by the kSG slices
+#pragma unroll
+                for (uint32_t pc = 0; pc < NP; pc++) {
+                    bf16x8 af[NB];
+#pragma unroll
+                    for (uint32_t tb = 0; tb < NB; tb++) af[tb] = afrag(sl, pc, tb, q, lo_r[jj]);
+#pragma unroll
+                    for (uint32_t i = 0; i < kSG; i++)
+#pragma unroll
+                        for (uint32_t tb = 0; tb < NB; tb++) acc[i][tb] = mma(af[tb], bw[i], acc[i][tb]);
+                }
+                __builtin_amdgcn_sched_barrier(0);  // keeps one k step's operands live at a time
+            }
+        }
+    }
+    WL_MEM void compute(uint32_t s, const uint8_t* sl, const WBuf& W) {
+        switch (cvar) {
+            case 0: return cu.sh ? comp_shared<1, 1>(s, sl, W) : comp_routed<1, 1>(s, sl, W);
+            case 1: return cu.sh ? comp_shared<2, 1>(s, sl, W) : comp_routed<2, 1>(s, sl, W);
+            case 2: return cu.sh ? comp_shared<1, 3>(s, sl, W) : comp_routed<1, 3>(s, sl, W);
+            default: return cu.sh ? comp_shared<2, 3>(s, sl, W) : comp_routed<2, 3>(s, sl, W);
+        }
+    }
+    WL_MEM void finish() {
+        const uint32_t ln = opaque_lane();
+        if (cu.sh) {
+            swiglu_store(acc[0], cu.nt, cps.pr, ln, [&](uint32_t m, uint32_t n, float x) {
+                store3(b.smid3 + (size_t)(cu.row0 + m) * 3u * SI + cu.part * kSlice + v * 8u + n, SI, x);
+            });
+            return;
+        }
 #pragma unroll
         for (uint32_t i = 0; i < kSG; i++) {
-            const uint32_t sl = min(sg * kSG + i, S - 1u);
-            sl_ok[i] = sg * kSG + i < S;
-            const uint32_t tile = sl * (kSlice / 8u) + v;
-            gu_voff[i] = (uint32_t)NL.gu + tile * nkg * 1024u + 16u * lane;
-            gus_voff[i] = (uint32_t)NL.gus + tile * cdiv(nkg, 16u) * 1024u + 16u * lane;
-        }
-        const uint32_t nblk = cdiv(nt, 16u);
-        f32x4 acc[kSG][2];
-#pragma unroll
-        for (uint32_t i = 0; i < kSG; i++) acc[i][0] = acc[i][1] = f32x4{0.f, 0.f, 0.f, 0.f};
-        auto row = [&](uint32_t m) { return b.norm + (size_t)tok[m] * H; };
-        auto issue = [&](uint32_t s, GuW& W) {
-            const bool live = s < nst;
-            const uint32_t kt0 = min(s * 2u, nkg - 1u), kt1 = min(s * 2u + 1u, nkg - 1u);
-#pragma unroll
-            for (uint32_t i = 0; i < kSG; i++) {
-                W.w[i][0] = bld16_nt(rs, gu_voff[i], live ? kt0 * 1024u : kOOB);
-                W.w[i][1] = bld16_nt(rs, gu_voff[i], live ? kt1 * 1024u : kOOB);
-                W.sv[i] = bld16_nt(rs, gus_voff[i], live ? (kt0 / 16u) * 1024u : kOOB);
-            }
-        };
-        GuW W0, W1;
-        issue(0, W0);
-        steps2(nst, W0, W1, [&](uint32_t s, const GuW& cur, GuW& nxt) {
-            AStage as;
-            a_load(as, row, nt, s * kKC, H);
-            issue(s + 1u, nxt);
-            lds_barrier();  // the previous step's readers of A are done
-            a_store(A, as);
-            lds_barrier();
-#pragma unroll
-            for (uint32_t q = 0; q < 2; q++) {
-                const uint32_t kt = s * 2u + q, o = kt % 16u;
-                float sc[kSG];
-#pragma unroll
-                for (uint32_t i = 0; i < kSG; i++) {
-                    const u32x4 sv = cur.sv[i];
-                    const uint32_t sw = (o / 4u == 0u) ? sv.x : (o / 4u == 1u) ? sv.y : (o / 4u == 2u) ? sv.z : sv.w;
-                    sc[i] = kt < nkg ? e8m0f((sw >> (8u * (o % 4u))) & 0xFFu) : 0.f;
-                }
-#pragma unroll
-                for (uint32_t jj = 0; jj < 4; jj++) {
-                    // the activation fragments of this k step, shared by the kSG slices
-                    const uint32_t col = q * 128u + 32u * g + 8u * jj;
-                    bf16x8 af[2][3];
-#pragma unroll
-                    for (uint32_t tb = 0; tb < 2; tb++)
-#pragma unroll
-                        for (uint32_t pc = 0; pc < 3; pc++) af[tb][pc] = afrag(A, pc, tb, col);
-#pragma unroll
-                    for (uint32_t i = 0; i < kSG; i++) {
-                        const bf16x8 bw = fp4x8_bf16(cur.w[i][q][jj], sc[i]);
-#pragma unroll
-                        for (uint32_t tb = 0; tb < 2; tb++) {
-                            if (tb < nblk) {
-#pragma unroll
-                                for (uint32_t pc = 0; pc < 3; pc++) acc[i][tb] = mma(af[tb][pc], bw, acc[i][tb]);
-                            }
-                        }
-                    }
-                }
-            }
-        });
-#pragma unroll
-        for (uint32_t i = 0; i < kSG; i++) {
-            if (!sl_ok[i]) continue;
-            const uint32_t sl = sg * kSG + i;
-            swiglu_store(acc[i], nt, [&](uint32_t m, uint32_t n, float x) {
-                gst(b.mid + (size_t)(c0 + m) * I + sl * kSlice + v * 8u + n, x);
+            const uint32_t sl = cu.part * kSG + i;
+            if (sl >= S) continue;
+            swiglu_store(acc[i], cu.nt, cps.pr, ln, [&](uint32_t m, uint32_t n, float x) {
+                store3(b.mid3 + (size_t)(cu.row0 + m) * 3u * I + sl * kSlice + v * 8u + n, I, x);
             });
         }
     }
+};
+__global__ void __launch_bounds__(kThreads) bup_kernel(const DecodeArgs* __restrict__ pa, const BatchArgs b) {
+    const DecodeArgs& a = *pa;
+    extern __shared__ __align__(16) uint8_t dyn[];
+    const uint32_t H = a.H, I = a.I, E = a.E;
+    const uint8_t* const* stab = load_slot_tab(a, E, (const uint8_t**)dyn);
+    const PassTab pt = load_pass_tab(b, E, (uint32_t*)(dyn + 8u * E));
+    UpK k{a, b};
+    k.H = H;
+    k.I = I;
+    k.SI = a.SI;
+    k.E = E;
+    k.K = a.K;
+    k.nkg = H / 128u;
+    k.nkt = H / 32u;
+    k.S = I / kSlice;
+    k.NSG = cdiv(k.S, kSG);
+    k.Ssh = a.SI / kSlice;
+    k.Us = cdiv(b.T, kMT) * k.Ssh;
+    k.nst = cdiv(H, kKC);
+    const uint32_t U = k.Us + pt.n * k.NSG;
+    k.nu = U > blockIdx.x ? cdiv(U - blockIdx.x, gridDim.x) : 0u;
+    k.lane = threadIdx.x & 63u;
+    k.g = k.lane >> 4;
+    k.v = uni(threadIdx.x >> 6);
+    k.pt = pt;
+    k.stab = stab;
+    k.NL = NativeLayout::make(H, I);
+    k.vgu = (uint32_t)k.NL.gu + k.v * k.nkg * 1024u + 16u * k.lane;
+    k.vgus = (uint32_t)k.NL.gus + k.v * cdiv(k.nkg, 16u) * 1024u + 16u * k.lane;
+    k.vsh = k.v * k.nkt * 1024u + 16u * k.lane;
+#pragma unroll
+    for (uint32_t j = 0; j < 4; j++) {
+        k.lo_r[j] = a_lane_off(4u * k.g + j);
+        k.lo_s[j] = a_lane_off(4u * j + k.g);
+    }
+    run_steps(k);
 }
 
-struct DnW {
-    u32x4 w[4];
-    u32x4 sv[4];
-};
-// Routed down. Unit u = (pass p, expert e, row block rb): tokens as in
-// bgu_kernel, output rows [256rb, 256rb + 256) (wave v: row pair q = 8rb + v,
-// rows 32q..32q+32, native dn chunks), K = I.
-__global__ void __launch_bounds__(kThreads) bdn_kernel(const DecodeArgs* __restrict__ pa, const BatchArgs b) {
-    const DecodeArgs& a = *pa;
-    const uint32_t H = a.H, I = a.I, E = a.E;
-    const uint32_t tid = threadIdx.x, lane = tid & 63u, n = lane & 15u, g = lane >> 4;
-    const uint32_t v = uni(tid >> 6) & 7u;
-    extern __shared__ __align__(16) uint8_t lds[];
-    uint16_t* A = (uint16_t*)lds;
-    uint32_t* s_cnt = (uint32_t*)(lds + kALds) + kMT;  // [E] counts, then [E] offsets
-    const NativeLayout NL = NativeLayout::make(H, I);
-    const uint32_t nq = H / 32u, RB = cdiv(nq, 8u), P = cdiv(b.T, kMT);
-    for (uint32_t f = tid; f < E; f += kThreads) {
-        s_cnt[f] = gld(b.counts + f);
-        s_cnt[E + f] = gld(b.offsets + f);
+// ---- down ---------------------------------------------------------------------
+// Shared unit (pass p, row block rb): output rows r0 = 128 rb + 16 v .. +16
+// per wave; native sdn: 16 bytes (8 bf16 columns of tile T) per row, lane
+// (n, g) of k step ks reads tile 4 ks + g of row r0 + n. K = SI.
+// Routed unit (expert pass, row block rb): wave v owns row pairs
+// q = 16 rb + 2v + h (h = 0, 1; 32 rows each, native dn chunks: 1 KB per
+// 64-column slice, v_permlane32_swap pairs the halves), K = I.
+// Output: f32 rows of shout / expout.
+static_assert(kWL == 8u && kSL == 4u, "down step = 4 slices x 2 row pairs");
+struct DownK {
+    const DecodeArgs& a;
+    const BatchArgs& b;
+    uint32_t H, I, SI, E, nq, NS, nks, RBs, RBr, Us, nst, nu, v, lane, n, g;
+    PassTab pt;
+    const uint8_t* const* stab;
+    NativeLayout NL;
+    Cursor ca, cw, cc;
+    rsrc_t wrs, srs;
+    bool wsh;
+    uint32_t wpart, wvoff, vdn, vdns;
+    // A fragment lane offsets: routed slice s4, half f (cg = 8 s4 + 4 (g & 1)
+    // + (g >> 1) + 2 f: lo_r[s4 & 1][f], hi = s4 >> 1); shared k tile k
+    // (cg = 4 k + g)
+    uint32_t lo_r[2][2], lo_s[4];
+    UnitInfo cu;
+    PassShape cps;
+    uint32_t cvar;  // compute variant: 0/1 pieces in rows, 1/2 blocks; 2/3 tokens in rows, 1/2 blocks
+    f32x4 d[2][2][2];  // [row pair h][x rows / y rows][row block tb]
+
+    WL_MEM UnitInfo unit(uint32_t i) const {
+        UnitInfo x{false, false, 0u, 0u, 0u, 0u};
+        if (i >= nu) return x;
+        const uint32_t u = blockIdx.x + gridDim.x * i;
+        x.live = true;
+        if (u < Us) {
+            const uint32_t p = u / RBs;
+            x.sh = true;
+            x.part = u % RBs;
+            x.nt = min(kMT, b.T - p * kMT);
+            x.row0 = p * kMT;
+        } else {
+            const Pass ps = pass_at(pt, E, (u - Us) / RBr);
+            x.part = (u - Us) % RBr;
+            x.e = ps.e;
+            x.nt = ps.nt;
+            x.row0 = ps.c0;
+        }
+        return x;
     }
-    lds_barrier();
-    for (uint32_t u = blockIdx.x; u < P * E * RB; u += gridDim.x) {
-        const uint32_t p = u / (E * RB), e = (u / RB) % E, rb = u % RB;
-        const uint32_t ne = uni(s_cnt[e]);
-        if (p * kMT >= ne) continue;
-        const uint32_t nt = min(kMT, ne - p * kMT), c0 = uni(s_cnt[E + e]) + p * kMT;
-        const uint8_t* blk = uni_ptr(gld(a.slot_tab + e));
-        if (blk == nullptr) continue;  // reported by bgu_kernel
-        const rsrc_t rs = make_rsrc(blk, (uint32_t)NL.total);
-        const uint32_t q = rb * 8u + v;
-        const bool qv = q < nq;
-        const uint32_t qq = qv ? q : nq - 1u;
-        const uint32_t nblk = cdiv(nt, 16u);
-        f32x4 d0[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
-        f32x4 d1[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
-        auto row = [&](uint32_t m) { return b.mid + (size_t)(c0 + m) * I; };
-        const uint32_t ca = 32u * (g & 1u) + 8u * (g >> 1);  // this lane group's slice columns (the swap order)
-        const uint32_t nst = cdiv(I, kKC), NS = I / kSlice;
-        auto issue = [&](uint32_t st, DnW& W) {
-            const bool live = st < nst;
+    WL_MEM void bind_a(uint32_t i, AStream& A) const {
+        const UnitInfo x = unit(i);
+        if (!x.live) return a_none(A);
+        const bool pr = pass_shape(x.nt).pr;
+        if (x.sh) a_bind(A, b.smid3, (uint64_t)b.T * 6u * SI, x.row0, x.nt, pr, SI);
+        else a_bind(A, b.mid3, (uint64_t)b.T * a.K * 6u * I, x.row0, x.nt, pr, I);
+    }
+    WL_MEM void bind_w(uint32_t i) {
+        const UnitInfo x = unit(i);
+        wsh = x.sh;
+        wpart = x.part;
+        const NativeShared NSh = NativeShared::make(H, SI);
+        const uint8_t* blk = x.live && !x.sh ? uni_ptr(stab[x.e]) : nullptr;
+        wrs = !x.live ? make_rsrc(nullptr, 0u)
+              : x.sh  ? make_rsrc(a.sh_native + NSh.sdn, (uint32_t)(NSh.total - NSh.sdn))
+                      : make_rsrc(blk, blk ? (uint32_t)NL.total : 0u);
+        srs = x.live && !x.sh ? wrs : make_rsrc(nullptr, 0u);
+        // the lane's weight offset base, chosen here (a select between two
+        // members at each load would take the members' addresses)
+        wvoff = x.sh ? (g * H + min(x.part * 128u + 16u * v + n, H - 1u)) * 16u : vdn;
+    }
+    WL_MEM void issue_w(uint32_t st, WBuf& W) const {
+        const uint32_t q0 = wpart * 16u + 2u * v;
 #pragma unroll
-            for (uint32_t s4 = 0; s4 < 4; s4++) {
-                const uint32_t j = min(st * 4u + s4, NS - 1u);
-                W.w[s4] = bld16_nt(rs, (uint32_t)NL.dn + j * nq * 1024u + 16u * lane, live ? qq * 1024u : kOOB);
-                W.sv[s4] = bld16_nt(rs, (uint32_t)NL.dns + j * cdiv(nq, 16u) * 1024u + 16u * lane,
-                                    live ? (qq / 16u) * 1024u : kOOB);
-            }
-        };
-        DnW W0, W1;
-        issue(0, W0);
-        steps2(nst, W0, W1, [&](uint32_t st, const DnW& cur, DnW& nxt) {
-            AStage as;
-            a_load(as, row, nt, st * kKC, I);
-            issue(st + 1u, nxt);
-            lds_barrier();
-            a_store(A, as);
-            lds_barrier();
+        for (uint32_t k = 0; k < kWL; k++) {
+            const uint32_t j = min(st * 4u + k / 2u, NS - 1u), q = min(q0 + k % 2u, nq - 1u);
+            const uint32_t ro = (j * nq + q) * 1024u;
+            const uint32_t so = min(8u * st + k, nks - 1u) * 4u * H * 16u;
+            W.w[k] = bld16_nt(wrs, wvoff, wsh ? so : ro);
+        }
+        const uint32_t qs = min(q0, nq - 1u);
 #pragma unroll
-            for (uint32_t s4 = 0; s4 < 4; s4++) {
-                const bool valid = st * 4u + s4 < NS;
-                const uint32_t o = qq % 16u;
-                const u32x4 sv = cur.sv[s4];
-                const uint32_t sw = (o / 4u == 0u) ? sv.x : (o / 4u == 1u) ? sv.y : (o / 4u == 2u) ? sv.z : sv.w;
-                const uint32_t sbyte = (sw >> (8u * (o % 4u))) & 0xFFu;
-                uint32_t sx, sy, x01, y01, x23, y23;
+        for (uint32_t i = 0; i < kSL; i++) {
+            const uint32_t j = min(st * 4u + i, NS - 1u);
+            W.s[i] = bld4(srs, vdns, (j * cdiv(nq, 16u) + qs / 16u) * 1024u + 4u * ((qs % 16u) / 4u));
+        }
+    }
+    WL_MEM void begin(uint32_t i) {
+        cu = unit(i);
+        cps = pass_shape(cu.nt);
+        cvar = (cps.pr ? 0u : 2u) + cps.nblk - 1u;
+#pragma unroll
+        for (uint32_t h = 0; h < 2; h++)
+#pragma unroll
+            for (uint32_t xy = 0; xy < 2; xy++) d[h][xy][0] = d[h][xy][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    template <uint32_t NB, uint32_t NP>
+    WL_MEM void comp_shared(uint32_t st, const uint8_t* sl, const WBuf& W) {
+#pragma unroll
+        for (uint32_t k = 0; k < 8u; k++) {
+            const u32x4 z = {0u, 0u, 0u, 0u};
+            const bf16x8 bw = as_bf16x8(8u * st + k < nks ? W.w[k] : z);
+#pragma unroll
+            for (uint32_t tb = 0; tb < NB; tb++)
+#pragma unroll
+                for (uint32_t pc = 0; pc < NP; pc++)
+                    d[0][0][tb] = mma(afrag(sl, pc, tb, k / 4u, lo_s[k % 4u]), bw, d[0][0][tb]);
+        }
+    }
+    template <uint32_t NB, uint32_t NP>
+    WL_MEM void comp_routed(uint32_t st, const uint8_t* sl, const WBuf& W) {
+        const uint32_t q0 = min(cu.part * 16u + 2u * v, nq - 1u);
+#pragma unroll
+        for (uint32_t s4 = 0; s4 < 4; s4++) {
+            const bool valid = st * 4u + s4 < NS;
+            float scx[2], scy[2];
+#pragma unroll
+            for (uint32_t h = 0; h < 2; h++) {
+                const uint32_t sbyte = (W.s[s4] >> (8u * ((q0 + h) % 4u))) & 0xFFu;
+                uint32_t sx, sy;
                 swap32(sbyte, sbyte, sx, sy);
-                swap32(cur.w[s4][0], cur.w[s4][1], x01, y01);
-                swap32(cur.w[s4][2], cur.w[s4][3], x23, y23);
-                const float scx = valid ? e8m0f(sx) : 0.f, scy = valid ? e8m0f(sy) : 0.f;
-                const uint32_t col = s4 * kSlice + ca;
-                const bf16x8 bx01 = fp4x8_bf16(x01, scx), bx23 = fp4x8_bf16(x23, scx);
-                const bf16x8 by01 = fp4x8_bf16(y01, scy), by23 = fp4x8_bf16(y23, scy);
+                scx[h] = valid ? e8m0f(sx) : 0.f;
+                scy[h] = valid ? e8m0f(sy) : 0.f;
+            }
+            // Column half f of the slice: lane group g's columns s4 * 64 +
+            // 32 (g & 1) + 8 (g >> 1) + 16 f (the swap order), from dwords
+            // 2f, 2f + 1 of each row pair's chunk.
 #pragma unroll
-                for (uint32_t tb = 0; tb < 2; tb++) {
-                    if (tb < nblk) {
+            for (uint32_t f = 0; f < 2; f++) {
+                bf16x8 bx[2], by[2];
 #pragma unroll
-                        for (uint32_t pc = 0; pc < 3; pc++) {
-                            const bf16x8 a0 = afrag(A, pc, tb, col), a1 = afrag(A, pc, tb, col + 16u);
-                            d0[tb] = mma(a0, bx01, d0[tb]);
-                            d0[tb] = mma(a1, bx23, d0[tb]);
-                            d1[tb] = mma(a0, by01, d1[tb]);
-                            d1[tb] = mma(a1, by23, d1[tb]);
+                for (uint32_t h = 0; h < 2; h++) {
+                    const u32x4 w = W.w[2u * s4 + h];
+                    uint32_t x, y;
+                    swap32(w[2u * f], w[2u * f + 1u], x, y);
+                    bx[h] = fp4x8_bf16(x, scx[h]);
+                    by[h] = fp4x8_bf16(y, scy[h]);
+                }
+#pragma unroll
+                for (uint32_t tb = 0; tb < NB; tb++) {
+#pragma unroll
+                    for (uint32_t pc = 0; pc < NP; pc++) {
+                        const bf16x8 af = afrag(sl, pc, tb, s4 / 2u, lo_r[s4 % 2u][f]);
+#pragma unroll
+                        for (uint32_t h = 0; h < 2; h++) {
+                            d[h][0][tb] = mma(af, bx[h], d[h][0][tb]);
+                            d[h][1][tb] = mma(af, by[h], d[h][1][tb]);
                         }
                     }
                 }
             }
-        });
-        if (qv) {
-#pragma unroll
-            for (uint32_t tb = 0; tb < 2; tb++) {
-#pragma unroll
-                for (uint32_t i = 0; i < 4; i++) {
-                    const uint32_t m = tb * 16u + 4u * g + i;
-                    if (m < nt) {
-                        float* o = b.expout + (size_t)(c0 + m) * H + 32u * q;
-                        gst(o + n, d0[tb][i]);
-                        gst(o + 16u + n, d1[tb][i]);
-                    }
-                }
-            }
+            __builtin_amdgcn_sched_barrier(0);  // keeps one slice's operands live at a time
         }
-        lds_barrier();
     }
-}
-
-struct BfW {
-    u32x4 w[8];
+    WL_MEM void compute(uint32_t st, const uint8_t* sl, const WBuf& W) {
+        switch (cvar) {
+            case 0: return cu.sh ? comp_shared<1, 1>(st, sl, W) : comp_routed<1, 1>(st, sl, W);
+            case 1: return cu.sh ? comp_shared<2, 1>(st, sl, W) : comp_routed<2, 1>(st, sl, W);
+            case 2: return cu.sh ? comp_shared<1, 3>(st, sl, W) : comp_routed<1, 3>(st, sl, W);
+            default: return cu.sh ? comp_shared<2, 3>(st, sl, W) : comp_routed<2, 3>(st, sl, W);
+        }
+    }
+    WL_MEM void finish() {
+        const uint32_t ln = opaque_lane(), nn = ln & 15u;
+        if (cu.sh) {
+            const uint32_t r = cu.part * 128u + 16u * v + nn;
+            if (r < H)
+                tile_each(d[0][0], cu.nt, cps.pr, ln,
+                          [&](uint32_t m, float x) { gst(b.shout + (size_t)(cu.row0 + m) * H + r, x); });
+            return;
+        }
+#pragma unroll
+        for (uint32_t h = 0; h < 2; h++) {
+            const uint32_t q = cu.part * 16u + 2u * v + h;
+            if (q >= nq) continue;
+            float* o = b.expout + (size_t)cu.row0 * H + 32u * q + nn;
+            tile_each(d[h][0], cu.nt, cps.pr, ln, [&](uint32_t m, float x) { gst(o + (size_t)m * H, x); });
+            tile_each(d[h][1], cu.nt, cps.pr, ln, [&](uint32_t m, float x) { gst(o + (size_t)m * H + 16u, x); });
+        }
+    }
 };
-// Shared gate/up + SwiGLU. Unit u = (pass p, slice j): tokens [p*kMT, +kMT),
-// rows [64j, 64j+64) of the shared gate and up (wave v: tile 8j + v, native
-// sgu chunks: 8 bf16 per lane), K = H.
-__global__ void __launch_bounds__(kThreads) bsgu_kernel(const DecodeArgs* __restrict__ pa, const BatchArgs b) {
+__global__ void __launch_bounds__(kThreads) bdown_kernel(const DecodeArgs* __restrict__ pa, const BatchArgs b) {
     const DecodeArgs& a = *pa;
-    const uint32_t H = a.H, SI = a.SI;
-    const uint32_t tid = threadIdx.x, lane = tid & 63u, g = lane >> 4;
-    const uint32_t v = uni(tid >> 6) & 7u;
-    extern __shared__ __align__(16) uint8_t lds[];
-    uint16_t* A = (uint16_t*)lds;
-    const NativeShared NS = NativeShared::make(H, SI);
-    const uint32_t S = SI / kSlice, nkt = H / 32u, P = cdiv(b.T, kMT);
-    const rsrc_t rs = make_rsrc(a.sh_native + NS.sgu, (uint32_t)(NS.sdn - NS.sgu));
-    for (uint32_t u = blockIdx.x; u < P * S; u += gridDim.x) {
-        const uint32_t p = u / S, j = u % S;
-        const uint32_t nt = min(kMT, b.T - p * kMT), t0 = p * kMT;
-        const uint32_t tile = j * (kSlice / 8u) + v;
-        const uint32_t voff = tile * nkt * 1024u + 16u * lane;
-        const uint32_t nblk = cdiv(nt, 16u);
-        f32x4 acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
-        auto row = [&](uint32_t m) { return b.norm + (size_t)(t0 + m) * H; };
-        const uint32_t nst = cdiv(H, kKC);
-        auto issue = [&](uint32_t st, BfW& W) {
-            const bool live = st < nst;
+    extern __shared__ __align__(16) uint8_t dyn[];
+    const uint32_t H = a.H, I = a.I, E = a.E;
+    const uint8_t* const* stab = load_slot_tab(a, E, (const uint8_t**)dyn);
+    const PassTab pt = load_pass_tab(b, E, (uint32_t*)(dyn + 8u * E));
+    DownK k{a, b};
+    k.H = H;
+    k.I = I;
+    k.SI = a.SI;
+    k.E = E;
+    k.nq = H / 32u;
+    k.NS = I / kSlice;
+    k.nks = a.SI / 32u;
+    k.RBs = cdiv(H, 128u);
+    k.RBr = cdiv(k.nq, 16u);
+    k.Us = cdiv(b.T, kMT) * k.RBs;
+    k.nst = cdiv(max(I, a.SI), kKC);  // the shorter kind's extra steps are masked
+    const uint32_t U = k.Us + pt.n * k.RBr;
+    k.nu = U > blockIdx.x ? cdiv(U - blockIdx.x, gridDim.x) : 0u;
+    k.lane = threadIdx.x & 63u;
+    k.n = k.lane & 15u;
+    k.g = k.lane >> 4;
+    k.v = uni(threadIdx.x >> 6);
+    k.pt = pt;
+    k.stab = stab;
+    k.NL = NativeLayout::make(H, I);
+    k.vdn = (uint32_t)k.NL.dn + 16u * k.lane;
+    k.vdns = (uint32_t)k.NL.dns + 16u * k.lane;
 #pragma unroll
-            for (uint32_t s8 = 0; s8 < 8; s8++)
-                W.w[s8] = bld16_nt(rs, voff, live ? min(st * 8u + s8, nkt - 1u) * 1024u : kOOB);
-        };
-        BfW W0, W1;
-        issue(0, W0);
-        steps2(nst, W0, W1, [&](uint32_t st, const BfW& cur, BfW& nxt) {
-            AStage as;
-            a_load(as, row, nt, st * kKC, H);
-            issue(st + 1u, nxt);
-            lds_barrier();
-            a_store(A, as);
-            lds_barrier();
-#pragma unroll
-            for (uint32_t s8 = 0; s8 < 8; s8++) {
-                const u32x4 z = {0u, 0u, 0u, 0u};
-                mma_blocks(acc, A, nblk, s8 * 32u + 8u * g, as_bf16x8(st * 8u + s8 < nkt ? cur.w[s8] : z));
-            }
-        });
-        swiglu_store(acc, nt, [&](uint32_t m, uint32_t n, float x) {
-            gst(b.smid + (size_t)(t0 + m) * SI + j * kSlice + v * 8u + n, x);
-        });
-        lds_barrier();
+    for (uint32_t j = 0; j < 4; j++) {
+        k.lo_r[j / 2u][j % 2u] = a_lane_off(8u * (j / 2u) + 4u * (k.g & 1u) + (k.g >> 1) + 2u * (j % 2u));
+        k.lo_s[j] = a_lane_off(4u * j + k.g);
     }
-}
-
-// Shared down. Unit u = (pass p, row block rb): output rows [128rb, +128)
-// (wave v: rows r0 = 128rb + 16v .. +16), K = SI. Native sdn: 16 bytes (8 bf16
-// columns of tile T) per row; lane (n, g) of k step s reads tile 4s + g of
-// row r0 + n.
-__global__ void __launch_bounds__(kThreads) bsdn_kernel(const DecodeArgs* __restrict__ pa, const BatchArgs b) {
-    const DecodeArgs& a = *pa;
-    const uint32_t H = a.H, SI = a.SI;
-    const uint32_t tid = threadIdx.x, lane = tid & 63u, n = lane & 15u, g = lane >> 4;
-    const uint32_t v = uni(tid >> 6) & 7u;
-    extern __shared__ __align__(16) uint8_t lds[];
-    uint16_t* A = (uint16_t*)lds;
-    const NativeShared NS = NativeShared::make(H, SI);
-    const uint32_t RB = cdiv(H, 128u), P = cdiv(b.T, kMT), nks = SI / 32u;
-    const rsrc_t rs = make_rsrc(a.sh_native + NS.sdn, (uint32_t)(NS.total - NS.sdn));
-    for (uint32_t u = blockIdx.x; u < P * RB; u += gridDim.x) {
-        const uint32_t p = u / RB, rb = u % RB;
-        const uint32_t nt = min(kMT, b.T - p * kMT), t0 = p * kMT;
-        const uint32_t r0 = rb * 128u + v * 16u;
-        const bool rv = r0 + n < H;
-        const uint32_t voff = (g * H + min(r0 + n, H - 1u)) * 16u;
-        const uint32_t nblk = cdiv(nt, 16u);
-        f32x4 acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
-        auto row = [&](uint32_t m) { return b.smid + (size_t)(t0 + m) * SI; };
-        const uint32_t nst = cdiv(SI, kKC);
-        auto issue = [&](uint32_t st, BfW& W) {
-            const bool live = st < nst;
-#pragma unroll
-            for (uint32_t s8 = 0; s8 < 8; s8++)
-                W.w[s8] = bld16_nt(rs, voff, live ? min(st * 8u + s8, nks - 1u) * 4u * H * 16u : kOOB);
-        };
-        BfW W0, W1;
-        issue(0, W0);
-        steps2(nst, W0, W1, [&](uint32_t st, const BfW& cur, BfW& nxt) {
-            AStage as;
-            a_load(as, row, nt, st * kKC, SI);
-            issue(st + 1u, nxt);
-            lds_barrier();
-            a_store(A, as);
-            lds_barrier();
-#pragma unroll
-            for (uint32_t s8 = 0; s8 < 8; s8++) {
-                const u32x4 z = {0u, 0u, 0u, 0u};
-                mma_blocks(acc, A, nblk, s8 * 32u + 8u * g, as_bf16x8(st * 8u + s8 < nks ? cur.w[s8] : z));
-            }
-        });
-        if (rv) {
-#pragma unroll
-            for (uint32_t tb = 0; tb < 2; tb++) {
-#pragma unroll
-                for (uint32_t i = 0; i < 4; i++) {
-                    const uint32_t m = tb * 16u + 4u * g + i;
-                    if (m < nt) gst(b.shout + (size_t)(t0 + m) * H + r0 + n, acc[tb][i]);
-                }
-            }
-        }
-        lds_barrier();
-    }
+    run_steps(k);
 }
 
 // out[t] = (resid[t] +) sum_k w[t][k] e_k[t] in slot order + shared[t]
@@ -628,26 +958,30 @@ int launch_batched(const DecodeArgs* d_args, const BatchArgs& b, uint32_t H, uin
     (void)SI;
     hipStream_t s = (hipStream_t)stream;
     hipError_t e;
-    const size_t route_lds = 0;
     const size_t topk_lds = 4u * (2u * E + 64u);
-    const size_t gemm_lds = kALds + 4u * kMT + 8u * E;
+    const size_t gemm_lds = gemm_tab_bytes(E);
     const struct { const void* fn; size_t lds; } attrs[] = {
-        {(const void*)btopk_kernel, topk_lds},
-        {(const void*)bgu_kernel, gemm_lds},     {(const void*)bdn_kernel, gemm_lds},
-        {(const void*)bsgu_kernel, gemm_lds},    {(const void*)bsdn_kernel, gemm_lds}};
+        {(const void*)btopk_kernel, topk_lds}, {(const void*)bup_kernel, gemm_lds}, {(const void*)bdown_kernel, gemm_lds}};
     for (const auto& at : attrs)
         if ((e = hipFuncSetAttribute(at.fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)at.lds)) != hipSuccess)
             return (int)e;
-    const uint32_t G = 2u * n_cu;  // two work-groups per CU fit the LDS of the GEMM kernels
+    // The GEMM kernels walk their units with a grid stride, so their grid is
+    // what the chip holds at once (the LDS ring allows one work-group per CU);
+    // a larger grid would leave its second part waiting for the first.
+    auto resident = [&](const void* fn) {
+        int nb = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, fn, kThreads, gemm_lds) != hipSuccess || nb < 1) nb = 1;
+        return n_cu * (uint32_t)nb;
+    };
+    const uint32_t nperm = b.T * K * (3u * H / 8u);
     hipLaunchKernelGGL(bnorm_kernel, dim3(b.T), dim3(kThreads), 0, s, d_args, b);
-    hipLaunchKernelGGL(broute_kernel, dim3(kRouteGX, (b.T + kTB - 1) / kTB), dim3(kThreads), route_lds, s, d_args, b);
+    hipLaunchKernelGGL(broute_kernel, dim3(kRouteGX, (b.T + kTB - 1) / kTB), dim3(kThreads), 0, s, d_args, b);
     hipLaunchKernelGGL(btopk_kernel, dim3(b.T), dim3(kThreads), topk_lds, s, d_args, b);
     hipLaunchKernelGGL(bcount_kernel, dim3(E), dim3(64), 0, s, b, K);
     hipLaunchKernelGGL(bscatter_kernel, dim3(E), dim3(256), 0, s, b, E);
-    hipLaunchKernelGGL(bsgu_kernel, dim3(G), dim3(kThreads), gemm_lds, s, d_args, b);
-    hipLaunchKernelGGL(bsdn_kernel, dim3(G), dim3(kThreads), gemm_lds, s, d_args, b);
-    hipLaunchKernelGGL(bgu_kernel, dim3(G), dim3(kThreads), gemm_lds, s, d_args, b);
-    hipLaunchKernelGGL(bdn_kernel, dim3(G), dim3(kThreads), gemm_lds, s, d_args, b);
+    hipLaunchKernelGGL(bpermute_kernel, dim3(std::min((nperm + 255u) / 256u, 8u * n_cu)), dim3(256), 0, s, b, H, K);
+    hipLaunchKernelGGL(bup_kernel, dim3(resident((const void*)bup_kernel)), dim3(kThreads), gemm_lds, s, d_args, b);
+    hipLaunchKernelGGL(bdown_kernel, dim3(resident((const void*)bdown_kernel)), dim3(kThreads), gemm_lds, s, d_args, b);
     hipLaunchKernelGGL(bcomb_kernel, dim3((H + 255) / 256, b.T), dim3(256), 0, s, b, H, K);
     return (int)hipGetLastError();
 }

@@ -6,6 +6,7 @@
 // glm::alloc_scratch (src/glm_loader.cuh:363-450).
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
@@ -597,6 +598,9 @@ wl_status wl_taps(wl_ctx* c, wl_taps_out* out) {
     return WL_OK;
 }
 
+// Tokens per batched launch (longer calls run in chunks of this many).
+constexpr uint32_t kBatchChunk = 4096;
+
 static wl_status batch_reserve(wl_ctx* c, uint32_t T) {
     BatchScratch& B = c->batch;
     if (T <= B.cap) return WL_OK;
@@ -615,10 +619,11 @@ static wl_status batch_reserve(wl_ctx* c, uint32_t T) {
         *p = (std::remove_reference_t<decltype(*p)>)q;
         return true;
     };
-    if (!get(&b.norm, 4 * t * H) || !get(&b.logits, 4 * t * E) || !get(&b.idx, 4 * t * K) || !get(&b.wts, 4 * t * K) ||
+    if (!get(&b.norm, 4 * t * H) || !get(&b.norm3, 6 * t * H) || !get(&b.xperm3, 6 * t * K * H) ||
+        !get(&b.logits, 4 * t * E) || !get(&b.idx, 4 * t * K) || !get(&b.wts, 4 * t * K) ||
         !get(&b.counts, 4 * E) || !get(&b.offsets, 4 * (E + 1)) || !get(&b.lists, 4 * E * t) ||
-        !get(&b.ent, 4 * t * K) || !get(&b.pos, 4 * t * K) || !get(&b.mid, 4 * t * K * I) ||
-        !get(&b.expout, 4 * t * K * H) || !get(&b.smid, 4 * t * SI) || !get(&b.shout, 4 * t * H)) {
+        !get(&b.ent, 4 * t * K) || !get(&b.pos, 4 * t * K) || !get(&b.mid3, 6 * t * K * I) ||
+        !get(&b.expout, 4 * t * K * H) || !get(&b.smid3, 6 * t * SI) || !get(&b.shout, 4 * t * H)) {
         for (void* p : B.bufs) (void)hipFree(p);
         B.bufs.clear();
         return fail(c, WL_ERR_OOM, "batched scratch for %u tokens", T);
@@ -639,16 +644,24 @@ wl_status wl_run_moe_batched(wl_ctx* c, uint32_t layer, uint32_t n_tokens, const
     if (c->n_bound[layer] != E)
         return fail(c, WL_ERR_NOT_RESIDENT, "batched layer %u needs every expert bound (%u of %u)", layer,
                     c->n_bound[layer], E);
-    wl_status s = batch_reserve(c, n_tokens);
+    // Tokens run in chunks: bounded scratch, and every piece array stays under
+    // 2 GB (the kernels address them with 32-bit buffer offsets).
+    const uint64_t H = c->cfg.hidden, K = c->cfg.n_experts_per_tok;
+    const uint64_t row = 6ull * K * std::max<uint64_t>(std::max<uint64_t>(H, c->cfg.moe_inter), c->SI);
+    const uint32_t chunk = (uint32_t)std::min<uint64_t>(kBatchChunk, ((1ull << 31) - 1) / row);
+    if (chunk == 0) return fail(c, WL_ERR_INVALID, "batched rows too large for 32-bit offsets");
+    wl_status s = batch_reserve(c, std::min(n_tokens, chunk));
     if (s != WL_OK) return s;
-    wl::BatchArgs b = c->batch.b;
-    b.T = n_tokens;
-    b.hidden = d_hidden;
-    b.resid = d_resid;
-    b.out = d_out;
-    int e = wl::launch_batched(c->d_largs + layer, b, c->cfg.hidden, c->cfg.moe_inter, c->SI, E,
-                               c->cfg.n_experts_per_tok, (uint32_t)c->n_cu, stream);
-    if (e != 0) return hip_fail(c, (hipError_t)e, "batched launch");
+    for (uint32_t t0 = 0; t0 < n_tokens; t0 += chunk) {
+        wl::BatchArgs b = c->batch.b;
+        b.T = std::min(chunk, n_tokens - t0);
+        b.hidden = d_hidden + (size_t)t0 * H;
+        b.resid = d_resid ? d_resid + (size_t)t0 * H : nullptr;
+        b.out = d_out + (size_t)t0 * H;
+        int e = wl::launch_batched(c->d_largs + layer, b, c->cfg.hidden, c->cfg.moe_inter, c->SI, E,
+                                   c->cfg.n_experts_per_tok, (uint32_t)c->n_cu, stream);
+        if (e != 0) return hip_fail(c, (hipError_t)e, "batched launch");
+    }
     return WL_OK;
 }
 
