@@ -269,14 +269,16 @@ def main():
                    "hidden": H, "moe_inter": c["moe_inter"], "n_routed_experts": c["n_routed_experts"],
                    "n_experts_per_tok": c["n_experts_per_tok"], "shared": "bf16 inter 2048",
                    ("chain_layers" if chain else "rotating_layers"): args.layers, "schedule": args.sched,
-                   "global_batch": 1},
+                   "global_batch": args.tokens if batched else 1},
         "tokens_per_s": round(1e6 / (us_per_layer * layers_per_step) * (args.tokens if batched else 1), 2),
         "tokens_per_s_per_layer": round(1e6 / us_per_layer, 1),
         "achieved_GBps": round(achieved, 1),
         "pct_of_hbm_peak": round(100 * achieved / PEAK_HBM_GBPS, 2),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
                      "frac": round(achieved / PEAK_HBM_GBPS, 4), "traffic": traffic,
-                     "algorithmic_bytes": nbytes, "kernel": "moe_decode_kernel"},
+                     "algorithmic_bytes": nbytes,
+                     "kernel": ("whole batched call (bup_kernel + bdown_kernel dominate)" if batched else
+                                "moe_decode_kernel")},
         "cpu_baseline": cpu,
         **({"batched": {"tokens": args.tokens, "unique_experts": uniq, "max_tokens_per_expert": int(cnt.max()),
                         "zipf": {"s": 1.1, "amplitude": args.zipf_amp}}} if batched else {}),

@@ -339,11 +339,10 @@ WL_DEV Pass pass_at(const PassTab& pt, uint32_t E, uint32_t j) {
 // steps of kKC columns. A work-group walks its units u = blockIdx.x + G i as
 // one flat sequence of steps z, so the pipeline runs across unit boundaries.
 // Step z:
-//   1. barrier: every wave is done with step z - 1, so LDS slot (z + 2) % 3
-//      (last read in step z - 1) is free;
-//   2. DMA the activations of step z + 2 into that slot (buffer_load ... lds,
-//      no registers), then load the weights of step z + 2 into register
-//      buffer (z + 2) % 3;
+//   1. load the weights of step z + 2 into register buffer (z + 2) % 3;
+//   2. barrier: every wave is done with step z - 1, so LDS slot (z + 2) % 3
+//      (last read in step z - 1) is free; DMA the activations of step z + 2
+//      into it (buffer_load ... lds, no registers);
 //   3. wait until this wave's loads of step z (issued two steps ago) have
 //      landed, barrier (so every wave's DMAs have);
 //   4. compute step z from slot z % 3 and buffer z % 3; after a unit's last
@@ -352,14 +351,16 @@ WL_DEV Pass pass_at(const PassTab& pt, uint32_t E, uint32_t j) {
 // the loads of steps z + 1 and z + 2 stay in flight, activations and weights
 // alike (a load under full load takes several microseconds, a step less). The
 // slots are separate LDS objects, so the compiler's own waits for DMA-written
-// LDS stay per slot.
+// LDS stay per slot. (Spreading the loads through the compute instead, to
+// avoid the eight waves issuing at once, makes the compiler wait for them
+// early: it loses track of which buffer is outstanding.)
 constexpr uint32_t kRows = 3u * kMT;            // LDS rows of a step
 constexpr uint32_t kRowB = kKC * 2u;            // bytes of a staged row
 constexpr uint32_t kSlotB = kRows * kRowB;      // 48 KB
 constexpr uint32_t kDma = kRows / 2u / kWaves;  // DMA instructions per wave per step (1 KB = 2 rows each)
 constexpr uint32_t kWL = 8;                     // 16-byte weight loads per step
 constexpr uint32_t kSL = 4;                     // 4-byte scale loads per step
-constexpr uint32_t kAfter = 2u * (kDma + kWL + kSL);
+constexpr uint32_t kAfter = 2u * (kDma + kWL + kSL);  // loads of two steps
 constexpr uint32_t kOOBV = 0x80000000u;  // a lane offset past every piece array (they stay below 2 GB)
 static_assert(kRows % (2u * kWaves) == 0u, "DMA rows must split evenly over the waves");
 static_assert(kAfter < 64u, "vmcnt is 6 bits");
@@ -388,37 +389,45 @@ WL_DEV bf16x8 afrag(const uint8_t* sl, uint32_t pc, uint32_t tb, uint32_t hi, ui
 }
 
 // Activation side of a unit: rows [row0, row0 + nt) of a piece array with
-// kdim columns (uniform values; dead: nt = 0).
+// kdim columns (uniform values; dead: nt = 0). DMA instruction k of wave v
+// writes slot rows 2j and 2j + 1 (j = v + kWaves k; lanes 0-31 the first), so
+// every row a lane writes has R & 15 = x = 2v + (lane >> 5): its 16-byte
+// group (column group cg = p ^ x) and, per layout, its token and piece differ
+// between k only by uniform amounts:
+//   pieces in rows: R = 4m + pc -> m = (x >> 2) + 4k, pc = x & 3;
+//   tokens in rows: R = 32 pc + m -> m = x + 16 (k & 1), pc = k >> 1.
+// So one lane offset per unit (base, at k = 0) plus a uniform offset per k.
 struct AStream {
     rsrc_t rs;
-    uint32_t row0, nt, kdim;
+    uint32_t base, nt, kd2;  // lane byte offset at k = 0, tokens, bytes per piece row
     bool pr;
 };
+WL_DEV uint32_t a_x() { return 2u * uni(threadIdx.x >> 6) + ((threadIdx.x & 63u) >> 5); }
 WL_DEV void a_bind(AStream& A, const uint16_t* base, uint64_t bytes, uint32_t row0, uint32_t nt, bool pr,
                    uint32_t kdim) {
     A.rs = make_rsrc(base, (uint32_t)bytes);
-    A.row0 = row0;
     A.nt = nt;
-    A.kdim = kdim;
+    A.kd2 = 2u * kdim;
     A.pr = pr;
+    const uint32_t x = a_x(), cg = (threadIdx.x & 31u) ^ x;
+    A.base = ((row0 + (pr ? x >> 2 : x)) * 3u + (pr ? x & 3u : 0u)) * A.kd2 + 16u * cg;
 }
 WL_DEV void a_none(AStream& A) { a_bind(A, nullptr, 0u, 0u, 0u, true, 0u); }
-// DMA instruction k of this wave writes slot rows 2j and 2j + 1 (j = v +
-// kWaves k; lanes 0-31 the first row), each lane 16 bytes: its byte offset in
-// the piece array (kOOBV: row absent, lands as zeros) is computed here rather
-// than kept in registers across the loop.
+// DMA instruction k of one step (columns [k0, k0 + kKC)); absent rows
+// (kOOBV) land as zeros.
+template <int S>
+WL_DEV void a_issue_one(const AStream& A, uint32_t k0, uint32_t k) {
+    const uint32_t v = uni(threadIdx.x >> 6), x = a_x();
+    const bool ok = A.pr ? (x >> 2) + 4u * k < A.nt && (x & 3u) < 3u : x + 16u * (k & 1u) < A.nt;
+    const uint32_t so = 2u * k0 + (A.pr ? 12u * k : 48u * (k & 1u) + (k >> 1)) * A.kd2;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        A.rs, (__attribute__((address_space(3))) void*)(slot<S>() + (v + kWaves * k) * 2u * kRowB), 16u,
+        ok ? A.base : kOOBV, so, 0, 0);
+}
 template <int S>
 WL_DEV void a_issue(const AStream& A, uint32_t k0) {
-    const uint32_t lane = threadIdx.x & 63u, v = uni(threadIdx.x >> 6);
 #pragma unroll
-    for (uint32_t k = 0; k < kDma; k++) {
-        const uint32_t R = 2u * (v + kWaves * k) + (lane >> 5), cg = (lane & 31u) ^ (R & 15u);
-        const uint32_t m = A.pr ? R >> 2 : R & 31u, pc = A.pr ? R & 3u : R >> 5;
-        const uint32_t voff = (m < A.nt && pc < 3u) ? (((A.row0 + m) * 3u + pc) * A.kdim + 8u * cg) * 2u : kOOBV;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            A.rs, (__attribute__((address_space(3))) void*)(slot<S>() + (v + kWaves * k) * 2u * kRowB), 16u, voff,
-            2u * k0, 0, 0);
-    }
+    for (uint32_t k = 0; k < kDma; k++) a_issue_one<S>(A, k0, k);
 }
 
 struct WBuf {
@@ -429,8 +438,9 @@ WL_DEV uint32_t bld4(rsrc_t r, uint32_t voff, uint32_t soff) {
     return __builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, 0);
 }
 
-// Step 1: this wave's LDS reads are done (lgkmcnt(0)), barrier.
+// Step 2: this wave's LDS reads are done (lgkmcnt(0)), barrier.
 WL_DEV void free_barrier() {
+    __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_waitcnt(0xC07Fu);  // lgkmcnt(0); vmcnt, expcnt not waited on
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
@@ -453,14 +463,20 @@ WL_DEV bool advance(Cursor& c, uint32_t nst) {
     c.i++;
     return true;
 }
+template <class Kn>
+WL_DEV void issue_w(const Kn& k, uint32_t s, WBuf& W) {
+#pragma unroll
+    for (uint32_t j = 0; j < kWL + kSL; j++) k.issue_w_one(s, W, j);
+}
 template <int S, class Kn>
 WL_DEV void pipe_step(Kn& k, AStream& A, const WBuf& cur, WBuf& nxt) {
+    // weights first: their registers are this wave's own, only the slot
+    // needs every wave to be done with the previous step
+    if (advance(k.cw, k.nst)) k.bind_w(k.cw.i);
+    issue_w(k, k.cw.s, nxt);
     free_barrier();
     if (advance(k.ca, k.nst)) k.bind_a(k.ca.i, A);
     a_issue<(S + 2) % 3>(A, k.ca.s * kKC);
-    __builtin_amdgcn_sched_barrier(0);
-    if (advance(k.cw, k.nst)) k.bind_w(k.cw.i);
-    k.issue_w(k.cw.s, nxt);
     step_barrier();
     if (k.cc.i < k.nu) {
         if (k.cc.s == 0u) k.begin(k.cc.i);
@@ -471,7 +487,8 @@ WL_DEV void pipe_step(Kn& k, AStream& A, const WBuf& cur, WBuf& nxt) {
 }
 // Runs the pipeline over this work-group's nu units. Kn provides nst, nu, the
 // cursors ca/cw/cc and bind_a(i, A) / bind_w(i) (unit i >= nu: nothing to
-// load), issue_w(s, W), begin(i), compute(s, slot, W), finish().
+// load), issue_w_one(s, W, j) (load j of kWL + kSL), begin(i),
+// compute(s, slot, W) and finish().
 template <class Kn>
 WL_DEV void run_steps(Kn& k) {
     if (k.nu == 0u) return;
@@ -479,14 +496,14 @@ WL_DEV void run_steps(Kn& k) {
     AStream A;
     WBuf B0, B1, B2;
     k.ca = k.cw = k.cc = Cursor{0u, 0u};
+    k.bind_w(0u);
+    issue_w(k, 0u, B0);
     k.bind_a(0u, A);
     a_issue<0>(A, 0u);
-    k.bind_w(0u);
-    k.issue_w(0u, B0);
+    if (advance(k.cw, k.nst)) k.bind_w(k.cw.i);
+    issue_w(k, k.cw.s, B1);
     if (advance(k.ca, k.nst)) k.bind_a(k.ca.i, A);
     a_issue<1>(A, k.ca.s * kKC);
-    if (advance(k.cw, k.nst)) k.bind_w(k.cw.i);
-    k.issue_w(k.cw.s, B1);
 #pragma unroll 1
     for (uint32_t z = 0; z < Z; z += 3u) {
         pipe_step<0>(k, A, B0, B2);
@@ -588,17 +605,14 @@ struct UpK {
         srs = x.live && !x.sh ? wrs : make_rsrc(nullptr, 0u);
         wvoff = x.sh ? vsh : vgu;  // chosen here, not per load (see DownK::bind_w)
     }
-    WL_MEM void issue_w(uint32_t s, WBuf& W) const {
-#pragma unroll
-        for (uint32_t k = 0; k < kWL; k++) {
-            const uint32_t sl = min(wpart * kSG + k / 2u, S - 1u);
-            const uint32_t ro = sl * 8u * nkg * 1024u + min(2u * s + k % 2u, nkg - 1u) * 1024u;
-            const uint32_t so = wpart * 8u * nkt * 1024u + min(8u * s + k, nkt - 1u) * 1024u;
-            W.w[k] = bld16_nt(wrs, wvoff, wsh ? so : ro);
-        }
-        const uint32_t kt = min(2u * s, nkg - 1u);
-#pragma unroll
-        for (uint32_t i = 0; i < kSL; i++) {
+    WL_MEM void issue_w_one(uint32_t s, WBuf& W, uint32_t j) const {
+        if (j < kWL) {
+            const uint32_t sl = min(wpart * kSG + j / 2u, S - 1u);
+            const uint32_t ro = sl * 8u * nkg * 1024u + min(2u * s + j % 2u, nkg - 1u) * 1024u;
+            const uint32_t so = wpart * 8u * nkt * 1024u + min(8u * s + j, nkt - 1u) * 1024u;
+            W.w[j] = bld16_nt(wrs, wvoff, wsh ? so : ro);
+        } else {
+            const uint32_t i = j - kWL, kt = min(2u * s, nkg - 1u);
             const uint32_t sl = min(wpart * kSG + i, S - 1u);
             W.s[i] = bld4(srs, vgus, sl * 8u * cdiv(nkg, 16u) * 1024u + (kt / 16u) * 1024u + 4u * ((kt % 16u) / 4u));
         }
@@ -624,10 +638,43 @@ struct UpK {
 #pragma unroll
                 for (uint32_t pc = 0; pc < NP; pc++)
                     acc[0][tb] = mma(afrag(sl, pc, tb, k / 4u, lo_s[k % 4u]), bw, acc[0][tb]);
+            __builtin_amdgcn_sched_barrier(0);
         }
     }
     template <uint32_t NB, uint32_t NP>
     WL_MEM void comp_routed(uint32_t s, const uint8_t* sl, const WBuf& W) {
+        if constexpr (NP == 1u) {
+            // Pieces in rows (NB fragments per k step): the fragments of the
+            // next k step are read while this one computes (LDS latency is
+            // not hidden by the one other wave of the SIMD otherwise).
+            float sc[2][kSG];
+#pragma unroll
+            for (uint32_t q = 0; q < 2; q++)
+#pragma unroll
+                for (uint32_t i = 0; i < kSG; i++)
+                    sc[q][i] = 2u * s + q < nkg ? e8m0f((W.s[i] >> (8u * ((2u * s + q) % 4u))) & 0xFFu) : 0.f;
+            bf16x8 af[2][NB];
+#pragma unroll
+            for (uint32_t tb = 0; tb < NB; tb++) af[0][tb] = afrag(sl, 0u, tb, 0u, lo_r[0]);
+#pragma unroll
+            for (uint32_t it = 0; it < 8; it++) {
+                const uint32_t q = it / 4u, jj = it % 4u, c = it % 2u;
+                if (it + 1u < 8u) {
+#pragma unroll
+                    for (uint32_t tb = 0; tb < NB; tb++)
+                        af[c ^ 1u][tb] = afrag(sl, 0u, tb, (it + 1u) / 4u, lo_r[(it + 1u) % 4u]);
+                }
+                bf16x8 bw[kSG];
+#pragma unroll
+                for (uint32_t i = 0; i < kSG; i++) bw[i] = fp4x8_bf16(W.w[2u * i + q][jj], sc[q][i]);
+#pragma unroll
+                for (uint32_t i = 0; i < kSG; i++)
+#pragma unroll
+                    for (uint32_t tb = 0; tb < NB; tb++) acc[i][tb] = mma(af[c][tb], bw[i], acc[i][tb]);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            return;
+        }
 #pragma unroll
         for (uint32_t q = 0; q < 2; q++) {
             const uint32_t kt = 2u * s + q;
@@ -789,20 +836,16 @@ struct DownK {
         // members at each load would take the members' addresses)
         wvoff = x.sh ? (g * H + min(x.part * 128u + 16u * v + n, H - 1u)) * 16u : vdn;
     }
-    WL_MEM void issue_w(uint32_t st, WBuf& W) const {
+    WL_MEM void issue_w_one(uint32_t st, WBuf& W, uint32_t j) const {
         const uint32_t q0 = wpart * 16u + 2u * v;
-#pragma unroll
-        for (uint32_t k = 0; k < kWL; k++) {
-            const uint32_t j = min(st * 4u + k / 2u, NS - 1u), q = min(q0 + k % 2u, nq - 1u);
-            const uint32_t ro = (j * nq + q) * 1024u;
-            const uint32_t so = min(8u * st + k, nks - 1u) * 4u * H * 16u;
-            W.w[k] = bld16_nt(wrs, wvoff, wsh ? so : ro);
-        }
-        const uint32_t qs = min(q0, nq - 1u);
-#pragma unroll
-        for (uint32_t i = 0; i < kSL; i++) {
-            const uint32_t j = min(st * 4u + i, NS - 1u);
-            W.s[i] = bld4(srs, vdns, (j * cdiv(nq, 16u) + qs / 16u) * 1024u + 4u * ((qs % 16u) / 4u));
+        if (j < kWL) {
+            const uint32_t sj = min(st * 4u + j / 2u, NS - 1u), q = min(q0 + j % 2u, nq - 1u);
+            const uint32_t ro = (sj * nq + q) * 1024u;
+            const uint32_t so = min(8u * st + j, nks - 1u) * 4u * H * 16u;
+            W.w[j] = bld16_nt(wrs, wvoff, wsh ? so : ro);
+        } else {
+            const uint32_t i = j - kWL, sj = min(st * 4u + i, NS - 1u), qs = min(q0, nq - 1u);
+            W.s[i] = bld4(srs, vdns, (sj * cdiv(nq, 16u) + qs / 16u) * 1024u + 4u * ((qs % 16u) / 4u));
         }
     }
     WL_MEM void begin(uint32_t i) {
@@ -825,6 +868,7 @@ struct DownK {
 #pragma unroll
                 for (uint32_t pc = 0; pc < NP; pc++)
                     d[0][0][tb] = mma(afrag(sl, pc, tb, k / 4u, lo_s[k % 4u]), bw, d[0][0][tb]);
+            __builtin_amdgcn_sched_barrier(0);
         }
     }
     template <uint32_t NB, uint32_t NP>
