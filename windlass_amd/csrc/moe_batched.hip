@@ -316,6 +316,19 @@ WL_DEV PassTab load_pass_tab(const BatchArgs& b, uint32_t E, uint32_t* s) {
     lds_barrier();
     return PassTab{cnt, off, pp, uni(pp[E])};
 }
+// Routed unit r (< n_passes * parts) -> (pass j, part). Units go in blocks
+// of 8 passes x parts, ordered so that unit r has j % 8 == r % 8 in full
+// blocks: with a grid of a multiple of 8 (work-group b runs on XCD b % 8),
+// the units of one pass run on one XCD and share its L2 copy of the pass's
+// activations.
+struct PassPart {
+    uint32_t j, part;
+};
+WL_DEV PassPart pass_part(uint32_t r, uint32_t parts, uint32_t npass) {
+    const uint32_t blk = r / (8u * parts), l = r % (8u * parts);
+    const uint32_t np = min(8u, npass - 8u * blk);
+    return PassPart{8u * blk + l % np, l / np};
+}
 // Pass j (< n): its expert (the largest e with pp[e] <= j, which has a pass
 // since pp[e + 1] > j), the pass within the expert, its token count and its
 // first compact entry.
@@ -340,27 +353,27 @@ WL_DEV Pass pass_at(const PassTab& pt, uint32_t E, uint32_t j) {
 // one flat sequence of steps z, so the pipeline runs across unit boundaries.
 // Step z:
 //   1. load the weights of step z + 2 into register buffer (z + 2) % 3;
-//   2. barrier: every wave is done with step z - 1, so LDS slot (z + 2) % 3
-//      (last read in step z - 1) is free; DMA the activations of step z + 2
-//      into it (buffer_load ... lds, no registers);
-//   3. wait until this wave's loads of step z (issued two steps ago) have
-//      landed, barrier (so every wave's DMAs have);
+//   2. wait until this wave's loads of step z (issued two steps ago) have
+//      landed, barrier: every wave's activation DMAs of step z have landed,
+//      and every wave is done with step z - 1;
+//   3. DMA the activations of step z + 2 (buffer_load ... lds, no registers)
+//      into slot (z + 2) % 3, the slot step z - 1 read;
 //   4. compute step z from slot z % 3 and buffer z % 3; after a unit's last
 //      step, its epilogue.
-// Loads complete in issue order, so 3 is "at most kAfter loads outstanding":
-// the loads of steps z + 1 and z + 2 stay in flight, activations and weights
-// alike (a load under full load takes several microseconds, a step less). The
-// slots are separate LDS objects, so the compiler's own waits for DMA-written
-// LDS stay per slot. (Spreading the loads through the compute instead, to
-// avoid the eight waves issuing at once, makes the compiler wait for them
-// early: it loses track of which buffer is outstanding.)
+// Loads complete in issue order, so 2 is "at most kAfter loads outstanding":
+// the weights of steps z + 1 and z + 2 and the activations of step z + 1 stay
+// in flight (a load under full load takes several microseconds, a step
+// less). The slots are separate LDS objects, so the compiler's own waits for
+// DMA-written LDS stay per slot. (Spreading the loads through the compute
+// instead, to avoid the eight waves issuing at once, makes the compiler wait
+// for them early: it loses track of which buffer is outstanding.)
 constexpr uint32_t kRows = 3u * kMT;            // LDS rows of a step
 constexpr uint32_t kRowB = kKC * 2u;            // bytes of a staged row
 constexpr uint32_t kSlotB = kRows * kRowB;      // 48 KB
 constexpr uint32_t kDma = kRows / 2u / kWaves;  // DMA instructions per wave per step (1 KB = 2 rows each)
 constexpr uint32_t kWL = 8;                     // 16-byte weight loads per step
 constexpr uint32_t kSL = 4;                     // 4-byte scale loads per step
-constexpr uint32_t kAfter = 2u * (kDma + kWL + kSL);  // loads of two steps
+constexpr uint32_t kAfter = kDma + 2u * (kWL + kSL);  // issued after step z's activations
 constexpr uint32_t kOOBV = 0x80000000u;  // a lane offset past every piece array (they stay below 2 GB)
 static_assert(kRows % (2u * kWaves) == 0u, "DMA rows must split evenly over the waves");
 static_assert(kAfter < 64u, "vmcnt is 6 bits");
@@ -438,14 +451,7 @@ WL_DEV uint32_t bld4(rsrc_t r, uint32_t voff, uint32_t soff) {
     return __builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, 0);
 }
 
-// Step 2: this wave's LDS reads are done (lgkmcnt(0)), barrier.
-WL_DEV void free_barrier() {
-    __builtin_amdgcn_sched_barrier(0);
-    __builtin_amdgcn_s_waitcnt(0xC07Fu);  // lgkmcnt(0); vmcnt, expcnt not waited on
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_sched_barrier(0);
-}
-// Step 3: s_waitcnt vmcnt(kAfter) (expcnt, lgkmcnt not waited on), barrier.
+// Step 2: s_waitcnt vmcnt(kAfter) (expcnt, lgkmcnt not waited on), barrier.
 WL_DEV void step_barrier() {
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_waitcnt((kAfter & 15u) | ((kAfter >> 4) << 14) | 0x0F70u);
@@ -470,14 +476,14 @@ WL_DEV void issue_w(const Kn& k, uint32_t s, WBuf& W) {
 }
 template <int S, class Kn>
 WL_DEV void pipe_step(Kn& k, AStream& A, const WBuf& cur, WBuf& nxt) {
-    // weights first: their registers are this wave's own, only the slot
-    // needs every wave to be done with the previous step
     if (advance(k.cw, k.nst)) k.bind_w(k.cw.i);
     issue_w(k, k.cw.s, nxt);
-    free_barrier();
+    step_barrier();
+    // after the barrier every wave is done with step z - 1: its slot takes
+    // the activations of step z + 2
     if (advance(k.ca, k.nst)) k.bind_a(k.ca.i, A);
     a_issue<(S + 2) % 3>(A, k.ca.s * kKC);
-    step_barrier();
+    __builtin_amdgcn_sched_barrier(0);
     if (k.cc.i < k.nu) {
         if (k.cc.s == 0u) k.begin(k.cc.i);
         k.compute(k.cc.s, slot<S>(), cur);
@@ -578,8 +584,9 @@ struct UpK {
             x.nt = min(kMT, b.T - p * kMT);
             x.row0 = p * kMT;
         } else {
-            const Pass ps = pass_at(pt, E, (u - Us) / NSG);
-            x.part = (u - Us) % NSG;
+            const PassPart jp = pass_part(u - Us, NSG, pt.n);
+            const Pass ps = pass_at(pt, E, jp.j);
+            x.part = jp.part;
             x.e = ps.e;
             x.nt = ps.nt;
             x.row0 = ps.c0;
@@ -807,8 +814,9 @@ struct DownK {
             x.nt = min(kMT, b.T - p * kMT);
             x.row0 = p * kMT;
         } else {
-            const Pass ps = pass_at(pt, E, (u - Us) / RBr);
-            x.part = (u - Us) % RBr;
+            const PassPart jp = pass_part(u - Us, RBr, pt.n);
+            const Pass ps = pass_at(pt, E, jp.j);
+            x.part = jp.part;
             x.e = ps.e;
             x.nt = ps.nt;
             x.row0 = ps.c0;
