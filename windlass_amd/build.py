@@ -14,6 +14,11 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 # Packed-FP32 VALU forms are disabled on purpose: some of them have given
 # wrong results on this hardware without any error.
 DEVICE_FLAGS = ["--offload-arch=gfx950", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+# Kernel arguments preloaded into SGPRs (gfx950 kernarg preloading): the
+# first dwords of every kernel's arguments are in registers when its waves
+# start, so the first loads of the decode kernel need no memory round trip to
+# learn their addresses. 14 = internal.h kPreloadDwords.
+PRELOAD_FLAGS = ["-mllvm", "-amdgpu-kernarg-preload-count=14"]
 COMMON = ["-O3", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-function", "-Wno-unknown-pragmas"]
 
 
@@ -23,7 +28,7 @@ def build(verbose: bool = False) -> str:
         path = os.path.join(CSRC, src)
         obj = os.path.join(CSRC, "_build", src + ".o")
         os.makedirs(os.path.dirname(obj), exist_ok=True)
-        cmd = [HIPCC] + COMMON + DEVICE_FLAGS + ["-c", path, "-o", obj]
+        cmd = [HIPCC] + COMMON + DEVICE_FLAGS + PRELOAD_FLAGS + ["-c", path, "-o", obj]
         if src.endswith(".cpp"):
             cmd = [HIPCC] + COMMON + ["-c", path, "-o", obj]
         if verbose:

@@ -104,14 +104,31 @@ struct DecodeArgs {
 // segment 0 (everything up to the published partials) and segment 1 (the
 // combine); a fused launch runs both (the combine waits for the epoch tags of
 // the partials it reads), the phased schedule runs each as its own launch.
+// The kernel is built with kernarg preloading: the record pointer and the
+// first 12 dwords below arrive in SGPRs, so the loads that start a layer (the
+// hidden state, the router row, the norm weight, the bias, the shared expert)
+// are issued without first waiting for a memory round trip to read their
+// addresses. The same pointers are also in the layer record (DecodeArgs) for
+// the other kernels.
 struct DecodeDyn {
     const float* hidden;        // [H] pre-norm residual stream
+    const uint8_t* sh_native;   // the layer's shared expert (NativeShared)
+    const uint16_t* router_w;   // [E][H] bf16
+    const uint16_t* ln_w;       // [H] bf16 or null (= ones)
+    const float* bias;          // [E] f32
+    uint32_t seg;               // bits 0-7: first segment, 8-15: last segment, 16: shared-expert tap on
+    uint32_t epoch;             // different for every call of the context, never 0
+    // not preloaded (read later in the layer)
+    const uint8_t* const* slot_tab;  // [E] block pointers of this layer
     const float* resid;         // [H] or null: out = resid + moe
     float* out;                 // [H]
-    uint32_t seg_lo, seg_hi;
-    uint32_t epoch;             // different for every call of the context, never 0
-    int32_t taps;               // 1: also produce the shared-expert output tap
+    __host__ __device__ uint32_t seg_lo() const { return seg & 0xFFu; }
+    __host__ __device__ uint32_t seg_hi() const { return (seg >> 8) & 0xFFu; }
+    __host__ __device__ int32_t taps() const { return (int32_t)((seg >> 16) & 1u); }
 };
+// Dwords of kernel arguments the decode kernel preloads into SGPRs (the
+// record pointer, then DecodeDyn up to `epoch`).
+constexpr int kPreloadDwords = 14;
 
 // Dynamic LDS layout of the decode kernel (byte offsets).
 struct LdsMap {

@@ -106,11 +106,11 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const DecodeDyn d) {
     Batch bA, bB;
 
     // ================= segment 0: everything but the combine ====================
-    if (d.seg_lo == 0u) {
+    if (d.seg_lo() == 0u) {
         WL_TL(0);
         // routing inputs that do not depend on this call's data, for experts
         // e = tid (E <= 512; the rest later): consumed long after they land
-        const rsrc_t bs_rs = make_rsrc(a.bias, E * 4u), sl_rs = make_rsrc(a.slot_tab, E * 8u);
+        const rsrc_t bs_rs = make_rsrc(d.bias, E * 4u), sl_rs = make_rsrc(d.slot_tab, E * 8u);
         const uint32_t bias0 = __builtin_amdgcn_raw_buffer_load_b32(bs_rs, (int)(4u * tid), 0, 0);
         const uint64_t slot0 = __builtin_bit_cast(uint64_t, __builtin_amdgcn_raw_buffer_load_b64(sl_rs, (int)(8u * tid), 0, 0));
         // hidden state and norm weight first: they are consumed first
@@ -118,7 +118,7 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const DecodeDyn d) {
         float4 hv[HV];
         uint2 lv[HV];
         const rsrc_t hid_rs = make_rsrc(d.hidden, H * 4u);
-        const rsrc_t ln_rs = make_rsrc(a.ln_w ? (const void*)a.ln_w : (const void*)d.hidden, H * 2u);
+        const rsrc_t ln_rs = make_rsrc(d.ln_w ? (const void*)d.ln_w : (const void*)d.hidden, H * 2u);
 #pragma unroll
         for (int i = 0; i < HV; i++) {
             const uint32_t j = tid + kThreads * i;  // float4 j = elements [4j, 4j+4)
@@ -128,7 +128,7 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const DecodeDyn d) {
         // the first router row of this work-group
         constexpr int RCH = kRCH;
         const uint32_t nch = H / 8;
-        const rsrc_t rt_rs = make_rsrc(a.router_w, E * H * 2u);
+        const rsrc_t rt_rs = make_rsrc(d.router_w, E * H * 2u);
         u32x4 rw[RCH];
 #pragma unroll
         for (int m = 0; m < RCH; m++) rw[m] = bld16_nt(rt_rs, 16u * min(tid + kThreads * m, nch - 1u), min(w, E - 1u) * H * 2u);
@@ -146,7 +146,7 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const DecodeDyn d) {
         const uint32_t sg_nb = at_least2(cdiv(sg_per, (uint32_t)kNB));
         // native shared expert: tile T, k tile kt is the 1 KB chunk T*(H/32)+kt
         const NativeShared NS = NativeShared::make(H, SI);
-        const rsrc_t sg_rs = make_rsrc(a.sh_native + NS.sgu, (uint32_t)(NS.sdn - NS.sgu));
+        const rsrc_t sg_rs = make_rsrc(d.sh_native + NS.sgu, (uint32_t)(NS.sdn - NS.sgu));
         auto sg_issue = [&](uint32_t tile, uint32_t b, Batch& B) {
             const uint32_t voff = min(tile, nsg - 1u) * nkt * 1024u + 16u * lane;
             const uint32_t kt0 = v * sg_per + b * kNB;
@@ -165,8 +165,10 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const DecodeDyn d) {
         };
         // shared down, columns [8t, 8t+8) of every row: thread tid takes rows
         // tid + 512*i, 16 bytes each (zero past the end)
-        constexpr int SDV = 16;  // rows per thread: H <= 8192
-        const rsrc_t sd_rs = make_rsrc(a.sh_native + NS.sdn, (uint32_t)(NS.total - NS.sdn));
+        // rows per thread: H / 512 at the GLM shape, 16 (H <= 8192) otherwise;
+        // the resource of a tile ends at its last row, so rows past H read
+        // zeros without touching memory (the next tile's rows are not fetched)
+        constexpr int SDV = GLM ? 12 : 16;
         u32x4 sdw[SDV];
         // logit slots of experts e = tid, loaded behind the last weights of the
         // shared expert: by then the router rows are long published
@@ -184,9 +186,10 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const DecodeDyn d) {
                 lsl_load();
                 lsl_sent = true;
             }
+            const rsrc_t sd_rs = make_rsrc(d.sh_native + NS.sdn + (size_t)min(tile, nsg - 1u) * H * 16u, H * 16u);
 #pragma unroll
-            for (int i = 0; i < SDV; i++)  // row tid + 512 i of the tile: 16 bytes, rows past H read zeros
-                sdw[i] = bld16_nt(sd_rs, (tile * H + tid) * 16u, kThreads * i * 16u);
+            for (int i = 0; i < SDV; i++)  // row tid + 512 i of the tile: 16 bytes
+                sdw[i] = bld16_nt(sd_rs, tid * 16u, kThreads * i * 16u);
         };
         const uint32_t tile0 = tile_of(0);
         sg_issue(tile0, 0, bA);
@@ -204,7 +207,7 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const DecodeDyn d) {
                 const uint32_t ls[4] = {lv[i].x & 0xFFFFu, lv[i].x >> 16, lv[i].y & 0xFFFFu, lv[i].y >> 16};
 #pragma unroll
                 for (int c = 0; c < 4; c++) {
-                    const float x = norm_value(xs[c], rinv, a.ln_w != nullptr, ls[c]);
+                    const float x = norm_value(xs[c], rinv, d.ln_w != nullptr, ls[c]);
                     const uint32_t col = 4 * j + c;
                     xn[col] = x;
                     uint32_t ph, pm, pl;
@@ -221,8 +224,8 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const DecodeDyn d) {
             tk_blk[tid] = (const uint8_t*)slot0;
         }
         for (uint32_t e = tid + kThreads; e < E; e += kThreads) {
-            tk_ch[e] = gld(a.bias + e);
-            tk_blk[e] = gld(a.slot_tab + e);
+            tk_ch[e] = gld(d.bias + e);
+            tk_blk[e] = gld(d.slot_tab + e);
         }
         lds_barrier();
         WL_TL(1);
@@ -314,7 +317,7 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const DecodeDyn d) {
         };
         // the deferred down columns, then (taps on) the shared-expert
         // contribution alone, published for the tap
-        bool tsh_pending = d.taps != 0;
+        bool tsh_pending = d.taps() != 0;
         auto finish_shared = [&]() {
             if (sd_pending) {
                 sd_compute();
@@ -383,7 +386,7 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const DecodeDyn d) {
         // at most one routed unit per work-group (GLM: exactly one): its down
         // items publish the partial rows directly
         const bool direct = P.U <= G && w < P.U;
-        rsrc_t r_rs = make_rsrc(a.router_w, 16u);  // rebound per unit
+        rsrc_t r_rs = make_rsrc(d.router_w, 16u);  // rebound per unit
         uint32_t gu_voff = 0, gus_voff = 0, dn_voff = 0, dns_voff = 0;
         // Native block: the gate/up items of this wave are 1 KB chunks
         // [tile*(H/128) + kt], the down items [slice*(H/32) + q]; one 16-byte
@@ -396,7 +399,9 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const DecodeDyn d) {
             const uint32_t wv = gu ? gu_voff : dn_voff;
 #pragma unroll
             for (int i = 0; i < kNB; i++) B.w[i] = bld16_nt(r_rs, wv, (i0 + i) * 1024u);
-            B.sv = bld16_nt(r_rs, gu ? gus_voff : dns_voff, (i0 / 16u) * 1024u);
+            // a scale chunk serves 16 items, i.e. two batches: default policy
+            // (not the streaming hint), so the second batch's load hits in L2
+            B.sv = bld16(r_rs, gu ? gus_voff : dns_voff, (i0 / 16u) * 1024u);
         };
         f32x4 racc;
         bf16x8 A0, A1;
@@ -517,7 +522,7 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const DecodeDyn d) {
 
     // ================= segment 1: combine ========================================
     // out[r] = sum over work-groups of their partials (fixed order), + resid.
-    if (d.seg_hi >= 1u) {
+    if (d.seg_hi() >= 1u) {
         constexpr uint32_t RB = kRowBlock;
         float* fin = pv;                   // [G][32]
         float* f2 = fin + (size_t)G * RB;  // [16][32]
@@ -581,7 +586,7 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const DecodeDyn d) {
             const uint32_t r = blkr * RB + tid;
             const float o = block_total(a.part, blkr);
             if (tid < RB) gst(d.out + r, d.resid ? __fadd_rn(gld(d.resid + r), o) : o);
-            if (d.taps) {
+            if (d.taps()) {
                 const float sh = block_total(a.tsh, blkr);
                 if (tid < RB) gst(a.shared_out + r, sh);
             }

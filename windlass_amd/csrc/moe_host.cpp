@@ -531,12 +531,15 @@ static wl_status run_layer(wl_ctx* c, uint32_t layer, const float* d_hidden, con
     if (++c->epoch >= 0x7FFFFFFFu) c->epoch = 1;
     dyn.epoch = c->epoch;
     dyn.hidden = d_hidden;
+    dyn.sh_native = L.shared;
+    dyn.router_w = L.router_w;
+    dyn.ln_w = L.ln;
+    dyn.bias = L.bias;
+    dyn.slot_tab = c->d_slot + (size_t)layer * E;
     dyn.resid = d_resid;
     dyn.out = d_out;
-    dyn.taps = c->taps;
     auto launch = [&](uint32_t lo, uint32_t hi) -> wl_status {
-        dyn.seg_lo = lo;
-        dyn.seg_hi = hi;
+        dyn.seg = lo | (hi << 8) | ((c->taps ? 1u : 0u) << 16);
         int e = wl::launch_decode(c->d_largs + layer, dyn, H, I, SI, E, K, c->grid, stream);
         if (e != 0) return hip_fail(c, (hipError_t)e, "decode launch");
         return WL_OK;
