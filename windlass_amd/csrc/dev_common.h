@@ -187,11 +187,21 @@ WL_DEV uint32_t batch_scale(const Batch& B, uint32_t item0, int i) {
     return (w >> (8u * (o % 4u))) & 0xFFu;
 }
 
+// A batch of the bf16 shared expert's gate/up stream: kSNB k tiles per wave,
+// plus one 8-byte read of a logit slot, so the logits are collected while the
+// weights stream. (Measured on MI355X: 4-tile batches shorten the norm's wait
+// but starve the stream, 8 is faster overall.)
+constexpr int kSNB = 8;
+struct SBatch {
+    u32x4 w[kSNB];
+    uint64_t pl;
+};
+
 // Two-deep software pipeline over nb >= 2 batches: A holds batch 0 and B
 // batch 1 on entry, both already issued. Batch b+2 is issued right after
 // batch b is consumed; no batch is issued that is not consumed.
-template <class IssueF, class ConsumeF>
-WL_DEV void pingpong(uint32_t nb, Batch& A, Batch& B, IssueF issue, ConsumeF consume) {
+template <class BT, class IssueF, class ConsumeF>
+WL_DEV void pingpong(uint32_t nb, BT& A, BT& B, IssueF issue, ConsumeF consume) {
     uint32_t b = 0;
 #pragma unroll 1
     for (; b + 3 < nb; b += 2) {

@@ -104,6 +104,7 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const DecodeDyn d) {
     float* smf = (float*)(misc + 16);           // [8] this tile's shared SwiGLU values
 
     Batch bA, bB;
+    SBatch sA, sB;
 
     // ================= segment 0: everything but the combine ====================
     if (d.seg_lo() == 0u) {
@@ -143,24 +144,38 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const DecodeDyn d) {
             return xcd_map ? (w & 7u) * (G / 8u) + (w >> 3) : t;
         };
         const uint32_t sg_per = cdiv(nkt, 8u);  // k tiles per wave: [v*sg_per, +sg_per)
-        const uint32_t sg_nb = at_least2(cdiv(sg_per, (uint32_t)kNB));
+        const uint32_t sg_nb = at_least2(cdiv(sg_per, (uint32_t)kSNB));
         // native shared expert: tile T, k tile kt is the 1 KB chunk T*(H/32)+kt
         const NativeShared NS = NativeShared::make(H, SI);
         const rsrc_t sg_rs = make_rsrc(d.sh_native + NS.sgu, (uint32_t)(NS.sdn - NS.sgu));
-        auto sg_issue = [&](uint32_t tile, uint32_t b, Batch& B) {
+        // every shared batch also reads the logit slot of expert min(tid, E-1)
+        // (agent scope): the logits published while the shared expert streams
+        // are collected on the way, without a separate round trip
+        const rsrc_t ls_rs = make_rsrc(a.lslot, E * 8u);
+        const uint32_t pe = min(tid, E - 1u);
+        auto sg_issue = [&](uint32_t tile, uint32_t b, SBatch& B) {
             const uint32_t voff = min(tile, nsg - 1u) * nkt * 1024u + 16u * lane;
-            const uint32_t kt0 = v * sg_per + b * kNB;
+            const uint32_t kt0 = v * sg_per + b * kSNB;
 #pragma unroll
-            for (int i = 0; i < kNB; i++) B.w[i] = bld16_nt(sg_rs, voff, (kt0 + i) * 1024u);
+            for (int i = 0; i < kSNB; i++) B.w[i] = bld16_nt(sg_rs, voff, (kt0 + i) * 1024u);
+            B.pl = __builtin_bit_cast(uint64_t, __builtin_amdgcn_raw_buffer_load_b64(ls_rs, (int)(8u * pe), 0, kSC1));
         };
         f32x4 gacc;
-        auto sg_consume = [&](uint32_t b, const Batch& B) {
+        bool seen = false;  // this call's logit of expert tid was read (only tid < E)
+        uint32_t lbits = 0;
+        auto sg_consume = [&](uint32_t b, const SBatch& B) {
 #pragma unroll
-            for (int i = 0; i < kNB; i++) {
-                const uint32_t m = b * kNB + i, kt = v * sg_per + m;
+            for (int i = 0; i < kSNB; i++) {
+                const uint32_t m = b * kSNB + i, kt = v * sg_per + m;
                 const bool valid = m < sg_per && kt < nkt;
                 const u32x4 z = {0u, 0u, 0u, 0u};
                 gacc = mma(a_lds(xp, xps, n, kt * 32u + 8u * g, valid), as_bf16x8(valid ? B.w[i] : z), gacc);
+            }
+            // threads tid >= E read slot E - 1 only to keep every batch the
+            // same shape; they own no expert and never record a logit
+            if (tid < E && !seen && (uint32_t)(B.pl >> 32) == d.epoch) {
+                seen = true;
+                lbits = (uint32_t)B.pl;
             }
         };
         // shared down, columns [8t, 8t+8) of every row: thread tid takes rows
@@ -170,30 +185,15 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const DecodeDyn d) {
         // zeros without touching memory (the next tile's rows are not fetched)
         constexpr int SDV = GLM ? 12 : 16;
         u32x4 sdw[SDV];
-        // logit slots of experts e = tid, loaded behind the last weights of the
-        // shared expert: by then the router rows are long published
-        uint64_t lsl = 0;
-        auto lsl_load = [&]() {
-            if (tid < E)
-                lsl = __hip_atomic_load((__attribute__((address_space(1))) uint64_t*)(a.lslot + tid), __ATOMIC_RELAXED,
-                                        __HIP_MEMORY_SCOPE_AGENT);
-        };
-        bool lsl_sent = false;
         auto sd_issue = [&](uint32_t tile) {
-            // the logit slots go first: the top-k reads them before it needs
-            // these rows, and loads complete in issue order
-            if (!lsl_sent) {
-                lsl_load();
-                lsl_sent = true;
-            }
             const rsrc_t sd_rs = make_rsrc(d.sh_native + NS.sdn + (size_t)min(tile, nsg - 1u) * H * 16u, H * 16u);
 #pragma unroll
             for (int i = 0; i < SDV; i++)  // row tid + 512 i of the tile: 16 bytes
                 sdw[i] = bld16_nt(sd_rs, tid * 16u, kThreads * i * 16u);
         };
         const uint32_t tile0 = tile_of(0);
-        sg_issue(tile0, 0, bA);
-        sg_issue(tile0, 1, bB);
+        sg_issue(tile0, 0, sA);
+        sg_issue(tile0, 1, sB);
 
         // RMSNorm: w * (x * (1/sqrt(mean(x^2) + eps))) in fp32
         // (tools/ref_glm_chain.py:63-80; src/glm_primitives.cuh:35-62)
@@ -242,6 +242,47 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const DecodeDyn d) {
         }
         WL_TL(2);
 
+        // ---- top-k (runs after the first shared tile's gate/up, whose
+        // batches collected most logits): every logit of this call must be
+        // present; slots still holding an older epoch are re-read
+        auto route = [&]() -> bool {
+            if (tid < E && seen) {
+                topk_score(__uint_as_float(lbits), tk_ch[tid], tid, tk_sc, tk_ch);
+                if (w == 0) gst(a.logits + tid, __uint_as_float(lbits));
+            }
+            uint32_t done = seen ? 1u : 0u;  // bit i: expert tid + 512*i scored (tk_ch[e] then holds its choice)
+            for (uint32_t spins = 0;; spins++) {
+                bool mine = true;
+                for (uint32_t i = 0, e = tid; e < E; i++, e += kThreads) {
+                    if ((done >> i) & 1u) continue;
+                    const uint64_t x = __hip_atomic_load((__attribute__((address_space(1))) uint64_t*)(a.lslot + e),
+                                                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    if ((uint32_t)(x >> 32) == d.epoch) {
+                        topk_score(__uint_as_float((uint32_t)x), tk_ch[e], e, tk_sc, tk_ch);
+                        if (w == 0) gst(a.logits + e, __uint_as_float((uint32_t)x));
+                        done |= 1u << i;
+                    } else {
+                        mine = false;
+                    }
+                }
+                if (block_all(mine, misc)) break;
+                if (spins > (1u << 20) || ld_sync(a.sync + SM.error) != 0u) {
+                    if (tid == 0 && spins > (1u << 20)) raise_error(a.sync, SM, E_SPIN);
+                    return false;
+                }
+                __builtin_amdgcn_s_sleep(2);
+            }
+            WL_TL(4);
+            if (E <= 256u) topk_argmax(E, K, tk_sc, tk_ch, tk_idx, tk_w);
+            else topk_rank(E, K, tk_sc, tk_ch, tk_idx, tk_w);
+            WL_TL(5);
+            if (w == 0 && tid < K) {
+                gst(a.idx + tid, (int32_t)tk_idx[tid]);
+                gst(a.topw + tid, topk_weight(a, K, tk_w, tid));
+            }
+            return true;
+        };
+
         // shared expert: SwiGLU of each tile's 8 rows, then those 8 columns of
         // the down projection applied to every output row, into pv
         const uint32_t ntiles = w < nsg ? cdiv(nsg - w, G) : 0u;
@@ -266,29 +307,27 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const DecodeDyn d) {
                 }
             }
         };
-        // The last tile's down columns are applied after the top-k and the
-        // first routed loads are issued: its rows stay in flight meanwhile, so
-        // HBM keeps streaming through the top-k.
-        bool sd_pending = false;
+        // The last tile's down columns are applied after the first routed
+        // loads are issued: its rows stay in flight meanwhile, so HBM keeps
+        // streaming through the top-k and into the routed units.
+        bool sd_pending = false, routed = false;
         for (uint32_t ti = 0; ti < ntiles; ti++) {
             const uint32_t tile = tile_of(ti);
             if (ti != 0) {
-                sg_issue(tile, 0, bA);
-                sg_issue(tile, 1, bB);
+                sg_issue(tile, 0, sA);
+                sg_issue(tile, 1, sB);
             }
             gacc = f32x4{0.f, 0.f, 0.f, 0.f};
-            bool sd_sent = false;
-            pingpong(sg_nb, bA, bB,
-                     [&](uint32_t b, Batch& B) {
-                         sg_issue(tile, b, B);
-                         if (b + 1 >= sg_nb && !sd_sent) {  // the last issue: shared-down rows follow it
-                             sd_issue(tile);
-                             sd_sent = true;
-                         }
-                     },
-                     sg_consume);
-            if (!sd_sent) sd_issue(tile);
+            pingpong(sg_nb, sA, sB, [&](uint32_t b, SBatch& B) { sg_issue(tile, b, B); }, sg_consume);
+            // the tile's shared-down rows are issued only now: issued with the
+            // last gate/up batch they delay it (the memory system serves both
+            // together), and with it the top-k
+            sd_issue(tile);
             if (lane < 16) red[v * 64 + n] = sum3(gacc);
+            if (!routed) {
+                if (!route()) return;
+                routed = true;
+            }
             lds_barrier();
             if (tid < 8) {
                 float gs = 0.f, us = 0.f;
@@ -309,6 +348,7 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const DecodeDyn d) {
                 sd_pending = true;
             }
         }
+        if (!routed && !route()) return;
         // pv -> rows [32b, 32b+32) into block b, slot w of dst ([H/32][G][32]),
         // tagged with this call's epoch
         auto publish = [&](uint64_t* dst) {
@@ -330,47 +370,6 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const DecodeDyn d) {
             }
         };
         WL_TL(3);
-
-        // ---- top-k: every logit of this call must be published (a slot that
-        // still holds an older epoch is re-read)
-        if (!lsl_sent) lsl_load();
-        {
-            bool ok = true;
-            uint32_t done = 0;  // bit i: expert tid + 512*i scored (tk_ch[e] then holds its choice, no longer the bias)
-            for (uint32_t spins = 0;; spins++) {
-                bool mine = true;
-                for (uint32_t i = 0, e = tid; e < E; i++, e += kThreads) {
-                    if ((done >> i) & 1u) continue;
-                    const uint64_t x = i == 0 ? lsl
-                                              : __hip_atomic_load((__attribute__((address_space(1))) uint64_t*)(a.lslot + e),
-                                                                  __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    if ((uint32_t)(x >> 32) == d.epoch) {
-                        topk_score(__uint_as_float((uint32_t)x), tk_ch[e], e, tk_sc, tk_ch);
-                        if (w == 0) gst(a.logits + e, __uint_as_float((uint32_t)x));
-                        done |= 1u << i;
-                    } else {
-                        mine = false;
-                    }
-                }
-                if (block_all(mine, misc)) break;
-                if (spins > (1u << 20) || ld_sync(a.sync + SM.error) != 0u) {
-                    if (tid == 0 && spins > (1u << 20)) raise_error(a.sync, SM, E_SPIN);
-                    ok = false;
-                    break;
-                }
-                __builtin_amdgcn_s_sleep(2);
-                lsl_load();
-            }
-            if (!ok) return;
-        }
-        WL_TL(4);
-        if (E <= 256u) topk_argmax(E, K, tk_sc, tk_ch, tk_idx, tk_w);
-        else topk_rank(E, K, tk_sc, tk_ch, tk_idx, tk_w);
-        WL_TL(5);
-        if (w == 0 && tid < K) {
-            gst(a.idx + tid, (int32_t)tk_idx[tid]);
-            gst(a.topw + tid, topk_weight(a, K, tk_w, tid));
-        }
 
         // ---- routed units u = w + G*i: items are gate/up k tiles (128 wide,
         // this wave's 8+8 row tile), then down row pairs (32 rows x the
