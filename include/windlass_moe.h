@@ -160,6 +160,17 @@ wl_status wl_run_moe_batched(wl_ctx* ctx, uint32_t layer, uint32_t n_tokens, con
  * 855-868). */
 wl_status wl_batched_counts(wl_ctx* ctx, uint32_t* h_counts);
 
+/* Test hook, no reference counterpart: the routing of the last chunk of the
+ * last wl_run_moe_batched call. *h_n_tokens = its token count T (WL_ERR_INVALID
+ * if T > max_tokens, nothing copied); then, for each non-null array (host,
+ * sized for max_tokens), the router logits [T][n_routed_experts], the selected
+ * ids [T][n_experts_per_tok] (descending biased score) and their weights
+ * [T][n_experts_per_tok]; synchronises the device. Per token these equal
+ * wl_taps' logits / topk_idx / topk_w after wl_run_moe on the same hidden
+ * state. */
+wl_status wl_batched_routing(wl_ctx* ctx, uint32_t max_tokens, uint32_t* h_n_tokens, float* h_logits,
+                             int32_t* h_idx, float* h_w);
+
 /* Device pointers to the last layer's intermediates (the substeps
  * test_glm_chain reads through SubstepHook, src/test_glm_chain.cu:434-441). */
 typedef struct wl_taps_out {

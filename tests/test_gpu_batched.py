@@ -43,6 +43,26 @@ def _decode(dm, h):
     return dout.download(np.float32)
 
 
+def _decode_routing(dm):
+    """Logits, ids and weights of the last wl_run_moe (taps)."""
+    tp = dm.ctx.taps()
+    E, K = dm.cfg.n_routed_experts, dm.cfg.n_experts_per_tok
+    return (H_.download_ptr(tp["logits"], np.float32, E), H_.download_ptr(tp["topk_idx"], np.int32, K),
+            H_.download_ptr(tp["topk_w"], np.float32, K))
+
+
+def _check_routing_bit_identical(dm, T, decode_routing):
+    """The batched router (many tokens per work-group, wave sums taken
+    together) performs the decode router's additions in the decode router's
+    order: logits, ids (in order) and weights equal bit for bit."""
+    lg, ids, w = dm.ctx.batched_routing(T)
+    assert lg.shape[0] == T
+    for t, (dl, di, dw) in enumerate(decode_routing):
+        assert np.array_equal(lg[t].view(np.uint32), dl.view(np.uint32)), t
+        assert np.array_equal(ids[t], di), t
+        assert np.array_equal(w[t].view(np.uint32), dw.view(np.uint32)), t
+
+
 @pytest.mark.parametrize("T", [1, 5, 33, 70])
 def test_small_batched_vs_oracle_and_decode(gpu, T):
     c = SMALL
@@ -52,14 +72,17 @@ def test_small_batched_vs_oracle_and_decode(gpu, T):
     out = _batched(dm, hs)
     src = O.ExpertSource(H, c["moe_inter"], 12)
     worst = 0.0
+    routing = []
     for t in range(T):
         dec = _decode(dm, hs[t])
+        routing.append(_decode_routing(dm))
         r = O.rel_to_scale(dec, out[t])
         worst = max(worst, r)
         assert r < TOL, (t, r)
         if t < 3 or t == T - 1:
             ref = O.moe_layer(hs[t], dm.dense[0], src, 0, c)["out"]
             assert O.rel_to_scale(ref, out[t]) < TOL, t
+    _check_routing_bit_identical(dm, T, routing)
     print(f"T={T}: worst batched-vs-decode rel_to_scale {worst:.2e}", flush=True)
     dm.close()
 
@@ -95,10 +118,13 @@ def test_glm_batched_64_vs_decode(gpu):
     hs = _tokens(H, T, 500)
     out = _batched(dm, hs)
     worst = 0.0
+    routing = []
     for t in range(T):
         r = O.rel_to_scale(_decode(dm, hs[t]), out[t])
+        routing.append(_decode_routing(dm))
         worst = max(worst, r)
         assert r < TOL, (t, r)
+    _check_routing_bit_identical(dm, T, routing)
     src = O.ExpertSource(H, c["moe_inter"], 14)
     ref = O.moe_layer(hs[5], dm.dense[0], src, 0, c)["out"]
     assert O.rel_to_scale(ref, out[5]) < TOL

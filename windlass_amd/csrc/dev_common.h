@@ -370,7 +370,7 @@ WL_DEV float norm_value(float x, float rinv, bool has_ln, uint32_t ln_bits) {
 // thread's chunk c = threadIdx.x + kThreads * m (from LDS or registers: the
 // arithmetic is the same either way).
 template <class XF>
-WL_DEV float router_partial_x(const u32x4 (&rw)[kRCH], XF x, uint32_t nch) {
+WL_DEV float router_chain_x(const u32x4 (&rw)[kRCH], XF x, uint32_t nch) {
     float pd = 0.f;
 #pragma unroll
     for (int m = 0; m < kRCH; m++) {
@@ -387,6 +387,13 @@ WL_DEV float router_partial_x(const u32x4 (&rw)[kRCH], XF x, uint32_t nch) {
             pd = fmaf(bf2f(rw[m].w >> 16), x1.w, pd);
         }
     }
+    return pd;
+}
+// The wave sum of router_chain_x: the butterfly x += shfl_xor(x, o), o = 32,
+// 16, ..., 1 (every lane ends with the same bits: fp32 addition commutes).
+template <class XF>
+WL_DEV float router_partial_x(const u32x4 (&rw)[kRCH], XF x, uint32_t nch) {
+    float pd = router_chain_x(rw, x, nch);
     for (int o = 32; o > 0; o >>= 1) pd += __shfl_xor(pd, o, 64);
     return pd;
 }

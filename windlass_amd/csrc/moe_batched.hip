@@ -39,7 +39,6 @@ namespace wl {
 constexpr uint32_t kMT = 32;         // tokens per pass: two MFMA row blocks of 16
 constexpr uint32_t kKC = 256;        // activation columns staged per step
 constexpr uint32_t kTB = 8;          // tokens per routing work-group
-constexpr uint32_t kRouteGX = 16;    // routing work-groups per token block (router rows r = x + 16 i)
 
 // Row layout of a pass's staged activations, chosen per pass from its token
 // count nt (wave-uniform):
@@ -151,15 +150,54 @@ __global__ void __launch_bounds__(kThreads) bnorm_kernel(const DecodeArgs* __res
     }
 }
 
-// Router logits of kTB tokens: each thread keeps its router_partial share of
-// every token's normalised input in registers; the rows r = x + gridDim.x i
-// stream through (next row prefetched). The per-row arithmetic and the
-// summation over waves are router_partial's and router_publish's.
+// Wave sums of NV values per lane at once (NV a power of two <= 64), each
+// summed over the 64 lanes by the same tree as router_partial_x's butterfly
+// (x += shfl_xor(x, o), o = 32, 16, ..., 1): at each of the first log2(NV)
+// levels a lane keeps half of its values and adds its partner's copy of them
+// (the two operands the butterfly adds in this lane at this level), the
+// levels after that are the butterfly itself. Afterwards lane l holds, in
+// x[0], the sum of value l >> (6 - log2 NV) — bit for bit the butterfly's.
+// (Levels are template parameters: every index into x is a constant, so x
+// stays in registers without indexed moves.)
+template <uint32_t N, uint32_t n, uint32_t o>  // values [0, 2n) -> [0, n) at offset o
+WL_DEV void wave_levels(float (&x)[N]) {
+    if constexpr (n >= 1u) {
+        const bool up = (threadIdx.x & o) != 0u;
+#pragma unroll
+        for (uint32_t j = 0; j < n; j++) {
+            const float keep = up ? x[j + n] : x[j];
+            const float send = up ? x[j] : x[j + n];
+            x[j] = keep + __shfl_xor(send, (int)o, 64);
+        }
+        wave_levels<N, n / 2u, o / 2u>(x);
+    } else if constexpr (o >= 1u) {
+        x[0] += __shfl_xor(x[0], (int)o, 64);
+        wave_levels<N, 0u, o / 2u>(x);
+    }
+}
+template <uint32_t NV>
+WL_DEV void multi_wave_sum(float (&x)[NV]) {
+    static_assert(NV >= 1u && NV <= 64u && (NV & (NV - 1u)) == 0u, "NV: a power of two <= 64");
+    wave_levels<NV, NV / 2u, 32u>(x);
+}
+
+// Router logits of kTB tokens: each thread keeps its router_chain_x share of
+// every token's normalised input in registers; the rows stream through, kRR
+// at a time (rows r = x + gridDim.x (kRR i + q), q < kRR; the next group
+// prefetched). The kRR x kTB wave sums of a group are taken together
+// (multi_wave_sum), then summed over the waves in order from 0 — the
+// arithmetic of router_partial and router_publish, so each logit equals the
+// one the decode and routing kernels compute for the token.
+constexpr uint32_t kRR = 4;  // router rows per group
 __global__ void __launch_bounds__(kThreads) broute_kernel(const DecodeArgs* __restrict__ pa, const BatchArgs b) {
     const DecodeArgs& a = *pa;
-    const uint32_t H = a.H, E = a.E, tid = threadIdx.x;
+    const uint32_t H = a.H, E = a.E, tid = threadIdx.x, lane = tid & 63u, v = uni(tid >> 6);
+    constexpr uint32_t NV = kRR * kTB;  // value q * kTB + tt: row q, token tt
+    constexpr uint32_t SH = 6u - __builtin_ctz(NV);
+    constexpr uint32_t kFL = 64;  // groups whose logits are buffered in LDS
     __shared__ float red[kWaves * 64];
-    const uint32_t t0 = blockIdx.y * kTB, nch = H / 8;
+    __shared__ float lgb[kFL * NV];
+    const uint32_t t0 = blockIdx.y * kTB, nch = H / 8, gx = gridDim.x;
     float4 xr[kTB][kRCH][2];  // xn[8c .. 8c+8) of chunks c = tid + 512 m, per token
 #pragma unroll
     for (uint32_t tt = 0; tt < kTB; tt++) {
@@ -173,30 +211,73 @@ __global__ void __launch_bounds__(kThreads) broute_kernel(const DecodeArgs* __re
         }
     }
     const rsrc_t rt_rs = make_rsrc(a.router_w, E * H * 2u);
-    u32x4 rn[kRCH];
+    auto row_of = [&](uint32_t i, uint32_t q) { return blockIdx.x + gx * (kRR * i + q); };
+    u32x4 rn[kRR][kRCH];
 #pragma unroll
-    for (int m = 0; m < kRCH; m++)
-        rn[m] = bld16(rt_rs, 16u * min(tid + kThreads * m, nch - 1u), min(blockIdx.x, E - 1u) * H * 2u);
-    for (uint32_t r = blockIdx.x; r < E; r += gridDim.x) {
-        u32x4 rw[kRCH];
+    for (uint32_t q = 0; q < kRR; q++)
+#pragma unroll
+        for (int m = 0; m < kRCH; m++)
+            rn[q][m] = bld16(rt_rs, 16u * min(tid + kThreads * m, nch - 1u), min(row_of(0u, q), E - 1u) * H * 2u);
+    for (uint32_t i = 0; row_of(i, 0u) < E; i++) {
+        u32x4 rw[kRR][kRCH];
+#pragma unroll
+        for (uint32_t q = 0; q < kRR; q++)
+#pragma unroll
+            for (int m = 0; m < kRCH; m++) {
+                rw[q][m] = rn[q][m];
+                rn[q][m] = bld16(rt_rs, 16u * min(tid + kThreads * m, nch - 1u), min(row_of(i + 1u, q), E - 1u) * H * 2u);
+            }
+        // router_chain_x for every (row, token) value, its chunks in the same
+        // order (m, then the 8 columns), with one branch per chunk instead of
+        // one per value, so the NV independent chains interleave
+        float x[NV];
+#pragma unroll
+        for (uint32_t j = 0; j < NV; j++) x[j] = 0.f;
 #pragma unroll
         for (int m = 0; m < kRCH; m++) {
-            rw[m] = rn[m];
-            rn[m] = bld16(rt_rs, 16u * min(tid + kThreads * m, nch - 1u), min(r + gridDim.x, E - 1u) * H * 2u);
-        }
+            if (tid + kThreads * m < nch) {
 #pragma unroll
-        for (uint32_t tt = 0; tt < kTB; tt++) {
-            const float pd = router_partial_x(rw, [&](int m, int h) { return xr[tt][m][h]; }, nch);
-            if ((tid & 63u) == 0) red[(tid >> 6) * 64 + 48 + tt] = pd;
+                for (uint32_t q = 0; q < kRR; q++) {
+                    const u32x4 r = rw[q][m];
+                    const float wv[8] = {bf2f(r.x & 0xFFFFu), bf2f(r.x >> 16), bf2f(r.y & 0xFFFFu), bf2f(r.y >> 16),
+                                         bf2f(r.z & 0xFFFFu), bf2f(r.z >> 16), bf2f(r.w & 0xFFFFu), bf2f(r.w >> 16)};
+#pragma unroll
+                    for (uint32_t tt = 0; tt < kTB; tt++) {
+                        const float4 x0 = xr[tt][m][0], x1 = xr[tt][m][1];
+                        float pd = x[q * kTB + tt];
+                        pd = fmaf(wv[0], x0.x, pd);
+                        pd = fmaf(wv[1], x0.y, pd);
+                        pd = fmaf(wv[2], x0.z, pd);
+                        pd = fmaf(wv[3], x0.w, pd);
+                        pd = fmaf(wv[4], x1.x, pd);
+                        pd = fmaf(wv[5], x1.y, pd);
+                        pd = fmaf(wv[6], x1.z, pd);
+                        pd = fmaf(wv[7], x1.w, pd);
+                        x[q * kTB + tt] = pd;
+                    }
+                }
+            }
         }
+        multi_wave_sum(x);
+        if ((lane & ((1u << SH) - 1u)) == 0u) red[v * 64u + (lane >> SH)] = x[0];
         lds_barrier();
-        if (tid < kTB && t0 + tid < b.T) {
+        if (tid < NV) {
             float sum = 0.f;  // the same order as router_publish
 #pragma unroll
-            for (int wv = 0; wv < kWaves; wv++) sum += red[wv * 64 + 48 + tid];
-            gst(b.logits + (size_t)(t0 + tid) * E + r, sum);
+            for (int wv = 0; wv < kWaves; wv++) sum += red[wv * 64 + tid];
+            lgb[(i % kFL) * NV + tid] = sum;
         }
         lds_barrier();
+        // the logits go out kFL groups at a time: a store in the loop would be
+        // waited for with the next group's rows (loads and stores share one
+        // counter), i.e. every group would wait for a store's round trip
+        if (i % kFL == kFL - 1u || row_of(i + 1u, 0u) >= E) {
+            const uint32_t i0 = i - i % kFL, n = (i % kFL + 1u) * NV;
+            for (uint32_t j = tid; j < n; j += kThreads) {
+                const uint32_t q = (j % NV) / kTB, tt = j % kTB, r = row_of(i0 + j / NV, q);
+                if (r < E && t0 + tt < b.T) gst(b.logits + (size_t)(t0 + tt) * E + r, lgb[j]);
+            }
+        }
     }
 }
 
@@ -1027,7 +1108,11 @@ int launch_batched(const DecodeArgs* d_args, const BatchArgs& b, uint32_t H, uin
     };
     const uint32_t nperm = b.T * K * (3u * H / 8u);
     hipLaunchKernelGGL(bnorm_kernel, dim3(b.T), dim3(kThreads), 0, s, d_args, b);
-    hipLaunchKernelGGL(broute_kernel, dim3(kRouteGX, (b.T + kTB - 1) / kTB), dim3(kThreads), 0, s, d_args, b);
+    // router: ~one work-group per CU; each token block's rows split over gx
+    // work-groups (each norm row is read gx times, the router once per block)
+    const uint32_t nblk = (b.T + kTB - 1) / kTB;
+    const uint32_t gx = std::max(1u, std::min(n_cu / nblk, (E + kRR - 1) / kRR));
+    hipLaunchKernelGGL(broute_kernel, dim3(gx, nblk), dim3(kThreads), 0, s, d_args, b);
     hipLaunchKernelGGL(btopk_kernel, dim3(b.T), dim3(kThreads), topk_lds, s, d_args, b);
     hipLaunchKernelGGL(bcount_kernel, dim3(E), dim3(64), 0, s, b, K);
     hipLaunchKernelGGL(bscatter_kernel, dim3(E), dim3(256), 0, s, b, E);

@@ -55,6 +55,7 @@ struct CacheState {
 // Scratch of the batched layer, sized for `cap` tokens.
 struct BatchScratch {
     uint32_t cap = 0;
+    uint32_t last_T = 0;  // tokens of the last chunk run
     std::vector<void*> bufs;
     wl::BatchArgs b{};
 };
@@ -658,6 +659,7 @@ wl_status wl_run_moe_batched(wl_ctx* c, uint32_t layer, uint32_t n_tokens, const
     for (uint32_t t0 = 0; t0 < n_tokens; t0 += chunk) {
         wl::BatchArgs b = c->batch.b;
         b.T = std::min(chunk, n_tokens - t0);
+        c->batch.last_T = b.T;
         b.hidden = d_hidden + (size_t)t0 * H;
         b.resid = d_resid ? d_resid + (size_t)t0 * H : nullptr;
         b.out = d_out + (size_t)t0 * H;
@@ -675,6 +677,23 @@ wl_status wl_batched_counts(wl_ctx* c, uint32_t* h_counts) {
     if (e == hipSuccess)
         e = hipMemcpy(h_counts, c->batch.b.counts, 4 * (size_t)c->cfg.n_routed_experts, hipMemcpyDeviceToHost);
     if (e != hipSuccess) return hip_fail(c, e, "batched counts");
+    return WL_OK;
+}
+
+wl_status wl_batched_routing(wl_ctx* c, uint32_t max_tokens, uint32_t* h_n_tokens, float* h_logits, int32_t* h_idx,
+                             float* h_w) {
+    if (!c || !h_n_tokens) return WL_ERR_INVALID;
+    if (!c->batch.cap) return fail(c, WL_ERR_STATE, "no batched call yet");
+    const wl::BatchArgs& b = c->batch.b;  // pointers; the chunk's token count is last_T
+    const uint32_t T = c->batch.last_T;
+    *h_n_tokens = T;
+    if (T > max_tokens) return fail(c, WL_ERR_INVALID, "the last chunk has %u tokens > max_tokens %u", T, max_tokens);
+    const size_t E = c->cfg.n_routed_experts, K = c->cfg.n_experts_per_tok;
+    hipError_t e = hipDeviceSynchronize();
+    if (e == hipSuccess && h_logits) e = hipMemcpy(h_logits, b.logits, 4 * (size_t)T * E, hipMemcpyDeviceToHost);
+    if (e == hipSuccess && h_idx) e = hipMemcpy(h_idx, b.idx, 4 * (size_t)T * K, hipMemcpyDeviceToHost);
+    if (e == hipSuccess && h_w) e = hipMemcpy(h_w, b.wts, 4 * (size_t)T * K, hipMemcpyDeviceToHost);
+    if (e != hipSuccess) return hip_fail(c, e, "batched routing");
     return WL_OK;
 }
 

@@ -84,6 +84,7 @@ def load():
         "wl_run_chain": [vp, u32, u32, vp, vp, vp],
         "wl_run_moe_batched": [vp, u32, u32, vp, vp, vp, vp],
         "wl_batched_counts": [vp, ctypes.POINTER(u32)],
+        "wl_batched_routing": [vp, u32, ctypes.POINTER(u32), vp, vp, vp],
         "wl_taps": [vp, ctypes.POINTER(Taps)],
         "wl_check_error": [vp, vp],
         "wl_set_schedule": [vp, i32],
@@ -243,6 +244,19 @@ class Context:
         self._ck(self.lib.wl_batched_counts(self.h, out.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32))),
                  "wl_batched_counts")
         return out
+
+    def batched_routing(self, max_tokens):
+        """(logits [T, E], ids [T, K], weights [T, K]) of the last batched chunk."""
+        import numpy as np
+        E, K = self.cfg.n_routed_experts, self.cfg.n_experts_per_tok
+        n = ctypes.c_uint32(0)
+        lg = np.zeros((max_tokens, E), np.float32)
+        ids = np.zeros((max_tokens, K), np.int32)
+        w = np.zeros((max_tokens, K), np.float32)
+        self._ck(self.lib.wl_batched_routing(self.h, max_tokens, ctypes.byref(n), lg.ctypes.data,
+                                             ids.ctypes.data, w.ctypes.data), "wl_batched_routing")
+        T = n.value
+        return lg[:T], ids[:T], w[:T]
 
     def run_chain(self, first_layer, n_layers, d_h, d_tmp, stream=0):
         self._ck(self.lib.wl_run_chain(self.h, first_layer, n_layers, d_h, d_tmp, stream), "wl_run_chain")
