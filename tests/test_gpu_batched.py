@@ -130,3 +130,23 @@ def test_glm_batched_64_vs_decode(gpu):
     assert O.rel_to_scale(ref, out[5]) < TOL
     print(f"GLM T=64: worst batched-vs-decode rel_to_scale {worst:.2e}", flush=True)
     dm.close()
+
+
+def test_misaligned_or_aliasing_buffers_rejected(gpu):
+    """The combine reads and writes rows 16 bytes at a time: buffers that are
+    not 16-byte aligned are an argument error (nothing is launched)."""
+    from windlass_amd.moe import WindlassError
+    c = SMALL
+    H = c["hidden"]
+    dm = DeviceModel(c, seed=12, n_layers=1)
+    T = 3
+    dh = H_.DeviceBuffer(4 * T * H + 64)
+    do = H_.DeviceBuffer(4 * T * H + 64)
+    for args in [(dh.ptr, None, do.ptr + 4), (dh.ptr + 8, None, do.ptr), (dh.ptr, dh.ptr + 4, do.ptr),
+                 (dh.ptr, None, dh.ptr)]:
+        with pytest.raises(WindlassError) as ei:
+            dm.ctx.run_moe_batched(0, T, *args)
+        assert ei.value.status == 1, args  # WL_ERR_INVALID
+    dm.ctx.run_moe_batched(0, T, dh.ptr, None, do.ptr)  # aligned: runs
+    dm.ctx.check_error()
+    dm.close()

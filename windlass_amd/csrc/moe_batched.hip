@@ -301,17 +301,28 @@ __global__ void __launch_bounds__(kThreads) btopk_kernel(const DecodeArgs* __res
 }
 
 // Entries of expert e in ascending (token, slot) order: one wave, 64 entries
-// per step, positions from a ballot prefix.
+// per step, positions from a ballot prefix; the ids of kCB steps are loaded
+// at once (one memory round trip per kCB steps).
+constexpr uint32_t kCB = 8;
 __global__ void __launch_bounds__(64) bcount_kernel(const BatchArgs b, uint32_t K) {
     const uint32_t e = blockIdx.x, lane = threadIdx.x, n = b.T * K;
+    const rsrc_t ids = make_rsrc(b.idx, n * 4u);  // past n: zeros, masked by i < n
     uint32_t base = 0;
-    for (uint32_t i0 = 0; i0 < n; i0 += 64) {
-        const uint32_t i = i0 + lane;
-        const bool hit = i < n && (uint32_t)gld(b.idx + i) == e;
-        const uint64_t bal = __builtin_amdgcn_ballot_w64(hit);
-        const uint32_t below = __builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
-        if (hit) gst(b.lists + (size_t)e * b.T + base + below, i);
-        base += (uint32_t)__builtin_popcountll(bal);
+    for (uint32_t i0 = 0; i0 < n; i0 += 64u * kCB) {
+        uint32_t id[kCB];
+#pragma unroll
+        for (uint32_t j = 0; j < kCB; j++)
+            id[j] = __builtin_amdgcn_raw_buffer_load_b32(ids, (int)(4u * (i0 + 64u * j + lane)), 0, 0);
+#pragma unroll
+        for (uint32_t j = 0; j < kCB; j++) {
+            const uint32_t i = i0 + 64u * j + lane;
+            const bool hit = i < n && id[j] == e;
+            const uint64_t bal = __builtin_amdgcn_ballot_w64(hit);
+            const uint32_t below =
+                __builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
+            if (hit) gst(b.lists + (size_t)e * b.T + base + below, i);
+            base += (uint32_t)__builtin_popcountll(bal);
+        }
     }
     if (lane == 0) gst(b.counts + e, base);
 }
@@ -1071,18 +1082,35 @@ __global__ void __launch_bounds__(kThreads) bdown_kernel(const DecodeArgs* __res
 
 // out[t] = (resid[t] +) sum_k w[t][k] e_k[t] in slot order + shared[t]
 // (reference pass 3, src/glm_layer_runner.cuh:904-921).
+// Thread: 4 consecutive rows (16-byte loads; H is a multiple of 128), each
+// with the scalar sequence acc = fma(w_k, e_k, acc) over k, + shared, + resid.
 __global__ void __launch_bounds__(256) bcomb_kernel(const BatchArgs b, uint32_t H, uint32_t K) {
     const uint32_t t = blockIdx.y;
-    const uint32_t r = blockIdx.x * blockDim.x + threadIdx.x;
+    const uint32_t r = 4u * (blockIdx.x * blockDim.x + threadIdx.x);
     if (r >= H) return;
-    float acc = 0.f;
+    float4 acc = {0.f, 0.f, 0.f, 0.f};
     for (uint32_t k = 0; k < K; k++) {
         const uint32_t c = gld(b.pos + (size_t)t * K + k);
-        acc = fmaf(gld(b.wts + (size_t)t * K + k), gld(b.expout + (size_t)c * H + r), acc);
+        const float w = gld(b.wts + (size_t)t * K + k);
+        const float4 x = *(const float4*)(b.expout + (size_t)c * H + r);
+        acc.x = fmaf(w, x.x, acc.x);
+        acc.y = fmaf(w, x.y, acc.y);
+        acc.z = fmaf(w, x.z, acc.z);
+        acc.w = fmaf(w, x.w, acc.w);
     }
-    acc += gld(b.shout + (size_t)t * H + r);
-    if (b.resid) acc = gld(b.resid + (size_t)t * H + r) + acc;
-    gst(b.out + (size_t)t * H + r, acc);
+    const float4 sh = *(const float4*)(b.shout + (size_t)t * H + r);
+    acc.x += sh.x;
+    acc.y += sh.y;
+    acc.z += sh.z;
+    acc.w += sh.w;
+    if (b.resid) {
+        const float4 rs = *(const float4*)(b.resid + (size_t)t * H + r);
+        acc.x = rs.x + acc.x;
+        acc.y = rs.y + acc.y;
+        acc.z = rs.z + acc.z;
+        acc.w = rs.w + acc.w;
+    }
+    *(float4*)(b.out + (size_t)t * H + r) = acc;
 }
 
 int launch_batched(const DecodeArgs* d_args, const BatchArgs& b, uint32_t H, uint32_t I, uint32_t SI, uint32_t E,
@@ -1119,7 +1147,7 @@ int launch_batched(const DecodeArgs* d_args, const BatchArgs& b, uint32_t H, uin
     hipLaunchKernelGGL(bpermute_kernel, dim3(std::min((nperm + 255u) / 256u, 8u * n_cu)), dim3(256), 0, s, b, H, K);
     hipLaunchKernelGGL(bup_kernel, dim3(resident((const void*)bup_kernel)), dim3(kThreads), gemm_lds, s, d_args, b);
     hipLaunchKernelGGL(bdown_kernel, dim3(resident((const void*)bdown_kernel)), dim3(kThreads), gemm_lds, s, d_args, b);
-    hipLaunchKernelGGL(bcomb_kernel, dim3((H + 255) / 256, b.T), dim3(256), 0, s, b, H, K);
+    hipLaunchKernelGGL(bcomb_kernel, dim3((H + 1023) / 1024, b.T), dim3(256), 0, s, b, H, K);
     return (int)hipGetLastError();
 }
 

@@ -644,6 +644,8 @@ wl_status wl_run_moe_batched(wl_ctx* c, uint32_t layer, uint32_t n_tokens, const
     if (n_tokens == 0 || n_tokens > 65535) return fail(c, WL_ERR_INVALID, "n_tokens=%u must be in [1,65535]", n_tokens);
     if (!d_hidden || !d_out || d_out == d_hidden || (d_resid && d_out == d_resid))
         return fail(c, WL_ERR_INVALID, "null or aliasing batched buffers");
+    if (((uintptr_t)d_hidden | (uintptr_t)d_out | (uintptr_t)d_resid) % 16u)
+        return fail(c, WL_ERR_INVALID, "batched buffers must be 16-byte aligned");
     const uint32_t E = c->cfg.n_routed_experts;
     if (c->n_bound[layer] != E)
         return fail(c, WL_ERR_NOT_RESIDENT, "batched layer %u needs every expert bound (%u of %u)", layer,
