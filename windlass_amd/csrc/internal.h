@@ -100,25 +100,29 @@ struct DecodeArgs {
     int32_t norm_topk;
 };
 
-// Per-call launch arguments (kernel arguments by value). A layer runs as
-// segment 0 (everything up to the published partials) and segment 1 (the
-// combine); a fused launch runs both (the combine waits for the epoch tags of
-// the partials it reads), the phased schedule runs each as its own launch.
-// The kernel is built with kernarg preloading: the record pointer and the
-// first 12 dwords below arrive in SGPRs, so the loads that start a layer (the
-// hidden state, the router row, the norm weight, the bias, the shared expert)
-// are issued without first waiting for a memory round trip to read their
-// addresses. The same pointers are also in the layer record (DecodeArgs) for
-// the other kernels.
+// Per-call launch arguments. A layer runs as segment 0 (everything up to the
+// published partials) and segment 1 (the combine); a fused launch runs both
+// (the combine waits for the epoch tags of the partials it reads), the phased
+// schedule runs each as its own launch. The decode kernel takes these as
+// separate scalar kernel arguments, the record pointer and the first fields
+// below up to `epoch` in front, and is built with kernarg preloading: those
+// 14 dwords arrive in SGPRs, so the loads that start a layer (the hidden
+// state, the norm weight, the router row, the shared expert and its logit
+// polls) are issued without first waiting for a memory round trip to read
+// their addresses. (A struct argument is not preloaded: its fields would be
+// read from the kernarg segment with scalar loads, two dependent round trips
+// before the first vector load.) The same pointers are also in the layer
+// record (DecodeArgs) for the other kernels.
 struct DecodeDyn {
     const float* hidden;        // [H] pre-norm residual stream
     const uint8_t* sh_native;   // the layer's shared expert (NativeShared)
     const uint16_t* router_w;   // [E][H] bf16
     const uint16_t* ln_w;       // [H] bf16 or null (= ones)
-    const float* bias;          // [E] f32
+    uint64_t* lslot;            // [E] the context's epoch-tagged logit slots
     uint32_t seg;               // bits 0-7: first segment, 8-15: last segment, 16: shared-expert tap on
     uint32_t epoch;             // different for every call of the context, never 0
     // not preloaded (read later in the layer)
+    const float* bias;          // [E] f32
     const uint8_t* const* slot_tab;  // [E] block pointers of this layer
     const float* resid;         // [H] or null: out = resid + moe
     float* out;                 // [H]
@@ -127,7 +131,7 @@ struct DecodeDyn {
     __host__ __device__ int32_t taps() const { return (int32_t)((seg >> 16) & 1u); }
 };
 // Dwords of kernel arguments the decode kernel preloads into SGPRs (the
-// record pointer, then DecodeDyn up to `epoch`).
+// record pointer, then hidden .. epoch).
 constexpr int kPreloadDwords = 14;
 
 // Dynamic LDS layout of the decode kernel (byte offsets).
@@ -140,15 +144,17 @@ struct LdsMap {
         auto al = [](uint32_t x) { return (x + 15u) & ~15u; };
         uint32_t o = 0;
         m.xp = o;   o += al(3u * (H + 8u) * 2u);
-        m.pv = o;   // normalised input; this work-group's partial; combine staging
-        uint32_t f32n = (p.G + 16u) * kRowBlock;
-        if (f32n < H) f32n = H;
-        o += al(f32n * 4u);
         m.rmp = o;  o += al(3u * (kSlice + 8u) * 2u);
         m.red = o;  o += kWaves * 64u * 4u;
         m.topk = o; o += al((2u * E + 64u) * 4u);
         m.slots = o; o += al(E * 8u);
         m.misc = o; o += 128u;
+        // last: its size depends on the grid, so no other offset does (the
+        // kernel's first loads then need no wait for the grid size)
+        m.pv = o;   // normalised input; this work-group's partial; combine staging
+        uint32_t f32n = (p.G + 16u) * kRowBlock;
+        if (f32n < H) f32n = H;
+        o += al(f32n * 4u);
         m.bytes = o;
         return m;
     }

@@ -78,8 +78,11 @@ WL_DEV void st_tag(uint64_t* p, uint32_t epoch, float x) {
 // every shape constant known; GLM = false reads the shapes from the record.
 template <bool GLM>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
-moe_decode_kernel(const DecodeArgs* __restrict__ pa, const DecodeDyn d) {
+moe_decode_kernel(const DecodeArgs* __restrict__ pa, const float* hidden, const uint8_t* sh_native,
+                  const uint16_t* router_w, const uint16_t* ln_w, uint64_t* lslot, uint32_t seg, uint32_t epoch,
+                  const float* bias, const uint8_t* const* slot_tab, const float* resid, float* out) {
     const DecodeArgs& a = *pa;
+    const DecodeDyn d{hidden, sh_native, router_w, ln_w, lslot, seg, epoch, bias, slot_tab, resid, out};
     const uint32_t H = GLM ? 6144u : a.H, I = GLM ? 2048u : a.I, SI = GLM ? 2048u : a.SI,
                    E = GLM ? 256u : a.E, K = GLM ? 8u : a.K;
     const uint32_t G = gridDim.x, w = blockIdx.x, tid = threadIdx.x;
@@ -109,11 +112,6 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const DecodeDyn d) {
     // ================= segment 0: everything but the combine ====================
     if (d.seg_lo() == 0u) {
         WL_TL(0);
-        // routing inputs that do not depend on this call's data, for experts
-        // e = tid (E <= 512; the rest later): consumed long after they land
-        const rsrc_t bs_rs = make_rsrc(d.bias, E * 4u), sl_rs = make_rsrc(d.slot_tab, E * 8u);
-        const uint32_t bias0 = __builtin_amdgcn_raw_buffer_load_b32(bs_rs, (int)(4u * tid), 0, 0);
-        const uint64_t slot0 = __builtin_bit_cast(uint64_t, __builtin_amdgcn_raw_buffer_load_b64(sl_rs, (int)(8u * tid), 0, 0));
         // hidden state and norm weight first: they are consumed first
         constexpr int HV = kHV;
         float4 hv[HV];
@@ -133,6 +131,14 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const DecodeDyn d) {
         u32x4 rw[RCH];
 #pragma unroll
         for (int m = 0; m < RCH; m++) rw[m] = bld16_nt(rt_rs, 16u * min(tid + kThreads * m, nch - 1u), min(w, E - 1u) * H * 2u);
+        // routing inputs that do not depend on this call's data, for experts
+        // e = tid (E <= 512; the rest later): consumed long after they land
+        // (their addresses are not preloaded: issued after the loads above,
+        // which the scheduling barrier keeps ahead of the wait for them)
+        __builtin_amdgcn_sched_barrier(0);
+        const rsrc_t bs_rs = make_rsrc(d.bias, E * 4u), sl_rs = make_rsrc(d.slot_tab, E * 8u);
+        const uint32_t bias0 = __builtin_amdgcn_raw_buffer_load_b32(bs_rs, (int)(4u * tid), 0, 0);
+        const uint64_t slot0 = __builtin_bit_cast(uint64_t, __builtin_amdgcn_raw_buffer_load_b64(sl_rs, (int)(8u * tid), 0, 0));
 
         // shared gate/up tiles (8 gate + 8 up rows). At G = SI/8 (GLM) the
         // tiles are mapped so that the 32 work-groups of one XCD hold 32
@@ -151,7 +157,7 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const DecodeDyn d) {
         // every shared batch also reads the logit slot of expert min(tid, E-1)
         // (agent scope): the logits published while the shared expert streams
         // are collected on the way, without a separate round trip
-        const rsrc_t ls_rs = make_rsrc(a.lslot, E * 8u);
+        const rsrc_t ls_rs = make_rsrc(d.lslot, E * 8u);
         const uint32_t pe = min(tid, E - 1u);
         auto sg_issue = [&](uint32_t tile, uint32_t b, SBatch& B) {
             const uint32_t voff = min(tile, nsg - 1u) * nkt * 1024u + 16u * lane;
@@ -238,7 +244,7 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const DecodeDyn d) {
 #pragma unroll
                 for (int m = 0; m < RCH; m++) rw[m] = bld16_nt(rt_rs, 16u * min(tid + kThreads * m, nch - 1u), r * H * 2u);
             }
-            router_publish(router_partial(rw, xn, nch), red, a.lslot, r, d.epoch);
+            router_publish(router_partial(rw, xn, nch), red, d.lslot, r, d.epoch);
         }
         WL_TL(2);
 
@@ -255,7 +261,7 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const DecodeDyn d) {
                 bool mine = true;
                 for (uint32_t i = 0, e = tid; e < E; i++, e += kThreads) {
                     if ((done >> i) & 1u) continue;
-                    const uint64_t x = __hip_atomic_load((__attribute__((address_space(1))) uint64_t*)(a.lslot + e),
+                    const uint64_t x = __hip_atomic_load((__attribute__((address_space(1))) uint64_t*)(d.lslot + e),
                                                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                     if ((uint32_t)(x >> 32) == d.epoch) {
                         topk_score(__uint_as_float((uint32_t)x), tk_ch[e], e, tk_sc, tk_ch);
@@ -934,12 +940,14 @@ int launch_decode(const DecodeArgs* d_args, const DecodeDyn& dyn, uint32_t H, ui
                                                : (const void*)moe_decode_kernel<false>;
     hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return (int)e;
+#define WL_DECODE_ARGS                                                                                        \
+    d_args, dyn.hidden, dyn.sh_native, dyn.router_w, dyn.ln_w, dyn.lslot, dyn.seg, dyn.epoch, dyn.bias, dyn.slot_tab, \
+        dyn.resid, dyn.out
     if (glm_shape(H, I, SI, E, K))
-        hipLaunchKernelGGL(moe_decode_kernel<true>, dim3(grid), dim3(kThreads), lds, (hipStream_t)stream, d_args,
-                           dyn);
+        hipLaunchKernelGGL(moe_decode_kernel<true>, dim3(grid), dim3(kThreads), lds, (hipStream_t)stream, WL_DECODE_ARGS);
     else
-        hipLaunchKernelGGL(moe_decode_kernel<false>, dim3(grid), dim3(kThreads), lds, (hipStream_t)stream, d_args,
-                           dyn);
+        hipLaunchKernelGGL(moe_decode_kernel<false>, dim3(grid), dim3(kThreads), lds, (hipStream_t)stream, WL_DECODE_ARGS);
+#undef WL_DECODE_ARGS
     return (int)hipGetLastError();
 }
 

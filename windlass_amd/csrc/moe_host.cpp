@@ -535,6 +535,7 @@ static wl_status run_layer(wl_ctx* c, uint32_t layer, const float* d_hidden, con
     dyn.sh_native = L.shared;
     dyn.router_w = L.router_w;
     dyn.ln_w = L.ln;
+    dyn.lslot = c->lslot;
     dyn.bias = L.bias;
     dyn.slot_tab = c->d_slot + (size_t)layer * E;
     dyn.resid = d_resid;
