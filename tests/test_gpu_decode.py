@@ -127,6 +127,28 @@ def test_layer_config1(gpu, glm_model, step):
           flush=True)
 
 
+def test_layer_config1_with_norm_weight(gpu):
+    """The GLM-shape kernel with a post-attention norm weight (a separate
+    kernel argument of its own) under both schedules."""
+    hip = gpu
+    H = GLM["hidden"]
+    ln = [(1.0 + synth.bf16_to_f32(synth.normal_bf16(5, 0, synth.TAG_LN, (H,), 0.25))).astype(np.float32)]
+    ln = [synth.f32_to_bf16(ln[0])]
+    dm = DeviceModel(GLM, seed=2, n_layers=1, ln_weights=ln)
+    h = synth.hidden_state(H, 321)
+    ref = O.moe_layer(h, dm.dense[0], O.ExpertSource(H, GLM["moe_inter"], 2), 0, GLM,
+                      ln_w=synth.bf16_to_f32(ln[0]))
+    for sched in [moe.SCHED_FUSED, moe.SCHED_PHASED]:
+        dm.ctx.set_schedule(sched)
+        dh, dout = make_io(H)
+        dh.upload(h)
+        dm.ctx.run_moe(0, dh.ptr, dout.ptr)
+        dm.ctx.check_error()
+        r = _check_layer(ref, _taps(dm, hip), dout.download(np.float32), f"ln sched{sched}")
+        print(f"config1 with norm weight, schedule {sched}: out rel_to_scale {r:.3e}", flush=True)
+    dm.ctx.close()
+
+
 def test_schedules_identical_and_stable(gpu, glm_model):
     hip = gpu
     dm = glm_model
