@@ -1,31 +1,33 @@
 // moe_decode.hip — gfx950 kernels of the bs=1 MoE decode layer.
 //
 // One persistent launch of G work-groups (one per CU, 8 wave64s each) runs a
-// layer in three segments separated by grid barriers:
+// layer in two segments (the phased schedule launches each on its own). No
+// grid barrier: values another work-group needs (a logit, a partial sum) are
+// 64-bit words epoch << 32 | f32 bits written with agent-scope stores, and the
+// reader polls, with a bounded wait, until it sees this call's epoch.
 //
 //   0  every work-group normalises the hidden state (RMSNorm, redundantly),
-//      computes one router row (logit) and one 8-gate + 8-up tile of the bf16
-//      shared expert, and publishes the logit and the 8 SwiGLU values.
-//      reference: rms_norm_bf16, matvec_bf16 (router), shared expert gate/up,
-//      src/glm_primitives.cuh:35-62,87-116, src/glm_layer_runner.cuh:370,387,431
-//   1  every work-group recomputes the top-k from the published logits
+//      computes its router row and publishes the logit, and streams one
+//      8-gate + 8-up tile of the bf16 shared expert, whose batches also read
+//      the published logits on the way. Then the top-k, on every work-group
 //      (sigmoid, +e_score_correction_bias, top-K with ties to the lowest index,
-//      renormalise, x routed_scaling; src/glm_layer_runner.cuh:304-336), then
-//      (a) applies 3 (16-row tile, k-half) units of the shared down projection,
-//          whose weights it loaded before the barrier, and
-//      (b) runs one routed unit (expert slot k, slice j): the 64 SwiGLU rows
-//          [64j, 64j+64) of expert k — MXFP4 gate/up, kept in LDS — times
-//          the 64 matching columns of its MXFP4 down projection, i.e. a
-//          split-K partial of expert k's output over all H rows.
-//      reference: dequant_matvec_mxfp4 x3 + silu_mul, src/glm_kernels.cuh:63-110,
-//      src/glm_layer_runner.cuh:338-341,424-427
-//   2  work-groups combine blocks of 32 output rows: e_k = sum_j partial(k, j),
-//      out = sum_k w_k e_k (slot order) + shared (src/glm_layer_runner.cuh:
-//      403,428,436).
+//      renormalise, x routed_scaling; src/glm_layer_runner.cuh:304-336), the
+//      tile's SwiGLU and its 8 columns of the shared down projection, and one
+//      routed unit (expert slot k, slice j): the 64 SwiGLU rows [64j, 64j+64)
+//      of expert k (MXFP4 gate/up) times the 64 matching columns of its MXFP4
+//      down projection, i.e. a split-K partial of expert k's output over all H
+//      rows, weighted by w_k and added to the shared columns' partial. The
+//      work-group's partial vector is published as tagged words.
+//      reference: rms_norm_bf16, matvec_bf16 (router), dequant_matvec_mxfp4 x3
+//      + silu_mul, shared expert; src/glm_primitives.cuh:35-62,87-116,
+//      src/glm_kernels.cuh:63-110, src/glm_layer_runner.cuh:338-341,370-436
+//   1  work-groups combine blocks of 32 output rows: the sum of the G partials
+//      (fixed order), + the residual when one is given (src/glm_layer_runner.cuh:
+//      403,428,436,675).
 //
 // Splitting the down projection by the SwiGLU slice a work-group computed
 // means no work-group waits for another one's SwiGLU output: the only
-// cross-work-group dependencies are the two grid barriers. Work-group w runs
+// cross-work-group waits are the logits and the partials. Work-group w runs
 // routed unit u = w, i.e. expert slot w mod 8 at K = 8; work-groups are
 // dispatched round-robin over the 8 XCDs, so all 32 slices of one expert run
 // on one XCD and the down-projection rows they share (32 bytes each per
