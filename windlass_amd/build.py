@@ -15,9 +15,10 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 # wrong results on this hardware without any error.
 DEVICE_FLAGS = ["--offload-arch=gfx950", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 # Kernel arguments preloaded into SGPRs (gfx950 kernarg preloading): the
-# first dwords of every kernel's arguments are in registers when its waves
-# start, so the first loads of the decode kernel need no memory round trip to
-# learn their addresses. 14 = internal.h kPreloadDwords.
+# first dwords of every kernel's scalar arguments are in registers when its
+# waves start (a struct argument is not preloaded), so the first loads of the
+# decode kernel need no memory round trip to learn their addresses.
+# 14 = internal.h kPreloadDwords.
 PRELOAD_FLAGS = ["-mllvm", "-amdgpu-kernarg-preload-count=14"]
 COMMON = ["-O3", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-function", "-Wno-unknown-pragmas"]
 

@@ -78,6 +78,9 @@ WL_DEV void st_tag(uint64_t* p, uint32_t epoch, float x) {
 // ---- the decode kernel -------------------------------------------------------
 // GLM = true compiles the GLM shape (H 6144, I 2048, SI 2048, E 256, K 8) with
 // every shape constant known; GLM = false reads the shapes from the record.
+// The preloaded arguments: the record pointer, the five pointers up to lslot,
+// seg and epoch.
+static_assert(6 * sizeof(void*) / 4 + 2 == kPreloadDwords, "preloaded kernel arguments");
 template <bool GLM>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 moe_decode_kernel(const DecodeArgs* __restrict__ pa, const float* hidden, const uint8_t* sh_native,
