@@ -59,6 +59,86 @@ def algorithmic_bytes(c):
     return K * expert + 3 * SI * H * 2 + E * H * 2 + E * 4 + 2 * H * 4
 
 
+def host_cores():
+    """(physical cores, logical CPUs) this process may run on: the distinct
+    (core, socket) pairs lscpu lists for the CPUs of the affinity set."""
+    import subprocess
+    cpus = os.sched_getaffinity(0)
+    try:
+        out = subprocess.run(["lscpu", "-p=CPU,CORE,SOCKET"], capture_output=True, text=True, check=True).stdout
+        pairs = set()
+        for ln in out.splitlines():
+            if ln.startswith("#"):
+                continue
+            cpu, core, sock = ln.split(",")[:3]
+            if int(cpu) in cpus:
+                pairs.add((core, sock))
+        phys = len(pairs) or len(cpus)
+    except (OSError, ValueError, subprocess.CalledProcessError):
+        phys = len(cpus)
+    return phys, len(cpus)
+
+
+def cpu_baseline_batched(c, seed, hb, bias_offset, threads, n_expert_sample=3, n_apply_sample=8,
+                         n_route_sample=32, n_shared_sample=4):
+    """The reference's batched layer on the CPU (tools/ref_glm_chain.py:789-868,
+    passes 2-4: route every position, then EXPERT-major: each routed expert
+    dequantised once and applied position by position with matvecs, then the
+    per-position combine), timed on a bounded sample and extrapolated:
+    routing per position (first n_route_sample positions), dequant per expert
+    and per-position expert applications (the first n_expert_sample experts in
+    sorted order, up to n_apply_sample applications each), shared expert per
+    position (n_shared_sample positions). Returns (us per call, sample text)."""
+    from threadpoolctl import threadpool_limits
+
+    from oracle import moe_oracle as O
+    from oracle import synth
+    H, I, E, K = c["hidden"], c["moe_inter"], c["n_routed_experts"], c["n_experts_per_tok"]
+    T = hb.shape[0]
+    dense = synth.dense_layer(H, E, I * c["n_shared"], seed, 0)
+    bias = (dense["bias"] + bias_offset).astype(np.float32)
+    rw = synth.bf16_to_f32(dense["router_w"]).reshape(E, H)
+    SG, SU, SD = O.shared_matrices(dense, H, I * c["n_shared"])
+    with threadpool_limits(limits=threads):
+        prep = []
+        t0 = time.perf_counter()
+        for t in range(T):
+            xn = O.rms_norm(hb[t], None, c["rms_eps"])
+            _, idx, wt, _ = O.route(xn, rw, bias, K, c["routed_scaling"], True)
+            prep.append((xn, idx, wt))
+            if t + 1 == n_route_sample:
+                t_route = (time.perf_counter() - t0) / n_route_sample
+        if T < n_route_sample:
+            t_route = (time.perf_counter() - t0) / T
+        routed = {}
+        for t, (_, idx, _) in enumerate(prep):
+            for k, e in enumerate(idx):
+                routed.setdefault(int(e), []).append((t, k))
+        t_deq, t_app = [], []
+        for e in sorted(routed)[:n_expert_sample]:
+            gw, gs, uw, us, dw, ds = synth.expert_block(H, I, seed, 0, e)
+            t0 = time.perf_counter()
+            G, U, D = O.dequant(gw, gs), O.dequant(uw, us), O.dequant(dw, ds)
+            t_deq.append(time.perf_counter() - t0)
+            for t, k in routed[e][:n_apply_sample]:
+                t0 = time.perf_counter()
+                O.expert_slot(prep[t][0], G, U, D)
+                t_app.append(time.perf_counter() - t0)
+        t_sh = []
+        for t in range(min(T, n_shared_sample)):
+            t0 = time.perf_counter()
+            O.silu(prep[t][0] @ SG.T) * (prep[t][0] @ SU.T) @ SD.T
+            t_sh.append(time.perf_counter() - t0)
+    uniq = len(routed)
+    total = (t_route * T + float(np.mean(t_deq)) * uniq + float(np.median(t_app)) * T * K
+             + float(np.median(t_sh)) * T)
+    text = (f"numpy oracle in the reference's batched order (route every position; each of the {uniq} experts "
+            f"dequantised once, then {T * K} per-position expert matvec applications; shared expert per position); "
+            f"timed on routing of {min(T, n_route_sample)} positions, dequant of {len(t_deq)} experts, "
+            f"{len(t_app)} expert applications and {len(t_sh)} shared applications, extrapolated to T={T}")
+    return total * 1e6, text
+
+
 def cpu_baseline(c, seed, n_layers_sample, threads):
     """The numpy oracle (the reference's algorithm: dequantise to fp32, then
     BLAS matvecs; tools/ref_glm_chain.py:646-711) on this host, over a small
@@ -117,7 +197,8 @@ def main():
     ap.add_argument("--zipf-amp", type=float, default=0.25,
                     help="cache workload: bias offset of the most popular expert (rank r gets amp * r^-1.1)")
     ap.add_argument("--seed", type=int, default=1)
-    ap.add_argument("--cpu-sample", type=int, default=3, help="layers timed for the CPU baseline (0: skip)")
+    ap.add_argument("--cpu-sample", type=int, default=6,
+                    help="layers timed for the CPU baseline after one warm-up, median reported (0: skip)")
     ap.add_argument("--traffic-json", default=os.path.join(ROOT, "profiles", "decode_layer_traffic.json"))
     ap.add_argument("--calib-copy-mb", type=int, default=0,
                     help="after the timed steps, one device-to-device copy of this many MiB (the reference "
@@ -161,9 +242,8 @@ def main():
             args.steps = 20
         if "--warmup" not in sys.argv:
             args.warmup = 3
-        dm = DeviceModel(c, seed=args.seed, n_layers=1,
-                         bias_offset=synthdata.zipf_bias_offset(c["n_routed_experts"], args.seed,
-                                                                amplitude=args.zipf_amp))
+        zipf_off = synthdata.zipf_bias_offset(c["n_routed_experts"], args.seed, amplitude=args.zipf_amp)
+        dm = DeviceModel(c, seed=args.seed, n_layers=1, bias_offset=zipf_off)
     else:
         dm = DeviceModel(c, seed=args.seed, n_layers=args.layers)
     dm.ctx.set_schedule(moe.SCHED_FUSED if args.sched == "fused" else moe.SCHED_PHASED)
@@ -238,14 +318,21 @@ def main():
 
     cpu = None
     if args.cpu_sample > 0:
-        ncores = len(os.sched_getaffinity(0))
-        ncores = min(ncores, 16)  # the box's CPU share for one GPU
-        us_all, n_all = cpu_baseline(c, args.seed, args.cpu_sample, ncores)
-        us_one, n_one = cpu_baseline(c, args.seed, max(1, args.cpu_sample - 1), 1)
-        cpu = {"value": round(us_all, 1), "unit": "us/layer", "cores": ncores, "kind": "port",
-               "sample": f"numpy oracle (dequant to f32 + OpenBLAS matvecs) on {n_all} config-1 layers, median; "
-                         f"router+8 experts+shared; expert bytes pre-generated"
-                         + ("; a chain token is 24 such layers (extrapolated x24)" if chain else ""),
+        phys, logical = host_cores()
+        ncores = min(phys, 16)  # physical cores, at most the box's CPU share for one GPU
+        if batched:
+            us_all, text = cpu_baseline_batched(c, args.seed, hb, zipf_off, ncores)
+            us_one, _ = cpu_baseline_batched(c, args.seed, hb, zipf_off, 1)
+            unit = "us/call"
+        else:
+            us_all, n_all = cpu_baseline(c, args.seed, args.cpu_sample, ncores)
+            us_one, n_one = cpu_baseline(c, args.seed, args.cpu_sample, 1)
+            unit = "us/layer"
+            text = (f"numpy oracle (dequant to f32 + OpenBLAS matvecs) on {n_all} config-1 layers after one "
+                    f"warm-up, median; router+8 experts+shared; expert bytes pre-generated"
+                    + ("; a chain token is 24 such layers (extrapolated x24)" if chain else ""))
+        cpu = {"value": round(us_all, 1), "unit": unit, "cores": ncores, "kind": "port", "sample": text,
+               "host_physical_cores": phys, "host_logical_cpus": logical,
                "value_1thread": round(us_one, 1), "gpu_speedup": round(us_all / us_per_layer, 1)}
 
     line = {
@@ -276,6 +363,9 @@ def main():
         "pct_of_hbm_peak": round(100 * achieved / PEAK_HBM_GBPS, 2),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
                      "frac": round(achieved / PEAK_HBM_GBPS, 4), "traffic": traffic,
+                     "traffic_source": (f"stored figure, not measured in this run: {os.path.relpath(args.traffic_json, ROOT)} "
+                                        "(rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE runs of this bench command, "
+                                        "scaled by a copy-kernel calibration)") if traffic is not None else None,
                      "algorithmic_bytes": nbytes,
                      "kernel": ("whole batched call (bup_kernel + bdown_kernel dominate)" if batched else
                                 "moe_decode_kernel")},

@@ -15,6 +15,16 @@
  *
  * Threading: one host thread per context. All device work of a call is
  * enqueued on the stream passed to that call, in call order.
+ *
+ * Co-residency: the decode and routing kernels run one work-group per CU, and
+ * those work-groups wait for each other's data (router logits, partial sums)
+ * with bounded polls. wl_create checks that the chip can hold the whole grid
+ * at once. While a layer runs, no other kernel may occupy the device's CUs
+ * (a kernel on another stream, another process's context): a work-group left
+ * unscheduled makes the others' waits expire, and the call reports
+ * WL_ERR_DEVICE (E_SPIN) through wl_check_error instead of hanging. An error
+ * aborts only the call that raised it; later calls run normally, while the
+ * error bits stay set until wl_check_error reads them.
  */
 #ifndef WINDLASS_MOE_H
 #define WINDLASS_MOE_H
@@ -189,9 +199,9 @@ wl_status wl_taps(wl_ctx* ctx, wl_taps_out* out);
 wl_status wl_check_error(wl_ctx* ctx, void* stream);
 
 /* Execution schedule of wl_run_moe: WL_SCHED_FUSED runs one persistent
- * kernel per layer (a grid barrier before the final combine); WL_SCHED_PHASED
- * runs the combine as a second stream-ordered launch. Both compute identical
- * results. */
+ * kernel per layer, whose combine waits for the epoch-tagged partial sums of
+ * the other work-groups (no grid barrier); WL_SCHED_PHASED runs the combine as
+ * a second stream-ordered launch. Both compute identical results. */
 #define WL_SCHED_FUSED  0
 #define WL_SCHED_PHASED 1
 wl_status wl_set_schedule(wl_ctx* ctx, int32_t sched);

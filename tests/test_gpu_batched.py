@@ -132,6 +132,77 @@ def test_glm_batched_64_vs_decode(gpu):
     dm.close()
 
 
+def _oracle_tokens(ids, T, kmt=32, want=10):
+    """Tokens to check against the oracle: the first and the last, and tokens
+    of the two experts with the most tokens (more than kmt of them, i.e. run
+    in several passes): the first of each pass boundary and the last."""
+    lists = {}
+    for t in range(T):
+        for e in ids[t]:
+            lists.setdefault(int(e), []).append(t)
+    hot = sorted(lists, key=lambda e: -len(lists[e]))[:2]
+    pick = [0, T - 1]
+    multi = []
+    for e in hot:
+        ts = lists[e]
+        if len(ts) > kmt:
+            multi.append(e)
+            pick += [ts[kmt - 1], ts[kmt], ts[-1]]
+    step = max(1, T // want)
+    for t in range(step // 2, T, step):
+        if len(set(pick)) >= want:
+            break
+        pick.append(t)
+    return sorted(set(pick)), multi, {e: len(lists[e]) for e in hot}
+
+
+@pytest.mark.parametrize("T", [256, 1024])
+def test_glm_batched_zipf_vs_decode_and_oracle(gpu, T):
+    """Config 3 at the GLM shape with the benchmark's Zipf(1.1) router bias:
+    every token's routing equals the decode path's bit for bit and its output
+    is within 1e-5 of the decode path's; at least 8 tokens (the first, the
+    last, and tokens on both sides of a 32-token pass boundary of the busiest
+    experts) are within 1e-5 of the oracle."""
+    c = GLM
+    H = c["hidden"]
+    zipf = synthdata.zipf_bias_offset(c["n_routed_experts"], 15, amplitude=0.25)
+    dm = DeviceModel(c, seed=15, n_layers=1, bias_offset=zipf)
+    hs = _tokens(H, T, 600 + T)
+    out = _batched(dm, hs)
+    lg, ids, w = dm.ctx.batched_routing(T)
+    counts = dm.ctx.batched_counts()
+    assert int(counts.sum()) == T * c["n_experts_per_tok"]
+    dh, dout = make_io(H)
+    worst = 0.0
+    tp = dm.ctx.taps()
+    E, K = c["n_routed_experts"], c["n_experts_per_tok"]
+    for t in range(T):
+        dh.upload(hs[t])
+        dm.ctx.run_moe(0, dh.ptr, dout.ptr)
+        dm.ctx.check_error()
+        dec = dout.download(np.float32)
+        assert np.array_equal(lg[t].view(np.uint32), H_.download_ptr(tp["logits"], np.float32, E).view(np.uint32)), t
+        assert np.array_equal(ids[t], H_.download_ptr(tp["topk_idx"], np.int32, K)), t
+        assert np.array_equal(w[t].view(np.uint32), H_.download_ptr(tp["topk_w"], np.float32, K).view(np.uint32)), t
+        r = O.rel_to_scale(dec, out[t])
+        worst = max(worst, r)
+        assert r < TOL, (t, r)
+    pick, multi, hot = _oracle_tokens(ids, T)
+    assert len(pick) >= 8
+    assert multi, f"no expert ran more than one 32-token pass at T={T}: {hot}"
+    src = O.ExpertSource(H, c["moe_inter"], 15, cache=48)
+    worst_ref = 0.0
+    for t in pick:
+        ref = O.moe_layer(hs[t], dm.dense[0], src, 0, c)
+        assert np.array_equal(np.sort(ref["topk_idx"]), np.sort(ids[t])), t
+        r = O.rel_to_scale(ref["out"], out[t])
+        worst_ref = max(worst_ref, r)
+        assert r < TOL, (t, r)
+    print(f"GLM T={T}: experts used {int((counts > 0).sum())}, busiest {hot}, "
+          f"worst vs decode {worst:.2e}, worst vs oracle {worst_ref:.2e} over tokens {pick}", flush=True)
+    dm.close()
+
+
 def test_misaligned_or_aliasing_buffers_rejected(gpu):
     """The combine reads and writes rows 16 bytes at a time: buffers that are
     not 16-byte aligned are an argument error (nothing is launched)."""

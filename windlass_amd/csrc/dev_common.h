@@ -155,9 +155,14 @@ WL_DEV void st_sync(uint32_t* p, uint32_t v) {
 WL_DEV uint32_t rmw_inc(uint32_t* p) {
     return __hip_atomic_fetch_add((g_u32*)p, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-WL_DEV void raise_error(uint32_t* sync, const SyncMap& m, uint32_t bits) {
+// Records error bits (sticky) and marks call `epoch` as aborted, so the other
+// work-groups of this call stop waiting for data that will not come.
+WL_DEV void raise_error(uint32_t* sync, const SyncMap& m, uint32_t bits, uint32_t epoch) {
     __hip_atomic_fetch_or((g_u32*)(sync + m.error), bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    st_sync(sync + m.abort, epoch);
 }
+// Whether call `epoch` was aborted by one of its work-groups.
+WL_DEV bool aborted(uint32_t* sync, const SyncMap& m, uint32_t epoch) { return ld_sync(sync + m.abort) == epoch; }
 
 
 // Sum over the 512 threads of the work-group (result in every thread).

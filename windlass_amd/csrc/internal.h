@@ -39,12 +39,19 @@ enum : uint32_t {
 };
 
 // Word offsets inside the uncached synchronisation block.
+//   error  sticky error bits, accumulated over calls until wl_check_error
+//          reads and clears them
+//   abort  the epoch of the last call that raised an error: a wait gives up
+//          early only when this equals its own call's epoch, so an error of
+//          one call never cuts short the waits of a later one
 struct SyncMap {
-    uint32_t error;     // sticky error bits
+    uint32_t error;
+    uint32_t abort;
     uint32_t words;
     __host__ __device__ static SyncMap make() {
         SyncMap m;
         m.error = 0;
+        m.abort = kLineWords / 2;
         m.words = kLineWords;
         return m;
     }
@@ -244,6 +251,10 @@ struct BatchArgs {
 int launch_decode(const DecodeArgs* d_args, const DecodeDyn& dyn, uint32_t H, uint32_t I, uint32_t SI,
                   uint32_t E, uint32_t K, uint32_t grid, void* stream);
 int decode_max_lds();
+// Work-groups of the decode / routing kernel one CU can hold at once
+// (hipOccupancyMaxActiveBlocksPerMultiprocessor at the kernel's LDS size).
+int decode_occupancy(uint32_t H, uint32_t I, uint32_t SI, uint32_t E, uint32_t K, uint32_t grid, int* per_cu);
+int route_occupancy(uint32_t H, uint32_t E, int* per_cu);
 // Routing only (cache-backed layers): norm, router, top-k -> idx/topw/logits.
 size_t route_lds_bytes(uint32_t H, uint32_t E);
 int launch_route(const DecodeArgs* d_args, const float* hidden, uint32_t epoch, uint32_t H, uint32_t E,

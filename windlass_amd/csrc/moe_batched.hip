@@ -720,7 +720,7 @@ struct UpK {
         cu = unit(i);
         cps = pass_shape(cu.nt);
         cvar = (cps.pr ? 0u : 2u) + cps.nblk - 1u;
-        if (!cu.sh && stab[cu.e] == nullptr && threadIdx.x == 0) raise_error(a.sync, SyncMap::make(), E_NOT_RESIDENT);
+        if (!cu.sh && stab[cu.e] == nullptr && threadIdx.x == 0) raise_error(a.sync, SyncMap::make(), E_NOT_RESIDENT, 0u);  // no waits in this path: epoch 0 aborts nothing
 #pragma unroll
         for (uint32_t j = 0; j < kSG; j++) acc[j][0] = acc[j][1] = f32x4{0.f, 0.f, 0.f, 0.f};
     }

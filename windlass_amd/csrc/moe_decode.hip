@@ -277,8 +277,8 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const float* hidden, const 
                     }
                 }
                 if (block_all(mine, misc)) break;
-                if (spins > (1u << 20) || ld_sync(a.sync + SM.error) != 0u) {
-                    if (tid == 0 && spins > (1u << 20)) raise_error(a.sync, SM, E_SPIN);
+                if (spins > (1u << 20) || aborted(a.sync, SM, d.epoch)) {
+                    if (tid == 0 && spins > (1u << 20)) raise_error(a.sync, SM, E_SPIN, d.epoch);
                     return false;
                 }
                 __builtin_amdgcn_s_sleep(2);
@@ -496,7 +496,7 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const float* hidden, const 
             blk = uni_ptr(tk_blk[tk_idx[uk]]);
             wk = topk_weight(a, K, tk_w, uk);
             if (blk == nullptr) {
-                if (tid == 0) raise_error(a.sync, SM, E_NOT_RESIDENT);
+                if (tid == 0) raise_error(a.sync, SM, E_NOT_RESIDENT, d.epoch);
                 continue;
             }
             if (!first_unit) lds_barrier();  // rmp of the previous unit fully read
@@ -566,10 +566,10 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const float* hidden, const 
                     }
                     if (stale == 0u) break;
                     if (spins >= (1u << 20)) {
-                        raise_error(a.sync, SM, E_SPIN);
+                        raise_error(a.sync, SM, E_SPIN, d.epoch);
                         break;
                     }
-                    if ((spins & 63u) == 63u && ld_sync(a.sync + SM.error) != 0u) break;
+                    if ((spins & 63u) == 63u && aborted(a.sync, SM, d.epoch)) break;
                     __builtin_amdgcn_s_sleep(2);
 #pragma unroll
                     for (uint32_t i = 0; i < kGrp; i++)  // every stale chunk again, all in flight together
@@ -679,7 +679,7 @@ __global__ void __launch_bounds__(kThreads) route_kernel(const DecodeArgs* __res
         }
         if (block_all(mine, flags)) break;
         if (spins > (1u << 20)) {
-            if (tid == 0) raise_error(a.sync, SM, E_SPIN);
+            if (tid == 0) raise_error(a.sync, SM, E_SPIN, epoch);
             return;
         }
         __builtin_amdgcn_s_sleep(2);
@@ -910,6 +910,23 @@ static bool glm_shape(uint32_t H, uint32_t I, uint32_t SI, uint32_t E, uint32_t 
 }
 
 int decode_max_lds() { return 160 * 1024; }
+
+int decode_occupancy(uint32_t H, uint32_t I, uint32_t SI, uint32_t E, uint32_t K, uint32_t grid, int* per_cu) {
+    const Plan p = Plan::make(H, I, SI, K, grid);
+    const size_t lds = LdsMap::make(H, SI, E, K, p).bytes;
+    const void* fn = glm_shape(H, I, SI, E, K) ? (const void*)moe_decode_kernel<true>
+                                               : (const void*)moe_decode_kernel<false>;
+    hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e == hipSuccess) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(per_cu, fn, kThreads, lds);
+    return (int)e;
+}
+
+int route_occupancy(uint32_t H, uint32_t E, int* per_cu) {
+    const size_t lds = route_lds_bytes(H, E);
+    hipError_t e = hipFuncSetAttribute((const void*)route_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e == hipSuccess) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(per_cu, (const void*)route_kernel, kThreads, lds);
+    return (int)e;
+}
 
 size_t route_lds_bytes(uint32_t H, uint32_t E) {
     return 4u * (((H + 3u) & ~3u) + kWaves * 64u + 2u * E + 64u + 8u);

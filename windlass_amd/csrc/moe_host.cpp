@@ -52,12 +52,15 @@ struct CacheState {
     std::vector<std::pair<uint32_t, uint8_t*>> resolved;  // last wl_cache_prefetch: key -> block
 };
 
-// Scratch of the batched layer, sized for `cap` tokens.
+// Scratch of the batched layer: one allocation sized for `cap` tokens
+// (wl_run_moe_batched). `last` holds the buffers and token count of the
+// last chunk run (read by the test hooks).
 struct BatchScratch {
     uint32_t cap = 0;
-    uint32_t last_T = 0;  // tokens of the last chunk run
-    std::vector<void*> bufs;
+    void* buf = nullptr;
     wl::BatchArgs b{};
+    wl::BatchArgs last{};
+    bool ran = false;
 };
 
 struct wl_ctx {
@@ -248,8 +251,10 @@ wl_status wl_create(const wl_moe_config* cfg, wl_ctx** out) {
     c->n_cu = prop.multiProcessorCount;
     const uint32_t H = cfg->hidden, I = cfg->moe_inter, E = cfg->n_routed_experts,
                    K = cfg->n_experts_per_tok, L = cfg->n_layers, SI = c->SI;
-    // one work-group per CU (all resident at once: the fused launch has grid
-    // barriers), a multiple of 8 so every XCD holds the same number
+    // one work-group per CU, a multiple of 8 so every XCD holds the same
+    // number. Work-groups of one launch wait for each other's data (logits,
+    // partial sums), so all of them must be resident at once: checked below
+    // against the occupancy the kernels' LDS and register use allow.
     uint32_t grid = (uint32_t)c->n_cu;
     if (const char* env = getenv("WL_DECODE_GRID")) {
         const int gv = atoi(env);
@@ -263,6 +268,18 @@ wl_status wl_create(const wl_moe_config* cfg, wl_ctx** out) {
     if ((int)lm.bytes > wl::decode_max_lds()) {
         delete c;
         return WL_ERR_INVALID;
+    }
+    {
+        int per_cu_decode = 0, per_cu_route = 0;
+        if (wl::decode_occupancy(H, I, SI, E, K, grid, &per_cu_decode) != 0 ||
+            wl::route_occupancy(H, E, &per_cu_route) != 0) {
+            delete c;
+            return WL_ERR_HIP;
+        }
+        if ((uint64_t)per_cu_decode * (uint64_t)c->n_cu < grid || (uint64_t)per_cu_route * (uint64_t)c->n_cu < grid) {
+            delete c;
+            return WL_ERR_INVALID;  // the grid could not be co-resident
+        }
     }
 
     c->layers.resize(L);
@@ -293,6 +310,7 @@ wl_status wl_create(const wl_moe_config* cfg, wl_ctx** out) {
         return WL_ERR_OOM;
     }
     c->sync = (uint32_t*)c->uc_block;
+
     e = hipMemset(c->d_slot, 0, sizeof(void*) * (size_t)L * E);
     // epoch 0 is never a call's: zeroed tagged arrays hold no valid word (a
     // reused allocation could otherwise carry another context's tags)
@@ -319,7 +337,7 @@ void wl_destroy(wl_ctx* c) {
         if (C.h_ids) (void)hipHostFree(C.h_ids);
         delete C.lru;
     }
-    for (void* p : c->batch.bufs) (void)hipFree(p);
+    if (c->batch.buf) (void)hipFree(c->batch.buf);
     for (void* p : c->allocs) (void)hipFree(p);
     uc_release(c->device, c->uc_bytes, c->uc_block);
     delete c;
@@ -432,6 +450,10 @@ static wl_status cache_resolve(wl_ctx* c, uint32_t layer, const int32_t* ids, ui
         const uint32_t key = layer * E + (uint32_t)ids[k];
         const wl::SlotLru::Result r = C.lru->request(key, !speculative);
         uint8_t* dst = C.pool + (size_t)r.slot * nb;
+        if (r.evicted) {  // a block wl_cache_get could still hand out is gone
+            auto& R = C.resolved;
+            R.erase(std::remove_if(R.begin(), R.end(), [&](const auto& x) { return x.first == r.evicted_key; }), R.end());
+        }
         if (speculative) C.spec_requests++;
         if (r.hit) {
             if (!speculative && C.spec[r.slot]) {
@@ -472,15 +494,17 @@ static wl_status cache_prepare(wl_ctx* c, uint32_t layer, const float* d_hidden,
     const uint32_t H = c->cfg.hidden, E = c->cfg.n_routed_experts, K = c->cfg.n_experts_per_tok;
     hipError_t e;
     if (++c->epoch >= 0x7FFFFFFFu) c->epoch = 1;
-    int le = wl::launch_route(c->d_largs + layer, d_hidden, c->epoch, H, E, c->grid, s);
+    const uint32_t route_epoch = c->epoch;
+    int le = wl::launch_route(c->d_largs + layer, d_hidden, route_epoch, H, E, c->grid, s);
     if (le != 0) return hip_fail(c, (hipError_t)le, "route launch");
+    // the abort word names the last call that raised an error: only an error of
+    // this routing launch fails this call (older ones stay for wl_check_error)
     if ((e = hipMemcpyAsync(C.h_ids, c->idx, 4 * (size_t)K, hipMemcpyDeviceToHost, s)) != hipSuccess ||
-        (e = hipMemcpyAsync(C.h_ids + 32, c->sync + c->sm.error, 4, hipMemcpyDeviceToHost, s)) != hipSuccess ||
+        (e = hipMemcpyAsync(C.h_ids + 32, c->sync + c->sm.abort, 4, hipMemcpyDeviceToHost, s)) != hipSuccess ||
         (e = hipEventRecord(C.ids_ev, s)) != hipSuccess || (e = hipEventSynchronize(C.ids_ev)) != hipSuccess)
         return hip_fail(c, e, "routing read-back");
-    if (C.h_ids[32] != 0)
-        return fail(c, WL_ERR_DEVICE, "device error bits 0x%x while routing layer %u (see wl_check_error)",
-                    (uint32_t)C.h_ids[32], layer);
+    if ((uint32_t)C.h_ids[32] == route_epoch)
+        return fail(c, WL_ERR_DEVICE, "the routing kernel of layer %u reported an error (see wl_check_error)", layer);
     uint8_t* ptrs[WL_MAX_TOPK];
     wl_status st = cache_resolve(c, layer, C.h_ids, K, s, false, ptrs);
     if (st != WL_OK) return st;
@@ -606,40 +630,59 @@ wl_status wl_taps(wl_ctx* c, wl_taps_out* out) {
 // Tokens per batched launch (longer calls run in chunks of this many).
 constexpr uint32_t kBatchChunk = 4096;
 
+// Byte layout of the batched layer's scratch for T tokens, every buffer
+// 256-byte aligned. With base null only the size is computed; otherwise the
+// pointers of *b are set into [base, base + size).
+static size_t batch_layout(const wl_ctx* c, uint32_t T, uint8_t* base, wl::BatchArgs* b) {
+    const size_t H = c->cfg.hidden, I = c->cfg.moe_inter, E = c->cfg.n_routed_experts, K = c->cfg.n_experts_per_tok,
+                 SI = c->SI, t = T;
+    size_t o = 0;
+    auto take = [&](auto** p, size_t bytes) {
+        o = (o + 255u) & ~(size_t)255u;
+        if (base) *p = (std::remove_reference_t<decltype(*p)>)(base + o);
+        o += bytes ? bytes : 16u;
+    };
+    wl::BatchArgs d{};
+    wl::BatchArgs& x = b ? *b : d;
+    take(&x.norm, 4 * t * H);
+    take(&x.norm3, 6 * t * H);
+    take(&x.xperm3, 6 * t * K * H);
+    take(&x.logits, 4 * t * E);
+    take(&x.idx, 4 * t * K);
+    take(&x.wts, 4 * t * K);
+    take(&x.counts, 4 * E);
+    take(&x.offsets, 4 * (E + 1));
+    take(&x.lists, 4 * E * t);
+    take(&x.ent, 4 * t * K);
+    take(&x.pos, 4 * t * K);
+    take(&x.mid3, 6 * t * K * I);
+    take(&x.expout, 4 * t * K * H);
+    take(&x.smid3, 6 * t * SI);
+    take(&x.shout, 4 * t * H);
+    return (o + 255u) & ~(size_t)255u;
+}
+
 static wl_status batch_reserve(wl_ctx* c, uint32_t T) {
     BatchScratch& B = c->batch;
     if (T <= B.cap) return WL_OK;
     hipError_t e = hipDeviceSynchronize();  // launches in flight may still use the old buffers
     if (e != hipSuccess) return hip_fail(c, e, "batched scratch resize");
-    for (void* p : B.bufs) (void)hipFree(p);
-    B.bufs.clear();
+    if (B.buf) (void)hipFree(B.buf);
+    B.buf = nullptr;
     B.cap = 0;
-    const size_t H = c->cfg.hidden, I = c->cfg.moe_inter, E = c->cfg.n_routed_experts, K = c->cfg.n_experts_per_tok,
-                 SI = c->SI, t = T;
-    wl::BatchArgs& b = B.b;
-    auto get = [&](auto** p, size_t bytes) -> bool {
-        void* q = nullptr;
-        if (hipMalloc(&q, bytes ? bytes : 16) != hipSuccess) return false;
-        B.bufs.push_back(q);
-        *p = (std::remove_reference_t<decltype(*p)>)q;
-        return true;
-    };
-    if (!get(&b.norm, 4 * t * H) || !get(&b.norm3, 6 * t * H) || !get(&b.xperm3, 6 * t * K * H) ||
-        !get(&b.logits, 4 * t * E) || !get(&b.idx, 4 * t * K) || !get(&b.wts, 4 * t * K) ||
-        !get(&b.counts, 4 * E) || !get(&b.offsets, 4 * (E + 1)) || !get(&b.lists, 4 * E * t) ||
-        !get(&b.ent, 4 * t * K) || !get(&b.pos, 4 * t * K) || !get(&b.mid3, 6 * t * K * I) ||
-        !get(&b.expout, 4 * t * K * H) || !get(&b.smid3, 6 * t * SI) || !get(&b.shout, 4 * t * H)) {
-        for (void* p : B.bufs) (void)hipFree(p);
-        B.bufs.clear();
-        return fail(c, WL_ERR_OOM, "batched scratch for %u tokens", T);
+    const size_t bytes = batch_layout(c, T, nullptr, nullptr);
+    if (hipMalloc(&B.buf, bytes) != hipSuccess) {
+        B.buf = nullptr;
+        return fail(c, WL_ERR_OOM, "batched scratch for %u tokens (%zu B)", T, bytes);
     }
+    batch_layout(c, T, (uint8_t*)B.buf, &B.b);
     B.cap = T;
     return WL_OK;
 }
 
-wl_status wl_run_moe_batched(wl_ctx* c, uint32_t layer, uint32_t n_tokens, const float* d_hidden,
-                             const float* d_resid, float* d_out, void* stream) {
-    if (!c) return WL_ERR_INVALID;
+// Argument checks of the batched layer.
+static wl_status batched_check(wl_ctx* c, uint32_t layer, uint32_t n_tokens, const float* d_hidden,
+                               const float* d_resid, float* d_out) {
     if (layer >= c->cfg.n_layers) return fail(c, WL_ERR_INVALID, "layer %u >= n_layers %u", layer, c->cfg.n_layers);
     if (!c->layers[layer].set) return fail(c, WL_ERR_STATE, "layer %u has no weights (wl_set_layer)", layer);
     if (n_tokens == 0 || n_tokens > 65535) return fail(c, WL_ERR_INVALID, "n_tokens=%u must be in [1,65535]", n_tokens);
@@ -651,34 +694,57 @@ wl_status wl_run_moe_batched(wl_ctx* c, uint32_t layer, uint32_t n_tokens, const
     if (c->n_bound[layer] != E)
         return fail(c, WL_ERR_NOT_RESIDENT, "batched layer %u needs every expert bound (%u of %u)", layer,
                     c->n_bound[layer], E);
-    // Tokens run in chunks: bounded scratch, and every piece array stays under
-    // 2 GB (the kernels address them with 32-bit buffer offsets).
+    return WL_OK;
+}
+
+// Chunk cap that keeps every piece array of the kernels under 2 GB (they
+// address them with 32-bit buffer offsets).
+static uint32_t batch_offset_cap(const wl_ctx* c) {
     const uint64_t H = c->cfg.hidden, K = c->cfg.n_experts_per_tok;
     const uint64_t row = 6ull * K * std::max<uint64_t>(std::max<uint64_t>(H, c->cfg.moe_inter), c->SI);
-    const uint32_t chunk = (uint32_t)std::min<uint64_t>(kBatchChunk, ((1ull << 31) - 1) / row);
-    if (chunk == 0) return fail(c, WL_ERR_INVALID, "batched rows too large for 32-bit offsets");
-    wl_status s = batch_reserve(c, std::min(n_tokens, chunk));
-    if (s != WL_OK) return s;
+    return (uint32_t)std::min<uint64_t>(kBatchChunk, ((1ull << 31) - 1) / row);
+}
+
+// The batched layer in chunks of at most `chunk` tokens, every chunk on the
+// buffers of `scratch` (sized for `chunk` tokens).
+static wl_status batched_run(wl_ctx* c, uint32_t layer, uint32_t n_tokens, const float* d_hidden,
+                             const float* d_resid, float* d_out, const wl::BatchArgs& scratch, uint32_t chunk,
+                             void* stream) {
+    const uint64_t H = c->cfg.hidden;
     for (uint32_t t0 = 0; t0 < n_tokens; t0 += chunk) {
-        wl::BatchArgs b = c->batch.b;
+        wl::BatchArgs b = scratch;
         b.T = std::min(chunk, n_tokens - t0);
-        c->batch.last_T = b.T;
         b.hidden = d_hidden + (size_t)t0 * H;
         b.resid = d_resid ? d_resid + (size_t)t0 * H : nullptr;
         b.out = d_out + (size_t)t0 * H;
-        int e = wl::launch_batched(c->d_largs + layer, b, c->cfg.hidden, c->cfg.moe_inter, c->SI, E,
-                                   c->cfg.n_experts_per_tok, (uint32_t)c->n_cu, stream);
+        c->batch.last = b;
+        c->batch.ran = true;
+        int e = wl::launch_batched(c->d_largs + layer, b, c->cfg.hidden, c->cfg.moe_inter, c->SI,
+                                   c->cfg.n_routed_experts, c->cfg.n_experts_per_tok, (uint32_t)c->n_cu, stream);
         if (e != 0) return hip_fail(c, (hipError_t)e, "batched launch");
     }
     return WL_OK;
 }
 
+wl_status wl_run_moe_batched(wl_ctx* c, uint32_t layer, uint32_t n_tokens, const float* d_hidden,
+                             const float* d_resid, float* d_out, void* stream) {
+    if (!c) return WL_ERR_INVALID;
+    wl_status s = batched_check(c, layer, n_tokens, d_hidden, d_resid, d_out);
+    if (s != WL_OK) return s;
+    // Tokens run in chunks: bounded scratch, and every piece array stays under
+    // 2 GB.
+    const uint32_t chunk = batch_offset_cap(c);
+    if (chunk == 0) return fail(c, WL_ERR_INVALID, "batched rows too large for 32-bit offsets");
+    if ((s = batch_reserve(c, std::min(n_tokens, chunk))) != WL_OK) return s;
+    return batched_run(c, layer, n_tokens, d_hidden, d_resid, d_out, c->batch.b, chunk, stream);
+}
+
 wl_status wl_batched_counts(wl_ctx* c, uint32_t* h_counts) {
     if (!c || !h_counts) return WL_ERR_INVALID;
-    if (!c->batch.cap) return fail(c, WL_ERR_STATE, "no batched call yet");
+    if (!c->batch.ran) return fail(c, WL_ERR_STATE, "no batched call yet");
     hipError_t e = hipDeviceSynchronize();
     if (e == hipSuccess)
-        e = hipMemcpy(h_counts, c->batch.b.counts, 4 * (size_t)c->cfg.n_routed_experts, hipMemcpyDeviceToHost);
+        e = hipMemcpy(h_counts, c->batch.last.counts, 4 * (size_t)c->cfg.n_routed_experts, hipMemcpyDeviceToHost);
     if (e != hipSuccess) return hip_fail(c, e, "batched counts");
     return WL_OK;
 }
@@ -686,9 +752,9 @@ wl_status wl_batched_counts(wl_ctx* c, uint32_t* h_counts) {
 wl_status wl_batched_routing(wl_ctx* c, uint32_t max_tokens, uint32_t* h_n_tokens, float* h_logits, int32_t* h_idx,
                              float* h_w) {
     if (!c || !h_n_tokens) return WL_ERR_INVALID;
-    if (!c->batch.cap) return fail(c, WL_ERR_STATE, "no batched call yet");
-    const wl::BatchArgs& b = c->batch.b;  // pointers; the chunk's token count is last_T
-    const uint32_t T = c->batch.last_T;
+    if (!c->batch.ran) return fail(c, WL_ERR_STATE, "no batched call yet");
+    const wl::BatchArgs& b = c->batch.last;
+    const uint32_t T = b.T;
     *h_n_tokens = T;
     if (T > max_tokens) return fail(c, WL_ERR_INVALID, "the last chunk has %u tokens > max_tokens %u", T, max_tokens);
     const size_t E = c->cfg.n_routed_experts, K = c->cfg.n_experts_per_tok;
