@@ -164,6 +164,21 @@ wl_status wl_run_chain(wl_ctx* ctx, uint32_t first_layer, uint32_t n_layers, flo
 wl_status wl_run_moe_batched(wl_ctx* ctx, uint32_t layer, uint32_t n_tokens, const float* d_hidden,
                              const float* d_resid, float* d_out, void* stream);
 
+/* The batched layer for callers that cannot allocate: no counterpart in the
+ * reference. It is for code that may not call hipMalloc during a call (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * allocation): the same arguments, kernels and results as wl_run_moe_batched,
+ * but the scratch comes from a static 64 MiB device array of the library
+ * (one per GPU, held until the process ends) instead of context memory that
+ * wl_run_moe_batched grows on demand, so the call performs no hipMalloc,
+ * hipFree or other allocation. Tokens run in chunks of as many as the array
+ * holds (97 at hidden 6144 / inter 2048 / 8 of 256 experts); a shape whose
+ * single token does not fit returns WL_ERR_INVALID. Every call on one GPU
+ * shares that GPU's array, which keeps the last call's contents: calls that
+ * overlap on one GPU (two streams, two contexts, two host threads) race. */
+wl_status wl_run_moe_batched_noalloc(wl_ctx* ctx, uint32_t layer, uint32_t n_tokens, const float* d_hidden,
+                                     const float* d_resid, float* d_out, void* stream);
+
 /* Tokens routed to each expert by the last chunk of the last wl_run_moe_batched
  * call (all of it when n_tokens <= 4096) (h_counts:
  * host array of n_routed_experts; synchronises the device). The grouping the

@@ -271,6 +271,11 @@ int launch_expert_ffn(const uint8_t* blk, uint64_t gw_off, uint64_t gs_off, uint
 // Batched layer (moe_batched.hip): every stage on `stream`.
 int launch_batched(const DecodeArgs* d_args, const BatchArgs& b, uint32_t H, uint32_t I, uint32_t SI, uint32_t E,
                    uint32_t K, uint32_t n_cu, void* stream);
+// The library's static device scratch (noalloc.hip): its device address on
+// `device` (which must be current), looked up once per device and kept;
+// and its size in bytes.
+int noalloc_scratch(int device, void** ptr);
+size_t noalloc_scratch_bytes();
 // Reference-layout block -> native block (src null: synthesise the native
 // block directly from the counter-based generator with `key`).
 int launch_expert_to_native(const uint8_t* src, uint8_t* dst, uint32_t H, uint32_t I, uint32_t key, void* stream);

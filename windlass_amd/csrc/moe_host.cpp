@@ -53,8 +53,9 @@ struct CacheState {
 };
 
 // Scratch of the batched layer: one allocation sized for `cap` tokens
-// (wl_run_moe_batched). `last` holds the buffers and token count of the
-// last chunk run (read by the test hooks).
+// (wl_run_moe_batched), or the library's static device array
+// (wl_run_moe_batched_noalloc). `last` holds the buffers and token count of
+// the last chunk either path ran (read by the test hooks).
 struct BatchScratch {
     uint32_t cap = 0;
     void* buf = nullptr;
@@ -104,6 +105,7 @@ struct wl_ctx {
     std::string err;
     CacheState cache;
     BatchScratch batch;
+    void* scratch = nullptr;  // this device's static scratch (wl_run_moe_batched_noalloc)
 };
 
 namespace {
@@ -310,6 +312,12 @@ wl_status wl_create(const wl_moe_config* cfg, wl_ctx** out) {
         return WL_ERR_OOM;
     }
     c->sync = (uint32_t*)c->uc_block;
+    // the static scratch of this device (wl_run_moe_batched_noalloc), looked
+    // up once per device, with the device current, at set-up
+    if (wl::noalloc_scratch(c->device, &c->scratch) != 0) {
+        wl_destroy(c);
+        return WL_ERR_HIP;
+    }
 
     e = hipMemset(c->d_slot, 0, sizeof(void*) * (size_t)L * E);
     // epoch 0 is never a call's: zeroed tagged arrays hold no valid word (a
@@ -662,6 +670,17 @@ static size_t batch_layout(const wl_ctx* c, uint32_t T, uint8_t* base, wl::Batch
     return (o + 255u) & ~(size_t)255u;
 }
 
+// Largest chunk of tokens whose scratch fits in `bytes` (0 if none).
+static uint32_t batch_tokens_fitting(const wl_ctx* c, size_t bytes) {
+    uint32_t lo = 0, hi = kBatchChunk;
+    while (lo < hi) {
+        const uint32_t mid = (lo + hi + 1u) / 2u;
+        if (batch_layout(c, mid, nullptr, nullptr) <= bytes) lo = mid;
+        else hi = mid - 1u;
+    }
+    return lo;
+}
+
 static wl_status batch_reserve(wl_ctx* c, uint32_t T) {
     BatchScratch& B = c->batch;
     if (T <= B.cap) return WL_OK;
@@ -737,6 +756,21 @@ wl_status wl_run_moe_batched(wl_ctx* c, uint32_t layer, uint32_t n_tokens, const
     if (chunk == 0) return fail(c, WL_ERR_INVALID, "batched rows too large for 32-bit offsets");
     if ((s = batch_reserve(c, std::min(n_tokens, chunk))) != WL_OK) return s;
     return batched_run(c, layer, n_tokens, d_hidden, d_resid, d_out, c->batch.b, chunk, stream);
+}
+
+wl_status wl_run_moe_batched_noalloc(wl_ctx* c, uint32_t layer, uint32_t n_tokens, const float* d_hidden,
+                                     const float* d_resid, float* d_out, void* stream) {
+    if (!c) return WL_ERR_INVALID;
+    wl_status s = batched_check(c, layer, n_tokens, d_hidden, d_resid, d_out);
+    if (s != WL_OK) return s;
+    if (!c->scratch) return fail(c, WL_ERR_STATE, "static scratch of device %d not resolved", c->device);
+    const uint32_t chunk = std::min(batch_offset_cap(c), batch_tokens_fitting(c, wl::noalloc_scratch_bytes()));
+    if (chunk == 0)
+        return fail(c, WL_ERR_INVALID, "one token's batched scratch (%zu B) exceeds the static scratch (%zu B)",
+                    batch_layout(c, 1, nullptr, nullptr), wl::noalloc_scratch_bytes());
+    wl::BatchArgs scratch{};
+    batch_layout(c, chunk, (uint8_t*)c->scratch, &scratch);
+    return batched_run(c, layer, n_tokens, d_hidden, d_resid, d_out, scratch, chunk, stream);
 }
 
 wl_status wl_batched_counts(wl_ctx* c, uint32_t* h_counts) {

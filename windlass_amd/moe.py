@@ -83,6 +83,7 @@ def load():
         "wl_run_moe_residual": [vp, u32, vp, vp, vp, vp],
         "wl_run_chain": [vp, u32, u32, vp, vp, vp],
         "wl_run_moe_batched": [vp, u32, u32, vp, vp, vp, vp],
+        "wl_run_moe_batched_noalloc": [vp, u32, u32, vp, vp, vp, vp],
         "wl_batched_counts": [vp, ctypes.POINTER(u32)],
         "wl_batched_routing": [vp, u32, ctypes.POINTER(u32), vp, vp, vp],
         "wl_taps": [vp, ctypes.POINTER(Taps)],
@@ -237,6 +238,10 @@ class Context:
     def run_moe_batched(self, layer, n_tokens, d_hidden, d_resid, d_out, stream=0):
         self._ck(self.lib.wl_run_moe_batched(self.h, layer, n_tokens, d_hidden, d_resid, d_out, stream),
                  "wl_run_moe_batched")
+
+    def run_moe_batched_noalloc(self, layer, n_tokens, d_hidden, d_resid, d_out, stream=0):
+        self._ck(self.lib.wl_run_moe_batched_noalloc(self.h, layer, n_tokens, d_hidden, d_resid, d_out, stream),
+                 "wl_run_moe_batched_noalloc")
 
     def batched_counts(self):
         import numpy as np
