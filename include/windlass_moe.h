@@ -88,7 +88,7 @@ const char* wl_last_error(const wl_ctx* ctx);
 
 /* Shared-expert storage formats for wl_set_layer. */
 #define WL_SHARED_BF16  0   /* [gate SI*H | up SI*H | down H*SI] bf16, row-major */
-#define WL_SHARED_MXFP4 1   /* one packed block in wl_expert_layout order, inter = SI */
+#define WL_SHARED_MXFP4 1   /* one packed block in wl_expert_layout order, inter = SI (n_shared = 1) */
 
 /* Binds the non-expert weights of MoE layer `layer` (0-based within the
  * context). Router, bias and norm pointers are caller-owned and must stay
@@ -101,6 +101,15 @@ const char* wl_last_error(const wl_ctx* ctx);
 wl_status wl_set_layer(wl_ctx* ctx, uint32_t layer, const uint16_t* d_router_w,
                        const float* d_router_bias, const uint16_t* d_post_attn_ln,
                        const void* d_shared, int32_t shared_dtype);
+
+/* The same with the shared expert given as the six MXFP4 tensors of
+ * glm::LayerWeights (sh_gate_w / sh_gate_s / sh_up_w / sh_up_s / sh_down_w /
+ * sh_down_s, src/glm_loader.cuh:271-273,608-610): gate/up [SI, H/2] nibbles +
+ * [SI, H/32] E8M0, down [H, SI/2] + [H, SI/32]. Requires n_shared = 1. */
+wl_status wl_set_layer_mxfp4(wl_ctx* ctx, uint32_t layer, const uint16_t* d_router_w, const float* d_router_bias,
+                             const uint16_t* d_post_attn_ln, const uint8_t* d_sh_gate_w, const uint8_t* d_sh_gate_s,
+                             const uint8_t* d_sh_up_w, const uint8_t* d_sh_up_s, const uint8_t* d_sh_down_w,
+                             const uint8_t* d_sh_down_s);
 
 /* ---- HBM slot table (replaces the pointer-returning ExpertSource::get of a
  * fully resident model, src/glm_layer_runner.cuh:34-48) ---------------------
@@ -126,14 +135,60 @@ wl_status wl_slot_unbind(wl_ctx* ctx, uint32_t layer, uint32_t expert);
 wl_status wl_slot_pool_create(wl_ctx* ctx, uint32_t n_slots);
 wl_status wl_slot_pool_ptr(wl_ctx* ctx, uint32_t slot, uint8_t** d_block);
 
+/* ---- expert source (the C form of glm::ExpertSource,
+ * src/glm_layer_runner.cuh:34-48) ------------------------------------------
+ * A caller-supplied provider of expert blocks in DEVICE memory, for layers
+ * whose experts are not bound in the slot table. `get` returns the block of
+ * (layer, expert) (required); `prefetch` announces the n experts a layer is
+ * about to read, so the source can start every fetch at once (optional, NULL
+ * = nothing to overlap); `get_async` returns a block and orders `stream` after
+ * its arrival (optional, NULL = get). A NULL return fails the call with
+ * WL_ERR_IO. `native` = 1: blocks are in the native layout
+ * (wl_native_block_bytes); 0: in the reference's packed layout
+ * (wl_expert_layout, the layer_N.bin record), which the library converts on
+ * `stream` into context-owned staging blocks before use.
+ *
+ * How the library calls it (run_moe's pattern, :391-418): a layer with no
+ * expert bound is routed on the device, its K ids are read back on the host
+ * (one host round trip per layer), then prefetch(layer, ids, K) and one
+ * get_async per id, in slot order. A batched layer (wl_run_moe_batched) reads
+ * back the routed set once, then fetches every unique expert exactly once, in
+ * ascending id order and in chunks of at most 32 (prefetch of the chunk, then
+ * get_async of each), running the chunk's GEMMs before the next chunk is
+ * announced (run_moe_batched, :862-902).
+ *
+ * A returned block must stay valid until the work this call enqueued on
+ * `stream` has completed; a source that reuses its buffers orders the reuse
+ * after `stream` (the reference's ExpertCache records a gate event on the
+ * caller's stream at prefetch for this, src/glm_expert_cache.cuh:204-208).
+ * `user` is passed back unchanged. All calls come from the thread that calls
+ * the library. */
+typedef struct wl_expert_source {
+    void* user;
+    const uint8_t* (*get)(void* user, uint32_t layer, uint32_t expert);
+    void (*prefetch)(void* user, uint32_t layer, const int32_t* experts, uint32_t n, void* stream);
+    const uint8_t* (*get_async)(void* user, uint32_t layer, uint32_t expert, void* stream);
+    int32_t native;
+} wl_expert_source;
+
+/* Attaches `src` (copied; NULL detaches) as the source of every layer of the
+ * context that has no expert bound. A reference-layout source gets
+ * n_experts_per_tok staging blocks (allocated here; the batched layer grows
+ * them to 32 on first use). WL_ERR_STATE if the context has a built-in cache
+ * (wl_cache_create installs the cache as the context's source). */
+wl_status wl_set_expert_source(wl_ctx* ctx, const wl_expert_source* src);
+
 /* ---- the MoE layer ------------------------------------------------------
- * Replaces glm::run_moe (src/glm_layer_runner.cuh:352-443) for a resident
- * layer: post-attention RMSNorm -> router GEMV -> sigmoid + bias -> top-k ->
- * renorm -> x routed_scaling -> K MXFP4 SwiGLU experts -> shared expert ->
+ * Replaces glm::run_moe (src/glm_layer_runner.cuh:352-443): post-attention
+ * RMSNorm -> router GEMV -> sigmoid + bias -> top-k -> renorm ->
+ * x routed_scaling -> K MXFP4 SwiGLU experts -> shared expert ->
  * out = sum_k w_k e_k + shared. d_hidden [H] f32 is the pre-norm residual
  * stream; d_out [H] f32 receives the block output WITHOUT the residual and must
- * not alias d_hidden. Returns WL_ERR_NOT_RESIDENT if any expert of the layer
- * is unbound. */
+ * not alias d_hidden. A layer with every expert bound runs with no host
+ * round trip; a layer with none bound runs through the context's expert
+ * source (wl_set_expert_source, or the built-in cache). Returns
+ * WL_ERR_NOT_RESIDENT for a partly bound layer, or an unbound one without a
+ * source. */
 wl_status wl_run_moe(wl_ctx* ctx, uint32_t layer, const float* d_hidden, float* d_out,
                      void* stream);
 
@@ -158,9 +213,12 @@ wl_status wl_run_chain(wl_ctx* ctx, uint32_t first_layer, uint32_t n_layers, flo
  * grouped by expert (stable, (token, slot) order) and every selected expert's
  * weights are streamed once per 32 of its tokens; the per-token combine sums
  * the slots in slot order, then the shared expert (the reference's pass 3).
- * Requires every expert of the layer bound (resident); n_tokens <= 65535, run
- * in chunks of up to 4096 tokens. Scratch grows to the largest chunk seen
- * (context-owned; growing synchronises the device). */
+ * A layer with every expert bound runs with no host round trip; a layer with
+ * none bound fetches its routed set through the context's expert source (see
+ * wl_expert_source: one host round trip per chunk of tokens, each unique
+ * expert fetched once). n_tokens <= 65535, run in chunks of up to 4096 tokens.
+ * Scratch grows to the largest chunk seen (context-owned; growing
+ * synchronises the device). */
 wl_status wl_run_moe_batched(wl_ctx* ctx, uint32_t layer, uint32_t n_tokens, const float* d_hidden,
                              const float* d_resid, float* d_out, void* stream);
 

@@ -30,8 +30,8 @@ def build(verbose: bool = False) -> str:
         obj = os.path.join(CSRC, "_build", src + ".o")
         os.makedirs(os.path.dirname(obj), exist_ok=True)
         cmd = [HIPCC] + COMMON + DEVICE_FLAGS + PRELOAD_FLAGS + ["-c", path, "-o", obj]
-        if src.endswith(".cpp"):
-            cmd = [HIPCC] + COMMON + ["-c", path, "-o", obj]
+        if src.endswith(".cpp"):  # host code: no kernels, but compiled for gfx950 only like the rest
+            cmd = [HIPCC] + COMMON + DEVICE_FLAGS + ["-c", path, "-o", obj]
         if verbose:
             print(" ".join(cmd), flush=True)
         r = subprocess.run(cmd, capture_output=True, text=True)

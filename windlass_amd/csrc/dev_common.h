@@ -73,6 +73,10 @@ constexpr int kNT = 2;
 WL_DEV u32x4 bld16_nt(rsrc_t r, uint32_t voff, uint32_t soff) {
     return __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, kNT);
 }
+// A lane offset past every resource: the load returns zeros without a
+// memory access. (The range check sees the lane offset; an out-of-range
+// value must be put there, not in the uniform offset.)
+constexpr uint32_t kOOB = 0x80000000u;
 WL_DEV uint32_t bld1(rsrc_t r, uint32_t voff, uint32_t soff) {
     return __builtin_amdgcn_raw_buffer_load_b8(r, (int)voff, (int)soff, 0);
 }
@@ -199,6 +203,16 @@ WL_DEV uint32_t batch_scale(const Batch& B, uint32_t item0, int i) {
 constexpr int kSNB = 8;
 struct SBatch {
     u32x4 w[kSNB];
+    uint64_t pl;
+};
+
+// A batch of an MXFP4 shared expert's gate/up stream (decode kernel): kSNB4
+// k tiles of this wave's share of the work-group's tile, their scale dwords,
+// and a logit slot read.
+constexpr int kSNB4 = 4;
+struct SBatch4 {
+    u32x4 w[kSNB4];
+    uint32_t s[kSNB4];
     uint64_t pl;
 };
 

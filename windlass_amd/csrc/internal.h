@@ -221,12 +221,40 @@ struct NativeShared {
     }
 };
 
+// An MXFP4 shared expert (WL_SHARED_MXFP4; inter SI = moe_inter):
+//   blk   the routed-expert native block (NativeLayout(H, SI)): gate/up of
+//         the decode kernel, gate/up and down of the batched kernels
+//   dn8   [SI/8 tiles][H rows] 4 bytes: the nibbles of columns [8T, 8T+8) of
+//         down row r (the decode kernel's work-group of tile T applies them)
+//   dns8  [SI/32][H rows] 1 byte: the scale of columns [32q, 32q+32) of row r
+struct NativeShared4 {
+    uint64_t blk, dn8, dns8, total;
+    __host__ __device__ static NativeShared4 make(uint32_t H, uint32_t SI) {
+        NativeShared4 m;
+        m.blk = 0;
+        m.dn8 = NativeLayout::make(H, SI).total;
+        m.dns8 = m.dn8 + (uint64_t)(SI / 8) * H * 4;
+        m.total = m.dns8 + (((uint64_t)(SI / 32) * H + 1023) & ~(uint64_t)1023);
+        return m;
+    }
+};
+
 // Batched (multi-token) layer, reference run_moe_batched
 // (src/glm_layer_runner.cuh:818-928): per-token routing, tokens grouped by
 // expert (stable: (token, slot) order), grouped GEMMs, per-token combine in
 // slot order. Scratch is context-owned and sized for T tokens.
+// BatchArgs::flags: experts whose slot-table entry is null get no GEMM units
+// (a source-backed layer runs its routed set in chunks of experts); the
+// shared expert's units are left out (they run with the first chunk only).
+// kBatchShared4: the shared expert is MXFP4 and runs as expert E of the pass
+// table (all T tokens, activations straight from norm3, outputs in the rows
+// [T*K, T*K + T) of mid3 and expout).
+enum : uint32_t { kBatchSkipUnbound = 1u, kBatchNoShared = 2u, kBatchShared4 = 4u };
+// launch_batched phases: routing (norm .. permute), the GEMMs, the combine.
+enum : uint32_t { kPhaseRoute = 1u, kPhaseGemm = 2u, kPhaseCombine = 4u, kPhaseAll = 7u };
 struct BatchArgs {
     uint32_t T;
+    uint32_t flags;
     const float* hidden;   // [T][H] pre-norm residual stream
     const float* resid;    // [T][H] or null
     float* out;            // [T][H]
@@ -241,15 +269,15 @@ struct BatchArgs {
     uint32_t* lists;       // [E][T] entries (token*K + slot) of expert e, ascending
     uint32_t* ent;         // [T*K] compact index -> token*K + slot (expert-major)
     uint32_t* pos;         // [T*K] token*K + slot -> compact index
-    uint16_t* mid3;        // [T*K][3][I] routed SwiGLU outputs (pieces), compact rows
-    float* expout;         // [T*K][H] routed expert outputs, compact rows
+    uint16_t* mid3;        // [T*K (+T)][3][I] routed (and MXFP4 shared) SwiGLU outputs (pieces), compact rows
+    float* expout;         // [T*K (+T)][H] routed (and MXFP4 shared) expert outputs, compact rows
     uint16_t* smid3;       // [T][3][SI] shared SwiGLU outputs (pieces)
     float* shout;          // [T][H]
 };
 
 // Launchers (moe_decode.hip).
 int launch_decode(const DecodeArgs* d_args, const DecodeDyn& dyn, uint32_t H, uint32_t I, uint32_t SI,
-                  uint32_t E, uint32_t K, uint32_t grid, void* stream);
+                  uint32_t E, uint32_t K, uint32_t grid, bool sh4, void* stream);
 int decode_max_lds();
 // Work-groups of the decode / routing kernel one CU can hold at once
 // (hipOccupancyMaxActiveBlocksPerMultiprocessor at the kernel's LDS size).
@@ -270,7 +298,7 @@ int launch_expert_ffn(const uint8_t* blk, uint64_t gw_off, uint64_t gs_off, uint
                       void* stream);
 // Batched layer (moe_batched.hip): every stage on `stream`.
 int launch_batched(const DecodeArgs* d_args, const BatchArgs& b, uint32_t H, uint32_t I, uint32_t SI, uint32_t E,
-                   uint32_t K, uint32_t n_cu, void* stream);
+                   uint32_t K, uint32_t n_cu, uint32_t phases, void* stream);
 // The library's static device scratch (noalloc.hip): its device address on
 // `device` (which must be current), looked up once per device and kept;
 // and its size in bytes.
@@ -280,6 +308,9 @@ size_t noalloc_scratch_bytes();
 // block directly from the counter-based generator with `key`).
 int launch_expert_to_native(const uint8_t* src, uint8_t* dst, uint32_t H, uint32_t I, uint32_t key, void* stream);
 int launch_shared_to_native(const uint16_t* src, uint16_t* dst, uint32_t H, uint32_t SI, void* stream);
+// The six reference tensors of an MXFP4 shared expert (gate_w, gate_s, up_w,
+// up_s, down_w, down_s) -> NativeShared4.
+int launch_shared4_to_native(const uint8_t* const* parts, uint8_t* dst, uint32_t H, uint32_t SI, void* stream);
 int launch_synth_expert(uint8_t* d_block, uint64_t gw_off, uint64_t gw_len, uint64_t gs_off,
                         uint64_t gs_len, uint64_t uw_off, uint64_t uw_len, uint64_t us_off,
                         uint64_t us_len, uint64_t dw_off, uint64_t dw_len, uint64_t ds_off,

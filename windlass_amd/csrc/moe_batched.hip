@@ -378,11 +378,21 @@ struct PassTab {
     const uint32_t* pp;
     uint32_t n;  // passes
 };
-WL_DEV PassTab load_pass_tab(const BatchArgs& b, uint32_t E, uint32_t* s) {
+// E counts the MXFP4 shared pseudo-expert (index E - 1) when there is one:
+// all T tokens, compact rows from T*K on.
+WL_DEV PassTab load_pass_tab(const BatchArgs& b, uint32_t E, uint32_t K, uint32_t* s, const uint8_t* const* stab) {
     const uint32_t tid = threadIdx.x;
     uint32_t *cnt = s, *off = s + E, *pp = s + 2u * E;
+    const bool skip = (b.flags & kBatchSkipUnbound) != 0u;
+    const uint32_t esh = (b.flags & kBatchShared4) ? E - 1u : E;
     for (uint32_t f = tid; f < E; f += kThreads) {
-        cnt[f] = gld(b.counts + f);
+        if (f == esh) {
+            cnt[f] = (b.flags & kBatchNoShared) ? 0u : b.T;
+            off[f] = b.T * K;
+            continue;
+        }
+        // stab[f] was written by this thread (load_slot_tab, same stride)
+        cnt[f] = skip && stab[f] == nullptr ? 0u : gld(b.counts + f);
         off[f] = gld(b.offsets + f);
     }
     lds_barrier();
@@ -612,11 +622,14 @@ WL_DEV void run_steps(Kn& k) {
 
 // Tables every GEMM work-group loads into LDS: the pass table and the
 // layer's expert block pointers.
-WL_DEV const uint8_t* const* load_slot_tab(const DecodeArgs& a, uint32_t E, const uint8_t** s) {
-    for (uint32_t f = threadIdx.x; f < E; f += kThreads) s[f] = gld(a.slot_tab + f);
+// With an MXFP4 shared expert, entry E is its block (NativeShared4::blk = 0).
+WL_DEV const uint8_t* const* load_slot_tab(const DecodeArgs& a, uint32_t E, bool sh4, const uint8_t** s) {
+    for (uint32_t f = threadIdx.x; f < E + (sh4 ? 1u : 0u); f += kThreads)
+        s[f] = f < E ? gld(a.slot_tab + f) : a.sh_native;
     return s;  // visible after the barrier in load_pass_tab
 }
-__host__ __device__ inline size_t gemm_tab_bytes(uint32_t E) { return 8u * E + 4u * (3u * E + 1u); }
+// LDS of the tables for E experts and the MXFP4 shared pseudo-expert.
+__host__ __device__ inline size_t gemm_tab_bytes(uint32_t E) { return 8u * (E + 1u) + 4u * (3u * (E + 1u) + 1u); }
 
 // Splits x into its three bf16 pieces at p[0], p[stride], p[2 stride].
 WL_DEV void store3(uint16_t* p, uint32_t stride, float x) {
@@ -690,6 +703,7 @@ struct UpK {
         if (!x.live) return a_none(A);
         const bool pr = pass_shape(x.nt).pr;
         if (x.sh) a_bind(A, b.norm3, (uint64_t)b.T * 6u * H, x.row0, x.nt, pr, H);
+        else if (x.e == a.E) a_bind(A, b.norm3, (uint64_t)b.T * 6u * H, x.row0 - b.T * K, x.nt, pr, H);  // MXFP4 shared
         else a_bind(A, b.xperm3, (uint64_t)b.T * K * 6u * H, x.row0, x.nt, pr, H);
     }
     WL_MEM void bind_w(uint32_t i) {
@@ -830,9 +844,11 @@ struct UpK {
 __global__ void __launch_bounds__(kThreads) bup_kernel(const DecodeArgs* __restrict__ pa, const BatchArgs b) {
     const DecodeArgs& a = *pa;
     extern __shared__ __align__(16) uint8_t dyn[];
-    const uint32_t H = a.H, I = a.I, E = a.E;
-    const uint8_t* const* stab = load_slot_tab(a, E, (const uint8_t**)dyn);
-    const PassTab pt = load_pass_tab(b, E, (uint32_t*)(dyn + 8u * E));
+    const uint32_t H = a.H, I = a.I;
+    const bool sh4 = (b.flags & kBatchShared4) != 0u;
+    const uint32_t E = a.E + (sh4 ? 1u : 0u);  // experts in the pass table
+    const uint8_t* const* stab = load_slot_tab(a, a.E, sh4, (const uint8_t**)dyn);
+    const PassTab pt = load_pass_tab(b, E, a.K, (uint32_t*)(dyn + 8u * E), stab);
     UpK k{a, b};
     k.H = H;
     k.I = I;
@@ -844,7 +860,7 @@ __global__ void __launch_bounds__(kThreads) bup_kernel(const DecodeArgs* __restr
     k.S = I / kSlice;
     k.NSG = cdiv(k.S, kSG);
     k.Ssh = a.SI / kSlice;
-    k.Us = cdiv(b.T, kMT) * k.Ssh;
+    k.Us = (b.flags & (kBatchNoShared | kBatchShared4)) ? 0u : cdiv(b.T, kMT) * k.Ssh;
     k.nst = cdiv(H, kKC);
     const uint32_t U = k.Us + pt.n * k.NSG;
     k.nu = U > blockIdx.x ? cdiv(U - blockIdx.x, gridDim.x) : 0u;
@@ -920,7 +936,7 @@ struct DownK {
         if (!x.live) return a_none(A);
         const bool pr = pass_shape(x.nt).pr;
         if (x.sh) a_bind(A, b.smid3, (uint64_t)b.T * 6u * SI, x.row0, x.nt, pr, SI);
-        else a_bind(A, b.mid3, (uint64_t)b.T * a.K * 6u * I, x.row0, x.nt, pr, I);
+        else a_bind(A, b.mid3, (uint64_t)b.T * (a.K + ((b.flags & kBatchShared4) ? 1u : 0u)) * 6u * I, x.row0, x.nt, pr, I);
     }
     WL_MEM void bind_w(uint32_t i) {
         const UnitInfo x = unit(i);
@@ -1046,9 +1062,11 @@ struct DownK {
 __global__ void __launch_bounds__(kThreads) bdown_kernel(const DecodeArgs* __restrict__ pa, const BatchArgs b) {
     const DecodeArgs& a = *pa;
     extern __shared__ __align__(16) uint8_t dyn[];
-    const uint32_t H = a.H, I = a.I, E = a.E;
-    const uint8_t* const* stab = load_slot_tab(a, E, (const uint8_t**)dyn);
-    const PassTab pt = load_pass_tab(b, E, (uint32_t*)(dyn + 8u * E));
+    const uint32_t H = a.H, I = a.I;
+    const bool sh4 = (b.flags & kBatchShared4) != 0u;
+    const uint32_t E = a.E + (sh4 ? 1u : 0u);  // experts in the pass table
+    const uint8_t* const* stab = load_slot_tab(a, a.E, sh4, (const uint8_t**)dyn);
+    const PassTab pt = load_pass_tab(b, E, a.K, (uint32_t*)(dyn + 8u * E), stab);
     DownK k{a, b};
     k.H = H;
     k.I = I;
@@ -1059,7 +1077,7 @@ __global__ void __launch_bounds__(kThreads) bdown_kernel(const DecodeArgs* __res
     k.nks = a.SI / 32u;
     k.RBs = cdiv(H, 128u);
     k.RBr = cdiv(k.nq, 16u);
-    k.Us = cdiv(b.T, kMT) * k.RBs;
+    k.Us = (b.flags & (kBatchNoShared | kBatchShared4)) ? 0u : cdiv(b.T, kMT) * k.RBs;
     k.nst = cdiv(max(I, a.SI), kKC);  // the shorter kind's extra steps are masked
     const uint32_t U = k.Us + pt.n * k.RBr;
     k.nu = U > blockIdx.x ? cdiv(U - blockIdx.x, gridDim.x) : 0u;
@@ -1098,7 +1116,8 @@ __global__ void __launch_bounds__(256) bcomb_kernel(const BatchArgs b, uint32_t 
         acc.z = fmaf(w, x.z, acc.z);
         acc.w = fmaf(w, x.w, acc.w);
     }
-    const float4 sh = *(const float4*)(b.shout + (size_t)t * H + r);
+    const float4 sh = (b.flags & kBatchShared4) ? *(const float4*)(b.expout + ((size_t)b.T * K + t) * H + r)
+                                                : *(const float4*)(b.shout + (size_t)t * H + r);
     acc.x += sh.x;
     acc.y += sh.y;
     acc.z += sh.z;
@@ -1114,7 +1133,7 @@ __global__ void __launch_bounds__(256) bcomb_kernel(const BatchArgs b, uint32_t 
 }
 
 int launch_batched(const DecodeArgs* d_args, const BatchArgs& b, uint32_t H, uint32_t I, uint32_t SI, uint32_t E,
-                   uint32_t K, uint32_t n_cu, void* stream) {
+                   uint32_t K, uint32_t n_cu, uint32_t phases, void* stream) {
     (void)I;
     (void)SI;
     hipStream_t s = (hipStream_t)stream;
@@ -1135,19 +1154,24 @@ int launch_batched(const DecodeArgs* d_args, const BatchArgs& b, uint32_t H, uin
         return n_cu * (uint32_t)nb;
     };
     const uint32_t nperm = b.T * K * (3u * H / 8u);
-    hipLaunchKernelGGL(bnorm_kernel, dim3(b.T), dim3(kThreads), 0, s, d_args, b);
-    // router: ~one work-group per CU; each token block's rows split over gx
-    // work-groups (each norm row is read gx times, the router once per block)
-    const uint32_t nblk = (b.T + kTB - 1) / kTB;
-    const uint32_t gx = std::max(1u, std::min(n_cu / nblk, (E + kRR - 1) / kRR));
-    hipLaunchKernelGGL(broute_kernel, dim3(gx, nblk), dim3(kThreads), 0, s, d_args, b);
-    hipLaunchKernelGGL(btopk_kernel, dim3(b.T), dim3(kThreads), topk_lds, s, d_args, b);
-    hipLaunchKernelGGL(bcount_kernel, dim3(E), dim3(64), 0, s, b, K);
-    hipLaunchKernelGGL(bscatter_kernel, dim3(E), dim3(256), 0, s, b, E);
-    hipLaunchKernelGGL(bpermute_kernel, dim3(std::min((nperm + 255u) / 256u, 8u * n_cu)), dim3(256), 0, s, b, H, K);
-    hipLaunchKernelGGL(bup_kernel, dim3(resident((const void*)bup_kernel)), dim3(kThreads), gemm_lds, s, d_args, b);
-    hipLaunchKernelGGL(bdown_kernel, dim3(resident((const void*)bdown_kernel)), dim3(kThreads), gemm_lds, s, d_args, b);
-    hipLaunchKernelGGL(bcomb_kernel, dim3((H + 1023) / 1024, b.T), dim3(256), 0, s, b, H, K);
+    if (phases & kPhaseRoute) {
+        hipLaunchKernelGGL(bnorm_kernel, dim3(b.T), dim3(kThreads), 0, s, d_args, b);
+        // router: ~one work-group per CU; each token block's rows split over gx
+        // work-groups (each norm row is read gx times, the router once per block)
+        const uint32_t nblk = (b.T + kTB - 1) / kTB;
+        const uint32_t gx = std::max(1u, std::min(n_cu / nblk, (E + kRR - 1) / kRR));
+        hipLaunchKernelGGL(broute_kernel, dim3(gx, nblk), dim3(kThreads), 0, s, d_args, b);
+        hipLaunchKernelGGL(btopk_kernel, dim3(b.T), dim3(kThreads), topk_lds, s, d_args, b);
+        hipLaunchKernelGGL(bcount_kernel, dim3(E), dim3(64), 0, s, b, K);
+        hipLaunchKernelGGL(bscatter_kernel, dim3(E), dim3(256), 0, s, b, E);
+        hipLaunchKernelGGL(bpermute_kernel, dim3(std::min((nperm + 255u) / 256u, 8u * n_cu)), dim3(256), 0, s, b, H, K);
+    }
+    if (phases & kPhaseGemm) {
+        hipLaunchKernelGGL(bup_kernel, dim3(resident((const void*)bup_kernel)), dim3(kThreads), gemm_lds, s, d_args, b);
+        hipLaunchKernelGGL(bdown_kernel, dim3(resident((const void*)bdown_kernel)), dim3(kThreads), gemm_lds, s, d_args, b);
+    }
+    if (phases & kPhaseCombine)
+        hipLaunchKernelGGL(bcomb_kernel, dim3((H + 1023) / 1024, b.T), dim3(256), 0, s, b, H, K);
     return (int)hipGetLastError();
 }
 

@@ -81,7 +81,8 @@ WL_DEV void st_tag(uint64_t* p, uint32_t epoch, float x) {
 // The preloaded arguments: the record pointer, the five pointers up to lslot,
 // seg and epoch.
 static_assert(6 * sizeof(void*) / 4 + 2 == kPreloadDwords, "preloaded kernel arguments");
-template <bool GLM>
+// SH4 = true: the shared expert is MXFP4 (NativeShared4) instead of bf16.
+template <bool GLM, bool SH4>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 moe_decode_kernel(const DecodeArgs* __restrict__ pa, const float* hidden, const uint8_t* sh_native,
                   const uint16_t* router_w, const uint16_t* ln_w, uint64_t* lslot, uint32_t seg, uint32_t epoch,
@@ -112,7 +113,8 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const float* hidden, const 
     float* smf = (float*)(misc + 16);           // [8] this tile's shared SwiGLU values
 
     Batch bA, bB;
-    SBatch sA, sB;
+    using SB = std::conditional_t<SH4, SBatch4, SBatch>;
+    SB sA, sB;
 
     // ================= segment 0: everything but the combine ====================
     if (d.seg_lo() == 0u) {
@@ -154,33 +156,70 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const float* hidden, const 
             const uint32_t t = w + G * i;
             return xcd_map ? (w & 7u) * (G / 8u) + (w >> 3) : t;
         };
-        const uint32_t sg_per = cdiv(nkt, 8u);  // k tiles per wave: [v*sg_per, +sg_per)
-        const uint32_t sg_nb = at_least2(cdiv(sg_per, (uint32_t)kSNB));
-        // native shared expert: tile T, k tile kt is the 1 KB chunk T*(H/32)+kt
+        // bf16: 32-column k tiles (1 KB chunk T*(H/32)+kt of the native shared
+        // expert); MXFP4: 128-column k tiles of the tile's gate/up chunks
+        // (NativeLayout gu, 1 KB each, kSNB4 per batch, scales from gus)
+        const uint32_t nkg = H / 128;
+        const uint32_t sg_per = SH4 ? cdiv(nkg, 8u) : cdiv(nkt, 8u);  // k tiles per wave: [v*sg_per, +sg_per)
+        const uint32_t sg_nb = at_least2(cdiv(sg_per, SH4 ? (uint32_t)kSNB4 : (uint32_t)kSNB));
         const NativeShared NS = NativeShared::make(H, SI);
-        const rsrc_t sg_rs = make_rsrc(d.sh_native + NS.sgu, (uint32_t)(NS.sdn - NS.sgu));
+        const NativeShared4 NS4 = NativeShared4::make(H, SI);
+        const NativeLayout NL4 = NativeLayout::make(H, SI);
+        const rsrc_t sg_rs = SH4 ? make_rsrc(d.sh_native + NS4.blk + NL4.gu, (uint32_t)(NL4.gus - NL4.gu))
+                                 : make_rsrc(d.sh_native + NS.sgu, (uint32_t)(NS.sdn - NS.sgu));
+        const rsrc_t sgs_rs = make_rsrc(d.sh_native + NS4.blk + NL4.gus, SH4 ? (uint32_t)(NL4.dn - NL4.gus) : 0u);
         // every shared batch also reads the logit slot of expert min(tid, E-1)
         // (agent scope): the logits published while the shared expert streams
         // are collected on the way, without a separate round trip
         const rsrc_t ls_rs = make_rsrc(d.lslot, E * 8u);
         const uint32_t pe = min(tid, E - 1u);
-        auto sg_issue = [&](uint32_t tile, uint32_t b, SBatch& B) {
-            const uint32_t voff = min(tile, nsg - 1u) * nkt * 1024u + 16u * lane;
-            const uint32_t kt0 = v * sg_per + b * kSNB;
+        auto sg_issue = [&](uint32_t tile, uint32_t b, SB& B) {
+            if constexpr (SH4) {
+                // items past this wave's share or past the tile read zeros
+                // without touching memory: their lane offset lies past the
+                // resource (the lane offset is what the range check sees)
+                const uint32_t tl = min(tile, nsg - 1u);
+                const uint32_t voff = tl * nkg * 1024u + 16u * lane;
+                const uint32_t soff0 = tl * cdiv(nkg, 16u) * 1024u + 16u * lane;
 #pragma unroll
-            for (int i = 0; i < kSNB; i++) B.w[i] = bld16_nt(sg_rs, voff, (kt0 + i) * 1024u);
+                for (int i = 0; i < kSNB4; i++) {
+                    const uint32_t m = b * kSNB4 + i, kt = v * sg_per + m;
+                    const bool ok = m < sg_per && kt < nkg;
+                    B.w[i] = bld16_nt(sg_rs, ok ? voff + kt * 1024u : kOOB, 0u);
+                    B.s[i] = __builtin_amdgcn_raw_buffer_load_b32(
+                        sgs_rs, (int)(ok ? soff0 + (kt / 16u) * 1024u + 4u * ((kt % 16u) / 4u) : kOOB), 0, 0);
+                }
+            } else {
+                const uint32_t voff = min(tile, nsg - 1u) * nkt * 1024u + 16u * lane;
+                const uint32_t kt0 = v * sg_per + b * kSNB;
+#pragma unroll
+                for (int i = 0; i < kSNB; i++) B.w[i] = bld16_nt(sg_rs, voff, (kt0 + i) * 1024u);
+            }
             B.pl = __builtin_bit_cast(uint64_t, __builtin_amdgcn_raw_buffer_load_b64(ls_rs, (int)(8u * pe), 0, kSC1));
         };
         f32x4 gacc;
         bool seen = false;  // this call's logit of expert tid was read (only tid < E)
         uint32_t lbits = 0;
-        auto sg_consume = [&](uint32_t b, const SBatch& B) {
+        auto sg_consume = [&](uint32_t b, const SB& B) {
+            if constexpr (SH4) {
 #pragma unroll
-            for (int i = 0; i < kSNB; i++) {
-                const uint32_t m = b * kSNB + i, kt = v * sg_per + m;
-                const bool valid = m < sg_per && kt < nkt;
-                const u32x4 z = {0u, 0u, 0u, 0u};
-                gacc = mma(a_lds(xp, xps, n, kt * 32u + 8u * g, valid), as_bf16x8(valid ? B.w[i] : z), gacc);
+                for (int i = 0; i < kSNB4; i++) {
+                    const uint32_t m = b * kSNB4 + i, kt = v * sg_per + m;
+                    const bool valid = m < sg_per && kt < nkg;
+                    const float sc = valid ? e8m0f((B.s[i] >> (8u * (kt % 4u))) & 0xFFu) : 0.f;
+#pragma unroll
+                    for (int jj = 0; jj < 4; jj++)
+                        gacc = mma(a_lds(xp, xps, n, kt * 128u + 32u * g + 8u * jj, valid), fp4x8_bf16(B.w[i][jj], sc),
+                                   gacc);
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < kSNB; i++) {
+                    const uint32_t m = b * kSNB + i, kt = v * sg_per + m;
+                    const bool valid = m < sg_per && kt < nkt;
+                    const u32x4 z = {0u, 0u, 0u, 0u};
+                    gacc = mma(a_lds(xp, xps, n, kt * 32u + 8u * g, valid), as_bf16x8(valid ? B.w[i] : z), gacc);
+                }
             }
             // threads tid >= E read slot E - 1 only to keep every batch the
             // same shape; they own no expert and never record a logit
@@ -194,13 +233,29 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const float* hidden, const 
         // rows per thread: H / 512 at the GLM shape, 16 (H <= 8192) otherwise;
         // the resource of a tile ends at its last row, so rows past H read
         // zeros without touching memory (the next tile's rows are not fetched)
+        // MXFP4: 4 nibble bytes (dn8) and one scale byte (dns8) per row
         constexpr int SDV = GLM ? 12 : 16;
-        u32x4 sdw[SDV];
+        u32x4 sdw[SH4 ? 1 : SDV];
+        uint32_t sdq[SH4 ? SDV : 1], sdsc[SH4 ? SDV : 1];
         auto sd_issue = [&](uint32_t tile) {
-            const rsrc_t sd_rs = make_rsrc(d.sh_native + NS.sdn + (size_t)min(tile, nsg - 1u) * H * 16u, H * 16u);
+            const uint32_t tl = min(tile, nsg - 1u);
+            if constexpr (SH4) {
+                const rsrc_t dq_rs = make_rsrc(d.sh_native + NS4.dn8 + (size_t)tl * H * 4u, H * 4u);
+                const rsrc_t dsc_rs = make_rsrc(d.sh_native + NS4.dns8 + (size_t)(tl / 4u) * H, H);
 #pragma unroll
-            for (int i = 0; i < SDV; i++)  // row tid + 512 i of the tile: 16 bytes
-                sdw[i] = bld16_nt(sd_rs, tid * 16u, kThreads * i * 16u);
+                for (int i = 0; i < SDV; i++) {  // row r = tid + 512 i of the tile (zeros past H)
+                    const uint32_t r = tid + kThreads * i;
+                    sdq[i] = __builtin_amdgcn_raw_buffer_load_b32(dq_rs, (int)(r < H ? 4u * r : kOOB), 0, kNT);
+                    sdsc[i] = bld1(dsc_rs, r < H ? r : kOOB, 0u);
+                }
+            } else {
+                const rsrc_t sd_rs = make_rsrc(d.sh_native + NS.sdn + (size_t)tl * H * 16u, H * 16u);
+#pragma unroll
+                for (int i = 0; i < SDV; i++) {  // row r = tid + 512 i of the tile: 16 bytes (zeros past H)
+                    const uint32_t r = tid + kThreads * i;
+                    sdw[i] = bld16_nt(sd_rs, r < H ? 16u * r : kOOB, 0u);
+                }
+            }
         };
         const uint32_t tile0 = tile_of(0);
         sg_issue(tile0, 0, sA);
@@ -301,6 +356,26 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const float* hidden, const 
         // the down columns of a tile: pv[r] += sum_c sdw[r][c] * smf[c]
         auto sd_compute = [&]() {
             const float4 m0 = *(const float4*)smf, m1 = *(const float4*)(smf + 4);
+            if constexpr (SH4) {
+#pragma unroll
+                for (int i = 0; i < SDV; i++) {
+                    const uint32_t r = tid + kThreads * i;
+                    if (r < H) {
+                        const bf16x8 wv = fp4x8_bf16(sdq[i], e8m0f(sdsc[i]));
+                        float x = 0.f;
+                        x = fmaf((float)wv[0], m0.x, x);
+                        x = fmaf((float)wv[1], m0.y, x);
+                        x = fmaf((float)wv[2], m0.z, x);
+                        x = fmaf((float)wv[3], m0.w, x);
+                        x = fmaf((float)wv[4], m1.x, x);
+                        x = fmaf((float)wv[5], m1.y, x);
+                        x = fmaf((float)wv[6], m1.z, x);
+                        x = fmaf((float)wv[7], m1.w, x);
+                        pv[r] += x;
+                    }
+                }
+                return;
+            }
 #pragma unroll
             for (int i = 0; i < SDV; i++) {
                 const uint32_t r = tid + kThreads * i;
@@ -329,7 +404,7 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const float* hidden, const 
                 sg_issue(tile, 1, sB);
             }
             gacc = f32x4{0.f, 0.f, 0.f, 0.f};
-            pingpong(sg_nb, sA, sB, [&](uint32_t b, SBatch& B) { sg_issue(tile, b, B); }, sg_consume);
+            pingpong(sg_nb, sA, sB, [&](uint32_t b, SB& B) { sg_issue(tile, b, B); }, sg_consume);
             // the tile's shared-down rows are issued only now: issued with the
             // last gate/up batch they delay it (the memory system serves both
             // together), and with it the top-k
@@ -385,7 +460,7 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const float* hidden, const 
         // ---- routed units u = w + G*i: items are gate/up k tiles (128 wide,
         // this wave's 8+8 row tile), then down row pairs (32 rows x the
         // slice's 64 columns), each wave a contiguous range of them
-        const uint32_t nkg = H / 128, nq = H / 32;
+        const uint32_t nq = H / 32;
         const uint32_t dq_per = cdiv(cdiv(nq, 8u), (uint32_t)kNB) * kNB;  // row pairs per wave: [v*dq_per, +dq_per)
         const uint32_t nbg = cdiv(nkg, (uint32_t)kNB);
         const uint32_t nbd = cdiv(dq_per, (uint32_t)kNB);
@@ -909,16 +984,28 @@ static bool glm_shape(uint32_t H, uint32_t I, uint32_t SI, uint32_t E, uint32_t 
     return H == 6144 && I == 2048 && SI == 2048 && E == 256 && K == 8;
 }
 
+// The decode kernel instantiation for a shape and shared-expert format.
+static const void* decode_fn(bool glm, bool sh4) {
+    return glm ? (sh4 ? (const void*)moe_decode_kernel<true, true> : (const void*)moe_decode_kernel<true, false>)
+               : (sh4 ? (const void*)moe_decode_kernel<false, true> : (const void*)moe_decode_kernel<false, false>);
+}
+
 int decode_max_lds() { return 160 * 1024; }
 
 int decode_occupancy(uint32_t H, uint32_t I, uint32_t SI, uint32_t E, uint32_t K, uint32_t grid, int* per_cu) {
     const Plan p = Plan::make(H, I, SI, K, grid);
     const size_t lds = LdsMap::make(H, SI, E, K, p).bytes;
-    const void* fn = glm_shape(H, I, SI, E, K) ? (const void*)moe_decode_kernel<true>
-                                               : (const void*)moe_decode_kernel<false>;
-    hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    if (e == hipSuccess) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(per_cu, fn, kThreads, lds);
-    return (int)e;
+    int lo = 1 << 30;
+    for (bool sh4 : {false, true}) {  // the fewest of either shared-expert format
+        const void* fn = decode_fn(glm_shape(H, I, SI, E, K), sh4);
+        int n = 0;
+        hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e == hipSuccess) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, kThreads, lds);
+        if (e != hipSuccess) return (int)e;
+        lo = n < lo ? n : lo;
+    }
+    *per_cu = lo;
+    return 0;
 }
 
 int route_occupancy(uint32_t H, uint32_t E, int* per_cu) {
@@ -955,20 +1042,21 @@ int launch_slot_fill(const uint8_t** table, uint32_t E, const int32_t* ids, cons
 }
 
 int launch_decode(const DecodeArgs* d_args, const DecodeDyn& dyn, uint32_t H, uint32_t I, uint32_t SI, uint32_t E,
-                  uint32_t K, uint32_t grid, void* stream) {
+                  uint32_t K, uint32_t grid, bool sh4, void* stream) {
     const Plan p = Plan::make(H, I, SI, K, grid);
     const size_t lds = LdsMap::make(H, SI, E, K, p).bytes;
-    const void* fn = glm_shape(H, I, SI, E, K) ? (const void*)moe_decode_kernel<true>
-                                               : (const void*)moe_decode_kernel<false>;
-    hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    const bool glm = glm_shape(H, I, SI, E, K);
+    hipError_t e = hipFuncSetAttribute(decode_fn(glm, sh4), hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return (int)e;
 #define WL_DECODE_ARGS                                                                                        \
     d_args, dyn.hidden, dyn.sh_native, dyn.router_w, dyn.ln_w, dyn.lslot, dyn.seg, dyn.epoch, dyn.bias, dyn.slot_tab, \
         dyn.resid, dyn.out
-    if (glm_shape(H, I, SI, E, K))
-        hipLaunchKernelGGL(moe_decode_kernel<true>, dim3(grid), dim3(kThreads), lds, (hipStream_t)stream, WL_DECODE_ARGS);
-    else
-        hipLaunchKernelGGL(moe_decode_kernel<false>, dim3(grid), dim3(kThreads), lds, (hipStream_t)stream, WL_DECODE_ARGS);
+    const dim3 gr(grid), bl(kThreads);
+    hipStream_t st = (hipStream_t)stream;
+    if (glm && sh4) hipLaunchKernelGGL((moe_decode_kernel<true, true>), gr, bl, lds, st, WL_DECODE_ARGS);
+    else if (glm) hipLaunchKernelGGL((moe_decode_kernel<true, false>), gr, bl, lds, st, WL_DECODE_ARGS);
+    else if (sh4) hipLaunchKernelGGL((moe_decode_kernel<false, true>), gr, bl, lds, st, WL_DECODE_ARGS);
+    else hipLaunchKernelGGL((moe_decode_kernel<false, false>), gr, bl, lds, st, WL_DECODE_ARGS);
 #undef WL_DECODE_ARGS
     return (int)hipGetLastError();
 }

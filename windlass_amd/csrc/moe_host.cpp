@@ -25,6 +25,7 @@ struct LayerState {
     const float* bias = nullptr;
     const uint16_t* ln = nullptr;
     uint8_t* shared = nullptr;  // context-owned native copy of the shared expert
+    size_t shared_bytes = 0;
     int32_t shared_dtype = WL_SHARED_BF16;
     bool set = false;
 };
@@ -43,8 +44,6 @@ struct CacheState {
     std::vector<uint8_t> spec;        // filled by a speculative copy, not yet requested
     hipEvent_t gate = nullptr;        // compute-stream point that copies into reused slots wait for
     bool gate_recorded = false;
-    hipEvent_t ids_ev = nullptr, pred_ev = nullptr;
-    int32_t* h_ids = nullptr;         // pinned: [0,32) ids, [32] error word, [40,72) predicted ids
     bool speculate = false;
     bool spec_pending = false;
     uint32_t spec_layer = 0;
@@ -58,6 +57,7 @@ struct CacheState {
 // the last chunk either path ran (read by the test hooks).
 struct BatchScratch {
     uint32_t cap = 0;
+    bool sh4 = false;  // sized with the MXFP4 shared expert's rows
     void* buf = nullptr;
     wl::BatchArgs b{};
     wl::BatchArgs last{};
@@ -106,6 +106,23 @@ struct wl_ctx {
     CacheState cache;
     BatchScratch batch;
     void* scratch = nullptr;  // this device's static scratch (wl_run_moe_batched_noalloc)
+    bool any_sh4 = false;     // some layer has an MXFP4 shared expert (the batched scratch keeps its rows)
+    // the expert source of layers with no expert bound (src.get null: none)
+    wl_expert_source src{};
+    bool src_cache = false;        // src is the built-in cache
+    wl_status src_status = WL_OK;  // a failure the built-in cache's callbacks reported
+    uint8_t* stage = nullptr;      // native staging blocks for a reference-layout source
+    uint32_t stage_n = 0;
+    int32_t* h_pin = nullptr;      // pinned host words, PinMap layout
+    std::vector<int32_t> uniq;     // a batched chunk's routed experts (capacity E, reserved once)
+    hipEvent_t ids_ev = nullptr, pred_ev = nullptr;
+};
+
+// Word offsets in wl_ctx::h_pin: routed ids, the abort word, predicted ids of
+// the next layer (speculation), the batched layer's per-expert counts.
+struct PinMap {
+    static constexpr uint32_t ids = 0, abort = 32, pred = 40, counts = 96;
+    static size_t bytes(uint32_t E) { return 4u * ((size_t)counts + E); }
 };
 
 namespace {
@@ -338,14 +355,16 @@ void wl_destroy(wl_ctx* c) {
     {
         CacheState& C = c->cache;
         for (hipEvent_t e : C.slot_ev) (void)hipEventDestroy(e);
-        for (hipEvent_t e : {C.gate, C.ids_ev, C.pred_ev})
-            if (e) (void)hipEventDestroy(e);
+        if (C.gate) (void)hipEventDestroy(C.gate);
         for (hipStream_t st : C.copy)
             if (st) (void)hipStreamDestroy(st);
-        if (C.h_ids) (void)hipHostFree(C.h_ids);
         delete C.lru;
     }
     if (c->batch.buf) (void)hipFree(c->batch.buf);
+    if (c->stage) (void)hipFree(c->stage);
+    if (c->h_pin) (void)hipHostFree(c->h_pin);
+    for (hipEvent_t e : {c->ids_ev, c->pred_ev})
+        if (e) (void)hipEventDestroy(e);
     for (void* p : c->allocs) (void)hipFree(p);
     uc_release(c->device, c->uc_bytes, c->uc_block);
     delete c;
@@ -353,32 +372,70 @@ void wl_destroy(wl_ctx* c) {
 
 const char* wl_last_error(const wl_ctx* c) { return c ? c->err.c_str() : "null context"; }
 
-wl_status wl_set_layer(wl_ctx* c, uint32_t layer, const uint16_t* d_router_w, const float* d_router_bias,
-                       const uint16_t* d_post_attn_ln, const void* d_shared, int32_t shared_dtype) {
+// Binds a layer's router, bias and norm, and converts its shared expert into
+// context-owned memory: bf16 (NativeShared) from `bf16`, or MXFP4
+// (NativeShared4) from the six reference tensors `parts` (gate_w, gate_s,
+// up_w, up_s, down_w, down_s).
+static wl_status set_layer(wl_ctx* c, uint32_t layer, const uint16_t* d_router_w, const float* d_router_bias,
+                           const uint16_t* d_post_attn_ln, const uint16_t* bf16, const uint8_t* const* parts) {
     if (!c) return WL_ERR_INVALID;
     if (layer >= c->cfg.n_layers) return fail(c, WL_ERR_INVALID, "layer %u >= n_layers %u", layer, c->cfg.n_layers);
-    if (!d_router_w || !d_router_bias || !d_shared)
-        return fail(c, WL_ERR_INVALID, "router weight, router bias and shared expert are required");
-    if (shared_dtype != WL_SHARED_BF16)
-        return fail(c, WL_ERR_INVALID, "shared_dtype %d not supported by this build (bf16 only)", shared_dtype);
+    if (!d_router_w || !d_router_bias) return fail(c, WL_ERR_INVALID, "router weight and router bias are required");
+    const uint32_t H = c->cfg.hidden, SI = c->SI;
+    if (parts) {
+        if (c->cfg.n_shared != 1)
+            return fail(c, WL_ERR_INVALID, "an MXFP4 shared expert needs n_shared = 1 (inter %u), not %u",
+                        c->cfg.moe_inter, c->cfg.n_shared);
+        for (int r = 0; r < 6; r++)
+            if (!parts[r]) return fail(c, WL_ERR_INVALID, "MXFP4 shared expert tensor %d is null", r);
+    } else if (!bf16) {
+        return fail(c, WL_ERR_INVALID, "the shared expert is required");
+    }
     LayerState& L = c->layers[layer];
+    const size_t need = parts ? wl::NativeShared4::make(H, SI).total : wl::NativeShared::make(H, SI).total;
+    if (L.shared_bytes < need) {
+        // a buffer too small for the new format stays owned by the context until it is destroyed
+        wl_status st = dalloc(c, &L.shared, need);
+        if (st != WL_OK) return st;
+        L.shared_bytes = need;
+    }
+    const int le = parts ? wl::launch_shared4_to_native(parts, L.shared, H, SI, nullptr)
+                         : wl::launch_shared_to_native(bf16, (uint16_t*)L.shared, H, SI, nullptr);
+    if (le != 0) return fail(c, WL_ERR_HIP, "shared expert conversion launch failed");
+    hipError_t se = hipDeviceSynchronize();
+    if (se != hipSuccess) return hip_fail(c, se, "shared expert conversion");
     L.router_w = d_router_w;
     L.bias = d_router_bias;
     L.ln = d_post_attn_ln;
-    if (!L.shared) {
-        wl_status st = dalloc(c, &L.shared, wl::NativeShared::make(c->cfg.hidden, c->SI).total);
-        if (st != WL_OK) return st;
-    }
-    if (wl::launch_shared_to_native((const uint16_t*)d_shared, (uint16_t*)L.shared, c->cfg.hidden, c->SI, nullptr) != 0)
-        return fail(c, WL_ERR_HIP, "shared expert conversion launch failed");
-    hipError_t se = hipDeviceSynchronize();
-    if (se != hipSuccess) return hip_fail(c, se, "shared expert conversion");
-    L.shared_dtype = shared_dtype;
+    L.shared_dtype = parts ? WL_SHARED_MXFP4 : WL_SHARED_BF16;
+    if (parts) c->any_sh4 = true;
     const wl::DecodeArgs a = layer_record(c, layer);
     hipError_t e = hipMemcpy(c->d_largs + layer, &a, sizeof(a), hipMemcpyHostToDevice);
     if (e != hipSuccess) return hip_fail(c, e, "layer record upload");
     L.set = true;
     return WL_OK;
+}
+
+wl_status wl_set_layer(wl_ctx* c, uint32_t layer, const uint16_t* d_router_w, const float* d_router_bias,
+                       const uint16_t* d_post_attn_ln, const void* d_shared, int32_t shared_dtype) {
+    if (!c) return WL_ERR_INVALID;
+    if (!d_shared) return fail(c, WL_ERR_INVALID, "the shared expert is required");
+    if (shared_dtype == WL_SHARED_BF16)
+        return set_layer(c, layer, d_router_w, d_router_bias, d_post_attn_ln, (const uint16_t*)d_shared, nullptr);
+    if (shared_dtype != WL_SHARED_MXFP4) return fail(c, WL_ERR_INVALID, "unknown shared_dtype %d", shared_dtype);
+    wl_expert_layout l;
+    if (wl_expert_layout_of(&c->cfg, c->SI, &l) != WL_OK) return fail(c, WL_ERR_INVALID, "shared expert layout");
+    const uint8_t* b = (const uint8_t*)d_shared;
+    const uint8_t* parts[6] = {b + l.gw_off, b + l.gs_off, b + l.uw_off, b + l.us_off, b + l.dw_off, b + l.ds_off};
+    return set_layer(c, layer, d_router_w, d_router_bias, d_post_attn_ln, nullptr, parts);
+}
+
+wl_status wl_set_layer_mxfp4(wl_ctx* c, uint32_t layer, const uint16_t* d_router_w, const float* d_router_bias,
+                             const uint16_t* d_post_attn_ln, const uint8_t* d_sh_gate_w, const uint8_t* d_sh_gate_s,
+                             const uint8_t* d_sh_up_w, const uint8_t* d_sh_up_s, const uint8_t* d_sh_down_w,
+                             const uint8_t* d_sh_down_s) {
+    const uint8_t* parts[6] = {d_sh_gate_w, d_sh_gate_s, d_sh_up_w, d_sh_up_s, d_sh_down_w, d_sh_down_s};
+    return set_layer(c, layer, d_router_w, d_router_bias, d_post_attn_ln, nullptr, parts);
 }
 
 wl_status wl_slot_bind(wl_ctx* c, uint32_t layer, uint32_t expert, const uint8_t* d_block) {
@@ -493,13 +550,85 @@ static wl_status cache_resolve(wl_ctx* c, uint32_t layer, const int32_t* ids, ui
     return WL_OK;
 }
 
-// Routes `layer` on the device, resolves its ids on the host and fills its
-// slot table; with speculation and a next layer, also routes `next` on the
-// same input and copies the predicted ids back (resolved after the layer's
+// The pinned words and events of the source path (allocated once).
+static wl_status ensure_pin(wl_ctx* c) {
+    hipError_t e;
+    if (!c->h_pin && (e = hipHostMalloc((void**)&c->h_pin, PinMap::bytes(c->cfg.n_routed_experts),
+                                        hipHostMallocDefault)) != hipSuccess) {
+        c->h_pin = nullptr;
+        return fail(c, WL_ERR_OOM, "pinned id buffer: %s", hipGetErrorString(e));
+    }
+    for (hipEvent_t* ev : {&c->ids_ev, &c->pred_ev})
+        if (!*ev && (e = hipEventCreateWithFlags(ev, hipEventDisableTiming)) != hipSuccess) {
+            *ev = nullptr;
+            return hip_fail(c, e, "source event");
+        }
+    c->uniq.reserve(c->cfg.n_routed_experts);
+    return WL_OK;
+}
+
+// At least n native staging blocks for a reference-layout source (growing
+// synchronises the device: blocks in use by queued work are freed).
+static wl_status ensure_stage(wl_ctx* c, uint32_t n) {
+    if (n <= c->stage_n) return WL_OK;
+    hipError_t e = hipDeviceSynchronize();
+    if (e != hipSuccess) return hip_fail(c, e, "staging resize");
+    if (c->stage) (void)hipFree(c->stage);
+    c->stage = nullptr;
+    c->stage_n = 0;
+    void* p = nullptr;
+    if ((e = hipMalloc(&p, (size_t)n * c->native_bytes)) != hipSuccess)
+        return fail(c, WL_ERR_OOM, "%u staging blocks: %s", n, hipGetErrorString(e));
+    c->stage = (uint8_t*)p;
+    c->stage_n = n;
+    return WL_OK;
+}
+
+// The blocks of n experts of `layer` through the source: get_async (or get)
+// each, in order; a reference-layout block is converted on `s` into staging
+// block k. ptrs[k] = the native block of ids[k].
+static wl_status source_fetch(wl_ctx* c, uint32_t layer, const int32_t* ids, uint32_t n, hipStream_t s,
+                              const uint8_t** ptrs) {
+    const wl_expert_source& S = c->src;
+    for (uint32_t k = 0; k < n; k++) {
+        c->src_status = WL_OK;
+        const uint8_t* p = S.get_async ? S.get_async(S.user, layer, (uint32_t)ids[k], (void*)s)
+                                       : S.get(S.user, layer, (uint32_t)ids[k]);
+        if (!p) {
+            if (c->src_status != WL_OK) return c->src_status;
+            return fail(c, WL_ERR_IO, "expert source returned no block for layer %u expert %d", layer, ids[k]);
+        }
+        if (!S.native) {
+            if (k >= c->stage_n) return fail(c, WL_ERR_STATE, "%u staging blocks for %u experts", c->stage_n, n);
+            uint8_t* dst = c->stage + (size_t)k * c->native_bytes;
+            if (wl::launch_expert_to_native(p, dst, c->cfg.hidden, c->cfg.moe_inter, 0, s) != 0)
+                return fail(c, WL_ERR_HIP, "expert conversion launch failed");
+            p = dst;
+        }
+        ptrs[k] = p;
+    }
+    return WL_OK;
+}
+
+// Announces n experts of `layer` to the source (its prefetch, if any).
+static wl_status source_prefetch(wl_ctx* c, uint32_t layer, const int32_t* ids, uint32_t n, hipStream_t s) {
+    if (!c->src.prefetch) return WL_OK;
+    c->src_status = WL_OK;
+    c->src.prefetch(c->src.user, layer, ids, n, (void*)s);
+    return c->src_status;
+}
+
+// A layer with no expert bound, through the expert source (run_moe's pattern,
+// src/glm_layer_runner.cuh:391-418): route it on the device, read its ids back
+// (the reference's one host round trip per layer), announce them, fetch each
+// and fill the layer's slot table with the blocks (every other entry null, so
+// a routing mismatch raises E_NOT_RESIDENT instead of reading a stale slot).
+// With the built-in cache and speculation on, also routes layer `next` on the
+// same input and copies its predicted ids back (resolved after the layer's
 // launch, by cache_speculate).
-static wl_status cache_prepare(wl_ctx* c, uint32_t layer, const float* d_hidden, uint32_t next, hipStream_t s) {
-    CacheState& C = c->cache;
+static wl_status source_prepare(wl_ctx* c, uint32_t layer, const float* d_hidden, uint32_t next, hipStream_t s) {
     const uint32_t H = c->cfg.hidden, E = c->cfg.n_routed_experts, K = c->cfg.n_experts_per_tok;
+    int32_t* pin = c->h_pin;
     hipError_t e;
     if (++c->epoch >= 0x7FFFFFFFu) c->epoch = 1;
     const uint32_t route_epoch = c->epoch;
@@ -507,24 +636,26 @@ static wl_status cache_prepare(wl_ctx* c, uint32_t layer, const float* d_hidden,
     if (le != 0) return hip_fail(c, (hipError_t)le, "route launch");
     // the abort word names the last call that raised an error: only an error of
     // this routing launch fails this call (older ones stay for wl_check_error)
-    if ((e = hipMemcpyAsync(C.h_ids, c->idx, 4 * (size_t)K, hipMemcpyDeviceToHost, s)) != hipSuccess ||
-        (e = hipMemcpyAsync(C.h_ids + 32, c->sync + c->sm.abort, 4, hipMemcpyDeviceToHost, s)) != hipSuccess ||
-        (e = hipEventRecord(C.ids_ev, s)) != hipSuccess || (e = hipEventSynchronize(C.ids_ev)) != hipSuccess)
+    if ((e = hipMemcpyAsync(pin + PinMap::ids, c->idx, 4 * (size_t)K, hipMemcpyDeviceToHost, s)) != hipSuccess ||
+        (e = hipMemcpyAsync(pin + PinMap::abort, c->sync + c->sm.abort, 4, hipMemcpyDeviceToHost, s)) != hipSuccess ||
+        (e = hipEventRecord(c->ids_ev, s)) != hipSuccess || (e = hipEventSynchronize(c->ids_ev)) != hipSuccess)
         return hip_fail(c, e, "routing read-back");
-    if ((uint32_t)C.h_ids[32] == route_epoch)
+    if ((uint32_t)pin[PinMap::abort] == route_epoch)
         return fail(c, WL_ERR_DEVICE, "the routing kernel of layer %u reported an error (see wl_check_error)", layer);
-    uint8_t* ptrs[WL_MAX_TOPK];
-    wl_status st = cache_resolve(c, layer, C.h_ids, K, s, false, ptrs);
+    wl_status st = source_prefetch(c, layer, pin + PinMap::ids, K, s);
     if (st != WL_OK) return st;
-    le = wl::launch_slot_fill(c->d_slot + (size_t)layer * E, E, C.h_ids, ptrs, K, s);
+    const uint8_t* ptrs[WL_MAX_TOPK];
+    if ((st = source_fetch(c, layer, pin + PinMap::ids, K, s, ptrs)) != WL_OK) return st;
+    le = wl::launch_slot_fill(c->d_slot + (size_t)layer * E, E, pin + PinMap::ids, ptrs, K, s);
     if (le != 0) return hip_fail(c, (hipError_t)le, "slot table fill");
+    CacheState& C = c->cache;
     C.spec_pending = false;
-    if (C.speculate && next < c->cfg.n_layers && c->n_bound[next] == 0 && c->layers[next].set) {
+    if (c->src_cache && C.speculate && next < c->cfg.n_layers && c->n_bound[next] == 0 && c->layers[next].set) {
         if (++c->epoch >= 0x7FFFFFFFu) c->epoch = 1;
         le = wl::launch_route(c->d_largs + next, d_hidden, c->epoch, H, E, c->grid, s);
         if (le != 0) return hip_fail(c, (hipError_t)le, "speculative route launch");
-        if ((e = hipMemcpyAsync(C.h_ids + 40, c->idx, 4 * (size_t)K, hipMemcpyDeviceToHost, s)) != hipSuccess ||
-            (e = hipEventRecord(C.pred_ev, s)) != hipSuccess)
+        if ((e = hipMemcpyAsync(pin + PinMap::pred, c->idx, 4 * (size_t)K, hipMemcpyDeviceToHost, s)) != hipSuccess ||
+            (e = hipEventRecord(c->pred_ev, s)) != hipSuccess)
             return hip_fail(c, e, "prediction read-back");
         C.spec_pending = true;
         C.spec_layer = next;
@@ -536,9 +667,9 @@ static wl_status cache_speculate(wl_ctx* c, hipStream_t s) {
     CacheState& C = c->cache;
     if (!C.spec_pending) return WL_OK;
     C.spec_pending = false;
-    hipError_t e = hipEventSynchronize(C.pred_ev);
+    hipError_t e = hipEventSynchronize(c->pred_ev);
     if (e != hipSuccess) return hip_fail(c, e, "prediction wait");
-    return cache_resolve(c, C.spec_layer, C.h_ids + 40, c->cfg.n_experts_per_tok, s, true, nullptr);
+    return cache_resolve(c, C.spec_layer, c->h_pin + PinMap::pred, c->cfg.n_experts_per_tok, s, true, nullptr);
 }
 
 static wl_status run_layer(wl_ctx* c, uint32_t layer, const float* d_hidden, const float* d_resid,
@@ -552,11 +683,12 @@ static wl_status run_layer(wl_ctx* c, uint32_t layer, const float* d_hidden, con
         return fail(c, WL_ERR_INVALID, "d_out must not alias the inputs");
     const uint32_t H = c->cfg.hidden, I = c->cfg.moe_inter, E = c->cfg.n_routed_experts,
                    K = c->cfg.n_experts_per_tok, SI = c->SI;
-    const bool cached = c->n_bound[layer] == 0 && c->cache.lru != nullptr;
+    const bool cached = c->n_bound[layer] == 0 && c->src.get != nullptr;
     if (!cached && c->n_bound[layer] != E)
-        return fail(c, WL_ERR_NOT_RESIDENT, "layer %u has %u of %u experts bound", layer, c->n_bound[layer], E);
+        return fail(c, WL_ERR_NOT_RESIDENT, "layer %u has %u of %u experts bound%s", layer, c->n_bound[layer], E,
+                    c->n_bound[layer] == 0 ? " and the context has no expert source" : "");
     if (cached) {
-        wl_status s = cache_prepare(c, layer, d_hidden, next, (hipStream_t)stream);
+        wl_status s = source_prepare(c, layer, d_hidden, next, (hipStream_t)stream);
         if (s != WL_OK) return s;
     }
 
@@ -574,7 +706,8 @@ static wl_status run_layer(wl_ctx* c, uint32_t layer, const float* d_hidden, con
     dyn.out = d_out;
     auto launch = [&](uint32_t lo, uint32_t hi) -> wl_status {
         dyn.seg = lo | (hi << 8) | ((c->taps ? 1u : 0u) << 16);
-        int e = wl::launch_decode(c->d_largs + layer, dyn, H, I, SI, E, K, c->grid, stream);
+        int e = wl::launch_decode(c->d_largs + layer, dyn, H, I, SI, E, K, c->grid,
+                                  L.shared_dtype == WL_SHARED_MXFP4, stream);
         if (e != 0) return hip_fail(c, (hipError_t)e, "decode launch");
         return WL_OK;
     };
@@ -663,8 +796,9 @@ static size_t batch_layout(const wl_ctx* c, uint32_t T, uint8_t* base, wl::Batch
     take(&x.lists, 4 * E * t);
     take(&x.ent, 4 * t * K);
     take(&x.pos, 4 * t * K);
-    take(&x.mid3, 6 * t * K * I);
-    take(&x.expout, 4 * t * K * H);
+    const size_t Kr = K + (c->any_sh4 ? 1u : 0u);  // + the MXFP4 shared expert's rows
+    take(&x.mid3, 6 * t * Kr * I);
+    take(&x.expout, 4 * t * Kr * H);
     take(&x.smid3, 6 * t * SI);
     take(&x.shout, 4 * t * H);
     return (o + 255u) & ~(size_t)255u;
@@ -683,7 +817,7 @@ static uint32_t batch_tokens_fitting(const wl_ctx* c, size_t bytes) {
 
 static wl_status batch_reserve(wl_ctx* c, uint32_t T) {
     BatchScratch& B = c->batch;
-    if (T <= B.cap) return WL_OK;
+    if (T <= B.cap && B.sh4 == c->any_sh4) return WL_OK;
     hipError_t e = hipDeviceSynchronize();  // launches in flight may still use the old buffers
     if (e != hipSuccess) return hip_fail(c, e, "batched scratch resize");
     if (B.buf) (void)hipFree(B.buf);
@@ -696,6 +830,7 @@ static wl_status batch_reserve(wl_ctx* c, uint32_t T) {
     }
     batch_layout(c, T, (uint8_t*)B.buf, &B.b);
     B.cap = T;
+    B.sh4 = c->any_sh4;
     return WL_OK;
 }
 
@@ -710,37 +845,97 @@ static wl_status batched_check(wl_ctx* c, uint32_t layer, uint32_t n_tokens, con
     if (((uintptr_t)d_hidden | (uintptr_t)d_out | (uintptr_t)d_resid) % 16u)
         return fail(c, WL_ERR_INVALID, "batched buffers must be 16-byte aligned");
     const uint32_t E = c->cfg.n_routed_experts;
-    if (c->n_bound[layer] != E)
-        return fail(c, WL_ERR_NOT_RESIDENT, "batched layer %u needs every expert bound (%u of %u)", layer,
-                    c->n_bound[layer], E);
+    if (c->n_bound[layer] != E && !(c->n_bound[layer] == 0 && c->src.get))
+        return fail(c, WL_ERR_NOT_RESIDENT, "batched layer %u has %u of %u experts bound%s", layer, c->n_bound[layer],
+                    E, c->n_bound[layer] == 0 ? " and the context has no expert source" : "");
     return WL_OK;
 }
 
 // Chunk cap that keeps every piece array of the kernels under 2 GB (they
 // address them with 32-bit buffer offsets).
 static uint32_t batch_offset_cap(const wl_ctx* c) {
-    const uint64_t H = c->cfg.hidden, K = c->cfg.n_experts_per_tok;
+    const uint64_t H = c->cfg.hidden, K = c->cfg.n_experts_per_tok + (c->any_sh4 ? 1u : 0u);
     const uint64_t row = 6ull * K * std::max<uint64_t>(std::max<uint64_t>(H, c->cfg.moe_inter), c->SI);
     return (uint32_t)std::min<uint64_t>(kBatchChunk, ((1ull << 31) - 1) / row);
 }
 
+// The GEMMs of a source-backed batched chunk (routing already enqueued): read
+// the per-expert counts back, then fetch the routed set through the source,
+// every unique expert once, in ascending order and in chunks of at most 32
+// (run_moe_batched's chunking, src/glm_layer_runner.cuh:869-902): announce
+// the chunk, fetch its blocks, point the slot table at them (null elsewhere)
+// and run the GEMMs of that chunk's experts (the shared expert's with the
+// first chunk). may_grow: reference-layout staging may grow to 32 blocks
+// (the allocation-free entry point keeps the staging it has).
+static wl_status batched_source_gemms(wl_ctx* c, uint32_t layer, wl::BatchArgs b, bool may_grow, hipStream_t s) {
+    const uint32_t E = c->cfg.n_routed_experts;
+    uint32_t* counts = (uint32_t*)(c->h_pin + PinMap::counts);
+    hipError_t e;
+    if ((e = hipMemcpyAsync(counts, b.counts, 4 * (size_t)E, hipMemcpyDeviceToHost, s)) != hipSuccess ||
+        (e = hipEventRecord(c->ids_ev, s)) != hipSuccess || (e = hipEventSynchronize(c->ids_ev)) != hipSuccess)
+        return hip_fail(c, e, "batched routing read-back");
+    std::vector<int32_t>& uniq = c->uniq;  // reserved for E ids: no allocation here
+    uniq.clear();
+    for (uint32_t x = 0; x < E; x++)
+        if (counts[x]) uniq.push_back((int32_t)x);
+    uint32_t ech = 32;
+    if (c->src_cache) ech = std::min(ech, c->cache.capacity / 2u);
+    if (!c->src.native) {
+        if (may_grow) {
+            wl_status st = ensure_stage(c, ech);
+            if (st != WL_OK) return st;
+        }
+        ech = std::min(ech, c->stage_n);
+    }
+    if (ech == 0) return fail(c, WL_ERR_STATE, "no room to fetch experts");
+    for (size_t i = 0; i < uniq.size(); i += ech) {
+        const uint32_t n = (uint32_t)std::min<size_t>(ech, uniq.size() - i);
+        const int32_t* ids = uniq.data() + i;
+        wl_status st = source_prefetch(c, layer, ids, n, s);
+        if (st != WL_OK) return st;
+        const uint8_t* ptrs[32];
+        if ((st = source_fetch(c, layer, ids, n, s, ptrs)) != WL_OK) return st;
+        int le = wl::launch_slot_fill(c->d_slot + (size_t)layer * E, E, ids, ptrs, n, s);
+        if (le != 0) return hip_fail(c, (hipError_t)le, "slot table fill");
+        b.flags = (b.flags & wl::kBatchShared4) | wl::kBatchSkipUnbound | (i == 0 ? 0u : wl::kBatchNoShared);
+        le = wl::launch_batched(c->d_largs + layer, b, c->cfg.hidden, c->cfg.moe_inter, c->SI, E,
+                                c->cfg.n_experts_per_tok, (uint32_t)c->n_cu, wl::kPhaseGemm, s);
+        if (le != 0) return hip_fail(c, (hipError_t)le, "batched GEMM launch");
+    }
+    return WL_OK;
+}
+
 // The batched layer in chunks of at most `chunk` tokens, every chunk on the
-// buffers of `scratch` (sized for `chunk` tokens).
+// buffers of `scratch` (sized for `chunk` tokens). A layer with no expert
+// bound fetches its experts through the context's source.
 static wl_status batched_run(wl_ctx* c, uint32_t layer, uint32_t n_tokens, const float* d_hidden,
                              const float* d_resid, float* d_out, const wl::BatchArgs& scratch, uint32_t chunk,
-                             void* stream) {
+                             bool may_grow, void* stream) {
     const uint64_t H = c->cfg.hidden;
+    const uint32_t E = c->cfg.n_routed_experts, K = c->cfg.n_experts_per_tok;
+    const bool via_src = c->n_bound[layer] == 0;
     for (uint32_t t0 = 0; t0 < n_tokens; t0 += chunk) {
         wl::BatchArgs b = scratch;
         b.T = std::min(chunk, n_tokens - t0);
+        b.flags = c->layers[layer].shared_dtype == WL_SHARED_MXFP4 ? wl::kBatchShared4 : 0u;
         b.hidden = d_hidden + (size_t)t0 * H;
         b.resid = d_resid ? d_resid + (size_t)t0 * H : nullptr;
         b.out = d_out + (size_t)t0 * H;
         c->batch.last = b;
         c->batch.ran = true;
-        int e = wl::launch_batched(c->d_largs + layer, b, c->cfg.hidden, c->cfg.moe_inter, c->SI,
-                                   c->cfg.n_routed_experts, c->cfg.n_experts_per_tok, (uint32_t)c->n_cu, stream);
-        if (e != 0) return hip_fail(c, (hipError_t)e, "batched launch");
+        auto launch = [&](uint32_t phases) -> wl_status {
+            const int e = wl::launch_batched(c->d_largs + layer, b, c->cfg.hidden, c->cfg.moe_inter, c->SI, E, K,
+                                             (uint32_t)c->n_cu, phases, stream);
+            return e == 0 ? WL_OK : hip_fail(c, (hipError_t)e, "batched launch");
+        };
+        wl_status s;
+        if (!via_src) {
+            if ((s = launch(wl::kPhaseAll)) != WL_OK) return s;
+            continue;
+        }
+        if ((s = launch(wl::kPhaseRoute)) != WL_OK) return s;
+        if ((s = batched_source_gemms(c, layer, b, may_grow, (hipStream_t)stream)) != WL_OK) return s;
+        if ((s = launch(wl::kPhaseCombine)) != WL_OK) return s;
     }
     return WL_OK;
 }
@@ -755,7 +950,7 @@ wl_status wl_run_moe_batched(wl_ctx* c, uint32_t layer, uint32_t n_tokens, const
     const uint32_t chunk = batch_offset_cap(c);
     if (chunk == 0) return fail(c, WL_ERR_INVALID, "batched rows too large for 32-bit offsets");
     if ((s = batch_reserve(c, std::min(n_tokens, chunk))) != WL_OK) return s;
-    return batched_run(c, layer, n_tokens, d_hidden, d_resid, d_out, c->batch.b, chunk, stream);
+    return batched_run(c, layer, n_tokens, d_hidden, d_resid, d_out, c->batch.b, chunk, true, stream);
 }
 
 wl_status wl_run_moe_batched_noalloc(wl_ctx* c, uint32_t layer, uint32_t n_tokens, const float* d_hidden,
@@ -770,7 +965,7 @@ wl_status wl_run_moe_batched_noalloc(wl_ctx* c, uint32_t layer, uint32_t n_token
                     batch_layout(c, 1, nullptr, nullptr), wl::noalloc_scratch_bytes());
     wl::BatchArgs scratch{};
     batch_layout(c, chunk, (uint8_t*)c->scratch, &scratch);
-    return batched_run(c, layer, n_tokens, d_hidden, d_resid, d_out, scratch, chunk, stream);
+    return batched_run(c, layer, n_tokens, d_hidden, d_resid, d_out, scratch, chunk, false, stream);
 }
 
 wl_status wl_batched_counts(wl_ctx* c, uint32_t* h_counts) {
@@ -800,10 +995,60 @@ wl_status wl_batched_routing(wl_ctx* c, uint32_t max_tokens, uint32_t* h_n_token
     return WL_OK;
 }
 
+// The built-in cache as an expert source (the reference's ExpertCache is an
+// ExpertSource too, src/glm_expert_cache.cuh:99): prefetch resolves the
+// experts (hits and misses counted, copies of the misses started on the side
+// streams), get_async hands out a resolved block with the caller's stream
+// ordered after its copy, get does the same and waits for the copy.
+// Failures are reported through wl_ctx::src_status (the message in c->err).
+static void cache_src_prefetch(void* u, uint32_t layer, const int32_t* ids, uint32_t n, void* stream) {
+    wl_ctx* c = (wl_ctx*)u;
+    const wl_status s = wl_cache_prefetch(c, layer, ids, n, stream);
+    if (s != WL_OK) c->src_status = s;
+}
+static const uint8_t* cache_src_get_async(void* u, uint32_t layer, uint32_t expert, void* stream) {
+    wl_ctx* c = (wl_ctx*)u;
+    uint8_t* p = nullptr;
+    const wl_status s = wl_cache_get(c, layer, expert, stream, &p);
+    if (s != WL_OK) {
+        c->src_status = s;
+        return nullptr;
+    }
+    return p;
+}
+static const uint8_t* cache_src_get(void* u, uint32_t layer, uint32_t expert) {
+    wl_ctx* c = (wl_ctx*)u;
+    const uint8_t* p = cache_src_get_async(u, layer, expert, nullptr);
+    if (p) {
+        const hipError_t e = hipStreamSynchronize(nullptr);
+        if (e != hipSuccess) {
+            c->src_status = hip_fail(c, e, "expert copy wait");
+            return nullptr;
+        }
+    }
+    return p;
+}
+
+wl_status wl_set_expert_source(wl_ctx* c, const wl_expert_source* src) {
+    if (!c) return WL_ERR_INVALID;
+    if (c->src_cache) return fail(c, WL_ERR_STATE, "the context's built-in cache is its expert source");
+    if (!src) {
+        c->src = wl_expert_source{};
+        return WL_OK;
+    }
+    if (!src->get) return fail(c, WL_ERR_INVALID, "an expert source needs get");
+    wl_status s = ensure_pin(c);
+    if (s != WL_OK) return s;
+    if (!src->native && (s = ensure_stage(c, c->cfg.n_experts_per_tok)) != WL_OK) return s;
+    c->src = *src;
+    return WL_OK;
+}
+
 wl_status wl_cache_create(wl_ctx* c, uint32_t capacity, wl_host_block_fn host_block, void* user) {
     if (!c) return WL_ERR_INVALID;
     CacheState& C = c->cache;
     if (C.lru) return fail(c, WL_ERR_STATE, "the context already has a cache");
+    if (c->src.get) return fail(c, WL_ERR_STATE, "the context already has an expert source");
     if (!host_block) return fail(c, WL_ERR_INVALID, "host_block is null");
     if (capacity < 2u * c->cfg.n_experts_per_tok)
         return fail(c, WL_ERR_INVALID, "capacity %u < 2 x n_experts_per_tok", capacity);
@@ -816,18 +1061,19 @@ wl_status wl_cache_create(wl_ctx* c, uint32_t capacity, wl_host_block_fn host_bl
     C.capacity = capacity;
     C.fn = host_block;
     C.user = user;
-    if ((e = hipHostMalloc((void**)&C.h_ids, 4 * 80, hipHostMallocDefault)) != hipSuccess)
-        return fail(c, WL_ERR_OOM, "pinned id buffer: %s", hipGetErrorString(e));
+    wl_status ps = ensure_pin(c);
+    if (ps != WL_OK) return ps;
     for (hipStream_t& st : C.copy)
         if ((e = hipStreamCreateWithFlags(&st, hipStreamNonBlocking)) != hipSuccess) return hip_fail(c, e, "copy stream");
-    for (hipEvent_t* ev : {&C.gate, &C.ids_ev, &C.pred_ev})
-        if ((e = hipEventCreateWithFlags(ev, hipEventDisableTiming)) != hipSuccess) return hip_fail(c, e, "cache event");
+    if ((e = hipEventCreateWithFlags(&C.gate, hipEventDisableTiming)) != hipSuccess) return hip_fail(c, e, "cache event");
     C.slot_ev.assign(capacity, nullptr);
     for (hipEvent_t& ev : C.slot_ev)
         if ((e = hipEventCreateWithFlags(&ev, hipEventDisableTiming)) != hipSuccess) return hip_fail(c, e, "slot event");
     C.has_ev.assign(capacity, 0);
     C.spec.assign(capacity, 0);
     C.lru = new wl::SlotLru(capacity);
+    c->src = wl_expert_source{c, cache_src_get, cache_src_prefetch, cache_src_get_async, 1};
+    c->src_cache = true;
     return WL_OK;
 }
 

@@ -12,16 +12,18 @@
 
 namespace wl {
 
+// The six regions of a reference-layout expert (gate_w, gate_s, up_w, up_s,
+// down_w, down_s): one pointer each (a packed block's regions, or six
+// separate tensors), or all null: synthesise from `key`.
 struct RefBlock {
-    const uint8_t* src;   // reference-layout block, or null: synthesise
-    uint64_t off[6];      // region offsets: gate_w, gate_s, up_w, up_s, down_w, down_s
+    const uint8_t* src[6];
     uint32_t salt[6];
     uint32_t key;
 };
 
 // 16 weight bytes at byte j (a multiple of 16) of region r.
 __device__ static inline uint4 ref16(const RefBlock& b, int r, uint64_t j) {
-    if (b.src) return *(const uint4*)(b.src + b.off[r] + j);
+    if (b.src[r]) return *(const uint4*)(b.src[r] + j);
     const uint32_t w0 = (uint32_t)(j / 4);
     uint4 v;
     v.x = mix32(mix32((w0 + 0) ^ b.salt[r]) ^ b.key);
@@ -30,9 +32,14 @@ __device__ static inline uint4 ref16(const RefBlock& b, int r, uint64_t j) {
     v.w = mix32(mix32((w0 + 3) ^ b.salt[r]) ^ b.key);
     return v;
 }
+// 4 weight bytes at byte j (a multiple of 4) of region r.
+__device__ static inline uint32_t ref4(const RefBlock& b, int r, uint64_t j) {
+    if (b.src[r]) return *(const uint32_t*)(b.src[r] + j);
+    return mix32(mix32((uint32_t)(j / 4) ^ b.salt[r]) ^ b.key);
+}
 // Scale byte j of region r.
 __device__ static inline uint32_t ref1(const RefBlock& b, int r, uint64_t j) {
-    if (b.src) return b.src[b.off[r] + j];
+    if (b.src[r]) return b.src[r][j];
     return 118u + mix32(mix32((uint32_t)j ^ b.salt[r]) ^ b.key) % 9u;
 }
 
@@ -107,18 +114,65 @@ __global__ void shared_to_native_kernel(const uint16_t* __restrict__ src, uint16
     }
 }
 
-int launch_expert_to_native(const uint8_t* src, uint8_t* dst, uint32_t H, uint32_t I, uint32_t key, void* stream) {
+// The down projection of an MXFP4 shared expert in the decode kernel's
+// per-tile order (NativeShared4): dn8[T][r] = the 4 bytes of columns
+// [8T, 8T + 8) of down row r, dns8[q][r] = the scale of columns [32q, +32).
+__global__ void shared4_down_kernel(const RefBlock b, uint8_t* __restrict__ dst, uint32_t H, uint32_t SI) {
+    const NativeShared4 L = NativeShared4::make(H, SI);
+    const uint64_t nw = (uint64_t)(SI / 8) * H, nb = (uint64_t)(SI / 32) * H;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < nw + nb;
+         i += (uint64_t)gridDim.x * blockDim.x) {
+        if (i < nw) {
+            const uint32_t T = (uint32_t)(i / H), r = (uint32_t)(i % H);
+            *(uint32_t*)(dst + L.dn8 + 4 * i) = ref4(b, 4, (uint64_t)r * (SI / 2) + 4 * T);
+        } else {
+            const uint64_t k = i - nw;
+            const uint32_t q = (uint32_t)(k / H), r = (uint32_t)(k % H);
+            dst[L.dns8 + k] = (uint8_t)ref1(b, 5, (uint64_t)r * (SI / 32) + q);
+        }
+    }
+}
+
+static RefBlock ref_block(const uint8_t* const* parts, uint32_t key) {
     RefBlock b;
-    b.src = src;
+    for (int r = 0; r < 6; r++) {
+        b.src[r] = parts ? parts[r] : nullptr;
+        b.salt[r] = mix32(0x632BE5ABu * (uint32_t)(r + 1));
+    }
+    b.key = key;
+    return b;
+}
+
+static void ref_parts(const uint8_t* src, uint32_t H, uint32_t I, const uint8_t** parts) {
     uint64_t o = 0;
     const uint64_t len[6] = {(uint64_t)I * H / 2, (uint64_t)I * H / 32, (uint64_t)I * H / 2,
                              (uint64_t)I * H / 32, (uint64_t)H * I / 2, (uint64_t)H * I / 32};
     for (int r = 0; r < 6; r++) {
-        b.off[r] = o;
+        parts[r] = src + o;
         o += len[r];
-        b.salt[r] = mix32(0x632BE5ABu * (uint32_t)(r + 1));
     }
-    b.key = key;
+}
+
+int launch_shared4_to_native(const uint8_t* const* parts, uint8_t* dst, uint32_t H, uint32_t SI, void* stream) {
+    const RefBlock b = ref_block(parts, 0u);
+    const uint64_t chunks = NativeLayout::make(H, SI).total / 16;
+    uint64_t blocks = (chunks + 255) / 256;
+    if (blocks > 16384) blocks = 16384;
+    hipLaunchKernelGGL(expert_to_native_kernel, dim3((uint32_t)blocks), dim3(256), 0, (hipStream_t)stream, b,
+                       dst + NativeShared4::make(H, SI).blk, H, SI);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return (int)e;
+    const uint64_t n = (uint64_t)(SI / 8) * H + (uint64_t)(SI / 32) * H;
+    blocks = (n + 255) / 256;
+    if (blocks > 16384) blocks = 16384;
+    hipLaunchKernelGGL(shared4_down_kernel, dim3((uint32_t)blocks), dim3(256), 0, (hipStream_t)stream, b, dst, H, SI);
+    return (int)hipGetLastError();
+}
+
+int launch_expert_to_native(const uint8_t* src, uint8_t* dst, uint32_t H, uint32_t I, uint32_t key, void* stream) {
+    const uint8_t* parts[6];
+    if (src) ref_parts(src, H, I, parts);
+    const RefBlock b = ref_block(src ? parts : nullptr, key);
     const uint64_t chunks = NativeLayout::make(H, I).total / 16;
     uint64_t blocks = (chunks + 255) / 256;
     if (blocks > 16384) blocks = 16384;

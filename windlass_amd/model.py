@@ -22,8 +22,14 @@ import numpy as np
 from . import hip, moe, synthdata
 
 
+# Synthetic MXFP4 shared experts use the routed generator under this expert
+# index (no routed expert has it).
+SHARED_KEY = 0xFFFF
+
+
 class _Layers:
-    def __init__(self, cfg, seed, n_layers, ln_weights=None, bias_offset=None, shared_alias=False):
+    def __init__(self, cfg, seed, n_layers, ln_weights=None, bias_offset=None, shared_alias=False,
+                 shared_mxfp4=False):
         self.c = dict(cfg)
         self.seed = seed
         self.L = n_layers
@@ -40,6 +46,7 @@ class _Layers:
         self._ln_weights = ln_weights
         self._bias_offset = bias_offset
         self._shared_alias = shared_alias
+        self.shared_mxfp4 = shared_mxfp4
         self.dense, self.bufs = [], []
 
     def _bind_dense(self):
@@ -57,14 +64,24 @@ class _Layers:
             rw = hip.DeviceBuffer.from_array(d["router_w"])
             bb = hip.DeviceBuffer.from_array(d["bias"])
             if shared0 is None or not self._shared_alias:
-                shared0 = hip.DeviceBuffer.from_array(d["shared_block"])
+                if self.shared_mxfp4:  # a reference-layout MXFP4 block, inter = SI
+                    shared0 = hip.DeviceBuffer(moe.expert_layout(self.cfg, self.SI).total)
+                    moe.synth_expert(self.cfg, self.seed, self.shared_key(l)[0], SHARED_KEY, shared0.ptr, inter=self.SI)
+                    hip.synchronize()
+                else:
+                    shared0 = hip.DeviceBuffer.from_array(d["shared_block"])
             sb = shared0
             lw = hip.DeviceBuffer.from_array(self._ln_weights[l]) if self._ln_weights is not None else None
             self.bufs.append((rw, bb, sb, lw))
-            self.ctx.set_layer(l, rw.ptr, bb.ptr, lw.ptr if lw else None, sb.ptr)
+            self.ctx.set_layer(l, rw.ptr, bb.ptr, lw.ptr if lw else None, sb.ptr,
+                               moe.SHARED_MXFP4 if self.shared_mxfp4 else moe.SHARED_BF16)
 
     def expert_source_key(self, layer, expert):
         return layer, expert
+
+    def shared_key(self, layer):
+        """(layer, expert) key of layer's synthetic MXFP4 shared expert."""
+        return (0 if self._shared_alias else layer), SHARED_KEY
 
     def close(self):
         self.ctx.close()
@@ -76,8 +93,8 @@ class DeviceModel(_Layers):
     expert fills each slot (default: its own)."""
 
     def __init__(self, cfg, seed, n_layers=1, ln_weights=None, bias_offset=None, expert_key=None,
-                 shared_alias=False):
-        super().__init__(cfg, seed, n_layers, ln_weights, bias_offset, shared_alias)
+                 shared_alias=False, shared_mxfp4=False):
+        super().__init__(cfg, seed, n_layers, ln_weights, bias_offset, shared_alias, shared_mxfp4)
         self._key = expert_key or (lambda l, e: (l, e))
         E = self.E
         self.ctx.slot_pool_create(n_layers * E)
@@ -96,8 +113,8 @@ class DeviceModel(_Layers):
 
 class CachedModel(_Layers):
     def __init__(self, cfg, seed, n_layers, capacity, n_host, ln_weights=None, bias_offset=None,
-                 shared_alias=False):
-        super().__init__(cfg, seed, n_layers, ln_weights, bias_offset, shared_alias)
+                 shared_alias=False, shared_mxfp4=False):
+        super().__init__(cfg, seed, n_layers, ln_weights, bias_offset, shared_alias, shared_mxfp4)
         self.n_host = n_host
         self.nb = moe.native_block_bytes(self.cfg)
         self.host = hip.HostBuffer(n_host * self.nb)
@@ -121,6 +138,59 @@ class CachedModel(_Layers):
     def close(self):
         super().close()
         self.host.free()
+
+
+class SourceModel(_Layers):
+    """The layers of a DeviceModel `dm` in a second context with no expert
+    bound: every expert comes through a wl_expert_source. native=True: the
+    source hands out dm's own slot blocks; native=False: reference-layout
+    blocks of the same synthetic experts (a pool written by wl_synth_expert),
+    which the library converts. with_prefetch / with_async drop the optional
+    callbacks when False. `missing` lists (layer, expert) keys the source has
+    no block for. Every call is logged in self.calls."""
+
+    def __init__(self, dm, native=True, with_prefetch=True, with_async=True, missing=()):
+        super().__init__(dm.c, dm.seed, dm.L, dm._ln_weights, dm._bias_offset, dm._shared_alias, dm.shared_mxfp4)
+        E = self.E
+        self.calls = []
+        self.missing = set(missing)
+        if native:
+            self.blocks = {(l, e): dm.ctx.slot_pool_ptr(l * E + e) for l in range(dm.L) for e in range(E)}
+            self.pool = None
+        else:
+            lay = moe.expert_layout(self.cfg)
+            self.pool = hip.DeviceBuffer(dm.L * E * lay.total)
+            self.blocks = {}
+            for l in range(dm.L):
+                for e in range(E):
+                    p = self.pool.ptr + (l * E + e) * lay.total
+                    kl, ke = dm.expert_source_key(l, e)
+                    moe.synth_expert(self.cfg, dm.seed, kl, ke, p)
+                    self.blocks[(l, e)] = p
+        self._bind_dense()
+
+        def block(layer, expert):
+            return 0 if (layer, expert) in self.missing else self.blocks[(layer, expert)]
+
+        def get(layer, expert):
+            self.calls.append(("get", layer, expert))
+            return block(layer, expert)
+
+        def prefetch(layer, ids, stream):
+            self.calls.append(("prefetch", layer, tuple(ids)))
+
+        def get_async(layer, expert, stream):
+            self.calls.append(("get_async", layer, expert))
+            return block(layer, expert)
+
+        self.ctx.set_expert_source(get, prefetch if with_prefetch else None, get_async if with_async else None,
+                                   native=native)
+        hip.synchronize()
+
+    def close(self):
+        super().close()
+        if self.pool is not None:
+            self.pool.free()
 
 
 def make_io(H):

@@ -54,6 +54,19 @@ class CacheStats(ctypes.Structure):
 HOST_BLOCK_FN = ctypes.CFUNCTYPE(ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint32)
 
 
+# wl_expert_source callbacks (the C form of glm::ExpertSource)
+SRC_GET_FN = ctypes.CFUNCTYPE(ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint32)
+SRC_PREFETCH_FN = ctypes.CFUNCTYPE(None, ctypes.c_void_p, ctypes.c_uint32, ctypes.POINTER(ctypes.c_int32),
+                                   ctypes.c_uint32, ctypes.c_void_p)
+SRC_GET_ASYNC_FN = ctypes.CFUNCTYPE(ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint32,
+                                    ctypes.c_void_p)
+
+
+class ExpertSourceC(ctypes.Structure):
+    _fields_ = [("user", ctypes.c_void_p), ("get", SRC_GET_FN), ("prefetch", SRC_PREFETCH_FN),
+                ("get_async", SRC_GET_ASYNC_FN), ("native", ctypes.c_int32)]
+
+
 class Taps(ctypes.Structure):
     _fields_ = [(n, ctypes.c_void_p) for n in ["norm", "logits", "topk_idx", "topk_w", "mid", "shared"]]
 
@@ -75,6 +88,7 @@ def load():
         "wl_expert_layout_of": [ctypes.POINTER(MoeConfig), u32, ctypes.POINTER(ExpertLayout)],
         "wl_create": [ctypes.POINTER(MoeConfig), ctypes.POINTER(vp)],
         "wl_set_layer": [vp, u32, vp, vp, vp, vp, i32],
+        "wl_set_layer_mxfp4": [vp, u32, vp, vp, vp, vp, vp, vp, vp, vp, vp],
         "wl_slot_bind": [vp, u32, u32, vp],
         "wl_slot_unbind": [vp, u32, u32],
         "wl_slot_pool_create": [vp, u32],
@@ -96,6 +110,7 @@ def load():
         "wl_dequant_matvec_mxfp4": [vp, vp, vp, vp, u32, u32, vp],
         "wl_expert_ffn": [vp, vp, vp, vp, vp, vp],
         "wl_cache_create": [vp, u32, HOST_BLOCK_FN, vp],
+        "wl_set_expert_source": [vp, ctypes.POINTER(ExpertSourceC)],
         "wl_cache_set_speculation": [vp, i32],
         "wl_cache_get_stats": [vp, ctypes.POINTER(CacheStats)],
         "wl_cache_reset_stats": [vp],
@@ -214,6 +229,10 @@ class Context:
         self._ck(self.lib.wl_set_layer(self.h, layer, router_w, bias, ln_w, shared, shared_dtype),
                  "wl_set_layer")
 
+    def set_layer_mxfp4(self, layer, router_w, bias, ln_w, gw, gs, uw, us, dw, ds):
+        self._ck(self.lib.wl_set_layer_mxfp4(self.h, layer, router_w, bias, ln_w, gw, gs, uw, us, dw, ds),
+                 "wl_set_layer_mxfp4")
+
     def slot_bind(self, layer, expert, d_block):
         self._ck(self.lib.wl_slot_bind(self.h, layer, expert, d_block), "wl_slot_bind")
 
@@ -282,6 +301,23 @@ class Context:
 
     def set_taps(self, enable):
         self._ck(self.lib.wl_set_taps(self.h, 1 if enable else 0), "wl_set_taps")
+
+    # ---- expert source ----------------------------------------------------
+    def set_expert_source(self, get, prefetch=None, get_async=None, native=True):
+        """get(layer, expert) -> device address (int, 0 = none); prefetch(layer,
+        ids, stream); get_async(layer, expert, stream) -> device address.
+        None detaches the source when get is None."""
+        if get is None:
+            self._src = None
+            self._ck(self.lib.wl_set_expert_source(self.h, None), "wl_set_expert_source")
+            return
+        g = SRC_GET_FN(lambda user, layer, expert: get(layer, expert) or None)
+        p = SRC_PREFETCH_FN(lambda user, layer, ids, n, stream: prefetch(layer, [ids[i] for i in range(n)], stream)) \
+            if prefetch else ctypes.cast(None, SRC_PREFETCH_FN)
+        a = SRC_GET_ASYNC_FN(lambda user, layer, expert, stream: get_async(layer, expert, stream) or None) \
+            if get_async else ctypes.cast(None, SRC_GET_ASYNC_FN)
+        self._src = ExpertSourceC(None, g, p, a, 1 if native else 0)
+        self._ck(self.lib.wl_set_expert_source(self.h, ctypes.byref(self._src)), "wl_set_expert_source")
 
     # ---- HBM expert cache -------------------------------------------------
     def cache_create(self, capacity, host_block):
