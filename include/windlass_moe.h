@@ -207,8 +207,9 @@ wl_status wl_run_chain(wl_ctx* ctx, uint32_t first_layer, uint32_t n_layers, flo
 /* The layer for n_tokens positions at once (prefill; reference
  * run_moe_batched, src/glm_layer_runner.cuh:818-928). d_hidden [n_tokens][H]
  * f32 pre-norm residual stream; d_out [n_tokens][H] = d_resid + moe(d_hidden)
- * row by row (d_resid may be NULL: moe only; d_out must alias neither; all
- * three 16-byte aligned). Each token is routed exactly as wl_run_moe routes
+ * row by row (d_resid may be NULL: moe only; d_out may be d_hidden and/or
+ * d_resid exactly, the reference's in-place update of b.hidden, but must not
+ * partly overlap them; all three 16-byte aligned). Each token is routed exactly as wl_run_moe routes
  * it (same ids); tokens are then
  * grouped by expert (stable, (token, slot) order) and every selected expert's
  * weights are streamed once per 32 of its tokens; the per-token combine sums

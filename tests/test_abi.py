@@ -1,10 +1,13 @@
 """The C-ABI library: loads, exports every declared symbol, host-only helpers.
 No device compute is called here (CPU suite)."""
 import ctypes
+import os
 
 import pytest
 
 from windlass_amd import moe
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 
 def test_library_exports_every_declared_function():
@@ -37,3 +40,24 @@ def test_invalid_shapes_rejected_without_device():
         assert h.value is None
     # null arguments
     assert lib.wl_dequant_matvec_mxfp4(None, None, None, None, 16, 128, None) == 1
+
+
+def test_reference_caller_compiles_against_the_shim(tmp_path):
+    """include/windlass_glm.hpp keeps the reference's run_moe / run_moe_batched
+    spellings: a caller written against them (tests/shim/reference_caller.cpp,
+    stand-in types with the reference's fields) compiles and links against
+    libwindlass_moe.so unchanged. Nothing is run (no GPU needed)."""
+    import shutil
+    import subprocess
+
+    from windlass_amd import moe
+    gxx = shutil.which("g++")
+    if gxx is None:
+        pytest.skip("no g++")
+    lib_dir = os.path.dirname(moe.LIB_PATH)
+    out = tmp_path / "caller"
+    cmd = [gxx, "-std=c++17", "-Wall", "-Werror", "-I", os.path.join(ROOT, "include"),
+           os.path.join(ROOT, "tests", "shim", "reference_caller.cpp"), "-o", str(out),
+           "-L", lib_dir, "-lwindlass_moe", "-Wl,-rpath," + lib_dir, "-Wl,--allow-shlib-undefined"]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr

@@ -205,7 +205,10 @@ def test_glm_batched_zipf_vs_decode_and_oracle(gpu, T):
 
 def test_misaligned_or_aliasing_buffers_rejected(gpu):
     """The combine reads and writes rows 16 bytes at a time: buffers that are
-    not 16-byte aligned are an argument error (nothing is launched)."""
+    not 16-byte aligned are an argument error (nothing is launched), and so
+    is an output that partly overlaps an input. Exact aliasing (the
+    reference's in-place b.hidden update) runs and gives the out-of-place
+    bits."""
     from windlass_amd.moe import WindlassError
     c = SMALL
     H = c["hidden"]
@@ -214,10 +217,16 @@ def test_misaligned_or_aliasing_buffers_rejected(gpu):
     dh = H_.DeviceBuffer(4 * T * H + 64)
     do = H_.DeviceBuffer(4 * T * H + 64)
     for args in [(dh.ptr, None, do.ptr + 4), (dh.ptr + 8, None, do.ptr), (dh.ptr, dh.ptr + 4, do.ptr),
-                 (dh.ptr, None, dh.ptr)]:
+                 (dh.ptr, None, dh.ptr + 4 * H)]:
         with pytest.raises(WindlassError) as ei:
             dm.ctx.run_moe_batched(0, T, *args)
         assert ei.value.status == 1, args  # WL_ERR_INVALID
-    dm.ctx.run_moe_batched(0, T, dh.ptr, None, do.ptr)  # aligned: runs
+    hs = _tokens(H, T, 450)
+    dh.upload(hs)
+    dm.ctx.run_moe_batched(0, T, dh.ptr, dh.ptr, do.ptr)  # aligned, out of place: runs
     dm.ctx.check_error()
+    ref = do.download(np.float32, T * H)
+    dm.ctx.run_moe_batched(0, T, dh.ptr, dh.ptr, dh.ptr)  # in place: hidden += moe(hidden)
+    dm.ctx.check_error()
+    assert np.array_equal(dh.download(np.float32, T * H).view(np.uint32), ref.view(np.uint32))
     dm.close()

@@ -840,8 +840,18 @@ static wl_status batched_check(wl_ctx* c, uint32_t layer, uint32_t n_tokens, con
     if (layer >= c->cfg.n_layers) return fail(c, WL_ERR_INVALID, "layer %u >= n_layers %u", layer, c->cfg.n_layers);
     if (!c->layers[layer].set) return fail(c, WL_ERR_STATE, "layer %u has no weights (wl_set_layer)", layer);
     if (n_tokens == 0 || n_tokens > 65535) return fail(c, WL_ERR_INVALID, "n_tokens=%u must be in [1,65535]", n_tokens);
-    if (!d_hidden || !d_out || d_out == d_hidden || (d_resid && d_out == d_resid))
-        return fail(c, WL_ERR_INVALID, "null or aliasing batched buffers");
+    if (!d_hidden || !d_out) return fail(c, WL_ERR_INVALID, "null batched buffers");
+    // d_out may be d_hidden and/or d_resid exactly (the reference adds the
+    // block output into b.hidden in place, src/glm_layer_runner.cuh:918-920):
+    // every chunk's rows are read before its combine writes them, each by the
+    // thread that writes them. Partial overlaps are rejected.
+    const size_t bytes = (size_t)n_tokens * c->cfg.hidden * 4;
+    auto overlap = [&](const void* a, const void* b) {
+        const char *x = (const char*)a, *y = (const char*)b;
+        return a && b && a != b && x < y + bytes && y < x + bytes;
+    };
+    if (overlap(d_out, d_hidden) || overlap(d_out, d_resid))
+        return fail(c, WL_ERR_INVALID, "d_out partly overlaps an input (only exact aliasing is allowed)");
     if (((uintptr_t)d_hidden | (uintptr_t)d_out | (uintptr_t)d_resid) % 16u)
         return fail(c, WL_ERR_INVALID, "batched buffers must be 16-byte aligned");
     const uint32_t E = c->cfg.n_routed_experts;
