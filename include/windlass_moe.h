@@ -311,6 +311,23 @@ wl_status wl_set_taps(wl_ctx* ctx, int32_t enable);
  * are counted in spec_* only. */
 typedef const uint8_t* (*wl_host_block_fn)(void* user, uint32_t layer, uint32_t expert);
 wl_status wl_cache_create(wl_ctx* ctx, uint32_t capacity, wl_host_block_fn host_block, void* user);
+/* The reference's file tier (ExpertCache::init, src/glm_expert_cache.cuh:
+ * 139-183): the same cache, its misses read from the packed expert files
+ * `dir`/layer_N.bin, N = first_layer + context layer (256 records of
+ * wl_expert_layout.total bytes in the reference layout, record e at offset
+ * e x total; tools/repack_experts_glm.py:5-14,46-55). A pool of io_threads
+ * workers pread each miss into one of its two pinned buffers, copies it to the
+ * device on its own non-blocking stream (after the gate event of the resolve
+ * that took the slot, so no kernel enqueued before still reads it) and
+ * converts it there into the slot's native layout; wl_cache_get (and the
+ * layer run) waits until the read is issued and orders the stream after it.
+ * io_threads = 0 reads on the calling thread. Every file must exist and hold
+ * all n_routed_experts records (WL_ERR_IO otherwise); a short read fails the
+ * call that needs the block with WL_ERR_IO. Each worker (one for
+ * io_threads = 0) holds two reference blocks of pinned memory and two of
+ * device staging. */
+wl_status wl_cache_create_files(wl_ctx* ctx, uint32_t capacity, const char* dir, uint32_t first_layer,
+                                uint32_t io_threads);
 wl_status wl_cache_set_speculation(wl_ctx* ctx, int32_t enable);
 
 typedef struct wl_cache_stats {

@@ -332,6 +332,9 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const float* hidden, const 
                     }
                 }
                 if (block_all(mine, misc)) break;
+                // every lane of a wave sees the same abort word (one load);
+                // a wave that leaves early drops out of the later barriers,
+                // and the others leave at their next spin
                 if (spins > (1u << 20) || aborted(a.sync, SM, d.epoch)) {
                     if (tid == 0 && spins > (1u << 20)) raise_error(a.sync, SM, E_SPIN, d.epoch);
                     return false;

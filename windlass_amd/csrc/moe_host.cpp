@@ -17,6 +17,7 @@
 #include <vector>
 
 #include "../../include/windlass_moe.h"
+#include "expert_files.h"
 #include "internal.h"
 #include "lru.h"
 
@@ -43,12 +44,19 @@ struct CacheState {
     std::vector<uint8_t> has_ev;      // slot_ev recorded at least once
     std::vector<uint8_t> spec;        // filled by a speculative copy, not yet requested
     hipEvent_t gate = nullptr;        // compute-stream point that copies into reused slots wait for
+    hipEvent_t cur_gate = nullptr;    // the gate recorded by the last real resolve (gate, or a ring entry)
     bool gate_recorded = false;
     bool speculate = false;
     bool spec_pending = false;
     uint32_t spec_layer = 0;
     uint64_t spec_requests = 0, spec_copies = 0, spec_hits = 0, bytes_h2d = 0;
     std::vector<std::pair<uint32_t, uint8_t*>> resolved;  // last wl_cache_prefetch: key -> block
+    // packed-file backing (wl_cache_create_files): the reads run on its
+    // workers; task_of[slot] is the slot's read not yet waited for
+    std::unique_ptr<wl::FileTier> files;
+    std::vector<wl::FileTask*> task_of;
+    hipEvent_t gates[4] = {nullptr, nullptr, nullptr, nullptr};  // per-resolve gates of file reads (a ring)
+    uint32_t gate_i = 0;
 };
 
 // Scratch of the batched layer: one allocation sized for `cap` tokens
@@ -351,11 +359,17 @@ wl_status wl_create(const wl_moe_config* cfg, wl_ctx** out) {
 
 void wl_destroy(wl_ctx* c) {
     if (!c) return;
+    // the file tier's workers first: a read still queued records the slot's
+    // event and writes into the pool, so they are joined (and their streams
+    // drained) before any event, stream or buffer goes
+    c->cache.files.reset();
     if (c->uc_block || c->cache.lru) (void)hipDeviceSynchronize();
     {
         CacheState& C = c->cache;
         for (hipEvent_t e : C.slot_ev) (void)hipEventDestroy(e);
         if (C.gate) (void)hipEventDestroy(C.gate);
+        for (hipEvent_t e : C.gates)
+            if (e) (void)hipEventDestroy(e);
         for (hipStream_t st : C.copy)
             if (st) (void)hipStreamDestroy(st);
         delete C.lru;
@@ -499,7 +513,13 @@ static wl_status cache_resolve(wl_ctx* c, uint32_t layer, const int32_t* ids, ui
     const size_t nb = c->native_bytes;
     hipError_t e;
     if (!speculative) {
-        if ((e = hipEventRecord(C.gate, s)) != hipSuccess) return hip_fail(c, e, "cache gate");
+        hipEvent_t g = C.gate;
+        if (C.files) {  // file reads wait on a ring of gates (a read issued late waits for its own resolve)
+            C.gate_i = (C.gate_i + 1) % 4u;
+            g = C.gates[C.gate_i];
+        }
+        if ((e = hipEventRecord(g, s)) != hipSuccess) return hip_fail(c, e, "cache gate");
+        C.cur_gate = g;
         C.gate_recorded = true;
     }
     for (uint32_t k = 0; k < n; k++) {
@@ -525,6 +545,39 @@ static wl_status cache_resolve(wl_ctx* c, uint32_t layer, const int32_t* ids, ui
                 C.spec_hits++;
                 C.spec[r.slot] = 0;
             }
+        } else if (C.files) {
+            // a read still pending on this slot (its key was evicted before it
+            // was waited for) lands first
+            if (wl::FileTask* old = C.task_of[r.slot]) {
+                const bool ok = C.files->wait_issued(old);
+                C.files->release(old);
+                C.task_of[r.slot] = nullptr;
+                if (!ok) {
+                    C.lru->forget(key);
+                    return fail(c, WL_ERR_IO, "an earlier read into slot %u failed", r.slot);
+                }
+            }
+            wl::FileTask* t = C.files->submit(layer, (uint32_t)ids[k], dst, C.gate_recorded ? C.cur_gate : nullptr,
+                                              C.slot_ev[r.slot]);
+            if (!t) {  // every task in flight: release the issued ones and retry once
+                for (wl::FileTask*& q : C.task_of)
+                    if (q && q->issued.load()) {
+                        C.files->wait_issued(q);
+                        C.files->release(q);
+                        q = nullptr;
+                    }
+                t = C.files->submit(layer, (uint32_t)ids[k], dst, C.gate_recorded ? C.cur_gate : nullptr,
+                                    C.slot_ev[r.slot]);
+            }
+            if (!t) {
+                C.lru->forget(key);
+                return fail(c, WL_ERR_STATE, "file read queue full");
+            }
+            C.task_of[r.slot] = t;
+            C.has_ev[r.slot] = 1;
+            C.spec[r.slot] = speculative ? 1 : 0;
+            C.bytes_h2d += C.files->ref_bytes();
+            if (speculative) C.spec_copies++;
         } else {
             const uint8_t* src = C.fn(C.user, layer, (uint32_t)ids[k]);
             if (!src) {
@@ -532,7 +585,7 @@ static wl_status cache_resolve(wl_ctx* c, uint32_t layer, const int32_t* ids, ui
                 return fail(c, WL_ERR_IO, "no host block for layer %u expert %d", layer, ids[k]);
             }
             hipStream_t cs = C.copy[C.next_copy++ & 1u];
-            if (C.gate_recorded && (e = hipStreamWaitEvent(cs, C.gate, 0)) != hipSuccess) return hip_fail(c, e, "copy gate");
+            if (C.gate_recorded && (e = hipStreamWaitEvent(cs, C.cur_gate, 0)) != hipSuccess) return hip_fail(c, e, "copy gate");
             if (C.has_ev[r.slot] && (e = hipStreamWaitEvent(cs, C.slot_ev[r.slot], 0)) != hipSuccess)
                 return hip_fail(c, e, "slot order");
             if ((e = hipMemcpyAsync(dst, src, nb, hipMemcpyHostToDevice, cs)) != hipSuccess)
@@ -543,7 +596,8 @@ static wl_status cache_resolve(wl_ctx* c, uint32_t layer, const int32_t* ids, ui
             C.bytes_h2d += nb;
             if (speculative) C.spec_copies++;
         }
-        if (!speculative && C.has_ev[r.slot] && (e = hipStreamWaitEvent(s, C.slot_ev[r.slot], 0)) != hipSuccess)
+        // (file reads: the stream waits in wl_cache_get, once the read is issued)
+        if (!speculative && !C.files && C.has_ev[r.slot] && (e = hipStreamWaitEvent(s, C.slot_ev[r.slot], 0)) != hipSuccess)
             return hip_fail(c, e, "wait for expert copy");
         if (ptrs) ptrs[k] = dst;
     }
@@ -1054,12 +1108,12 @@ wl_status wl_set_expert_source(wl_ctx* c, const wl_expert_source* src) {
     return WL_OK;
 }
 
-wl_status wl_cache_create(wl_ctx* c, uint32_t capacity, wl_host_block_fn host_block, void* user) {
-    if (!c) return WL_ERR_INVALID;
+// The slot pool, LRU, side streams and events of a cache, and the cache as
+// the context's expert source.
+static wl_status cache_init(wl_ctx* c, uint32_t capacity) {
     CacheState& C = c->cache;
     if (C.lru) return fail(c, WL_ERR_STATE, "the context already has a cache");
     if (c->src.get) return fail(c, WL_ERR_STATE, "the context already has an expert source");
-    if (!host_block) return fail(c, WL_ERR_INVALID, "host_block is null");
     if (capacity < 2u * c->cfg.n_experts_per_tok)
         return fail(c, WL_ERR_INVALID, "capacity %u < 2 x n_experts_per_tok", capacity);
     void* p = nullptr;
@@ -1069,8 +1123,6 @@ wl_status wl_cache_create(wl_ctx* c, uint32_t capacity, wl_host_block_fn host_bl
     c->allocs.push_back(p);
     C.pool = (uint8_t*)p;
     C.capacity = capacity;
-    C.fn = host_block;
-    C.user = user;
     wl_status ps = ensure_pin(c);
     if (ps != WL_OK) return ps;
     for (hipStream_t& st : C.copy)
@@ -1081,9 +1133,41 @@ wl_status wl_cache_create(wl_ctx* c, uint32_t capacity, wl_host_block_fn host_bl
         if ((e = hipEventCreateWithFlags(&ev, hipEventDisableTiming)) != hipSuccess) return hip_fail(c, e, "slot event");
     C.has_ev.assign(capacity, 0);
     C.spec.assign(capacity, 0);
+    C.task_of.assign(capacity, nullptr);
     C.lru = new wl::SlotLru(capacity);
     c->src = wl_expert_source{c, cache_src_get, cache_src_prefetch, cache_src_get_async, 1};
     c->src_cache = true;
+    return WL_OK;
+}
+
+wl_status wl_cache_create(wl_ctx* c, uint32_t capacity, wl_host_block_fn host_block, void* user) {
+    if (!c) return WL_ERR_INVALID;
+    if (!host_block) return fail(c, WL_ERR_INVALID, "host_block is null");
+    wl_status s = cache_init(c, capacity);
+    if (s != WL_OK) return s;
+    c->cache.fn = host_block;
+    c->cache.user = user;
+    return WL_OK;
+}
+
+wl_status wl_cache_create_files(wl_ctx* c, uint32_t capacity, const char* dir, uint32_t first_layer,
+                                uint32_t io_threads) {
+    if (!c) return WL_ERR_INVALID;
+    if (!dir) return fail(c, WL_ERR_INVALID, "dir is null");
+    if (io_threads > 64) return fail(c, WL_ERR_INVALID, "io_threads %u > 64", io_threads);
+    if (c->cache.lru) return fail(c, WL_ERR_STATE, "the context already has a cache");
+    std::unique_ptr<wl::FileTier> files(new wl::FileTier());
+    const std::string err = files->open(dir, first_layer, c->cfg.n_layers, c->cfg.n_routed_experts, c->lay.total,
+                                        c->native_bytes, c->cfg.hidden, c->cfg.moe_inter, io_threads, c->device);
+    if (!err.empty()) return fail(c, WL_ERR_IO, "%s", err.c_str());
+    wl_status s = cache_init(c, capacity);
+    if (s != WL_OK) return s;
+    CacheState& C = c->cache;
+    for (hipEvent_t& ev : C.gates) {
+        const hipError_t e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+        if (e != hipSuccess) return hip_fail(c, e, "gate event");
+    }
+    C.files = std::move(files);
     return WL_OK;
 }
 
@@ -1140,16 +1224,28 @@ wl_status wl_cache_get(wl_ctx* c, uint32_t layer, uint32_t expert, void* stream,
     if (layer >= c->cfg.n_layers || expert >= c->cfg.n_routed_experts)
         return fail(c, WL_ERR_INVALID, "(%u,%u) out of range", layer, expert);
     const uint32_t key = layer * c->cfg.n_routed_experts + expert;
-    for (const auto& r : C.resolved)
-        if (r.first == key) {
-            *d_block = r.second;  // the prefetch already ordered the stream after its copy
-            return WL_OK;
-        }
-    const int32_t id = (int32_t)expert;
     uint8_t* p = nullptr;
-    wl_status s = cache_resolve(c, layer, &id, 1, (hipStream_t)stream, false, &p);
-    if (s == WL_OK) *d_block = p;
-    return s;
+    for (const auto& r : C.resolved)
+        if (r.first == key) p = r.second;  // the prefetch ordered the stream after a host copy
+    if (!p) {
+        const int32_t id = (int32_t)expert;
+        wl_status s = cache_resolve(c, layer, &id, 1, (hipStream_t)stream, false, &p);
+        if (s != WL_OK) return s;
+    }
+    if (C.files) {  // the slot's read: wait until its worker has issued it, then order the stream after it
+        const uint32_t slot = (uint32_t)((p - C.pool) / c->native_bytes);
+        if (wl::FileTask* t = C.task_of[slot]) {
+            const bool ok = C.files->wait_issued(t);
+            C.files->release(t);
+            C.task_of[slot] = nullptr;
+            if (!ok) return fail(c, WL_ERR_IO, "read of layer %u expert %u failed", layer, expert);
+        }
+        hipError_t e;
+        if (C.has_ev[slot] && (e = hipStreamWaitEvent((hipStream_t)stream, C.slot_ev[slot], 0)) != hipSuccess)
+            return hip_fail(c, e, "wait for expert read");
+    }
+    *d_block = p;
+    return WL_OK;
 }
 
 wl_status wl_lru_replay(uint32_t capacity, const uint32_t* keys, uint32_t n_keys, uint32_t batch, uint8_t* hit_out,

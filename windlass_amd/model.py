@@ -193,5 +193,19 @@ class SourceModel(_Layers):
             self.pool.free()
 
 
+class FileModel(_Layers):
+    """The layers with their experts behind the HBM cache over packed expert
+    files: directory/layer_{first_layer + l}.bin holds E reference-layout
+    records, record e being the synthetic expert (l, e) (the caller writes
+    the files)."""
+
+    def __init__(self, cfg, seed, n_layers, capacity, directory, first_layer=0, io_threads=4, ln_weights=None,
+                 bias_offset=None, shared_alias=False, shared_mxfp4=False):
+        super().__init__(cfg, seed, n_layers, ln_weights, bias_offset, shared_alias, shared_mxfp4)
+        self.ctx.cache_create_files(capacity, directory, first_layer, io_threads)
+        self._bind_dense()
+        hip.synchronize()
+
+
 def make_io(H):
     return hip.DeviceBuffer(4 * H), hip.DeviceBuffer(4 * H)
