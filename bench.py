@@ -194,6 +194,12 @@ def main():
     ap.add_argument("--host-blocks", type=int, default=512)
     ap.add_argument("--spec", action="store_true",
                     help="cache workload: cross-layer speculative prefetch (layer l+1's router on layer l's input)")
+    ap.add_argument("--policies", default="lru",
+                    help="cache workload: comma-separated replacement/admission policies (lru, lfu, slru, 2q, "
+                         "tinylfu), each measured on a flushed cache in turn; the first is the line's value")
+    ap.add_argument("--pin-top", type=int, default=0,
+                    help="cache workload: pin the N keys requested most often by a profile pass over the warm-up "
+                         "tokens (popularity pinning)")
     ap.add_argument("--zipf-amp", type=float, default=0.25,
                     help="cache workload: bias offset of the most popular expert (rank r gets amp * r^-1.1)")
     ap.add_argument("--seed", type=int, default=1)
@@ -274,22 +280,50 @@ def main():
         l = i % args.layers
         dm.ctx.run_moe(l, d_hs.ptr + 4 * H * (i % n_h), d_out.ptr + 4 * H * l, stream.handle)
 
-    for i in range(args.warmup):
-        step(i)
-    dm.ctx.check_error(stream.handle)
-    hip.synchronize()
-    if cache:
-        dm.ctx.cache_reset_stats()
-    e0, e1 = hip.Event(), hip.Event()
-    e0.record(stream)
-    for i in range(args.steps):
-        step(args.warmup + i)
-    e1.record(stream)
-    e1.synchronize()
-    ms = e0.elapsed_ms(e1)
-    dm.ctx.check_error(stream.handle)
-    cstats = dm.ctx.cache_stats() if cache else None
+    def measure():
+        for i in range(args.warmup):
+            step(i)
+        dm.ctx.check_error(stream.handle)
+        hip.synchronize()
+        if cache:
+            dm.ctx.cache_reset_stats()
+        e0, e1 = hip.Event(), hip.Event()
+        e0.record(stream)
+        for i in range(args.steps):
+            step(args.warmup + i)
+        e1.record(stream)
+        e1.synchronize()
+        ms_ = e0.elapsed_ms(e1)
+        dm.ctx.check_error(stream.handle)
+        return ms_, (dm.ctx.cache_stats() if cache else None)
+
     layers_per_step = args.layers if chain else 1
+    policies = [p.strip() for p in args.policies.split(",") if p.strip()] if cache else ["-"]
+    pinned = []
+    if cache and args.pin_top > 0:
+        # profile pass: the warm-up tokens layer by layer, the routed keys read back
+        from collections import Counter
+        E_, K_ = c["n_routed_experts"], c["n_experts_per_tok"]
+        cnt = Counter()
+        for i in range(args.warmup):
+            hip.copy_d2d(d_h.ptr, d_hs.ptr + 4 * H * (i % n_h), 4 * H, stream.handle)
+            cur, nxt = d_h, d_tmp
+            for l in range(args.layers):
+                dm.ctx.run_moe_residual(l, cur.ptr, cur.ptr, nxt.ptr, stream.handle)
+                stream.synchronize()
+                for e in hip.download_ptr(dm.ctx.taps()["topk_idx"], np.int32, K_):
+                    cnt[l * E_ + int(e)] += 1
+                cur, nxt = nxt, cur
+        pinned = [k for k, _ in cnt.most_common(args.pin_top)]
+        for k in pinned:
+            dm.ctx.cache_pin(k // E_, k % E_)
+    per_policy = {}
+    for pol in policies:
+        if cache:
+            dm.ctx.cache_set_policy(pol)
+        ms_p, st_p = measure()
+        per_policy[pol] = (ms_p, st_p)
+    ms, cstats = per_policy[policies[0]]
     us_per_layer = ms * 1e3 / args.steps / layers_per_step
 
     if args.calib_copy_mb > 0:
@@ -378,7 +412,13 @@ def main():
                       "spec_copies": cstats["spec_copies"], "spec_hits": cstats["spec_hits"],
                       "h2d_GB": round(cstats["bytes_h2d"] / 1e9, 3),
                       "h2d_GBps": round(cstats["bytes_h2d"] / (ms * 1e-3) / 1e9, 2),
-                      "host_blocks": args.host_blocks, "slots": args.cache_slots,
+                      "host_blocks": args.host_blocks, "slots": args.cache_slots, "policy": policies[0],
+                      "bypassed": cstats["bypassed"], "pinned": len(pinned),
+                      "policies": {pol: {"hit_rate": round(st["hits"] / max(1, st["hits"] + st["misses"]), 4),
+                                         "us_per_layer": round(m * 1e3 / args.steps / layers_per_step, 1),
+                                         "tokens_per_s": round(1e6 / (m * 1e3 / args.steps), 3),
+                                         "bypassed": st["bypassed"], "h2d_GB": round(st["bytes_h2d"] / 1e9, 3)}
+                                   for pol, (m, st) in per_policy.items()},
                       "zipf": {"s": 1.1, "amplitude": args.zipf_amp}}} if cache else {}),
         "build_s": round(build_s, 1),
     }

@@ -337,6 +337,7 @@ typedef struct wl_cache_stats {
     uint64_t spec_hits;                /* real requests served by a speculative copy */
     uint64_t bytes_h2d;                /* bytes copied host -> device */
     uint32_t used, capacity;           /* occupied / total slots */
+    uint64_t bypassed;                 /* misses served from a transient slot, not retained */
 } wl_cache_stats;
 wl_status wl_cache_get_stats(wl_ctx* ctx, wl_cache_stats* out);
 wl_status wl_cache_reset_stats(wl_ctx* ctx);
@@ -348,6 +349,48 @@ wl_status wl_cache_reset_stats(wl_ctx* ctx);
  * expert that was not resolved resolves it alone. */
 wl_status wl_cache_prefetch(wl_ctx* ctx, uint32_t layer, const int32_t* experts, uint32_t n, void* stream);
 wl_status wl_cache_get(wl_ctx* ctx, uint32_t layer, uint32_t expert, void* stream, uint8_t** d_block);
+
+/* Replacement and admission policy of the cache (no reference counterpart
+ * except WL_POLICY_LRU, the reference's ExpertCache semantics and the
+ * default):
+ *   WL_POLICY_LFU      evict the key requested least often so far (ties: the
+ *                      least recent)
+ *   WL_POLICY_SLRU     segmented LRU: a miss enters a probationary segment, a
+ *                      hit there promotes the key to a protected segment of
+ *                      protected_frac x capacity slots (its least recent key
+ *                      demoted back); victims come from the probationary end
+ *   WL_POLICY_2Q       admission on a second miss: a key missing for the first
+ *                      time (not among the last `ghost` first misses; 0 =
+ *                      capacity) is served but not retained
+ *   WL_POLICY_TINYLFU  frequency admission: a missing key is retained only if
+ *                      it has been requested more often than its victim
+ * Victims are never keys of the request batch being resolved, nor pinned
+ * keys. A miss that is not retained is copied into one of 2 x
+ * n_experts_per_tok transient slots beyond `capacity` (allocated with the
+ * cache) and counted in wl_cache_stats.bypassed. */
+#define WL_POLICY_LRU     0
+#define WL_POLICY_LFU     1
+#define WL_POLICY_SLRU    2
+#define WL_POLICY_2Q      3
+#define WL_POLICY_TINYLFU 4
+typedef struct wl_cache_policy {
+    int32_t  kind;            /* WL_POLICY_* */
+    float    protected_frac;  /* SLRU: share of the slots in the protected segment (0.5) */
+    uint32_t ghost;           /* 2Q: first misses remembered (0 = capacity) */
+} wl_cache_policy;
+/* Empties the cache (every slot free, counters zero) and sets its policy;
+ * synchronises the device and waits for pending reads. */
+wl_status wl_cache_set_policy(wl_ctx* ctx, const wl_cache_policy* policy);
+/* Pins (pinned != 0) or unpins the key (layer, expert): a pinned key is always
+ * admitted and never evicted (popularity pinning: pin the most requested keys of a profile). At
+ * most capacity - 2 x n_experts_per_tok keys may be pinned. */
+wl_status wl_cache_pin(wl_ctx* ctx, uint32_t layer, uint32_t expert, int32_t pinned);
+/* Test hook (no device use): wl_lru_replay under `policy`, with `n_pinned`
+ * pinned keys; hit_out[i] is 1 for a hit, 0 for a retained miss, 3 for a miss
+ * not retained, 2 for a skipped duplicate. */
+wl_status wl_policy_replay(const wl_cache_policy* policy, uint32_t capacity, const uint32_t* keys, uint32_t n_keys,
+                           uint32_t batch, const uint32_t* pinned, uint32_t n_pinned, uint8_t* hit_out,
+                           uint64_t* hits, uint64_t* misses, uint64_t* evictions);
 
 /* Test hook (no device use): replays `n_keys` requests through the cache's
  * LRU bookkeeping with `capacity` slots, in batches of `batch` keys (keys

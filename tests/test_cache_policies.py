@@ -1,0 +1,95 @@
+"""The cache's replacement and admission policies (CPU): the library's engine
+(wl_policy_replay, windlass_amd/csrc/lru.h) against the oracle's independent
+restatement (oracle/policies.py) request by request on Zipf-skewed batched
+key streams, with and without pinned keys, plus small sequences whose
+outcome is worked out by hand for each policy."""
+import numpy as np
+import pytest
+
+from oracle import lru as OL
+from oracle import policies as OP
+from windlass_amd import moe
+
+
+def zipf_batches(n_batches, batch, n_keys, s, seed):
+    rng = np.random.default_rng(seed)
+    p = 1.0 / np.arange(1, n_keys + 1) ** s
+    p /= p.sum()
+    perm = rng.permutation(n_keys)
+    keys = []
+    for _ in range(n_batches):
+        keys += [int(perm[i]) for i in rng.choice(n_keys, size=batch, replace=False, p=p)]
+    return keys
+
+
+@pytest.mark.parametrize("kind", ["lru", "lfu", "slru", "2q", "tinylfu"])
+@pytest.mark.parametrize("seed", [0, 1])
+def test_engine_matches_oracle(kind, seed):
+    keys = zipf_batches(400, 8, 300, 1.1, seed)
+    for cap, ghost, frac in [(40, 0, 0.5), (64, 100, 0.3), (16, 0, 0.8)]:
+        got = moe.policy_replay(moe.make_policy(kind, frac, ghost), cap, keys, 8)
+        want = OP.replay(kind, cap, keys, 8, frac, ghost)
+        assert list(got[0]) == want[0], (kind, cap)
+        assert got[1:] == want[1:], (kind, cap, got[1:], want[1:])
+
+
+@pytest.mark.parametrize("kind", ["lru", "lfu", "slru", "2q", "tinylfu"])
+def test_engine_matches_oracle_with_pins(kind):
+    keys = zipf_batches(300, 8, 200, 1.1, 7)
+    pinned = [keys[3], keys[17], keys[40], 199]
+    got = moe.policy_replay(kind, 32, keys, 8, pinned=pinned)
+    want = OP.replay(kind, 32, keys, 8, pinned=pinned)
+    assert list(got[0]) == want[0] and got[1:] == want[1:]
+    # a pinned key, once in, is never a miss again
+    for pk in pinned:
+        idx = [i for i, k in enumerate(keys) if k == pk]
+        if idx:
+            assert all(got[0][i] in (1, 2) for i in idx[1:]), pk
+
+
+def test_lru_policy_is_the_reference_lru():
+    keys = zipf_batches(300, 8, 120, 1.1, 3)
+    assert moe.policy_replay("lru", 24, keys, 8)[1:] == OL.replay(24, keys, 8)[1:]
+    assert moe.lru_replay(24, keys, 8)[1:] == OL.replay(24, keys, 8)[1:]
+
+
+# Hand-worked sequences, batches of one key, capacity 2 (the state after each
+# request written out, most recent first).
+SEQ = [1, 2, 1, 3, 1, 3, 2]
+
+
+def test_hand_lru():
+    # [1] [2 1] [1 2]h [3 1]e2 [1 3]h [3 1]h [2 3]e1
+    out, h, m, e = moe.policy_replay("lru", 2, SEQ, 1)
+    assert list(out) == [0, 0, 1, 0, 1, 1, 0] and (h, m, e) == (3, 4, 2)
+
+
+def test_hand_lfu():
+    # counts: 1:1 [1]; 2:1 [2 1]; 1:2 h; 3: victim = least count among {1:2, 2:1} -> 2, [3 1];
+    # 1:3 h; 3:2 h; 2: victim least count {1:3, 3:2} -> 3, [2 1]
+    out, h, m, e = moe.policy_replay("lfu", 2, SEQ, 1)
+    assert list(out) == [0, 0, 1, 0, 1, 1, 0] and (h, m, e) == (3, 4, 2)
+
+
+def test_hand_2q():
+    # 1, 2 fill the free slots; 1 hit; 3 first miss: ghost {3}, not retained;
+    # 1 hit; 3 second miss: retained, evicts LRU 2 (cache [3 1]); 2 first miss
+    # after its eviction: ghost {2}, not retained
+    out, h, m, e = moe.policy_replay("2q", 2, SEQ, 1)
+    assert list(out) == [0, 0, 1, 3, 1, 0, 3] and (h, m, e) == (2, 5, 1)
+
+
+def test_hand_tinylfu():
+    # 3 (count 1) vs victim 2 (count 1): not retained; 1 hit (count 3); 3 (count 2)
+    # vs victim 2 (count 1): retained, evicts 2; 2 (count 2) vs victim 1 (count 3): not retained
+    out, h, m, e = moe.policy_replay("tinylfu", 2, SEQ, 1)
+    assert list(out) == [0, 0, 1, 3, 1, 0, 3] and (h, m, e) == (2, 5, 1)
+
+
+def test_hand_slru():
+    # capacity 2, protected 1: 1 -> prob[1]; 2 -> prob[2 1]; 1 hit -> prot[1] prob[2];
+    # 3 miss: victim prob's oldest 2 -> prob[3]; 1 hit in prot; 3 hit in prob ->
+    # prot[3], 1 demoted to prob[1]; 2 miss: victim prob's oldest 1 -> prob[2]
+    out, h, m, e = moe.policy_replay("slru", 2, SEQ, 1)
+    assert list(out) == [0, 0, 1, 0, 1, 1, 0] and (h, m, e) == (3, 4, 2)
+    assert OP.replay("slru", 2, SEQ, 1)[1:] == (3, 4, 2)

@@ -149,3 +149,51 @@ def test_glm_shape_cached_equals_resident(gpu):
     print(f"GLM cache: {cm.ctx.cache_stats()}", flush=True)
     cm.close()
     rm.close()
+
+
+@pytest.mark.parametrize("kind", ["lfu", "slru", "2q", "tinylfu"])
+def test_policy_cached_equals_resident(gpu, kind):
+    """Every policy (and pinned keys) keeps the layer's bits: cached outputs
+    equal the resident layer's (decode and batched), and the decode part's
+    counters equal the oracle's replay of the requested ids under that policy
+    (oracle/policies.py), misses not retained included."""
+    from oracle import policies as OP
+    hip = gpu
+    c = SMALL
+    H, E, K, L, cap = c["hidden"], c["n_routed_experts"], c["n_experts_per_tok"], 4, 16
+    cm, rm = _pair(c, 9, L, capacity=cap, n_host=120)
+    cm.ctx.cache_set_policy(kind)
+    pins = [0 * E + 3, 2 * E + 11]
+    for k in pins:
+        cm.ctx.cache_pin(k // E, k % E)
+    keys = []
+    for t in range(6):
+        h = synth.hidden_state(H, 980 + t)
+        for l in range(L):
+            outs = []
+            for m in (cm, rm):
+                dh, dout = make_io(H)
+                dh.upload(h)
+                m.ctx.run_moe_residual(l, dh.ptr, dh.ptr, dout.ptr)
+                m.ctx.check_error()
+                outs.append(dout.download(np.float32))
+            keys += [l * E + int(i) for i in hip.download_ptr(cm.ctx.taps()["topk_idx"], np.int32, K)]
+            assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32)), (kind, t, l)
+            h = outs[0]
+    st = cm.ctx.cache_stats()
+    out, hits, misses, ev = OP.replay(kind, cap, keys, K, pinned=pins)
+    print(f"{kind}: {st}", flush=True)
+    assert (st["hits"], st["misses"], st["evictions"]) == (hits, misses, ev)
+    assert st["bypassed"] == sum(1 for x in out if x == 3)
+    T = 30  # the batched layer through the same cache
+    hs = np.stack([synth.hidden_state(H, 990, i) for i in range(T)]).astype(np.float32)
+    bo = []
+    for m in (cm, rm):
+        dh = hip.DeviceBuffer.from_array(hs)
+        do = hip.DeviceBuffer(4 * T * H)
+        m.ctx.run_moe_batched(1, T, dh.ptr, None, do.ptr)
+        m.ctx.check_error()
+        bo.append(do.download(np.float32))
+    assert np.array_equal(bo[0].view(np.uint32), bo[1].view(np.uint32)), kind
+    cm.close()
+    rm.close()

@@ -34,6 +34,10 @@ struct LayerState {
 // HBM expert cache (config 4): LRU slot pool filled from pinned host blocks.
 struct CacheState {
     wl::SlotLru* lru = nullptr;
+    wl_cache_policy policy{WL_POLICY_LRU, 0.5f, 0u};
+    uint32_t transient = 0;          // slots [capacity, capacity + transient): misses not retained
+    std::vector<uint32_t> pinned;    // pinned keys (kept across wl_cache_set_policy)
+    uint64_t bypassed = 0;           // misses served from a transient slot
     uint8_t* pool = nullptr;
     uint32_t capacity = 0;
     wl_host_block_fn fn = nullptr;
@@ -522,6 +526,7 @@ static wl_status cache_resolve(wl_ctx* c, uint32_t layer, const int32_t* ids, ui
         C.cur_gate = g;
         C.gate_recorded = true;
     }
+    C.lru->begin_batch();  // no key of this batch is evicted by another of it
     for (uint32_t k = 0; k < n; k++) {
         if (ids[k] < 0 || (uint32_t)ids[k] >= E)
             return fail(c, WL_ERR_INVALID, "expert id %d of layer %u out of range", ids[k], layer);
@@ -535,6 +540,11 @@ static wl_status cache_resolve(wl_ctx* c, uint32_t layer, const int32_t* ids, ui
         const uint32_t key = layer * E + (uint32_t)ids[k];
         const wl::SlotLru::Result r = C.lru->request(key, !speculative);
         uint8_t* dst = C.pool + (size_t)r.slot * nb;
+        if (r.transient) {
+            if (speculative) continue;  // a prediction the policy would not retain: nothing to fetch early
+            if (!C.transient) return fail(c, WL_ERR_STATE, "no transient slot for a miss that is not retained");
+            C.bypassed++;
+        }
         if (r.evicted) {  // a block wl_cache_get could still hand out is gone
             auto& R = C.resolved;
             R.erase(std::remove_if(R.begin(), R.end(), [&](const auto& x) { return x.first == r.evicted_key; }), R.end());
@@ -943,7 +953,9 @@ static wl_status batched_source_gemms(wl_ctx* c, uint32_t layer, wl::BatchArgs b
     for (uint32_t x = 0; x < E; x++)
         if (counts[x]) uniq.push_back((int32_t)x);
     uint32_t ech = 32;
-    if (c->src_cache) ech = std::min(ech, c->cache.capacity / 2u);
+    // the cache: a chunk's misses that are not retained each need a distinct
+    // transient slot while the chunk's GEMMs run
+    if (c->src_cache) ech = std::min(ech, std::min(c->cache.capacity / 2u, c->cache.transient));
     if (!c->src.native) {
         if (may_grow) {
             wl_status st = ensure_stage(c, ech);
@@ -1116,10 +1128,14 @@ static wl_status cache_init(wl_ctx* c, uint32_t capacity) {
     if (c->src.get) return fail(c, WL_ERR_STATE, "the context already has an expert source");
     if (capacity < 2u * c->cfg.n_experts_per_tok)
         return fail(c, WL_ERR_INVALID, "capacity %u < 2 x n_experts_per_tok", capacity);
+    // 2K transient slots beyond the capacity: a miss the policy does not
+    // retain (or that finds no evictable key) still needs its block in HBM
+    C.transient = 2u * c->cfg.n_experts_per_tok;
+    const uint32_t nslots = capacity + C.transient;
     void* p = nullptr;
-    hipError_t e = hipMalloc(&p, (size_t)capacity * c->native_bytes);
+    hipError_t e = hipMalloc(&p, (size_t)nslots * c->native_bytes);
     if (e != hipSuccess)
-        return fail(c, WL_ERR_OOM, "cache pool of %u x %zu B: %s", capacity, c->native_bytes, hipGetErrorString(e));
+        return fail(c, WL_ERR_OOM, "cache pool of %u x %zu B: %s", nslots, c->native_bytes, hipGetErrorString(e));
     c->allocs.push_back(p);
     C.pool = (uint8_t*)p;
     C.capacity = capacity;
@@ -1128,13 +1144,13 @@ static wl_status cache_init(wl_ctx* c, uint32_t capacity) {
     for (hipStream_t& st : C.copy)
         if ((e = hipStreamCreateWithFlags(&st, hipStreamNonBlocking)) != hipSuccess) return hip_fail(c, e, "copy stream");
     if ((e = hipEventCreateWithFlags(&C.gate, hipEventDisableTiming)) != hipSuccess) return hip_fail(c, e, "cache event");
-    C.slot_ev.assign(capacity, nullptr);
+    C.slot_ev.assign(nslots, nullptr);
     for (hipEvent_t& ev : C.slot_ev)
         if ((e = hipEventCreateWithFlags(&ev, hipEventDisableTiming)) != hipSuccess) return hip_fail(c, e, "slot event");
-    C.has_ev.assign(capacity, 0);
-    C.spec.assign(capacity, 0);
-    C.task_of.assign(capacity, nullptr);
-    C.lru = new wl::SlotLru(capacity);
+    C.has_ev.assign(nslots, 0);
+    C.spec.assign(nslots, 0);
+    C.task_of.assign(nslots, nullptr);
+    C.lru = new wl::SlotLru(capacity, WL_POLICY_LRU, 0.5f, 0u, C.transient);
     c->src = wl_expert_source{c, cache_src_get, cache_src_prefetch, cache_src_get_async, 1};
     c->src_cache = true;
     return WL_OK;
@@ -1191,6 +1207,7 @@ wl_status wl_cache_get_stats(wl_ctx* c, wl_cache_stats* out) {
     out->bytes_h2d = C.bytes_h2d;
     out->used = C.lru->used();
     out->capacity = C.capacity;
+    out->bypassed = C.bypassed;
     return WL_OK;
 }
 
@@ -1199,7 +1216,7 @@ wl_status wl_cache_reset_stats(wl_ctx* c) {
     CacheState& C = c->cache;
     if (!C.lru) return fail(c, WL_ERR_STATE, "no cache (wl_cache_create)");
     C.lru->reset_stats();
-    C.spec_requests = C.spec_copies = C.spec_hits = C.bytes_h2d = 0;
+    C.spec_requests = C.spec_copies = C.spec_hits = C.bytes_h2d = C.bypassed = 0;
     return WL_OK;
 }
 
@@ -1248,12 +1265,21 @@ wl_status wl_cache_get(wl_ctx* c, uint32_t layer, uint32_t expert, void* stream,
     return WL_OK;
 }
 
-wl_status wl_lru_replay(uint32_t capacity, const uint32_t* keys, uint32_t n_keys, uint32_t batch, uint8_t* hit_out,
-                        uint64_t* hits, uint64_t* misses, uint64_t* evictions) {
-    if (capacity == 0 || (n_keys && !keys) || batch == 0) return WL_ERR_INVALID;
-    wl::SlotLru lru(capacity);
+static bool policy_ok(const wl_cache_policy* p) {
+    return p && p->kind >= WL_POLICY_LRU && p->kind <= WL_POLICY_TINYLFU && p->protected_frac >= 0.f &&
+           p->protected_frac <= 1.f;
+}
+
+wl_status wl_policy_replay(const wl_cache_policy* policy, uint32_t capacity, const uint32_t* keys, uint32_t n_keys,
+                           uint32_t batch, const uint32_t* pinned, uint32_t n_pinned, uint8_t* hit_out, uint64_t* hits,
+                           uint64_t* misses, uint64_t* evictions) {
+    if (!policy_ok(policy) || capacity == 0 || (n_keys && !keys) || batch == 0 || (n_pinned && !pinned))
+        return WL_ERR_INVALID;
+    wl::SlotLru lru(capacity, policy->kind, policy->protected_frac, policy->ghost, 2u * batch);
+    for (uint32_t i = 0; i < n_pinned; i++) lru.pin(pinned[i], true);
     for (uint32_t b0 = 0; b0 < n_keys; b0 += batch) {
         const uint32_t b1 = b0 + batch < n_keys ? b0 + batch : n_keys;
+        lru.begin_batch();
         for (uint32_t i = b0; i < b1; i++) {
             bool dup = false;
             for (uint32_t j = b0; j < i; j++) dup = dup || keys[j] == keys[i];
@@ -1262,12 +1288,66 @@ wl_status wl_lru_replay(uint32_t capacity, const uint32_t* keys, uint32_t n_keys
                 continue;
             }
             const wl::SlotLru::Result r = lru.request(keys[i]);
-            if (hit_out) hit_out[i] = r.hit ? 1 : 0;
+            if (hit_out) hit_out[i] = r.hit ? 1 : r.transient ? 3 : 0;
         }
     }
     if (hits) *hits = lru.hits();
     if (misses) *misses = lru.misses();
     if (evictions) *evictions = lru.evictions();
+    return WL_OK;
+}
+
+wl_status wl_lru_replay(uint32_t capacity, const uint32_t* keys, uint32_t n_keys, uint32_t batch, uint8_t* hit_out,
+                        uint64_t* hits, uint64_t* misses, uint64_t* evictions) {
+    const wl_cache_policy lru{WL_POLICY_LRU, 0.5f, 0u};
+    return wl_policy_replay(&lru, capacity, keys, n_keys, batch, nullptr, 0, hit_out, hits, misses, evictions);
+}
+
+// Empties the cache (every slot free, counters zero) under a new policy;
+// pinned keys stay pinned. Waits for the device and for every pending read.
+wl_status wl_cache_set_policy(wl_ctx* c, const wl_cache_policy* policy) {
+    if (!c) return WL_ERR_INVALID;
+    CacheState& C = c->cache;
+    if (!C.lru) return fail(c, WL_ERR_STATE, "no cache (wl_cache_create)");
+    if (!policy_ok(policy)) return fail(c, WL_ERR_INVALID, "bad cache policy");
+    hipError_t e = hipDeviceSynchronize();
+    if (e != hipSuccess) return hip_fail(c, e, "cache flush");
+    if (C.files)
+        for (wl::FileTask*& t : C.task_of)
+            if (t) {
+                C.files->wait_issued(t);
+                C.files->release(t);
+                t = nullptr;
+            }
+    if ((e = hipDeviceSynchronize()) != hipSuccess) return hip_fail(c, e, "cache flush");
+    delete C.lru;
+    C.lru = new wl::SlotLru(C.capacity, policy->kind, policy->protected_frac, policy->ghost, C.transient);
+    for (uint32_t k : C.pinned) C.lru->pin(k, true);
+    C.policy = *policy;
+    std::fill(C.spec.begin(), C.spec.end(), 0);
+    C.resolved.clear();
+    C.spec_pending = false;
+    C.spec_requests = C.spec_copies = C.spec_hits = C.bytes_h2d = C.bypassed = 0;
+    return WL_OK;
+}
+
+wl_status wl_cache_pin(wl_ctx* c, uint32_t layer, uint32_t expert, int32_t pinned) {
+    if (!c) return WL_ERR_INVALID;
+    CacheState& C = c->cache;
+    if (!C.lru) return fail(c, WL_ERR_STATE, "no cache (wl_cache_create)");
+    if (layer >= c->cfg.n_layers || expert >= c->cfg.n_routed_experts)
+        return fail(c, WL_ERR_INVALID, "(%u,%u) out of range", layer, expert);
+    const uint32_t key = layer * c->cfg.n_routed_experts + expert;
+    const bool on = pinned != 0;
+    auto it = std::find(C.pinned.begin(), C.pinned.end(), key);
+    if (on && it == C.pinned.end()) {
+        if (C.pinned.size() + 2u * c->cfg.n_experts_per_tok >= C.capacity)
+            return fail(c, WL_ERR_INVALID, "pinning more than capacity - 2 x n_experts_per_tok keys");
+        C.pinned.push_back(key);
+    } else if (!on && it != C.pinned.end()) {
+        C.pinned.erase(it);
+    }
+    C.lru->pin(key, on);
     return WL_OK;
 }
 

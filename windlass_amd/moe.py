@@ -47,7 +47,18 @@ class ExpertLayout(ctypes.Structure):
 class CacheStats(ctypes.Structure):
     _fields_ = [(n, ctypes.c_uint64) for n in ["hits", "misses", "evictions", "spec_requests", "spec_copies",
                                                "spec_hits", "bytes_h2d"]] + \
-               [("used", ctypes.c_uint32), ("capacity", ctypes.c_uint32)]
+               [("used", ctypes.c_uint32), ("capacity", ctypes.c_uint32), ("bypassed", ctypes.c_uint64)]
+
+
+POLICY = {"lru": 0, "lfu": 1, "slru": 2, "2q": 3, "tinylfu": 4}
+
+
+class CachePolicy(ctypes.Structure):
+    _fields_ = [("kind", ctypes.c_int32), ("protected_frac", ctypes.c_float), ("ghost", ctypes.c_uint32)]
+
+
+def make_policy(name="lru", protected_frac=0.5, ghost=0):
+    return CachePolicy(POLICY[name], protected_frac, ghost)
 
 
 # const uint8_t* host_block(void* user, uint32_t layer, uint32_t expert)
@@ -120,6 +131,11 @@ def load():
         "wl_lru_replay": [u32, ctypes.POINTER(u32), u32, u32, ctypes.POINTER(ctypes.c_uint8),
                           ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_uint64),
                           ctypes.POINTER(ctypes.c_uint64)],
+        "wl_policy_replay": [ctypes.POINTER(CachePolicy), u32, ctypes.POINTER(u32), u32, u32, ctypes.POINTER(u32), u32,
+                             ctypes.POINTER(ctypes.c_uint8), ctypes.POINTER(ctypes.c_uint64),
+                             ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_uint64)],
+        "wl_cache_set_policy": [vp, ctypes.POINTER(CachePolicy)],
+        "wl_cache_pin": [vp, u32, u32, i32],
     }
     for name, args in sig.items():
         fn = getattr(lib, name)
@@ -190,6 +206,25 @@ def lru_replay(capacity, keys, batch):
                               ctypes.byref(e))
     if rc != WL_OK:
         raise WindlassError(rc, "wl_lru_replay")
+    return out, h.value, m.value, e.value
+
+
+def policy_replay(policy, capacity, keys, batch, pinned=()):
+    """The cache's bookkeeping under `policy` (a CachePolicy or a name) over a
+    key sequence (no device use): (per-key 1 hit / 0 retained miss / 3 miss
+    not retained / 2 skipped duplicate, hits, misses, evictions)."""
+    import numpy as np
+    pol = make_policy(policy) if isinstance(policy, str) else policy
+    k = np.ascontiguousarray(keys, dtype=np.uint32)
+    pn = np.ascontiguousarray(list(pinned), dtype=np.uint32)
+    out = np.zeros(len(k), dtype=np.uint8)
+    h, m, e = ctypes.c_uint64(), ctypes.c_uint64(), ctypes.c_uint64()
+    P32 = ctypes.POINTER(ctypes.c_uint32)
+    rc = load().wl_policy_replay(ctypes.byref(pol), capacity, k.ctypes.data_as(P32), len(k), batch,
+                                 pn.ctypes.data_as(P32), len(pn), out.ctypes.data_as(ctypes.POINTER(ctypes.c_uint8)),
+                                 ctypes.byref(h), ctypes.byref(m), ctypes.byref(e))
+    if rc != WL_OK:
+        raise WindlassError(rc, "wl_policy_replay")
     return out, h.value, m.value, e.value
 
 
@@ -338,6 +373,13 @@ class Context:
         st = CacheStats()
         self._ck(self.lib.wl_cache_get_stats(self.h, ctypes.byref(st)), "wl_cache_get_stats")
         return {n: getattr(st, n) for n, _ in CacheStats._fields_}
+
+    def cache_set_policy(self, name="lru", protected_frac=0.5, ghost=0):
+        pol = make_policy(name, protected_frac, ghost)
+        self._ck(self.lib.wl_cache_set_policy(self.h, ctypes.byref(pol)), "wl_cache_set_policy")
+
+    def cache_pin(self, layer, expert, pinned=True):
+        self._ck(self.lib.wl_cache_pin(self.h, layer, expert, 1 if pinned else 0), "wl_cache_pin")
 
     def cache_reset_stats(self):
         self._ck(self.lib.wl_cache_reset_stats(self.h), "wl_cache_reset_stats")
