@@ -44,7 +44,9 @@ typedef enum wl_status {
     WL_ERR_NOT_RESIDENT = 4, /* a routed expert has no HBM slot bound */
     WL_ERR_STATE = 5,        /* call made in the wrong state (e.g. layer not set) */
     WL_ERR_DEVICE = 6,       /* the device kernel reported an error (see wl_check_error) */
-    WL_ERR_IO = 7            /* host backing store read failed */
+    WL_ERR_IO = 7,           /* host backing store or checkpoint read failed */
+    WL_ERR_NOT_FOUND = 8,    /* a checkpoint tensor is absent */
+    WL_ERR_FORMAT = 9        /* a checkpoint file is malformed or does not match the config */
 } wl_status;
 
 /* MoE fields of glm::Config (reference src/glm_loader.cuh:35-47). */
@@ -398,6 +400,81 @@ wl_status wl_policy_replay(const wl_cache_policy* policy, uint32_t capacity, con
  * (optional) is 1 for a hit, 0 for a miss, 2 for a skipped duplicate. */
 wl_status wl_lru_replay(uint32_t capacity, const uint32_t* keys, uint32_t n_keys, uint32_t batch,
                         uint8_t* hit_out, uint64_t* hits, uint64_t* misses, uint64_t* evictions);
+
+/* ---- checkpoint loader (safetensors) -------------------------------------
+ * A sharded safetensors checkpoint: model.safetensors.index.json maps each
+ * tensor name to a shard file; a shard is an 8-byte little-endian header
+ * length, a JSON header {name: {dtype, shape, data_offsets}} and the data.
+ * Host-only: these calls use no device. One thread per wl_st. */
+typedef struct wl_st wl_st;
+
+#define WL_ST_MAX_DIMS 8
+typedef struct wl_st_tensor {
+    char     dtype[16];          /* "BF16", "F32", "U8", ... as in the header */
+    uint32_t ndim;
+    uint64_t shape[WL_ST_MAX_DIMS];
+    uint64_t nbytes;
+    uint64_t file_offset;        /* absolute offset of its first byte in its shard */
+    uint32_t shard;              /* index of its shard file */
+} wl_st_tensor;
+
+/* Replaces st::open (src/safetensors_io.cuh:89-186). `path` is a checkpoint
+ * directory (with model.safetensors.index.json, or a single
+ * model.safetensors) or one .safetensors file. Every tensor the index names
+ * must be in its shard's header; allow_missing_shards != 0 skips shard files
+ * that do not exist (their tensors are then absent, as in st::open). Each
+ * tensor's byte range must lie inside its shard, and for the fixed-width
+ * dtypes match its shape (WL_ERR_FORMAT otherwise). On failure *out is NULL
+ * and wl_st_last_error(NULL) gives this thread's message. */
+wl_status   wl_st_open(const char* path, int32_t allow_missing_shards, wl_st** out);
+void        wl_st_close(wl_st* st);                                      /* st::close */
+const char* wl_st_last_error(const wl_st* st);
+uint32_t    wl_st_count(const wl_st* st);                                /* tensors, */
+const char* wl_st_name(const wl_st* st, uint32_t i);                     /* in name order */
+/* Replaces st::info (src/safetensors_io.cuh:194-197): WL_ERR_NOT_FOUND for
+ * an absent tensor. */
+wl_status   wl_st_info(const wl_st* st, const char* name, wl_st_tensor* out);
+/* Replaces st::read_bytes (src/safetensors_io.cuh:199-229): the tensor's raw
+ * bytes into h_dst (capacity >= nbytes), by positional reads. */
+wl_status   wl_st_read(wl_st* st, const char* name, void* h_dst, size_t capacity);
+
+/* Replaces the MoE fields of glm::load_layer (src/glm_loader.cuh:524-620):
+ * loads checkpoint layer `ckpt_layer`'s
+ *   model.layers.N.post_attention_layernorm.weight       BF16 [H]
+ *   model.layers.N.mlp.gate.weight                       BF16 [E, H]
+ *   model.layers.N.mlp.gate.e_score_correction_bias      F32  [E]
+ *   model.layers.N.mlp.shared_experts.{gate,up,down}_proj.weight
+ * into context layer `layer`. A tensor is MXFP4 when "<name>_scale" exists
+ * (as in the reference): then the weight is U8 [rows, cols/2] and the scale
+ * U8 [rows, cols/32] (gate/up: rows SI, cols H; down: rows H, cols SI), and
+ * the shared expert is bound as by wl_set_layer_mxfp4; without scales the
+ * shared projections are BF16 [rows, cols] and bound as WL_SHARED_BF16. The
+ * router, bias and norm copies are owned by the context (freed when the layer
+ * is bound again or the context destroyed). Errors: WL_ERR_NOT_FOUND for a
+ * missing tensor, WL_ERR_FORMAT for a dtype or size that does not match the
+ * config, WL_ERR_IO for a failed read. Synchronises the device. */
+wl_status wl_load_layer(wl_ctx* ctx, wl_st* st, uint32_t ckpt_layer, uint32_t layer);
+
+/* Populates the slot table from the checkpoint: routed experts experts[i]
+ * (experts NULL: expert i), i < n, of checkpoint layer `ckpt_layer`
+ * (model.layers.N.mlp.experts.e.{gate,up,down}_proj.weight and
+ * .weight_scale, MXFP4 as above) are read into pinned buffers, copied to the
+ * device, converted into the native layout in context pool slot first_slot +
+ * i (wl_slot_pool_create) and bound to (layer, experts[i]). Every tensor is
+ * checked before any slot is written. Reads of one expert overlap the copy
+ * and conversion of the previous one on `stream`; the call returns after the
+ * stream has drained and the slots are bound. Reference: the packed block of
+ * tools/repack_experts_glm.py:46-55 filled into an ExpertCache slot
+ * (src/glm_expert_cache.cuh:394-433), here straight from the shards. */
+wl_status wl_load_experts(wl_ctx* ctx, wl_st* st, uint32_t ckpt_layer, uint32_t layer, const uint32_t* experts,
+                          uint32_t n, uint32_t first_slot, void* stream);
+
+/* Writes `path` as the packed expert file of checkpoint layer `ckpt_layer`
+ * (the input of wl_cache_create_files): n_routed_experts records of
+ * wl_expert_layout_of(cfg, 0).total bytes, record e the six tensors of expert
+ * e in layout order (tools/repack_experts_glm.py:5-14,46-55). Host-only;
+ * errors in wl_st_last_error(st); a failed call removes the partial file. */
+wl_status wl_st_pack_layer(wl_st* st, const wl_moe_config* cfg, uint32_t ckpt_layer, const char* path);
 
 /* ---- single-expert building blocks ---------------------------------------
  * y[N] = W . x for MXFP4 W ([N,K/2] packed nibbles + [N,K/32] E8M0 scales) and

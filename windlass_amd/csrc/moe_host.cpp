@@ -18,6 +18,7 @@
 
 #include "../../include/windlass_moe.h"
 #include "expert_files.h"
+#include "host_internal.h"
 #include "internal.h"
 #include "lru.h"
 
@@ -29,6 +30,7 @@ struct LayerState {
     size_t shared_bytes = 0;
     int32_t shared_dtype = WL_SHARED_BF16;
     bool set = false;
+    std::vector<void*> owned;  // router / bias / norm buffers the context took over (wl_load_layer)
 };
 
 // HBM expert cache (config 4): LRU slot pool filled from pinned host blocks.
@@ -380,6 +382,8 @@ void wl_destroy(wl_ctx* c) {
     }
     if (c->batch.buf) (void)hipFree(c->batch.buf);
     if (c->stage) (void)hipFree(c->stage);
+    for (LayerState& L : c->layers)
+        for (void* p : L.owned) (void)hipFree(p);
     if (c->h_pin) (void)hipHostFree(c->h_pin);
     for (hipEvent_t e : {c->ids_ev, c->pred_ev})
         if (e) (void)hipEventDestroy(e);
@@ -394,9 +398,9 @@ const char* wl_last_error(const wl_ctx* c) { return c ? c->err.c_str() : "null c
 // context-owned memory: bf16 (NativeShared) from `bf16`, or MXFP4
 // (NativeShared4) from the six reference tensors `parts` (gate_w, gate_s,
 // up_w, up_s, down_w, down_s).
-static wl_status set_layer(wl_ctx* c, uint32_t layer, const uint16_t* d_router_w, const float* d_router_bias,
-                           const uint16_t* d_post_attn_ln, const uint16_t* bf16, const uint8_t* const* parts) {
-    if (!c) return WL_ERR_INVALID;
+static wl_status set_layer_checked(wl_ctx* c, uint32_t layer, const uint16_t* d_router_w, const float* d_router_bias,
+                                   const uint16_t* d_post_attn_ln, const uint16_t* bf16, const uint8_t* const* parts,
+                                   std::vector<void*>& take) {
     if (layer >= c->cfg.n_layers) return fail(c, WL_ERR_INVALID, "layer %u >= n_layers %u", layer, c->cfg.n_layers);
     if (!d_router_w || !d_router_bias) return fail(c, WL_ERR_INVALID, "router weight and router bias are required");
     const uint32_t H = c->cfg.hidden, SI = c->SI;
@@ -431,7 +435,22 @@ static wl_status set_layer(wl_ctx* c, uint32_t layer, const uint16_t* d_router_w
     hipError_t e = hipMemcpy(c->d_largs + layer, &a, sizeof(a), hipMemcpyHostToDevice);
     if (e != hipSuccess) return hip_fail(c, e, "layer record upload");
     L.set = true;
+    // the device was synchronised above: no kernel still reads the buffers the layer used before
+    for (void* p : L.owned) (void)hipFree(p);
+    L.owned.clear();
+    L.owned.swap(take);  // take is left empty: the caller frees nothing
     return WL_OK;
+}
+
+// set_layer_checked with the buffers in `take` (router, bias, norm) handed to
+// the context: kept by the layer on success, freed on failure.
+static wl_status set_layer(wl_ctx* c, uint32_t layer, const uint16_t* d_router_w, const float* d_router_bias,
+                           const uint16_t* d_post_attn_ln, const uint16_t* bf16, const uint8_t* const* parts,
+                           std::vector<void*> take = {}) {
+    wl_status st = c ? set_layer_checked(c, layer, d_router_w, d_router_bias, d_post_attn_ln, bf16, parts, take)
+                     : WL_ERR_INVALID;
+    for (void* p : take) (void)hipFree(p);  // empty after a success
+    return st;
 }
 
 wl_status wl_set_layer(wl_ctx* c, uint32_t layer, const uint16_t* d_router_w, const float* d_router_bias,
@@ -455,6 +474,24 @@ wl_status wl_set_layer_mxfp4(wl_ctx* c, uint32_t layer, const uint16_t* d_router
     const uint8_t* parts[6] = {d_sh_gate_w, d_sh_gate_s, d_sh_up_w, d_sh_up_s, d_sh_down_w, d_sh_down_s};
     return set_layer(c, layer, d_router_w, d_router_bias, d_post_attn_ln, nullptr, parts);
 }
+
+}  // extern "C"
+
+namespace wl {
+
+const wl_moe_config& ctx_config(const wl_ctx* c) { return c->cfg; }
+uint32_t ctx_shared_inter(const wl_ctx* c) { return c->SI; }
+
+wl_status ctx_fail(wl_ctx* c, wl_status s, const std::string& msg) { return fail(c, s, "%s", msg.c_str()); }
+
+wl_status ctx_set_layer_owned(wl_ctx* c, uint32_t layer, uint16_t* router_w, float* bias, uint16_t* ln,
+                              const uint16_t* bf16_shared, const uint8_t* const* mxfp4_parts) {
+    return set_layer(c, layer, router_w, bias, ln, bf16_shared, mxfp4_parts, {router_w, bias, ln});
+}
+
+}  // namespace wl
+
+extern "C" {
 
 wl_status wl_slot_bind(wl_ctx* c, uint32_t layer, uint32_t expert, const uint8_t* d_block) {
     if (!c) return WL_ERR_INVALID;

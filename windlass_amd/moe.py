@@ -14,7 +14,7 @@ HEADER = os.path.join(os.path.dirname(HERE), "include", "windlass_moe.h")
 
 WL_OK = 0
 STATUS = {0: "WL_OK", 1: "WL_ERR_INVALID", 2: "WL_ERR_HIP", 3: "WL_ERR_OOM", 4: "WL_ERR_NOT_RESIDENT",
-          5: "WL_ERR_STATE", 6: "WL_ERR_DEVICE", 7: "WL_ERR_IO"}
+          5: "WL_ERR_STATE", 6: "WL_ERR_DEVICE", 7: "WL_ERR_IO", 8: "WL_ERR_NOT_FOUND", 9: "WL_ERR_FORMAT"}
 SHARED_BF16, SHARED_MXFP4 = 0, 1
 SCHED_FUSED, SCHED_PHASED = 0, 1
 MAX_TOPK = 32
@@ -78,6 +78,11 @@ class ExpertSourceC(ctypes.Structure):
                 ("get_async", SRC_GET_ASYNC_FN), ("native", ctypes.c_int32)]
 
 
+class StTensor(ctypes.Structure):
+    _fields_ = [("dtype", ctypes.c_char * 16), ("ndim", ctypes.c_uint32), ("shape", ctypes.c_uint64 * 8),
+                ("nbytes", ctypes.c_uint64), ("file_offset", ctypes.c_uint64), ("shard", ctypes.c_uint32)]
+
+
 class Taps(ctypes.Structure):
     _fields_ = [(n, ctypes.c_void_p) for n in ["norm", "logits", "topk_idx", "topk_w", "mid", "shared"]]
 
@@ -136,6 +141,12 @@ def load():
                              ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_uint64)],
         "wl_cache_set_policy": [vp, ctypes.POINTER(CachePolicy)],
         "wl_cache_pin": [vp, u32, u32, i32],
+        "wl_st_open": [ctypes.c_char_p, i32, ctypes.POINTER(vp)],
+        "wl_st_info": [vp, ctypes.c_char_p, ctypes.POINTER(StTensor)],
+        "wl_st_read": [vp, ctypes.c_char_p, vp, ctypes.c_size_t],
+        "wl_st_pack_layer": [vp, ctypes.POINTER(MoeConfig), u32, ctypes.c_char_p],
+        "wl_load_layer": [vp, vp, u32, u32],
+        "wl_load_experts": [vp, vp, u32, u32, ctypes.POINTER(u32), u32, u32, vp],
     }
     for name, args in sig.items():
         fn = getattr(lib, name)
@@ -147,6 +158,14 @@ def load():
     lib.wl_destroy.restype = None
     lib.wl_last_error.argtypes = [vp]
     lib.wl_last_error.restype = ctypes.c_char_p
+    lib.wl_st_close.argtypes = [vp]
+    lib.wl_st_close.restype = None
+    lib.wl_st_last_error.argtypes = [vp]
+    lib.wl_st_last_error.restype = ctypes.c_char_p
+    lib.wl_st_count.argtypes = [vp]
+    lib.wl_st_count.restype = u32
+    lib.wl_st_name.argtypes = [vp, u32]
+    lib.wl_st_name.restype = ctypes.c_char_p
     _lib = lib
     return lib
 
@@ -234,6 +253,61 @@ def dequant_matvec_mxfp4(d_W, d_S, d_x, d_y, N, K, stream=0):
         raise WindlassError(rc, "wl_dequant_matvec_mxfp4")
 
 
+class SafeTensors:
+    """An open safetensors checkpoint (wl_st_*): a directory with
+    model.safetensors.index.json or model.safetensors, or one .safetensors
+    file. Host-only."""
+
+    def __init__(self, path, allow_missing_shards=False):
+        self.lib = load()
+        h = ctypes.c_void_p()
+        rc = self.lib.wl_st_open(os.fsencode(path), 1 if allow_missing_shards else 0, ctypes.byref(h))
+        if rc != WL_OK:
+            raise WindlassError(rc, f"wl_st_open: {self.lib.wl_st_last_error(None).decode()}")
+        self.h = h.value
+
+    def _ck(self, rc, what):
+        if rc != WL_OK:
+            raise WindlassError(rc, f"{what}: {self.lib.wl_st_last_error(self.h).decode()}")
+
+    def names(self):
+        return [self.lib.wl_st_name(self.h, i).decode() for i in range(self.lib.wl_st_count(self.h))]
+
+    def info(self, name):
+        """dict(dtype, shape, nbytes, file_offset, shard), or None if absent."""
+        t = StTensor()
+        rc = self.lib.wl_st_info(self.h, name.encode(), ctypes.byref(t))
+        if rc == 8:  # WL_ERR_NOT_FOUND
+            return None
+        self._ck(rc, "wl_st_info")
+        return {"dtype": t.dtype.decode(), "shape": tuple(t.shape[i] for i in range(t.ndim)), "nbytes": t.nbytes,
+                "file_offset": t.file_offset, "shard": t.shard}
+
+    def read(self, name, capacity=None):
+        """The tensor's raw bytes (numpy uint8)."""
+        import numpy as np
+        t = self.info(name)
+        n = t["nbytes"] if t else 0
+        buf = np.empty(max(n, 1) if capacity is None else capacity, np.uint8)
+        self._ck(self.lib.wl_st_read(self.h, name.encode(), buf.ctypes.data, buf.nbytes), f"wl_st_read({name})")
+        return buf[:n]
+
+    def pack_layer(self, cfg, ckpt_layer, path):
+        self._ck(self.lib.wl_st_pack_layer(self.h, ctypes.byref(cfg), ckpt_layer, os.fsencode(path)),
+                 "wl_st_pack_layer")
+
+    def close(self):
+        if self.h:
+            self.lib.wl_st_close(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
 class Context:
     """One wl_ctx: the MoE layers of a model on the current device."""
 
@@ -268,6 +342,18 @@ class Context:
     def set_layer_mxfp4(self, layer, router_w, bias, ln_w, gw, gs, uw, us, dw, ds):
         self._ck(self.lib.wl_set_layer_mxfp4(self.h, layer, router_w, bias, ln_w, gw, gs, uw, us, dw, ds),
                  "wl_set_layer_mxfp4")
+
+    def load_layer(self, st, ckpt_layer, layer):
+        self._ck(self.lib.wl_load_layer(self.h, st.h, ckpt_layer, layer), "wl_load_layer")
+
+    def load_experts(self, st, ckpt_layer, layer, experts=None, n=None, first_slot=0, stream=0):
+        if experts is None:
+            arr, cnt = None, n
+        else:
+            arr = (ctypes.c_uint32 * len(experts))(*[int(e) for e in experts])
+            cnt = len(experts)
+        self._ck(self.lib.wl_load_experts(self.h, st.h, ckpt_layer, layer, arr, cnt, first_slot, stream),
+                 "wl_load_experts")
 
     def slot_bind(self, layer, expert, d_block):
         self._ck(self.lib.wl_slot_bind(self.h, layer, expert, d_block), "wl_slot_bind")
