@@ -93,3 +93,60 @@ def test_hand_slru():
     out, h, m, e = moe.policy_replay("slru", 2, SEQ, 1)
     assert list(out) == [0, 0, 1, 0, 1, 1, 0] and (h, m, e) == (3, 4, 2)
     assert OP.replay("slru", 2, SEQ, 1)[1:] == (3, 4, 2)
+
+
+# The hand answers above, and one sequence that separates LFU from LRU:
+# capacity 2, [1 1 2 3 1]: LRU evicts 1 (least recent) for 3, so the last 1
+# misses; LFU evicts 2 (count 1 < 2), so it hits.
+HAND = {"lru": ([0, 0, 1, 0, 1, 1, 0], (3, 4, 2)), "lfu": ([0, 0, 1, 0, 1, 1, 0], (3, 4, 2)),
+        "slru": ([0, 0, 1, 0, 1, 1, 0], (3, 4, 2)), "2q": ([0, 0, 1, 3, 1, 0, 3], (2, 5, 1)),
+        "tinylfu": ([0, 0, 1, 3, 1, 0, 3], (2, 5, 1))}
+SEQ2 = [1, 1, 2, 3, 1]
+HAND2 = {"lru": ([0, 1, 0, 0, 0], (1, 4, 2)), "lfu": ([0, 1, 0, 0, 1], (2, 3, 1))}
+
+
+def _replay_with(cls, kind, cap, keys):
+    c = cls(kind, cap)
+    out = [c.request(k, {k}) for k in keys]
+    return out, (c.hits, c.misses, c.evictions)
+
+
+@pytest.mark.parametrize("kind", sorted(HAND))
+def test_oracle_hand_cases(kind):
+    """The oracle itself against the hand answers (the engine is checked
+    against the oracle on random streams)."""
+    out, h, m, e = OP.replay(kind, 2, SEQ, 1)
+    assert (out, (h, m, e)) == HAND[kind]
+    if kind in HAND2:
+        out, h, m, e = OP.replay(kind, 2, SEQ2, 1)
+        assert (out, (h, m, e)) == HAND2[kind]
+        got = moe.policy_replay(kind, 2, SEQ2, 1)
+        assert (list(got[0]), got[1:]) == HAND2[kind]
+
+
+def test_planted_mistakes_fail_the_hand_cases():
+    """Mistakes planted in a copy of the oracle: each changes a hand answer."""
+
+    class MostRecentVictim(OP.PolicyCache):  # evicts the newest key instead of the oldest
+        def _victim(self, batch):
+            ok = [k for k in list(self.main) + list(self.prot) if k not in batch and k not in self.pinned]
+            return ok[-1] if ok else None
+
+    class AdmitOnTie(OP.PolicyCache):  # TinyLFU admission with >= instead of >
+        def request(self, key, batch):
+            self.freq[key] += 1  # compared one higher: count + 1 > victim's  <=>  count >= victim's
+            r = super().request(key, batch)
+            self.freq[key] -= 1
+            return r
+
+    class LfuTiesToNewest(OP.PolicyCache):  # LFU ties broken toward the most recent key
+        def _victim(self, batch):
+            ok = [k for k in list(self.main) + list(self.prot) if k not in batch and k not in self.pinned]
+            return min(reversed(ok), key=lambda k: self.freq[k]) if ok else None
+
+    assert _replay_with(OP.PolicyCache, "lru", 2, SEQ) == HAND["lru"]
+    assert _replay_with(MostRecentVictim, "lru", 2, SEQ) != HAND["lru"]
+    assert _replay_with(OP.PolicyCache, "tinylfu", 2, SEQ) == HAND["tinylfu"]
+    assert _replay_with(AdmitOnTie, "tinylfu", 2, SEQ) != HAND["tinylfu"]
+    assert _replay_with(OP.PolicyCache, "lfu", 2, [1, 2, 3, 1]) != _replay_with(LfuTiesToNewest, "lfu", 2,
+                                                                                 [1, 2, 3, 1])
