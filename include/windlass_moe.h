@@ -476,6 +476,96 @@ wl_status wl_load_experts(wl_ctx* ctx, wl_st* st, uint32_t ckpt_layer, uint32_t 
  * errors in wl_st_last_error(st); a failed call removes the partial file. */
 wl_status wl_st_pack_layer(wl_st* st, const wl_moe_config* cfg, uint32_t ckpt_layer, const char* path);
 
+/* ---- the caller side of a decoder layer: MLA attention and dense MLP ------
+ * Replaces run_attention / run_layer (src/glm_layer_runner.cuh:525-675) and
+ * the dense branch of run_moe (:373-384) at decode (one position per call).
+ * A wl_attn holds the attention weights of n_layers decoder layers (caller-
+ * owned device pointers), their KV caches (context-owned, max_seq positions:
+ * kv_c [L] and k_rot [qk_rope] f32 per position, the absorbed-MLA form, plus
+ * the indexer keys [index_head_dim] f32 on indexer-owning layers) and the
+ * scratch. One host thread per wl_attn; work is enqueued on the given stream. */
+typedef struct wl_attn_config {
+    uint32_t hidden;          /* hidden_size               6144 */
+    uint32_t n_heads;         /* num_attention_heads         64 */
+    uint32_t q_lora_rank;     /*                           2048 */
+    uint32_t kv_lora_rank;    /*                            512 */
+    uint32_t qk_nope;         /* qk_nope_head_dim           192 */
+    uint32_t qk_rope;         /* qk_rope_head_dim            64 */
+    uint32_t v_head;          /* v_head_dim                 256 */
+    uint32_t index_n_heads;   /* DSA indexer heads           32 */
+    uint32_t index_head_dim;  /*                            128 */
+    uint32_t index_topk;      /* keys kept per query       2048 */
+    uint32_t dense_inter;     /* intermediate_size (dense MLP) 12288 */
+    uint32_t n_layers;        /* decoder layers served by the context */
+    uint32_t max_seq;         /* KV-cache capacity in positions */
+    float    rms_eps;         /* rms_norm_eps of input / post-attention norms 1e-5 */
+    float    rope_theta;
+} wl_attn_config;
+
+typedef struct wl_attn wl_attn;
+
+/* Attention weights of one layer (glm::LayerWeights' attention fields,
+ * src/glm_loader.cuh:259-339), bf16 [out, in] row-major unless stated. The
+ * five idx_* pointers are all set on an indexer-owning ("full") layer and all
+ * NULL on a "shared" layer, which reuses the selection the last owning layer
+ * made at the same position (IndexShare, src/glm_layer_runner.cuh:461-519). */
+typedef struct wl_attn_weights {
+    const uint16_t* input_ln;          /* [H] */
+    const uint16_t* q_a_proj;          /* [q_lora, H] */
+    const uint16_t* q_a_ln;            /* [q_lora] */
+    const uint16_t* q_b_proj;          /* [n_heads * (qk_nope + qk_rope), q_lora] */
+    const uint16_t* kv_a_proj;         /* [kv_lora + qk_rope, H] (kv_a_proj_with_mqa) */
+    const uint16_t* kv_a_ln;           /* [kv_lora] */
+    const uint16_t* kv_b_proj;         /* [n_heads * (qk_nope + v_head), kv_lora] */
+    const uint16_t* o_proj;            /* [H, n_heads * v_head] */
+    const uint16_t* idx_wq_b;          /* [index_n_heads * index_head_dim, q_lora] */
+    const uint16_t* idx_wk;            /* [index_head_dim, H] */
+    const uint16_t* idx_k_norm_w;      /* [index_head_dim] (LayerNorm weight) */
+    const uint16_t* idx_k_norm_b;      /* [index_head_dim] (LayerNorm bias) */
+    const float*    idx_weights_proj;  /* [index_n_heads, H] f32 */
+} wl_attn_weights;
+
+/* Creates the context on the current device (KV caches zeroed). Shapes:
+ * hidden, q_lora_rank, kv_lora_rank, n_heads * v_head and dense_inter are
+ * multiples of 8 and at most 16384; kv_lora_rank <= 512; qk_rope a multiple
+ * of 4 and <= index_head_dim <= 256; index_n_heads * index_head_dim <= 16384;
+ * n_heads a multiple of 16 or at most 16; v_head a multiple of 8. On
+ * failure wl_attn_last_error(NULL) gives this thread's message. */
+wl_status   wl_attn_create(const wl_attn_config* cfg, wl_attn** out);
+void        wl_attn_destroy(wl_attn* a);
+const char* wl_attn_last_error(const wl_attn* a);
+wl_status   wl_attn_set_layer(wl_attn* a, uint32_t layer, const wl_attn_weights* w);
+/* A dense MLP layer (layer < dense_first): post_attention_layernorm [H],
+ * gate / up [dense_inter, H], down [H, dense_inter], bf16. */
+wl_status   wl_attn_set_dense_mlp(wl_attn* a, uint32_t layer, const uint16_t* d_post_ln, const uint16_t* d_gate,
+                                  const uint16_t* d_up, const uint16_t* d_down);
+/* run_attention: d_hidden [H] f32 <- d_hidden + o_proj(attention(input_ln(
+ * d_hidden))) at position pos (< max_seq), writing the layer's cache row pos;
+ * the keys attended are 0..pos (those of the DSA selection when pos + 1 >
+ * index_topk). A "shared" layer with no selection published at pos by an
+ * owning layer fails with WL_ERR_STATE (the reference raises, M:418). */
+wl_status   wl_run_attention(wl_attn* a, uint32_t layer, uint32_t pos, float* d_hidden, void* stream);
+/* d_hidden <- d_hidden + down(silu(gate(x)) * up(x)), x = post_ln(d_hidden). */
+wl_status   wl_run_dense_mlp(wl_attn* a, uint32_t layer, float* d_hidden, void* stream);
+/* run_layer: attention, then the dense MLP (a layer set with
+ * wl_attn_set_dense_mlp) or the MoE layer moe_layer of `moe` (wl_run_moe +
+ * residual), d_hidden updated in place. */
+wl_status   wl_run_layer(wl_attn* a, wl_ctx* moe, uint32_t layer, uint32_t moe_layer, uint32_t pos, float* d_hidden,
+                         void* stream);
+/* Device pointers to the last call's intermediates (test hook): the input
+ * norm [H], q_resid [q_lora], the attention context before o_proj
+ * [n_heads * v_head], the o_proj output [H], the index scores [pos + 1] and
+ * keep mask [pos + 1] (uint8, 1 = attended) of the last owning layer. */
+typedef struct wl_attn_taps_out {
+    void* norm;
+    void* q_resid;
+    void* attn;
+    void* attn_out;
+    void* index_score;
+    void* keep;
+} wl_attn_taps_out;
+wl_status   wl_attn_taps(wl_attn* a, wl_attn_taps_out* out);
+
 /* ---- single-expert building blocks ---------------------------------------
  * y[N] = W . x for MXFP4 W ([N,K/2] packed nibbles + [N,K/32] E8M0 scales) and
  * f32 x [K]. Replaces launch_dequant_matvec_mxfp4 (src/glm_kernels.cuh:104-110).

@@ -12,6 +12,13 @@ Run in the build container: python tests/golden/make_golden.py
   float32 on this repository's synthetic inputs (oracle/synth.py), with the
   routed MXFP4 experts dequantised by transformers. Stores the expected
   substeps, not the inputs (the inputs are regenerated from the seeds).
+* attn_tf_small.npz — two small MLA attention layers with the DSA indexer
+  (layer 0 "full", layer 1 "shared": it reuses layer 0's selection) and a
+  dense MLP, run by transformers' GlmMoeDsaAttention / GlmMoeDsaMLP in
+  float32 (eager) over a 12-position sequence, with weights from
+  windlass_amd.synthdata.attention_layer / dense_mlp; stores each
+  position's o_proj output, the indexer's selection (as a keep mask over the
+  causal keys) and the MLP outputs.
 
 Neither the reference's Python nor this repository's oracle computes any
 expected value here.
@@ -27,6 +34,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.dirname(os.path.dirname(HERE)))
 
 from oracle import synth  # noqa: E402  (inputs only)
+from windlass_amd import synthdata  # noqa: E402  (inputs only)
 
 from transformers.integrations.mxfp4 import _convert_moe_packed_tensors  # noqa: E402
 from transformers.models.glm_moe_dsa import modeling_glm_moe_dsa as M  # noqa: E402
@@ -102,6 +110,76 @@ def moe_small(seed):
             "margin": np.float32(srt[K - 1] - srt[K])}
 
 
+ATT = dict(hidden=256, n_heads=4, q_lora_rank=64, kv_lora_rank=32, qk_nope=16, qk_rope=16, v_head=24,
+           index_n_heads=4, index_head_dim=32, index_topk=6, dense_inter=384, rms_eps=1e-5, rope_theta=10000.0)
+ATT_SEQ, ATT_SEED = 12, 7
+
+
+def attn_small():
+    a = ATT
+    H, S = a["hidden"], ATT_SEQ
+    cfg = GlmMoeDsaConfig(hidden_size=H, num_attention_heads=a["n_heads"], num_key_value_heads=a["n_heads"],
+                          q_lora_rank=a["q_lora_rank"], kv_lora_rank=a["kv_lora_rank"],
+                          qk_nope_head_dim=a["qk_nope"], qk_rope_head_dim=a["qk_rope"], v_head_dim=a["v_head"],
+                          index_n_heads=a["index_n_heads"], index_head_dim=a["index_head_dim"],
+                          index_topk=a["index_topk"], intermediate_size=a["dense_inter"], num_hidden_layers=2,
+                          first_k_dense_replace=1, indexer_types=["full", "shared"], rms_norm_eps=a["rms_eps"],
+                          rope_parameters={"rope_type": "default", "rope_theta": a["rope_theta"]},
+                          hidden_act="silu", attention_bias=False)
+    cfg._attn_implementation = "eager"
+    rot = M.GlmMoeDsaRotaryEmbedding(cfg)
+    pos = torch.arange(S).reshape(1, S)
+    out = {}
+    prev = None
+    for layer in range(2):
+        w = synthdata.as_f32(synthdata.attention_layer(a, ATT_SEED, layer, owner=(layer == 0)))
+        att = M.GlmMoeDsaAttention(cfg, layer).float().eval()
+        norm = M.GlmMoeDsaRMSNorm(H, eps=a["rms_eps"]).float().eval()
+        t = lambda k: torch.from_numpy(w[k])
+        with torch.no_grad():
+            norm.weight.copy_(t("input_ln"))
+            att.q_a_proj.weight.copy_(t("q_a_proj"))
+            att.q_a_layernorm.weight.copy_(t("q_a_ln"))
+            att.q_b_proj.weight.copy_(t("q_b_proj"))
+            att.kv_a_proj_with_mqa.weight.copy_(t("kv_a_proj"))
+            att.kv_a_layernorm.weight.copy_(t("kv_a_ln"))
+            att.kv_b_proj.weight.copy_(t("kv_b_proj"))
+            att.o_proj.weight.copy_(t("o_proj"))
+            if layer == 0:
+                att.indexer.wq_b.weight.copy_(t("idx_wq_b"))
+                att.indexer.wk.weight.copy_(t("idx_wk"))
+                att.indexer.k_norm.weight.copy_(t("idx_k_norm_w"))
+                att.indexer.k_norm.bias.copy_(t("idx_k_norm_b"))
+                att.indexer.weights_proj.weight.copy_(t("idx_weights_proj"))
+            hs = torch.from_numpy(np.stack([synth.hidden_state(H, ATT_SEED * 100 + layer, p) for p in range(S)]))
+            x = norm(hs.reshape(1, S, H))
+            cos, sin = rot(x, pos)
+            o, _, topk = att(x, (cos, sin), None, None, pos, prev_topk_indices=prev)
+        if layer == 0:
+            prev = topk
+            keep = np.zeros((S, S), bool)  # keep[q, k]: key k (causal, k <= q) selected for query q
+            for q in range(S):
+                for k in topk[0, q].numpy():
+                    if 0 <= k <= q:
+                        keep[q, k] = True
+            out["keep"] = keep
+        out[f"attn_out{layer}"] = o[0].numpy()
+    mw = synthdata.as_f32(synthdata.dense_mlp(H, a["dense_inter"], ATT_SEED, 0))
+    mlp = M.GlmMoeDsaMLP(cfg, intermediate_size=a["dense_inter"]).float().eval()
+    pn = M.GlmMoeDsaRMSNorm(H, eps=a["rms_eps"]).float().eval()
+    with torch.no_grad():
+        mlp.gate_proj.weight.copy_(torch.from_numpy(mw["gate"]))
+        mlp.up_proj.weight.copy_(torch.from_numpy(mw["up"]))
+        mlp.down_proj.weight.copy_(torch.from_numpy(mw["down"]))
+        pn.weight.copy_(torch.from_numpy(mw["post_ln"]))
+        hs = torch.from_numpy(np.stack([synth.hidden_state(H, ATT_SEED * 100 + 9, p) for p in range(4)]))
+        out["mlp_out"] = mlp(pn(hs)).numpy()
+    out["config"] = np.array(json.dumps(ATT))
+    out["seq"] = np.array(ATT_SEQ)
+    out["seed"] = np.array(ATT_SEED)
+    return out
+
+
 def main():
     with open(os.path.join(HERE, "mxfp4_hand_fixture.json"), "w") as f:
         json.dump(hand_fixture(), f, indent=1)
@@ -113,6 +191,7 @@ def main():
     arrs["config"] = np.array(json.dumps(SMALL))
     arrs["seeds"] = np.array(SMALL_SEEDS)
     np.savez_compressed(os.path.join(HERE, "moe_tf_small.npz"), **arrs)
+    np.savez_compressed(os.path.join(HERE, "attn_tf_small.npz"), **attn_small())
     print("wrote fixtures to", HERE)
 
 

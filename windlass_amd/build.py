@@ -10,7 +10,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libwindlass_moe.so")
 SOURCES = ["moe_decode.hip", "moe_batched.hip", "synth.hip", "native.hip", "noalloc.hip", "moe_host.cpp",
-           "expert_files.cpp", "safetensors.cpp", "loader.cpp"]
+           "expert_files.cpp", "safetensors.cpp", "loader.cpp", "attention.hip", "attn_host.cpp"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 # Packed-FP32 VALU forms are disabled on purpose: some of them have given
 # wrong results on this hardware without any error.

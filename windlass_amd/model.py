@@ -209,3 +209,40 @@ class FileModel(_Layers):
 
 def make_io(H):
     return hip.DeviceBuffer(4 * H), hip.DeviceBuffer(4 * H)
+
+
+class AttnModel:
+    """Decoder-layer attention (and dense MLPs) with synthetic weights
+    (synthdata.attention_layer / dense_mlp) uploaded once: `owners[l]` says
+    whether layer l has its own indexer; layers in `dense` get a dense MLP."""
+
+    def __init__(self, a, seed, n_layers, owners, dense=(), max_seq=4096):
+        self.a = dict(a)
+        self.cfg = moe.make_attn_config(hidden=a["hidden"], n_heads=a["n_heads"], q_lora_rank=a["q_lora_rank"],
+                                        kv_lora_rank=a["kv_lora_rank"], qk_nope=a["qk_nope"], qk_rope=a["qk_rope"],
+                                        v_head=a["v_head"], index_n_heads=a["index_n_heads"],
+                                        index_head_dim=a["index_head_dim"], index_topk=a["index_topk"],
+                                        dense_inter=a.get("dense_inter", 0), n_layers=n_layers, max_seq=max_seq,
+                                        rms_eps=a.get("rms_eps", 1e-5), rope_theta=a.get("rope_theta", 10000.0))
+        self.attn = moe.Attention(self.cfg)
+        self.weights, self.mlp, self.bufs = [], {}, []
+        for l in range(n_layers):
+            w = synthdata.attention_layer(a, seed, l, owner=owners[l])
+            self.weights.append(w)
+            ptrs = {}
+            for k, v in w.items():
+                b = hip.DeviceBuffer.from_array(v)
+                self.bufs.append(b)
+                ptrs[k] = b.ptr
+            self.attn.set_layer(l, ptrs)
+            if l in dense:
+                m = synthdata.dense_mlp(a["hidden"], a["dense_inter"], seed, l)
+                self.mlp[l] = m
+                bs = [hip.DeviceBuffer.from_array(m[k]) for k in ("post_ln", "gate", "up", "down")]
+                self.bufs += bs
+                self.attn.set_dense_mlp(l, *[b.ptr for b in bs])
+        hip.synchronize()
+
+    def close(self):
+        self.attn.close()
+        self.bufs = []

@@ -83,6 +83,25 @@ class StTensor(ctypes.Structure):
                 ("nbytes", ctypes.c_uint64), ("file_offset", ctypes.c_uint64), ("shard", ctypes.c_uint32)]
 
 
+class AttnConfig(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_uint32) for n in
+                ["hidden", "n_heads", "q_lora_rank", "kv_lora_rank", "qk_nope", "qk_rope", "v_head", "index_n_heads",
+                 "index_head_dim", "index_topk", "dense_inter", "n_layers", "max_seq"]] + \
+               [("rms_eps", ctypes.c_float), ("rope_theta", ctypes.c_float)]
+
+
+ATTN_WEIGHTS = ["input_ln", "q_a_proj", "q_a_ln", "q_b_proj", "kv_a_proj", "kv_a_ln", "kv_b_proj", "o_proj",
+                "idx_wq_b", "idx_wk", "idx_k_norm_w", "idx_k_norm_b", "idx_weights_proj"]
+
+
+class AttnWeights(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_void_p) for n in ATTN_WEIGHTS]
+
+
+class AttnTaps(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_void_p) for n in ["norm", "q_resid", "attn", "attn_out", "index_score", "keep"]]
+
+
 class Taps(ctypes.Structure):
     _fields_ = [(n, ctypes.c_void_p) for n in ["norm", "logits", "topk_idx", "topk_w", "mid", "shared"]]
 
@@ -147,6 +166,13 @@ def load():
         "wl_st_pack_layer": [vp, ctypes.POINTER(MoeConfig), u32, ctypes.c_char_p],
         "wl_load_layer": [vp, vp, u32, u32],
         "wl_load_experts": [vp, vp, u32, u32, ctypes.POINTER(u32), u32, u32, vp],
+        "wl_attn_create": [ctypes.POINTER(AttnConfig), ctypes.POINTER(vp)],
+        "wl_attn_set_layer": [vp, u32, ctypes.POINTER(AttnWeights)],
+        "wl_attn_set_dense_mlp": [vp, u32, vp, vp, vp, vp],
+        "wl_run_attention": [vp, u32, u32, vp, vp],
+        "wl_run_dense_mlp": [vp, u32, vp, vp],
+        "wl_run_layer": [vp, vp, u32, u32, u32, vp, vp],
+        "wl_attn_taps": [vp, ctypes.POINTER(AttnTaps)],
     }
     for name, args in sig.items():
         fn = getattr(lib, name)
@@ -158,6 +184,10 @@ def load():
     lib.wl_destroy.restype = None
     lib.wl_last_error.argtypes = [vp]
     lib.wl_last_error.restype = ctypes.c_char_p
+    lib.wl_attn_destroy.argtypes = [vp]
+    lib.wl_attn_destroy.restype = None
+    lib.wl_attn_last_error.argtypes = [vp]
+    lib.wl_attn_last_error.restype = ctypes.c_char_p
     lib.wl_st_close.argtypes = [vp]
     lib.wl_st_close.restype = None
     lib.wl_st_last_error.argtypes = [vp]
@@ -299,6 +329,64 @@ class SafeTensors:
     def close(self):
         if self.h:
             self.lib.wl_st_close(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def make_attn_config(hidden=6144, n_heads=64, q_lora_rank=2048, kv_lora_rank=512, qk_nope=192, qk_rope=64,
+                     v_head=256, index_n_heads=32, index_head_dim=128, index_topk=2048, dense_inter=12288,
+                     n_layers=1, max_seq=4096, rms_eps=1e-5, rope_theta=1e6):
+    return AttnConfig(hidden, n_heads, q_lora_rank, kv_lora_rank, qk_nope, qk_rope, v_head, index_n_heads,
+                      index_head_dim, index_topk, dense_inter, n_layers, max_seq, rms_eps, rope_theta)
+
+
+class Attention:
+    """One wl_attn: the attention (and dense MLP) side of decoder layers."""
+
+    def __init__(self, cfg):
+        self.lib = load()
+        self.cfg = cfg
+        h = ctypes.c_void_p()
+        rc = self.lib.wl_attn_create(ctypes.byref(cfg), ctypes.byref(h))
+        if rc != WL_OK:
+            raise WindlassError(rc, f"wl_attn_create: {self.lib.wl_attn_last_error(None).decode()}")
+        self.h = h.value
+
+    def _ck(self, rc, what):
+        if rc != WL_OK:
+            raise WindlassError(rc, f"{what}: {self.lib.wl_attn_last_error(self.h).decode()}")
+
+    def set_layer(self, layer, ptrs):
+        """ptrs: dict of ATTN_WEIGHTS names -> device pointers (idx_* absent on a shared layer)."""
+        w = AttnWeights(*[ptrs.get(n) for n in ATTN_WEIGHTS])
+        self._ck(self.lib.wl_attn_set_layer(self.h, layer, ctypes.byref(w)), "wl_attn_set_layer")
+
+    def set_dense_mlp(self, layer, post_ln, gate, up, down):
+        self._ck(self.lib.wl_attn_set_dense_mlp(self.h, layer, post_ln, gate, up, down), "wl_attn_set_dense_mlp")
+
+    def run_attention(self, layer, pos, d_hidden, stream=0):
+        self._ck(self.lib.wl_run_attention(self.h, layer, pos, d_hidden, stream), "wl_run_attention")
+
+    def run_dense_mlp(self, layer, d_hidden, stream=0):
+        self._ck(self.lib.wl_run_dense_mlp(self.h, layer, d_hidden, stream), "wl_run_dense_mlp")
+
+    def run_layer(self, moe_ctx, layer, moe_layer, pos, d_hidden, stream=0):
+        self._ck(self.lib.wl_run_layer(self.h, moe_ctx.h if moe_ctx else None, layer, moe_layer, pos, d_hidden,
+                                       stream), "wl_run_layer")
+
+    def taps(self):
+        t = AttnTaps()
+        self._ck(self.lib.wl_attn_taps(self.h, ctypes.byref(t)), "wl_attn_taps")
+        return {n: getattr(t, n) for n, _ in AttnTaps._fields_}
+
+    def close(self):
+        if self.h:
+            self.lib.wl_attn_destroy(self.h)
             self.h = None
 
     def __del__(self):

@@ -11,6 +11,10 @@ config says bf16:
   hidden state [H] bf16 ~ N(0, 1), widened to f32   tag 6 (layer slot = step)
   post-attention norm weight [H] bf16            tag 7
 
+Attention and dense-MLP weights of a decoder layer (attention_layer,
+dense_mlp): bf16 (the indexer's weights_proj f32) ~ N(0, 1/fan_in) so that
+projections keep unit scale, norm weights 1 + N(0, 0.1), tags 20-34.
+
 The oracle restates the same recipe independently (oracle/synth.py);
 tests/test_oracle.py checks that both give identical arrays.
 """
@@ -67,3 +71,53 @@ def zipf_bias_offset(E, seed, s=1.1, amplitude=0.05):
     off = np.empty(E, dtype=np.float32)
     off[perm] = (np.float32(amplitude) * (np.arange(1, E + 1, dtype=np.float64) ** -s)).astype(np.float32)
     return off
+
+
+def _w_bf16(seed, layer, tag, shape, fan_in, scale=1.0):
+    return normal_bf16(seed, layer, tag, shape, scale / np.sqrt(fan_in))
+
+
+def _norm_w(seed, layer, tag, n):
+    x = np.float32(1.0) + _rng(seed, layer, tag).standard_normal(size=n, dtype=np.float32) * np.float32(0.1)
+    return f32_to_bf16(x)
+
+
+def attention_layer(a, seed, layer, owner=True):
+    """Synthetic weights of one MLA attention block with the DSA indexer
+    (owner: the layer has its own indexer). `a` holds hidden, n_heads,
+    q_lora_rank, kv_lora_rank, qk_nope, qk_rope, v_head, index_n_heads,
+    index_head_dim. bf16 arrays are uint16 bits in the checkpoint's
+    [out, in] row-major layout."""
+    H, HN, Q, L = a["hidden"], a["n_heads"], a["q_lora_rank"], a["kv_lora_rank"]
+    NP, RP, VD = a["qk_nope"], a["qk_rope"], a["v_head"]
+    IH, ID = a["index_n_heads"], a["index_head_dim"]
+    w = {"input_ln": _norm_w(seed, layer, 20, H),
+         "q_a_proj": _w_bf16(seed, layer, 21, (Q, H), H),
+         "q_a_ln": _norm_w(seed, layer, 22, Q),
+         "q_b_proj": _w_bf16(seed, layer, 23, (HN * (NP + RP), Q), Q),
+         "kv_a_proj": _w_bf16(seed, layer, 24, (L + RP, H), H),
+         "kv_a_ln": _norm_w(seed, layer, 25, L),
+         "kv_b_proj": _w_bf16(seed, layer, 26, (HN * (NP + VD), L), L),
+         "o_proj": _w_bf16(seed, layer, 27, (H, HN * VD), HN * VD, 0.5)}
+    if owner:
+        w.update({"idx_wq_b": _w_bf16(seed, layer, 28, (IH * ID, Q), Q),
+                  "idx_wk": _w_bf16(seed, layer, 29, (ID, H), H),
+                  "idx_k_norm_w": _norm_w(seed, layer, 30, ID),
+                  "idx_k_norm_b": normal_bf16(seed, layer, 31, (ID,), 0.1),
+                  "idx_weights_proj": (_rng(seed, layer, 32).standard_normal(size=(IH, H), dtype=np.float32)
+                                       * np.float32(1.0 / np.sqrt(H))).astype(np.float32)})
+    return w
+
+
+def dense_mlp(H, DI, seed, layer):
+    """Synthetic weights of a dense SwiGLU MLP layer: post_ln [H], gate / up
+    [DI, H], down [H, DI] (bf16 bits)."""
+    return {"post_ln": _norm_w(seed, layer, 33, H),
+            "gate": _w_bf16(seed, layer, 34, (DI, H), H),
+            "up": _w_bf16(seed, layer, 35, (DI, H), H),
+            "down": _w_bf16(seed, layer, 36, (H, DI), DI)}
+
+
+def as_f32(w):
+    """The same weights widened to f32 (bf16 bits -> values), for the oracle."""
+    return {k: (bf16_to_f32(v) if v.dtype == np.uint16 else v) for k, v in w.items()}
