@@ -24,6 +24,14 @@ chain (step time / 24) and tokens_per_s is reported beside it.
 offset; `value` is microseconds per layer call (all T tokens), with
 tokens_per_s and the achieved bytes of the experts actually used.
 
+--workload attention measures the caller side of a decoder layer (the
+run_layer row): MLA attention with the DSA indexer at the GLM shape (hidden
+6144, 64 heads, q_lora 2048, kv_lora 512, index_topk 2048) after --context
+cached positions, over 4 rotating layers (two owning the indexer, two
+sharing it); a step is one token through the 4 layers, `value` is
+microseconds per attention layer; the dense MLP (intermediate 12288) is
+timed beside it.
+
 --workload cache measures configs[4]: 75 MoE layers whose 19,200 experts sit
 behind the HBM expert cache (3,094 slots, 62 GB) and are copied from pinned
 host memory on a miss; router bias shaped by Zipf(1.1) popularity; a step is
@@ -177,6 +185,154 @@ def cpu_baseline(c, seed, n_layers_sample, threads):
     return float(np.median(times)) * 1e6, len(times)
 
 
+GLM_ATTN = dict(hidden=6144, n_heads=64, q_lora_rank=2048, kv_lora_rank=512, qk_nope=192, qk_rope=64, v_head=256,
+                index_n_heads=32, index_head_dim=128, index_topk=2048, dense_inter=12288, rms_eps=1e-5,
+                rope_theta=1e6)
+
+
+def attention_bytes(a, T, owner):
+    """Bytes one decode attention layer must move at T cached keys: its bf16
+    projections (the indexer's on owning layers, weights_proj f32), the KV
+    cache rows (kv_c | k_rot f32) and, on owning layers, the indexer keys."""
+    H, HN, Q, L = a["hidden"], a["n_heads"], a["q_lora_rank"], a["kv_lora_rank"]
+    NP, RP, VD, IH, ID = a["qk_nope"], a["qk_rope"], a["v_head"], a["index_n_heads"], a["index_head_dim"]
+    w = 2 * (Q * H + HN * (NP + RP) * Q + (L + RP) * H + HN * (NP + VD) * L + H * HN * VD) + 2 * H
+    kv = 4 * T * (L + RP)
+    if owner:
+        w += 2 * (IH * ID * Q + ID * H) + 4 * IH * H
+        kv += 4 * T * ID
+    return w + kv + 2 * 4 * H
+
+
+def cpu_baseline_attention(a, T, threads, n_sample=3):
+    """The numpy oracle's step (oracle/attention.py attn_block: projections,
+    indexer, attention over T cached keys, o_proj) on one owning layer with
+    T - 1 rows of random cache; median of n_sample positions after one
+    warm-up."""
+    from threadpoolctl import threadpool_limits
+
+    from oracle import attention as A
+    from windlass_amd import synthdata
+    W = synthdata.as_f32(synthdata.attention_layer(a, 1, 0, owner=True))
+    rng = np.random.default_rng(0)
+    HN, DH, VD, ID = a["n_heads"], a["qk_nope"] + a["qk_rope"], a["v_head"], a["index_head_dim"]
+    cache = A.LayerCache()
+    cache.k = list(rng.standard_normal((T - 1, HN, DH), dtype=np.float32))
+    cache.v = list(rng.standard_normal((T - 1, HN, VD), dtype=np.float32))
+    cache.ik = list(rng.standard_normal((T - 1, ID), dtype=np.float32))
+    cos, sin = A.rope_tables(T + n_sample + 1, a["qk_rope"], a["rope_theta"])
+    times = []
+    with threadpool_limits(limits=threads):
+        for i in range(n_sample + 1):
+            h = synthdata.hidden_state(a["hidden"], 9000 + i)
+            t0 = time.perf_counter()
+            A.attn_block(h, W, a, T - 1, cos, sin, cache, True, A.IndexShare())
+            if i > 0:
+                times.append(time.perf_counter() - t0)
+            for lst in (cache.k, cache.v, cache.ik):
+                lst.pop()
+    return float(np.median(times)) * 1e6, len(times)
+
+
+def bench_attention(args):
+    from windlass_amd import hip
+    from windlass_amd.model import AttnModel
+    a = dict(GLM_ATTN)
+    H = a["hidden"]
+    if "--steps" not in sys.argv:
+        args.steps = 200
+    if "--warmup" not in sys.argv:
+        args.warmup = 10
+    n_l = 4
+    owners = [True, False, True, False]
+    t_build = time.time()
+    am = AttnModel(a, args.seed, n_l, owners=owners, dense=[0, 1], max_seq=args.context + args.warmup + args.steps + 1)
+    n_h = 64
+    d_hs = hip.DeviceBuffer.from_array(np.stack([synthdata_hidden(H, 5000 + i) for i in range(n_h)]))
+    d_h = hip.DeviceBuffer(4 * H)
+    stream = hip.Stream()
+    # fill the KV caches: positions 0 .. context-1 through every layer
+    for pos in range(args.context):
+        hip.copy_d2d(d_h.ptr, d_hs.ptr + 4 * H * (pos % n_h), 4 * H, stream.handle)
+        for l in range(n_l):
+            am.attn.run_attention(l, pos, d_h.ptr, stream.handle)
+    stream.synchronize()
+    build_s = time.time() - t_build
+
+    def token(pos):
+        hip.copy_d2d(d_h.ptr, d_hs.ptr + 4 * H * (pos % n_h), 4 * H, stream.handle)
+        for l in range(n_l):
+            am.attn.run_attention(l, pos, d_h.ptr, stream.handle)
+
+    pos = args.context
+    for i in range(args.warmup):
+        token(pos)
+        pos += 1
+    stream.synchronize()
+    e0, e1 = hip.Event(), hip.Event()
+    e0.record(stream)
+    for i in range(args.steps):
+        token(pos)
+        pos += 1
+    e1.record(stream)
+    e1.synchronize()
+    us_layer = e0.elapsed_ms(e1) * 1e3 / args.steps / n_l
+    T = pos - args.steps // 2  # mean cached keys of the timed tokens
+    nbytes = (attention_bytes(a, T, True) + attention_bytes(a, T, False)) / 2
+    achieved = nbytes / (us_layer * 1e-6) / 1e9
+    # dense MLP beside it (two rotating layers)
+    for i in range(args.warmup):
+        am.attn.run_dense_mlp(i % 2, d_h.ptr, stream.handle)
+    e0.record(stream)
+    for i in range(args.steps):
+        am.attn.run_dense_mlp(i % 2, d_h.ptr, stream.handle)
+    e1.record(stream)
+    e1.synchronize()
+    us_mlp = e0.elapsed_ms(e1) * 1e3 / args.steps
+    mlp_bytes = 3 * a["dense_inter"] * H * 2 + H * 2 + 2 * 4 * H
+    cpu = None
+    if args.cpu_sample > 0:
+        phys, logical = host_cores()
+        ncores = min(phys, 16)
+        us_all, n_all = cpu_baseline_attention(a, T, ncores)
+        cpu = {"value": round(us_all, 1), "unit": "us/layer", "cores": ncores, "kind": "port",
+               "sample": f"numpy oracle attn_block (projections, indexer, attention over {T} keys, o_proj) on one "
+                         f"indexer-owning layer, median of {n_all} positions after one warm-up",
+               "host_physical_cores": phys, "host_logical_cpus": logical, "gpu_speedup": round(us_all / us_layer, 1)}
+    line = {
+        "metric": "us_per_attention_layer",
+        "value": round(us_layer, 3),
+        "unit": "us/layer",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(us_layer * n_l / 1e3, 6),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16 weights, f32 activations, KV cache and accumulation",
+        "data": "synthetic",
+        "config": {"workload": f"run_layer attention side: MLA + DSA indexer, decode at {args.context}+ cached "
+                               f"positions, 4 rotating layers (2 indexer-owning, 2 sharing)", **a},
+        "achieved_GBps": round(achieved, 1),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
+                     "frac": round(achieved / PEAK_HBM_GBPS, 4), "traffic": None,
+                     "algorithmic_bytes": int(nbytes), "kernel": "whole attention layer (gemv_kernel dominates)"},
+        "dense_mlp": {"us_per_layer": round(us_mlp, 3), "algorithmic_bytes": mlp_bytes,
+                      "achieved_GBps": round(mlp_bytes / (us_mlp * 1e-6) / 1e9, 1),
+                      "frac": round(mlp_bytes / (us_mlp * 1e-6) / 1e9 / PEAK_HBM_GBPS, 4)},
+        "cpu_baseline": cpu,
+        "build_s": round(build_s, 1),
+    }
+    am.close()
+    print(json.dumps(line), flush=True)
+
+
+def synthdata_hidden(H, seed):
+    from windlass_amd import synthdata
+    return synthdata.hidden_state(H, seed)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -184,7 +340,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--layers", type=int, default=8, help="distinct resident layer copies to rotate over")
     ap.add_argument("--sched", choices=["fused", "phased"], default="fused")
-    ap.add_argument("--workload", choices=["layer", "chain", "batched", "cache"], default="layer",
+    ap.add_argument("--workload", choices=["layer", "chain", "batched", "cache", "attention"], default="layer",
                     help="layer: config 1 (default); chain: config 2, 24 layers per step; "
                          "batched: config 3, --tokens positions per step; cache: config 4, 75 cache-backed layers per step")
     ap.add_argument("--tokens", type=int, default=256, help="batched workload: positions per layer call")
@@ -202,6 +358,8 @@ def main():
                          "tokens (popularity pinning)")
     ap.add_argument("--zipf-amp", type=float, default=0.25,
                     help="cache workload: bias offset of the most popular expert (rank r gets amp * r^-1.1)")
+    ap.add_argument("--context", type=int, default=4096,
+                    help="attention workload: cached positions before the timed tokens")
     ap.add_argument("--seed", type=int, default=1)
     ap.add_argument("--cpu-sample", type=int, default=6,
                     help="layers timed for the CPU baseline after one warm-up, median reported (0: skip)")
@@ -223,6 +381,8 @@ def main():
     if hip.device_count() < 1:
         print("bench.py: no GPU visible", file=sys.stderr)
         sys.exit(1)
+    if args.workload == "attention":
+        return bench_attention(args)
 
     c = dict(GLM)
     H = c["hidden"]

@@ -573,6 +573,12 @@ wl_status   wl_attn_taps(wl_attn* a, wl_attn_taps_out* out);
 wl_status wl_dequant_matvec_mxfp4(const uint8_t* d_W, const uint8_t* d_S, const float* d_x, float* d_y,
                                   uint32_t N, uint32_t K, void* stream);
 
+/* y[N] = W . x for bf16 W [N, K] row-major and f32 x [K] (K % 8 == 0,
+ * K <= 16384, 16-byte aligned pointers): the GEMV kernel of the attention
+ * and dense-MLP projections. Replaces launch_matvec_bf16
+ * (src/glm_primitives.cuh:87-116). */
+wl_status wl_matvec_bf16(const uint16_t* d_W, const float* d_x, float* d_y, uint32_t N, uint32_t K, void* stream);
+
 /* One routed expert applied to one position, without the routing weight:
  * y = down(silu(gate x) * up x), d_block in wl_expert_layout order, x f32 [H],
  * y f32 [H] and, if d_y_bf16 is not NULL, its bf16 (round-to-nearest-even)

@@ -197,3 +197,21 @@ def test_errors(gpu):
     am.close()
     with pytest.raises(moe.WindlassError):
         moe.Attention(moe.make_attn_config(n_heads=24))
+
+
+@pytest.mark.parametrize("N,K", [(48, 256), (2048, 6144), (6144, 16384), (100, 24), (16384, 2048)])
+def test_matvec_bf16(gpu, N, K):
+    """wl_matvec_bf16 against an fp64 product of the same bf16 weights and f32
+    input, within 1e-5 term-relative (the reference's matvec test bar,
+    src/test_glm_mxfp4.cu:186-191, applied to bf16)."""
+    rng = np.random.default_rng(N + K)
+    W = synthdata.f32_to_bf16(rng.standard_normal((N, K), dtype=np.float32))
+    x = rng.standard_normal(K).astype(np.float32)
+    dW, dx, dy = H_.DeviceBuffer.from_array(W), H_.DeviceBuffer.from_array(x), H_.DeviceBuffer(4 * N)
+    moe.matvec_bf16(dW.ptr, dx.ptr, dy.ptr, N, K)
+    H_.synchronize()
+    y = dy.download(np.float32)
+    Wf = synthdata.bf16_to_f32(W).astype(np.float64)
+    ref = Wf @ x.astype(np.float64)
+    scale = np.abs(Wf) @ np.abs(x.astype(np.float64))
+    assert np.max(np.abs(y - ref) / scale) < 1e-5

@@ -33,7 +33,10 @@ struct GemvJob {
     uint32_t rows_wg;   // rows per work-group: kGemvRows x (256 >> tpr_log2)
 };
 constexpr int kMaxJobs = 4;
-constexpr uint32_t kGemvRows = 8;    // rows per thread group
+#ifndef WL_GEMV_ROWS
+#define WL_GEMV_ROWS 4
+#endif
+constexpr uint32_t kGemvRows = WL_GEMV_ROWS;  // rows per thread group
 constexpr uint32_t kGemvThreads = 256;
 struct GemvLaunch {
     GemvJob job[kMaxJobs];

@@ -27,6 +27,10 @@ namespace attn {
 namespace {
 
 constexpr int kMaxIt = 8;  // chunk iterations per thread: K <= 8 x 8 x 256 = 16384
+#ifndef WL_GEMV_PRE
+#define WL_GEMV_PRE 3
+#endif
+constexpr int kPre = WL_GEMV_PRE;  // chunk iterations whose weight loads are issued before the input transform
 
 WL_DEV float silu(float x) { return x / (1.0f + expf(-x)); }
 
@@ -40,6 +44,26 @@ WL_DEV void bf8(u32x4 v, float* o) {
 }
 
 WL_DEV u32x4 ld16_nt(const void* p) { return __builtin_nontemporal_load((const u32x4*)p); }
+
+// Walks the flat indices i = t0, t0 + step, ... < rows x cols of a row-major
+// grid as (row, col) pairs without a division per element (one at the start).
+struct Walk2 {
+    uint32_t r, c, dr, dc, cols;
+    __device__ __forceinline__ Walk2(uint32_t t0, uint32_t step, uint32_t cols_) : cols(cols_) {
+        r = t0 / cols;
+        c = t0 - r * cols;
+        dr = step / cols;
+        dc = step - dr * cols;
+    }
+    __device__ __forceinline__ void next() {
+        r += dr;
+        c += dc;
+        if (c >= cols) {
+            c -= cols;
+            r++;
+        }
+    }
+};
 
 // Sum over the `tpr` lanes of a thread group (groups aligned to tpr lanes; for
 // tpr > 64 through LDS `red`, kGemvThreads / 64 entries per value, index v).
@@ -80,8 +104,27 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(GemvLaunch L) {
     const uint32_t r0 = (b - j.wg0) * j.rows_wg + grp * kGemvRows;
     const uint32_t K = j.K, nch = K >> 3;
     const uint32_t nit = (nch + tpr - 1) >> tl2;
-    // the group's x (rows of one group share it: G % kGemvRows == 0)
-    const float* x = j.x + (size_t)((r0 < j.N ? r0 : 0) / j.G) * j.XS;
+    // the group's x and W rows (rows of one thread group share a group: G % kGemvRows == 0)
+    const uint32_t rg = j.GS ? (r0 < j.N ? r0 : 0) / j.G : 0;
+    const float* x = j.x + (size_t)rg * j.XS;
+    const uint32_t wr0 = j.GS ? rg * j.GS + j.OFF + (r0 - rg * j.G) : r0;
+    size_t roff[kGemvRows];
+#pragma unroll
+    for (int r = 0; r < (int)kGemvRows; r++) roff[r] = (size_t)(wr0 + r) * K;
+    // the first chunks' weights are requested before the input is read and
+    // normalised, so the work-group's first memory latency overlaps that work
+    u32x4 pre[kPre][kGemvRows];
+    if (!j.f32w) {
+        const uint16_t* W = (const uint16_t*)j.W;
+#pragma unroll
+        for (int i = 0; i < kPre; i++) {
+            const uint32_t c = lt + ((uint32_t)i << tl2);
+            if (i < (int)nit && c < nch)
+#pragma unroll
+                for (int r = 0; r < (int)kGemvRows; r++)
+                    if (r0 + r < j.N) pre[i][r] = ld16_nt(W + roff[r] + 8 * c);
+        }
+    }
     float xv[kMaxIt][8];
     float ss[1] = {0.f};
 #pragma unroll
@@ -134,14 +177,8 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(GemvLaunch L) {
         }
     }
     float acc[kGemvRows];
-    size_t roff[kGemvRows];
 #pragma unroll
-    for (int r = 0; r < (int)kGemvRows; r++) {
-        acc[r] = 0.f;
-        const uint32_t row = r0 + r;
-        const uint32_t wr = (row / j.G) * j.GS + j.OFF + row % j.G;
-        roff[r] = (size_t)wr * K;
-    }
+    for (int r = 0; r < (int)kGemvRows; r++) acc[r] = 0.f;
     if (j.f32w) {
         const float* W = (const float*)j.W;
 #pragma unroll
@@ -170,7 +207,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(GemvLaunch L) {
                 u32x4 wv[kGemvRows];
 #pragma unroll
                 for (int r = 0; r < (int)kGemvRows; r++)
-                    if (r0 + r < j.N) wv[r] = ld16_nt(W + roff[r] + 8 * c);
+                    if (r0 + r < j.N) wv[r] = i < kPre ? pre[i < kPre ? i : 0][r] : ld16_nt(W + roff[r] + 8 * c);
 #pragma unroll
                 for (int r = 0; r < (int)kGemvRows; r++) {
                     if (r0 + r < j.N) {
@@ -300,7 +337,21 @@ __global__ __launch_bounds__(256) void attn_absorb_kernel(Shape s, AttnPtrs p, u
     if (rlane < rl) {
         const float* qh = p.q + (size_t)h * DH;
         const uint16_t* wb = p.kv_b + (size_t)h * (s.NP + s.VD) * s.L + c0 + 8 * cl;
-        for (uint32_t d = rlane; d < s.NP; d += rl) {
+        uint32_t d = rlane;
+        for (; d + 3 * rl < s.NP; d += 4 * rl) {  // four rows' loads in flight
+            u32x4 v[4];
+#pragma unroll
+            for (int u = 0; u < 4; u++) v[u] = ld16_nt(wb + (size_t)(d + u * rl) * s.L);
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                float w[8];
+                bf8(v[u], w);
+                const float qv = qh[d + u * rl];
+#pragma unroll
+                for (int e = 0; e < 8; e++) acc[e] += qv * w[e];
+            }
+        }
+        for (; d < s.NP; d += rl) {
             float w[8];
             bf8(ld16_nt(wb + (size_t)d * s.L), w);
             const float qv = qh[d];
@@ -318,32 +369,49 @@ __global__ __launch_bounds__(256) void attn_absorb_kernel(Shape s, AttnPtrs p, u
     }
 }
 
-// isc[t] = sum_h w[h] * relu(q[h] . k[t] * ID^-0.5): 32 keys per work-group,
-// 8 threads per key (each ID/8 dims, summed by shuffles), heads in order.
+// isc[t] = sum_h w[h] * relu(q[h] . k[t] * ID^-0.5): 16 keys per
+// work-group; thread (key, head part): 2 consecutive heads of one key over
+// all ID dims from LDS, then the head parts summed by shuffles in head order.
+constexpr uint32_t kIdxKeys = 16;
+
 __global__ __launch_bounds__(256) void index_score_kernel(Shape s, AttnPtrs p, uint32_t T) {
-    extern __shared__ float lq[];  // [IH][ID] then [IH]
-    const uint32_t tid = threadIdx.x;
-    for (uint32_t i = tid; i < s.IH * s.ID; i += 256) lq[i] = p.iqr[i];
-    for (uint32_t i = tid; i < s.IH; i += 256) lq[s.IH * s.ID + i] = p.iw[i];
+    extern __shared__ float lq[];  // q [IH][ID + 4] | w [IH] | k [kIdxKeys][ID + 4]
+    const uint32_t tid = threadIdx.x, QS = s.ID + 4;
+    float* lw = lq + s.IH * QS;
+    float* lk = lw + s.IH;
+    const uint32_t k0 = blockIdx.x * kIdxKeys;
+    const uint32_t nk = (T - k0) < kIdxKeys ? (T - k0) : kIdxKeys;
+    for (Walk2 w(tid, 256, s.ID / 4); w.r < s.IH; w.next())
+        *(f32x4*)(lq + w.r * QS + 4 * w.c) = *(const f32x4*)(p.iqr + (size_t)w.r * s.ID + 4 * w.c);
+    for (uint32_t i = tid; i < s.IH; i += 256) lw[i] = p.iw[i];
+    for (Walk2 w(tid, 256, s.ID / 4); w.r < nk; w.next())
+        *(f32x4*)(lk + w.r * QS + 4 * w.c) = *(const f32x4*)(p.idx_k + (size_t)(k0 + w.r) * s.ID + 4 * w.c);
     __syncthreads();
-    const uint32_t key = blockIdx.x * 32 + (tid >> 3), part = tid & 7, dp = s.ID / 8;
-    const bool live = key < T;
-    float k[32];
-#pragma unroll
-    for (uint32_t e = 0; e < 32; e++) k[e] = (live && e < dp) ? p.idx_k[(size_t)key * s.ID + part * dp + e] : 0.f;
+    const uint32_t key = tid >> 4, hp = tid & 15;
+    const uint32_t hpt = (s.IH + 15) / 16;  // heads per thread (2 at IH = 32)
     float sc = 0.f;
-    for (uint32_t h = 0; h < s.IH; h++) {
-        const float* qh = lq + (size_t)h * s.ID + part * dp;
-        float d = 0.f;
-#pragma unroll
-        for (uint32_t e = 0; e < 32; e++)
-            if (e < dp) d += qh[e] * k[e];
-        d += __shfl_xor(d, 1, 64);
-        d += __shfl_xor(d, 2, 64);
-        d += __shfl_xor(d, 4, 64);
-        sc += lq[s.IH * s.ID + h] * fmaxf(d * p.ix_scale, 0.f);
+    if (key < nk) {
+        for (uint32_t j = 0; j < hpt; j++) {
+            const uint32_t h = hp * hpt + j;
+            if (h >= s.IH) break;
+            const float* q = lq + h * QS;
+            const float* k = lk + key * QS;
+            float d = 0.f;
+            for (uint32_t c = 0; c < s.ID; c += 4) {
+                const f32x4 x = *(const f32x4*)(q + c), y = *(const f32x4*)(k + c);
+                d += x[0] * y[0];
+                d += x[1] * y[1];
+                d += x[2] * y[2];
+                d += x[3] * y[3];
+            }
+            sc += lw[h] * fmaxf(d * p.ix_scale, 0.f);
+        }
     }
-    if (live && part == 0) p.isc[key] = sc;
+    sc += __shfl_xor(sc, 1, 64);
+    sc += __shfl_xor(sc, 2, 64);
+    sc += __shfl_xor(sc, 4, 64);
+    sc += __shfl_xor(sc, 8, 64);
+    if (key < nk && hp == 0) p.isc[k0 + key] = sc;
 }
 
 // Order-preserving key of an f32 (larger float -> larger key).
@@ -357,7 +425,7 @@ WL_DEV uint32_t okey(float f) {
 // TOPK-th largest key (4 passes of 8 bits), then the marking.
 __global__ __launch_bounds__(1024) void index_topk_kernel(const float* isc, uint8_t* keep, uint32_t T, uint32_t K) {
     __shared__ uint32_t hist[256];
-    __shared__ uint32_t cnt[1024];
+    __shared__ uint32_t cnt[16];
     __shared__ uint32_t sh_prefix, sh_kk;
     const uint32_t tid = threadIdx.x;
     if (T <= K) {
@@ -373,15 +441,25 @@ __global__ __launch_bounds__(1024) void index_topk_kernel(const float* isc, uint
             if ((u & mask) == prefix) atomicAdd(&hist[(u >> shift) & 255u], 1u);
         }
         __syncthreads();
-        if (tid == 0) {
-            uint32_t cum = 0;
-            int d = 255;
-            for (; d > 0; d--) {
-                if (cum + hist[d] >= kk) break;
-                cum += hist[d];
+        if (tid < 64) {
+            // the digit d with (count above d) < kk <= (count above d) + hist[d]:
+            // lane l holds bins 4l .. 4l + 3; counts above a lane by a suffix scan
+            const uint32_t b0 = hist[4 * tid], b1 = hist[4 * tid + 1], b2 = hist[4 * tid + 2], b3 = hist[4 * tid + 3];
+            const uint32_t own = b0 + b1 + b2 + b3;
+            uint32_t inc = own;  // sum over lanes >= tid
+            for (int o = 1; o < 64; o <<= 1) {
+                const uint32_t v = __shfl_down(inc, o, 64);
+                if (tid + o < 64) inc += v;
             }
-            sh_prefix = prefix | ((uint32_t)d << shift);
-            sh_kk = kk - cum;
+            uint32_t above = inc - own;
+            const uint32_t bins[4] = {b0, b1, b2, b3};
+            for (int b = 3; b >= 0; b--) {
+                if (above < kk && kk <= above + bins[b]) {
+                    sh_prefix = prefix | ((4 * tid + b) << shift);
+                    sh_kk = kk - above;
+                }
+                above += bins[b];
+            }
         }
         __syncthreads();
         prefix = sh_prefix;
@@ -394,10 +472,16 @@ __global__ __launch_bounds__(1024) void index_topk_kernel(const float* isc, uint
     const uint32_t per = (T + 1023) / 1024, t0 = tid * per, t1 = (t0 + per < T) ? t0 + per : T;
     uint32_t eq = 0;
     for (uint32_t t = t0; t < t1; t++) eq += okey(isc[t]) == prefix;
-    cnt[tid] = eq;
+    // exclusive prefix of eq over the threads: a scan in each wave, then the wave totals
+    uint32_t inc = eq;
+    for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t v = __shfl_up(inc, o, 64);
+        if ((tid & 63) >= (uint32_t)o) inc += v;
+    }
+    if ((tid & 63) == 63) cnt[tid >> 6] = inc;
     __syncthreads();
-    uint32_t before = 0;
-    for (uint32_t i = 0; i < tid; i++) before += cnt[i];
+    uint32_t before = inc - eq;
+    for (uint32_t w = 0; w < (tid >> 6); w++) before += cnt[w];
     for (uint32_t t = t0; t < t1; t++) {
         const uint32_t u = okey(isc[t]);
         uint8_t k = u > prefix;
@@ -409,77 +493,133 @@ __global__ __launch_bounds__(1024) void index_topk_kernel(const float* isc, uint
     }
 }
 
-// Attention over keys [s kps, min(T, (s + 1) kps)) for heads [hg HG, hg HG +
-// HG): 32 keys at a time staged in LDS (kv_c | k_rot per row), scores for all
-// heads, an online softmax, and the unnormalised context; partial max, sum
-// and context go to the split's slots.
+// Attention over keys [s kps, min(T, (s + 1) kps)) for heads [hg 16,
+// hg 16 + 16) (all heads when fewer): 32 keys at a time staged in LDS
+// (kv_c | k_rot per row). Scores: thread = (4 heads x 4 keys tile, one of 8
+// column parts), the parts summed by shuffles. Online softmax per head.
+// Context: thread = (4 heads x 8 columns) over the chunk's keys. Partial
+// max, sum and unnormalised context go to the split's slots.
 constexpr uint32_t kHG = 16;
 constexpr uint32_t kKeys = 32;
+constexpr uint32_t kSplitThreads = 512;  // two waves per SIMD hide the LDS latency of the tiles
 
-__global__ __launch_bounds__(256) void attn_split_kernel(Shape s, AttnPtrs p, uint32_t T) {
+__global__ __launch_bounds__(kSplitThreads) void attn_split_kernel(Shape s, AttnPtrs p, uint32_t T) {
     extern __shared__ float lds[];
     const uint32_t tid = threadIdx.x;
     const uint32_t HG = s.HN < kHG ? s.HN : kHG;
     const uint32_t NHG = s.HN / HG;
     const uint32_t hg = blockIdx.x % NHG, sp = blockIdx.x / NHG;
-    const uint32_t L = s.L, RP = s.RP, KS = L + RP + 4;
-    float* qa = lds;                      // [HG][L + RP]: q_abs | q_rope
-    float* kv = qa + HG * (L + RP);       // [kKeys][KS]
-    float* ps = kv + kKeys * KS;          // [HG][kKeys]
-    float* al = ps + HG * kKeys;          // [HG] rescale of this step
-    float* mx = al + HG;                  // [HG] running max
-    float* sm = mx + HG;                  // [HG] running sum
-    for (uint32_t i = tid; i < HG * L; i += 256) qa[(i / L) * (L + RP) + i % L] = p.q_abs[(size_t)(hg * HG) * L + i];
-    for (uint32_t i = tid; i < HG * RP; i += 256) qa[(i / RP) * (L + RP) + L + i % RP] = p.q_rope[(size_t)(hg * HG) * RP + i];
-    if (tid < HG) {
+    const uint32_t L = s.L, RP = s.RP, W = L + RP, KS = W + 4;
+    float* qa = lds;                  // [kHG][KS]: q_abs | q_rope (rows >= HG zero)
+    float* kv = qa + kHG * KS;        // [kKeys][KS]
+    float* ps = kv + kKeys * KS;      // [kKeys][kHG] scores, then probabilities
+    float* al = ps + kKeys * kHG;     // [kHG] rescale of this chunk
+    float* mx = al + kHG;             // [kHG] running max
+    float* sm = mx + kHG;             // [kHG] running sum
+    for (Walk2 w(tid, kSplitThreads, W / 4); w.r < kHG; w.next()) {
+        const uint32_t h = w.r, c = 4 * w.c;
+        f32x4 v = {0.f, 0.f, 0.f, 0.f};
+        if (h < HG)
+            v = c < L ? *(const f32x4*)(p.q_abs + (size_t)(hg * HG + h) * L + c)
+                      : *(const f32x4*)(p.q_rope + (size_t)(hg * HG + h) * RP + (c - L));
+        *(f32x4*)(qa + h * KS + c) = v;
+    }
+    if (tid < kHG) {
         mx[tid] = -INFINITY;
         sm[tid] = 0.f;
     }
-    // context accumulators: thread -> 8 columns x up to 4 heads
-    const uint32_t tph = L / 8, rp = 256 / tph;  // threads per head row, head rows per pass
-    const uint32_t cc = (tid % tph) * 8, hr = tid / tph;
-    float acc[4][8];
+    // score tile of this thread: 4 heads x 4 keys, one of 16 column parts
+    const uint32_t part = tid & 15, tile = tid >> 4;
+    const uint32_t th = (tile & 3) * 4, tk = (tile >> 2) * 4;
+    const uint32_t nch = W / 4;  // float4 columns
+    // context tile of this thread: 4 heads x 4 columns
+    const uint32_t ncg = L / 4;  // column groups
+    const uint32_t cg = tid % ncg, chg = tid / ncg;  // chg < 4: heads 4 chg .. 4 chg + 3
+    const bool cact = chg < 4;
+    const uint32_t cc = cg * 4;
+    float acc[4][4];
 #pragma unroll
     for (int a = 0; a < 4; a++)
 #pragma unroll
-        for (int e = 0; e < 8; e++) acc[a][e] = 0.f;
+        for (int e = 0; e < 4; e++) acc[a][e] = 0.f;
     const uint32_t k0 = sp * p.kps, k1 = (k0 + p.kps < T) ? k0 + p.kps : T;
+    // the chunk's rows are read into registers one chunk ahead (each thread
+    // its kPf float4 of the 32 x W/4 grid), so their latency overlaps the
+    // previous chunk's compute
+    constexpr int kPf = 12;  // (kKeys x W/4) / kSplitThreads <= 12: W <= 768
+    f32x4 pf[kPf];
+    auto fetch = [&](uint32_t kb) {
+        const uint32_t nk = (k1 - kb) < kKeys ? (k1 - kb) : kKeys;
+        Walk2 w(tid, kSplitThreads, W / 4);
+#pragma unroll
+        for (int i = 0; i < kPf; i++) {
+            const uint32_t r = w.r, c = 4 * w.c;
+            f32x4 v = {0.f, 0.f, 0.f, 0.f};
+            if (r < nk)
+                v = c < L ? *(const f32x4*)(p.kv_c + (size_t)(kb + r) * L + c)
+                          : *(const f32x4*)(p.k_rot + (size_t)(kb + r) * RP + (c - L));
+            pf[i] = v;
+            w.next();
+        }
+    };
+    if (k0 < k1) fetch(k0);
     for (uint32_t kb = k0; kb < k1; kb += kKeys) {
         const uint32_t nk = (k1 - kb) < kKeys ? (k1 - kb) : kKeys;
         __syncthreads();
-        for (uint32_t i = tid; i < nk * (L / 4); i += 256) {
-            const uint32_t r = i / (L / 4), c = i % (L / 4);
-            *(f32x4*)(kv + r * KS + 4 * c) = *(const f32x4*)(p.kv_c + (size_t)(kb + r) * L + 4 * c);
-        }
-        for (uint32_t i = tid; i < nk * RP; i += 256) {
-            const uint32_t r = i / RP, c = i % RP;
-            kv[r * KS + L + c] = p.k_rot[(size_t)(kb + r) * RP + c];
-        }
-        __syncthreads();
-        // scores: dot (h, key) for HG x kKeys pairs, two per thread
-        for (uint32_t d = tid; d < HG * kKeys; d += 256) {
-            const uint32_t h = d / kKeys, key = d % kKeys;
-            float v = -INFINITY;
-            if (key < nk && (!p.keep || p.keep[kb + key])) {
-                const float* a = qa + h * (L + RP);
-                const float* b = kv + key * KS;
-                float t = 0.f;
-                for (uint32_t c = 0; c < L + RP; c += 4) {
-                    const f32x4 x = *(const f32x4*)(a + c), y = *(const f32x4*)(b + c);
-                    t += x[0] * y[0];
-                    t += x[1] * y[1];
-                    t += x[2] * y[2];
-                    t += x[3] * y[3];
-                }
-                v = t * p.qk_scale;
+        {
+            Walk2 w(tid, kSplitThreads, W / 4);
+#pragma unroll
+            for (int i = 0; i < kPf; i++) {
+                if (w.r < kKeys) *(f32x4*)(kv + w.r * KS + 4 * w.c) = pf[i];
+                w.next();
             }
-            ps[h * kKeys + key] = v;
         }
         __syncthreads();
-        // online softmax: one wave per head at a time
-        for (uint32_t h = tid >> 6; h < HG; h += 4) {
+        if (kb + kKeys < k1) fetch(kb + kKeys);
+        float t[4][4];
+#pragma unroll
+        for (int a = 0; a < 4; a++)
+#pragma unroll
+            for (int b = 0; b < 4; b++) t[a][b] = 0.f;
+        for (uint32_t c4 = part; c4 < nch; c4 += 16) {
+            f32x4 x[4], y[4];
+#pragma unroll
+            for (int a = 0; a < 4; a++) x[a] = *(const f32x4*)(qa + (th + a) * KS + 4 * c4);
+#pragma unroll
+            for (int b = 0; b < 4; b++) y[b] = *(const f32x4*)(kv + (tk + b) * KS + 4 * c4);
+#pragma unroll
+            for (int a = 0; a < 4; a++)
+#pragma unroll
+                for (int b = 0; b < 4; b++) {
+                    t[a][b] += x[a][0] * y[b][0];
+                    t[a][b] += x[a][1] * y[b][1];
+                    t[a][b] += x[a][2] * y[b][2];
+                    t[a][b] += x[a][3] * y[b][3];
+                }
+        }
+#pragma unroll
+        for (int a = 0; a < 4; a++)
+#pragma unroll
+            for (int b = 0; b < 4; b++) {
+                t[a][b] += __shfl_xor(t[a][b], 1, 64);
+                t[a][b] += __shfl_xor(t[a][b], 2, 64);
+                t[a][b] += __shfl_xor(t[a][b], 4, 64);
+                t[a][b] += __shfl_xor(t[a][b], 8, 64);
+            }
+        if (part == 0) {
+#pragma unroll
+            for (int b = 0; b < 4; b++) {
+                const uint32_t key = tk + b;
+                const bool live = key < nk && (!p.keep || p.keep[kb + key]);
+#pragma unroll
+                for (int a = 0; a < 4; a++) ps[key * kHG + th + a] = live ? t[a][b] * p.qk_scale : -INFINITY;
+            }
+        }
+        __syncthreads();
+        // online softmax: one wave per head at a time, lanes over the keys
+        for (uint32_t h = tid >> 6; h < HG; h += kSplitThreads / 64) {
             const uint32_t ln = tid & 63;
-            const float v = ln < kKeys ? ps[h * kKeys + ln] : -INFINITY;
+            const float v = ln < kKeys ? ps[ln * kHG + h] : -INFINITY;
             float m = v;
             for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
             const float mo = mx[h];
@@ -488,81 +628,104 @@ __global__ __launch_bounds__(256) void attn_split_kernel(Shape s, AttnPtrs p, ui
             float z = e;
             for (int o = 32; o > 0; o >>= 1) z += __shfl_xor(z, o, 64);
             const float a = (mo == -INFINITY) ? 0.f : expf(mo - mn);
-            if (ln < kKeys) ps[h * kKeys + ln] = e;
+            if (ln < kKeys) ps[ln * kHG + h] = e;
             if (ln == 0) {
-                al[h] = (mn == -INFINITY) ? 1.f : a;
+                const float r = (mn == -INFINITY) ? 1.f : a;
+                al[h] = r;
                 mx[h] = mn;
-                sm[h] = sm[h] * ((mn == -INFINITY) ? 1.f : a) + z;
+                sm[h] = sm[h] * r + z;
             }
         }
         __syncthreads();
-        // context: acc[h][c] = acc * alpha[h] + sum_key p[h][key] kv_c[key][c]
+        if (cact) {
+            const uint32_t h0 = 4 * chg;
+            float r[4];
 #pragma unroll
-        for (int a = 0; a < 4; a++) {
-            const uint32_t h = hr + a * rp;
-            if (h < HG) {
-                const float sc = al[h];
+            for (int a = 0; a < 4; a++) r[a] = (h0 + a < HG) ? al[h0 + a] : 0.f;
 #pragma unroll
-                for (int e = 0; e < 8; e++) acc[a][e] *= sc;
-                for (uint32_t key = 0; key < nk; key++) {
-                    const float w = ps[h * kKeys + key];
-                    const f32x4 x = *(const f32x4*)(kv + key * KS + cc), y = *(const f32x4*)(kv + key * KS + cc + 4);
-                    acc[a][0] += w * x[0];
-                    acc[a][1] += w * x[1];
-                    acc[a][2] += w * x[2];
-                    acc[a][3] += w * x[3];
-                    acc[a][4] += w * y[0];
-                    acc[a][5] += w * y[1];
-                    acc[a][6] += w * y[2];
-                    acc[a][7] += w * y[3];
+            for (int a = 0; a < 4; a++)
+#pragma unroll
+                for (int e = 0; e < 4; e++) acc[a][e] *= r[a];
+            for (uint32_t key = 0; key < nk; key++) {
+                const f32x4 w = *(const f32x4*)(ps + key * kHG + h0);
+                const f32x4 x = *(const f32x4*)(kv + key * KS + cc);
+#pragma unroll
+                for (int a = 0; a < 4; a++) {
+                    acc[a][0] += w[a] * x[0];
+                    acc[a][1] += w[a] * x[1];
+                    acc[a][2] += w[a] * x[2];
+                    acc[a][3] += w[a] * x[3];
                 }
             }
         }
     }
     __syncthreads();
-    const uint32_t h0 = hg * HG;
+    const uint32_t hb = hg * HG;
     if (tid < HG) {
-        p.part_m[(size_t)sp * s.HN + h0 + tid] = mx[tid];
-        p.part_l[(size_t)sp * s.HN + h0 + tid] = sm[tid];
+        p.part_m[(size_t)sp * s.HN + hb + tid] = mx[tid];
+        p.part_l[(size_t)sp * s.HN + hb + tid] = sm[tid];
     }
+    if (cact) {
 #pragma unroll
-    for (int a = 0; a < 4; a++) {
-        const uint32_t h = hr + a * rp;
-        if (h < HG) {
-            float* o = p.part_ctx + ((size_t)sp * s.HN + h0 + h) * L + cc;
-            *(f32x4*)o = f32x4{acc[a][0], acc[a][1], acc[a][2], acc[a][3]};
-            *(f32x4*)(o + 4) = f32x4{acc[a][4], acc[a][5], acc[a][6], acc[a][7]};
+        for (int a = 0; a < 4; a++) {
+            const uint32_t h = 4 * chg + a;
+            if (h < HG) {
+                float* o = p.part_ctx + ((size_t)sp * s.HN + hb + h) * L + cc;
+                *(f32x4*)o = f32x4{acc[a][0], acc[a][1], acc[a][2], acc[a][3]};
+            }
         }
     }
 }
 
-// ctx[h] = sum_s e^(m_s - M) ctx_s[h] / sum_s e^(m_s - M) l_s, M = max_s m_s.
+// ctx[h] = sum_s e^(m_s - M) ctx_s[h] / sum_s e^(m_s - M) l_s, M = max_s m_s:
+// work-group (head, 256 columns); the split weights once into LDS.
 __global__ __launch_bounds__(256) void attn_combine_kernel(Shape s, AttnPtrs p, uint32_t S) {
-    const uint32_t h = blockIdx.x;
-    float M = -INFINITY;
-    for (uint32_t i = 0; i < S; i++) M = fmaxf(M, p.part_m[(size_t)i * s.HN + h]);
-    float z = 0.f;
-    for (uint32_t i = 0; i < S; i++) {
-        const float m = p.part_m[(size_t)i * s.HN + h];
-        if (m != -INFINITY) z += expf(m - M) * p.part_l[(size_t)i * s.HN + h];
+    __shared__ float w[64];
+    __shared__ float zz;
+    const uint32_t h = blockIdx.x / ((s.L + 255) / 256), c = (blockIdx.x % ((s.L + 255) / 256)) * 256 + threadIdx.x;
+    const uint32_t tid = threadIdx.x;
+    if (tid < 64) {
+        const float m = tid < S ? p.part_m[(size_t)tid * s.HN + h] : -INFINITY;
+        float M = m;
+        for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
+        const float e = (m == -INFINITY) ? 0.f : expf(m - M);
+        w[tid] = e;
+        float z = tid < S ? e * p.part_l[(size_t)tid * s.HN + h] : 0.f;
+        for (int o = 32; o > 0; o >>= 1) z += __shfl_xor(z, o, 64);
+        if (tid == 0) zz = z;
     }
-    const float inv = 1.0f / z;
-    for (uint32_t c = threadIdx.x; c < s.L; c += 256) {
+    __syncthreads();
+    if (c < s.L) {
         float t = 0.f;
-        for (uint32_t i = 0; i < S; i++) {
-            const float m = p.part_m[(size_t)i * s.HN + h];
-            if (m != -INFINITY) t += expf(m - M) * p.part_ctx[((size_t)i * s.HN + h) * s.L + c];
-        }
-        p.ctx[(size_t)h * s.L + c] = t * inv;
+        const float* src = p.part_ctx + (size_t)h * s.L + c;
+#pragma unroll 8
+        for (uint32_t i = 0; i < S; i++) t += w[i] * src[(size_t)i * s.HN * s.L];
+        p.ctx[(size_t)h * s.L + c] = t / zz;
     }
 }
 
 }  // namespace
 
+#ifndef WL_GEMV_TPR_MIN
+#define WL_GEMV_TPR_MIN 64
+#endif
+// Threads per row: the fewest (from WL_GEMV_TPR_MIN, one wave: the sums need
+// no barrier) whose chunk iterations fit the kMaxIt input registers, then
+// doubled while the launch would have fewer than 512 work-groups (small
+// matrices: more, shorter work-groups spread the rows over the chip); never
+// more than the row has chunks. Measured on MI355X: 16384 x 2048 at 64
+// threads per row 3.6 TB/s (2.4 at 256), 2048 x 6144 at 256 2.7 TB/s (2.4 at
+// 64).
 uint32_t gemv_plan(GemvJob& j) {
     const uint32_t nch = j.K / 8;
     uint32_t l2 = 0;
-    while ((1u << (l2 + 1)) <= nch && (1u << (l2 + 1)) <= kGemvThreads) l2++;
+    while ((1u << (l2 + 1)) <= nch && (1u << (l2 + 1)) <= WL_GEMV_TPR_MIN) l2++;
+    while ((nch + (1u << l2) - 1) >> l2 > (uint32_t)kMaxIt && (1u << l2) < kGemvThreads) l2++;
+    auto wgs = [&](uint32_t t2) {
+        const uint32_t rows = kGemvRows * (kGemvThreads >> t2);
+        return (j.N + rows - 1) / rows;
+    };
+    while (wgs(l2) < 512 && (1u << (l2 + 1)) <= nch && (1u << l2) < kGemvThreads) l2++;
     j.tpr_log2 = l2;
     j.rows_wg = kGemvRows * (kGemvThreads >> l2);
     return (j.N + j.rows_wg - 1) / j.rows_wg;
@@ -587,11 +750,12 @@ int launch_attn_absorb(const Shape& s, const AttnPtrs& p, uint32_t pos, bool own
 }
 
 int launch_index_select(const Shape& s, const AttnPtrs& p, uint32_t T, void* stream) {
-    const size_t lds = ((size_t)s.IH * s.ID + s.IH) * 4;
+    const size_t lds = ((size_t)s.IH * (s.ID + 4) + s.IH + (size_t)kIdxKeys * (s.ID + 4)) * 4;
     hipError_t ae = hipFuncSetAttribute((const void*)index_score_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
                                         (int)lds);
     if (ae != hipSuccess) return (int)ae;
-    hipLaunchKernelGGL(index_score_kernel, dim3((T + 31) / 32), dim3(256), lds, (hipStream_t)stream, s, p, T);
+    hipLaunchKernelGGL(index_score_kernel, dim3((T + kIdxKeys - 1) / kIdxKeys), dim3(256), lds, (hipStream_t)stream, s,
+                       p, T);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return (int)e;
     hipLaunchKernelGGL(index_topk_kernel, dim3(1), dim3(1024), 0, (hipStream_t)stream, (const float*)p.isc, p.keep, T,
@@ -611,8 +775,7 @@ uint32_t attn_splits(const Shape& s, uint32_t T, uint32_t max_splits) {
 }
 
 size_t attn_split_lds(const Shape& s) {
-    const uint32_t HG = s.HN < kHG ? s.HN : kHG;
-    return 4 * ((size_t)HG * (s.L + s.RP) + (size_t)kKeys * (s.L + s.RP + 4) + (size_t)HG * kKeys + 3 * HG);
+    return 4 * ((size_t)(kHG + kKeys) * (s.L + s.RP + 4) + (size_t)kKeys * kHG + 3 * kHG);
 }
 
 int launch_attn_core(const Shape& s, const AttnPtrs& p0, uint32_t T, uint32_t splits, void* stream) {
@@ -626,10 +789,12 @@ int launch_attn_core(const Shape& s, const AttnPtrs& p0, uint32_t T, uint32_t sp
     hipError_t ae = hipFuncSetAttribute((const void*)attn_split_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
                                         (int)attn_split_lds(s));
     if (ae != hipSuccess) return (int)ae;
-    hipLaunchKernelGGL(attn_split_kernel, dim3(NHG * S), dim3(256), attn_split_lds(s), (hipStream_t)stream, s, p, T);
+    hipLaunchKernelGGL(attn_split_kernel, dim3(NHG * S), dim3(kSplitThreads), attn_split_lds(s), (hipStream_t)stream,
+                       s, p, T);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return (int)e;
-    hipLaunchKernelGGL(attn_combine_kernel, dim3(s.HN), dim3(256), 0, (hipStream_t)stream, s, p, S);
+    hipLaunchKernelGGL(attn_combine_kernel, dim3(s.HN * ((s.L + 255) / 256)), dim3(256), 0, (hipStream_t)stream, s, p,
+                       S);
     return (int)hipGetLastError();
 }
 

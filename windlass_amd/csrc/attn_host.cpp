@@ -88,6 +88,8 @@ wl_status validate(const wl_attn_config* c, wl_attn* a) {
         return fail(a, WL_ERR_INVALID, "hidden, q_lora_rank, kv_lora_rank, n_heads x v_head and dense_inter must be "
                                        "multiples of 8 in [8, 16384]");
     if (c->kv_lora_rank > 512) return fail(a, WL_ERR_INVALID, "kv_lora_rank %u exceeds 512", c->kv_lora_rank);
+    if (c->kv_lora_rank + c->qk_rope > 768)
+        return fail(a, WL_ERR_INVALID, "kv_lora_rank + qk_rope = %u exceeds 768", c->kv_lora_rank + c->qk_rope);
     if (c->qk_rope == 0 || c->qk_rope % 4 || c->qk_rope > c->index_head_dim || c->index_head_dim > 256 ||
         c->index_head_dim % 8)
         return fail(a, WL_ERR_INVALID,
@@ -104,9 +106,9 @@ wl_status validate(const wl_attn_config* c, wl_attn* a) {
     return WL_OK;
 }
 
-// Appends a job to a launch, returning false if the launch is full.
+// Appends a job to a launch (at most kMaxJobs per launch; callers add at most four).
 void add_job(wl::attn::GemvLaunch& l, uint32_t& n_wg, wl::attn::GemvJob j) {
-    if (j.G == 0) {
+    if (j.G == 0) {  // ungrouped: row r is W row r, x is shared (GS == 0 marks it)
         j.G = j.N;
         j.GS = 0;
         j.OFF = 0;
@@ -419,6 +421,15 @@ wl_status wl_run_layer(wl_attn* a, wl_ctx* moe, uint32_t layer, uint32_t moe_lay
                                   (hipStream_t)stream);
     if (e != hipSuccess) return fail(a, WL_ERR_HIP, "residual copy: %s", hipGetErrorString(e));
     return WL_OK;
+}
+
+wl_status wl_matvec_bf16(const uint16_t* d_W, const float* d_x, float* d_y, uint32_t N, uint32_t K, void* stream) {
+    if (!d_W || !d_x || !d_y || N == 0 || K == 0 || K % 8 || K > 16384) return WL_ERR_INVALID;
+    if (((uintptr_t)d_W | (uintptr_t)d_x) % 16) return WL_ERR_INVALID;
+    wl::attn::GemvLaunch l{};
+    uint32_t n = 0;
+    add_job(l, n, job(d_W, d_x, d_y, N, K));
+    return wl::attn::launch_gemv(l, n, stream) == 0 ? WL_OK : WL_ERR_HIP;
 }
 
 wl_status wl_attn_taps(wl_attn* a, wl_attn_taps_out* out) {

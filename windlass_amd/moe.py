@@ -173,6 +173,7 @@ def load():
         "wl_run_dense_mlp": [vp, u32, vp, vp],
         "wl_run_layer": [vp, vp, u32, u32, u32, vp, vp],
         "wl_attn_taps": [vp, ctypes.POINTER(AttnTaps)],
+        "wl_matvec_bf16": [vp, vp, vp, u32, u32, vp],
     }
     for name, args in sig.items():
         fn = getattr(lib, name)
@@ -275,6 +276,12 @@ def policy_replay(policy, capacity, keys, batch, pinned=()):
     if rc != WL_OK:
         raise WindlassError(rc, "wl_policy_replay")
     return out, h.value, m.value, e.value
+
+
+def matvec_bf16(d_W, d_x, d_y, N, K, stream=0):
+    rc = load().wl_matvec_bf16(d_W, d_x, d_y, N, K, stream)
+    if rc != WL_OK:
+        raise WindlassError(rc, "wl_matvec_bf16")
 
 
 def dequant_matvec_mxfp4(d_W, d_S, d_x, d_y, N, K, stream=0):
