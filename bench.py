@@ -32,6 +32,14 @@ sharing it); a step is one token through the 4 layers, `value` is
 microseconds per attention layer; the dense MLP (intermediate 12288) is
 timed beside it.
 
+--workload files measures the file tier and the loader (rows f1, f4) at the
+GLM shape: --file-layers packed layer_N.bin files written from the
+synthetic generator to local disk, read through a --file-slots HBM cache by
+4 pread workers, once through the page cache and once with O_DIRECT; then a
+one-layer safetensors checkpoint loaded into the slot table (wl_load_layer +
+wl_load_experts) and packed back into a layer file (wl_st_pack_layer). The
+line reports GB/s of each path; the files are removed at the end.
+
 --workload cache measures configs[4]: 75 MoE layers whose 19,200 experts sit
 behind the HBM expert cache (3,094 slots, 62 GB) and are copied from pinned
 host memory on a miss; router bias shaped by Zipf(1.1) popularity; a step is
@@ -328,6 +336,129 @@ def bench_attention(args):
     print(json.dumps(line), flush=True)
 
 
+def bench_files(args):
+    import shutil
+    import tempfile
+
+    from windlass_amd import checkpoint, hip, moe, synthdata
+    from windlass_amd.model import FileModel
+    c = dict(GLM)
+    H, I, E = c["hidden"], c["moe_inter"], c["n_routed_experts"]
+    L = args.file_layers
+    work = tempfile.mkdtemp(prefix="wl_files_", dir=args.file_dir)
+    out = {}
+    try:
+        cfg = moe.make_config(hidden=H, moe_inter=I, n_routed_experts=E, n_experts_per_tok=c["n_experts_per_tok"],
+                              n_shared=1, n_layers=L)
+        blk = moe.expert_layout(cfg).total
+        d_ref, h_ref = hip.DeviceBuffer(blk), hip.HostBuffer(blk)
+
+        def expert_bytes(l, e):
+            moe.synth_expert(cfg, args.seed, l, e, d_ref.ptr)
+            hip.copy_d2h_ptr(h_ref.ptr, d_ref.ptr, blk)
+            return h_ref.view(np.uint8, blk)
+
+        t0 = time.time()
+        for l in range(L):
+            with open(os.path.join(work, f"layer_{l}.bin"), "wb") as f:
+                for e in range(E):
+                    f.write(expert_bytes(l, e).tobytes())
+        out["write_s"] = round(time.time() - t0, 1)
+        zipf = synthdata.zipf_bias_offset(E, args.seed, amplitude=args.zipf_amp)
+        n_h = 64
+        d_hs = hip.DeviceBuffer.from_array(np.stack([synthdata.hidden_state(H, 5000 + i) for i in range(n_h)]))
+        d_h, d_tmp = hip.DeviceBuffer(4 * H), hip.DeviceBuffer(4 * H)
+        stream = hip.Stream()
+        for direct, steps, warm in ((False, 16, 4), (True, 4, 2)):
+            fm = FileModel(c, args.seed, L, capacity=args.file_slots, directory=work, io_threads=4,
+                           shared_alias=True, bias_offset=zipf, direct=direct)
+            fm.ctx.set_taps(False)
+
+            def token(i):
+                hip.copy_d2d(d_h.ptr, d_hs.ptr + 4 * H * (i % n_h), 4 * H, stream.handle)
+                fm.ctx.run_chain(0, L, d_h.ptr, d_tmp.ptr, stream.handle)
+
+            for i in range(warm):
+                token(i)
+            stream.synchronize()
+            fm.ctx.cache_reset_stats()
+            e0, e1 = hip.Event(), hip.Event()
+            e0.record(stream)
+            for i in range(steps):
+                token(warm + i)
+            e1.record(stream)
+            e1.synchronize()
+            ms = e0.elapsed_ms(e1)
+            fm.ctx.check_error(stream.handle)
+            st = fm.ctx.cache_stats()
+            out["direct" if direct else "page_cache"] = {
+                "us_per_layer": round(ms * 1e3 / steps / L, 1), "tokens": steps,
+                "hit_rate": round(st["hits"] / max(1, st["hits"] + st["misses"]), 4), "misses": st["misses"],
+                "file_GBps": round(st["misses"] * blk / (ms * 1e-3) / 1e9, 2)}
+            fm.close()
+        # loader: a one-layer checkpoint (dense fields + 256 experts) -> slot table, and -> packed file
+        d = synthdata.dense_layer(H, E, I, args.seed, 0)
+        P = "model.layers.0."
+        lay = moe.expert_layout(cfg)
+        parts = [(lay.gw_off, lay.gw_len, (I, H // 2)), (lay.gs_off, lay.gs_len, (I, H // 32)),
+                 (lay.uw_off, lay.uw_len, (I, H // 2)), (lay.us_off, lay.us_len, (I, H // 32)),
+                 (lay.dw_off, lay.dw_len, (H, I // 2)), (lay.ds_off, lay.ds_len, (H, I // 32))]
+        names = ["gate_proj.weight", "gate_proj.weight_scale", "up_proj.weight", "up_proj.weight_scale",
+                 "down_proj.weight", "down_proj.weight_scale"]
+        ts = [(P + "post_attention_layernorm.weight", "BF16", (H,), np.full(H, 0x3F80, np.uint16)),
+              (P + "mlp.gate.weight", "BF16", (E, H), d["router_w"]),
+              (P + "mlp.gate.e_score_correction_bias", "F32", (E,), d["bias"]),
+              (P + "mlp.shared_experts.gate_proj.weight", "BF16", (I, H), d["sh_gate"]),
+              (P + "mlp.shared_experts.up_proj.weight", "BF16", (I, H), d["sh_up"]),
+              (P + "mlp.shared_experts.down_proj.weight", "BF16", (H, I), d["sh_down"])]
+        cur = {}
+
+        def part_of(e, j):
+            def f():
+                if cur.get("e") != e:
+                    cur["e"], cur["b"] = e, expert_bytes(0, e).copy()
+                off, n, _ = parts[j]
+                return cur["b"][off:off + n]
+            return f
+
+        for e in range(E):
+            for j in range(6):
+                ts.append((f"{P}mlp.experts.{e}.{names[j]}", "U8", parts[j][2], (part_of(e, j), parts[j][1])))
+        ck = os.path.join(work, "ckpt")
+        checkpoint.write_checkpoint(ck, ts, n_shards=1)
+        c1 = moe.make_config(hidden=H, moe_inter=I, n_routed_experts=E, n_experts_per_tok=c["n_experts_per_tok"],
+                             n_shared=1, n_layers=1)
+        ctx = moe.Context(c1)
+        ctx.slot_pool_create(E)
+        t0 = time.time()
+        st = moe.SafeTensors(ck)
+        t_open = time.time() - t0
+        t0 = time.time()
+        ctx.load_layer(st, 0, 0)
+        t_layer = time.time() - t0
+        t0 = time.time()
+        ctx.load_experts(st, 0, 0, n=E, first_slot=0)
+        t_exp = time.time() - t0
+        t0 = time.time()
+        st.pack_layer(c1, 0, os.path.join(work, "packed_0.bin"))
+        t_pack = time.time() - t0
+        out["loader"] = {"open_ms": round(t_open * 1e3, 1), "load_layer_ms": round(t_layer * 1e3, 1),
+                         "load_experts_s": round(t_exp, 3), "load_experts_GBps": round(E * blk / t_exp / 1e9, 2),
+                         "pack_layer_s": round(t_pack, 3), "pack_layer_GBps": round(E * blk / t_pack / 1e9, 2),
+                         "note": "checkpoint just written: read through the page cache"}
+        ctx.close()
+        st.close()
+    finally:
+        shutil.rmtree(work, ignore_errors=True)
+    line = {"metric": "file_tier_GBps", "value": out["page_cache"]["file_GBps"], "unit": "GB/s", "n_gpus": 1,
+            "higher_is_better": True, "data": "synthetic", "dtype": "mxfp4 expert records",
+            "config": {"workload": f"file tier: {L} GLM layer files ({L * E} records of {blk} B), "
+                                   f"{args.file_slots}-slot HBM cache, 4 pread workers, bs=1 tokens",
+                       "zipf_amplitude": args.zipf_amp},
+            **out}
+    print(json.dumps(line), flush=True)
+
+
 def synthdata_hidden(H, seed):
     from windlass_amd import synthdata
     return synthdata.hidden_state(H, seed)
@@ -340,7 +471,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--layers", type=int, default=8, help="distinct resident layer copies to rotate over")
     ap.add_argument("--sched", choices=["fused", "phased"], default="fused")
-    ap.add_argument("--workload", choices=["layer", "chain", "batched", "cache", "attention"], default="layer",
+    ap.add_argument("--workload", choices=["layer", "chain", "batched", "cache", "attention", "files"], default="layer",
                     help="layer: config 1 (default); chain: config 2, 24 layers per step; "
                          "batched: config 3, --tokens positions per step; cache: config 4, 75 cache-backed layers per step")
     ap.add_argument("--tokens", type=int, default=256, help="batched workload: positions per layer call")
@@ -358,6 +489,9 @@ def main():
                          "tokens (popularity pinning)")
     ap.add_argument("--zipf-amp", type=float, default=0.25,
                     help="cache workload: bias offset of the most popular expert (rank r gets amp * r^-1.1)")
+    ap.add_argument("--file-layers", type=int, default=2, help="files workload: packed layer files")
+    ap.add_argument("--file-slots", type=int, default=64, help="files workload: HBM cache slots")
+    ap.add_argument("--file-dir", default=None, help="files workload: directory for the files (default: a temp dir)")
     ap.add_argument("--context", type=int, default=4096,
                     help="attention workload: cached positions before the timed tokens")
     ap.add_argument("--seed", type=int, default=1)
@@ -383,6 +517,8 @@ def main():
         sys.exit(1)
     if args.workload == "attention":
         return bench_attention(args)
+    if args.workload == "files":
+        return bench_files(args)
 
     c = dict(GLM)
     H = c["hidden"]

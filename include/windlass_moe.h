@@ -330,6 +330,13 @@ wl_status wl_cache_create(wl_ctx* ctx, uint32_t capacity, wl_host_block_fn host_
  * device staging. */
 wl_status wl_cache_create_files(wl_ctx* ctx, uint32_t capacity, const char* dir, uint32_t first_layer,
                                 uint32_t io_threads);
+/* The same with flags: WL_FILES_DIRECT reads with O_DIRECT (bypassing the
+ * host page cache; the record size must be a multiple of 4096 bytes, as it is
+ * at the GLM shape: 20,054,016 = 4,896 x 4,096). No reference counterpart:
+ * the reference reads through the page cache. */
+#define WL_FILES_DIRECT 1
+wl_status wl_cache_create_files_ex(wl_ctx* ctx, uint32_t capacity, const char* dir, uint32_t first_layer,
+                                   uint32_t io_threads, uint32_t flags);
 wl_status wl_cache_set_speculation(wl_ctx* ctx, int32_t enable);
 
 typedef struct wl_cache_stats {

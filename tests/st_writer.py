@@ -1,56 +1,14 @@
 """Safetensors checkpoints for the loader tests, written from the synthetic
 generator under the reference's tensor names (src/glm_loader.cuh:597-611;
-tools/repack_experts_glm.py:46-53).
-
-The writer follows the published safetensors format (8-byte little-endian
-header length, a JSON header {name: {dtype, shape, data_offsets}} padded with
-spaces to a multiple of 8 bytes, then the data) and is itself checked against
-the `safetensors` library in tests/test_loader.py."""
-import json
-import os
-import struct
-
+tools/repack_experts_glm.py:46-53). The file writer is
+windlass_amd.checkpoint's, itself checked against the `safetensors` library
+in tests/test_loader.py."""
 import numpy as np
 
 from oracle import synth
 from windlass_amd import synthdata
+from windlass_amd.checkpoint import write_checkpoint, write_safetensors  # noqa: F401 (re-exported)
 from windlass_amd.model import SHARED_KEY
-
-
-def write_safetensors(path, tensors, metadata=None):
-    """tensors: list of (name, dtype, shape, bytes) in file order."""
-    header = {}
-    if metadata is not None:
-        header["__metadata__"] = metadata
-    off = 0
-    for name, dtype, shape, data in tensors:
-        header[name] = {"dtype": dtype, "shape": list(shape), "data_offsets": [off, off + len(data)]}
-        off += len(data)
-    h = json.dumps(header).encode()
-    h += b" " * (-len(h) % 8)
-    with open(path, "wb") as f:
-        f.write(struct.pack("<Q", len(h)))
-        f.write(h)
-        for _, _, _, data in tensors:
-            f.write(data)
-
-
-def write_checkpoint(directory, tensors, n_shards=2):
-    """A sharded checkpoint: tensors dealt round robin over n_shards files
-    model-0000i-of-0000n.safetensors, plus model.safetensors.index.json."""
-    os.makedirs(directory, exist_ok=True)
-    shards = [[] for _ in range(n_shards)]
-    for i, t in enumerate(tensors):
-        shards[i % n_shards].append(t)
-    weight_map, total = {}, 0
-    for s, ts in enumerate(shards):
-        fn = f"model-{s + 1:05d}-of-{n_shards:05d}.safetensors"
-        write_safetensors(os.path.join(directory, fn), ts, metadata={"format": "pt"})
-        for name, _, _, data in ts:
-            weight_map[name] = fn
-            total += len(data)
-    with open(os.path.join(directory, "model.safetensors.index.json"), "w") as f:
-        json.dump({"metadata": {"total_size": total}, "weight_map": weight_map}, f, indent=2)
 
 
 def ln_weight(H, seed, layer):

@@ -15,12 +15,16 @@
 //      nothing).
 #include "expert_files.h"
 
+#ifndef _GNU_SOURCE
+#define _GNU_SOURCE  // O_DIRECT
+#endif
 #include <fcntl.h>
 #include <sys/stat.h>
 #include <unistd.h>
 
 #include <cerrno>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 
 #include "internal.h"
@@ -45,22 +49,28 @@ std::string FileTier::make_worker(Worker& w) {
         if ((e = hipEventCreateWithFlags(&w.buf_ev[b], hipEventDisableTiming)) != hipSuccess)
             return std::string("io event: ") + hipGetErrorString(e);
     }
+    if (direct_) {
+        void* p = nullptr;
+        if (posix_memalign(&p, 4096, ref_bytes_) != 0) return "bounce buffer: out of host memory";
+        w.bounce = (uint8_t*)p;
+    }
     return "";
 }
 
 std::string FileTier::open(const std::string& dir, uint32_t first_layer, uint32_t n_layers, uint32_t n_experts,
                            size_t ref_bytes, size_t native_bytes, uint32_t H, uint32_t I, uint32_t io_threads,
-                           int device) {
+                           int device, bool direct) {
     first_ = first_layer;
     ref_bytes_ = ref_bytes;
     native_bytes_ = native_bytes;
     H_ = H;
     I_ = I;
     device_ = device;
+    direct_ = direct;
     for (uint32_t l = 0; l < n_layers; l++) {
         char path[4096];
         snprintf(path, sizeof(path), "%s/layer_%u.bin", dir.c_str(), first_layer + l);
-        const int fd = ::open(path, O_RDONLY);
+        const int fd = ::open(path, O_RDONLY | (direct ? O_DIRECT : 0));
         if (fd < 0) return std::string("open ") + path + ": " + std::strerror(errno);
         fds_.push_back(fd);
         struct stat st;
@@ -105,6 +115,7 @@ FileTier::~FileTier() {
             if (w.buf_ev[b]) (void)hipEventDestroy(w.buf_ev[b]);
         }
         if (w.stream) (void)hipStreamDestroy(w.stream);
+        free(w.bounce);
     };
     for (Worker& w : workers_) drop(w);
     drop(inline_);
@@ -129,6 +140,7 @@ FileTask* FileTier::submit(uint32_t layer, uint32_t expert, uint8_t* dst, hipEve
     t->expert = expert;
     t->failed.store(false, std::memory_order_relaxed);
     t->issued.store(false, std::memory_order_relaxed);
+    t->why[0] = 0;
     if (inline_mode_) {  // the calling thread is the worker
         if (!run(inline_, t)) t->failed.store(true, std::memory_order_relaxed);
         t->issued.store(true, std::memory_order_release);
@@ -156,20 +168,34 @@ void FileTier::release(FileTask* t) {
 bool FileTier::run(Worker& w, FileTask* t) {
     const uint32_t b = w.turn;
     w.turn ^= 1u;
-    if (w.used[b] && hipEventSynchronize(w.buf_ev[b]) != hipSuccess) return false;
-    uint8_t* buf = w.pinned[b];
+    if (w.used[b] && hipEventSynchronize(w.buf_ev[b]) != hipSuccess) {
+        snprintf(t->why, sizeof(t->why), "wait for the io buffer failed");
+        return false;
+    }
+    uint8_t* buf = w.bounce ? w.bounce : w.pinned[b];
     size_t got = 0;
     while (got < ref_bytes_) {
         const ssize_t r = ::pread(t->fd, buf + got, ref_bytes_ - got, (off_t)(t->off + got));
         if (r < 0 && errno == EINTR) continue;
-        if (r <= 0) return false;
+        if (r <= 0) {
+            snprintf(t->why, sizeof(t->why), "pread at %llu: %s", (unsigned long long)(t->off + got),
+                     r < 0 ? std::strerror(errno) : "end of file");
+            return false;
+        }
         got += (size_t)r;
     }
-    if (t->gate && hipStreamWaitEvent(w.stream, t->gate, 0) != hipSuccess) return false;
-    if (hipMemcpyAsync(w.stage[b], buf, ref_bytes_, hipMemcpyHostToDevice, w.stream) != hipSuccess) return false;
-    if (launch_expert_to_native(w.stage[b], t->dst, H_, I_, 0u, w.stream) != 0) return false;
-    if (hipEventRecord(t->done, w.stream) != hipSuccess) return false;
-    if (hipEventRecord(w.buf_ev[b], w.stream) != hipSuccess) return false;
+    if (w.bounce) std::memcpy(w.pinned[b], w.bounce, ref_bytes_);
+    buf = w.pinned[b];
+    auto bad = [t](const char* what) {
+        snprintf(t->why, sizeof(t->why), "%s failed", what);
+        return false;
+    };
+    if (t->gate && hipStreamWaitEvent(w.stream, t->gate, 0) != hipSuccess) return bad("gate wait");
+    if (hipMemcpyAsync(w.stage[b], buf, ref_bytes_, hipMemcpyHostToDevice, w.stream) != hipSuccess)
+        return bad("host-to-device copy");
+    if (launch_expert_to_native(w.stage[b], t->dst, H_, I_, 0u, w.stream) != 0) return bad("conversion launch");
+    if (hipEventRecord(t->done, w.stream) != hipSuccess) return bad("event record");
+    if (hipEventRecord(w.buf_ev[b], w.stream) != hipSuccess) return bad("event record");
     w.used[b] = true;
     return true;
 }

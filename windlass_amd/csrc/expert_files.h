@@ -30,6 +30,7 @@ struct FileTask {
     uint32_t layer = 0, expert = 0;
     std::atomic<bool> issued{false};  // the worker has recorded `done` (or failed)
     std::atomic<bool> failed{false};
+    char why[96] = {0};               // the failure, set before `issued`
 };
 
 class FileTier {
@@ -37,9 +38,12 @@ public:
     // Opens dir/layer_{first_layer + l}.bin for l < n_layers and checks that
     // each holds n_experts records of ref_bytes; starts io_threads workers
     // (0: every read runs on the calling thread). H, I: the shapes for the
-    // device conversion. Returns an empty string or an error message.
+    // device conversion. direct: O_DIRECT reads (ref_bytes a multiple of
+    // 4096) into a page-aligned bounce buffer per worker, copied into the
+    // pinned buffer. Returns an empty string or an error message.
     std::string open(const std::string& dir, uint32_t first_layer, uint32_t n_layers, uint32_t n_experts,
-                     size_t ref_bytes, size_t native_bytes, uint32_t H, uint32_t I, uint32_t io_threads, int device);
+                     size_t ref_bytes, size_t native_bytes, uint32_t H, uint32_t I, uint32_t io_threads, int device,
+                     bool direct = false);
     ~FileTier();
 
     // Queues the read of (layer, expert) into dst; the copy waits for `gate`
@@ -58,6 +62,8 @@ private:
     struct Worker {
         hipStream_t stream = nullptr;
         uint8_t* pinned[2] = {nullptr, nullptr};
+        uint8_t* bounce = nullptr;  // direct mode: page-aligned ordinary memory the O_DIRECT reads land in
+                                    // (direct I/O into the runtime's pinned mappings fails with EFAULT)
         uint8_t* stage[2] = {nullptr, nullptr};  // device copies of the reference-layout block
         hipEvent_t buf_ev[2] = {nullptr, nullptr};
         bool used[2] = {false, false};
@@ -77,6 +83,7 @@ private:
     std::vector<Worker> workers_;
     Worker inline_;  // io_threads == 0
     bool inline_mode_ = false;
+    bool direct_ = false;
     std::vector<std::thread> threads_;
     std::deque<FileTask*> q_;
     std::mutex qm_;

@@ -597,11 +597,12 @@ static wl_status cache_resolve(wl_ctx* c, uint32_t layer, const int32_t* ids, ui
             // was waited for) lands first
             if (wl::FileTask* old = C.task_of[r.slot]) {
                 const bool ok = C.files->wait_issued(old);
+                const std::string why = old->why;
                 C.files->release(old);
                 C.task_of[r.slot] = nullptr;
                 if (!ok) {
                     C.lru->forget(key);
-                    return fail(c, WL_ERR_IO, "an earlier read into slot %u failed", r.slot);
+                    return fail(c, WL_ERR_IO, "an earlier read into slot %u failed: %s", r.slot, why.c_str());
                 }
             }
             wl::FileTask* t = C.files->submit(layer, (uint32_t)ids[k], dst, C.gate_recorded ? C.cur_gate : nullptr,
@@ -1205,13 +1206,23 @@ wl_status wl_cache_create(wl_ctx* c, uint32_t capacity, wl_host_block_fn host_bl
 
 wl_status wl_cache_create_files(wl_ctx* c, uint32_t capacity, const char* dir, uint32_t first_layer,
                                 uint32_t io_threads) {
+    return wl_cache_create_files_ex(c, capacity, dir, first_layer, io_threads, 0u);
+}
+
+wl_status wl_cache_create_files_ex(wl_ctx* c, uint32_t capacity, const char* dir, uint32_t first_layer,
+                                   uint32_t io_threads, uint32_t flags) {
     if (!c) return WL_ERR_INVALID;
     if (!dir) return fail(c, WL_ERR_INVALID, "dir is null");
+    if (flags & ~(uint32_t)WL_FILES_DIRECT) return fail(c, WL_ERR_INVALID, "unknown flags 0x%x", flags);
+    if ((flags & WL_FILES_DIRECT) && c->lay.total % 4096u)
+        return fail(c, WL_ERR_INVALID, "WL_FILES_DIRECT needs records of a multiple of 4096 bytes, not %zu",
+                    c->lay.total);
     if (io_threads > 64) return fail(c, WL_ERR_INVALID, "io_threads %u > 64", io_threads);
     if (c->cache.lru) return fail(c, WL_ERR_STATE, "the context already has a cache");
     std::unique_ptr<wl::FileTier> files(new wl::FileTier());
     const std::string err = files->open(dir, first_layer, c->cfg.n_layers, c->cfg.n_routed_experts, c->lay.total,
-                                        c->native_bytes, c->cfg.hidden, c->cfg.moe_inter, io_threads, c->device);
+                                        c->native_bytes, c->cfg.hidden, c->cfg.moe_inter, io_threads, c->device,
+                                        (flags & WL_FILES_DIRECT) != 0u);
     if (!err.empty()) return fail(c, WL_ERR_IO, "%s", err.c_str());
     wl_status s = cache_init(c, capacity);
     if (s != WL_OK) return s;
@@ -1290,9 +1301,10 @@ wl_status wl_cache_get(wl_ctx* c, uint32_t layer, uint32_t expert, void* stream,
         const uint32_t slot = (uint32_t)((p - C.pool) / c->native_bytes);
         if (wl::FileTask* t = C.task_of[slot]) {
             const bool ok = C.files->wait_issued(t);
+            const std::string why = t->why;
             C.files->release(t);
             C.task_of[slot] = nullptr;
-            if (!ok) return fail(c, WL_ERR_IO, "read of layer %u expert %u failed", layer, expert);
+            if (!ok) return fail(c, WL_ERR_IO, "read of layer %u expert %u failed: %s", layer, expert, why.c_str());
         }
         hipError_t e;
         if (C.has_ev[slot] && (e = hipStreamWaitEvent((hipStream_t)stream, C.slot_ev[slot], 0)) != hipSuccess)

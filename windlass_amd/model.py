@@ -200,9 +200,9 @@ class FileModel(_Layers):
     the files)."""
 
     def __init__(self, cfg, seed, n_layers, capacity, directory, first_layer=0, io_threads=4, ln_weights=None,
-                 bias_offset=None, shared_alias=False, shared_mxfp4=False):
+                 bias_offset=None, shared_alias=False, shared_mxfp4=False, direct=False):
         super().__init__(cfg, seed, n_layers, ln_weights, bias_offset, shared_alias, shared_mxfp4)
-        self.ctx.cache_create_files(capacity, directory, first_layer, io_threads)
+        self.ctx.cache_create_files(capacity, directory, first_layer, io_threads, direct=direct)
         self._bind_dense()
         hip.synchronize()
 

@@ -146,6 +146,7 @@ def load():
         "wl_expert_ffn": [vp, vp, vp, vp, vp, vp],
         "wl_cache_create": [vp, u32, HOST_BLOCK_FN, vp],
         "wl_cache_create_files": [vp, u32, ctypes.c_char_p, u32, u32],
+        "wl_cache_create_files_ex": [vp, u32, ctypes.c_char_p, u32, u32, u32],
         "wl_set_expert_source": [vp, ctypes.POINTER(ExpertSourceC)],
         "wl_cache_set_speculation": [vp, i32],
         "wl_cache_get_stats": [vp, ctypes.POINTER(CacheStats)],
@@ -542,10 +543,9 @@ class Context:
         self._host_block_cb = HOST_BLOCK_FN(lambda user, layer, expert: host_block(layer, expert))
         self._ck(self.lib.wl_cache_create(self.h, capacity, self._host_block_cb, None), "wl_cache_create")
 
-    def cache_create_files(self, capacity, directory, first_layer=0, io_threads=4):
-        """The cache over packed expert files directory/layer_N.bin."""
-        self._ck(self.lib.wl_cache_create_files(self.h, capacity, os.fsencode(directory), first_layer, io_threads),
-                 "wl_cache_create_files")
+    def cache_create_files(self, capacity, directory, first_layer=0, io_threads=4, direct=False):
+        self._ck(self.lib.wl_cache_create_files_ex(self.h, capacity, os.fsencode(directory), first_layer, io_threads,
+                                                   1 if direct else 0), "wl_cache_create_files")
 
     def cache_set_speculation(self, enable):
         self._ck(self.lib.wl_cache_set_speculation(self.h, 1 if enable else 0), "wl_cache_set_speculation")
