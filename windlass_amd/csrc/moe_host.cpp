@@ -351,6 +351,8 @@ wl_status wl_create(const wl_moe_config* cfg, wl_ctx** out) {
     }
 
     e = hipMemset(c->d_slot, 0, sizeof(void*) * (size_t)L * E);
+    // records of layers not yet bound are zero, not stale bytes
+    if (e == hipSuccess) e = hipMemset(c->d_largs, 0, sizeof(wl::DecodeArgs) * (size_t)L);
     // epoch 0 is never a call's: zeroed tagged arrays hold no valid word (a
     // reused allocation could otherwise carry another context's tags)
     if (e == hipSuccess) e = hipMemset(c->lslot, 0, 8 * (size_t)E);
