@@ -740,79 +740,66 @@ struct UpK {
     }
     // One step for a pass of NB row blocks and NP planes (shape-specialised
     // so the inner loops carry no branches).
+    //
+    // Shared: one MFMA per activation fragment, all on this wave's one weight
+    // tile. MFMA it (k step k, plane pc, block tb) accumulates into
+    // acc[(NP k + pc) % 4][tb], so consecutive MFMAs of a block do not wait on
+    // each other; finish() adds the four. Fragments are read kSPD MFMAs ahead
+    // (LDS latency is not hidden by the one other wave of the SIMD otherwise).
+    static constexpr uint32_t kSPD = 6;
     template <uint32_t NB, uint32_t NP>
     WL_MEM void comp_shared(uint32_t s, const uint8_t* sl, const WBuf& W) {
+        constexpr uint32_t N = 8u * NP * NB;
+        bf16x8 af[kSPD + 1u];
+        auto frag = [&](uint32_t it) {  // it = (k NP + pc) NB + tb
+            const uint32_t tb = it % NB, pc = (it / NB) % NP, k = it / (NB * NP);
+            return afrag(sl, pc, tb, k / 4u, lo_s[k % 4u]);
+        };
 #pragma unroll
-        for (uint32_t k = 0; k < 8u; k++) {
+        for (uint32_t it = 0; it < kSPD && it < N; it++) af[it] = frag(it);
+#pragma unroll
+        for (uint32_t it = 0; it < N; it++) {
+            const uint32_t tb = it % NB, kp = it / NB, k = kp / NP;
+            if (it + kSPD < N) af[(it + kSPD) % (kSPD + 1u)] = frag(it + kSPD);
             const u32x4 z = {0u, 0u, 0u, 0u};
             const bf16x8 bw = as_bf16x8(8u * s + k < nkt ? W.w[k] : z);
-#pragma unroll
-            for (uint32_t tb = 0; tb < NB; tb++)
-#pragma unroll
-                for (uint32_t pc = 0; pc < NP; pc++)
-                    acc[0][tb] = mma(afrag(sl, pc, tb, k / 4u, lo_s[k % 4u]), bw, acc[0][tb]);
+            acc[kp % 4u][tb] = mma(af[it % (kSPD + 1u)], bw, acc[kp % 4u][tb]);
             __builtin_amdgcn_sched_barrier(0);
         }
     }
+    // Routed: iteration it = NP (4 q + jj) + pc runs plane pc of k step
+    // (q, jj) (columns q * 128 + 32 g + 8 jj) against the kSG slices; the
+    // next iteration's NB fragments are read while this one's MFMAs run.
     template <uint32_t NB, uint32_t NP>
     WL_MEM void comp_routed(uint32_t s, const uint8_t* sl, const WBuf& W) {
-        if constexpr (NP == 1u) {
-            // Pieces in rows (NB fragments per k step): the fragments of the
-            // next k step are read while this one computes (LDS latency is
-            // not hidden by the one other wave of the SIMD otherwise).
-            float sc[2][kSG];
+        float sc[2][kSG];
 #pragma unroll
-            for (uint32_t q = 0; q < 2; q++)
+        for (uint32_t q = 0; q < 2; q++)
 #pragma unroll
-                for (uint32_t i = 0; i < kSG; i++)
-                    sc[q][i] = 2u * s + q < nkg ? e8m0f((W.s[i] >> (8u * ((2u * s + q) % 4u))) & 0xFFu) : 0.f;
-            bf16x8 af[2][NB];
+            for (uint32_t i = 0; i < kSG; i++)
+                sc[q][i] = 2u * s + q < nkg ? e8m0f((W.s[i] >> (8u * ((2u * s + q) % 4u))) & 0xFFu) : 0.f;
+        constexpr uint32_t N = 8u * NP;
+        bf16x8 af[2][NB];
 #pragma unroll
-            for (uint32_t tb = 0; tb < NB; tb++) af[0][tb] = afrag(sl, 0u, tb, 0u, lo_r[0]);
+        for (uint32_t tb = 0; tb < NB; tb++) af[0][tb] = afrag(sl, 0u, tb, 0u, lo_r[0]);
+        bf16x8 bw[kSG];
 #pragma unroll
-            for (uint32_t it = 0; it < 8; it++) {
-                const uint32_t q = it / 4u, jj = it % 4u, c = it % 2u;
-                if (it + 1u < 8u) {
+        for (uint32_t it = 0; it < N; it++) {
+            const uint32_t pc = it % NP, ks = it / NP, q = ks / 4u, jj = ks % 4u, c = it % 2u;
+            if (it + 1u < N) {
+                const uint32_t n = it + 1u, nks = n / NP;
 #pragma unroll
-                    for (uint32_t tb = 0; tb < NB; tb++)
-                        af[c ^ 1u][tb] = afrag(sl, 0u, tb, (it + 1u) / 4u, lo_r[(it + 1u) % 4u]);
-                }
-                bf16x8 bw[kSG];
+                for (uint32_t tb = 0; tb < NB; tb++) af[c ^ 1u][tb] = afrag(sl, n % NP, tb, nks / 4u, lo_r[nks % 4u]);
+            }
+            if (pc == 0u) {
 #pragma unroll
                 for (uint32_t i = 0; i < kSG; i++) bw[i] = fp4x8_bf16(W.w[2u * i + q][jj], sc[q][i]);
-#pragma unroll
-                for (uint32_t i = 0; i < kSG; i++)
-#pragma unroll
-                    for (uint32_t tb = 0; tb < NB; tb++) acc[i][tb] = mma(af[c][tb], bw[i], acc[i][tb]);
-                __builtin_amdgcn_sched_barrier(0);
             }
-            return;
-        }
 #pragma unroll
-        for (uint32_t q = 0; q < 2; q++) {
-            const uint32_t kt = 2u * s + q;
-            float sc[kSG];
+            for (uint32_t i = 0; i < kSG; i++)
 #pragma unroll
-            for (uint32_t i = 0; i < kSG; i++) sc[i] = kt < nkg ? e8m0f((W.s[i] >> (8u * (kt % 4u))) & 0xFFu) : 0.f;
-#pragma unroll
-            for (uint32_t jj = 0; jj < 4; jj++) {
-                bf16x8 bw[kSG];
-#pragma unroll
-                for (uint32_t i = 0; i < kSG; i++) bw[i] = fp4x8_bf16(W.w[2u * i + q][jj], sc[i]);
-                // the activation fragments of this k step (columns q * 128 +
-                // 32 g + 8 jj), one plane at a time, shared by the kSG slices
-#pragma unroll
-                for (uint32_t pc = 0; pc < NP; pc++) {
-                    bf16x8 af[NB];
-#pragma unroll
-                    for (uint32_t tb = 0; tb < NB; tb++) af[tb] = afrag(sl, pc, tb, q, lo_r[jj]);
-#pragma unroll
-                    for (uint32_t i = 0; i < kSG; i++)
-#pragma unroll
-                        for (uint32_t tb = 0; tb < NB; tb++) acc[i][tb] = mma(af[tb], bw[i], acc[i][tb]);
-                }
-                __builtin_amdgcn_sched_barrier(0);  // keeps one k step's operands live at a time
-            }
+                for (uint32_t tb = 0; tb < NB; tb++) acc[i][tb] = mma(af[c][tb], bw[i], acc[i][tb]);
+            __builtin_amdgcn_sched_barrier(0);
         }
     }
     WL_MEM void compute(uint32_t s, const uint8_t* sl, const WBuf& W) {
@@ -826,6 +813,8 @@ struct UpK {
     WL_MEM void finish() {
         const uint32_t ln = opaque_lane();
         if (cu.sh) {
+#pragma unroll
+            for (uint32_t tb = 0; tb < 2; tb++) acc[0][tb] = (acc[0][tb] + acc[1][tb]) + (acc[2][tb] + acc[3][tb]);
             swiglu_store(acc[0], cu.nt, cps.pr, ln, [&](uint32_t m, uint32_t n, float x) {
                 store3(b.smid3 + (size_t)(cu.row0 + m) * 3u * SI + cu.part * kSlice + v * 8u + n, SI, x);
             });
@@ -973,41 +962,65 @@ struct DownK {
 #pragma unroll
             for (uint32_t xy = 0; xy < 2; xy++) d[h][xy][0] = d[h][xy][1] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
+    // Shared: as UpK::comp_shared, MFMA it (k step k, plane pc, block tb)
+    // into accumulator j = (NP k + pc) % 4 of block tb (d[j >> 1][j & 1][tb]),
+    // fragments read kSPD MFMAs ahead; finish() adds the four.
+    static constexpr uint32_t kSPD = 6;
     template <uint32_t NB, uint32_t NP>
     WL_MEM void comp_shared(uint32_t st, const uint8_t* sl, const WBuf& W) {
+        constexpr uint32_t N = 8u * NP * NB;
+        bf16x8 af[kSPD + 1u];
+        auto frag = [&](uint32_t it) {  // it = (k NP + pc) NB + tb
+            const uint32_t tb = it % NB, pc = (it / NB) % NP, k = it / (NB * NP);
+            return afrag(sl, pc, tb, k / 4u, lo_s[k % 4u]);
+        };
 #pragma unroll
-        for (uint32_t k = 0; k < 8u; k++) {
+        for (uint32_t it = 0; it < kSPD && it < N; it++) af[it] = frag(it);
+#pragma unroll
+        for (uint32_t it = 0; it < N; it++) {
+            const uint32_t tb = it % NB, kp = it / NB, k = kp / NP, j = kp % 4u;
+            if (it + kSPD < N) af[(it + kSPD) % (kSPD + 1u)] = frag(it + kSPD);
             const u32x4 z = {0u, 0u, 0u, 0u};
             const bf16x8 bw = as_bf16x8(8u * st + k < nks ? W.w[k] : z);
-#pragma unroll
-            for (uint32_t tb = 0; tb < NB; tb++)
-#pragma unroll
-                for (uint32_t pc = 0; pc < NP; pc++)
-                    d[0][0][tb] = mma(afrag(sl, pc, tb, k / 4u, lo_s[k % 4u]), bw, d[0][0][tb]);
+            d[j >> 1][j & 1u][tb] = mma(af[it % (kSPD + 1u)], bw, d[j >> 1][j & 1u][tb]);
             __builtin_amdgcn_sched_barrier(0);
         }
     }
+    // Routed: iteration it = NB NP (2 s4 + f) + NP tb + pc runs the fragment
+    // of plane pc, block tb at column half f of slice s4 against both row
+    // pairs; the next iteration's fragment is read while this one's four
+    // MFMAs run.
     template <uint32_t NB, uint32_t NP>
     WL_MEM void comp_routed(uint32_t st, const uint8_t* sl, const WBuf& W) {
         const uint32_t q0 = min(cu.part * 16u + 2u * v, nq - 1u);
+        constexpr uint32_t NI = NB * NP, N = 8u * NI;
+        auto frag = [&](uint32_t it) {
+            const uint32_t o = it / NI, in = it % NI, s4 = o / 2u, f = o % 2u;
+            return afrag(sl, in % NP, in / NP, s4 / 2u, lo_r[s4 % 2u][f]);
+        };
+        bf16x8 af[2];
+        af[0] = frag(0u);
+        float scx[2], scy[2];
+        bf16x8 bx[2], by[2];
 #pragma unroll
-        for (uint32_t s4 = 0; s4 < 4; s4++) {
-            const bool valid = st * 4u + s4 < NS;
-            float scx[2], scy[2];
+        for (uint32_t it = 0; it < N; it++) {
+            const uint32_t o = it / NI, in = it % NI, s4 = o / 2u, f = o % 2u, tb = in / NP;
+            if (it + 1u < N) af[(it + 1u) % 2u] = frag(it + 1u);
+            if (in == 0u) {
+                if (f == 0u) {
+                    const bool valid = st * 4u + s4 < NS;
 #pragma unroll
-            for (uint32_t h = 0; h < 2; h++) {
-                const uint32_t sbyte = (W.s[s4] >> (8u * ((q0 + h) % 4u))) & 0xFFu;
-                uint32_t sx, sy;
-                swap32(sbyte, sbyte, sx, sy);
-                scx[h] = valid ? e8m0f(sx) : 0.f;
-                scy[h] = valid ? e8m0f(sy) : 0.f;
-            }
-            // Column half f of the slice: lane group g's columns s4 * 64 +
-            // 32 (g & 1) + 8 (g >> 1) + 16 f (the swap order), from dwords
-            // 2f, 2f + 1 of each row pair's chunk.
-#pragma unroll
-            for (uint32_t f = 0; f < 2; f++) {
-                bf16x8 bx[2], by[2];
+                    for (uint32_t h = 0; h < 2; h++) {
+                        const uint32_t sbyte = (W.s[s4] >> (8u * ((q0 + h) % 4u))) & 0xFFu;
+                        uint32_t sx, sy;
+                        swap32(sbyte, sbyte, sx, sy);
+                        scx[h] = valid ? e8m0f(sx) : 0.f;
+                        scy[h] = valid ? e8m0f(sy) : 0.f;
+                    }
+                }
+                // Column half f of the slice: lane group g's columns s4 * 64 +
+                // 32 (g & 1) + 8 (g >> 1) + 16 f (the swap order), from dwords
+                // 2f, 2f + 1 of each row pair's chunk.
 #pragma unroll
                 for (uint32_t h = 0; h < 2; h++) {
                     const u32x4 w = W.w[2u * s4 + h];
@@ -1016,20 +1029,14 @@ struct DownK {
                     bx[h] = fp4x8_bf16(x, scx[h]);
                     by[h] = fp4x8_bf16(y, scy[h]);
                 }
-#pragma unroll
-                for (uint32_t tb = 0; tb < NB; tb++) {
-#pragma unroll
-                    for (uint32_t pc = 0; pc < NP; pc++) {
-                        const bf16x8 af = afrag(sl, pc, tb, s4 / 2u, lo_r[s4 % 2u][f]);
-#pragma unroll
-                        for (uint32_t h = 0; h < 2; h++) {
-                            d[h][0][tb] = mma(af, bx[h], d[h][0][tb]);
-                            d[h][1][tb] = mma(af, by[h], d[h][1][tb]);
-                        }
-                    }
-                }
             }
-            __builtin_amdgcn_sched_barrier(0);  // keeps one slice's operands live at a time
+            const bf16x8 a = af[it % 2u];
+#pragma unroll
+            for (uint32_t h = 0; h < 2; h++) {
+                d[h][0][tb] = mma(a, bx[h], d[h][0][tb]);
+                d[h][1][tb] = mma(a, by[h], d[h][1][tb]);
+            }
+            __builtin_amdgcn_sched_barrier(0);
         }
     }
     WL_MEM void compute(uint32_t st, const uint8_t* sl, const WBuf& W) {
@@ -1043,6 +1050,9 @@ struct DownK {
     WL_MEM void finish() {
         const uint32_t ln = opaque_lane(), nn = ln & 15u;
         if (cu.sh) {
+#pragma unroll
+            for (uint32_t tb = 0; tb < 2; tb++)
+                d[0][0][tb] = (d[0][0][tb] + d[0][1][tb]) + (d[1][0][tb] + d[1][1][tb]);
             const uint32_t r = cu.part * 128u + 16u * v + nn;
             if (r < H)
                 tile_each(d[0][0], cu.nt, cps.pr, ln,
