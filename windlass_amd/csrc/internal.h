@@ -99,8 +99,8 @@ struct DecodeArgs {
     float* shared_out;          // [H] (written when taps are on)
     // cross-work-group arrays (agent-scope stores and loads)
     uint64_t* lslot;            // [E] logit of this call: epoch << 32 | f32 bits
-    uint64_t* part;             // [H/32][G][32] partials, block-major, epoch << 32 | f32 bits
-    uint64_t* tsh;              // [H/32][G][32] shared-expert partials (taps on), tagged likewise
+    uint32_t* part;             // [H/32][G][32] partials, block-major: f32 at 21 mantissa bits | 2-bit call tag
+    uint32_t* tsh;              // [H/32][G][32] shared-expert partials (taps on), tagged likewise
     uint32_t* sync;             // synchronisation block (SyncMap), uncached
     uint32_t H, I, E, K, SI;
     float eps, scaling;
@@ -126,7 +126,8 @@ struct DecodeDyn {
     const uint16_t* router_w;   // [E][H] bf16
     const uint16_t* ln_w;       // [H] bf16 or null (= ones)
     uint64_t* lslot;            // [E] the context's epoch-tagged logit slots
-    uint32_t seg;               // bits 0-7: first segment, 8-15: last segment, 16: shared-expert tap on
+    uint32_t seg;               // bits 0-7: first segment, 8-15: last segment, 16: shared-expert tap on,
+                                // 24-25: the partials' tag of this call (1-3, differs from the previous call's)
     uint32_t epoch;             // different for every call of the context, never 0
     // not preloaded (read later in the layer)
     const float* bias;          // [E] f32
@@ -136,6 +137,7 @@ struct DecodeDyn {
     __host__ __device__ uint32_t seg_lo() const { return seg & 0xFFu; }
     __host__ __device__ uint32_t seg_hi() const { return (seg >> 8) & 0xFFu; }
     __host__ __device__ int32_t taps() const { return (int32_t)((seg >> 16) & 1u); }
+    __host__ __device__ uint32_t ptag() const { return (seg >> 24) & 3u; }
 };
 // Dwords of kernel arguments the decode kernel preloads into SGPRs (the
 // record pointer, then hidden .. epoch).

@@ -2,9 +2,11 @@
 //
 // One persistent launch of G work-groups (one per CU, 8 wave64s each) runs a
 // layer in two segments (the phased schedule launches each on its own). No
-// grid barrier: values another work-group needs (a logit, a partial sum) are
-// 64-bit words epoch << 32 | f32 bits written with agent-scope stores, and the
-// reader polls, with a bounded wait, until it sees this call's epoch.
+// grid barrier: values another work-group needs are written with agent-scope
+// stores and carry a tag of this call, and the reader polls, with a bounded
+// wait, until it sees that tag: a logit is a 64-bit word epoch << 32 | f32
+// bits; a partial sum is a 32-bit word, the f32 rounded to 21 stored mantissa
+// bits with the call's 2-bit tag (1, 2 or 3) in the freed low bits.
 //
 //   0  every work-group normalises the hidden state (RMSNorm, redundantly),
 //      computes its router row and publishes the logit, and streams one
@@ -72,6 +74,16 @@ __device__ uint64_t g_tl[kMaxGrid * 16];
 // store, so a reader that sees the epoch sees the value.
 WL_DEV void st_tag(uint64_t* p, uint32_t epoch, float x) {
     __hip_atomic_store((__attribute__((address_space(1))) uint64_t*)p, ((uint64_t)epoch << 32) | __float_as_uint(x),
+                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// A partial sum with this call's tag (1-3): the f32 rounded to nearest at 21
+// stored mantissa bits (the combine's error grows from 2.0e-7 to 2.5e-7 of
+// the output scale at the GLM shape), the tag in the two freed low bits; one
+// 4-byte agent-scope store, so a reader that sees the tag sees the value.
+// Every call writes every word of the partial arrays, so a word still holding
+// an older call's tag is stale (consecutive calls' tags differ).
+WL_DEV void st_part(uint32_t* p, uint32_t tag, float x) {
+    __hip_atomic_store((__attribute__((address_space(1))) uint32_t*)p, ((__float_as_uint(x) + 2u) & ~3u) | tag,
                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
@@ -352,6 +364,18 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const float* hidden, const 
             return true;
         };
 
+        // pv -> rows [32b, 32b+32) into block b, slot w of dst ([H/32][G][32]),
+        // tagged with this call's tag (each thread stores the rows it wrote)
+        auto publish = [&](uint32_t* dst) {
+            for (uint32_t r = tid; r < H; r += kThreads)
+                st_part(dst + ((size_t)(r / kRowBlock) * G + w) * kRowBlock + r % kRowBlock, d.ptag(), pv[r]);
+        };
+        // A work-group that leaves an aborted call still writes its words (pv
+        // as it stands), so the arrays keep holding one call's tags.
+        auto leave = [&]() {
+            publish(a.part);
+            if (d.taps()) publish(a.tsh);
+        };
         // shared expert: SwiGLU of each tile's 8 rows, then those 8 columns of
         // the down projection applied to every output row, into pv
         const uint32_t ntiles = w < nsg ? cdiv(nsg - w, G) : 0u;
@@ -414,7 +438,7 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const float* hidden, const 
             sd_issue(tile);
             if (lane < 16) red[v * 64 + n] = sum3(gacc);
             if (!routed) {
-                if (!route()) return;
+                if (!route()) return leave();
                 routed = true;
             }
             lds_barrier();
@@ -437,13 +461,7 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const float* hidden, const 
                 sd_pending = true;
             }
         }
-        if (!routed && !route()) return;
-        // pv -> rows [32b, 32b+32) into block b, slot w of dst ([H/32][G][32]),
-        // tagged with this call's epoch
-        auto publish = [&](uint64_t* dst) {
-            for (uint32_t r = tid; r < H; r += kThreads)
-                st_tag(dst + ((size_t)(r / kRowBlock) * G + w) * kRowBlock + r % kRowBlock, d.epoch, pv[r]);
-        };
+        if (!routed && !route()) return leave();
         // the deferred down columns, then (taps on) the shared-expert
         // contribution alone, published for the tap
         bool tsh_pending = d.taps() != 0;
@@ -559,7 +577,7 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const float* hidden, const 
                     // to block q of the partials
                     if (valid && lane < 32) {
                         const float x = pv[q * 32u + lane] + wk * (lane < 16 ? s0 : s1);
-                        if (direct) st_tag(a.part + ((size_t)q * G + w) * kRowBlock + lane, d.epoch, x);
+                        if (direct) st_part(a.part + ((size_t)q * G + w) * kRowBlock + lane, d.ptag(), x);
                         else pv[q * 32u + lane] = x;
                     }
                 }
@@ -601,8 +619,8 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const float* hidden, const 
 
         // ---- publish this work-group's partial (the combine of block b reads
         // its G slots contiguously), unless the down items already did. No
-        // barrier follows: the combine waits for the epoch tags of the words
-        // it reads.
+        // barrier follows: the combine waits for the tags of the words it
+        // reads.
         if (!(direct && ran)) publish(a.part);
         lds_barrier();  // pv is the combine's staging area
         WL_TL(9);
@@ -615,28 +633,29 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const float* hidden, const 
         float* fin = pv;                   // [G][32]
         float* f2 = fin + (size_t)G * RB;  // [16][32]
         // sum of the G slots of block blkr of src; the result is in threads
-        // 0..31. Each thread reads 16-byte chunks (two tagged words) of the
+        // 0..31. Each thread reads 16-byte chunks (four tagged words) of the
         // block with agent-scope loads: all at once first, then, for chunks
-        // whose writer has not finished (an older epoch), again until this
-        // call's epoch shows (bounded; the error word ends the wait too).
-        auto block_total = [&](const uint64_t* src, uint32_t blkr) -> float {
-            const uint32_t nchunk = G * RB / 2u;
-            const rsrc_t rs = make_rsrc(src + (size_t)blkr * G * RB, G * RB * 8u);
-            constexpr uint32_t kGrp = 8;
+        // whose writers have not finished (an older call's tag), again until
+        // this call's tag shows (bounded; the error word ends the wait too).
+        auto block_total = [&](const uint32_t* src, uint32_t blkr) -> float {
+            const uint32_t nchunk = G * RB / 4u, tag = d.ptag();
+            const rsrc_t rs = make_rsrc(src + (size_t)blkr * G * RB, G * RB * 4u);
+            constexpr uint32_t kGrp = 4;
             for (uint32_t c0 = 0; c0 < nchunk; c0 += kThreads * kGrp) {
                 u32x4 q[kGrp];
 #pragma unroll
                 for (uint32_t i = 0; i < kGrp; i++) q[i] = bld16_ag(rs, 16u * (c0 + tid + kThreads * i), 0u);
-                uint32_t stale = 0;  // bit i: chunk i still holds an older epoch
+                uint32_t stale = 0;  // bit i: chunk i still holds an older call's tag
                 for (uint32_t spins = 0;; spins++) {
 #pragma unroll
                     for (uint32_t i = 0; i < kGrp; i++) {
                         const uint32_t ch = c0 + tid + kThreads * i;
                         const bool mine = ch < nchunk && (spins == 0 || ((stale >> i) & 1u));
                         if (!mine) continue;
-                        if (q[i].y == d.epoch && q[i].w == d.epoch) {
-                            fin[2u * ch] = __uint_as_float(q[i].x);
-                            fin[2u * ch + 1u] = __uint_as_float(q[i].z);
+                        if (((q[i].x & 3u) == tag) & ((q[i].y & 3u) == tag) & ((q[i].z & 3u) == tag) &
+                            ((q[i].w & 3u) == tag)) {
+                            *(float4*)(fin + 4u * ch) = make_float4(__uint_as_float(q[i].x & ~3u), __uint_as_float(q[i].y & ~3u),
+                                                                    __uint_as_float(q[i].z & ~3u), __uint_as_float(q[i].w & ~3u));
                             stale &= ~(1u << i);
                         } else {
                             stale |= 1u << i;

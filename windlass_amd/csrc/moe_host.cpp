@@ -103,8 +103,9 @@ struct wl_ctx {
     int32_t taps = 1;
     // cross-work-group arrays (agent-scope stores and loads)
     uint64_t* lslot = nullptr;
-    uint64_t* part = nullptr;
-    uint64_t* tsh = nullptr;
+    uint32_t* part = nullptr;
+    uint32_t* tsh = nullptr;
+    uint32_t ptag = 0;  // the partials' tag of the last decode call: 1, 2, 3, 1, ...
     uint32_t* sync = nullptr;   // barrier words (uncached)
     wl::SyncMap sm{};
     wl::Plan plan{};
@@ -330,8 +331,8 @@ wl_status wl_create(const wl_moe_config* cfg, wl_ctx** out) {
         (s = dalloc(c, &c->ffn_mid_p, 2 * 3 * (size_t)I)) != WL_OK ||
         (s = dalloc(c, &c->logits, 4 * (size_t)E)) != WL_OK ||
         (s = dalloc(c, &c->lslot, 8 * (size_t)E)) != WL_OK ||
-        (s = dalloc(c, &c->part, 8 * (size_t)H * grid)) != WL_OK ||
-        (s = dalloc(c, &c->tsh, 8 * (size_t)H * grid)) != WL_OK) {
+        (s = dalloc(c, &c->part, 4 * (size_t)H * grid)) != WL_OK ||
+        (s = dalloc(c, &c->tsh, 4 * (size_t)H * grid)) != WL_OK) {
         wl_destroy(c);
         return s;
     }
@@ -356,8 +357,9 @@ wl_status wl_create(const wl_moe_config* cfg, wl_ctx** out) {
     // epoch 0 is never a call's: zeroed tagged arrays hold no valid word (a
     // reused allocation could otherwise carry another context's tags)
     if (e == hipSuccess) e = hipMemset(c->lslot, 0, 8 * (size_t)E);
-    if (e == hipSuccess) e = hipMemset(c->part, 0, 8 * (size_t)H * grid);
-    if (e == hipSuccess) e = hipMemset(c->tsh, 0, 8 * (size_t)H * grid);
+    // tag 0 is never a call's either
+    if (e == hipSuccess) e = hipMemset(c->part, 0, 4 * (size_t)H * grid);
+    if (e == hipSuccess) e = hipMemset(c->tsh, 0, 4 * (size_t)H * grid);
     if (e == hipSuccess) e = hipMemset(c->uc_block, 0, c->uc_bytes);
     if (e == hipSuccess) e = hipDeviceSynchronize();
     if (e != hipSuccess) { wl_destroy(c); return WL_ERR_HIP; }
@@ -799,6 +801,9 @@ static wl_status run_layer(wl_ctx* c, uint32_t layer, const float* d_hidden, con
     wl::DecodeDyn dyn{};
     if (++c->epoch >= 0x7FFFFFFFu) c->epoch = 1;
     dyn.epoch = c->epoch;
+    // per decode call (the routing launches also take epochs), so consecutive
+    // calls' partials never share a tag
+    c->ptag = c->ptag % 3u + 1u;
     dyn.hidden = d_hidden;
     dyn.sh_native = L.shared;
     dyn.router_w = L.router_w;
@@ -809,7 +814,7 @@ static wl_status run_layer(wl_ctx* c, uint32_t layer, const float* d_hidden, con
     dyn.resid = d_resid;
     dyn.out = d_out;
     auto launch = [&](uint32_t lo, uint32_t hi) -> wl_status {
-        dyn.seg = lo | (hi << 8) | ((c->taps ? 1u : 0u) << 16);
+        dyn.seg = lo | (hi << 8) | ((c->taps ? 1u : 0u) << 16) | (c->ptag << 24);
         int e = wl::launch_decode(c->d_largs + layer, dyn, H, I, SI, E, K, c->grid,
                                   L.shared_dtype == WL_SHARED_MXFP4, stream);
         if (e != 0) return hip_fail(c, (hipError_t)e, "decode launch");
@@ -1410,8 +1415,11 @@ wl_status wl_check_error(wl_ctx* c, void* stream) {
     e = hipMemcpy(&flag, c->sync + c->sm.error, 4, hipMemcpyDeviceToHost);
     if (e != hipSuccess) return hip_fail(c, e, "error flag read");
     if (flag) {
-        // a launch that gave up may have left barrier counters mid-count
+        // a launch that gave up may have left barrier counters mid-count, and
+        // partial words of an older call whose tag a later call would reuse
         (void)hipMemset(c->sync, 0, 4 * (size_t)c->sm.words);
+        (void)hipMemset(c->part, 0, 4 * (size_t)c->cfg.hidden * c->grid);
+        (void)hipMemset(c->tsh, 0, 4 * (size_t)c->cfg.hidden * c->grid);
         (void)hipDeviceSynchronize();
         return fail(c, WL_ERR_DEVICE, "device error bits 0x%x%s%s", flag,
                     (flag & wl::E_SPIN) ? " [dependency wait expired]" : "",
