@@ -221,6 +221,39 @@ def test_generic_shapes(gpu, shape):
     dm.ctx.close()
 
 
+def test_partial_tags_over_consecutive_calls(gpu):
+    """The combine takes a partial word as this call's only when its 2-bit
+    tag matches, and the tag repeats every third call: eight back-to-back
+    calls with a different hidden state each (both schedules, the shared tap
+    on and off, two layers), nothing synchronised between them, each output
+    against the oracle. A stale word accepted as fresh would carry another
+    call's input."""
+    c = dict(hidden=384, moe_inter=256, n_routed_experts=48, n_experts_per_tok=6, n_shared=1,
+             routed_scaling=2.5, rms_eps=1e-5)
+    H, I = c["hidden"], c["moe_inter"]
+    dm = DeviceModel(c, seed=5, n_layers=2)
+    src = O.ExpertSource(H, I, 5)
+    n = 8
+    hs = [synth.hidden_state(H, 300 + i) for i in range(n)]
+    dhs, douts = [], []
+    for i in range(n):
+        dh, dout = make_io(H)
+        dh.upload(hs[i])
+        dhs.append(dh)
+        douts.append(dout)
+    for i in range(n):
+        dm.ctx.set_schedule(moe.SCHED_PHASED if i % 3 == 1 else moe.SCHED_FUSED)
+        dm.ctx.set_taps(i % 2 == 0)
+        dm.ctx.run_moe(i % 2, dhs[i].ptr, douts[i].ptr)
+    dm.ctx.check_error()
+    for i in range(n):
+        ref = O.moe_layer(hs[i], dm.dense[i % 2], src, i % 2, c)["out"]
+        r = O.rel_to_scale(ref, douts[i].download(np.float32))
+        assert r < TOL, (i, r)
+    dm.ctx.set_schedule(moe.SCHED_FUSED)
+    dm.ctx.close()
+
+
 def test_chain_residual(gpu):
     """h <- h + moe(h) over 3 layers, 2 steps (the MoE half of run_chain)."""
     hip = gpu
