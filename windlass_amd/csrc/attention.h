@@ -74,8 +74,13 @@ struct AttnPtrs {
     float* q_rope;         // [HN][RP]
     float* rope_cs;        // [RP] cos | sin of the position (written by the prep kernel)
     float* isc;            // [T] index scores
-    uint8_t* keep;         // [T] 1: key kept (written by owner layers; null: every key kept)
-    uint32_t kps;          // keys per split (multiple of 32)
+    uint8_t* keep;         // [T] 1: key kept (written by owner layers)
+    uint32_t* klist;       // [max_seq + 1]: the kept keys in ascending order, [max_seq] = their count
+    uint32_t max_seq;
+    uint32_t kps;          // kept keys per split (multiple of 32)
+    uint32_t count;        // kept keys: min(T, TOPK)
+    uint32_t ident;        // 1: every key kept (klist is 0, 1, ..., T - 1 and is not read)
+    uint32_t nsplit;       // splits (slots of part_m / part_l / part_ctx)
     float* part_m;         // [S][HN]
     float* part_l;         // [S][HN]
     float* part_ctx;       // [S][HN][L]
@@ -91,10 +96,10 @@ int launch_attn_prep(const Shape& s, const AttnPtrs& p, uint32_t pos, bool owner
 // layers, of the indexer query (in place).
 int launch_attn_absorb(const Shape& s, const AttnPtrs& p, uint32_t pos, bool owner, void* stream);
 // Index scores over T keys, then the keep mask of the top-k (all kept when
-// T <= TOPK).
+// T <= TOPK) and the list of the kept keys.
 int launch_index_select(const Shape& s, const AttnPtrs& p, uint32_t T, void* stream);
-// Scores, softmax and context over T keys (keep mask applied), in S splits,
-// then the combine into ctx.
+// Scores, softmax and context over the kept keys of klist (T keys at
+// position T - 1), in S splits, then the combine into ctx.
 uint32_t attn_splits(const Shape& s, uint32_t T, uint32_t max_splits);
 size_t attn_split_lds(const Shape& s);
 int launch_attn_core(const Shape& s, const AttnPtrs& p, uint32_t T, uint32_t splits, void* stream);

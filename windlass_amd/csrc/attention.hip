@@ -421,15 +421,23 @@ WL_DEV uint32_t okey(float f) {
 }
 
 // keep[t] = 1 for the TOPK largest scores of [0, T) (ties to the lowest
-// index), every key when T <= TOPK. One work-group: a radix select of the
-// TOPK-th largest key (4 passes of 8 bits), then the marking.
-__global__ __launch_bounds__(1024) void index_topk_kernel(const float* isc, uint8_t* keep, uint32_t T, uint32_t K) {
+// index), every key when T <= TOPK; klist[0, count) the kept keys in
+// ascending order and klist[max_seq] = count (the list the attention core
+// walks). One work-group: a radix select of the TOPK-th largest key (4
+// passes of 8 bits), then the marking, then the list (each thread's kept
+// keys at the exclusive prefix of the threads' counts).
+__global__ __launch_bounds__(1024) void index_topk_kernel(const float* isc, uint8_t* keep, uint32_t* klist,
+                                                          uint32_t max_seq, uint32_t T, uint32_t K) {
     __shared__ uint32_t hist[256];
     __shared__ uint32_t cnt[16];
     __shared__ uint32_t sh_prefix, sh_kk;
     const uint32_t tid = threadIdx.x;
     if (T <= K) {
-        for (uint32_t t = tid; t < T; t += 1024) keep[t] = 1;
+        for (uint32_t t = tid; t < T; t += 1024) {
+            keep[t] = 1;
+            klist[t] = t;
+        }
+        if (tid == 0) klist[max_seq] = T;
         return;
     }
     uint32_t prefix = 0, mask = 0, kk = K;
@@ -482,6 +490,7 @@ __global__ __launch_bounds__(1024) void index_topk_kernel(const float* isc, uint
     __syncthreads();
     uint32_t before = inc - eq;
     for (uint32_t w = 0; w < (tid >> 6); w++) before += cnt[w];
+    uint32_t mine = 0;
     for (uint32_t t = t0; t < t1; t++) {
         const uint32_t u = okey(isc[t]);
         uint8_t k = u > prefix;
@@ -490,146 +499,215 @@ __global__ __launch_bounds__(1024) void index_topk_kernel(const float* isc, uint
             before++;
         }
         keep[t] = k;
+        mine += k;
     }
+    // the list: exclusive prefix of the kept counts, as above
+    __syncthreads();  // cnt is free again
+    inc = mine;
+    for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t v = __shfl_up(inc, o, 64);
+        if ((tid & 63) >= (uint32_t)o) inc += v;
+    }
+    if ((tid & 63) == 63) cnt[tid >> 6] = inc;
+    __syncthreads();
+    uint32_t at = inc - mine;
+    for (uint32_t w = 0; w < (tid >> 6); w++) at += cnt[w];
+    for (uint32_t t = t0; t < t1; t++)
+        if (keep[t]) klist[at++] = t;
+    if (tid == 0) klist[max_seq] = K;
 }
 
-// Attention over keys [s kps, min(T, (s + 1) kps)) for heads [hg 16,
-// hg 16 + 16) (all heads when fewer): 32 keys at a time staged in LDS
-// (kv_c | k_rot per row). Scores: thread = (4 heads x 4 keys tile, one of 8
-// column parts), the parts summed by shuffles. Online softmax per head.
-// Context: thread = (4 heads x 8 columns) over the chunk's keys. Partial
-// max, sum and unnormalised context go to the split's slots.
+// Attention over the kept keys klist[sp kps, min(count, (sp + 1) kps)) (the
+// selection in ascending key order, count = klist[max_seq]) for heads
+// [hg 16, hg 16 + 16) (all heads when fewer), 32 keys at a time, on the
+// matrix cores (v_mfma_f32_16x16x4_f32: f32 products and sums). LDS rows of
+// W16 = W rounded up to 16 floats (zero past W) at a stride of W16 + 4 floats
+// (an odd number of 16-byte groups, so the 16 rows an MFMA operand reads sit
+// in different banks): the queries qa [16][.] and the chunk's rows kv [32][.]
+// (kv_c | k_rot of each key, zero rows past the chunk).
+//   scores  S[16 heads][32 keys]: wave w takes key tile w & 1 and the 16-float
+//           column blocks b = (w >> 1) + 4i; lane (n, g) reads floats
+//           [16 b + 4 g, +4) of query row n and of key row n of the tile (one
+//           16-byte read each) and feeds them to 4 MFMAs (k index g), so the
+//           4 partial tiles of a key tile sum to the full dot products;
+//   softmax online per head (running max, sum and rescale of the context);
+//   context C[16 heads][L] += P[16][32] V[32][L]: wave w owns column tiles
+//           w + 8 i, 8 MFMAs (4 keys each) per tile per chunk.
+// The split's max, sum and unnormalised context go to its slots.
 constexpr uint32_t kHG = 16;
 constexpr uint32_t kKeys = 32;
-constexpr uint32_t kSplitThreads = 512;  // two waves per SIMD hide the LDS latency of the tiles
+constexpr uint32_t kSplitThreads = 512;
+constexpr uint32_t kCT = 4;  // context column tiles per wave: L <= 512 = 8 waves x 4 x 16
+// float4 elements per thread of the query block (16 x W16/4) and of a chunk
+// (32 x W16/4), W <= 768
+constexpr uint32_t kQE = 6, kKE = 12;
 
-__global__ __launch_bounds__(kSplitThreads) void attn_split_kernel(Shape s, AttnPtrs p, uint32_t T) {
-    extern __shared__ float lds[];
-    const uint32_t tid = threadIdx.x;
+WL_DEV f32x4 mma_f32(float a, float b, f32x4 c) { return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0); }
+// Max / sum over each 32-lane half of the wave, in every lane of the half:
+// DPP within the 16-lane rows (pairs at xor 1 and 2, then the mirrored
+// 8-lane halves and rows), one permute across the two rows of the half.
+template <int CTRL>
+WL_DEV float dpp(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(x), __float_as_int(x), CTRL, 0xF, 0xF, false));
+}
+WL_DEV float half_max(float x) {
+    x = fmaxf(x, dpp<0xB1>(x));   // quad_perm [1,0,3,2]
+    x = fmaxf(x, dpp<0x4E>(x));   // quad_perm [2,3,0,1]
+    x = fmaxf(x, dpp<0x141>(x));  // row_half_mirror
+    x = fmaxf(x, dpp<0x140>(x));  // row_mirror
+    return fmaxf(x, __shfl_xor(x, 16, 32));
+}
+WL_DEV float half_sum(float x) {
+    x += dpp<0xB1>(x);
+    x += dpp<0x4E>(x);
+    x += dpp<0x141>(x);
+    x += dpp<0x140>(x);
+    return x + __shfl_xor(x, 16, 32);
+}
+
+__global__ __launch_bounds__(kSplitThreads) void attn_split_kernel(Shape s, AttnPtrs p) {
+    extern __shared__ __align__(16) float lds[];
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wv = tid >> 6;
+    const uint32_t n = lane & 15u, g = lane >> 4;
     const uint32_t HG = s.HN < kHG ? s.HN : kHG;
     const uint32_t NHG = s.HN / HG;
-    const uint32_t hg = blockIdx.x % NHG, sp = blockIdx.x / NHG;
-    const uint32_t L = s.L, RP = s.RP, W = L + RP, KS = W + 4;
-    float* qa = lds;                  // [kHG][KS]: q_abs | q_rope (rows >= HG zero)
-    float* kv = qa + kHG * KS;        // [kKeys][KS]
-    float* ps = kv + kKeys * KS;      // [kKeys][kHG] scores, then probabilities
-    float* al = ps + kKeys * kHG;     // [kHG] rescale of this chunk
-    float* mx = al + kHG;             // [kHG] running max
-    float* sm = mx + kHG;             // [kHG] running sum
-    for (Walk2 w(tid, kSplitThreads, W / 4); w.r < kHG; w.next()) {
-        const uint32_t h = w.r, c = 4 * w.c;
-        f32x4 v = {0.f, 0.f, 0.f, 0.f};
-        if (h < HG)
-            v = c < L ? *(const f32x4*)(p.q_abs + (size_t)(hg * HG + h) * L + c)
-                      : *(const f32x4*)(p.q_rope + (size_t)(hg * HG + h) * RP + (c - L));
-        *(f32x4*)(qa + h * KS + c) = v;
+    // work-group b runs on XCD b % 8: the head groups of split sp all run on
+    // XCD sp % 8, so the chunk rows one of them fetches serve the others from
+    // that XCD's L2 (the grid is NHG x the splits rounded up to 8)
+    const uint32_t xcd = blockIdx.x % 8u, slot = blockIdx.x / 8u;
+    const uint32_t hg = slot % NHG, sp = xcd + 8u * (slot / NHG);
+    if (sp >= p.nsplit) return;  // the grid's rounding: no split, no slots (the whole work-group)
+    const uint32_t L = s.L, RP = s.RP, W = L + RP, W16 = (W + 15u) & ~15u, KS = W16 + 4u;
+    const uint32_t NCT = (L + 15u) / 16u;
+    float* qa = lds;                // [kHG][KS]
+    float* kv = qa + kHG * KS;      // [kKeys][KS]
+    float* st = kv + kKeys * KS;    // [8 waves][16 x 16] partial score tiles
+    float* ps = st + 8u * 256u;     // [kKeys][kHG] scores, then probabilities
+    float* al = ps + kKeys * kHG;   // [kHG] rescale of this chunk
+    float* mx = al + kHG;           // [kHG] running max
+    float* sm = mx + kHG;           // [kHG] running sum
+    // every load of the queries and of a chunk is issued before any is
+    // stored, branch-free (an element outside the data loads from a valid
+    // address and is zeroed after), so they are all in flight together
+    const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
+    f32x4 qv[kQE];
+    uint32_t qok = 0;  // bit i: element i is inside the queries (the zeroing waits for the store)
+    {
+        Walk2 w(tid, kSplitThreads, W16 / 4);
+#pragma unroll
+        for (uint32_t i = 0; i < kQE; i++) {
+            const uint32_t h = w.r, c = 4 * w.c;
+            const bool ok = h < HG && c < W;
+            const float* src = c < L ? p.q_abs + (size_t)(hg * HG + h) * L + c
+                                     : p.q_rope + (size_t)(hg * HG + h) * RP + (c - L);
+            qv[i] = *(const f32x4*)(ok ? src : p.q_abs);
+            qok |= (ok ? 1u : 0u) << i;
+            w.next();
+        }
     }
     if (tid < kHG) {
         mx[tid] = -INFINITY;
         sm[tid] = 0.f;
     }
-    // score tile of this thread: 4 heads x 4 keys, one of 16 column parts
-    const uint32_t part = tid & 15, tile = tid >> 4;
-    const uint32_t th = (tile & 3) * 4, tk = (tile >> 2) * 4;
-    const uint32_t nch = W / 4;  // float4 columns
-    // context tile of this thread: 4 heads x 4 columns
-    const uint32_t ncg = L / 4;  // column groups
-    const uint32_t cg = tid % ncg, chg = tid / ncg;  // chg < 4: heads 4 chg .. 4 chg + 3
-    const bool cact = chg < 4;
-    const uint32_t cc = cg * 4;
-    float acc[4][4];
+    f32x4 acc[kCT];
 #pragma unroll
-    for (int a = 0; a < 4; a++)
+    for (uint32_t i = 0; i < kCT; i++) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const uint32_t k0 = sp * p.kps, k1 = (k0 + p.kps < p.count) ? k0 + p.kps : p.count;
+    const uint32_t tile = wv & 1u, kq = wv >> 1;
+    const Walk2 w0(tid, kSplitThreads, W16 / 4);
+    // the key of each element of chunk kb (the list, or the position itself
+    // when every key is kept; past the chunk's keys: 0)
+    uint32_t key[kKE];
+    auto load_keys = [&](uint32_t kb, uint32_t nk) {
+        const rsrc_t kl = make_rsrc(p.klist + kb, 4u * nk);
+        Walk2 w = w0;
 #pragma unroll
-        for (int e = 0; e < 4; e++) acc[a][e] = 0.f;
-    const uint32_t k0 = sp * p.kps, k1 = (k0 + p.kps < T) ? k0 + p.kps : T;
-    // the chunk's rows are read into registers one chunk ahead (each thread
-    // its kPf float4 of the 32 x W/4 grid), so their latency overlaps the
-    // previous chunk's compute
-    constexpr int kPf = 12;  // (kKeys x W/4) / kSplitThreads <= 12: W <= 768
-    f32x4 pf[kPf];
-    auto fetch = [&](uint32_t kb) {
-        const uint32_t nk = (k1 - kb) < kKeys ? (k1 - kb) : kKeys;
-        Walk2 w(tid, kSplitThreads, W / 4);
-#pragma unroll
-        for (int i = 0; i < kPf; i++) {
-            const uint32_t r = w.r, c = 4 * w.c;
-            f32x4 v = {0.f, 0.f, 0.f, 0.f};
-            if (r < nk)
-                v = c < L ? *(const f32x4*)(p.kv_c + (size_t)(kb + r) * L + c)
-                          : *(const f32x4*)(p.k_rot + (size_t)(kb + r) * RP + (c - L));
-            pf[i] = v;
+        for (uint32_t i = 0; i < kKE; i++) {
+            key[i] = p.ident ? kb + w.r : __builtin_amdgcn_raw_buffer_load_b32(kl, (int)(4u * w.r), 0, 0);
             w.next();
         }
     };
-    if (k0 < k1) fetch(k0);
+    // the first chunk's keys are in flight with the queries; the queries go
+    // to LDS while they arrive (qa is not read before the first barrier)
+    if (k0 < k1) load_keys(k0, (k1 - k0) < kKeys ? (k1 - k0) : kKeys);
+    {
+        Walk2 wq(tid, kSplitThreads, W16 / 4);
+#pragma unroll
+        for (uint32_t i = 0; i < kQE; i++) {
+            if (wq.r < kHG) *(f32x4*)(qa + wq.r * KS + 4 * wq.c) = ((qok >> i) & 1u) ? qv[i] : z4;
+            wq.next();
+        }
+    }
     for (uint32_t kb = k0; kb < k1; kb += kKeys) {
         const uint32_t nk = (k1 - kb) < kKeys ? (k1 - kb) : kKeys;
-        __syncthreads();
         {
-            Walk2 w(tid, kSplitThreads, W / 4);
+            f32x4 v[kKE];
+            if (kb != k0) load_keys(kb, nk);
+            Walk2 w = w0;
 #pragma unroll
-            for (int i = 0; i < kPf; i++) {
-                if (w.r < kKeys) *(f32x4*)(kv + w.r * KS + 4 * w.c) = pf[i];
+            for (uint32_t i = 0; i < kKE; i++) {
+                const uint32_t r = w.r, c = 4 * w.c;
+                const bool ok = r < nk && c < W;
+                const uint32_t k = ok ? key[i] : 0u;
+                const float* src = c < L ? p.kv_c + (size_t)k * L + c : p.k_rot + (size_t)k * RP + (c - L);
+                const f32x4 x = *(const f32x4*)(ok ? src : p.kv_c);
+                v[i] = ok ? x : z4;
+                w.next();
+            }
+            __syncthreads();  // the previous chunk's rows and probabilities are read
+            w = w0;
+#pragma unroll
+            for (uint32_t i = 0; i < kKE; i++) {
+                if (w.r < kKeys) *(f32x4*)(kv + w.r * KS + 4 * w.c) = v[i];
                 w.next();
             }
         }
         __syncthreads();
-        if (kb + kKeys < k1) fetch(kb + kKeys);
-        float t[4][4];
+        {
+            // two accumulators (even / odd column blocks), so consecutive
+            // MFMAs do not wait on each other
+            f32x4 t0 = {0.f, 0.f, 0.f, 0.f}, t1 = t0;
+            const float* qrow = qa + n * KS + 4u * g;
+            const float* krow = kv + (16u * tile + n) * KS + 4u * g;
+            const uint32_t NB = W16 / 16u;
+            uint32_t b = kq;
+            for (; b + 4u < NB; b += 8u) {
+                const f32x4 x0 = *(const f32x4*)(qrow + 16u * b), y0 = *(const f32x4*)(krow + 16u * b);
+                const f32x4 x1 = *(const f32x4*)(qrow + 16u * (b + 4u)), y1 = *(const f32x4*)(krow + 16u * (b + 4u));
 #pragma unroll
-        for (int a = 0; a < 4; a++)
-#pragma unroll
-            for (int b = 0; b < 4; b++) t[a][b] = 0.f;
-        for (uint32_t c4 = part; c4 < nch; c4 += 16) {
-            f32x4 x[4], y[4];
-#pragma unroll
-            for (int a = 0; a < 4; a++) x[a] = *(const f32x4*)(qa + (th + a) * KS + 4 * c4);
-#pragma unroll
-            for (int b = 0; b < 4; b++) y[b] = *(const f32x4*)(kv + (tk + b) * KS + 4 * c4);
-#pragma unroll
-            for (int a = 0; a < 4; a++)
-#pragma unroll
-                for (int b = 0; b < 4; b++) {
-                    t[a][b] += x[a][0] * y[b][0];
-                    t[a][b] += x[a][1] * y[b][1];
-                    t[a][b] += x[a][2] * y[b][2];
-                    t[a][b] += x[a][3] * y[b][3];
+                for (uint32_t i = 0; i < 4; i++) {
+                    t0 = mma_f32(x0[i], y0[i], t0);
+                    t1 = mma_f32(x1[i], y1[i], t1);
                 }
-        }
-#pragma unroll
-        for (int a = 0; a < 4; a++)
-#pragma unroll
-            for (int b = 0; b < 4; b++) {
-                t[a][b] += __shfl_xor(t[a][b], 1, 64);
-                t[a][b] += __shfl_xor(t[a][b], 2, 64);
-                t[a][b] += __shfl_xor(t[a][b], 4, 64);
-                t[a][b] += __shfl_xor(t[a][b], 8, 64);
             }
-        if (part == 0) {
+            if (b < NB) {
+                const f32x4 x0 = *(const f32x4*)(qrow + 16u * b), y0 = *(const f32x4*)(krow + 16u * b);
 #pragma unroll
-            for (int b = 0; b < 4; b++) {
-                const uint32_t key = tk + b;
-                const bool live = key < nk && (!p.keep || p.keep[kb + key]);
-#pragma unroll
-                for (int a = 0; a < 4; a++) ps[key * kHG + th + a] = live ? t[a][b] * p.qk_scale : -INFINITY;
+                for (uint32_t i = 0; i < 4; i++) t0 = mma_f32(x0[i], y0[i], t0);
             }
+            // lane (n, g) holds S[head 4 g + j][key 16 tile + n]
+#pragma unroll
+            for (uint32_t j = 0; j < 4; j++) st[wv * 256u + (4u * g + j) * 16u + n] = t0[j] + t1[j];
         }
         __syncthreads();
-        // online softmax: one wave per head at a time, lanes over the keys
-        for (uint32_t h = tid >> 6; h < HG; h += kSplitThreads / 64) {
-            const uint32_t ln = tid & 63;
-            const float v = ln < kKeys ? ps[ln * kHG + h] : -INFINITY;
-            float m = v;
-            for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+        // the four column-block partials (in block order), then the online
+        // softmax: two heads per wave, one per 32-lane half, lanes over the keys
+        {
+            const uint32_t h = wv + 8u * (lane >> 5), key = lane & 31u, t = key >> 4;
+            const uint32_t idx = h * 16u + (key & 15u);
+            float v = ((st[t * 256u + idx] + st[(2u + t) * 256u + idx]) + st[(4u + t) * 256u + idx]) +
+                      st[(6u + t) * 256u + idx];
+            v = key < nk ? v * p.qk_scale : -INFINITY;
+            const float m = half_max(v);
             const float mo = mx[h];
             const float mn = fmaxf(mo, m);
-            const float e = (ln < kKeys && v != -INFINITY) ? expf(v - mn) : 0.f;
-            float z = e;
-            for (int o = 32; o > 0; o >>= 1) z += __shfl_xor(z, o, 64);
-            const float a = (mo == -INFINITY) ? 0.f : expf(mo - mn);
-            if (ln < kKeys) ps[ln * kHG + h] = e;
-            if (ln == 0) {
+            const float e = v != -INFINITY ? expf(v - mn) : 0.f;
+            const float z = half_sum(e);
+            ps[key * kHG + h] = e;
+            // head h is this half-wave's alone; its LDS reads of mx[h] above
+            // precede the write below in the wave's program order
+            if (key == 0 && h < HG) {
+                const float a = (mo == -INFINITY) ? 0.f : expf(mo - mn);
                 const float r = (mn == -INFINITY) ? 1.f : a;
                 al[h] = r;
                 mx[h] = mn;
@@ -637,25 +715,18 @@ __global__ __launch_bounds__(kSplitThreads) void attn_split_kernel(Shape s, Attn
             }
         }
         __syncthreads();
-        if (cact) {
-            const uint32_t h0 = 4 * chg;
-            float r[4];
+        float r[4];
 #pragma unroll
-            for (int a = 0; a < 4; a++) r[a] = (h0 + a < HG) ? al[h0 + a] : 0.f;
+        for (uint32_t j = 0; j < 4; j++) r[j] = (4u * g + j < HG) ? al[4u * g + j] : 0.f;
 #pragma unroll
-            for (int a = 0; a < 4; a++)
+        for (uint32_t i = 0; i < kCT; i++) {
+            const uint32_t ct = wv + 8u * i;
+            if (ct < NCT) {
 #pragma unroll
-                for (int e = 0; e < 4; e++) acc[a][e] *= r[a];
-            for (uint32_t key = 0; key < nk; key++) {
-                const f32x4 w = *(const f32x4*)(ps + key * kHG + h0);
-                const f32x4 x = *(const f32x4*)(kv + key * KS + cc);
+                for (uint32_t j = 0; j < 4; j++) acc[i][j] *= r[j];
 #pragma unroll
-                for (int a = 0; a < 4; a++) {
-                    acc[a][0] += w[a] * x[0];
-                    acc[a][1] += w[a] * x[1];
-                    acc[a][2] += w[a] * x[2];
-                    acc[a][3] += w[a] * x[3];
-                }
+                for (uint32_t kk = 0; kk < kKeys / 4u; kk++)
+                    acc[i] = mma_f32(ps[(4u * kk + g) * kHG + n], kv[(4u * kk + g) * KS + 16u * ct + n], acc[i]);
             }
         }
     }
@@ -665,13 +736,14 @@ __global__ __launch_bounds__(kSplitThreads) void attn_split_kernel(Shape s, Attn
         p.part_m[(size_t)sp * s.HN + hb + tid] = mx[tid];
         p.part_l[(size_t)sp * s.HN + hb + tid] = sm[tid];
     }
-    if (cact) {
 #pragma unroll
-        for (int a = 0; a < 4; a++) {
-            const uint32_t h = 4 * chg + a;
-            if (h < HG) {
-                float* o = p.part_ctx + ((size_t)sp * s.HN + hb + h) * L + cc;
-                *(f32x4*)o = f32x4{acc[a][0], acc[a][1], acc[a][2], acc[a][3]};
+    for (uint32_t i = 0; i < kCT; i++) {
+        const uint32_t ct = wv + 8u * i, col = 16u * ct + n;
+        if (ct < NCT && col < L) {
+#pragma unroll
+            for (uint32_t j = 0; j < 4; j++) {
+                const uint32_t h = 4u * g + j;
+                if (h < HG) p.part_ctx[((size_t)sp * s.HN + hb + h) * L + col] = acc[i][j];
             }
         }
     }
@@ -758,15 +830,18 @@ int launch_index_select(const Shape& s, const AttnPtrs& p, uint32_t T, void* str
                        p, T);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return (int)e;
-    hipLaunchKernelGGL(index_topk_kernel, dim3(1), dim3(1024), 0, (hipStream_t)stream, (const float*)p.isc, p.keep, T,
-                       s.TOPK);
+    hipLaunchKernelGGL(index_topk_kernel, dim3(1), dim3(1024), 0, (hipStream_t)stream, (const float*)p.isc, p.keep,
+                       p.klist, p.max_seq, T, s.TOPK);
     return (int)hipGetLastError();
 }
 
+// Splits of the kept keys (at most min(T, TOPK) of them): about 512
+// work-groups, each split a multiple of 32 keys.
 uint32_t attn_splits(const Shape& s, uint32_t T, uint32_t max_splits) {
     const uint32_t HG = s.HN < kHG ? s.HN : kHG;
     const uint32_t NHG = s.HN / HG;
-    uint32_t S = (T + kKeys - 1) / kKeys;
+    const uint32_t nk = T < s.TOPK ? T : s.TOPK;
+    uint32_t S = (nk + kKeys - 1) / kKeys;
     const uint32_t want = (512 + NHG - 1) / NHG;
     if (S > want) S = want;
     if (S > max_splits) S = max_splits;
@@ -775,22 +850,27 @@ uint32_t attn_splits(const Shape& s, uint32_t T, uint32_t max_splits) {
 }
 
 size_t attn_split_lds(const Shape& s) {
-    return 4 * ((size_t)(kHG + kKeys) * (s.L + s.RP + 4) + (size_t)kKeys * kHG + 3 * kHG);
+    const size_t KS = ((s.L + s.RP + 15) & ~15u) + 4;
+    return 4 * ((size_t)(kHG + kKeys) * KS + 8 * 256 + (size_t)kKeys * kHG + 3 * kHG);
 }
 
 int launch_attn_core(const Shape& s, const AttnPtrs& p0, uint32_t T, uint32_t splits, void* stream) {
     AttnPtrs p = p0;
     const uint32_t HG = s.HN < kHG ? s.HN : kHG;
     const uint32_t NHG = s.HN / HG;
-    uint32_t kps = (T + splits - 1) / splits;
+    const uint32_t nk = T < s.TOPK ? T : s.TOPK;  // the selection's size
+    uint32_t kps = (nk + splits - 1) / splits;
     kps = (kps + kKeys - 1) / kKeys * kKeys;
-    const uint32_t S = (T + kps - 1) / kps;  // every split holds at least one key
+    const uint32_t S = (nk + kps - 1) / kps;  // every split holds at least one key
     p.kps = kps;
+    p.count = nk;
+    p.ident = T <= s.TOPK ? 1u : 0u;
     hipError_t ae = hipFuncSetAttribute((const void*)attn_split_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
                                         (int)attn_split_lds(s));
     if (ae != hipSuccess) return (int)ae;
-    hipLaunchKernelGGL(attn_split_kernel, dim3(NHG * S), dim3(kSplitThreads), attn_split_lds(s), (hipStream_t)stream,
-                       s, p, T);
+    p.nsplit = S;
+    hipLaunchKernelGGL(attn_split_kernel, dim3(NHG * ((S + 7u) / 8u) * 8u), dim3(kSplitThreads), attn_split_lds(s),
+                       (hipStream_t)stream, s, p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return (int)e;
     hipLaunchKernelGGL(attn_combine_kernel, dim3(s.HN * ((s.L + 255) / 256)), dim3(256), 0, (hipStream_t)stream, s, p,

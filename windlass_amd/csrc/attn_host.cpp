@@ -30,6 +30,7 @@ struct AttnLayer {
     float* k_rot = nullptr;  // [max_seq][RP]
     float* idx_k = nullptr;  // [max_seq][ID] (owner)
     uint8_t* keep = nullptr; // [max_seq] (owner)
+    uint32_t* klist = nullptr;  // [max_seq + 1] (owner): kept keys, then their count
 };
 
 }  // namespace
@@ -224,7 +225,8 @@ wl_status wl_attn_set_layer(wl_attn* a, uint32_t layer, const wl_attn_weights* w
     if (L.owner && !L.idx_k) {
         wl_status st;
         if ((st = dalloc(a, &L.idx_k, (size_t)a->cfg.max_seq * a->sh.ID * sizeof(float), true)) != WL_OK ||
-            (st = dalloc(a, &L.keep, a->cfg.max_seq, true)) != WL_OK)
+            (st = dalloc(a, &L.keep, a->cfg.max_seq, true)) != WL_OK ||
+            (st = dalloc(a, &L.klist, ((size_t)a->cfg.max_seq + 1) * sizeof(uint32_t), true)) != WL_OK)
             return st;
     }
     L.set = true;
@@ -257,14 +259,17 @@ wl_status wl_run_attention(wl_attn* a, uint32_t layer, uint32_t pos, float* d_hi
     const wl::attn::Shape& s = a->sh;
     const uint32_t T = pos + 1, DH = s.NP + s.RP;
     uint8_t* keep = nullptr;
+    uint32_t* klist = nullptr;
     if (!L.owner) {
         if (a->share_layer < 0 || a->share_pos != pos)
             return fail(a, WL_ERR_STATE,
                         "layer %u is \"shared\" and no indexer-owning layer published a selection at position %u", layer,
                         pos);
         keep = a->layers[a->share_layer].keep;
+        klist = a->layers[a->share_layer].klist;
     } else {
         keep = L.keep;
+        klist = L.klist;
     }
     hipStream_t st = (hipStream_t)stream;
     wl_status rs;
@@ -316,6 +321,8 @@ wl_status wl_run_attention(wl_attn* a, uint32_t layer, uint32_t pos, float* d_hi
     p.rope_cs = a->rope_cs;
     p.isc = a->isc;
     p.keep = keep;
+    p.klist = klist;
+    p.max_seq = a->cfg.max_seq;
     p.part_m = a->part_m;
     p.part_l = a->part_l;
     p.part_ctx = a->part_ctx;
