@@ -41,7 +41,9 @@
 // bf16 pieces x = hi + mid + lo (exact for fp32 x), one piece per A row, so
 // D[0..2][n] summed is the full-precision dot product of row n. MXFP4 weights
 // are widened to bf16 with v_cvt_scalef32_pk_bf16_fp4, which applies the E8M0
-// block scale exactly (e2m1 x 2^(s-127) is representable in bf16), low nibble =
+// block scale exactly (e2m1 x 2^(s-127) is a bf16 value, subnormal at s = 1,
+// except at s = 254 with |e2m1| >= 2, which overflows to inf and turns the
+// 3-piece product into NaN where an f32 product would give inf), low nibble =
 // even column as in the reference (src/glm_kernels.cuh:4-33).
 //
 // Weight loads are 16 bytes per lane (one 1 KB request per wave instruction)
