@@ -779,15 +779,16 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(Shape s, AttnPtrs p, 
 }  // namespace
 
 #ifndef WL_GEMV_TPR_MIN
-#define WL_GEMV_TPR_MIN 64
+#define WL_GEMV_TPR_MIN 32
 #endif
-// Threads per row: the fewest (from WL_GEMV_TPR_MIN, one wave: the sums need
-// no barrier) whose chunk iterations fit the kMaxIt input registers, then
-// doubled while the launch would have fewer than 512 work-groups (small
-// matrices: more, shorter work-groups spread the rows over the chip); never
-// more than the row has chunks. Measured on MI355X: 16384 x 2048 at 64
-// threads per row 3.6 TB/s (2.4 at 256), 2048 x 6144 at 256 2.7 TB/s (2.4 at
-// 64).
+// Threads per row: the fewest (from WL_GEMV_TPR_MIN; at most one wave, so the
+// sums need no barrier) whose chunk iterations fit the kMaxIt input
+// registers, then doubled while the launch would have fewer than 512
+// work-groups (small matrices: more, shorter work-groups spread the rows over
+// the chip); never more than the row has chunks. Measured on MI355X (µs,
+// wl_matvec_bf16): 16384 x 512 7.2 at 32 threads per row (9.2 at 64),
+// 16384 x 2048 17.0 at 32 (18.4 at 64, 2.4 TB/s at 256), 2048 x 6144 2.7 TB/s
+// at 128 (2.4 at 64); a minimum of 8 or 16 ends at the same 32 for these.
 uint32_t gemv_plan(GemvJob& j) {
     const uint32_t nch = j.K / 8;
     uint32_t l2 = 0;
