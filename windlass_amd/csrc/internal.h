@@ -47,12 +47,14 @@ enum : uint32_t {
 struct SyncMap {
     uint32_t error;
     uint32_t abort;
+    uint32_t ticket;  // [3] combine-ticket counters, one per partial tag (tag t: ticket + t - 1)
     uint32_t words;
     __host__ __device__ static SyncMap make() {
         SyncMap m;
         m.error = 0;
         m.abort = kLineWords / 2;
-        m.words = kLineWords;
+        m.ticket = kLineWords;
+        m.words = 2 * kLineWords;
         return m;
     }
 };
@@ -68,7 +70,9 @@ struct SyncMap {
 //   partials         every work-group's w_k-weighted routed and shared
 //                    contributions, summed per output row in LDS, published as
 //                    one H-vector per work-group of epoch-tagged words
-//   combine          H/32 blocks of 32 rows, block b on b mod G
+//   combine          H/32 blocks of 32 rows; the work-group that takes ticket t
+//                    (tickets in the order work-groups finish their own work)
+//                    combines blocks t, t + G, ...
 constexpr uint32_t kRowBlock = 32;  // rows per combine block (= rows per down item)
 struct Plan {
     uint32_t G, S, U, NB;

@@ -125,6 +125,10 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const float* hidden, const 
     const uint8_t** tk_blk = (const uint8_t**)(lds + L.slots);
     uint32_t* misc = (uint32_t*)(lds + L.misc);  // [0..8) vote flags, [8] barrier flag
     float* smf = (float*)(misc + 16);           // [8] this tile's shared SwiGLU values
+    // the next call's combine-ticket counter starts at zero: cleared first
+    // thing by the launch that holds the combine (the counter was last used
+    // two calls back, which has ended)
+    if (d.seg_hi() >= 1u && w == 0 && tid == 0) st_sync(a.sync + SM.ticket + d.ptag() % 3u, 0u);
 
     Batch bA, bB;
     using SB = std::conditional_t<SH4, SBatch4, SBatch>;
@@ -691,7 +695,14 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const float* hidden, const 
             lds_barrier();
             return o;
         };
-        for (uint32_t blkr = w; blkr < P.NB; blkr += G) {
+        // blocks go to work-groups in the order they get here (one ticket
+        // each), so the work-groups that finish their own work last do not
+        // also combine: with H/32 <= G they take no block
+        if (tid == 0) misc[9] = rmw_inc(a.sync + SM.ticket + d.ptag() - 1u);
+        lds_barrier();
+        const uint32_t t0 = uni(misc[9]);
+        WL_TL(11);
+        for (uint32_t blkr = t0; blkr < P.NB; blkr += G) {
             const uint32_t r = blkr * RB + tid;
             const float o = block_total(a.part, blkr);
             if (tid < RB) gst(d.out + r, d.resid ? __fadd_rn(gld(d.resid + r), o) : o);
