@@ -111,6 +111,32 @@ class DeviceModel(_Layers):
         return self._key(layer, expert)
 
 
+class AliasedModel(_Layers):
+    """Every (layer, expert) resident, bound to one of `n_blocks` device blocks:
+    (layer, expert) -> block (layer * E + expert) mod n_blocks, which holds the
+    synthetic expert (b // E, b % E). This is CachedModel's host mapping, so the
+    two compute the same layers: a resident counterpart for cache runs whose
+    distinct experts would not fit in HBM (75 GLM layers)."""
+
+    def __init__(self, cfg, seed, n_layers, n_blocks, ln_weights=None, bias_offset=None, shared_alias=False,
+                 shared_mxfp4=False):
+        super().__init__(cfg, seed, n_layers, ln_weights, bias_offset, shared_alias, shared_mxfp4)
+        self.n_blocks = n_blocks
+        E = self.E
+        self.ctx.slot_pool_create(n_blocks)
+        for b in range(n_blocks):
+            kl, ke = divmod(b, E)
+            moe.synth_expert_native(self.cfg, seed, kl, ke, self.ctx.slot_pool_ptr(b))
+        for l in range(n_layers):
+            for e in range(E):
+                self.ctx.slot_bind(l, e, self.ctx.slot_pool_ptr((l * E + e) % n_blocks))
+        self._bind_dense()
+        hip.synchronize()
+
+    def expert_source_key(self, layer, expert):
+        return divmod((layer * self.E + expert) % self.n_blocks, self.E)
+
+
 class CachedModel(_Layers):
     def __init__(self, cfg, seed, n_layers, capacity, n_host, ln_weights=None, bias_offset=None,
                  shared_alias=False, shared_mxfp4=False):
