@@ -88,16 +88,18 @@ struct AttnPtrs {
 };
 
 int launch_gemv(const GemvLaunch& l, uint32_t n_wg, void* stream);
-// After the first GEMV stage: the KV-cache row of `pos` (kv_a_layernorm of
-// the compressed KV, RoPE of the shared rope key) and, on owner layers, the
-// indexer key row (LayerNorm + RoPE) and the head weights' scale.
-int launch_attn_prep(const Shape& s, const AttnPtrs& p, uint32_t pos, bool owner, void* stream);
+// A GEMV launch of n_wg work-groups followed by the prep stage's work-groups:
+// the KV-cache row of `pos` (kv_a_layernorm of the compressed KV, RoPE of the
+// shared rope key) and, on owner layers, the indexer key row (LayerNorm +
+// RoPE) and the head weights' scale. Both read only the first GEMV stage.
+int launch_gemv_prep(const GemvLaunch& l, uint32_t n_wg, const Shape& s, const AttnPtrs& p, uint32_t pos, bool owner,
+                     void* stream);
 // q_abs[h] = q_nope[h] . W_kb[h]; RoPE of q_rot (into q_rope) and, on owner
-// layers, of the indexer query (in place).
-int launch_attn_absorb(const Shape& s, const AttnPtrs& p, uint32_t pos, bool owner, void* stream);
-// Index scores over T keys, then the keep mask of the top-k (all kept when
-// T <= TOPK) and the list of the kept keys.
-int launch_index_select(const Shape& s, const AttnPtrs& p, uint32_t T, void* stream);
+// layers, of the indexer query (into iqr), and the index scores over T keys.
+int launch_attn_absorb(const Shape& s, const AttnPtrs& p, bool owner, uint32_t T, void* stream);
+// The keep mask of the top-k of the index scores (all kept when T <= TOPK)
+// and the list of the kept keys.
+int launch_index_topk(const Shape& s, const AttnPtrs& p, uint32_t T, void* stream);
 // Scores, softmax and context over the kept keys of klist (T keys at
 // position T - 1), in S splits, then the combine into ctx.
 uint32_t attn_splits(const Shape& s, uint32_t T, uint32_t max_splits);
@@ -106,6 +108,8 @@ int launch_attn_core(const Shape& s, const AttnPtrs& p, uint32_t T, uint32_t spl
 
 // Work-group count of a GEMV job (sets tpr_log2, rows_wg).
 uint32_t gemv_plan(GemvJob& j);
+// Dynamic LDS bytes of the index-score work-groups.
+size_t index_score_lds(const Shape& s);
 
 }  // namespace attn
 }  // namespace wl

@@ -91,9 +91,9 @@ WL_DEV void group_sum(float (&v)[NV], uint32_t tpr_log2, float* red) {
     }
 }
 
-__global__ __launch_bounds__(kGemvThreads) void gemv_kernel(GemvLaunch L) {
+// Work-group b of a GEMV launch.
+WL_DEV void gemv_body(const GemvLaunch& L, uint32_t b) {
     __shared__ float red[(kGemvRows + 1) * 4];
-    const uint32_t b = blockIdx.x;
     // the job of this work-group (uniform branches: kernel-argument loads at fixed offsets)
     GemvJob j = L.job[0];
     if (L.n_jobs > 3 && b >= L.job[3].wg0) j = L.job[3];
@@ -233,6 +233,8 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(GemvLaunch L) {
     }
 }
 
+__global__ __launch_bounds__(kGemvThreads) void gemv_kernel(GemvLaunch L) { gemv_body(L, blockIdx.x); }
+
 // Sum / max over the 256 threads of a work-group (result in every thread).
 WL_DEV float wg_sum(float v, float* red) {
     for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
@@ -269,16 +271,18 @@ WL_DEV void rope(const float* in, uint32_t istride, float* out, uint32_t ostride
     }
 }
 
-__global__ __launch_bounds__(256) void attn_prep_kernel(Shape s, AttnPtrs p, uint32_t pos) {
+static_assert(kGemvThreads == 256, "the prep and GEMV bodies share a launch of 256-thread work-groups");
+// Work-group blk (0: the KV rows, 1: the indexer key row) of the prep stage.
+WL_DEV void prep_body(const Shape& s, const AttnPtrs& p, uint32_t pos, uint32_t blk) {
     __shared__ float red[4];
     __shared__ float kbuf[1024];
     __shared__ float cs[512];
     const uint32_t tid = threadIdx.x;
     rope_table(cs, s.RP, pos, s.theta);
     __syncthreads();
-    if (blockIdx.x == 0)
+    if (blk == 0)
         for (uint32_t i = tid; i < s.RP; i += 256) p.rope_cs[i] = cs[i];  // for the query RoPE
-    if (blockIdx.x == 0) {
+    if (blk == 0) {
         // kv_c row = RMSNorm(kv_raw[0, L), kv_a_ln, 1e-6); k_rot row = RoPE(kv_raw[L, L + RP))
         float ss = 0.f;
         for (uint32_t i = tid; i < s.L; i += 256) ss += p.kv_raw[i] * p.kv_raw[i];
@@ -306,15 +310,33 @@ __global__ __launch_bounds__(256) void attn_prep_kernel(Shape s, AttnPtrs p, uin
     }
 }
 
+// A GEMV launch whose last work-groups run the prep stage (the two depend on
+// the same earlier stage only), so the prep needs no launch of its own.
+__global__ __launch_bounds__(kGemvThreads) void gemv_prep_kernel(GemvLaunch L, uint32_t n_gemv, Shape s, AttnPtrs p,
+                                                                 uint32_t pos) {
+    if (blockIdx.x < n_gemv) gemv_body(L, blockIdx.x);
+    else prep_body(s, p, pos, blockIdx.x - n_gemv);
+}
+
 // q_abs[h][c] = sum_{d < NP} q[h][d] * kv_b[h (NP + VD) + d][c]: work-group
 // (h, column block of up to 128 columns); 8 columns per thread, the rows
 // split over the remaining thread dimension and summed through LDS. The last
 // work-group applies RoPE to the queries.
-__global__ __launch_bounds__(256) void attn_absorb_kernel(Shape s, AttnPtrs p, uint32_t owner) {
+WL_DEV void index_score_body(const Shape& s, const AttnPtrs& p, uint32_t T, uint32_t blk, float* lq);
+
+// Work-groups [0, HN nb): the absorption; HN nb: the RoPE of the queries;
+// after it, on owner layers, the index scores over T keys (kIdxKeys per
+// work-group), which depend on the same earlier stages only.
+__global__ __launch_bounds__(256) void attn_absorb_kernel(Shape s, AttnPtrs p, uint32_t owner, uint32_t T) {
     __shared__ float red[2048];
+    extern __shared__ float dyn[];
     const uint32_t tid = threadIdx.x;
     const uint32_t nb = (s.L + 127) / 128;
     const uint32_t DH = s.NP + s.RP;
+    if (blockIdx.x > s.HN * nb) {
+        index_score_body(s, p, T, blockIdx.x - s.HN * nb - 1u, dyn);
+        return;
+    }
     if (blockIdx.x == s.HN * nb) {
         float* cs = red;
         for (uint32_t i = tid; i < s.RP; i += 256) cs[i] = p.rope_cs[i];
@@ -374,15 +396,22 @@ __global__ __launch_bounds__(256) void attn_absorb_kernel(Shape s, AttnPtrs p, u
 // all ID dims from LDS, then the head parts summed by shuffles in head order.
 constexpr uint32_t kIdxKeys = 16;
 
-__global__ __launch_bounds__(256) void index_score_kernel(Shape s, AttnPtrs p, uint32_t T) {
-    extern __shared__ float lq[];  // q [IH][ID + 4] | w [IH] | k [kIdxKeys][ID + 4]
+// Work-group blk of the index scores. lq: q [IH][ID + 4] | w [IH] |
+// k [kIdxKeys][ID + 4] | RoPE table [RP]. The query is the wq_b output with
+// RoPE on its leading RP dims, applied here as the absorb stage's RoPE
+// work-group applies it, so the scores need not wait for that work-group.
+WL_DEV void index_score_body(const Shape& s, const AttnPtrs& p, uint32_t T, uint32_t blk, float* lq) {
     const uint32_t tid = threadIdx.x, QS = s.ID + 4;
     float* lw = lq + s.IH * QS;
     float* lk = lw + s.IH;
-    const uint32_t k0 = blockIdx.x * kIdxKeys;
+    float* cs = lk + kIdxKeys * QS;
+    const uint32_t k0 = blk * kIdxKeys;
     const uint32_t nk = (T - k0) < kIdxKeys ? (T - k0) : kIdxKeys;
-    for (Walk2 w(tid, 256, s.ID / 4); w.r < s.IH; w.next())
-        *(f32x4*)(lq + w.r * QS + 4 * w.c) = *(const f32x4*)(p.iqr + (size_t)w.r * s.ID + 4 * w.c);
+    for (uint32_t i = tid; i < s.RP; i += 256) cs[i] = p.rope_cs[i];
+    __syncthreads();
+    rope(p.iq, s.ID, lq, QS, s.IH, cs, s.RP);
+    for (Walk2 w(tid, 256, (s.ID - s.RP) / 4); w.r < s.IH; w.next())
+        *(f32x4*)(lq + w.r * QS + s.RP + 4 * w.c) = *(const f32x4*)(p.iq + (size_t)w.r * s.ID + s.RP + 4 * w.c);
     for (uint32_t i = tid; i < s.IH; i += 256) lw[i] = p.iw[i];
     for (Walk2 w(tid, 256, s.ID / 4); w.r < nk; w.next())
         *(f32x4*)(lk + w.r * QS + 4 * w.c) = *(const f32x4*)(p.idx_k + (size_t)(k0 + w.r) * s.ID + 4 * w.c);
@@ -413,6 +442,7 @@ __global__ __launch_bounds__(256) void index_score_kernel(Shape s, AttnPtrs p, u
     sc += __shfl_xor(sc, 8, 64);
     if (key < nk && hp == 0) p.isc[k0 + key] = sc;
 }
+
 
 // Order-preserving key of an f32 (larger float -> larger key).
 WL_DEV uint32_t okey(float f) {
@@ -809,28 +839,31 @@ int launch_gemv(const GemvLaunch& l, uint32_t n_wg, void* stream) {
     return (int)hipGetLastError();
 }
 
-int launch_attn_prep(const Shape& s, const AttnPtrs& p, uint32_t pos, bool owner, void* stream) {
-    hipLaunchKernelGGL(attn_prep_kernel, dim3(owner ? 2 : 1), dim3(256), 0, (hipStream_t)stream, s, p, pos);
+// Dynamic LDS of the index scores: q [IH][ID + 4], w [IH], k [kIdxKeys][ID + 4], RoPE table [RP].
+size_t index_score_lds(const Shape& s) {
+    return ((size_t)s.IH * (s.ID + 4) + s.IH + (size_t)kIdxKeys * (s.ID + 4) + s.RP) * 4;
+}
+
+int launch_gemv_prep(const GemvLaunch& l, uint32_t n_wg, const Shape& s, const AttnPtrs& p, uint32_t pos, bool owner,
+                     void* stream) {
+    hipLaunchKernelGGL(gemv_prep_kernel, dim3(n_wg + (owner ? 2u : 1u)), dim3(kGemvThreads), 0, (hipStream_t)stream, l,
+                       n_wg, s, p, pos);
     return (int)hipGetLastError();
 }
 
-int launch_attn_absorb(const Shape& s, const AttnPtrs& p, uint32_t pos, bool owner, void* stream) {
+int launch_attn_absorb(const Shape& s, const AttnPtrs& p, bool owner, uint32_t T, void* stream) {
     const uint32_t nb = (s.L + 127) / 128;
-    (void)pos;
-    hipLaunchKernelGGL(attn_absorb_kernel, dim3(s.HN * nb + 1), dim3(256), 0, (hipStream_t)stream, s, p,
-                       owner ? 1u : 0u);
-    return (int)hipGetLastError();
-}
-
-int launch_index_select(const Shape& s, const AttnPtrs& p, uint32_t T, void* stream) {
-    const size_t lds = ((size_t)s.IH * (s.ID + 4) + s.IH + (size_t)kIdxKeys * (s.ID + 4)) * 4;
-    hipError_t ae = hipFuncSetAttribute((const void*)index_score_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+    const uint32_t nsc = owner ? (T + kIdxKeys - 1) / kIdxKeys : 0u;
+    const size_t lds = owner ? index_score_lds(s) : 0;
+    hipError_t ae = hipFuncSetAttribute((const void*)attn_absorb_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
                                         (int)lds);
     if (ae != hipSuccess) return (int)ae;
-    hipLaunchKernelGGL(index_score_kernel, dim3((T + kIdxKeys - 1) / kIdxKeys), dim3(256), lds, (hipStream_t)stream, s,
-                       p, T);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return (int)e;
+    hipLaunchKernelGGL(attn_absorb_kernel, dim3(s.HN * nb + 1 + nsc), dim3(256), lds, (hipStream_t)stream, s, p,
+                       owner ? 1u : 0u, T);
+    return (int)hipGetLastError();
+}
+
+int launch_index_topk(const Shape& s, const AttnPtrs& p, uint32_t T, void* stream) {
     hipLaunchKernelGGL(index_topk_kernel, dim3(1), dim3(1024), 0, (hipStream_t)stream, (const float*)p.isc, p.keep,
                        p.klist, p.max_seq, T, s.TOPK);
     return (int)hipGetLastError();

@@ -327,9 +327,8 @@ wl_status wl_run_attention(wl_attn* a, uint32_t layer, uint32_t pos, float* d_hi
     p.part_l = a->part_l;
     p.part_ctx = a->part_ctx;
     p.ctx = a->ctx;
-    // 2. cache rows of pos (kv_c, k_rot, indexer key)
-    if ((rs = launched(a, wl::attn::launch_attn_prep(s, p, pos, L.owner, st), "attention prep")) != WL_OK) return rs;
-    // 3. q_a_layernorm (fused) -> q_b, and the indexer query
+    // 2. q_a_layernorm (fused) -> q_b, and the indexer query; in the same
+    // launch, the cache rows of pos (kv_c, k_rot, indexer key)
     {
         wl::attn::GemvLaunch l{};
         uint32_t n = 0;
@@ -344,22 +343,23 @@ wl_status wl_run_attention(wl_attn* a, uint32_t layer, uint32_t pos, float* d_hi
             j.eps = 1e-6f;
             add_job(l, n, j);
         }
-        if ((rs = launched(a, wl::attn::launch_gemv(l, n, st), "query projections")) != WL_OK) return rs;
+        if ((rs = launched(a, wl::attn::launch_gemv_prep(l, n, s, p, pos, L.owner, st), "query projections")) != WL_OK)
+            return rs;
     }
-    // 4. absorbed query, RoPE of the queries
-    if ((rs = launched(a, wl::attn::launch_attn_absorb(s, p, pos, L.owner, st), "query absorption")) != WL_OK)
+    // 3. absorbed query, RoPE of the queries and (owning layers) the index scores
+    if ((rs = launched(a, wl::attn::launch_attn_absorb(s, p, L.owner, T, st), "query absorption")) != WL_OK)
         return rs;
-    // 5. the DSA selection (owning layers), published for the shared layers
+    // 4. the DSA selection (owning layers), published for the shared layers
     if (L.owner) {
-        if ((rs = launched(a, wl::attn::launch_index_select(s, p, T, st), "indexer")) != WL_OK) return rs;
+        if ((rs = launched(a, wl::attn::launch_index_topk(s, p, T, st), "indexer")) != WL_OK) return rs;
         a->share_layer = (int32_t)layer;
         a->share_pos = pos;
         a->last_owner = (int32_t)layer;
     }
-    // 6. attention over keys 0..pos
+    // 5. attention over keys 0..pos
     const uint32_t S = wl::attn::attn_splits(s, T, kMaxSplits);
     if ((rs = launched(a, wl::attn::launch_attn_core(s, p, T, S, st), "attention")) != WL_OK) return rs;
-    // 7. value projection per head, then o_proj + residual
+    // 6. value projection per head, then o_proj + residual
     {
         wl::attn::GemvLaunch l{};
         uint32_t n = 0;
