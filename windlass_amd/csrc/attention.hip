@@ -453,30 +453,45 @@ WL_DEV uint32_t okey(float f) {
 // keep[t] = 1 for the TOPK largest scores of [0, T) (ties to the lowest
 // index), every key when T <= TOPK; klist[0, count) the kept keys in
 // ascending order and klist[max_seq] = count (the list the attention core
-// walks). One work-group: a radix select of the TOPK-th largest key (4
-// passes of 8 bits), then the marking, then the list (each thread's kept
-// keys at the exclusive prefix of the threads' counts).
-__global__ __launch_bounds__(1024) void index_topk_kernel(const float* isc, uint8_t* keep, uint32_t* klist,
-                                                          uint32_t max_seq, uint32_t T, uint32_t K) {
+// walks). One work-group; thread tid owns keys [tid per, tid per + per): a
+// radix select of the TOPK-th largest key (4 passes of 8 bits), then the
+// marking, then the list (each thread's kept keys at the exclusive prefix of
+// the threads' counts). CACHED (per <= kTopkCache): each thread's keys stay
+// in registers across the passes instead of being read again from memory.
+constexpr uint32_t kTopkCache = 8;
+
+template <bool CACHED>
+WL_DEV void index_topk_body(const float* isc, uint8_t* keep, uint32_t* klist, uint32_t max_seq, uint32_t T,
+                            uint32_t K) {
     __shared__ uint32_t hist[256];
     __shared__ uint32_t cnt[16];
     __shared__ uint32_t sh_prefix, sh_kk;
     const uint32_t tid = threadIdx.x;
-    if (T <= K) {
-        for (uint32_t t = tid; t < T; t += 1024) {
-            keep[t] = 1;
-            klist[t] = t;
-        }
-        if (tid == 0) klist[max_seq] = T;
-        return;
+    const uint32_t per = (T + 1023) / 1024, t0 = tid * per, t1 = (t0 + per < T) ? t0 + per : T;
+    const uint32_t n = t1 > t0 ? t1 - t0 : 0u;
+    uint32_t kc[CACHED ? kTopkCache : 1];
+    if (CACHED) {
+#pragma unroll
+        for (uint32_t i = 0; i < kTopkCache; i++) kc[i] = i < n ? okey(isc[t0 + i]) : 0u;
     }
+    // the key of this thread's i-th score
+    auto key = [&](uint32_t i) { return CACHED ? kc[i] : okey(isc[t0 + i]); };
+    constexpr uint32_t kLoop = CACHED ? kTopkCache : 0xFFFFFFFFu;
     uint32_t prefix = 0, mask = 0, kk = K;
     for (int shift = 24; shift >= 0; shift -= 8) {
         for (uint32_t i = tid; i < 256; i += 1024) hist[i] = 0;
         __syncthreads();
-        for (uint32_t t = tid; t < T; t += 1024) {
-            const uint32_t u = okey(isc[t]);
-            if ((u & mask) == prefix) atomicAdd(&hist[(u >> shift) & 255u], 1u);
+        if (CACHED) {
+#pragma unroll
+            for (uint32_t i = 0; i < kTopkCache; i++) {
+                const uint32_t u = kc[i];
+                if (i < n && (u & mask) == prefix) atomicAdd(&hist[(u >> shift) & 255u], 1u);
+            }
+        } else {
+            for (uint32_t t = tid; t < T; t += 1024) {  // coalesced
+                const uint32_t u = okey(isc[t]);
+                if ((u & mask) == prefix) atomicAdd(&hist[(u >> shift) & 255u], 1u);
+            }
         }
         __syncthreads();
         if (tid < 64) {
@@ -507,9 +522,9 @@ __global__ __launch_bounds__(1024) void index_topk_kernel(const float* isc, uint
     }
     // prefix: the key of the K-th largest score; kk (>= 1) of the keys equal
     // to it are kept, the lowest indices first
-    const uint32_t per = (T + 1023) / 1024, t0 = tid * per, t1 = (t0 + per < T) ? t0 + per : T;
     uint32_t eq = 0;
-    for (uint32_t t = t0; t < t1; t++) eq += okey(isc[t]) == prefix;
+#pragma unroll
+    for (uint32_t i = 0; i < kLoop && i < n; i++) eq += key(i) == prefix;
     // exclusive prefix of eq over the threads: a scan in each wave, then the wave totals
     uint32_t inc = eq;
     for (int o = 1; o < 64; o <<= 1) {
@@ -520,16 +535,18 @@ __global__ __launch_bounds__(1024) void index_topk_kernel(const float* isc, uint
     __syncthreads();
     uint32_t before = inc - eq;
     for (uint32_t w = 0; w < (tid >> 6); w++) before += cnt[w];
-    uint32_t mine = 0;
-    for (uint32_t t = t0; t < t1; t++) {
-        const uint32_t u = okey(isc[t]);
+    uint32_t mine = 0, kept = 0;  // kept: bit i = key i kept (cached path)
+#pragma unroll
+    for (uint32_t i = 0; i < kLoop && i < n; i++) {
+        const uint32_t u = key(i);
         uint8_t k = u > prefix;
         if (u == prefix) {
             k = before < kk;
             before++;
         }
-        keep[t] = k;
+        keep[t0 + i] = k;
         mine += k;
+        if (CACHED) kept |= (uint32_t)k << i;
     }
     // the list: exclusive prefix of the kept counts, as above
     __syncthreads();  // cnt is free again
@@ -542,9 +559,25 @@ __global__ __launch_bounds__(1024) void index_topk_kernel(const float* isc, uint
     __syncthreads();
     uint32_t at = inc - mine;
     for (uint32_t w = 0; w < (tid >> 6); w++) at += cnt[w];
-    for (uint32_t t = t0; t < t1; t++)
-        if (keep[t]) klist[at++] = t;
+#pragma unroll
+    for (uint32_t i = 0; i < kLoop && i < n; i++)
+        if (CACHED ? ((kept >> i) & 1u) : keep[t0 + i]) klist[at++] = t0 + i;
     if (tid == 0) klist[max_seq] = K;
+}
+
+__global__ __launch_bounds__(1024) void index_topk_kernel(const float* isc, uint8_t* keep, uint32_t* klist,
+                                                          uint32_t max_seq, uint32_t T, uint32_t K) {
+    const uint32_t tid = threadIdx.x;
+    if (T <= K) {
+        for (uint32_t t = tid; t < T; t += 1024) {
+            keep[t] = 1;
+            klist[t] = t;
+        }
+        if (tid == 0) klist[max_seq] = T;
+        return;
+    }
+    if ((T + 1023) / 1024 <= kTopkCache) index_topk_body<true>(isc, keep, klist, max_seq, T, K);
+    else index_topk_body<false>(isc, keep, klist, max_seq, T, K);
 }
 
 // Attention over the kept keys klist[sp kps, min(count, (sp + 1) kps)) (the
