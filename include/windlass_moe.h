@@ -202,7 +202,9 @@ wl_status wl_run_moe_residual(wl_ctx* ctx, uint32_t layer, const float* d_hidden
 
 /* n_layers consecutive layers starting at first_layer, h <- h + moe(h) per
  * layer (the MoE half of run_chain's per-layer loop, src/glm_layer_runner.cuh:
- * 1065-1068). d_h [H] is updated in place; d_tmp [H] is caller scratch. */
+ * 1065-1068). d_h [H] is updated in place (each layer reads all of h before
+ * any of it is written); d_tmp [H] is accepted for the reference's calling
+ * shape and not written. */
 wl_status wl_run_chain(wl_ctx* ctx, uint32_t first_layer, uint32_t n_layers, float* d_h,
                        float* d_tmp, void* stream);
 

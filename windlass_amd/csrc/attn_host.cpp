@@ -16,6 +16,10 @@
 #include "../../include/windlass_moe.h"
 #include "attention.h"
 
+namespace wl {
+wl_status run_moe_in_place(wl_ctx* c, uint32_t layer, float* d_h, void* stream);  // moe_host.cpp
+}
+
 namespace {
 
 constexpr uint32_t kMaxSplits = 64;
@@ -44,7 +48,7 @@ struct wl_attn {
     float *x_norm = nullptr, *qa_raw = nullptr, *q_resid = nullptr, *kv_raw = nullptr, *ik_raw = nullptr,
           *iw = nullptr, *q = nullptr, *iq = nullptr, *iqr = nullptr, *q_abs = nullptr, *q_rope = nullptr,
           *rope_cs = nullptr, *isc = nullptr, *part_m = nullptr, *part_l = nullptr, *part_ctx = nullptr,
-          *ctx = nullptr, *attn = nullptr, *attn_out = nullptr, *g = nullptr, *u = nullptr, *moe_out = nullptr;
+          *ctx = nullptr, *attn = nullptr, *attn_out = nullptr, *g = nullptr, *u = nullptr;
     int32_t share_layer = -1;          // the owning layer whose selection is current
     uint32_t share_pos = 0xFFFFFFFFu;  // the position it was made at
     int32_t last_owner = -1;
@@ -180,7 +184,7 @@ wl_status wl_attn_create(const wl_attn_config* cfg, wl_attn** out) {
         (st = dalloc(a, &a->part_ctx, S * s.HN * s.L * f)) != WL_OK ||
         (st = dalloc(a, &a->ctx, (size_t)s.HN * s.L * f)) != WL_OK ||
         (st = dalloc(a, &a->attn, (size_t)s.HN * s.VD * f)) != WL_OK ||
-        (st = dalloc(a, &a->attn_out, s.H * f)) != WL_OK || (st = dalloc(a, &a->moe_out, s.H * f)) != WL_OK ||
+        (st = dalloc(a, &a->attn_out, s.H * f)) != WL_OK ||
         (st = dalloc(a, &a->g, (size_t)(s.DI ? s.DI : 8) * f)) != WL_OK ||
         (st = dalloc(a, &a->u, (size_t)(s.DI ? s.DI : 8) * f)) != WL_OK) {
         t_create_err = a->err;
@@ -422,11 +426,8 @@ wl_status wl_run_layer(wl_attn* a, wl_ctx* moe, uint32_t layer, uint32_t moe_lay
     if (rs != WL_OK) return rs;
     if (a->layers[layer].dense) return wl_run_dense_mlp(a, layer, d_hidden, stream);
     if (!moe) return fail(a, WL_ERR_INVALID, "layer %u is not dense and no MoE context was given", layer);
-    rs = wl_run_moe_residual(moe, moe_layer, d_hidden, d_hidden, a->moe_out, stream);
+    rs = wl::run_moe_in_place(moe, moe_layer, d_hidden, stream);
     if (rs != WL_OK) return fail(a, rs, "MoE layer %u: %s", moe_layer, wl_last_error(moe));
-    hipError_t e = hipMemcpyAsync(d_hidden, a->moe_out, a->sh.H * sizeof(float), hipMemcpyDeviceToDevice,
-                                  (hipStream_t)stream);
-    if (e != hipSuccess) return fail(a, WL_ERR_HIP, "residual copy: %s", hipGetErrorString(e));
     return WL_OK;
 }
 

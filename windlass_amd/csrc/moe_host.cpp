@@ -778,14 +778,19 @@ static wl_status cache_speculate(wl_ctx* c, hipStream_t s) {
     return cache_resolve(c, C.spec_layer, c->h_pin + PinMap::pred, c->cfg.n_experts_per_tok, s, true, nullptr);
 }
 
+// in_place: d_out == d_hidden == d_resid is allowed (h <- h + moe(h)): every
+// work-group reads all of h for its norm before it publishes any partial, and
+// a combine block is written only after every partial of it is in, so no
+// read of h can see a written value.
 static wl_status run_layer(wl_ctx* c, uint32_t layer, const float* d_hidden, const float* d_resid,
-                           float* d_out, void* stream, uint32_t next = 0xFFFFFFFFu) {
+                           float* d_out, void* stream, uint32_t next = 0xFFFFFFFFu, bool in_place = false) {
     if (!c) return WL_ERR_INVALID;
     if (layer >= c->cfg.n_layers) return fail(c, WL_ERR_INVALID, "layer %u >= n_layers %u", layer, c->cfg.n_layers);
     const LayerState& L = c->layers[layer];
     if (!L.set) return fail(c, WL_ERR_STATE, "layer %u has no weights (wl_set_layer)", layer);
     if (!d_hidden || !d_out) return fail(c, WL_ERR_INVALID, "null hidden/out");
-    if (d_out == d_hidden || (d_resid && d_out == d_resid))
+    if (in_place ? (d_out != d_hidden || d_resid != d_hidden)
+                 : (d_out == d_hidden || (d_resid && d_out == d_resid)))
         return fail(c, WL_ERR_INVALID, "d_out must not alias the inputs");
     const uint32_t H = c->cfg.hidden, I = c->cfg.moe_inter, E = c->cfg.n_routed_experts,
                    K = c->cfg.n_experts_per_tok, SI = c->SI;
@@ -831,6 +836,18 @@ static wl_status run_layer(wl_ctx* c, uint32_t layer, const float* d_hidden, con
     return cache_speculate(c, (hipStream_t)stream);
 }
 
+}  // extern "C"
+
+namespace wl {
+// One MoE layer with its residual, in place: h <- h + moe(h) (wl_run_layer
+// holds a single hidden buffer).
+wl_status run_moe_in_place(wl_ctx* c, uint32_t layer, float* d_h, void* stream) {
+    return run_layer(c, layer, d_h, d_h, d_h, stream, 0xFFFFFFFFu, true);
+}
+}  // namespace wl
+
+extern "C" {
+
 wl_status wl_run_moe(wl_ctx* c, uint32_t layer, const float* d_hidden, float* d_out, void* stream) {
     return run_layer(c, layer, d_hidden, nullptr, d_out, stream);
 }
@@ -848,20 +865,11 @@ wl_status wl_run_chain(wl_ctx* c, uint32_t first_layer, uint32_t n_layers, float
     if (first_layer + (uint64_t)n_layers > c->cfg.n_layers)
         return fail(c, WL_ERR_INVALID, "layers [%u,%u) exceed n_layers %u", first_layer,
                     first_layer + n_layers, c->cfg.n_layers);
-    float* cur = d_h;
-    float* nxt = d_tmp;
+    // every layer in place (see run_layer); d_tmp is not written
     for (uint32_t l = 0; l < n_layers; l++) {
         const uint32_t next = l + 1 < n_layers ? first_layer + l + 1 : 0xFFFFFFFFu;
-        wl_status s = run_layer(c, first_layer + l, cur, cur, nxt, stream, next);
+        wl_status s = run_layer(c, first_layer + l, d_h, d_h, d_h, stream, next, true);
         if (s != WL_OK) return s;
-        float* t = cur;
-        cur = nxt;
-        nxt = t;
-    }
-    if (cur != d_h) {
-        hipError_t e = hipMemcpyAsync(d_h, cur, 4 * (size_t)c->cfg.hidden, hipMemcpyDeviceToDevice,
-                                      (hipStream_t)stream);
-        if (e != hipSuccess) return hip_fail(c, e, "chain copy-back");
     }
     return WL_OK;
 }
