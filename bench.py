@@ -506,7 +506,7 @@ def main():
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE={world}); "
-              "the multi-GPU sharding of the MoE layer is described in DESIGN.md but not built.", file=sys.stderr)
+              "the multi-GPU sharding of the MoE layer is not built.", file=sys.stderr)
         sys.exit(2)
 
     from windlass_amd import hip, moe, synthdata

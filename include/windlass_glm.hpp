@@ -25,7 +25,8 @@
 // come through the caller's ExpertSource on every call (the library's source
 // path: one host round trip per layer, as the reference's run_moe). A caller
 // that keeps its experts resident gets the faster path by binding them once
-// with wl_slot_bind. The dense-MLP layers below
+// with wl_slot_bind (wl_slot_pool_create + wl_expert_to_native fill the
+// slots). The dense-MLP layers below
 // dense_first are not part of the MoE path: calling run_moe on one aborts.
 // Errors abort with the library's message, the reference's error policy
 // (GLM_CUDA_OK -> abort, src/glm_loader.cuh:24-26). One host thread, as in
