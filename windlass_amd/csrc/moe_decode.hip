@@ -25,7 +25,9 @@
 //      src/glm_kernels.cuh:63-110, src/glm_layer_runner.cuh:338-341,370-436
 //   1  work-groups combine blocks of 32 output rows: the sum of the G partials
 //      (fixed order), + the residual when one is given (src/glm_layer_runner.cuh:
-//      403,428,436,675).
+//      403,428,436,675). A work-group takes a ticket from this call's counter
+//      as it gets here and combines blocks ticket, ticket + G, ...: the first
+//      to finish their own work do the combining.
 //
 // Splitting the down projection by the SwiGLU slice a work-group computed
 // means no work-group waits for another one's SwiGLU output: the only
