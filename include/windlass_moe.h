@@ -222,6 +222,8 @@ wl_status wl_run_chain(wl_ctx* ctx, uint32_t first_layer, uint32_t n_layers, flo
  * none bound fetches its routed set through the context's expert source (see
  * wl_expert_source: one host round trip per chunk of tokens, each unique
  * expert fetched once). n_tokens <= 65535, run in chunks of up to 4096 tokens.
+ * At most 816 routed experts (the GEMM kernels keep the expert tables in LDS
+ * beside the activation slots); a wider config fails with WL_ERR_INVALID.
  * Scratch grows to the largest chunk seen (context-owned; growing
  * synchronises the device). */
 wl_status wl_run_moe_batched(wl_ctx* ctx, uint32_t layer, uint32_t n_tokens, const float* d_hidden,

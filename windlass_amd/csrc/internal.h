@@ -303,6 +303,9 @@ int launch_expert_ffn(const uint8_t* blk, uint64_t gw_off, uint64_t gs_off, uint
                       uint32_t I, float* mid, uint16_t* mid_p, float* y, uint16_t* y_bf16,
                       void* stream);
 // Batched layer (moe_batched.hip): every stage on `stream`.
+// The most routed experts the batched layer supports (its GEMM kernels keep
+// the expert tables in LDS beside the activation slots).
+uint32_t batched_max_experts();
 int launch_batched(const DecodeArgs* d_args, const BatchArgs& b, uint32_t H, uint32_t I, uint32_t SI, uint32_t E,
                    uint32_t K, uint32_t n_cu, uint32_t phases, void* stream);
 // The library's static device scratch (noalloc.hip): its device address on

@@ -1142,6 +1142,14 @@ __global__ void __launch_bounds__(256) bcomb_kernel(const BatchArgs b, uint32_t 
     *(float4*)(b.out + (size_t)t * H + r) = acc;
 }
 
+uint32_t batched_max_experts() {
+    // the GEMM kernels' LDS: the three activation slots and the expert tables
+    const size_t lds = (size_t)decode_max_lds(), ring = 3u * (size_t)kSlotB;
+    uint32_t e = 0;
+    while (ring + gemm_tab_bytes(e + 16u) <= lds) e += 16u;
+    return e;
+}
+
 int launch_batched(const DecodeArgs* d_args, const BatchArgs& b, uint32_t H, uint32_t I, uint32_t SI, uint32_t E,
                    uint32_t K, uint32_t n_cu, uint32_t phases, void* stream) {
     (void)I;

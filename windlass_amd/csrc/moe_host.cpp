@@ -972,6 +972,9 @@ static wl_status batched_check(wl_ctx* c, uint32_t layer, uint32_t n_tokens, con
     if (((uintptr_t)d_hidden | (uintptr_t)d_out | (uintptr_t)d_resid) % 16u)
         return fail(c, WL_ERR_INVALID, "batched buffers must be 16-byte aligned");
     const uint32_t E = c->cfg.n_routed_experts;
+    if (E > wl::batched_max_experts())
+        return fail(c, WL_ERR_INVALID, "the batched layer supports at most %u routed experts (config: %u)",
+                    wl::batched_max_experts(), E);
     if (c->n_bound[layer] != E && !(c->n_bound[layer] == 0 && c->src.get))
         return fail(c, WL_ERR_NOT_RESIDENT, "batched layer %u has %u of %u experts bound%s", layer, c->n_bound[layer],
                     E, c->n_bound[layer] == 0 ? " and the context has no expert source" : "");
