@@ -2,7 +2,9 @@
 experts, where the decode kernel ranks the choices instead of running its
 one-wave argmax, more than 512, where the bias and slot loads take a second
 pass over the threads, and the largest top-k the reference allows
-(MAX_TOPK = 32, src/glm_loader.cuh:86). The decode layer (both schedules)
+(MAX_TOPK = 32, src/glm_loader.cuh:86); also the widest hidden state (8192)
+with 16 shared experts and the weights neither renormalised nor scaled
+(norm_topk_prob false, routed_scaling 1). The decode layer (both schedules)
 against the numpy oracle: ids exact, in order, and every tap and the output
 within 1e-5 rel_to_scale; the batched layer (up to its 816-expert limit)
 against the decode layer, routing bit for bit (reference router_sigmoid_topk, src/glm_layer_runner.cuh:304-336,
@@ -21,6 +23,9 @@ SHAPES = [
     dict(hidden=1024, moe_inter=256, n_routed_experts=384, n_experts_per_tok=8, n_shared=1),
     dict(hidden=768, moe_inter=128, n_routed_experts=1024, n_experts_per_tok=12, n_shared=2),
     dict(hidden=512, moe_inter=128, n_routed_experts=4096, n_experts_per_tok=32, n_shared=1),
+    # the widest hidden state, 16 shared experts, weights not renormalised, no scaling
+    dict(hidden=8192, moe_inter=128, n_routed_experts=64, n_experts_per_tok=4, n_shared=16,
+         norm_topk_prob=False, routed_scaling=1.0),
 ]
 
 
@@ -36,9 +41,10 @@ def _taps(dm):
             "shared": H_.download_ptr(t["shared"], np.float32, H)}
 
 
-@pytest.mark.parametrize("shape", SHAPES, ids=lambda s: f"E{s['n_routed_experts']}_K{s['n_experts_per_tok']}")
+@pytest.mark.parametrize("shape", SHAPES,
+                         ids=lambda s: f"H{s['hidden']}_E{s['n_routed_experts']}_K{s['n_experts_per_tok']}")
 def test_wide_routing_decode_vs_oracle_and_batched_vs_decode(gpu, shape):
-    c = dict(shape, routed_scaling=2.5, rms_eps=1e-5)
+    c = dict(dict(routed_scaling=2.5, rms_eps=1e-5), **shape)
     H, I, K = c["hidden"], c["moe_inter"], c["n_experts_per_tok"]
     dm = DeviceModel(c, seed=21, n_layers=1)
     src = O.ExpertSource(H, I, 21)
