@@ -148,6 +148,19 @@ def test_long_sequence_sparse_selection(gpu):
     am.close()
 
 
+def test_very_long_sequence_topk_from_memory(gpu):
+    """8,400 positions: past 8,192 keys the top-k kernel's threads hold more
+    scores than it keeps in registers and read them from memory on every
+    radix pass; positions on both sides of that switch are checked."""
+    a = dict(FCFG, index_topk=100)
+    T = 8400
+    am = AttnModel(a, 24, 2, owners=[True, False], max_seq=T)
+    W = [synthdata.as_f32(w) for w in am.weights]
+    Hs = np.stack([synth.hidden_state(a["hidden"], 2400, p) for p in range(T)]).astype(np.float32)
+    _check_positions(am, W, a, Hs, {8000, 8191, 8192, 8399}, None, "very long sequence")
+    am.close()
+
+
 def test_run_layer_composes(gpu):
     """wl_run_layer == run_attention then the MoE layer + residual (or the
     dense MLP), bit for bit."""
