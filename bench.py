@@ -65,14 +65,15 @@ GLM = dict(hidden=6144, moe_inter=2048, n_routed_experts=256, n_experts_per_tok=
            routed_scaling=2.5, rms_eps=1e-5)
 
 
-def algorithmic_bytes(c):
+def algorithmic_bytes(c, shared_mxfp4=False):
     """Bytes one decode layer must move at least once: K expert blocks, the
-    bf16 shared expert, the bf16 router, the f32 bias, the f32 input and
-    output vectors."""
+    shared expert (bf16, or one MXFP4 block of inter SI), the bf16 router,
+    the f32 bias, the f32 input and output vectors."""
     H, I, E, K = c["hidden"], c["moe_inter"], c["n_routed_experts"], c["n_experts_per_tok"]
     SI = I * c["n_shared"]
     expert = 3 * I * H // 2 + 3 * I * H // 32
-    return K * expert + 3 * SI * H * 2 + E * H * 2 + E * 4 + 2 * H * 4
+    shared = 3 * SI * H // 2 + 3 * SI * H // 32 if shared_mxfp4 else 3 * SI * H * 2
+    return K * expert + shared + E * H * 2 + E * 4 + 2 * H * 4
 
 
 def host_cores():
@@ -495,6 +496,9 @@ def main():
     ap.add_argument("--context", type=int, default=4096,
                     help="attention workload: cached positions before the timed tokens")
     ap.add_argument("--seed", type=int, default=1)
+    ap.add_argument("--shared", choices=["bf16", "mxfp4"], default="bf16",
+                    help="layer/chain workloads: the shared expert's format (bf16, the benchmark configuration; "
+                         "mxfp4 is the checkpoint's own format)")
     ap.add_argument("--cpu-sample", type=int, default=6,
                     help="layers timed for the CPU baseline after one warm-up, median reported (0: skip)")
     ap.add_argument("--traffic-json", default=os.path.join(ROOT, "profiles", "decode_layer_traffic.json"))
@@ -523,6 +527,7 @@ def main():
     c = dict(GLM)
     H = c["hidden"]
     cache = args.workload == "cache"
+    sh4 = args.shared == "mxfp4" and args.workload in ("layer", "chain")
     batched = args.workload == "batched"
     chain = args.workload == "chain" or cache
     if chain:
@@ -547,7 +552,7 @@ def main():
         zipf_off = synthdata.zipf_bias_offset(c["n_routed_experts"], args.seed, amplitude=args.zipf_amp)
         dm = DeviceModel(c, seed=args.seed, n_layers=1, bias_offset=zipf_off)
     else:
-        dm = DeviceModel(c, seed=args.seed, n_layers=args.layers)
+        dm = DeviceModel(c, seed=args.seed, n_layers=args.layers, shared_mxfp4=sh4)
     dm.ctx.set_schedule(moe.SCHED_FUSED if args.sched == "fused" else moe.SCHED_PHASED)
     dm.ctx.set_taps(False)  # the shared-expert output tap is a test hook
     n_h = 64
@@ -630,7 +635,7 @@ def main():
         src.free()
         dst.free()
 
-    nbytes = algorithmic_bytes(c)
+    nbytes = algorithmic_bytes(c, sh4)
     if batched:  # the experts this batch used (each read once), shared, router, T input/output rows
         cnt = dm.ctx.batched_counts()
         H_, I_ = c["hidden"], c["moe_inter"]
@@ -640,14 +645,14 @@ def main():
             c["n_routed_experts"] * 4 + 2 * H_ * 4 * args.tokens
     achieved = nbytes / (us_per_layer * 1e-6) / 1e9
     traffic = None
-    if args.workload in ("layer", "chain") and os.path.exists(args.traffic_json):
+    if args.workload in ("layer", "chain") and not sh4 and os.path.exists(args.traffic_json):
         try:
             traffic = json.load(open(args.traffic_json)).get("hbm_bytes_per_layer")
         except Exception:
             traffic = None
 
     cpu = None
-    if args.cpu_sample > 0:
+    if args.cpu_sample > 0 and not sh4:  # the CPU sample is the bf16-shared layer
         phys, logical = host_cores()
         ncores = min(phys, 16)  # physical cores, at most the box's CPU share for one GPU
         if batched:
@@ -684,7 +689,8 @@ def main():
                                 f"config2: chain of {args.layers} resident GLM MoE decode layers, bs=1, "
                                 f"h <- h + moe(h)" if chain else "config1: one GLM MoE decode layer, bs=1"),
                    "hidden": H, "moe_inter": c["moe_inter"], "n_routed_experts": c["n_routed_experts"],
-                   "n_experts_per_tok": c["n_experts_per_tok"], "shared": "bf16 inter 2048",
+                   "n_experts_per_tok": c["n_experts_per_tok"],
+                   "shared": ("mxfp4" if sh4 else "bf16") + " inter 2048",
                    ("chain_layers" if chain else "rotating_layers"): args.layers, "schedule": args.sched,
                    "global_batch": args.tokens if batched else 1},
         "tokens_per_s": round(1e6 / (us_per_layer * layers_per_step) * (args.tokens if batched else 1), 2),
