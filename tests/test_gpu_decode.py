@@ -12,8 +12,7 @@ import pytest
 
 from oracle import moe_oracle as O
 from oracle import native, synth
-from windlass_amd import moe
-
+from windlass_amd import hip as H_, moe
 from windlass_amd.model import DeviceModel, make_io
 
 pytestmark = pytest.mark.gpu
@@ -275,7 +274,7 @@ def test_chain_residual(gpu):
     dm.ctx.close()
 
 
-def test_not_resident_is_an_error(gpu):
+def test_not_resident_is_an_error_then_recovers(gpu):
     fx, c, _ = _small()
     H = c["hidden"]
     dm = DeviceModel(c, seed=1, n_layers=1)
@@ -284,6 +283,31 @@ def test_not_resident_is_an_error(gpu):
     with pytest.raises(moe.WindlassError) as ei:
         dm.ctx.run_moe(0, dh.ptr, dout.ptr)
     assert ei.value.status == 4
+    T = 3
+    do_b = H_.DeviceBuffer(4 * T * H)
+    with pytest.raises(moe.WindlassError) as ei:
+        dm.ctx.run_moe_batched(0, T, dh.ptr, None, do_b.ptr)
+    assert ei.value.status == 4
+    # the refusals leave the context usable: bind the expert again and both
+    # schedules and the batched layer match the oracle
+    dm.ctx.slot_bind(0, 5, dm.ctx.slot_pool_ptr(5))
+    src = O.ExpertSource(H, c["moe_inter"], 1)
+    hs = np.stack([synth.hidden_state(H, 410 + t) for t in range(T)]).astype(np.float32)
+    refs = [O.moe_layer(hs[t], dm.dense[0], src, 0, c)["out"] for t in range(T)]
+    for sched in (moe.SCHED_FUSED, moe.SCHED_PHASED):
+        dm.ctx.set_schedule(sched)
+        for t in range(T):
+            dh.upload(hs[t])
+            dm.ctx.run_moe(0, dh.ptr, dout.ptr)
+            dm.ctx.check_error()
+            assert O.rel_to_scale(refs[t], dout.download(np.float32)) < TOL, (sched, t)
+    dm.ctx.set_schedule(moe.SCHED_FUSED)
+    dhb = H_.DeviceBuffer.from_array(hs)
+    dm.ctx.run_moe_batched(0, T, dhb.ptr, None, do_b.ptr)
+    dm.ctx.check_error()
+    outs = do_b.download(np.float32).reshape(T, H)
+    for t in range(T):
+        assert O.rel_to_scale(refs[t], outs[t]) < TOL, t
     dm.ctx.close()
 
 
