@@ -230,3 +230,34 @@ def test_misaligned_or_aliasing_buffers_rejected(gpu):
     dm.ctx.check_error()
     assert np.array_equal(dh.download(np.float32, T * H).view(np.uint32), ref.view(np.uint32))
     dm.close()
+
+
+def test_calls_longer_than_a_chunk(gpu):
+    """A call of more than 4096 tokens runs in chunks of 4096 on the same
+    scratch: 4,141 tokens with a residual give the same rows, bit for bit, as
+    two calls over [0, 4096) and [4096, 4141), and agree within the bar with
+    a call split elsewhere (other passes per expert), with the decode path
+    around the boundary and with the oracle at both ends."""
+    c = SMALL
+    H = c["hidden"]
+    T = 4096 + 45
+    dm = DeviceModel(c, seed=14, n_layers=1)
+    hs = _tokens(H, T, 1400)
+    resid = _tokens(H, T, 1401)
+    whole = _batched(dm, hs, resid)
+    first = _batched(dm, hs[:4096], resid[:4096])
+    rest = _batched(dm, hs[4096:], resid[4096:])
+    assert np.array_equal(whole[:4096], first)
+    assert np.array_equal(whole[4096:], rest)
+    other = np.concatenate([_batched(dm, hs[:2000], resid[:2000]), _batched(dm, hs[2000:], resid[2000:])])
+    worst = max(O.rel_to_scale(whole[t] - resid[t], other[t] - resid[t]) for t in range(T))
+    assert worst < TOL, worst
+    src = O.ExpertSource(H, c["moe_inter"], 14)
+    for t in (0, 4094, 4095, 4096, 4097, T - 1):
+        moe_t = whole[t] - resid[t]
+        assert O.rel_to_scale(_decode(dm, hs[t]), moe_t) < TOL, t
+        if t in (0, T - 1):
+            ref = O.moe_layer(hs[t], dm.dense[0], src, 0, c)["out"]
+            assert O.rel_to_scale(ref, moe_t) < TOL, t
+    print(f"T={T}: chunked call equals per-chunk calls; worst vs another split {worst:.2e}", flush=True)
+    dm.close()
