@@ -30,6 +30,15 @@ WL_DEV float e8m0f(uint32_t b) {
     v = (b == 0xFFu) ? __uint_as_float(0x7FC00000u) : v;
     return v;
 }
+// e8m0f(b) if on, else +0, for a wave-uniform on: the decoded bits ANDed
+// with an all-ones or all-zero scalar mask. (A select on a uniform condition
+// compiles to a branch around the decode, several per step; the mask is kept
+// opaque so it is not folded back into that select.)
+WL_DEV float e8m0f_if(uint32_t b, bool on) {
+    uint32_t m = __builtin_amdgcn_readfirstlane(on ? ~0u : 0u);
+    asm("" : "+s"(m));
+    return __uint_as_float(__float_as_uint(e8m0f(b)) & m);
+}
 // 8 FP4 values (one dword, low nibble first) -> 8 scaled bf16 values.
 WL_DEV bf16x8 fp4x8_bf16(uint32_t w, float sc) {
     bf16x2 c0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 0);

@@ -777,7 +777,7 @@ struct UpK {
         for (uint32_t q = 0; q < 2; q++)
 #pragma unroll
             for (uint32_t i = 0; i < kSG; i++)
-                sc[q][i] = 2u * s + q < nkg ? e8m0f((W.s[i] >> (8u * ((2u * s + q) % 4u))) & 0xFFu) : 0.f;
+                sc[q][i] = e8m0f_if((W.s[i] >> (8u * ((2u * s + q) % 4u))) & 0xFFu, 2u * s + q < nkg);
         constexpr uint32_t N = 8u * NP;
         bf16x8 af[2][NB];
 #pragma unroll
