@@ -1011,11 +1011,12 @@ struct DownK {
                     const bool valid = st * 4u + s4 < NS;
 #pragma unroll
                     for (uint32_t h = 0; h < 2; h++) {
-                        const uint32_t sbyte = (W.s[s4] >> (8u * ((q0 + h) % 4u))) & 0xFFu;
+                        // decoded once, then swapped like the weight dwords
+                        const uint32_t sv = __float_as_uint(e8m0f((W.s[s4] >> (8u * ((q0 + h) % 4u))) & 0xFFu));
                         uint32_t sx, sy;
-                        swap32(sbyte, sbyte, sx, sy);
-                        scx[h] = valid ? e8m0f(sx) : 0.f;
-                        scy[h] = valid ? e8m0f(sy) : 0.f;
+                        swap32(sv, sv, sx, sy);
+                        scx[h] = valid ? __uint_as_float(sx) : 0.f;
+                        scy[h] = valid ? __uint_as_float(sy) : 0.f;
                     }
                 }
                 // Column half f of the slice: lane group g's columns s4 * 64 +
