@@ -570,10 +570,11 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const float* hidden, const 
                     const uint32_t m = m0 + i, q = v * dq_per + m;
                     const bool valid = m < dq_per && q < nq;
                     uint32_t sx, sy, x01, y01, x23, y23;
-                    swap32(sbyte, sbyte, sx, sy);
+                    const uint32_t sv = __float_as_uint(e8m0f(sbyte));
+                    swap32(sv, sv, sx, sy);
                     swap32(B.w[i][0], B.w[i][1], x01, y01);
                     swap32(B.w[i][2], B.w[i][3], x23, y23);
-                    const float scx = e8m0f(sx), scy = e8m0f(sy);
+                    const float scx = __uint_as_float(sx), scy = __uint_as_float(sy);
                     f32x4 d0 = mma(A0, fp4x8_bf16(x01, scx), f32x4{0.f, 0.f, 0.f, 0.f});
                     d0 = mma(A1, fp4x8_bf16(x23, scx), d0);
                     f32x4 d1 = mma(A0, fp4x8_bf16(y01, scy), f32x4{0.f, 0.f, 0.f, 0.f});
