@@ -95,7 +95,8 @@ WL_DEV void swiglu_store(const f32x4 (&acc)[2], uint32_t nt, bool pr, uint32_t l
         for (uint32_t i = 0; i < 4; i++) {
             if (pr && i > 0) continue;
             const float v = pr ? sum3(acc[tb]) : acc[tb][i];
-            const float up = __shfl(v, (lane + 8u) & 63u, 64);
+            // lane n < 8 takes lane n + 8 of its 16-lane row (DPP row_ror:8)
+            const float up = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xF, 0xF, false));
             const uint32_t m = pr ? 4u * tb + g : tb * 16u + 4u * g + i;
             if (n < 8u && m < nt) put(m, n, silu_mul(v, up));
         }
