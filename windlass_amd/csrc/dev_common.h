@@ -197,13 +197,19 @@ struct Batch {
     u32x4 w[kNB];
     u32x4 sv;  // the 16-byte scale chunk holding this batch's scales (MXFP4 streams)
 };
-// Scale byte of slot i of a batch whose first item is item0 (scale chunks hold
-// 16 consecutive items).
-WL_DEV uint32_t batch_scale(const Batch& B, uint32_t item0, int i) {
-    const uint32_t o = item0 % 16u + (uint32_t)i;
-    const uint32_t w = (o / 4u == 0u) ? B.sv.x : (o / 4u == 1u) ? B.sv.y : (o / 4u == 2u) ? B.sv.z : B.sv.w;
-    return (w >> (8u * (o % 4u))) & 0xFFu;
+// Scale chunks hold 16 consecutive items, and a batch's first item is a
+// multiple of kNB = 8, so its scales are one half of the chunk: the half is
+// chosen once per batch (lo, hi = its two dwords), and item i's byte sits at
+// a compile-time position.
+static_assert(kNB == 8, "a batch's scales are half of a 16-byte chunk");
+struct BatchScales {
+    uint32_t lo, hi;
+};
+WL_DEV BatchScales batch_scales(const Batch& B, uint32_t item0) {
+    const bool upper = (item0 & 8u) != 0u;
+    return BatchScales{upper ? B.sv.z : B.sv.x, upper ? B.sv.w : B.sv.y};
 }
+WL_DEV uint32_t batch_scale8(const BatchScales& s, int i) { return ((i < 4 ? s.lo : s.hi) >> (8 * (i % 4))) & 0xFFu; }
 
 // A batch of the bf16 shared expert's gate/up stream: kSNB k tiles per wave,
 // plus one 8-byte read of a logit slot, so the logits are collected while the

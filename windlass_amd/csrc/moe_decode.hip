@@ -521,13 +521,14 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const float* hidden, const 
         bf16x8 A0, A1;
         auto r_consume = [&](uint32_t b, const Batch& B) {
             if (b < nbg) {
+                const BatchScales bs = batch_scales(B, b * kNB);
 #pragma unroll
                 for (int i = 0; i < kNB; i++) {
                     const uint32_t kt = b * kNB + i;
                     const bool valid = kt < nkg;
                     // a masked item reads another tile (or zeros past the
                     // block): scale 0 makes its B operand exactly zero
-                    const float sc = valid ? e8m0f(batch_scale(B, b * kNB, i)) : 0.f;
+                    const float sc = valid ? e8m0f(batch_scale8(bs, i)) : 0.f;
 #pragma unroll
                     for (int jj = 0; jj < 4; jj++)
                         racc = mma(a_lds(xp, xps, n, kt * 128u + 32u * g + 8u * jj, valid),
@@ -559,9 +560,10 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const float* hidden, const 
                 }
             } else {
                 const uint32_t m0 = (b - nbg) * kNB;
+                const BatchScales bs = batch_scales(B, v * dq_per + m0);
 #pragma unroll
                 for (int i = 0; i < kNB; i++) {
-                    const uint32_t sbyte = batch_scale(B, v * dq_per + m0, i);
+                    const uint32_t sbyte = batch_scale8(bs, i);
                     // lane (n, g) holds 16 bytes of row n + 16*(g>>1): columns
                     // [32*(g&1), +32) of the slice, and that block's scale.
                     // One swap of lane halves turns dwords (0,1) into the B
