@@ -117,6 +117,14 @@ WL_DEV bf16x8 a_lds(const uint16_t* base, uint32_t stride, uint32_t r, uint32_t 
     if (r < 3u && valid) v = *(const u32x4*)(base + r * stride + col);
     return as_bf16x8(v);
 }
+// The A operand of an MFMA whose callers read output rows 0-2 only (the
+// three pieces of one vector): lanes of rows 3-15 read row 2 again, so the
+// read needs no per-lane condition (their output rows are never read). A
+// masked item (valid false, wave-uniform) reads column 0 instead; its B
+// operand is exactly zero, so the finite values read there add nothing.
+WL_DEV bf16x8 a_rows3(const uint16_t* base, uint32_t stride, uint32_t r, uint32_t col, bool valid) {
+    return as_bf16x8(*(const u32x4*)(base + min(r, 2u) * stride + (valid ? col : 0u)));
+}
 WL_DEV bf16x8 a_any(const uint16_t* base, uint32_t stride, uint32_t r, uint32_t col, bool valid) {
     u32x4 v = {0u, 0u, 0u, 0u};
     if (r < 3u && valid) v = *(const u32x4*)(base + r * stride + col);

@@ -229,7 +229,7 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const float* hidden, const 
                     const float sc = valid ? e8m0f((B.s[i] >> (8u * (kt % 4u))) & 0xFFu) : 0.f;
 #pragma unroll
                     for (int jj = 0; jj < 4; jj++)
-                        gacc = mma(a_lds(xp, xps, n, kt * 128u + 32u * g + 8u * jj, valid), fp4x8_bf16(B.w[i][jj], sc),
+                        gacc = mma(a_rows3(xp, xps, n, kt * 128u + 32u * g + 8u * jj, valid), fp4x8_bf16(B.w[i][jj], sc),
                                    gacc);
                 }
             } else {
@@ -238,7 +238,7 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const float* hidden, const 
                     const uint32_t m = b * kSNB + i, kt = v * sg_per + m;
                     const bool valid = m < sg_per && kt < nkt;
                     const u32x4 z = {0u, 0u, 0u, 0u};
-                    gacc = mma(a_lds(xp, xps, n, kt * 32u + 8u * g, valid), as_bf16x8(valid ? B.w[i] : z), gacc);
+                    gacc = mma(a_rows3(xp, xps, n, kt * 32u + 8u * g, valid), as_bf16x8(valid ? B.w[i] : z), gacc);
                 }
             }
             // threads tid >= E read slot E - 1 only to keep every batch the
@@ -531,7 +531,7 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const float* hidden, const 
                     const float sc = valid ? e8m0f(batch_scale8(bs, i)) : 0.f;
 #pragma unroll
                     for (int jj = 0; jj < 4; jj++)
-                        racc = mma(a_lds(xp, xps, n, kt * 128u + 32u * g + 8u * jj, valid),
+                        racc = mma(a_rows3(xp, xps, n, kt * 128u + 32u * g + 8u * jj, valid),
                                    fp4x8_bf16(B.w[i][jj], sc), racc);
                 }
                 if (b == nbg - 1u) {
@@ -555,8 +555,8 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const float* hidden, const 
                     // {0,32,8,40}[g] (+16 for the second), matching the
                     // lane order the row-pair swap below produces
                     const uint32_t c0 = 32u * (g & 1u) + 8u * (g >> 1);
-                    A0 = a_lds(rmp, rps, n, c0, true);
-                    A1 = a_lds(rmp, rps, n, c0 + 16u, true);
+                    A0 = a_rows3(rmp, rps, n, c0, true);
+                    A1 = a_rows3(rmp, rps, n, c0 + 16u, true);
                 }
             } else {
                 const uint32_t m0 = (b - nbg) * kNB;
