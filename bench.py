@@ -460,6 +460,173 @@ def bench_files(args):
     print(json.dumps(line), flush=True)
 
 
+def bench_expert(args):
+    """Config 0: one MXFP4 expert SwiGLU FFN at bs=1 (wl_expert_ffn: gate/up +
+    SwiGLU, then down), over 64 reference-layout blocks (8 seeds x 8 experts,
+    1.28 GB) rotated so that no step finds its block in the 256 MB Infinity
+    Cache, each step with its own bf16 N(0,1) input."""
+    import ctypes
+
+    from windlass_amd import hip, moe, synthdata
+    c = dict(GLM)
+    H, I = c["hidden"], c["moe_inter"]
+    cfg = moe.make_config(hidden=H, moe_inter=I, n_routed_experts=c["n_routed_experts"],
+                          n_experts_per_tok=c["n_experts_per_tok"], n_shared=1, n_layers=1)
+    ctx = moe.Context(cfg)
+    lay = moe.expert_layout(cfg)
+    seeds, per_seed = 8, 8
+    nblk = seeds * per_seed
+    pool = hip.DeviceBuffer(nblk * lay.total)
+    for s in range(seeds):
+        for e in range(per_seed):
+            moe.synth_expert(cfg, s, 0, e, pool.ptr + (s * per_seed + e) * lay.total)
+    hip.synchronize()
+    n_x = 16
+    xs = np.stack([synthdata.hidden_state(H, 8000 + i) for i in range(n_x)])
+    d_x = hip.DeviceBuffer.from_array(xs)
+    d_y = hip.DeviceBuffer(4 * H * n_x)
+    stream = hip.Stream()
+    lib = moe.load()
+
+    def step(i):
+        b = i % nblk
+        rc = lib.wl_expert_ffn(ctx.h, pool.ptr + b * lay.total, d_x.ptr + 4 * H * (i % n_x),
+                               d_y.ptr + 4 * H * (i % n_x), None, stream.handle)
+        if rc != moe.WL_OK:
+            raise moe.WindlassError(rc, "wl_expert_ffn")
+
+    for i in range(args.warmup):
+        step(i)
+    ctx.check_error(stream.handle)
+    hip.synchronize()
+    e0, e1 = hip.Event(), hip.Event()
+    e0.record(stream)
+    for i in range(args.steps):
+        step(args.warmup + i)
+    e1.record(stream)
+    e1.synchronize()
+    us = e0.elapsed_ms(e1) * 1e3 / args.steps
+    ctx.check_error(stream.handle)
+    nbytes = lay.total + 2 * 4 * H  # the block, the f32 input and output
+    achieved = nbytes / (us * 1e-6) / 1e9
+
+    cpu = None
+    if args.cpu_sample > 0:
+        from oracle import moe_oracle as O
+        phys, logical = host_cores()
+        ncores = min(phys, 16)
+
+        from threadpoolctl import threadpool_limits
+
+        from oracle import synth
+        # packed expert bytes are generated beforehand (not timed: the
+        # reference reads them from its packed files); dequant + matvecs are
+        blocks = [synth.expert_block(H, I, k % seeds, 0, k % per_seed) for k in range(min(args.cpu_sample + 1, 4))]
+
+        def cpu_leg(threads):
+            times = []
+            with threadpool_limits(limits=threads):
+                for k in range(args.cpu_sample + 1):
+                    gw, gs, uw, us_, dw, ds = blocks[k % len(blocks)]
+                    t0 = time.perf_counter()
+                    O.expert_slot(xs[k % n_x], O.dequant(gw, gs), O.dequant(uw, us_), O.dequant(dw, ds))
+                    times.append(time.perf_counter() - t0)
+            return float(np.median(times[1:])) * 1e6
+
+        us_all = cpu_leg(ncores)
+        us_one = cpu_leg(1)
+        cpu = {"value": round(us_all, 1), "unit": "us/expert", "cores": ncores, "kind": "port",
+               "sample": f"numpy oracle (dequant to f32 + OpenBLAS matvecs) on {args.cpu_sample} expert FFNs after one "
+                         f"warm-up, median; expert bytes pre-generated",
+               "host_physical_cores": phys, "host_logical_cpus": logical, "value_1thread": round(us_one, 1),
+               "gpu_speedup": round(us_all / us, 1)}
+    line = {
+        "metric": "us_per_mxfp4_expert_ffn", "value": round(us, 3), "unit": "us/expert", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(us / 1e3, 6), "higher_is_better": False,
+        "scaling": "weak", "vs_baseline": None, "dtype": "mxfp4 weights, f32 activations and accumulation",
+        "data": "synthetic",
+        "config": {"workload": "config0: one MXFP4 expert SwiGLU FFN, bs=1 (wl_expert_ffn)", "hidden": H,
+                   "moe_inter": I, "rotating_blocks": nblk, "seeds": seeds, "global_batch": 1},
+        "achieved_GBps": round(achieved, 1), "pct_of_hbm_peak": round(100 * achieved / PEAK_HBM_GBPS, 2),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
+                     "frac": round(achieved / PEAK_HBM_GBPS, 4), "traffic": None, "algorithmic_bytes": nbytes,
+                     "kernel": "ffn_gu_kernel + ffn_down_kernel (two launches)"},
+        "cpu_baseline": cpu,
+    }
+    ctx.close()
+    print(json.dumps(line), flush=True)
+
+
+def bench_shim(args):
+    """The drop-in shim (include/windlass_glm.hpp) driven by the reference's
+    own call sites: tests/shim/_build/reference_caller runs decode steps of
+    one dense layer and --shim-layers MoE layers at the GLM shape (shared
+    expert in the checkpoint's MXFP4 format, as the reference's LayerWeights
+    hold it), once with the experts made resident on first use and once with
+    every expert fetched through the caller's ExpertSource (reference-layout
+    blocks, converted per call). Runs as a child process; this process does
+    not touch the GPU."""
+    import subprocess
+    import tempfile
+
+    from windlass_amd import synthdata
+    binary = os.path.join(ROOT, "tests", "shim", "_build", "reference_caller")
+    if not os.path.exists(binary):
+        print(f"bench.py: {binary} is missing (run __graft_entry__.build())", file=sys.stderr)
+        sys.exit(1)
+    c = dict(GLM)
+    H, I, E, K = c["hidden"], c["moe_inter"], c["n_routed_experts"], c["n_experts_per_tok"]
+    DI, NL, T, seed = 12288, 1 + args.shim_layers, 16, args.seed
+    res = {}
+    with tempfile.TemporaryDirectory() as d:
+        with open(os.path.join(d, "cfg.txt"), "w") as f:
+            f.write(f"{NL} 1 {H} {I} {E} {K} 1 {DI} {T} {seed} {c['rms_eps']} {c['routed_scaling']}\n")
+        w = synthdata.dense_mlp(H, DI, seed, 0)
+        for k, name in (("post_ln", "ln"), ("gate", "gate"), ("up", "up"), ("down", "down")):
+            w[k].tofile(os.path.join(d, f"l0_{name}.bin"))
+        del w
+        for l in range(1, NL):
+            r = synthdata.router_only(H, E, seed, l)
+            r["router_w"].tofile(os.path.join(d, f"l{l}_router.bin"))
+            r["bias"].tofile(os.path.join(d, f"l{l}_bias.bin"))
+            synthdata._norm_w(seed, l, synthdata.TAG_LN, H).tofile(os.path.join(d, f"l{l}_ln.bin"))
+        np.stack([synthdata.hidden_state(H, 9000 + t) for t in range(T)]).astype(np.float32).tofile(
+            os.path.join(d, "h0.bin"))
+        for mode in ("resident", "source"):
+            print(f"bench shim: {mode}, {NL} layers, {args.steps} steps", file=sys.stderr, flush=True)
+            r = subprocess.run([binary, d, mode, str(args.steps)], capture_output=True, text=True, timeout=900)
+            if r.returncode != 0:
+                print(r.stdout + r.stderr, file=sys.stderr)
+                sys.exit(r.returncode)
+            res[mode] = json.loads(r.stdout.strip().splitlines()[-1])
+    us = res["resident"]["us_per_moe_layer"]
+    nbytes = algorithmic_bytes(c, shared_mxfp4=True)
+    achieved = nbytes / (us * 1e-6) / 1e9
+    dense_bytes = 3 * DI * H * 2 + H * 2 + 2 * H * 4
+    line = {
+        "metric": "us_per_moe_decode_layer", "value": round(us, 3), "unit": "us/layer", "n_gpus": 1,
+        "steps": args.steps, "warmup": 2, "ms_per_step": round(res["resident"]["wall_us_per_step"] / 1e3, 6),
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "mxfp4/bf16 weights, f32 activations and accumulation", "data": "synthetic",
+        "config": {"workload": f"shim: the reference's run_layer/run_chain call sites through include/windlass_glm.hpp, "
+                               f"1 dense + {args.shim_layers} MoE GLM layers per decode step, MXFP4 shared expert",
+                   "hidden": H, "moe_inter": I, "n_routed_experts": E, "n_experts_per_tok": K, "dense_inter": DI,
+                   "global_batch": 1},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
+                     "frac": round(achieved / PEAK_HBM_GBPS, 4), "traffic": None, "algorithmic_bytes": nbytes,
+                     "kernel": "moe_decode_kernel (resident MoE layer through the shim)"},
+        "shim": {"resident_us_per_moe_layer": res["resident"]["us_per_moe_layer"],
+                 "source_us_per_moe_layer": res["source"]["us_per_moe_layer"],
+                 "dense_us_per_layer": res["resident"]["us_per_dense_layer"],
+                 "dense_GBps": round(dense_bytes / (res["resident"]["us_per_dense_layer"] * 1e-6) / 1e9, 1),
+                 "source_note": "every MoE call routes on the device, reads the ids back (one host round trip), "
+                                "fetches 8 reference-layout blocks from the caller's ExpertSource and converts "
+                                "each into the native layout before the decode kernel"},
+        "cpu_baseline": None,
+    }
+    print(json.dumps(line), flush=True)
+
+
 def synthdata_hidden(H, seed):
     from windlass_amd import synthdata
     return synthdata.hidden_state(H, seed)
@@ -472,7 +639,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--layers", type=int, default=8, help="distinct resident layer copies to rotate over")
     ap.add_argument("--sched", choices=["fused", "phased"], default="fused")
-    ap.add_argument("--workload", choices=["layer", "chain", "batched", "cache", "attention", "files"], default="layer",
+    ap.add_argument("--workload", choices=["layer", "chain", "batched", "cache", "attention", "files", "expert", "shim"],
+                    default="layer",
                     help="layer: config 1 (default); chain: config 2, 24 layers per step; "
                          "batched: config 3, --tokens positions per step; cache: config 4, 75 cache-backed layers per step")
     ap.add_argument("--tokens", type=int, default=256, help="batched workload: positions per layer call")
@@ -495,6 +663,7 @@ def main():
     ap.add_argument("--file-dir", default=None, help="files workload: directory for the files (default: a temp dir)")
     ap.add_argument("--context", type=int, default=4096,
                     help="attention workload: cached positions before the timed tokens")
+    ap.add_argument("--shim-layers", type=int, default=4, help="shim workload: MoE layers after the dense one")
     ap.add_argument("--seed", type=int, default=1)
     ap.add_argument("--shared", choices=["bf16", "mxfp4"], default="bf16",
                     help="layer/chain workloads: the shared expert's format (bf16, the benchmark configuration; "
@@ -513,6 +682,11 @@ def main():
               "the multi-GPU sharding of the MoE layer is not built.", file=sys.stderr)
         sys.exit(2)
 
+    if args.workload == "shim":  # a child process drives the GPU
+        if "--steps" not in sys.argv:
+            args.steps = 40
+        return bench_shim(args)
+
     from windlass_amd import hip, moe, synthdata
     from windlass_amd.model import CachedModel, DeviceModel
 
@@ -523,6 +697,8 @@ def main():
         return bench_attention(args)
     if args.workload == "files":
         return bench_files(args)
+    if args.workload == "expert":
+        return bench_expert(args)
 
     c = dict(GLM)
     H = c["hidden"]

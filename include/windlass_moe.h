@@ -113,6 +113,21 @@ wl_status wl_set_layer_mxfp4(wl_ctx* ctx, uint32_t layer, const uint16_t* d_rout
                              const uint8_t* d_sh_up_w, const uint8_t* d_sh_up_s, const uint8_t* d_sh_down_w,
                              const uint8_t* d_sh_down_s);
 
+/* Binds layer `layer` as a dense MLP layer, the dense branch of run_moe for
+ * the layers below first_k_dense_replace (src/glm_layer_runner.cuh:373-384;
+ * glm::LayerWeights' post_attn_ln / mlp_gate / mlp_up / mlp_down,
+ * src/glm_loader.cuh:259-339): post_attention_layernorm [H] bf16 (NULL = all
+ * ones), gate / up [dense_inter, H] and down [H, dense_inter] bf16 row-major,
+ * caller-owned, 16-byte aligned, valid while the layer is run. wl_run_moe on
+ * the layer writes down(silu(gate x) * up x), x = RMSNorm(d_hidden), without
+ * the residual (two GEMV launches, no host round trip); wl_run_moe_residual,
+ * wl_run_chain and wl_run_moe_batched (one position at a time, as the
+ * reference's layer-major prefill does for these layers, :985-994) add the
+ * residual. The norm tap holds x. Synchronises the device. dense_inter: a
+ * multiple of 8, at most 16384. */
+wl_status wl_set_layer_dense(wl_ctx* ctx, uint32_t layer, const uint16_t* d_post_ln, const uint16_t* d_gate,
+                             const uint16_t* d_up, const uint16_t* d_down, uint32_t dense_inter);
+
 /* ---- HBM slot table (replaces the pointer-returning ExpertSource::get of a
  * fully resident model, src/glm_layer_runner.cuh:34-48) ---------------------
  * The device keeps a table slot_of[layer][expert] -> block pointer, and the
@@ -179,6 +194,18 @@ typedef struct wl_expert_source {
  * them to 32 on first use). WL_ERR_STATE if the context has a built-in cache
  * (wl_cache_create installs the cache as the context's source). */
 wl_status wl_set_expert_source(wl_ctx* ctx, const wl_expert_source* src);
+
+/* Makes layer `layer` resident from the context's expert source: one
+ * context-owned allocation of n_routed_experts native blocks (held until
+ * wl_destroy), filled with every expert's block from the source (get_async,
+ * else get, in id order; reference-layout blocks are converted on `stream`),
+ * then bound in the slot table, so the layer runs from then on with no host
+ * round trip and no per-call conversion. Synchronises `stream`. For the
+ * reference's resident models, whose ExpertSource hands out the same VRAM
+ * blocks on every call (src/glm_layer_runner.cuh:34-48). WL_ERR_STATE if the
+ * context has no source, the built-in cache is its source, or the layer is
+ * partly bound; WL_ERR_OOM if the blocks do not fit. */
+wl_status wl_make_resident(wl_ctx* ctx, uint32_t layer, void* stream);
 
 /* ---- the MoE layer ------------------------------------------------------
  * Replaces glm::run_moe (src/glm_layer_runner.cuh:352-443): post-attention

@@ -88,6 +88,21 @@ struct AttnPtrs {
 };
 
 int launch_gemv(const GemvLaunch& l, uint32_t n_wg, void* stream);
+// A dense SwiGLU MLP layer (the dense branch of run_moe,
+// src/glm_layer_runner.cuh:373-384): post_ln [H] bf16, gate / up [DI, H],
+// down [H, DI] bf16 row-major.
+struct DenseMlp {
+    const uint16_t *post_ln, *gate, *up, *down;
+    uint32_t H, DI;
+    float eps;
+};
+// y = add + down(silu(gate x') * up x'), x' = RMSNorm(x) with post_ln (add may
+// be null; y may alias x and add exactly: each output row reads add[r] before
+// it writes y[r], and x is read by the first launch only). g, u: [DI] f32
+// scratch; x_norm (optional): x'; y_raw (optional): y without add. Two
+// stream-ordered launches; returns the first failing launch's hipError_t.
+int launch_dense_mlp(const DenseMlp& m, const float* x, const float* add, float* y, float* g, float* u, float* x_norm,
+                     float* y_raw, void* stream);
 // A GEMV launch of n_wg work-groups followed by the prep stage's work-groups:
 // the KV-cache row of `pos` (kv_a_layernorm of the compressed KV, RoPE of the
 // shared rope key) and, on owner layers, the indexer key row (LayerNorm +

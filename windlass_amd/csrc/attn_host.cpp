@@ -141,6 +141,39 @@ wl_status launched(wl_attn* a, int e, const char* what) {
 
 }  // namespace
 
+namespace wl {
+namespace attn {
+
+// post_ln -> gate / up (one launch, the norm fused into each job) -> SwiGLU
+// fused into the down job's input -> y = add + down . mid (a second launch).
+int launch_dense_mlp(const DenseMlp& m, const float* x, const float* add, float* y, float* g, float* u, float* x_norm,
+                     float* y_raw, void* stream) {
+    GemvLaunch l{};
+    uint32_t n = 0;
+    auto j = job(m.gate, x, g, m.DI, m.H);
+    j.norm_w = m.post_ln;
+    j.eps = m.eps;
+    j.x_out = x_norm;
+    add_job(l, n, j);
+    j = job(m.up, x, u, m.DI, m.H);
+    j.norm_w = m.post_ln;
+    j.eps = m.eps;
+    add_job(l, n, j);
+    int e = launch_gemv(l, n, stream);
+    if (e != 0) return e;
+    GemvLaunch d{};
+    n = 0;
+    j = job(m.down, g, y, m.H, m.DI);
+    j.x2 = u;
+    j.add = add;
+    j.y_raw = y_raw;
+    add_job(d, n, j);
+    return launch_gemv(d, n, stream);
+}
+
+}  // namespace attn
+}  // namespace wl
+
 extern "C" {
 
 wl_status wl_attn_create(const wl_attn_config* cfg, wl_attn** out) {
@@ -394,30 +427,10 @@ wl_status wl_run_dense_mlp(wl_attn* a, uint32_t layer, float* d_hidden, void* st
     if (!L.dense) return fail(a, WL_ERR_STATE, "layer %u has no dense MLP (wl_attn_set_dense_mlp)", layer);
     if (!d_hidden || (uintptr_t)d_hidden % 16) return fail(a, WL_ERR_INVALID, "hidden must be 16-byte aligned");
     const wl::attn::Shape& s = a->sh;
-    hipStream_t st = (hipStream_t)stream;
-    wl_status rs;
-    {
-        wl::attn::GemvLaunch l{};
-        uint32_t n = 0;
-        auto j = job(L.gate, d_hidden, a->g, s.DI, s.H);
-        j.norm_w = L.post_ln;
-        j.eps = s.eps;
-        j.x_out = a->x_norm;
-        add_job(l, n, j);
-        j = job(L.up, d_hidden, a->u, s.DI, s.H);
-        j.norm_w = L.post_ln;
-        j.eps = s.eps;
-        add_job(l, n, j);
-        if ((rs = launched(a, wl::attn::launch_gemv(l, n, st), "MLP gate/up")) != WL_OK) return rs;
-    }
-    wl::attn::GemvLaunch l{};
-    uint32_t n = 0;
-    auto j = job(L.down, a->g, d_hidden, s.H, s.DI);
-    j.x2 = a->u;
-    j.add = d_hidden;
-    j.y_raw = a->attn_out;
-    add_job(l, n, j);
-    return launched(a, wl::attn::launch_gemv(l, n, st), "MLP down");
+    const wl::attn::DenseMlp m{L.post_ln, L.gate, L.up, L.down, s.H, s.DI, s.eps};
+    return launched(a, wl::attn::launch_dense_mlp(m, d_hidden, d_hidden, d_hidden, a->g, a->u, a->x_norm,
+                                                  a->attn_out, stream),
+                    "dense MLP");
 }
 
 wl_status wl_run_layer(wl_attn* a, wl_ctx* moe, uint32_t layer, uint32_t moe_layer, uint32_t pos, float* d_hidden,

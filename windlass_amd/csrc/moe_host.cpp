@@ -17,6 +17,7 @@
 #include <vector>
 
 #include "../../include/windlass_moe.h"
+#include "attention.h"
 #include "expert_files.h"
 #include "host_internal.h"
 #include "internal.h"
@@ -31,6 +32,10 @@ struct LayerState {
     int32_t shared_dtype = WL_SHARED_BF16;
     bool set = false;
     std::vector<void*> owned;  // router / bias / norm buffers the context took over (wl_load_layer)
+    // a dense MLP layer (wl_set_layer_dense): no router, no experts
+    bool dense = false;
+    const uint16_t *mlp_gate = nullptr, *mlp_up = nullptr, *mlp_down = nullptr;
+    uint32_t dense_inter = 0;
 };
 
 // HBM expert cache (config 4): LRU slot pool filled from pinned host blocks.
@@ -106,6 +111,7 @@ struct wl_ctx {
     uint32_t* part = nullptr;
     uint32_t* tsh = nullptr;
     uint32_t ptag = 0;  // the partials' tag of the last decode call: 1, 2, 3, 1, ...
+    bool stale_partials = false;  // a phased call's combine launch failed after its first segment ran
     uint32_t* sync = nullptr;   // barrier words (uncached)
     wl::SyncMap sm{};
     wl::Plan plan{};
@@ -131,6 +137,11 @@ struct wl_ctx {
     int32_t* h_pin = nullptr;      // pinned host words, PinMap layout
     std::vector<int32_t> uniq;     // a batched chunk's routed experts (capacity E, reserved once)
     hipEvent_t ids_ev = nullptr, pred_ev = nullptr;
+    // dense MLP layers: gate / up outputs [dense_cap] f32, and an all-ones
+    // norm weight [H] bf16 for a layer bound without one
+    float *dense_g = nullptr, *dense_u = nullptr;
+    uint32_t dense_cap = 0;
+    uint16_t* ones_ln = nullptr;
 };
 
 // Word offsets in wl_ctx::h_pin: routed ids, the abort word, predicted ids of
@@ -434,6 +445,7 @@ static wl_status set_layer_checked(wl_ctx* c, uint32_t layer, const uint16_t* d_
     L.bias = d_router_bias;
     L.ln = d_post_attn_ln;
     L.shared_dtype = parts ? WL_SHARED_MXFP4 : WL_SHARED_BF16;
+    L.dense = false;
     if (parts) c->any_sh4 = true;
     const wl::DecodeArgs a = layer_record(c, layer);
     hipError_t e = hipMemcpy(c->d_largs + layer, &a, sizeof(a), hipMemcpyHostToDevice);
@@ -477,6 +489,49 @@ wl_status wl_set_layer_mxfp4(wl_ctx* c, uint32_t layer, const uint16_t* d_router
                              const uint8_t* d_sh_down_s) {
     const uint8_t* parts[6] = {d_sh_gate_w, d_sh_gate_s, d_sh_up_w, d_sh_up_s, d_sh_down_w, d_sh_down_s};
     return set_layer(c, layer, d_router_w, d_router_bias, d_post_attn_ln, nullptr, parts);
+}
+
+wl_status wl_set_layer_dense(wl_ctx* c, uint32_t layer, const uint16_t* d_post_ln, const uint16_t* d_gate,
+                             const uint16_t* d_up, const uint16_t* d_down, uint32_t dense_inter) {
+    if (!c) return WL_ERR_INVALID;
+    if (layer >= c->cfg.n_layers) return fail(c, WL_ERR_INVALID, "layer %u >= n_layers %u", layer, c->cfg.n_layers);
+    if (!d_gate || !d_up || !d_down) return fail(c, WL_ERR_INVALID, "gate, up and down are required");
+    if (dense_inter == 0 || dense_inter % 8 || dense_inter > 16384)
+        return fail(c, WL_ERR_INVALID, "dense_inter=%u must be a positive multiple of 8, at most 16384", dense_inter);
+    if (((uintptr_t)d_gate | (uintptr_t)d_up | (uintptr_t)d_down | (uintptr_t)d_post_ln) % 16)
+        return fail(c, WL_ERR_INVALID, "dense MLP tensors must be 16-byte aligned");
+    const uint32_t H = c->cfg.hidden;
+    // no kernel may still read what the layer held before (owned router /
+    // bias / norm copies, or the dense scratch being replaced)
+    hipError_t e = hipDeviceSynchronize();
+    if (e != hipSuccess) return hip_fail(c, e, "dense layer bind");
+    if (dense_inter > c->dense_cap) {
+        wl_status st;
+        if ((st = dalloc(c, &c->dense_g, 4 * (size_t)dense_inter)) != WL_OK ||
+            (st = dalloc(c, &c->dense_u, 4 * (size_t)dense_inter)) != WL_OK)
+            return st;  // a smaller pair stays owned by the context until it is destroyed
+        c->dense_cap = dense_inter;
+    }
+    if (!d_post_ln && !c->ones_ln) {
+        wl_status st = dalloc(c, &c->ones_ln, 2 * (size_t)H);
+        if (st != WL_OK) return st;
+        const std::vector<uint16_t> ones(H, 0x3F80u);  // bf16 1.0
+        if ((e = hipMemcpy(c->ones_ln, ones.data(), 2 * (size_t)H, hipMemcpyHostToDevice)) != hipSuccess)
+            return hip_fail(c, e, "norm weight upload");
+    }
+    LayerState& L = c->layers[layer];
+    for (void* p : L.owned) (void)hipFree(p);
+    L.owned.clear();
+    L.router_w = nullptr;
+    L.bias = nullptr;
+    L.ln = d_post_ln ? d_post_ln : c->ones_ln;
+    L.mlp_gate = d_gate;
+    L.mlp_up = d_up;
+    L.mlp_down = d_down;
+    L.dense_inter = dense_inter;
+    L.dense = true;
+    L.set = true;
+    return WL_OK;
 }
 
 }  // extern "C"
@@ -756,7 +811,8 @@ static wl_status source_prepare(wl_ctx* c, uint32_t layer, const float* d_hidden
     if (le != 0) return hip_fail(c, (hipError_t)le, "slot table fill");
     CacheState& C = c->cache;
     C.spec_pending = false;
-    if (c->src_cache && C.speculate && next < c->cfg.n_layers && c->n_bound[next] == 0 && c->layers[next].set) {
+    if (c->src_cache && C.speculate && next < c->cfg.n_layers && c->n_bound[next] == 0 && c->layers[next].set &&
+        !c->layers[next].dense) {
         if (++c->epoch >= 0x7FFFFFFFu) c->epoch = 1;
         le = wl::launch_route(c->d_largs + next, d_hidden, c->epoch, H, E, c->grid, s);
         if (le != 0) return hip_fail(c, (hipError_t)le, "speculative route launch");
@@ -778,6 +834,24 @@ static wl_status cache_speculate(wl_ctx* c, hipStream_t s) {
     return cache_resolve(c, C.spec_layer, c->h_pin + PinMap::pred, c->cfg.n_experts_per_tok, s, true, nullptr);
 }
 
+// A dense MLP layer (the dense branch of run_moe, src/glm_layer_runner.cuh:
+// 373-384): out = resid + down(silu(gate x) * up x), x = RMSNorm(hidden), in
+// two stream-ordered GEMV launches; the norm goes to the norm tap. d_out may
+// alias d_hidden and d_resid exactly (launch_dense_mlp reads hidden in its
+// first launch and each resid row before writing it).
+static wl_status run_dense(wl_ctx* c, uint32_t layer, const float* d_hidden, const float* d_resid, float* d_out,
+                           void* stream) {
+    const LayerState& L = c->layers[layer];
+    if (((uintptr_t)d_hidden | (uintptr_t)d_out | (uintptr_t)d_resid) % 16)
+        return fail(c, WL_ERR_INVALID, "a dense layer's hidden, residual and output must be 16-byte aligned");
+    const wl::attn::DenseMlp m{L.ln, L.mlp_gate, L.mlp_up, L.mlp_down, c->cfg.hidden, L.dense_inter,
+                               c->cfg.rms_eps};
+    const int e = wl::attn::launch_dense_mlp(m, d_hidden, d_resid, d_out, c->dense_g, c->dense_u, c->norm, nullptr,
+                                             stream);
+    if (e != 0) return hip_fail(c, (hipError_t)e, "dense MLP launch");
+    return WL_OK;
+}
+
 // in_place: d_out == d_hidden == d_resid is allowed (h <- h + moe(h)): every
 // work-group reads all of h for its norm before it publishes any partial, and
 // a combine block is written only after every partial of it is in, so no
@@ -792,6 +866,7 @@ static wl_status run_layer(wl_ctx* c, uint32_t layer, const float* d_hidden, con
     if (in_place ? (d_out != d_hidden || d_resid != d_hidden)
                  : (d_out == d_hidden || (d_resid && d_out == d_resid)))
         return fail(c, WL_ERR_INVALID, "d_out must not alias the inputs");
+    if (L.dense) return run_dense(c, layer, d_hidden, d_resid, d_out, stream);
     const uint32_t H = c->cfg.hidden, I = c->cfg.moe_inter, E = c->cfg.n_routed_experts,
                    K = c->cfg.n_experts_per_tok, SI = c->SI;
     const bool cached = c->n_bound[layer] == 0 && c->src.get != nullptr;
@@ -807,8 +882,22 @@ static wl_status run_layer(wl_ctx* c, uint32_t layer, const float* d_hidden, con
     if (++c->epoch >= 0x7FFFFFFFu) c->epoch = 1;
     dyn.epoch = c->epoch;
     // per decode call (the routing launches also take epochs), so consecutive
-    // calls' partials never share a tag
-    c->ptag = c->ptag % 3u + 1u;
+    // calls' partials never share a tag. The tag is kept only once every
+    // launch of the call is enqueued: a launch that fails enqueues nothing,
+    // so the next call reuses the tag (the combine's ticket counter for it
+    // was cleared by the last call that ran a combine).
+    if (c->stale_partials) {
+        // a segment-0 launch ran without its combine: its words carry a tag
+        // the next calls will use, and the next tag's ticket was not cleared
+        hipError_t e = hipDeviceSynchronize();
+        if (e == hipSuccess) e = hipMemset(c->sync + c->sm.ticket, 0, 4 * 3);
+        if (e == hipSuccess) e = hipMemset(c->part, 0, 4 * (size_t)H * c->grid);
+        if (e == hipSuccess) e = hipMemset(c->tsh, 0, 4 * (size_t)H * c->grid);
+        if (e == hipSuccess) e = hipDeviceSynchronize();
+        if (e != hipSuccess) return hip_fail(c, e, "partial-sum reset");
+        c->stale_partials = false;
+    }
+    const uint32_t ptag = c->ptag % 3u + 1u;
     dyn.hidden = d_hidden;
     dyn.sh_native = L.shared;
     dyn.router_w = L.router_w;
@@ -819,7 +908,7 @@ static wl_status run_layer(wl_ctx* c, uint32_t layer, const float* d_hidden, con
     dyn.resid = d_resid;
     dyn.out = d_out;
     auto launch = [&](uint32_t lo, uint32_t hi) -> wl_status {
-        dyn.seg = lo | (hi << 8) | ((c->taps ? 1u : 0u) << 16) | (c->ptag << 24);
+        dyn.seg = lo | (hi << 8) | ((c->taps ? 1u : 0u) << 16) | (ptag << 24);
         int e = wl::launch_decode(c->d_largs + layer, dyn, H, I, SI, E, K, c->grid,
                                   L.shared_dtype == WL_SHARED_MXFP4, stream);
         if (e != 0) return hip_fail(c, (hipError_t)e, "decode launch");
@@ -827,12 +916,19 @@ static wl_status run_layer(wl_ctx* c, uint32_t layer, const float* d_hidden, con
     };
     if (c->sched == WL_SCHED_FUSED) {
         wl_status s = launch(0, 1);
-        if (s != WL_OK || !cached) return s;
+        if (s != WL_OK) return s;
+        c->ptag = ptag;
+        if (!cached) return s;
         return cache_speculate(c, (hipStream_t)stream);
     }
     wl_status s;
     if ((s = launch(0, 0)) != WL_OK) return s;
-    if ((s = launch(1, 1)) != WL_OK || !cached) return s;
+    if ((s = launch(1, 1)) != WL_OK) {
+        c->stale_partials = true;
+        return s;
+    }
+    c->ptag = ptag;
+    if (!cached) return s;
     return cache_speculate(c, (hipStream_t)stream);
 }
 
@@ -971,6 +1067,7 @@ static wl_status batched_check(wl_ctx* c, uint32_t layer, uint32_t n_tokens, con
         return fail(c, WL_ERR_INVALID, "d_out partly overlaps an input (only exact aliasing is allowed)");
     if (((uintptr_t)d_hidden | (uintptr_t)d_out | (uintptr_t)d_resid) % 16u)
         return fail(c, WL_ERR_INVALID, "batched buffers must be 16-byte aligned");
+    if (c->layers[layer].dense) return WL_OK;
     const uint32_t E = c->cfg.n_routed_experts;
     if (E > wl::batched_max_experts())
         return fail(c, WL_ERR_INVALID, "the batched layer supports at most %u routed experts (config: %u)",
@@ -1072,11 +1169,25 @@ static wl_status batched_run(wl_ctx* c, uint32_t layer, uint32_t n_tokens, const
     return WL_OK;
 }
 
+// A dense layer of a batched call: the dense MLP per position (the reference
+// has nothing to amortise there either and runs run_moe + residual_add per
+// position, src/glm_layer_runner.cuh:985-994). No scratch beyond the layer's.
+static wl_status batched_dense(wl_ctx* c, uint32_t layer, uint32_t n_tokens, const float* d_hidden,
+                               const float* d_resid, float* d_out, void* stream) {
+    const size_t H = c->cfg.hidden;
+    for (uint32_t t = 0; t < n_tokens; t++) {
+        wl_status s = run_dense(c, layer, d_hidden + t * H, d_resid ? d_resid + t * H : nullptr, d_out + t * H, stream);
+        if (s != WL_OK) return s;
+    }
+    return WL_OK;
+}
+
 wl_status wl_run_moe_batched(wl_ctx* c, uint32_t layer, uint32_t n_tokens, const float* d_hidden,
                              const float* d_resid, float* d_out, void* stream) {
     if (!c) return WL_ERR_INVALID;
     wl_status s = batched_check(c, layer, n_tokens, d_hidden, d_resid, d_out);
     if (s != WL_OK) return s;
+    if (c->layers[layer].dense) return batched_dense(c, layer, n_tokens, d_hidden, d_resid, d_out, stream);
     // Tokens run in chunks: bounded scratch, and every piece array stays under
     // 2 GB.
     const uint32_t chunk = batch_offset_cap(c);
@@ -1090,6 +1201,7 @@ wl_status wl_run_moe_batched_noalloc(wl_ctx* c, uint32_t layer, uint32_t n_token
     if (!c) return WL_ERR_INVALID;
     wl_status s = batched_check(c, layer, n_tokens, d_hidden, d_resid, d_out);
     if (s != WL_OK) return s;
+    if (c->layers[layer].dense) return batched_dense(c, layer, n_tokens, d_hidden, d_resid, d_out, stream);
     if (!c->scratch) return fail(c, WL_ERR_STATE, "static scratch of device %d not resolved", c->device);
     const uint32_t chunk = std::min(batch_offset_cap(c), batch_tokens_fitting(c, wl::noalloc_scratch_bytes()));
     if (chunk == 0)
@@ -1173,6 +1285,49 @@ wl_status wl_set_expert_source(wl_ctx* c, const wl_expert_source* src) {
     if (s != WL_OK) return s;
     if (!src->native && (s = ensure_stage(c, c->cfg.n_experts_per_tok)) != WL_OK) return s;
     c->src = *src;
+    return WL_OK;
+}
+
+wl_status wl_make_resident(wl_ctx* c, uint32_t layer, void* stream) {
+    if (!c) return WL_ERR_INVALID;
+    if (layer >= c->cfg.n_layers) return fail(c, WL_ERR_INVALID, "layer %u >= n_layers %u", layer, c->cfg.n_layers);
+    if (c->layers[layer].dense) return fail(c, WL_ERR_INVALID, "layer %u is a dense layer: it has no experts", layer);
+    if (!c->src.get) return fail(c, WL_ERR_STATE, "the context has no expert source");
+    if (c->src_cache) return fail(c, WL_ERR_STATE, "the built-in cache is the context's source");
+    const uint32_t E = c->cfg.n_routed_experts;
+    if (c->n_bound[layer] == E) return WL_OK;
+    if (c->n_bound[layer] != 0)
+        return fail(c, WL_ERR_STATE, "layer %u has %u of %u experts bound", layer, c->n_bound[layer], E);
+    const size_t nb = c->native_bytes;
+    void* mem = nullptr;
+    hipError_t e = hipMalloc(&mem, (size_t)E * nb);
+    if (e != hipSuccess)
+        return fail(c, WL_ERR_OOM, "%u native blocks for layer %u: %s", E, layer, hipGetErrorString(e));
+    c->allocs.push_back(mem);
+    uint8_t* blocks = (uint8_t*)mem;
+    const wl_expert_source& S = c->src;
+    hipStream_t s = (hipStream_t)stream;
+    for (uint32_t x = 0; x < E; x++) {
+        c->src_status = WL_OK;
+        const uint8_t* p = S.get_async ? S.get_async(S.user, layer, x, (void*)s) : S.get(S.user, layer, x);
+        if (!p) {
+            if (c->src_status != WL_OK) return c->src_status;
+            return fail(c, WL_ERR_IO, "expert source returned no block for layer %u expert %u", layer, x);
+        }
+        uint8_t* dst = blocks + (size_t)x * nb;
+        if (S.native) {
+            if ((e = hipMemcpyAsync(dst, p, nb, hipMemcpyDeviceToDevice, s)) != hipSuccess)
+                return hip_fail(c, e, "resident block copy");
+        } else if (wl::launch_expert_to_native(p, dst, c->cfg.hidden, c->cfg.moe_inter, 0, s) != 0) {
+            return fail(c, WL_ERR_HIP, "expert conversion launch failed");
+        }
+    }
+    if ((e = hipStreamSynchronize(s)) != hipSuccess) return hip_fail(c, e, "resident fill");
+    const size_t row = (size_t)layer * E;
+    for (uint32_t x = 0; x < E; x++) c->h_slot[row + x] = blocks + (size_t)x * nb;
+    c->n_bound[layer] = E;
+    e = hipMemcpy(c->d_slot + row, &c->h_slot[row], sizeof(void*) * E, hipMemcpyHostToDevice);
+    if (e != hipSuccess) return hip_fail(c, e, "slot table update");
     return WL_OK;
 }
 

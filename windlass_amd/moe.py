@@ -124,6 +124,8 @@ def load():
         "wl_create": [ctypes.POINTER(MoeConfig), ctypes.POINTER(vp)],
         "wl_set_layer": [vp, u32, vp, vp, vp, vp, i32],
         "wl_set_layer_mxfp4": [vp, u32, vp, vp, vp, vp, vp, vp, vp, vp, vp],
+        "wl_set_layer_dense": [vp, u32, vp, vp, vp, vp, u32],
+        "wl_make_resident": [vp, u32, vp],
         "wl_slot_bind": [vp, u32, u32, vp],
         "wl_slot_unbind": [vp, u32, u32],
         "wl_slot_pool_create": [vp, u32],
@@ -438,6 +440,13 @@ class Context:
     def set_layer_mxfp4(self, layer, router_w, bias, ln_w, gw, gs, uw, us, dw, ds):
         self._ck(self.lib.wl_set_layer_mxfp4(self.h, layer, router_w, bias, ln_w, gw, gs, uw, us, dw, ds),
                  "wl_set_layer_mxfp4")
+
+    def set_layer_dense(self, layer, post_ln, gate, up, down, dense_inter):
+        self._ck(self.lib.wl_set_layer_dense(self.h, layer, post_ln, gate, up, down, dense_inter),
+                 "wl_set_layer_dense")
+
+    def make_resident(self, layer, stream=0):
+        self._ck(self.lib.wl_make_resident(self.h, layer, stream), "wl_make_resident")
 
     def load_layer(self, st, ckpt_layer, layer):
         self._ck(self.lib.wl_load_layer(self.h, st.h, ckpt_layer, layer), "wl_load_layer")
