@@ -801,6 +801,32 @@ def main():
         ms_p, st_p = measure()
         per_policy[pol] = (ms_p, st_p)
     ms, cstats = per_policy[policies[0]]
+    replay = None
+    if cache:
+        # the request trace of the measured tokens (warm-up + timed, the same
+        # start states), recorded layer by layer through the taps, replayed
+        # through every policy and through Belady's offline bound; hit rates
+        # over the timed tokens, as measured
+        E_, K_ = c["n_routed_experts"], c["n_experts_per_tok"]
+        dm.ctx.cache_set_policy(policies[0])
+        trace = []
+        for i in range(args.warmup + args.steps):
+            hip.copy_d2d(d_h.ptr, d_hs.ptr + 4 * H * (i % n_h), 4 * H, stream.handle)
+            cur, nxt = d_h, d_tmp
+            for l in range(args.layers):
+                dm.ctx.run_moe_residual(l, cur.ptr, cur.ptr, nxt.ptr, stream.handle)
+                stream.synchronize()
+                trace += [l * E_ + int(e) for e in hip.download_ptr(dm.ctx.taps()["topk_idx"], np.int32, K_)]
+                cur, nxt = nxt, cur
+        dm.ctx.check_error(stream.handle)
+        t0 = args.warmup * args.layers * K_
+        replay = {}
+        for pol in ["lru", "lfu", "slru", "2q", "tinylfu", "belady", "belady_bypass"]:
+            out = moe.policy_replay(pol, args.cache_slots, trace, K_, pinned=pinned if "belady" not in pol else ())[0]
+            timed = out[t0:]
+            h_ = int((timed == 1).sum())
+            m_ = int(((timed == 0) | (timed == 3)).sum())
+            replay[pol] = round(h_ / max(1, h_ + m_), 4)
     us_per_layer = ms * 1e3 / args.steps / layers_per_step
 
     if args.calib_copy_mb > 0:
@@ -897,6 +923,10 @@ def main():
                                          "tokens_per_s": round(1e6 / (m * 1e3 / args.steps), 3),
                                          "bypassed": st["bypassed"], "h2d_GB": round(st["bytes_h2d"] / 1e9, 3)}
                                    for pol, (m, st) in per_policy.items()},
+                      "replay_hit_rate": replay,
+                      "replay_note": "the timed tokens' request trace (recorded on the GPU) replayed through each "
+                                     "policy (pinned keys as measured) and Belady's offline optimum of plain paging "
+                                     "without / with bypass (an upper bound for every policy)",
                       "zipf": {"s": 1.1, "amplitude": args.zipf_amp}}} if cache else {}),
         "build_s": round(build_s, 1),
     }

@@ -267,7 +267,11 @@ wl_status wl_run_moe_batched(wl_ctx* ctx, uint32_t layer, uint32_t n_tokens, con
  * holds (97 at hidden 6144 / inter 2048 / 8 of 256 experts); a shape whose
  * single token does not fit returns WL_ERR_INVALID. Every call on one GPU
  * shares that GPU's array, which keeps the last call's contents: calls that
- * overlap on one GPU (two streams, two contexts, two host threads) race. */
+ * overlap on one GPU (two streams, two contexts, two host threads) race.
+ * A layer with every expert bound, or a dense layer, enqueues kernels only
+ * and can be captured into a HIP graph and replayed; a layer that runs
+ * through the expert source reads its routing back on the host per chunk,
+ * and fails with WL_ERR_STATE on a stream under capture. */
 wl_status wl_run_moe_batched_noalloc(wl_ctx* ctx, uint32_t layer, uint32_t n_tokens, const float* d_hidden,
                                      const float* d_resid, float* d_out, void* stream);
 
@@ -413,6 +417,19 @@ wl_status wl_cache_get(wl_ctx* ctx, uint32_t layer, uint32_t expert, void* strea
 #define WL_POLICY_SLRU    2
 #define WL_POLICY_2Q      3
 #define WL_POLICY_TINYLFU 4
+/* Offline bounds, accepted by wl_policy_replay only, without pinned keys
+ * (they read every future request of the replayed sequence;
+ * wl_cache_set_policy refuses them):
+ *   WL_POLICY_BELADY         Belady's MIN: evict the key whose next request
+ *                            comes last; every miss is retained
+ *   WL_POLICY_BELADY_BYPASS  MIN with bypass: a missing key whose own next
+ *                            request comes after the victim's is not retained
+ * Both drop the rule that a batch's misses do not evict the keys the batch
+ * has already requested, which makes them the optimum of plain paging, and
+ * an upper bound on the hits of every policy of the same kind (retaining
+ * every miss, or free to decline one) under the batch rule, pinned or not. */
+#define WL_POLICY_BELADY        5
+#define WL_POLICY_BELADY_BYPASS 6
 typedef struct wl_cache_policy {
     int32_t  kind;            /* WL_POLICY_* */
     float    protected_frac;  /* SLRU: share of the slots in the protected segment (0.5) */
@@ -425,9 +442,10 @@ wl_status wl_cache_set_policy(wl_ctx* ctx, const wl_cache_policy* policy);
  * admitted and never evicted (popularity pinning: pin the most requested keys of a profile). At
  * most capacity - 2 x n_experts_per_tok keys may be pinned. */
 wl_status wl_cache_pin(wl_ctx* ctx, uint32_t layer, uint32_t expert, int32_t pinned);
-/* Test hook (no device use): wl_lru_replay under `policy`, with `n_pinned`
- * pinned keys; hit_out[i] is 1 for a hit, 0 for a retained miss, 3 for a miss
- * not retained, 2 for a skipped duplicate. */
+/* Replay hook (no device use): wl_lru_replay under `policy` (an online
+ * policy, or one of the offline bounds), with `n_pinned` pinned keys;
+ * hit_out[i] is 1 for a hit, 0 for a retained miss, 3 for a miss not
+ * retained, 2 for a skipped duplicate. */
 wl_status wl_policy_replay(const wl_cache_policy* policy, uint32_t capacity, const uint32_t* keys, uint32_t n_keys,
                            uint32_t batch, const uint32_t* pinned, uint32_t n_pinned, uint8_t* hit_out,
                            uint64_t* hits, uint64_t* misses, uint64_t* evictions);

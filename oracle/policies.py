@@ -108,3 +108,49 @@ def replay(kind, capacity, keys, batch, protected_frac=0.5, ghost=0, pinned=()):
             out.append(c.request(k, seen))
             seen.add(k)
     return out, c.hits, c.misses, c.evictions
+
+
+def belady(capacity, keys, batch, bypass=False):
+    """Belady's offline bound (no reference counterpart; the library's
+    WL_POLICY_BELADY / WL_POLICY_BELADY_BYPASS replay kinds): keys repeated
+    within a batch are skipped; with every future request known, a miss
+    evicts the resident key whose next request comes last (keys never
+    requested again first, the smaller key of those first); with bypass, a
+    miss whose own next request comes after that victim's is not retained.
+    Unlike replay(), a batch's miss may evict a key the batch has already
+    requested: the bound is plain paging, where this rule is the optimum.
+    Returns (per-key codes, hits, misses, evictions) like replay(). Written
+    as a forward scan for each next request, independently of the library's
+    precomputed next-use table."""
+    never = float("inf")
+
+    def next_use(k, i):
+        for j in range(i + 1, len(keys)):
+            b0 = j - j % batch
+            if keys[j] == k and k not in keys[b0:j]:
+                return j
+        return never
+
+    cache = set()
+    out = []
+    hits = misses = evictions = 0
+    for i, k in enumerate(keys):
+        b0 = i - i % batch
+        if k in keys[b0:i]:
+            out.append(2)
+            continue
+        if k in cache:
+            hits += 1
+            out.append(1)
+            continue
+        misses += 1
+        if len(cache) >= capacity:
+            victim = max(cache, key=lambda c: (next_use(c, i), -c))
+            if bypass and not next_use(k, i) < next_use(victim, i):
+                out.append(3)
+                continue
+            cache.remove(victim)
+            evictions += 1
+        cache.add(k)
+        out.append(0)
+    return out, hits, misses, evictions

@@ -150,3 +150,107 @@ def test_planted_mistakes_fail_the_hand_cases():
     assert _replay_with(AdmitOnTie, "tinylfu", 2, SEQ) != HAND["tinylfu"]
     assert _replay_with(OP.PolicyCache, "lfu", 2, [1, 2, 3, 1]) != _replay_with(LfuTiesToNewest, "lfu", 2,
                                                                                  [1, 2, 3, 1])
+
+
+# ---- Belady's offline bound ------------------------------------------------
+
+def _optimum(capacity, keys, batch, bypass, protect_batch):
+    """The most hits any eviction schedule reaches (exhaustive search over
+    every victim choice at every miss, and every decline when bypass is
+    allowed). protect_batch: a miss may not evict a key its batch has already
+    requested (the library's online rule); without it, plain paging."""
+    from functools import lru_cache
+    n = len(keys)
+
+    @lru_cache(maxsize=None)
+    def best(i, cache):
+        if i == n:
+            return 0
+        k = keys[i]
+        b0 = i - i % batch
+        if k in keys[b0:i]:
+            return best(i + 1, cache)
+        if k in cache:
+            return 1 + best(i + 1, cache)
+        if len(cache) < capacity:
+            return best(i + 1, cache | {k})
+        held = set(keys[b0:i]) if protect_batch else set()
+        opts = [best(i + 1, (cache - {v}) | {k}) for v in cache if v not in held]
+        if bypass or not opts:
+            opts.append(best(i + 1, cache))
+        return max(opts)
+
+    return best(0, frozenset())
+
+
+def test_belady_hand_case():
+    # capacity 2, SEQ = 1 2 1 3 1 3 2: 3 misses with {1 (next at 4), 2 (next
+    # at 6)} resident and evicts 2; the last 2 finds {1, 3}, both never
+    # requested again: without bypass it evicts 1 (the smaller key), with
+    # bypass it is not retained (its own next request, never, is not earlier)
+    for got in (moe.policy_replay("belady", 2, SEQ, 1), OP.belady(2, SEQ, 1)):
+        assert (list(got[0]), tuple(got[1:])) == ([0, 0, 1, 0, 1, 1, 0], (3, 4, 2))
+    for got in (moe.policy_replay("belady_bypass", 2, SEQ, 1), OP.belady(2, SEQ, 1, bypass=True)):
+        assert (list(got[0]), tuple(got[1:])) == ([0, 0, 1, 0, 1, 1, 3], (3, 4, 1))
+
+
+@pytest.mark.parametrize("bypass", [False, True])
+def test_belady_is_the_optimum_on_small_sequences(bypass):
+    """Exhaustive search pins the bound: on random small batched sequences
+    Belady's hits equal the most any eviction schedule reaches in plain
+    paging, and are at least the most under the online batch rule."""
+    rng = np.random.default_rng(11 + bypass)
+    for case in range(150):
+        batch = int(rng.integers(1, 3))
+        cap = int(rng.integers(batch + 1, 4))
+        keys = []
+        for _ in range(int(rng.integers(4, 9))):
+            keys += [int(x) for x in rng.integers(0, 6, size=batch)]
+        want = _optimum(cap, tuple(keys), batch, bypass, False)
+        kind = "belady_bypass" if bypass else "belady"
+        assert moe.policy_replay(kind, cap, keys, batch)[1] == want, (case, cap, batch, keys)
+        assert OP.belady(cap, keys, batch, bypass)[1] == want, (case, cap, batch, keys)
+        assert _optimum(cap, tuple(keys), batch, bypass, True) <= want
+
+
+@pytest.mark.parametrize("seed", [0, 1])
+def test_belady_engine_matches_oracle_and_bounds_every_policy(seed):
+    keys = zipf_batches(300, 8, 200, 1.1, seed)
+    pinned = [keys[5], keys[60]]
+    for cap in (24, 48):
+        for bypass in (False, True):
+            got = moe.policy_replay("belady_bypass" if bypass else "belady", cap, keys, 8)
+            want = OP.belady(cap, keys, 8, bypass)
+            assert list(got[0]) == want[0] and got[1:] == want[1:], (cap, bypass)
+        bound = moe.policy_replay("belady", cap, keys, 8)[1]
+        bound_bypass = moe.policy_replay("belady_bypass", cap, keys, 8)[1]
+        assert bound <= bound_bypass
+        for kind in ("lru", "lfu", "slru"):
+            assert moe.policy_replay(kind, cap, keys, 8)[1] <= bound, (kind, cap)
+            assert moe.policy_replay(kind, cap, keys, 8, pinned=pinned)[1] <= bound, (kind, cap)
+        for kind in ("2q", "tinylfu"):
+            assert moe.policy_replay(kind, cap, keys, 8)[1] <= bound_bypass, (kind, cap)
+    with pytest.raises(moe.WindlassError):  # the bound takes no pinned keys
+        moe.policy_replay("belady", 24, keys, 8, pinned=pinned)
+
+
+def test_planted_mistake_fails_the_belady_hand_case():
+    """Evicting the key whose next request comes FIRST (a planted sign
+    mistake, in a copy of the oracle's rule) changes the hand answer."""
+    never = float("inf")
+
+    def nearest_victim(capacity, keys):
+        cache, hits = [], 0
+        for i, k in enumerate(keys):
+            if k in cache:
+                hits += 1
+                continue
+            if len(cache) >= capacity:
+                nxt = {c: next((j for j in range(i + 1, len(keys)) if keys[j] == c), never) for c in cache}
+                cache.remove(min(cache, key=lambda c: nxt[c]))
+            cache.append(k)
+        return hits
+
+    assert nearest_victim(2, SEQ) != OP.belady(2, SEQ, 1)[1]
+    assert moe.policy_replay("belady", 2, [1, 2, 3, 1, 2], 1)[1] == 1
+    assert moe.policy_replay("lru", 2, [1, 2, 3, 1, 2], 1)[1] == 0

@@ -11,7 +11,7 @@ import pytest
 from oracle import moe_oracle as O
 from oracle import synth
 from windlass_amd import hip as H_
-from windlass_amd import synthdata
+from windlass_amd import moe, synthdata
 from windlass_amd.model import DeviceModel
 
 pytestmark = pytest.mark.gpu
@@ -62,4 +62,59 @@ def test_noalloc_matches_batched(gpu, shape):
         else:
             ref = _run(dm, hs, resid, False)
             assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+    dm.close()
+
+
+def test_noalloc_allocates_nothing_and_replays_from_a_graph(gpu):
+    """The resident path of the allocation-free entry point: device free
+    memory is unchanged across a call; captured into a HIP graph on a stream,
+    it replays to the eager call's bits three times, with eager work of the
+    program (an allocating batched call on other tokens, a buffer clear,
+    synchronisations) between the replays. A source-backed layer refuses to
+    run under capture."""
+    from windlass_amd.model import SourceModel
+    c = SMALL
+    H = c["hidden"]
+    dm = DeviceModel(c, seed=22, n_layers=1)
+    T = 40
+    hs = _tokens(H, T, 950)
+    dh = H_.DeviceBuffer.from_array(hs)
+    do = H_.DeviceBuffer(4 * T * H)
+    other = H_.DeviceBuffer.from_array(_tokens(H, 9, 951))
+    other_out = H_.DeviceBuffer(4 * 9 * H)
+    st = H_.Stream()
+    # scratch of the allocating path grown beforehand, so later eager calls allocate nothing either
+    dm.ctx.run_moe_batched(0, 9, other.ptr, None, other_out.ptr, st.handle)
+    st.synchronize()
+    free0, _ = H_.mem_info()
+    dm.ctx.run_moe_batched_noalloc(0, T, dh.ptr, None, do.ptr, st.handle)
+    dm.ctx.check_error(st.handle)
+    assert H_.mem_info()[0] == free0
+    eager = do.download(np.float32)
+    g = H_.Graph(st)
+    g.begin()
+    dm.ctx.run_moe_batched_noalloc(0, T, dh.ptr, None, do.ptr, st.handle)
+    g.end()
+    try:
+        for rep in range(3):
+            do.zero()
+            H_.synchronize()
+            g.launch()
+            st.synchronize()
+            got = do.download(np.float32)
+            assert np.array_equal(got.view(np.uint32), eager.view(np.uint32)), rep
+            dm.ctx.run_moe_batched(0, 9, other.ptr, None, other_out.ptr, st.handle)
+            dm.ctx.check_error(st.handle)
+        print("noalloc graph: 3 replays bit-equal to the eager call", flush=True)
+    finally:
+        g.destroy()
+    sm = SourceModel(dm, native=True)
+    g2 = H_.Graph(st)
+    g2.begin()
+    with pytest.raises(moe.WindlassError) as ei:
+        sm.ctx.run_moe_batched_noalloc(0, T, dh.ptr, None, do.ptr, st.handle)
+    g2.end()
+    g2.destroy()
+    assert ei.value.status == 5  # WL_ERR_STATE
+    sm.close()
     dm.close()

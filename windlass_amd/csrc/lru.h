@@ -29,13 +29,15 @@
 #include <stdint.h>
 
 #include <list>
+#include <set>
 #include <unordered_map>
 #include <unordered_set>
+#include <utility>
 #include <vector>
 
 namespace wl {
 
-enum Policy : int32_t { kLru = 0, kLfu = 1, kSlru = 2, k2Q = 3, kTinyLfu = 4 };
+enum Policy : int32_t { kLru = 0, kLfu = 1, kSlru = 2, k2Q = 3, kTinyLfu = 4, kBelady = 5, kBeladyBypass = 6 };
 
 class SlotLru {
 public:
@@ -227,5 +229,85 @@ private:
     std::unordered_set<uint32_t> pinned_;
     uint64_t hits_ = 0, misses_ = 0, evictions_ = 0;
 };
+
+// Belady's offline bound over a whole request sequence (replay only: it
+// needs every future request; no reference counterpart, the reference's
+// results discuss LRU only, docs/RESULTS.md:113,123). Keys repeated within a
+// batch are skipped (marked 2), as in SlotLru. The bound drops the one
+// constraint SlotLru adds to plain paging, that a key the current batch has
+// requested is not evicted by the batch's later misses; without it the
+// problem is classic paging, where MIN is the optimum, and the relaxed
+// optimum bounds every policy under the constraint (and with pinned keys)
+// from above. A miss takes a free slot while one is left; otherwise the
+// resident key whose next request comes last (never requested again first)
+// is evicted. With bypass, a missing key whose own next request comes after
+// that victim's is not retained (marked 3), the optimum of a cache that may
+// decline a key (the model of the admission policies); without bypass, of
+// one that retains every miss (LRU, LFU, SLRU). Ties (keys never requested
+// again) go to the smaller key. hit_out[i]: 1 hit, 0 retained miss, 3 miss
+// not retained, 2 duplicate within its batch.
+inline void belady_replay(uint32_t capacity, const uint32_t* keys, uint32_t n, uint32_t batch, bool bypass,
+                          uint8_t* hit_out, uint64_t* hits, uint64_t* misses, uint64_t* evictions) {
+    const uint64_t kNever = ~0ull;
+    std::vector<uint8_t> dup(n, 0);
+    for (uint32_t b0 = 0; b0 < n; b0 += batch) {
+        const uint32_t b1 = b0 + batch < n ? b0 + batch : n;
+        for (uint32_t i = b0; i < b1; i++)
+            for (uint32_t j = b0; j < i && !dup[i]; j++) dup[i] = keys[j] == keys[i];
+    }
+    // next[i]: the position of the next request of keys[i] (duplicates skipped)
+    std::vector<uint64_t> next(n, kNever);
+    {
+        std::unordered_map<uint32_t, uint64_t> seen;
+        for (uint32_t i = n; i-- > 0;) {
+            if (dup[i]) continue;
+            auto it = seen.find(keys[i]);
+            next[i] = it == seen.end() ? kNever : it->second;
+            seen[keys[i]] = i;
+        }
+    }
+    std::unordered_map<uint32_t, uint64_t> due;  // resident key -> its next request
+    // (next request, key): the victim is the last element, so among keys
+    // never requested again the smallest is stored as the largest
+    std::set<std::pair<uint64_t, uint32_t>> by_due;
+    auto order_key = [](uint32_t k) { return ~k; };
+    uint64_t h = 0, m = 0, ev = 0;
+    for (uint32_t i = 0; i < n; i++) {
+        if (dup[i]) {
+            if (hit_out) hit_out[i] = 2;
+            continue;
+        }
+        const uint32_t k = keys[i];
+        auto it = due.find(k);
+        if (it != due.end()) {
+            by_due.erase({it->second, order_key(k)});
+            it->second = next[i];
+            by_due.insert({next[i], order_key(k)});
+            h++;
+            if (hit_out) hit_out[i] = 1;
+            continue;
+        }
+        m++;
+        uint8_t code = 0;
+        if (due.size() >= capacity) {
+            const auto v = std::prev(by_due.end());
+            if (bypass && !(next[i] < v->first)) {
+                code = 3;
+            } else {
+                due.erase(~v->second);
+                by_due.erase(v);
+                ev++;
+            }
+        }
+        if (code == 0) {
+            due[k] = next[i];
+            by_due.insert({next[i], order_key(k)});
+        }
+        if (hit_out) hit_out[i] = code;
+    }
+    if (hits) *hits = h;
+    if (misses) *misses = m;
+    if (evictions) *evictions = ev;
+}
 
 }  // namespace wl

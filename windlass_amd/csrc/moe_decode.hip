@@ -226,11 +226,13 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const float* hidden, const 
                 for (int i = 0; i < kSNB4; i++) {
                     const uint32_t m = b * kSNB4 + i, kt = v * sg_per + m;
                     const bool valid = m < sg_per && kt < nkg;
+                    // a masked item's nibbles are zero (read past the
+                    // resource) and are selected as zero besides: +0 under any scale
                     const float sc = valid ? e8m0f((B.s[i] >> (8u * (kt % 4u))) & 0xFFu) : 0.f;
 #pragma unroll
                     for (int jj = 0; jj < 4; jj++)
-                        gacc = mma(a_rows3(xp, xps, n, kt * 128u + 32u * g + 8u * jj, valid), fp4x8_bf16(B.w[i][jj], sc),
-                                   gacc);
+                        gacc = mma(a_rows3(xp, xps, n, kt * 128u + 32u * g + 8u * jj, valid),
+                                   fp4x8_bf16(valid ? B.w[i][jj] : 0u, sc), gacc);
                 }
             } else {
 #pragma unroll
@@ -527,12 +529,14 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const float* hidden, const 
                     const uint32_t kt = b * kNB + i;
                     const bool valid = kt < nkg;
                     // a masked item reads another tile (or zeros past the
-                    // block): scale 0 makes its B operand exactly zero
+                    // block): its nibbles are selected as zero, so its B
+                    // operand is +0 under any scale (no item is masked at the
+                    // GLM shape, where the select folds away)
                     const float sc = valid ? e8m0f(batch_scale8(bs, i)) : 0.f;
 #pragma unroll
                     for (int jj = 0; jj < 4; jj++)
                         racc = mma(a_rows3(xp, xps, n, kt * 128u + 32u * g + 8u * jj, valid),
-                                   fp4x8_bf16(B.w[i][jj], sc), racc);
+                                   fp4x8_bf16((GLM || valid) ? B.w[i][jj] : 0u, sc), racc);
                 }
                 if (b == nbg - 1u) {
                     // SwiGLU of this wave's 8 rows: lane r < 8 holds gate row r,

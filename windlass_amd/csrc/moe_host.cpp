@@ -1202,6 +1202,13 @@ wl_status wl_run_moe_batched_noalloc(wl_ctx* c, uint32_t layer, uint32_t n_token
     wl_status s = batched_check(c, layer, n_tokens, d_hidden, d_resid, d_out);
     if (s != WL_OK) return s;
     if (c->layers[layer].dense) return batched_dense(c, layer, n_tokens, d_hidden, d_resid, d_out, stream);
+    if (c->n_bound[layer] == 0) {
+        // a source-backed layer reads its routing back on the host (a
+        // synchronisation), which a stream under capture does not allow
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        if (hipStreamIsCapturing((hipStream_t)stream, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone)
+            return fail(c, WL_ERR_STATE, "layer %u runs through the expert source: it cannot be captured", layer);
+    }
     if (!c->scratch) return fail(c, WL_ERR_STATE, "static scratch of device %d not resolved", c->device);
     const uint32_t chunk = std::min(batch_offset_cap(c), batch_tokens_fitting(c, wl::noalloc_scratch_bytes()));
     if (chunk == 0)
@@ -1487,16 +1494,23 @@ wl_status wl_cache_get(wl_ctx* c, uint32_t layer, uint32_t expert, void* stream,
     return WL_OK;
 }
 
-static bool policy_ok(const wl_cache_policy* p) {
-    return p && p->kind >= WL_POLICY_LRU && p->kind <= WL_POLICY_TINYLFU && p->protected_frac >= 0.f &&
-           p->protected_frac <= 1.f;
+// An online policy (offline = true also admits the Belady bounds).
+static bool policy_ok(const wl_cache_policy* p, bool offline = false) {
+    return p && p->kind >= WL_POLICY_LRU && p->kind <= (offline ? WL_POLICY_BELADY_BYPASS : WL_POLICY_TINYLFU) &&
+           p->protected_frac >= 0.f && p->protected_frac <= 1.f;
 }
 
 wl_status wl_policy_replay(const wl_cache_policy* policy, uint32_t capacity, const uint32_t* keys, uint32_t n_keys,
                            uint32_t batch, const uint32_t* pinned, uint32_t n_pinned, uint8_t* hit_out, uint64_t* hits,
                            uint64_t* misses, uint64_t* evictions) {
-    if (!policy_ok(policy) || capacity == 0 || (n_keys && !keys) || batch == 0 || (n_pinned && !pinned))
+    if (!policy_ok(policy, true) || capacity == 0 || (n_keys && !keys) || batch == 0 || (n_pinned && !pinned))
         return WL_ERR_INVALID;
+    if (policy->kind == WL_POLICY_BELADY || policy->kind == WL_POLICY_BELADY_BYPASS) {
+        if (n_pinned) return WL_ERR_INVALID;  // the bound has no pinned keys (it bounds pinned policies too)
+        wl::belady_replay(capacity, keys, n_keys, batch, policy->kind == WL_POLICY_BELADY_BYPASS, hit_out, hits,
+                          misses, evictions);
+        return WL_OK;
+    }
     wl::SlotLru lru(capacity, policy->kind, policy->protected_frac, policy->ghost, 2u * batch);
     for (uint32_t i = 0; i < n_pinned; i++) lru.pin(pinned[i], true);
     for (uint32_t b0 = 0; b0 < n_keys; b0 += batch) {

@@ -34,6 +34,12 @@ for name, args in [
     ("hipMemGetInfo", [ctypes.POINTER(_sz), ctypes.POINTER(_sz)]),
     ("hipHostMalloc", [ctypes.POINTER(_vp), _sz, ctypes.c_uint]),
     ("hipHostFree", [_vp]),
+    ("hipStreamBeginCapture", [_vp, ctypes.c_int]),
+    ("hipStreamEndCapture", [_vp, ctypes.POINTER(_vp)]),
+    ("hipGraphInstantiate", [ctypes.POINTER(_vp), _vp, _vp, ctypes.c_char_p, _sz]),
+    ("hipGraphLaunch", [_vp, _vp]),
+    ("hipGraphExecDestroy", [_vp]),
+    ("hipGraphDestroy", [_vp]),
 ]:
     fn = getattr(_hip, name)
     fn.argtypes = args
@@ -185,3 +191,37 @@ class Event:
         ms = ctypes.c_float(0)
         check(_hip.hipEventElapsedTime(ctypes.byref(ms), _vp(self.handle), _vp(end.handle)), "elapsed")
         return ms.value
+
+
+class Graph:
+    """A HIP graph captured from one stream (global capture mode): the work
+    enqueued between begin() and end() is recorded, not run; launch() replays
+    it on a stream."""
+
+    def __init__(self, stream):
+        self.stream = stream
+        self.graph = None
+        self.exec = None
+
+    def begin(self):
+        check(_hip.hipStreamBeginCapture(_vp(self.stream.handle), 0), "hipStreamBeginCapture")
+
+    def end(self):
+        g = _vp()
+        check(_hip.hipStreamEndCapture(_vp(self.stream.handle), ctypes.byref(g)), "hipStreamEndCapture")
+        self.graph = g.value
+        if self.graph:
+            e = _vp()
+            check(_hip.hipGraphInstantiate(ctypes.byref(e), _vp(self.graph), None, None, 0), "hipGraphInstantiate")
+            self.exec = e.value
+
+    def launch(self):
+        check(_hip.hipGraphLaunch(_vp(self.exec), _vp(self.stream.handle)), "hipGraphLaunch")
+
+    def destroy(self):
+        if self.exec:
+            _hip.hipGraphExecDestroy(_vp(self.exec))
+            self.exec = None
+        if self.graph:
+            _hip.hipGraphDestroy(_vp(self.graph))
+            self.graph = None

@@ -50,7 +50,7 @@ class CacheStats(ctypes.Structure):
                [("used", ctypes.c_uint32), ("capacity", ctypes.c_uint32), ("bypassed", ctypes.c_uint64)]
 
 
-POLICY = {"lru": 0, "lfu": 1, "slru": 2, "2q": 3, "tinylfu": 4}
+POLICY = {"lru": 0, "lfu": 1, "slru": 2, "2q": 3, "tinylfu": 4, "belady": 5, "belady_bypass": 6}
 
 
 class CachePolicy(ctypes.Structure):
