@@ -4,8 +4,9 @@ attention with the DSA indexer (run_attention, src/glm_layer_runner.cuh:
 
 Checked against transformers' GlmMoeDsaAttention / GlmMoeDsaMLP
 (tests/golden/attn_tf_small.npz) and against the oracle (oracle/attention.py)
-at the fixture's shape, at the GLM shape and over a 2,500-position sequence
-whose DSA selection drops most keys. Bars: f32 outputs within 1e-5
+at the fixture's shape, at the GLM shape (with a small index_topk, and with
+GLM's own 2048 over 2,112 positions) and over 2,500- and 8,400-position
+sequences whose DSA selection drops most keys. Bars: f32 outputs within 1e-5
 rel_to_scale; the selection equal to the oracle's, except where two index
 scores at the top-k boundary are within 1e-5 of each other (then the oracle
 is run with the GPU's selection, as the reference's --force-oracle-topk
@@ -133,6 +134,20 @@ def test_glm_shape(gpu):
     T = 40
     Hs = np.stack([synth.hidden_state(a["hidden"], 2100, p) for p in range(T)]).astype(np.float32)
     _check_positions(am, W, a, Hs, {0, 1, 23, 24, 25, 39}, None, "GLM shape")
+    am.close()
+
+
+def test_glm_shape_at_glm_selection_size(gpu):
+    """GLM dimensions (hidden 6144, 64 heads, q_lora 2048, kv_lora 512,
+    32 indexer heads of 128) with GLM's own index_topk of 2048 over 2,112
+    positions: every key kept up to position 2047, then the radix select
+    dropping 1, 2, 3 and 64 keys (positions 2048-2050 and the last)."""
+    a = dict(GLM_ATTN, index_topk=2048)
+    T = 2112
+    am = AttnModel(a, 25, 2, owners=[True, False], max_seq=T)
+    W = [synthdata.as_f32(w) for w in am.weights]
+    Hs = np.stack([synth.hidden_state(a["hidden"], 2500, p) for p in range(T)]).astype(np.float32)
+    _check_positions(am, W, a, Hs, {1000, 2046, 2047, 2048, 2049, 2050, T - 1}, None, "GLM at index_topk 2048")
     am.close()
 
 
