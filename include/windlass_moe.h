@@ -353,16 +353,20 @@ wl_status wl_cache_create(wl_ctx* ctx, uint32_t capacity, wl_host_block_fn host_
  * `dir`/layer_N.bin, N = first_layer + context layer (256 records of
  * wl_expert_layout.total bytes in the reference layout, record e at offset
  * e x total; tools/repack_experts_glm.py:5-14,46-55). A pool of io_threads
- * workers pread each miss into one of its two pinned buffers, copies it to the
- * device on its own non-blocking stream (after the gate event of the resolve
- * that took the slot, so no kernel enqueued before still reads it) and
- * converts it there into the slot's native layout; wl_cache_get (and the
- * layer run) waits until the read is issued and orders the stream after it.
- * io_threads = 0 reads on the calling thread. Every file must exist and hold
- * all n_routed_experts records (WL_ERR_IO otherwise); a short read fails the
- * call that needs the block with WL_ERR_IO. Each worker (one for
- * io_threads = 0) holds two reference blocks of pinned memory and two of
- * device staging. */
+ * workers pread each miss into one of its two pinned buffers and copies it,
+ * as it is, into the slot on its own non-blocking stream (after the gate
+ * event of the resolve that took the slot, so no kernel enqueued before still
+ * reads it). The workers launch no kernel: a copy engine moves the block, so
+ * nothing shares the CUs with the persistent kernels (see Co-residency).
+ * wl_cache_get (and the layer run) waits until the read is issued, orders the
+ * stream after it and, the first time the slot is handed out, converts it
+ * into the native layout on that stream (one kernel, ~13 us at the GLM
+ * shape, into a spare block that then takes the slot's place). io_threads = 0
+ * reads on the calling thread. Every file must exist and hold all
+ * n_routed_experts records (WL_ERR_IO otherwise); a short read fails the call
+ * that needs the block with WL_ERR_IO. Each worker (one for io_threads = 0)
+ * holds two reference blocks of pinned memory; the cache holds one spare
+ * device block. */
 wl_status wl_cache_create_files(wl_ctx* ctx, uint32_t capacity, const char* dir, uint32_t first_layer,
                                 uint32_t io_threads);
 /* The same with flags: WL_FILES_DIRECT reads with O_DIRECT (bypassing the

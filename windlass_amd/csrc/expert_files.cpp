@@ -8,11 +8,12 @@
 //   2. pread the whole record (a short read fails the task);
 //   3. its stream waits for the task's gate (recorded on the caller's stream
 //      when the slot was resolved: no kernel enqueued before it still reads
-//      the slot), copies host -> device staging, converts staging -> slot
-//      (native layout), records the slot's event and the buffer's event;
+//      the slot), copies the record host -> slot (a DMA copy: no kernel runs
+//      on the worker's stream, so nothing shares the CUs with the caller's
+//      persistent kernels), records the slot's event and the buffer's event;
 //   4. the task is marked issued, so wl_cache_get can order the caller's
 //      stream after the slot's event (an event not yet recorded would order
-//      nothing).
+//      nothing) and convert the record into the native layout on that stream.
 #include "expert_files.h"
 
 #ifndef _GNU_SOURCE
@@ -42,10 +43,6 @@ std::string FileTier::make_worker(Worker& w) {
             w.pinned[b] = nullptr;
             return std::string("pinned io buffer: ") + hipGetErrorString(e);
         }
-        if ((e = hipMalloc((void**)&w.stage[b], ref_bytes_)) != hipSuccess) {
-            w.stage[b] = nullptr;
-            return std::string("device io staging: ") + hipGetErrorString(e);
-        }
         if ((e = hipEventCreateWithFlags(&w.buf_ev[b], hipEventDisableTiming)) != hipSuccess)
             return std::string("io event: ") + hipGetErrorString(e);
     }
@@ -58,13 +55,9 @@ std::string FileTier::make_worker(Worker& w) {
 }
 
 std::string FileTier::open(const std::string& dir, uint32_t first_layer, uint32_t n_layers, uint32_t n_experts,
-                           size_t ref_bytes, size_t native_bytes, uint32_t H, uint32_t I, uint32_t io_threads,
-                           int device, bool direct) {
+                           size_t ref_bytes, uint32_t io_threads, int device, bool direct) {
     first_ = first_layer;
     ref_bytes_ = ref_bytes;
-    native_bytes_ = native_bytes;
-    H_ = H;
-    I_ = I;
     device_ = device;
     direct_ = direct;
     for (uint32_t l = 0; l < n_layers; l++) {
@@ -111,7 +104,6 @@ FileTier::~FileTier() {
         if (w.stream) (void)hipStreamSynchronize(w.stream);
         for (int b = 0; b < 2; b++) {
             if (w.pinned[b]) (void)hipHostFree(w.pinned[b]);
-            if (w.stage[b]) (void)hipFree(w.stage[b]);
             if (w.buf_ev[b]) (void)hipEventDestroy(w.buf_ev[b]);
         }
         if (w.stream) (void)hipStreamDestroy(w.stream);
@@ -191,9 +183,8 @@ bool FileTier::run(Worker& w, FileTask* t) {
         return false;
     };
     if (t->gate && hipStreamWaitEvent(w.stream, t->gate, 0) != hipSuccess) return bad("gate wait");
-    if (hipMemcpyAsync(w.stage[b], buf, ref_bytes_, hipMemcpyHostToDevice, w.stream) != hipSuccess)
+    if (hipMemcpyAsync(t->dst, buf, ref_bytes_, hipMemcpyHostToDevice, w.stream) != hipSuccess)
         return bad("host-to-device copy");
-    if (launch_expert_to_native(w.stage[b], t->dst, H_, I_, 0u, w.stream) != 0) return bad("conversion launch");
     if (hipEventRecord(t->done, w.stream) != hipSuccess) return bad("event record");
     if (hipEventRecord(w.buf_ev[b], w.stream) != hipSuccess) return bad("event record");
     w.used[b] = true;

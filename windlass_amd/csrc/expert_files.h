@@ -2,9 +2,10 @@
 // `dir`/layer_N.bin (the reference's packed expert files: 256 records of one
 // reference-layout expert block each, record e at e x block bytes;
 // tools/repack_experts_glm.py:5-14,46-55) by a pool of pread workers, each
-// with two pinned host buffers and a non-blocking stream, copied to the device
-// and converted there into the slot's native layout (reference I/O path:
-// src/glm_expert_cache.cuh:29-62,339-475). Host-only.
+// with two pinned host buffers and a non-blocking stream, and copied as they
+// are (reference layout) into the slot; the cache converts a slot into the
+// native layout on the caller's stream when it first hands it out (reference
+// I/O path: src/glm_expert_cache.cuh:29-62,339-475). Host-only.
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -20,7 +21,8 @@
 
 namespace wl {
 
-// One block read: record `expert` of file `layer` into device slot `dst`.
+// One block read: record `expert` of file `layer` into device slot `dst`
+// (the record's bytes as they are in the file).
 struct FileTask {
     int fd = -1;
     uint64_t off = 0;
@@ -37,13 +39,12 @@ class FileTier {
 public:
     // Opens dir/layer_{first_layer + l}.bin for l < n_layers and checks that
     // each holds n_experts records of ref_bytes; starts io_threads workers
-    // (0: every read runs on the calling thread). H, I: the shapes for the
-    // device conversion. direct: O_DIRECT reads (ref_bytes a multiple of
-    // 4096) into a page-aligned bounce buffer per worker, copied into the
-    // pinned buffer. Returns an empty string or an error message.
+    // (0: every read runs on the calling thread). direct: O_DIRECT reads
+    // (ref_bytes a multiple of 4096) into a page-aligned bounce buffer per
+    // worker, copied into the pinned buffer. Returns an empty string or an
+    // error message.
     std::string open(const std::string& dir, uint32_t first_layer, uint32_t n_layers, uint32_t n_experts,
-                     size_t ref_bytes, size_t native_bytes, uint32_t H, uint32_t I, uint32_t io_threads, int device,
-                     bool direct = false);
+                     size_t ref_bytes, uint32_t io_threads, int device, bool direct = false);
     ~FileTier();
 
     // Queues the read of (layer, expert) into dst; the copy waits for `gate`
@@ -64,18 +65,17 @@ private:
         uint8_t* pinned[2] = {nullptr, nullptr};
         uint8_t* bounce = nullptr;  // direct mode: page-aligned ordinary memory the O_DIRECT reads land in
                                     // (direct I/O into the runtime's pinned mappings fails with EFAULT)
-        uint8_t* stage[2] = {nullptr, nullptr};  // device copies of the reference-layout block
         hipEvent_t buf_ev[2] = {nullptr, nullptr};
         bool used[2] = {false, false};
         uint32_t turn = 0;
     };
     std::string make_worker(Worker& w);
     void loop(uint32_t i);
-    bool run(Worker& w, FileTask* t);  // read, copy, convert, record; false on a short read
+    bool run(Worker& w, FileTask* t);  // read, copy, record; false on a short read
 
     std::vector<int> fds_;
-    uint32_t first_ = 0, H_ = 0, I_ = 0;
-    size_t ref_bytes_ = 0, native_bytes_ = 0;
+    uint32_t first_ = 0;
+    size_t ref_bytes_ = 0;
     int device_ = 0;
     std::vector<std::unique_ptr<FileTask>> tasks_;
     std::vector<FileTask*> free_;

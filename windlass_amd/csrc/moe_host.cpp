@@ -61,13 +61,23 @@ struct CacheState {
     bool spec_pending = false;
     uint32_t spec_layer = 0;
     uint64_t spec_requests = 0, spec_copies = 0, spec_hits = 0, bytes_h2d = 0;
-    std::vector<std::pair<uint32_t, uint8_t*>> resolved;  // last wl_cache_prefetch: key -> block
+    std::vector<std::pair<uint32_t, uint32_t>> resolved;  // last wl_cache_prefetch: key -> slot
+    std::vector<uint8_t*> blk;  // the block of each slot (a file-backed cache swaps them, below)
     // packed-file backing (wl_cache_create_files): the reads run on its
     // workers; task_of[slot] is the slot's read not yet waited for
     std::unique_ptr<wl::FileTier> files;
     std::vector<wl::FileTask*> task_of;
     hipEvent_t gates[4] = {nullptr, nullptr, nullptr, nullptr};  // per-resolve gates of file reads (a ring)
     uint32_t gate_i = 0;
+    // A file read lands in its slot as the file's record (reference layout):
+    // raw[slot] until wl_cache_get converts it on the caller's stream into
+    // `spare` and swaps the two blocks, so no kernel runs beside the caller's
+    // persistent kernels. spare_ev: the last conversion out of the block
+    // that is now the spare (the next conversion into it waits for it).
+    std::vector<uint8_t> raw;
+    uint8_t* spare = nullptr;
+    hipEvent_t spare_ev = nullptr;
+    bool spare_rec = false;
 };
 
 // Scratch of the batched layer: one allocation sized for `cap` tokens
@@ -391,6 +401,7 @@ void wl_destroy(wl_ctx* c) {
         if (C.gate) (void)hipEventDestroy(C.gate);
         for (hipEvent_t e : C.gates)
             if (e) (void)hipEventDestroy(e);
+        if (C.spare_ev) (void)hipEventDestroy(C.spare_ev);
         for (hipStream_t st : C.copy)
             if (st) (void)hipStreamDestroy(st);
         delete C.lru;
@@ -607,7 +618,7 @@ wl_status wl_slot_pool_ptr(wl_ctx* c, uint32_t slot, uint8_t** d_block) {
 // after the copy of their slot; speculative ones only start copies (their
 // victims are never among the last real batch's experts: capacity >= 2K).
 static wl_status cache_resolve(wl_ctx* c, uint32_t layer, const int32_t* ids, uint32_t n, hipStream_t s,
-                               bool speculative, uint8_t** ptrs) {
+                               bool speculative, uint32_t* slots) {
     CacheState& C = c->cache;
     const uint32_t E = c->cfg.n_routed_experts;
     const size_t nb = c->native_bytes;
@@ -630,12 +641,12 @@ static wl_status cache_resolve(wl_ctx* c, uint32_t layer, const int32_t* ids, ui
         for (uint32_t j = 0; j < k; j++)
             if (ids[j] == ids[k]) {
                 dup = true;
-                if (ptrs) ptrs[k] = ptrs[j];
+                if (slots) slots[k] = slots[j];
             }
         if (dup) continue;
         const uint32_t key = layer * E + (uint32_t)ids[k];
         const wl::SlotLru::Result r = C.lru->request(key, !speculative);
-        uint8_t* dst = C.pool + (size_t)r.slot * nb;
+        uint8_t* dst = C.blk[r.slot];
         if (r.transient) {
             if (speculative) continue;  // a prediction the policy would not retain: nothing to fetch early
             if (!C.transient) return fail(c, WL_ERR_STATE, "no transient slot for a miss that is not retained");
@@ -681,6 +692,7 @@ static wl_status cache_resolve(wl_ctx* c, uint32_t layer, const int32_t* ids, ui
                 return fail(c, WL_ERR_STATE, "file read queue full");
             }
             C.task_of[r.slot] = t;
+            C.raw[r.slot] = 1;
             C.has_ev[r.slot] = 1;
             C.spec[r.slot] = speculative ? 1 : 0;
             C.bytes_h2d += C.files->ref_bytes();
@@ -706,7 +718,7 @@ static wl_status cache_resolve(wl_ctx* c, uint32_t layer, const int32_t* ids, ui
         // (file reads: the stream waits in wl_cache_get, once the read is issued)
         if (!speculative && !C.files && C.has_ev[r.slot] && (e = hipStreamWaitEvent(s, C.slot_ev[r.slot], 0)) != hipSuccess)
             return hip_fail(c, e, "wait for expert copy");
-        if (ptrs) ptrs[k] = dst;
+        if (slots) slots[k] = r.slot;
     }
     return WL_OK;
 }
@@ -1368,6 +1380,9 @@ static wl_status cache_init(wl_ctx* c, uint32_t capacity) {
     C.has_ev.assign(nslots, 0);
     C.spec.assign(nslots, 0);
     C.task_of.assign(nslots, nullptr);
+    C.raw.assign(nslots, 0);
+    C.blk.resize(nslots);
+    for (uint32_t i = 0; i < nslots; i++) C.blk[i] = C.pool + (size_t)i * c->native_bytes;
     C.lru = new wl::SlotLru(capacity, WL_POLICY_LRU, 0.5f, 0u, C.transient);
     c->src = wl_expert_source{c, cache_src_get, cache_src_prefetch, cache_src_get_async, 1};
     c->src_cache = true;
@@ -1400,9 +1415,10 @@ wl_status wl_cache_create_files_ex(wl_ctx* c, uint32_t capacity, const char* dir
     if (io_threads > 64) return fail(c, WL_ERR_INVALID, "io_threads %u > 64", io_threads);
     if (c->cache.lru) return fail(c, WL_ERR_STATE, "the context already has a cache");
     std::unique_ptr<wl::FileTier> files(new wl::FileTier());
+    if (c->lay.total != c->native_bytes)
+        return fail(c, WL_ERR_INVALID, "a file record (%zu B) must fill a slot (%zu B)", c->lay.total, c->native_bytes);
     const std::string err = files->open(dir, first_layer, c->cfg.n_layers, c->cfg.n_routed_experts, c->lay.total,
-                                        c->native_bytes, c->cfg.hidden, c->cfg.moe_inter, io_threads, c->device,
-                                        (flags & WL_FILES_DIRECT) != 0u);
+                                        io_threads, c->device, (flags & WL_FILES_DIRECT) != 0u);
     if (!err.empty()) return fail(c, WL_ERR_IO, "%s", err.c_str());
     wl_status s = cache_init(c, capacity);
     if (s != WL_OK) return s;
@@ -1411,6 +1427,13 @@ wl_status wl_cache_create_files_ex(wl_ctx* c, uint32_t capacity, const char* dir
         const hipError_t e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
         if (e != hipSuccess) return hip_fail(c, e, "gate event");
     }
+    hipError_t e = hipEventCreateWithFlags(&C.spare_ev, hipEventDisableTiming);
+    if (e != hipSuccess) return hip_fail(c, e, "spare event");
+    if ((e = hipMalloc((void**)&C.spare, c->native_bytes)) != hipSuccess) {
+        C.spare = nullptr;
+        return fail(c, WL_ERR_OOM, "spare block: %s", hipGetErrorString(e));
+    }
+    c->allocs.push_back(C.spare);  // (swapped into the pool and back: freed with the pool's allocation list)
     C.files = std::move(files);
     return WL_OK;
 }
@@ -1454,11 +1477,11 @@ wl_status wl_cache_prefetch(wl_ctx* c, uint32_t layer, const int32_t* experts, u
     if (!C.lru) return fail(c, WL_ERR_STATE, "no cache (wl_cache_create)");
     if (layer >= c->cfg.n_layers || (n && !experts) || n > WL_MAX_TOPK || n > C.capacity / 2u)
         return fail(c, WL_ERR_INVALID, "bad prefetch request (layer %u, n %u)", layer, n);
-    uint8_t* ptrs[WL_MAX_TOPK];
-    wl_status s = cache_resolve(c, layer, experts, n, (hipStream_t)stream, false, ptrs);
+    uint32_t slots[WL_MAX_TOPK];
+    wl_status s = cache_resolve(c, layer, experts, n, (hipStream_t)stream, false, slots);
     if (s != WL_OK) return s;
     C.resolved.clear();
-    for (uint32_t k = 0; k < n; k++) C.resolved.push_back({layer * c->cfg.n_routed_experts + (uint32_t)experts[k], ptrs[k]});
+    for (uint32_t k = 0; k < n; k++) C.resolved.push_back({layer * c->cfg.n_routed_experts + (uint32_t)experts[k], slots[k]});
     return WL_OK;
 }
 
@@ -1469,28 +1492,49 @@ wl_status wl_cache_get(wl_ctx* c, uint32_t layer, uint32_t expert, void* stream,
     if (layer >= c->cfg.n_layers || expert >= c->cfg.n_routed_experts)
         return fail(c, WL_ERR_INVALID, "(%u,%u) out of range", layer, expert);
     const uint32_t key = layer * c->cfg.n_routed_experts + expert;
-    uint8_t* p = nullptr;
+    uint32_t slot = 0;
+    bool found = false;
     for (const auto& r : C.resolved)
-        if (r.first == key) p = r.second;  // the prefetch ordered the stream after a host copy
-    if (!p) {
+        if (r.first == key) {  // the prefetch ordered the stream after a host copy
+            slot = r.second;
+            found = true;
+        }
+    if (!found) {
         const int32_t id = (int32_t)expert;
-        wl_status s = cache_resolve(c, layer, &id, 1, (hipStream_t)stream, false, &p);
+        wl_status s = cache_resolve(c, layer, &id, 1, (hipStream_t)stream, false, &slot);
         if (s != WL_OK) return s;
     }
     if (C.files) {  // the slot's read: wait until its worker has issued it, then order the stream after it
-        const uint32_t slot = (uint32_t)((p - C.pool) / c->native_bytes);
+        hipStream_t st = (hipStream_t)stream;
         if (wl::FileTask* t = C.task_of[slot]) {
             const bool ok = C.files->wait_issued(t);
             const std::string why = t->why;
             C.files->release(t);
             C.task_of[slot] = nullptr;
-            if (!ok) return fail(c, WL_ERR_IO, "read of layer %u expert %u failed: %s", layer, expert, why.c_str());
+            if (!ok) {
+                C.raw[slot] = 0;
+                return fail(c, WL_ERR_IO, "read of layer %u expert %u failed: %s", layer, expert, why.c_str());
+            }
         }
         hipError_t e;
-        if (C.has_ev[slot] && (e = hipStreamWaitEvent((hipStream_t)stream, C.slot_ev[slot], 0)) != hipSuccess)
+        if (C.has_ev[slot] && (e = hipStreamWaitEvent(st, C.slot_ev[slot], 0)) != hipSuccess)
             return hip_fail(c, e, "wait for expert read");
+        if (C.raw[slot]) {
+            // the file's record -> the native layout, into the spare block, on
+            // the caller's stream (ordered with its other kernels); the two
+            // blocks then trade places
+            if (C.spare_rec && (e = hipStreamWaitEvent(st, C.spare_ev, 0)) != hipSuccess)
+                return hip_fail(c, e, "wait for the spare block");
+            if (wl::launch_expert_to_native(C.blk[slot], C.spare, c->cfg.hidden, c->cfg.moe_inter, 0, st) != 0)
+                return fail(c, WL_ERR_HIP, "expert conversion launch failed");
+            std::swap(C.blk[slot], C.spare);
+            if ((e = hipEventRecord(C.spare_ev, st)) != hipSuccess || (e = hipEventRecord(C.slot_ev[slot], st)) != hipSuccess)
+                return hip_fail(c, e, "conversion event");
+            C.spare_rec = true;
+            C.raw[slot] = 0;
+        }
     }
-    *d_block = p;
+    *d_block = C.blk[slot];
     return WL_OK;
 }
 
@@ -1561,6 +1605,7 @@ wl_status wl_cache_set_policy(wl_ctx* c, const wl_cache_policy* policy) {
     for (uint32_t k : C.pinned) C.lru->pin(k, true);
     C.policy = *policy;
     std::fill(C.spec.begin(), C.spec.end(), 0);
+    std::fill(C.raw.begin(), C.raw.end(), 0);  // the keys are gone; a slot is read again before it is handed out
     C.resolved.clear();
     C.spec_pending = false;
     C.spec_requests = C.spec_copies = C.spec_hits = C.bytes_h2d = C.bypassed = 0;
