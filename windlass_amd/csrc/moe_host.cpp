@@ -1415,8 +1415,8 @@ wl_status wl_cache_create_files_ex(wl_ctx* c, uint32_t capacity, const char* dir
     if (io_threads > 64) return fail(c, WL_ERR_INVALID, "io_threads %u > 64", io_threads);
     if (c->cache.lru) return fail(c, WL_ERR_STATE, "the context already has a cache");
     std::unique_ptr<wl::FileTier> files(new wl::FileTier());
-    if (c->lay.total != c->native_bytes)
-        return fail(c, WL_ERR_INVALID, "a file record (%zu B) must fill a slot (%zu B)", c->lay.total, c->native_bytes);
+    if (c->lay.total > c->native_bytes)  // a record lands in its slot before it is converted
+        return fail(c, WL_ERR_INVALID, "a file record (%zu B) exceeds a slot (%zu B)", c->lay.total, c->native_bytes);
     const std::string err = files->open(dir, first_layer, c->cfg.n_layers, c->cfg.n_routed_experts, c->lay.total,
                                         io_threads, c->device, (flags & WL_FILES_DIRECT) != 0u);
     if (!err.empty()) return fail(c, WL_ERR_IO, "%s", err.c_str());
