@@ -550,7 +550,7 @@ def bench_expert(args):
         "achieved_GBps": round(achieved, 1), "pct_of_hbm_peak": round(100 * achieved / PEAK_HBM_GBPS, 2),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
                      "frac": round(achieved / PEAK_HBM_GBPS, 4), "traffic": None, "algorithmic_bytes": nbytes,
-                     "kernel": "ffn_gu_kernel + ffn_down_kernel (two launches)"},
+                     "kernel": "ffn1_kernel (one persistent launch)"},
         "cpu_baseline": cpu,
     }
     ctx.close()

@@ -298,6 +298,19 @@ int launch_slot_fill(const uint8_t** table, uint32_t E, const int32_t* ids, cons
                      void* stream);
 int launch_dequant_matvec(const uint8_t* W, const uint8_t* S, const float* x, float* y, uint32_t N,
                           uint32_t K, void* stream);
+// The one-launch expert FFN (moe_decode.hip): its arguments.
+struct FfnArgs {
+    const uint8_t* blk;  // reference-layout block
+    uint64_t gw_off, gs_off, uw_off, us_off, dw_off, ds_off;
+    const float* x;      // [H]
+    float* y;            // [H]
+    uint16_t* y_bf16;    // [H] or null
+    uint64_t* tag;       // [I] epoch-tagged SwiGLU values (context scratch, zeroed at creation)
+    uint32_t* sync;      // synchronisation block (error and abort words)
+    uint32_t H, I, epoch;
+};
+// Returns -1 (nothing launched) for a shape or grid it is not built for.
+int launch_expert_ffn1(const FfnArgs& a, uint32_t grid, void* stream);
 int launch_expert_ffn(const uint8_t* blk, uint64_t gw_off, uint64_t gs_off, uint64_t uw_off,
                       uint64_t us_off, uint64_t dw_off, uint64_t ds_off, const float* x, uint32_t H,
                       uint32_t I, float* mid, uint16_t* mid_p, float* y, uint16_t* y_bf16,

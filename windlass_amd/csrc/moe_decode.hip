@@ -54,6 +54,7 @@
 // unconditionally (indices past the end are clamped to a valid address and
 // their contribution masked), so the compiler's wait counts stay exact.
 #include <hip/hip_runtime.h>
+#include <algorithm>
 #include "dev_common.h"
 #include "internal.h"
 
@@ -1021,6 +1022,192 @@ int launch_expert_ffn(const uint8_t* blk, uint64_t gw_off, uint64_t gs_off, uint
     if (e != hipSuccess) return (int)e;
     hipLaunchKernelGGL(ffn_down_kernel, dim3(H / (16 * kDownRT)), dim3(kThreads), 0, (hipStream_t)stream, blk,
                        dw_off, ds_off, mid_p, H, I, y, y_bf16);
+    return (int)hipGetLastError();
+}
+
+// ---- one expert FFN in one launch (config 0, wl_expert_ffn) --------------------
+// A persistent launch of G work-groups (one per CU) over one reference-layout
+// block: work-group w takes inter rows [RPW w, RPW w + RPW) of gate and up
+// (wave v: rows RPW w + v + 8 j) and output rows [DPW w, DPW w + DPW) of down
+// (wave v: rows DPW w + v + 8 j), and issues every weight load of both phases
+// before it computes anything, so the whole block streams at once. Gate/up:
+// lane l holds blocks l + 64 b of its row (16 bytes of nibbles, one E8M0
+// byte), widened to f32 exactly (v_cvt_scalef32_pk_f32_fp4) and dotted with
+// x in f32; a wave sum gives the row; SwiGLU; the value is published as an
+// epoch-tagged word (epoch << 32 | f32 bits, agent scope). Down: every
+// work-group reads the I tagged values (re-reading stale ones, bounded), then
+// lane l dots block l of each of its rows with them. No partial sums: each
+// output row is one work-group's. Reference: the per-expert sequence of
+// run_moe, 3 x dequant_matvec_mxfp4 + silu_mul (src/glm_layer_runner.cuh:
+// 424-427; src/glm_kernels.cuh:63-110).
+typedef __attribute__((ext_vector_type(2))) float f32x2;
+// acc + the 8 values of one dword (two per byte, low nibble first) times x[0..8)
+WL_DEV float fp4x8_dot(uint32_t d, float sc, const float* x, float acc) {
+    const f32x2 v0 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(d, sc, 0);
+    const f32x2 v1 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(d, sc, 1);
+    const f32x2 v2 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(d, sc, 2);
+    const f32x2 v3 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(d, sc, 3);
+    const float4 xa = *(const float4*)x, xb = *(const float4*)(x + 4);
+    acc = fmaf(v0.x, xa.x, acc);
+    acc = fmaf(v0.y, xa.y, acc);
+    acc = fmaf(v1.x, xa.z, acc);
+    acc = fmaf(v1.y, xa.w, acc);
+    acc = fmaf(v2.x, xb.x, acc);
+    acc = fmaf(v2.y, xb.y, acc);
+    acc = fmaf(v3.x, xb.z, acc);
+    return fmaf(v3.y, xb.w, acc);
+}
+// One 32-value block: 16 bytes of nibbles at scale sc against x[0..32).
+WL_DEV float fp4_dot32(u32x4 w, float sc, const float* x) {
+    float acc = fp4x8_dot(w.x, sc, x, 0.f);
+    acc = fp4x8_dot(w.y, sc, x + 8, acc);
+    acc = fp4x8_dot(w.z, sc, x + 16, acc);
+    return fp4x8_dot(w.w, sc, x + 24, acc);
+}
+WL_DEV float wave_sum(float v) {
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+template <int NBL, int GJ, int NBD, int DJ>
+__global__ void __launch_bounds__(kThreads) ffn1_kernel(FfnArgs a) {
+    const uint32_t H = a.H, I = a.I, w = blockIdx.x, tid = threadIdx.x;
+    const uint32_t v = uni(tid >> 6), lane = tid & 63;
+    constexpr uint32_t RPW = 8u * GJ, DPW = 8u * DJ;
+    extern __shared__ __align__(16) uint8_t lds[];
+    float* xs = (float*)lds;    // [H]
+    float* ms = xs + H;         // [I] the SwiGLU values
+    uint32_t* flag = (uint32_t*)(ms + I);
+    const SyncMap SM = SyncMap::make();
+    WL_TL(12);
+    // x first (it returns first: a wave's loads complete in order), then
+    // every weight load of the work-group
+    constexpr int XV = (int)(NBL * 64 * 32 / 4 / kThreads);  // float4 of x per thread (H = NBL * 2048)
+    float4 xv[XV];
+    const rsrc_t x_rs = make_rsrc(a.x, H * 4u);
+#pragma unroll
+    for (int i = 0; i < XV; i++) xv[i] = __builtin_bit_cast(float4, bld16(x_rs, 16u * (tid + kThreads * i), 0u));
+    const rsrc_t gw_rs = make_rsrc(a.blk + a.gw_off, I * H / 2u), gs_rs = make_rsrc(a.blk + a.gs_off, I * H / 32u);
+    const rsrc_t uw_rs = make_rsrc(a.blk + a.uw_off, I * H / 2u), us_rs = make_rsrc(a.blk + a.us_off, I * H / 32u);
+    const rsrc_t dw_rs = make_rsrc(a.blk + a.dw_off, H * I / 2u), ds_rs = make_rsrc(a.blk + a.ds_off, H * I / 32u);
+    u32x4 gw[GJ][NBL], uw[GJ][NBL], dw[DJ][NBD];
+    uint32_t gs[GJ][NBL], us[GJ][NBL], dsc[DJ][NBD];
+#pragma unroll
+    for (int j = 0; j < GJ; j++) {
+        const uint32_t r = RPW * w + v + 8u * j;
+#pragma unroll
+        for (int b = 0; b < NBL; b++) {
+            const uint32_t blk = lane + 64u * b;
+            gw[j][b] = bld16_nt(gw_rs, r * (H / 2u) + 16u * blk, 0u);
+            uw[j][b] = bld16_nt(uw_rs, r * (H / 2u) + 16u * blk, 0u);
+            gs[j][b] = bld1(gs_rs, r * (H / 32u) + blk, 0u);
+            us[j][b] = bld1(us_rs, r * (H / 32u) + blk, 0u);
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < DJ; j++) {
+        const uint32_t r = DPW * w + v + 8u * j;
+#pragma unroll
+        for (int b = 0; b < NBD; b++) {
+            const uint32_t blk = lane + 64u * b;
+            dw[j][b] = bld16_nt(dw_rs, r * (I / 2u) + 16u * blk, 0u);
+            dsc[j][b] = bld1(ds_rs, r * (I / 32u) + blk, 0u);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < XV; i++) *(float4*)(xs + 4u * (tid + kThreads * i)) = xv[i];
+    lds_barrier();
+    WL_TL(13);
+    // gate / up rows, SwiGLU, published
+#pragma unroll
+    for (int j = 0; j < GJ; j++) {
+        float g = 0.f, u = 0.f;
+#pragma unroll
+        for (int b = 0; b < NBL; b++) {
+            const float* xb = xs + 32u * (lane + 64u * b);
+            g += fp4_dot32(gw[j][b], e8m0f(gs[j][b]), xb);
+            u += fp4_dot32(uw[j][b], e8m0f(us[j][b]), xb);
+        }
+        g = wave_sum(g);
+        u = wave_sum(u);
+        if (lane == 0) {
+            const uint32_t r = RPW * w + v + 8u * j;
+            __hip_atomic_store((__attribute__((address_space(1))) uint64_t*)(a.tag + r),
+                               ((uint64_t)a.epoch << 32) | __float_as_uint(silu_mul(g, u)), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+    WL_TL(14);
+    // every SwiGLU value of this call, into LDS: each thread's 16-byte chunks
+    // (two tagged words each) all in flight together, then the stale ones
+    // again until this call's epoch shows (bounded)
+    constexpr int MC = (int)(NBD * 64 * 32 / 2 / kThreads);  // chunks per thread (I = NBD * 2048)
+    // (one round in flight at a time: measured, several rounds in flight
+    // from every work-group hot-spot the channels holding the 16 KB array and
+    // were slower, 16.9 against 13.3 us per expert)
+    const rsrc_t tg_rs = make_rsrc(a.tag, I * 8u);
+    u32x4 mc[MC];
+#pragma unroll
+    for (int i = 0; i < MC; i++) mc[i] = bld16_ag(tg_rs, 16u * (tid + kThreads * i), 0u);
+    uint32_t stale = 0;
+    for (uint32_t spins = 0;; spins++) {
+#pragma unroll
+        for (int i = 0; i < MC; i++) {
+            if (spins != 0 && !((stale >> i) & 1u)) continue;
+            if (mc[i].y == a.epoch && mc[i].w == a.epoch) {
+                const uint32_t c = tid + kThreads * i;
+                ms[2u * c] = __uint_as_float(mc[i].x);
+                ms[2u * c + 1u] = __uint_as_float(mc[i].z);
+                stale &= ~(1u << i);
+            } else {
+                stale |= 1u << i;
+            }
+        }
+        if (block_all(stale == 0u, flag)) break;
+        if (spins > (1u << 20) || aborted(a.sync, SM, a.epoch)) {
+            if (tid == 0 && spins > (1u << 20)) raise_error(a.sync, SM, E_SPIN, a.epoch);
+            return;
+        }
+        __builtin_amdgcn_s_sleep(2);
+#pragma unroll
+        for (int i = 0; i < MC; i++)
+            if ((stale >> i) & 1u) mc[i] = bld16_ag(tg_rs, 16u * (tid + kThreads * i), 0u);
+    }
+    WL_TL(15);
+    // down rows
+#pragma unroll
+    for (int j = 0; j < DJ; j++) {
+        float y = 0.f;
+#pragma unroll
+        for (int b = 0; b < NBD; b++) y += fp4_dot32(dw[j][b], e8m0f(dsc[j][b]), ms + 32u * (lane + 64u * b));
+        y = wave_sum(y);
+        if (lane == 0) {
+            const uint32_t r = DPW * w + v + 8u * j;
+            a.y[r] = y;
+            if (a.y_bf16) a.y_bf16[r] = (uint16_t)f2bf(y);
+        }
+    }
+}
+
+// The one-launch expert FFN for the shapes it is instantiated for (GLM: H
+// 6144, I 2048 on 256 work-groups); -1 for any other (the caller then runs
+// launch_expert_ffn).
+int launch_expert_ffn1(const FfnArgs& a, uint32_t grid, void* stream) {
+    // more than half of a CU's 160 KB: one work-group per CU (the launch has
+    // one per CU, and they wait for each other: two on one CU would share its
+    // bandwidth while another CU idles)
+    const size_t lds = std::max<size_t>(4u * ((size_t)a.H + a.I) + 64u, 84u * 1024u);
+    if (!(a.H == 6144 && a.I == 2048 && grid == 256)) return -1;
+    // every work-group must be resident at once (they wait for each other's
+    // SwiGLU values): checked once per process (one launch shape)
+    static const int per_cu = [&] {
+        int n = 0;
+        const void* fn = (const void*)ffn1_kernel<3, 1, 1, 3>;
+        if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess) return 0;
+        return hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, kThreads, lds) == hipSuccess ? n : 0;
+    }();
+    if (per_cu < 1) return -1;
+    hipLaunchKernelGGL((ffn1_kernel<3, 1, 1, 3>), dim3(grid), dim3(kThreads), lds, (hipStream_t)stream, a);
     return (int)hipGetLastError();
 }
 

@@ -115,6 +115,7 @@ struct wl_ctx {
     float* topw = nullptr;
     float* shared_out = nullptr;
     uint16_t* ffn_mid_p = nullptr;  // wl_expert_ffn's SwiGLU pieces
+    uint64_t* ffn_tag = nullptr;    // wl_expert_ffn's epoch-tagged SwiGLU values [I] (agent-scope exchange)
     int32_t taps = 1;
     // cross-work-group arrays (agent-scope stores and loads)
     uint64_t* lslot = nullptr;
@@ -350,6 +351,7 @@ wl_status wl_create(const wl_moe_config* cfg, wl_ctx** out) {
         (s = dalloc(c, &c->topw, 4 * (size_t)WL_MAX_TOPK)) != WL_OK ||
         (s = dalloc(c, &c->shared_out, 4 * (size_t)H)) != WL_OK ||
         (s = dalloc(c, &c->ffn_mid_p, 2 * 3 * (size_t)I)) != WL_OK ||
+        (s = dalloc(c, &c->ffn_tag, 8 * (size_t)I)) != WL_OK ||
         (s = dalloc(c, &c->logits, 4 * (size_t)E)) != WL_OK ||
         (s = dalloc(c, &c->lslot, 8 * (size_t)E)) != WL_OK ||
         (s = dalloc(c, &c->part, 4 * (size_t)H * grid)) != WL_OK ||
@@ -378,6 +380,7 @@ wl_status wl_create(const wl_moe_config* cfg, wl_ctx** out) {
     // epoch 0 is never a call's: zeroed tagged arrays hold no valid word (a
     // reused allocation could otherwise carry another context's tags)
     if (e == hipSuccess) e = hipMemset(c->lslot, 0, 8 * (size_t)E);
+    if (e == hipSuccess) e = hipMemset(c->ffn_tag, 0, 8 * (size_t)I);
     // tag 0 is never a call's either
     if (e == hipSuccess) e = hipMemset(c->part, 0, 4 * (size_t)H * grid);
     if (e == hipSuccess) e = hipMemset(c->tsh, 0, 4 * (size_t)H * grid);
@@ -1678,9 +1681,15 @@ wl_status wl_expert_ffn(wl_ctx* c, const uint8_t* d_block, const float* d_x, flo
                         void* stream) {
     if (!c) return WL_ERR_INVALID;
     if (!d_block || !d_x || !d_y) return fail(c, WL_ERR_INVALID, "null block/x/y");
-    int e = wl::launch_expert_ffn(d_block, c->lay.gw_off, c->lay.gs_off, c->lay.uw_off, c->lay.us_off,
-                                  c->lay.dw_off, c->lay.ds_off, d_x, c->cfg.hidden, c->cfg.moe_inter,
-                                  c->rmid, c->ffn_mid_p, d_y, d_y_bf16, stream);
+    if (++c->epoch >= 0x7FFFFFFFu) c->epoch = 1;
+    const wl::FfnArgs a{d_block,  c->lay.gw_off, c->lay.gs_off, c->lay.uw_off, c->lay.us_off, c->lay.dw_off,
+                        c->lay.ds_off, d_x,      d_y,           d_y_bf16,      c->ffn_tag,    c->sync,
+                        c->cfg.hidden, c->cfg.moe_inter, c->epoch};
+    int e = wl::launch_expert_ffn1(a, c->grid, stream);
+    if (e < 0)  // a shape the one-launch kernel is not built for: gate/up, then down
+        e = wl::launch_expert_ffn(d_block, c->lay.gw_off, c->lay.gs_off, c->lay.uw_off, c->lay.us_off,
+                                  c->lay.dw_off, c->lay.ds_off, d_x, c->cfg.hidden, c->cfg.moe_inter, c->rmid,
+                                  c->ffn_mid_p, d_y, d_y_bf16, stream);
     if (e != 0) return hip_fail(c, (hipError_t)e, "expert ffn launch");
     return WL_OK;
 }
