@@ -543,7 +543,8 @@ def bench_expert(args):
     line = {
         "metric": "us_per_mxfp4_expert_ffn", "value": round(us, 3), "unit": "us/expert", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(us / 1e3, 6), "higher_is_better": False,
-        "scaling": "weak", "vs_baseline": None, "dtype": "mxfp4 weights, f32 activations and accumulation",
+        "scaling": "weak", "vs_baseline": None,
+        "dtype": "mxfp4 weights widened exactly to f32, f32 activations and accumulation",
         "data": "synthetic",
         "config": {"workload": "config0: one MXFP4 expert SwiGLU FFN, bs=1 (wl_expert_ffn)", "hidden": H,
                    "moe_inter": I, "rotating_blocks": nblk, "seeds": seeds, "global_batch": 1},
@@ -607,7 +608,8 @@ def bench_shim(args):
         "metric": "us_per_moe_decode_layer", "value": round(us, 3), "unit": "us/layer", "n_gpus": 1,
         "steps": args.steps, "warmup": 2, "ms_per_step": round(res["resident"]["wall_us_per_step"] / 1e3, 6),
         "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
-        "dtype": "mxfp4/bf16 weights, f32 activations and accumulation", "data": "synthetic",
+        "dtype": "mxfp4/bf16 weights, f32 activations and accumulation; the decode kernel's cross-work-group partial "
+                 "sums are exchanged as f32 rounded to 21 stored mantissa bits", "data": "synthetic",
         "config": {"workload": f"shim: the reference's run_layer/run_chain call sites through include/windlass_glm.hpp, "
                                f"1 dense + {args.shim_layers} MoE GLM layers per decode step, MXFP4 shared expert",
                    "hidden": H, "moe_inter": I, "n_routed_experts": E, "n_experts_per_tok": K, "dense_inter": DI,
@@ -883,7 +885,11 @@ def main():
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "mxfp4/bf16 weights, f32 activations and accumulation",
+        "dtype": ("mxfp4/bf16 weights, f32 activations and accumulation (bf16 MFMA on three exact bf16 pieces "
+                  "of each f32 activation); the cross-work-group partial sums are exchanged as f32 rounded to "
+                  "21 stored mantissa bits" if not batched else
+                  "mxfp4/bf16 weights, f32 activations and accumulation (bf16 MFMA on three exact bf16 pieces "
+                  "of each f32 activation)"),
         "data": "synthetic",
         "config": {"workload": (f"config3: one GLM MoE layer over {args.tokens} tokens (batched)" if batched else
                                 f"config4: {args.layers} GLM MoE layers behind a {args.cache_slots}-slot HBM expert "
