@@ -35,10 +35,13 @@ timed beside it.
 --workload files measures the file tier and the loader (rows f1, f4) at the
 GLM shape: --file-layers packed layer_N.bin files written from the
 synthetic generator to local disk, read through a --file-slots HBM cache by
-4 pread workers, once through the page cache and once with O_DIRECT; then a
-one-layer safetensors checkpoint loaded into the slot table (wl_load_layer +
+4 pread workers: through the page cache with speculation off and on, and
+with O_DIRECT; the same tokens then run through config 4's pinned-host cache
+at the same layers and capacity, speculation off and on. Then a one-layer
+safetensors checkpoint is loaded into the slot table (wl_load_layer +
 wl_load_experts) and packed back into a layer file (wl_st_pack_layer). The
-line reports GB/s of each path; the files are removed at the end.
+line reports hit rate, µs per layer and GB/s copied of each pass; the files
+are removed at the end.
 
 --workload cache measures configs[4]: 75 MoE layers whose 19,200 experts sit
 behind the HBM expert cache (3,094 slots, 62 GB) and are copied from pinned
@@ -342,7 +345,7 @@ def bench_files(args):
     import tempfile
 
     from windlass_amd import checkpoint, hip, moe, synthdata
-    from windlass_amd.model import FileModel
+    from windlass_amd.model import CachedModel, FileModel
     c = dict(GLM)
     H, I, E = c["hidden"], c["moe_inter"], c["n_routed_experts"]
     L = args.file_layers
@@ -370,10 +373,24 @@ def bench_files(args):
         d_hs = hip.DeviceBuffer.from_array(np.stack([synthdata.hidden_state(H, 5000 + i) for i in range(n_h)]))
         d_h, d_tmp = hip.DeviceBuffer(4 * H), hip.DeviceBuffer(4 * H)
         stream = hip.Stream()
-        for direct, steps, warm in ((False, 16, 4), (True, 4, 2)):
-            fm = FileModel(c, args.seed, L, capacity=args.file_slots, directory=work, io_threads=4,
-                           shared_alias=True, bias_offset=zipf, direct=direct)
+        # the same tokens through every pass, so the routed keys (and the
+        # LRU's hits and misses without speculation) are the same in each;
+        # "pinned_host" is config 4's path (native blocks in pinned host
+        # memory, aliased over 512 blocks) at the same layers and capacity
+        passes = (("page_cache", "files", False, False, 16, 4), ("page_cache_spec", "files", False, True, 16, 4),
+                  ("direct", "files", True, False, 4, 2), ("pinned_host", "host", False, False, 16, 4),
+                  ("pinned_host_spec", "host", False, True, 16, 4))
+        for name, kind, direct, spec, steps, warm in passes:
+            print(f"bench files: {name}, {L} layers, {args.file_slots} slots, {steps} tokens", file=sys.stderr,
+                  flush=True)
+            if kind == "files":
+                fm = FileModel(c, args.seed, L, capacity=args.file_slots, directory=work, io_threads=4,
+                               shared_alias=True, bias_offset=zipf, direct=direct)
+            else:
+                fm = CachedModel(c, args.seed, L, capacity=args.file_slots, n_host=min(L * E, 512),
+                                 shared_alias=True, bias_offset=zipf)
             fm.ctx.set_taps(False)
+            fm.ctx.cache_set_speculation(spec)
 
             def token(i):
                 hip.copy_d2d(d_h.ptr, d_hs.ptr + 4 * H * (i % n_h), 4 * H, stream.handle)
@@ -392,10 +409,14 @@ def bench_files(args):
             ms = e0.elapsed_ms(e1)
             fm.ctx.check_error(stream.handle)
             st = fm.ctx.cache_stats()
-            out["direct" if direct else "page_cache"] = {
+            req = st["hits"] + st["misses"]
+            copied = st["bytes_h2d"]
+            out[name] = {
                 "us_per_layer": round(ms * 1e3 / steps / L, 1), "tokens": steps,
-                "hit_rate": round(st["hits"] / max(1, st["hits"] + st["misses"]), 4), "misses": st["misses"],
-                "file_GBps": round(st["misses"] * blk / (ms * 1e-3) / 1e9, 2)}
+                "tokens_per_s": round(steps / (ms * 1e-3), 2),
+                "hit_rate": round(st["hits"] / max(1, req), 4), "misses": st["misses"],
+                "spec_copies": st["spec_copies"], "spec_hits": st["spec_hits"],
+                "GBps_copied": round(copied / (ms * 1e-3) / 1e9, 2)}
             fm.close()
         # loader: a one-layer checkpoint (dense fields + 256 experts) -> slot table, and -> packed file
         d = synthdata.dense_layer(H, E, I, args.seed, 0)
@@ -451,7 +472,7 @@ def bench_files(args):
         st.close()
     finally:
         shutil.rmtree(work, ignore_errors=True)
-    line = {"metric": "file_tier_GBps", "value": out["page_cache"]["file_GBps"], "unit": "GB/s", "n_gpus": 1,
+    line = {"metric": "file_tier_GBps", "value": out["page_cache"]["GBps_copied"], "unit": "GB/s", "n_gpus": 1,
             "higher_is_better": True, "data": "synthetic", "dtype": "mxfp4 expert records",
             "config": {"workload": f"file tier: {L} GLM layer files ({L * E} records of {blk} B), "
                                    f"{args.file_slots}-slot HBM cache, 4 pread workers, bs=1 tokens",
@@ -567,6 +588,7 @@ def bench_shim(args):
     every expert fetched through the caller's ExpertSource (reference-layout
     blocks, converted per call). Runs as a child process; this process does
     not touch the GPU."""
+    import contextlib
     import subprocess
     import tempfile
 
@@ -579,7 +601,10 @@ def bench_shim(args):
     H, I, E, K = c["hidden"], c["moe_inter"], c["n_routed_experts"], c["n_experts_per_tok"]
     DI, NL, T, seed = 12288, 1 + args.shim_layers, 16, args.seed
     res = {}
-    with tempfile.TemporaryDirectory() as d:
+    keep = args.shim_dir
+    if keep:
+        os.makedirs(keep, exist_ok=True)
+    with (contextlib.nullcontext(keep) if keep else tempfile.TemporaryDirectory()) as d:
         with open(os.path.join(d, "cfg.txt"), "w") as f:
             f.write(f"{NL} 1 {H} {I} {E} {K} 1 {DI} {T} {seed} {c['rms_eps']} {c['routed_scaling']}\n")
         w = synthdata.dense_mlp(H, DI, seed, 0)
@@ -666,6 +691,9 @@ def main():
     ap.add_argument("--context", type=int, default=4096,
                     help="attention workload: cached positions before the timed tokens")
     ap.add_argument("--shim-layers", type=int, default=4, help="shim workload: MoE layers after the dense one")
+    ap.add_argument("--shim-dir", default=None,
+                    help="shim workload: write the caller's inputs here and keep them (default: a temp dir), so that "
+                         "tests/shim/_build/reference_caller DIR resident|source STEPS can be profiled on its own")
     ap.add_argument("--seed", type=int, default=1)
     ap.add_argument("--shared", choices=["bf16", "mxfp4"], default="bf16",
                     help="layer/chain workloads: the shared expert's format (bf16, the benchmark configuration; "

@@ -311,10 +311,12 @@ def test_not_resident_is_an_error_then_recovers(gpu):
     dm.ctx.close()
 
 
-@pytest.mark.parametrize("shape", [(256, 128), (384, 256), (6144, 2048)])
+@pytest.mark.parametrize("shape", [(256, 128), (384, 256), (6144, 2048), (2176, 2176)])
 def test_native_layout(gpu, shape):
     """wl_synth_expert_native == wl_expert_to_native(wl_synth_expert block) ==
-    the numpy restatement of the native layout (oracle/native_layout.py)."""
+    the numpy restatement of the native layout (oracle/native_layout.py).
+    (2176, 2176): 17 k tiles (a last group of one), 68 down row pairs (a last
+    scale group of four) and 34 slices (a second slice group of two)."""
     from oracle import native_layout
     hip = gpu
     H, I = shape

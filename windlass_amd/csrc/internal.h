@@ -329,6 +329,10 @@ size_t noalloc_scratch_bytes();
 // Reference-layout block -> native block (src null: synthesise the native
 // block directly from the counter-based generator with `key`).
 int launch_expert_to_native(const uint8_t* src, uint8_t* dst, uint32_t H, uint32_t I, uint32_t key, void* stream);
+// n reference-layout packed blocks src[i] -> native blocks dst[i], up to 16
+// per launch.
+int launch_experts_to_native(const uint8_t* const* src, uint8_t* const* dst, uint32_t n, uint32_t H, uint32_t I,
+                             void* stream);
 int launch_shared_to_native(const uint16_t* src, uint16_t* dst, uint32_t H, uint32_t SI, void* stream);
 // The six reference tensors of an MXFP4 shared expert (gate_w, gate_s, up_w,
 // up_s, down_w, down_s) -> NativeShared4.

@@ -766,6 +766,7 @@ static wl_status ensure_stage(wl_ctx* c, uint32_t n) {
 static wl_status source_fetch(wl_ctx* c, uint32_t layer, const int32_t* ids, uint32_t n, hipStream_t s,
                               const uint8_t** ptrs) {
     const wl_expert_source& S = c->src;
+    if (!S.native && n > c->stage_n) return fail(c, WL_ERR_STATE, "%u staging blocks for %u experts", c->stage_n, n);
     for (uint32_t k = 0; k < n; k++) {
         c->src_status = WL_OK;
         const uint8_t* p = S.get_async ? S.get_async(S.user, layer, (uint32_t)ids[k], (void*)s)
@@ -774,14 +775,18 @@ static wl_status source_fetch(wl_ctx* c, uint32_t layer, const int32_t* ids, uin
             if (c->src_status != WL_OK) return c->src_status;
             return fail(c, WL_ERR_IO, "expert source returned no block for layer %u expert %d", layer, ids[k]);
         }
-        if (!S.native) {
-            if (k >= c->stage_n) return fail(c, WL_ERR_STATE, "%u staging blocks for %u experts", c->stage_n, n);
-            uint8_t* dst = c->stage + (size_t)k * c->native_bytes;
-            if (wl::launch_expert_to_native(p, dst, c->cfg.hidden, c->cfg.moe_inter, 0, s) != 0)
-                return fail(c, WL_ERR_HIP, "expert conversion launch failed");
-            p = dst;
-        }
         ptrs[k] = p;
+    }
+    if (S.native) return WL_OK;
+    // every block of the call is valid until the call's work has run (the
+    // source contract), so all n convert in one launch (16 per launch)
+    uint8_t* dst[64];
+    for (uint32_t k0 = 0; k0 < n; k0 += 64) {
+        const uint32_t m = std::min(64u, n - k0);
+        for (uint32_t k = 0; k < m; k++) dst[k] = c->stage + (size_t)(k0 + k) * c->native_bytes;
+        if (wl::launch_experts_to_native(ptrs + k0, dst, m, c->cfg.hidden, c->cfg.moe_inter, s) != 0)
+            return fail(c, WL_ERR_HIP, "expert conversion launch failed");
+        for (uint32_t k = 0; k < m; k++) ptrs[k0 + k] = dst[k];
     }
     return WL_OK;
 }
@@ -1329,20 +1334,28 @@ wl_status wl_make_resident(wl_ctx* c, uint32_t layer, void* stream) {
     uint8_t* blocks = (uint8_t*)mem;
     const wl_expert_source& S = c->src;
     hipStream_t s = (hipStream_t)stream;
-    for (uint32_t x = 0; x < E; x++) {
-        c->src_status = WL_OK;
-        const uint8_t* p = S.get_async ? S.get_async(S.user, layer, x, (void*)s) : S.get(S.user, layer, x);
-        if (!p) {
-            if (c->src_status != WL_OK) return c->src_status;
-            return fail(c, WL_ERR_IO, "expert source returned no block for layer %u expert %u", layer, x);
-        }
-        uint8_t* dst = blocks + (size_t)x * nb;
-        if (S.native) {
-            if ((e = hipMemcpyAsync(dst, p, nb, hipMemcpyDeviceToDevice, s)) != hipSuccess)
+    // K experts at a time: a source holds the blocks of one call (K) valid
+    // until that call's work has run, as run_moe needs
+    const uint32_t K = c->cfg.n_experts_per_tok;
+    std::vector<const uint8_t*> src(K);
+    std::vector<uint8_t*> dst(K);
+    for (uint32_t x0 = 0; x0 < E; x0 += K) {
+        const uint32_t m = std::min(K, E - x0);
+        for (uint32_t i = 0; i < m; i++) {
+            const uint32_t x = x0 + i;
+            c->src_status = WL_OK;
+            const uint8_t* p = S.get_async ? S.get_async(S.user, layer, x, (void*)s) : S.get(S.user, layer, x);
+            if (!p) {
+                if (c->src_status != WL_OK) return c->src_status;
+                return fail(c, WL_ERR_IO, "expert source returned no block for layer %u expert %u", layer, x);
+            }
+            src[i] = p;
+            dst[i] = blocks + (size_t)x * nb;
+            if (S.native && (e = hipMemcpyAsync(dst[i], p, nb, hipMemcpyDeviceToDevice, s)) != hipSuccess)
                 return hip_fail(c, e, "resident block copy");
-        } else if (wl::launch_expert_to_native(p, dst, c->cfg.hidden, c->cfg.moe_inter, 0, s) != 0) {
-            return fail(c, WL_ERR_HIP, "expert conversion launch failed");
         }
+        if (!S.native && wl::launch_experts_to_native(src.data(), dst.data(), m, c->cfg.hidden, c->cfg.moe_inter, s) != 0)
+            return fail(c, WL_ERR_HIP, "expert conversion launch failed");
     }
     if ((e = hipStreamSynchronize(s)) != hipSuccess) return hip_fail(c, e, "resident fill");
     const size_t row = (size_t)layer * E;
