@@ -14,6 +14,13 @@ tools/repack_experts_glm.py:46-55); it reorders the same bytes so that every
        32q + n + 16(g >> 1), bytes [32j + 16(g & 1), +16)
   dns  [I/64][ceil(H/512)] 1 KB: lane byte i = scale of that row, pair
        16c + i, block 2j + (g & 1)
+  bgus [ceil(I/256) groups sg][8 waves v][ceil(H/256) steps s] 512 B: lane
+       byte 2i + q = scale of the lane's gu row in tile 8(4sg + i) + v, k tile
+       2s + q, block 4kt + g (the batched kernels' gate/up scales)
+  bdns [ceil(H/512) row blocks rb][8 v][ceil(I/256) steps st] 512 B: lane byte
+       2i + h = scale of down row 32q + n + 16(g >> 1), q = 16rb + 2v + h,
+       slice 4st + i, block 2j + (g & 1) (the batched kernels' down scales)
+(scales past the end of a dimension are 0).
 """
 import numpy as np
 
@@ -23,7 +30,9 @@ def native_sizes(H, I):
     gus = (I // 8) * ((H // 128 + 15) // 16) * 1024
     dn = (I // 64) * (H // 32) * 1024
     dns = (I // 64) * ((H // 32 + 15) // 16) * 1024
-    return gu, gus, dn, dns
+    bgus = -(-I // 256) * 8 * -(-H // 256) * 512
+    bdns = -(-H // 512) * 8 * -(-I // 256) * 512
+    return gu, gus, dn, dns, bgus, bdns
 
 
 def to_native(parts, H, I):
@@ -67,5 +76,30 @@ def to_native(parts, H, I):
     row = 32 * np.minimum(qv, nq - 1) + n[None, None, :, None] + 16 * (g[None, None, :, None] >> 1)
     col = 2 * j + (g[None, None, :, None] & 1)
     s = np.where(qv < nq, ds[row, col], 0).astype(np.uint8)
+    out.append(s.reshape(-1))
+    # bgus: [sg][v][s][lane][8]
+    S, nstu = I // 64, -(-H // 256)
+    sg = np.arange(-(-I // 256))[:, None, None, None, None]
+    v = np.arange(8)[None, :, None, None, None]
+    st = np.arange(nstu)[None, None, :, None, None]
+    bb = np.arange(8)[None, None, None, None, :]
+    i, q = bb // 2, bb % 2
+    sl = 4 * sg + i
+    kt = 2 * st + q
+    row = 8 * (8 * np.minimum(sl, S - 1) + v) + (n & 7)[None, None, None, :, None]
+    col = 4 * np.minimum(kt, nkt - 1) + g[None, None, None, :, None]
+    s = np.where((n < 8)[None, None, None, :, None], gs[row, col], us[row, col])
+    s = np.where((sl < S) & (kt < nkt), s, 0).astype(np.uint8)
+    out.append(s.reshape(-1))
+    # bdns: [rb][v][st][lane][8]
+    nj, nstd = I // 64, -(-I // 256)
+    rb = np.arange(-(-H // 512))[:, None, None, None, None]
+    st = np.arange(nstd)[None, None, :, None, None]
+    h = bb % 2
+    qq = 16 * rb + 2 * v + h
+    sj = 4 * st + i
+    row = 32 * np.minimum(qq, nq - 1) + n[None, None, None, :, None] + 16 * (g[None, None, None, :, None] >> 1)
+    col = 2 * np.minimum(sj, nj - 1) + (g[None, None, None, :, None] & 1)
+    s = np.where((qq < nq) & (sj < nj), ds[row, col], 0).astype(np.uint8)
     out.append(s.reshape(-1))
     return np.concatenate(out).astype(np.uint8)

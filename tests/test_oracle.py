@@ -211,8 +211,8 @@ def test_native_layout_is_a_reordering(shape):
     H, I = shape
     parts = synth.expert_block(H, I, 5, 1, 7)
     nat = native_layout.to_native(parts, H, I)
-    gu, gus, dn, dns = native_layout.native_sizes(H, I)
-    assert nat.size == gu + gus + dn + dns
+    gu, gus, dn, dns, bgus, bdns = native_layout.native_sizes(H, I)
+    assert nat.size == gu + gus + dn + dns + bgus + bdns
     assert np.array_equal(np.sort(nat[:gu]), np.sort(np.concatenate([parts[0].ravel(), parts[2].ravel()])))
     assert np.array_equal(np.sort(nat[gu + gus:gu + gus + dn]), np.sort(parts[4].ravel()))
     # lane (n=3, g=2) of tile 1, k tile 1: gate row 11, bytes [64 + 32, +16)
@@ -222,3 +222,19 @@ def test_native_layout_is_a_reordering(shape):
     # its scale: byte 1 of lane 35's chunk in tile 1's first scale chunk = gate_s[11, 4*1 + 2]
     sc = nat[gu + 1 * ((nkt + 15) // 16) * 1024:][:1024].reshape(64, 16)
     assert sc[35, 1] == parts[1][11, 6]
+    # the batched kernels' copy of the same scales: group 0, wave 1 (tile 1 =
+    # 8 * slice 0 + 1), step 0, lane 35, byte 2 * 0 + 1 (k tile 1)
+    base = gu + gus + dn + dns
+    word = nat[base + ((0 * 8 + 1) * -(-H // 256) + 0) * 512:][:512].reshape(64, 8)
+    assert word[35, 1] == parts[1][11, 6]
+    # and every scale byte of each region appears in it as often as the
+    # kernels read it: each real gate/up scale once, each real down scale once
+    bg = nat[base:base + bgus]
+    assert np.array_equal(np.sort(bg[bg != 0]), np.sort(np.concatenate([parts[1].ravel(), parts[3].ravel()])[
+        np.concatenate([parts[1].ravel(), parts[3].ravel()]) != 0]))
+    bd = nat[base + bgus:base + bgus + bdns]
+    assert np.array_equal(np.sort(bd[bd != 0]), np.sort(parts[5].ravel()[parts[5].ravel() != 0]))
+    # down: row block 0, wave 2 (row pairs 4, 5), step 0, lane (n=3, g=3): byte
+    # 2 * 1 + 1 = slice 1, pair 5: down row 32 * 5 + 3 + 16 = 179, block 2 * 1 + 1
+    word = nat[base + bgus + ((0 * 8 + 2) * -(-I // 256) + 0) * 512:][:512].reshape(64, 8)
+    assert word[3 * 16 + 3, 3] == parts[5][179, 3]

@@ -199,8 +199,18 @@ __host__ __device__ inline uint32_t mix32(uint32_t x) {
 //        32q + n + 16(g>>1), bytes [32j + 16(g&1), +16)
 //   dns  [I/64 slices][ceil(H/512)] 1 KB: lane byte i = scale of the lane's
 //        row at pair 16c + i, block 2j + (g&1)
+// The same scales again in the order of the batched GEMM kernels
+// (moe_batched.hip: units of 4 slices or 16 row pairs, 8 waves, 256-column
+// steps), so that a wave reads one 8-byte word per lane and step:
+//   bgus [ceil(I/256) slice groups sg][8 waves v][ceil(H/256) steps s] 512 B:
+//        lane (n,g) byte 2i + q = scale of the lane's row of tile
+//        8(4sg + i) + v at k tile 2s + q, block 4kt + g
+//   bdns [ceil(H/512) row blocks rb][8 waves v][ceil(I/256) steps st] 512 B:
+//        lane (n,g) byte 2i + h = scale of down row 32q + n + 16(g>>1),
+//        q = 16rb + 2v + h, at slice 4st + i, block 2j + (g&1)
+// (0 past the end of either dimension).
 struct NativeLayout {
-    uint64_t gu, gus, dn, dns, total;
+    uint64_t gu, gus, dn, dns, bgus, bdns, total;
     __host__ __device__ static NativeLayout make(uint32_t H, uint32_t I) {
         NativeLayout m;
         uint64_t o = 0;
@@ -208,6 +218,8 @@ struct NativeLayout {
         m.gus = o; o += (uint64_t)(I / 8) * ((H / 128 + 15) / 16) * 1024;
         m.dn = o;  o += (uint64_t)(I / 64) * (H / 32) * 1024;
         m.dns = o; o += (uint64_t)(I / 64) * ((H / 32 + 15) / 16) * 1024;
+        m.bgus = o; o += (uint64_t)((I + 255) / 256) * 8 * ((H + 255) / 256) * 512;
+        m.bdns = o; o += (uint64_t)((H + 511) / 512) * 8 * ((I + 255) / 256) * 512;
         m.total = o;
         return m;
     }

@@ -475,7 +475,7 @@ constexpr uint32_t kRowB = kKC * 2u;            // bytes of a staged row
 constexpr uint32_t kSlotB = kRows * kRowB;      // 48 KB
 constexpr uint32_t kDma = kRows / 2u / kWaves;  // DMA instructions per wave per step (1 KB = 2 rows each)
 constexpr uint32_t kWL = 8;                     // 16-byte weight loads per step
-constexpr uint32_t kSL = 4;                     // 4-byte scale loads per step
+constexpr uint32_t kSL = 1;                     // 8-byte scale loads per step (NativeLayout::bgus / bdns)
 constexpr uint32_t kAfter = kDma + 2u * (kWL + kSL);  // issued after step z's activations
 constexpr uint32_t kOOBV = 0x80000000u;  // a lane offset past every piece array (they stay below 2 GB)
 static_assert(kRows % (2u * kWaves) == 0u, "DMA rows must split evenly over the waves");
@@ -548,10 +548,12 @@ WL_DEV void a_issue(const AStream& A, uint32_t k0) {
 
 struct WBuf {
     u32x4 w[kWL];
-    uint32_t s[kSL];
+    uint32_t s[2];  // the step's 8 scale bytes
 };
-WL_DEV uint32_t bld4(rsrc_t r, uint32_t voff, uint32_t soff) {
-    return __builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, 0);
+WL_DEV void bld8(rsrc_t r, uint32_t voff, uint32_t soff, uint32_t (&s)[2]) {
+    const uint2 v = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, (int)voff, (int)soff, 0));
+    s[0] = v.x;
+    s[1] = v.y;
 }
 
 // Step 2: s_waitcnt vmcnt(kAfter) (expcnt, lgkmcnt not waited on), barrier.
@@ -656,7 +658,7 @@ struct UnitInfo {
 // 1 KB per 128-column k tile, one scale byte per k tile), K = H.
 // Output: the SwiGLU values as pieces, smid3 / mid3 rows.
 constexpr uint32_t kSG = 4;
-static_assert(kWL == 2u * kSG && kSL == kSG, "gate/up step = 2 k tiles x kSG slices");
+static_assert(kWL == 2u * kSG && kSG == 4u, "gate/up step = 2 k tiles x 4 slices (one 8-byte scale word)");
 struct UpK {
     const DecodeArgs& a;
     const BatchArgs& b;
@@ -726,9 +728,7 @@ struct UpK {
             const uint32_t so = wpart * 8u * nkt * 1024u + min(8u * s + j, nkt - 1u) * 1024u;
             W.w[j] = bld16_nt(wrs, wvoff, wsh ? so : ro);
         } else {
-            const uint32_t i = j - kWL, kt = min(2u * s, nkg - 1u);
-            const uint32_t sl = min(wpart * kSG + i, S - 1u);
-            W.s[i] = bld4(srs, vgus, sl * 8u * cdiv(nkg, 16u) * 1024u + (kt / 16u) * 1024u + 4u * ((kt % 16u) / 4u));
+            bld8(srs, vgus, (wpart * 8u * nst + s) * 512u, W.s);
         }
     }
     WL_MEM void begin(uint32_t i) {
@@ -778,7 +778,7 @@ struct UpK {
         for (uint32_t q = 0; q < 2; q++)
 #pragma unroll
             for (uint32_t i = 0; i < kSG; i++)
-                sc[q][i] = e8m0f_if((W.s[i] >> (8u * ((2u * s + q) % 4u))) & 0xFFu, 2u * s + q < nkg);
+                sc[q][i] = e8m0f_if((W.s[i >> 1] >> (8u * (2u * (i & 1u) + q))) & 0xFFu, 2u * s + q < nkg);
         constexpr uint32_t N = 8u * NP;
         bf16x8 af[2][NB];
 #pragma unroll
@@ -861,7 +861,7 @@ __global__ void __launch_bounds__(kThreads) bup_kernel(const DecodeArgs* __restr
     k.stab = stab;
     k.NL = NativeLayout::make(H, I);
     k.vgu = (uint32_t)k.NL.gu + k.v * k.nkg * 1024u + 16u * k.lane;
-    k.vgus = (uint32_t)k.NL.gus + k.v * cdiv(k.nkg, 16u) * 1024u + 16u * k.lane;
+    k.vgus = (uint32_t)k.NL.bgus + k.v * k.nst * 512u + 8u * k.lane;
     k.vsh = k.v * k.nkt * 1024u + 16u * k.lane;
 #pragma unroll
     for (uint32_t j = 0; j < 4; j++) {
@@ -879,11 +879,11 @@ __global__ void __launch_bounds__(kThreads) bup_kernel(const DecodeArgs* __restr
 // q = 16 rb + 2v + h (h = 0, 1; 32 rows each, native dn chunks: 1 KB per
 // 64-column slice, v_permlane32_swap pairs the halves), K = I.
 // Output: f32 rows of shout / expout.
-static_assert(kWL == 8u && kSL == 4u, "down step = 4 slices x 2 row pairs");
+static_assert(kWL == 8u && kSL == 1u, "down step = 4 slices x 2 row pairs (one 8-byte scale word)");
 struct DownK {
     const DecodeArgs& a;
     const BatchArgs& b;
-    uint32_t H, I, SI, E, nq, NS, nks, RBs, RBr, Us, nst, nu, v, lane, n, g;
+    uint32_t H, I, SI, E, nq, NS, nks, RBs, RBr, Us, nst, nstd, nu, v, lane, n, g;
     PassTab pt;
     const uint8_t* const* stab;
     NativeLayout NL;
@@ -950,8 +950,7 @@ struct DownK {
             const uint32_t so = min(8u * st + j, nks - 1u) * 4u * H * 16u;
             W.w[j] = bld16_nt(wrs, wvoff, wsh ? so : ro);
         } else {
-            const uint32_t i = j - kWL, sj = min(st * 4u + i, NS - 1u), qs = min(q0, nq - 1u);
-            W.s[i] = bld4(srs, vdns, (sj * cdiv(nq, 16u) + qs / 16u) * 1024u + 4u * ((qs % 16u) / 4u));
+            bld8(srs, vdns, (wpart * 8u * nstd + min(st, nstd - 1u)) * 512u, W.s);
         }
     }
     WL_MEM void begin(uint32_t i) {
@@ -993,7 +992,6 @@ struct DownK {
     // MFMAs run.
     template <uint32_t NB, uint32_t NP>
     WL_MEM void comp_routed(uint32_t st, const uint8_t* sl, const WBuf& W) {
-        const uint32_t q0 = min(cu.part * 16u + 2u * v, nq - 1u);
         constexpr uint32_t NI = NB * NP, N = 8u * NI;
         auto frag = [&](uint32_t it) {
             const uint32_t o = it / NI, in = it % NI, s4 = o / 2u, f = o % 2u;
@@ -1013,7 +1011,7 @@ struct DownK {
 #pragma unroll
                     for (uint32_t h = 0; h < 2; h++) {
                         // decoded once, then swapped like the weight dwords
-                        const uint32_t sv = __float_as_uint(e8m0f((W.s[s4] >> (8u * ((q0 + h) % 4u))) & 0xFFu));
+                        const uint32_t sv = __float_as_uint(e8m0f((W.s[s4 >> 1] >> (8u * (2u * (s4 & 1u) + h))) & 0xFFu));
                         uint32_t sx, sy;
                         swap32(sv, sv, sx, sy);
                         scx[h] = valid ? __uint_as_float(sx) : 0.f;
@@ -1101,7 +1099,8 @@ __global__ void __launch_bounds__(kThreads) bdown_kernel(const DecodeArgs* __res
     k.stab = stab;
     k.NL = NativeLayout::make(H, I);
     k.vdn = (uint32_t)k.NL.dn + 16u * k.lane;
-    k.vdns = (uint32_t)k.NL.dns + 16u * k.lane;
+    k.nstd = cdiv(I, kKC);
+    k.vdns = (uint32_t)k.NL.bdns + k.v * k.nstd * 512u + 8u * k.lane;
 #pragma unroll
     for (uint32_t j = 0; j < 4; j++) {
         k.lo_r[j / 2u][j % 2u] = a_lane_off(8u * (j / 2u) + 4u * (k.g & 1u) + (k.g >> 1) + 2u * (j % 2u));

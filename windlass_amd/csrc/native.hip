@@ -61,12 +61,15 @@ constexpr uint32_t kConvThreads = 256;
 constexpr uint32_t kRowPad = 1040;  // LDS stride of a staged 1 KB row (16 B of padding: no bank conflicts)
 constexpr uint32_t kScPad = 68;     // LDS stride of a staged row of 64 scale bytes
 constexpr uint32_t kConvLds = 512 * kScPad;  // the largest role (down scales, 512 rows)
-static_assert(kConvLds >= 32 * kRowPad && kConvLds >= 16 * kRowPad + 16 * kScPad, "conversion LDS");
+static_assert(kConvLds >= 32 * kRowPad && kConvLds >= 16 * kRowPad + 16 * kScPad && kConvLds >= 64 * 260,
+              "conversion LDS");
 
 // Work items per block: role A = gate/up tile T x 16 k tiles (cc), role B =
-// 32 down rows (q) x 32 slices (jb), role C = 512 down rows (cc) x 32 slices.
+// 32 down rows (q) x 32 slices (jb), role C = 512 down rows (cc) x 32 slices,
+// role D = bgus (slice group, wave) x 32 steps, role E = bdns (row block,
+// wave) x 32 steps.
 struct ConvGrid {
-    uint32_t nkt, ncca, nq, nccc, nj, njb, nA, nB, nC;
+    uint32_t nkt, ncca, nq, nccc, nj, njb, nsg, nstu, nrb, nstd, nA, nB, nC, nD, nE;
     __host__ __device__ static ConvGrid make(uint32_t H, uint32_t I) {
         ConvGrid g;
         g.nkt = H / 128;
@@ -75,12 +78,19 @@ struct ConvGrid {
         g.nccc = (g.nq + 15) / 16;
         g.nj = I / 64;
         g.njb = (g.nj + 31) / 32;
+        g.nsg = (I + 255) / 256;
+        g.nstu = (H + 255) / 256;
+        g.nrb = (H + 511) / 512;
+        g.nstd = (I + 255) / 256;
         g.nA = (I / 8) * g.ncca;
         g.nB = g.nq * g.njb;
         g.nC = g.nccc * g.njb;
+        g.nD = g.nsg * 8 * ((g.nstu + 31) / 32);
+        g.nE = g.nrb * 8 * ((g.nstd + 31) / 32);
         return g;
     }
 };
+constexpr uint32_t kBPad = 260;  // LDS stride of a staged row of 256 scale bytes
 
 __global__ void __launch_bounds__(kConvThreads) to_native_kernel(const ConvBatch cb, uint32_t H, uint32_t I) {
     const RefBlock& b = cb.b[blockIdx.y];
@@ -135,6 +145,62 @@ __global__ void __launch_bounds__(kConvThreads) to_native_kernel(const ConvBatch
         return;
     }
     w -= G.nB;
+    if (w >= G.nC) {
+        w -= G.nC;
+        if (w < G.nD) {
+            // bgus words (sg, v, s) for 32 steps: LDS row 16i + n = the scale
+            // row of tile 8(4sg + i) + v, row n, bytes [256c, +256) (64 k tiles)
+            const uint32_t nc = (G.nstu + 31) / 32, sg = w / (8 * nc), v = (w / nc) % 8, c = w % nc;
+            const uint32_t S = G.nj, nb = min(256u, H / 32 - 256u * c);  // scale bytes per row in this item
+            for (uint32_t u = tid; u < 64u * (nb / 4u); u += kConvThreads) {
+                const uint32_t r = u / (nb / 4u), cw = u % (nb / 4u), i = r / 16u, n = r % 16u, sl = 4u * sg + i;
+                const uint32_t row = 8u * (8u * sl + v) + (n & 7u);
+                *(uint32_t*)(lds + r * kBPad + 4u * cw) =
+                    sl < S ? ref4s(b, n < 8 ? 1 : 3, (uint64_t)row * (H / 32) + 256u * c + 4u * cw) : 0u;
+            }
+            __syncthreads();
+            const uint32_t ns = min(32u, G.nstu - 32u * c);
+            for (uint32_t u = tid; u < 64u * ns; u += kConvThreads) {
+                const uint32_t sl = u / 64u, lane = u % 64u, n = lane % 16u, g = lane / 16u;
+                uint32_t v2[2] = {0u, 0u};
+#pragma unroll
+                for (uint32_t bb = 0; bb < 8; bb++) {
+                    const uint32_t i = bb / 2u, q = bb % 2u, kt = 2u * (32u * c + sl) + q;
+                    if (kt < G.nkt)  // tiles past I were staged as zeros
+                        v2[bb / 4] |= (uint32_t)lds[(16u * i + n) * kBPad + 4u * (kt - 64u * c) + g] << (8 * (bb % 4));
+                }
+                *(uint2*)(dst + L.bgus + ((uint64_t)(sg * 8u + v) * G.nstu + 32u * c + sl) * 512 + 8u * lane) =
+                    uint2{v2[0], v2[1]};
+            }
+            return;
+        }
+        w -= G.nD;
+        // bdns words (rb, v, st) for 32 steps: LDS row 32h + r = the scale row
+        // of down row 32q + r, q = 16rb + 2v + h, bytes [256c, +256) (128 slices)
+        const uint32_t nc = (G.nstd + 31) / 32, rb = w / (8 * nc), v = (w / nc) % 8, c = w % nc;
+        const uint32_t nb = min(256u, I / 32 - 256u * c);
+        for (uint32_t u = tid; u < 64u * (nb / 4u); u += kConvThreads) {
+            const uint32_t r = u / (nb / 4u), cw = u % (nb / 4u), q = 16u * rb + 2u * v + r / 32u;
+            *(uint32_t*)(lds + r * kBPad + 4u * cw) =
+                q < G.nq ? ref4s(b, 5, (uint64_t)(32u * q + r % 32u) * (I / 32) + 256u * c + 4u * cw) : 0u;
+        }
+        __syncthreads();
+        const uint32_t ns = min(32u, G.nstd - 32u * c);
+        for (uint32_t u = tid; u < 64u * ns; u += kConvThreads) {
+            const uint32_t sl = u / 64u, lane = u % 64u, n = lane % 16u, g = lane / 16u;
+            uint32_t v2[2] = {0u, 0u};
+#pragma unroll
+            for (uint32_t bb = 0; bb < 8; bb++) {
+                const uint32_t i = bb / 2u, h = bb % 2u, sj = 4u * (32u * c + sl) + i;
+                if (sj < G.nj)  // row pairs past H were staged as zeros
+                    v2[bb / 4] |= (uint32_t)lds[(32u * h + n + 16u * (g >> 1)) * kBPad + 2u * (sj - 128u * c) + (g & 1u)]
+                                  << (8 * (bb % 4));
+            }
+            *(uint2*)(dst + L.bdns + ((uint64_t)(rb * 8u + v) * G.nstd + 32u * c + sl) * 512 + 8u * lane) =
+                uint2{v2[0], v2[1]};
+        }
+        return;
+    }
     {
         // dns chunks (j, cc) for 32 slices: LDS row r = down row 512cc + r,
         // its scale bytes [64jb, +2 nsl)
@@ -225,7 +291,8 @@ static void ref_parts(const uint8_t* src, uint32_t H, uint32_t I, const uint8_t*
 
 static int launch_conv(const ConvBatch& cb, uint32_t n, uint32_t H, uint32_t I, void* stream) {
     const ConvGrid G = ConvGrid::make(H, I);
-    hipLaunchKernelGGL(to_native_kernel, dim3(G.nA + G.nB + G.nC, n), dim3(kConvThreads), 0, (hipStream_t)stream, cb,
+    hipLaunchKernelGGL(to_native_kernel, dim3(G.nA + G.nB + G.nC + G.nD + G.nE, n), dim3(kConvThreads), 0,
+                       (hipStream_t)stream, cb,
                        H, I);
     return (int)hipGetLastError();
 }
