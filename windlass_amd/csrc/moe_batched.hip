@@ -476,10 +476,8 @@ constexpr uint32_t kSlotB = kRows * kRowB;      // 48 KB
 constexpr uint32_t kDma = kRows / 2u / kWaves;  // DMA instructions per wave per step (1 KB = 2 rows each)
 constexpr uint32_t kWL = 8;                     // 16-byte weight loads per step
 constexpr uint32_t kSL = 1;                     // 8-byte scale loads per step (NativeLayout::bgus / bdns)
-constexpr uint32_t kAfter = kDma + 2u * (kWL + kSL);  // issued after step z's activations
 constexpr uint32_t kOOBV = 0x80000000u;  // a lane offset past every piece array (they stay below 2 GB)
 static_assert(kRows % (2u * kWaves) == 0u, "DMA rows must split evenly over the waves");
-static_assert(kAfter < 64u, "vmcnt is 6 bits");
 
 // Slot layout: row R (512 bytes); its 16-byte group p holds columns
 // [k0 + 8 (p ^ (R & 15)), +8) of the step, so the 16 rows an A fragment reads
@@ -546,6 +544,85 @@ WL_DEV void a_issue(const AStream& A, uint32_t k0) {
     for (uint32_t k = 0; k < kDma; k++) a_issue_one<S>(A, k0, k);
 }
 
+// ---- wide passes: 64 tokens, 128-column steps ----------------------------------
+// The same slots hold 192 rows of 256 bytes: row R = 64 pc + m (token m,
+// piece pc; tokens in rows only), its 16-byte group p holding columns
+// [k0 + 8 (p ^ (R & 15)), +8). DMA instruction k of wave v writes rows 4j ..
+// 4j + 3 (j = v + kWaves k; lanes 16r .. 16r + 15 row 4j + r), so a lane's
+// rows are r0 + 32k with r0 = 4v + (lane >> 4) < 32: token r0 + 32 (k & 1),
+// piece k >> 1, R & 15 = r0 & 15.
+constexpr uint32_t kMTW = 64;
+constexpr uint32_t kKCW = 128;
+constexpr uint32_t kRowBW = 2u * kKCW;
+static_assert(3u * kMTW * kRowBW == kSlotB, "a wide step fills one slot");
+static_assert(3u * kMTW * kRowBW / 1024u / kWaves == kDma, "a wide step takes kDma DMAs per wave");
+struct AStreamW {
+    rsrc_t rs;
+    uint32_t base, nt, kd2;  // lane byte offset at k = 0, tokens, bytes per piece row
+};
+WL_DEV uint32_t aw_r0() { return 4u * uni(threadIdx.x >> 6) + ((threadIdx.x & 63u) >> 4); }
+WL_DEV void aw_bind(AStreamW& A, const uint16_t* base, uint64_t bytes, uint32_t row0, uint32_t nt, uint32_t kdim) {
+    A.rs = make_rsrc(base, (uint32_t)bytes);
+    A.nt = nt;
+    A.kd2 = 2u * kdim;
+    const uint32_t r0 = aw_r0(), cg = (threadIdx.x & 15u) ^ (r0 & 15u);
+    A.base = (row0 + r0) * 3u * A.kd2 + 16u * cg;
+}
+// The kDma DMAs of one wide step (columns [k0, k0 + kKCW)); absent rows land
+// as zeros.
+template <int S>
+WL_DEV void aw_issue(const AStreamW& A, uint32_t k0) {
+    const uint32_t v = uni(threadIdx.x >> 6), r0 = aw_r0();
+#pragma unroll
+    for (uint32_t k = 0; k < kDma; k++) {
+        const bool ok = r0 + 32u * (k & 1u) < A.nt;
+        const uint32_t so = 2u * k0 + (96u * (k & 1u) + (k >> 1)) * A.kd2;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            A.rs, (__attribute__((address_space(3))) void*)(slot<S>() + (v + kWaves * k) * 1024u), 16u,
+            ok ? A.base : kOOBV, so, 0, 0);
+    }
+}
+// Lane (m, g) A fragment of row 64 pc + 16 tb + m at column group cg (< 16):
+// lane part m * kRowBW + 16 (cg ^ m).
+WL_DEV uint32_t aw_lane_off(uint32_t cg) {
+    const uint32_t m = threadIdx.x & 15u;
+    return m * kRowBW + 16u * (cg ^ m);
+}
+WL_DEV bf16x8 afragw(const uint8_t* sl, uint32_t pc, uint32_t tb, uint32_t lane_off) {
+    return as_bf16x8(*(const u32x4*)(sl + (pc * kMTW + tb * 16u) * kRowBW + lane_off));
+}
+// The outputs of NB token blocks of a tile (tokens in rows): lane (n, g) calls
+// f(m, value) for each live token m whose column-n value it holds.
+template <uint32_t NB, class F>
+WL_DEV void tile_each_w(const f32x4 (&acc)[NB], uint32_t nt, uint32_t lane, F f) {
+    const uint32_t g = lane >> 4;
+#pragma unroll
+    for (uint32_t tb = 0; tb < NB; tb++)
+#pragma unroll
+        for (uint32_t i = 0; i < 4; i++) {
+            const uint32_t m = tb * 16u + 4u * g + i;
+            if (m < nt) f(m, acc[tb][i]);
+        }
+}
+// SwiGLU epilogue of a gate/up tile (columns n < 8 gate rows, n + 8 the
+// matching up rows): put(m, n, value) for n < 8 and live tokens.
+template <uint32_t NB, class PutF>
+WL_DEV void swiglu_store_w(const f32x4 (&acc)[NB], uint32_t nt, uint32_t lane, PutF put) {
+    const uint32_t n = lane & 15u, g = lane >> 4;
+#pragma unroll
+    for (uint32_t tb = 0; tb < NB; tb++)
+#pragma unroll
+        for (uint32_t i = 0; i < 4; i++) {
+            const float v = acc[tb][i];
+            const float up = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xF, 0xF, false));
+            const uint32_t m = tb * 16u + 4u * g + i;
+            if (n < 8u && m < nt) put(m, n, silu_mul(v, up));
+        }
+}
+struct WBufW {
+    u32x4 w[8];
+};
+
 struct WBuf {
     u32x4 w[kWL];
     uint32_t s[2];  // the step's 8 scale bytes
@@ -556,10 +633,20 @@ WL_DEV void bld8(rsrc_t r, uint32_t voff, uint32_t soff, uint32_t (&s)[2]) {
     s[1] = v.y;
 }
 
-// Step 2: s_waitcnt vmcnt(kAfter) (expcnt, lgkmcnt not waited on), barrier.
+// Step 2: s_waitcnt vmcnt(N) (expcnt, lgkmcnt not waited on), barrier.
+template <uint32_t N>
 WL_DEV void step_barrier() {
+    static_assert(N < 64u, "vmcnt is 6 bits");
     __builtin_amdgcn_sched_barrier(0);
-    __builtin_amdgcn_s_waitcnt((kAfter & 15u) | ((kAfter >> 4) << 14) | 0x0F70u);
+    __builtin_amdgcn_s_waitcnt((N & 15u) | ((N >> 4) << 14) | 0x0F70u);
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+// Between two pipelines of one kernel: every load and DMA of the first has
+// landed and every wave is done with its slots.
+WL_DEV void pipeline_drain() {
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(0x0F70u);
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
@@ -575,19 +662,21 @@ WL_DEV bool advance(Cursor& c, uint32_t nst) {
     return true;
 }
 template <class Kn>
-WL_DEV void issue_w(const Kn& k, uint32_t s, WBuf& W) {
+WL_DEV void issue_w(const Kn& k, uint32_t s, typename Kn::WB& W) {
 #pragma unroll
-    for (uint32_t j = 0; j < kWL + kSL; j++) k.issue_w_one(s, W, j);
+    for (uint32_t j = 0; j < Kn::kLoads; j++) k.issue_w_one(s, W, j);
 }
 template <int S, class Kn>
-WL_DEV void pipe_step(Kn& k, AStream& A, const WBuf& cur, WBuf& nxt) {
+WL_DEV void pipe_step(Kn& k, typename Kn::AS& A, const typename Kn::WB& cur, typename Kn::WB& nxt) {
     if (advance(k.cw, k.nst)) k.bind_w(k.cw.i);
     issue_w(k, k.cw.s, nxt);
-    step_barrier();
+    // loads issued after step z's activations: its weights' successors and
+    // the activations of step z + 1
+    step_barrier<kDma + 2u * Kn::kLoads>();
     // after the barrier every wave is done with step z - 1: its slot takes
     // the activations of step z + 2
     if (advance(k.ca, k.nst)) k.bind_a(k.ca.i, A);
-    a_issue<(S + 2) % 3>(A, k.ca.s * kKC);
+    Kn::template issue_a<(S + 2) % 3>(A, k.ca.s);
     __builtin_amdgcn_sched_barrier(0);
     if (k.cc.i < k.nu) {
         if (k.cc.s == 0u) k.begin(k.cc.i);
@@ -596,25 +685,27 @@ WL_DEV void pipe_step(Kn& k, AStream& A, const WBuf& cur, WBuf& nxt) {
     }
     advance(k.cc, k.nst);
 }
-// Runs the pipeline over this work-group's nu units. Kn provides nst, nu, the
-// cursors ca/cw/cc and bind_a(i, A) / bind_w(i) (unit i >= nu: nothing to
-// load), issue_w_one(s, W, j) (load j of kWL + kSL), begin(i),
-// compute(s, slot, W) and finish().
+// Runs the pipeline over this work-group's nu units. Kn provides the types
+// AS (activation stream) and WB (register buffer of one step's loads), kLoads
+// (loads per step into a WB), nst, nu, the cursors ca/cw/cc and
+// bind_a(i, A) / bind_w(i) (unit i >= nu: nothing to load),
+// issue_w_one(s, W, j), issue_a<slot>(A, s) (kDma DMAs of step s),
+// begin(i), compute(s, slot, W) and finish().
 template <class Kn>
 WL_DEV void run_steps(Kn& k) {
     if (k.nu == 0u) return;
     const uint32_t Z = k.nu * k.nst;
-    AStream A;
-    WBuf B0, B1, B2;
+    typename Kn::AS A;
+    typename Kn::WB B0, B1, B2;
     k.ca = k.cw = k.cc = Cursor{0u, 0u};
     k.bind_w(0u);
     issue_w(k, 0u, B0);
     k.bind_a(0u, A);
-    a_issue<0>(A, 0u);
+    Kn::template issue_a<0>(A, 0u);
     if (advance(k.cw, k.nst)) k.bind_w(k.cw.i);
     issue_w(k, k.cw.s, B1);
     if (advance(k.ca, k.nst)) k.bind_a(k.ca.i, A);
-    a_issue<1>(A, k.ca.s * kKC);
+    Kn::template issue_a<1>(A, k.ca.s);
 #pragma unroll 1
     for (uint32_t z = 0; z < Z; z += 3u) {
         pipe_step<0>(k, A, B0, B2);
@@ -660,9 +751,17 @@ struct UnitInfo {
 constexpr uint32_t kSG = 4;
 static_assert(kWL == 2u * kSG && kSG == 4u, "gate/up step = 2 k tiles x 4 slices (one 8-byte scale word)");
 struct UpK {
+    using AS = AStream;
+    using WB = WBuf;
+    static constexpr uint32_t kLoads = kWL + kSL;
+    template <int S>
+    static __device__ __forceinline__ void issue_a(const AStream& A, uint32_t s) {
+        a_issue<S>(A, s * kKC);
+    }
     const DecodeArgs& a;
     const BatchArgs& b;
     uint32_t H, I, SI, E, K, nkg, nkt, S, NSG, Ssh, Us, nst, nu, v, lane, g;
+    uint32_t uoff;  // unit u runs on work-group (u + uoff) % grid
     PassTab pt;
     const uint8_t* const* stab;
     NativeLayout NL;
@@ -683,7 +782,7 @@ struct UpK {
     WL_MEM UnitInfo unit(uint32_t i) const {
         UnitInfo x{false, false, 0u, 0u, 0u, 0u};
         if (i >= nu) return x;
-        const uint32_t u = blockIdx.x + gridDim.x * i;
+        const uint32_t u = (blockIdx.x + gridDim.x - uoff) % gridDim.x + gridDim.x * i;
         x.live = true;
         if (u < Us) {
             const uint32_t p = u / Ssh;
@@ -831,6 +930,145 @@ struct UpK {
         }
     }
 };
+// Shared gate/up in wide passes (batches of more than kMT tokens): unit
+// (pass p of kMTW tokens, slice pair j): wave v owns tiles T_i = 8 (2j + i) + v
+// (i = 0, 1); step s covers columns [128 s, +128): per tile the native sgu
+// chunks (T_i, 4s + k), k < 4 (lane (n, g): row n, columns [32 kt + 8 g, +8)).
+// A work-group step moves 64 KB of weights and 48 KB of activations for 768
+// MFMAs (a kMT unit: the same bytes for 384), and each A fragment feeds two
+// tiles.
+struct SharedUpW {
+    using AS = AStreamW;
+    using WB = WBufW;
+    static constexpr uint32_t kLoads = 8;
+    template <int S>
+    static __device__ __forceinline__ void issue_a(const AStreamW& A, uint32_t s) {
+        aw_issue<S>(A, s * kKCW);
+    }
+    const DecodeArgs& a;
+    const BatchArgs& b;
+    uint32_t H, SI, nkt, nsl, npair, npass, nst, nu, v, lane;
+    Cursor ca, cw, cc;
+    rsrc_t wrs;
+    uint32_t wpair, vbase;
+    uint32_t lo[4];  // A fragment lane offsets of k step k (cg = 4k + g)
+    uint32_t cpair, cnt, crow0, cnb;
+    f32x4 acc[2][4];
+
+    struct Unit {
+        bool live;
+        uint32_t pair, nt, row0;
+    };
+    WL_MEM Unit unit(uint32_t i) const {
+        Unit x{false, 0u, 0u, 0u};
+        if (i >= nu) return x;
+        const PassPart jp = pass_part(blockIdx.x + gridDim.x * i, npair, npass);
+        x.live = true;
+        x.pair = jp.part;
+        x.row0 = jp.j * kMTW;
+        x.nt = min(kMTW, b.T - x.row0);
+        return x;
+    }
+    WL_MEM void bind_a(uint32_t i, AStreamW& A) const {
+        const Unit x = unit(i);
+        if (!x.live) return aw_bind(A, nullptr, 0u, 0u, 0u, 0u);
+        aw_bind(A, b.norm3, (uint64_t)b.T * 6u * H, x.row0, x.nt, H);
+    }
+    WL_MEM void bind_w(uint32_t i) {
+        const Unit x = unit(i);
+        const NativeShared NS = NativeShared::make(H, SI);
+        wrs = x.live ? make_rsrc(a.sh_native + NS.sgu, (uint32_t)(NS.sdn - NS.sgu)) : make_rsrc(nullptr, 0u);
+        wpair = x.pair;
+    }
+    WL_MEM void issue_w_one(uint32_t s, WBufW& W, uint32_t j) const {
+        const uint32_t T = 8u * min(2u * wpair + j / 4u, nsl - 1u) + v;
+        W.w[j] = bld16(wrs, vbase, (T * nkt + 4u * s + j % 4u) * 1024u);  // re-read by every pass: cached
+    }
+    WL_MEM void begin(uint32_t i) {
+        const Unit x = unit(i);
+        cpair = x.pair;
+        cnt = x.nt;
+        crow0 = x.row0;
+        cnb = cdiv(x.nt, 16u);
+#pragma unroll
+        for (uint32_t t = 0; t < 2; t++)
+#pragma unroll
+            for (uint32_t tb = 0; tb < 4; tb++) acc[t][tb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    // Iteration it = 3 k + pc: plane pc of k step k against both tiles; the
+    // next iteration's NB fragments are read while this one's MFMAs run.
+    template <uint32_t NB>
+    WL_MEM void comp(const uint8_t* sl, const WBufW& W) {
+        bf16x8 af[2][NB];
+#pragma unroll
+        for (uint32_t tb = 0; tb < NB; tb++) af[0][tb] = afragw(sl, 0u, tb, lo[0]);
+#pragma unroll
+        for (uint32_t it = 0; it < 12u; it++) {
+            const uint32_t k = it / 3u, c = it & 1u;
+            if (it + 1u < 12u) {
+                const uint32_t nx = it + 1u;
+#pragma unroll
+                for (uint32_t tb = 0; tb < NB; tb++) af[c ^ 1u][tb] = afragw(sl, nx % 3u, tb, lo[nx / 3u]);
+            }
+#pragma unroll
+            for (uint32_t t = 0; t < 2; t++) {
+                const bf16x8 bw = as_bf16x8(W.w[4u * t + k]);
+#pragma unroll
+                for (uint32_t tb = 0; tb < NB; tb++) acc[t][tb] = mma(af[c][tb], bw, acc[t][tb]);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    WL_MEM void compute(uint32_t, const uint8_t* sl, const WBufW& W) {
+        switch (cnb) {
+            case 1: return comp<1>(sl, W);
+            case 2: return comp<2>(sl, W);
+            case 3: return comp<3>(sl, W);
+            default: return comp<4>(sl, W);
+        }
+    }
+    WL_MEM void finish() {
+        const uint32_t ln = opaque_lane();
+#pragma unroll
+        for (uint32_t t = 0; t < 2; t++) {
+            const uint32_t sl = 2u * cpair + t;
+            if (sl >= nsl) continue;
+            const uint32_t col = 8u * (8u * sl + v);
+            swiglu_store_w(acc[t], cnt, ln, [&](uint32_t m, uint32_t n, float x) {
+                store3(b.smid3 + (size_t)(crow0 + m) * 3u * SI + col + n, SI, x);
+            });
+        }
+    }
+};
+// The shared expert's wide-pass units run first when there are at least as
+// many as work-groups (the bf16 shared expert in this launch); returns their
+// count (0: the shared expert runs as kMT units among the routed ones). A
+// wide unit is about three routed units of work, so with fewer of them than
+// work-groups the ones that hold one end last (measured: T = 64 and 256
+// slower, T = 1024 3.8 % faster per call).
+WL_DEV uint32_t run_shared_up_wide(const DecodeArgs& a, const BatchArgs& b) {
+    if ((b.flags & (kBatchNoShared | kBatchShared4)) ||
+        cdiv(b.T, kMTW) * cdiv(a.SI / kSlice, 2u) < gridDim.x)
+        return 0u;
+    SharedUpW w{a, b};
+    w.H = a.H;
+    w.SI = a.SI;
+    w.nkt = a.H / 32u;
+    w.nsl = a.SI / kSlice;
+    w.npair = cdiv(w.nsl, 2u);
+    w.npass = cdiv(b.T, kMTW);
+    w.nst = a.H / kKCW;
+    const uint32_t U = w.npass * w.npair;
+    w.nu = U > blockIdx.x ? cdiv(U - blockIdx.x, gridDim.x) : 0u;
+    w.lane = threadIdx.x & 63u;
+    w.v = uni(threadIdx.x >> 6);
+    w.vbase = 16u * w.lane;
+#pragma unroll
+    for (uint32_t k = 0; k < 4; k++) w.lo[k] = aw_lane_off(4u * k + (w.lane >> 4));
+    run_steps(w);
+    pipeline_drain();
+    return U;
+}
 __global__ void __launch_bounds__(kThreads) bup_kernel(const DecodeArgs* __restrict__ pa, const BatchArgs b) {
     const DecodeArgs& a = *pa;
     extern __shared__ __align__(16) uint8_t dyn[];
@@ -839,6 +1077,7 @@ __global__ void __launch_bounds__(kThreads) bup_kernel(const DecodeArgs* __restr
     const uint32_t E = a.E + (sh4 ? 1u : 0u);  // experts in the pass table
     const uint8_t* const* stab = load_slot_tab(a, a.E, sh4, (const uint8_t**)dyn);
     const PassTab pt = load_pass_tab(b, E, a.K, (uint32_t*)(dyn + 8u * E), stab);
+    const uint32_t Uw = run_shared_up_wide(a, b);
     UpK k{a, b};
     k.H = H;
     k.I = I;
@@ -850,10 +1089,12 @@ __global__ void __launch_bounds__(kThreads) bup_kernel(const DecodeArgs* __restr
     k.S = I / kSlice;
     k.NSG = cdiv(k.S, kSG);
     k.Ssh = a.SI / kSlice;
-    k.Us = (b.flags & (kBatchNoShared | kBatchShared4)) ? 0u : cdiv(b.T, kMT) * k.Ssh;
+    k.Us = (b.flags & (kBatchNoShared | kBatchShared4)) || Uw ? 0u : cdiv(b.T, kMT) * k.Ssh;
     k.nst = cdiv(H, kKC);
     const uint32_t U = k.Us + pt.n * k.NSG;
-    k.nu = U > blockIdx.x ? cdiv(U - blockIdx.x, gridDim.x) : 0u;
+    k.uoff = Uw % gridDim.x;  // the work-groups after the wide units' last ones start
+    const uint32_t b0 = (blockIdx.x + gridDim.x - k.uoff) % gridDim.x;
+    k.nu = U > b0 ? cdiv(U - b0, gridDim.x) : 0u;
     k.lane = threadIdx.x & 63u;
     k.g = k.lane >> 4;
     k.v = uni(threadIdx.x >> 6);
@@ -881,9 +1122,17 @@ __global__ void __launch_bounds__(kThreads) bup_kernel(const DecodeArgs* __restr
 // Output: f32 rows of shout / expout.
 static_assert(kWL == 8u && kSL == 1u, "down step = 4 slices x 2 row pairs (one 8-byte scale word)");
 struct DownK {
+    using AS = AStream;
+    using WB = WBuf;
+    static constexpr uint32_t kLoads = kWL + kSL;
+    template <int S>
+    static __device__ __forceinline__ void issue_a(const AStream& A, uint32_t s) {
+        a_issue<S>(A, s * kKC);
+    }
     const DecodeArgs& a;
     const BatchArgs& b;
     uint32_t H, I, SI, E, nq, NS, nks, RBs, RBr, Us, nst, nstd, nu, v, lane, n, g;
+    uint32_t uoff;  // unit u runs on work-group (u + uoff) % grid
     PassTab pt;
     const uint8_t* const* stab;
     NativeLayout NL;
@@ -903,7 +1152,7 @@ struct DownK {
     WL_MEM UnitInfo unit(uint32_t i) const {
         UnitInfo x{false, false, 0u, 0u, 0u, 0u};
         if (i >= nu) return x;
-        const uint32_t u = blockIdx.x + gridDim.x * i;
+        const uint32_t u = (blockIdx.x + gridDim.x - uoff) % gridDim.x + gridDim.x * i;
         x.live = true;
         if (u < Us) {
             const uint32_t p = u / RBs;
@@ -1069,6 +1318,129 @@ struct DownK {
         }
     }
 };
+// Shared down in wide passes (batches of more than kMT tokens): unit (pass p
+// of kMTW tokens, row block rb of 256 output rows): wave v owns rows
+// 256 rb + 32 v + 16 i + n (i = 0, 1); step st covers columns [128 st, +128)
+// of SI: native sdn (16 bytes = 8 bf16 columns [8T, 8T + 8) of a row), lane
+// (n, g) of k step k reads tile 4 (4 st + k) + g of its row.
+struct SharedDownW {
+    using AS = AStreamW;
+    using WB = WBufW;
+    static constexpr uint32_t kLoads = 8;
+    template <int S>
+    static __device__ __forceinline__ void issue_a(const AStreamW& A, uint32_t s) {
+        aw_issue<S>(A, s * kKCW);
+    }
+    const DecodeArgs& a;
+    const BatchArgs& b;
+    uint32_t H, SI, nrb, npass, nst, nu, v, lane, n, g;
+    Cursor ca, cw, cc;
+    rsrc_t wrs;
+    uint32_t wvoff[2];
+    uint32_t lo[4];
+    uint32_t crb, cnt, crow0, cnb;
+    f32x4 d[2][4];
+
+    struct Unit {
+        bool live;
+        uint32_t rb, nt, row0;
+    };
+    WL_MEM Unit unit(uint32_t i) const {
+        Unit x{false, 0u, 0u, 0u};
+        if (i >= nu) return x;
+        const PassPart jp = pass_part(blockIdx.x + gridDim.x * i, nrb, npass);
+        x.live = true;
+        x.rb = jp.part;
+        x.row0 = jp.j * kMTW;
+        x.nt = min(kMTW, b.T - x.row0);
+        return x;
+    }
+    WL_MEM void bind_a(uint32_t i, AStreamW& A) const {
+        const Unit x = unit(i);
+        if (!x.live) return aw_bind(A, nullptr, 0u, 0u, 0u, 0u);
+        aw_bind(A, b.smid3, (uint64_t)b.T * 6u * SI, x.row0, x.nt, SI);
+    }
+    WL_MEM void bind_w(uint32_t i) {
+        const Unit x = unit(i);
+        const NativeShared NS = NativeShared::make(H, SI);
+        wrs = x.live ? make_rsrc(a.sh_native + NS.sdn, (uint32_t)(NS.total - NS.sdn)) : make_rsrc(nullptr, 0u);
+#pragma unroll
+        for (uint32_t t = 0; t < 2; t++) wvoff[t] = (g * H + min(256u * x.rb + 32u * v + 16u * t + n, H - 1u)) * 16u;
+    }
+    WL_MEM void issue_w_one(uint32_t st, WBufW& W, uint32_t j) const {
+        W.w[j] = bld16(wrs, wvoff[j / 4u], (16u * st + 4u * (j % 4u)) * H * 16u);  // re-read by every pass: cached
+    }
+    WL_MEM void begin(uint32_t i) {
+        const Unit x = unit(i);
+        crb = x.rb;
+        cnt = x.nt;
+        crow0 = x.row0;
+        cnb = cdiv(x.nt, 16u);
+#pragma unroll
+        for (uint32_t t = 0; t < 2; t++)
+#pragma unroll
+            for (uint32_t tb = 0; tb < 4; tb++) d[t][tb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    template <uint32_t NB>
+    WL_MEM void comp(const uint8_t* sl, const WBufW& W) {
+        bf16x8 af[2][NB];
+#pragma unroll
+        for (uint32_t tb = 0; tb < NB; tb++) af[0][tb] = afragw(sl, 0u, tb, lo[0]);
+#pragma unroll
+        for (uint32_t it = 0; it < 12u; it++) {
+            const uint32_t k = it / 3u, c = it & 1u;
+            if (it + 1u < 12u) {
+                const uint32_t nx = it + 1u;
+#pragma unroll
+                for (uint32_t tb = 0; tb < NB; tb++) af[c ^ 1u][tb] = afragw(sl, nx % 3u, tb, lo[nx / 3u]);
+            }
+#pragma unroll
+            for (uint32_t t = 0; t < 2; t++) {
+                const bf16x8 bw = as_bf16x8(W.w[4u * t + k]);
+#pragma unroll
+                for (uint32_t tb = 0; tb < NB; tb++) d[t][tb] = mma(af[c][tb], bw, d[t][tb]);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    WL_MEM void compute(uint32_t, const uint8_t* sl, const WBufW& W) {
+        switch (cnb) {
+            case 1: return comp<1>(sl, W);
+            case 2: return comp<2>(sl, W);
+            case 3: return comp<3>(sl, W);
+            default: return comp<4>(sl, W);
+        }
+    }
+    WL_MEM void finish() {
+        const uint32_t ln = opaque_lane(), nn = ln & 15u;
+#pragma unroll
+        for (uint32_t t = 0; t < 2; t++) {
+            const uint32_t r = 256u * crb + 32u * v + 16u * t + nn;
+            if (r < H)
+                tile_each_w(d[t], cnt, ln, [&](uint32_t m, float x) { gst(b.shout + (size_t)(crow0 + m) * H + r, x); });
+        }
+    }
+};
+WL_DEV uint32_t run_shared_down_wide(const DecodeArgs& a, const BatchArgs& b) {
+    if ((b.flags & (kBatchNoShared | kBatchShared4)) || cdiv(b.T, kMTW) * cdiv(a.H, 256u) < gridDim.x) return 0u;
+    SharedDownW w{a, b};
+    w.H = a.H;
+    w.SI = a.SI;
+    w.nrb = cdiv(a.H, 256u);
+    w.npass = cdiv(b.T, kMTW);
+    w.nst = a.SI / kKCW;
+    const uint32_t U = w.npass * w.nrb;
+    w.nu = U > blockIdx.x ? cdiv(U - blockIdx.x, gridDim.x) : 0u;
+    w.lane = threadIdx.x & 63u;
+    w.n = w.lane & 15u;
+    w.g = w.lane >> 4;
+    w.v = uni(threadIdx.x >> 6);
+#pragma unroll
+    for (uint32_t k = 0; k < 4; k++) w.lo[k] = aw_lane_off(4u * k + w.g);
+    run_steps(w);
+    pipeline_drain();
+    return U;
+}
 __global__ void __launch_bounds__(kThreads) bdown_kernel(const DecodeArgs* __restrict__ pa, const BatchArgs b) {
     const DecodeArgs& a = *pa;
     extern __shared__ __align__(16) uint8_t dyn[];
@@ -1077,6 +1449,7 @@ __global__ void __launch_bounds__(kThreads) bdown_kernel(const DecodeArgs* __res
     const uint32_t E = a.E + (sh4 ? 1u : 0u);  // experts in the pass table
     const uint8_t* const* stab = load_slot_tab(a, a.E, sh4, (const uint8_t**)dyn);
     const PassTab pt = load_pass_tab(b, E, a.K, (uint32_t*)(dyn + 8u * E), stab);
+    const uint32_t Uw = run_shared_down_wide(a, b);
     DownK k{a, b};
     k.H = H;
     k.I = I;
@@ -1087,10 +1460,12 @@ __global__ void __launch_bounds__(kThreads) bdown_kernel(const DecodeArgs* __res
     k.nks = a.SI / 32u;
     k.RBs = cdiv(H, 128u);
     k.RBr = cdiv(k.nq, 16u);
-    k.Us = (b.flags & (kBatchNoShared | kBatchShared4)) ? 0u : cdiv(b.T, kMT) * k.RBs;
+    k.Us = (b.flags & (kBatchNoShared | kBatchShared4)) || Uw ? 0u : cdiv(b.T, kMT) * k.RBs;
     k.nst = cdiv(max(I, a.SI), kKC);  // the shorter kind's extra steps are masked
     const uint32_t U = k.Us + pt.n * k.RBr;
-    k.nu = U > blockIdx.x ? cdiv(U - blockIdx.x, gridDim.x) : 0u;
+    k.uoff = Uw % gridDim.x;  // the work-groups after the wide units' last ones start
+    const uint32_t b0 = (blockIdx.x + gridDim.x - k.uoff) % gridDim.x;
+    k.nu = U > b0 ? cdiv(U - b0, gridDim.x) : 0u;
     k.lane = threadIdx.x & 63u;
     k.n = k.lane & 15u;
     k.g = k.lane >> 4;
