@@ -270,3 +270,44 @@ def test_corner_scales_through_batched(corners, shared):
         S, M = _mid_scales(f, ids, O.rms_norm(hs[t], None, c["rms_eps"]))
         _check_rows(f, ids, ref["topk_w"], S[0], M[0], ref["out"], out[t], (shared, "batched", t))
     print(f"batched ({shared} shared): {T_BATCH} tokens, planted rows within {TOL}", flush=True)
+
+
+@pytest.mark.parametrize("shared", ["bf16", "mxfp4"])
+def test_corner_scales_through_batched_wide_passes(corners, shared):
+    """1024 tokens, all routed to the planted experts: every planted expert
+    (and the shared expert) runs in the batched kernels' wide passes (tokens
+    split evenly over passes of at most 48, the shared expert in passes of
+    64). Twelve tokens spread over the passes are held to the corner bars
+    against the oracle; every token's other output rows to 1e-5 against the
+    decode kernel (the planted down rows D, E, F scale a SwiGLU value by up to
+    2^126, so two implementations that each meet its term-relative bar can
+    differ there by more than 1e-5 of the row scale)."""
+    f = corners
+    ctx, c = f["ctx"], GLM
+    H, T = c["hidden"], 1024
+    sh = _bind_shared(f, shared)
+    hs = _hidden(T)
+    d_in = H_.DeviceBuffer.from_array(hs)
+    d_out = H_.DeviceBuffer(4 * H * T)
+    ctx.run_moe_batched(0, T, d_in.ptr, None, d_out.ptr)
+    ctx.check_error()
+    counts = ctx.batched_counts()
+    assert sorted(np.nonzero(counts)[0].tolist())[:8] == PLANTED and counts.max() == T
+    out = d_out.download(np.float32).reshape(T, H)
+    for t in (0, 1, 21, 22, 47, 48, 300, 511, 512, 700, 1000, 1023):
+        ref = O.moe_layer(hs[t], f["dense"], f["src"], 0, c, shared_f32=sh)
+        S, M = _mid_scales(f, ref["topk_idx"], O.rms_norm(hs[t], None, c["rms_eps"]))
+        _check_rows(f, ref["topk_idx"], ref["topk_w"], S[0], M[0], ref["out"], out[t], (shared, "wide", t))
+    d_h, d_o = H_.DeviceBuffer(4 * H), H_.DeviceBuffer(4 * H)
+    rest = np.setdiff1d(np.arange(H), ROWS_D + ROWS_E + ROWS_F)
+    worst = 0.0
+    for t in range(T):
+        d_h.upload(hs[t])
+        ctx.run_moe(0, d_h.ptr, d_o.ptr)
+        dec = d_o.download(np.float32)
+        r = O.rel_to_scale(dec[rest].astype(np.float64), out[t][rest])
+        worst = max(worst, r)
+        assert r < TOL, (shared, t, r)
+    ctx.check_error()
+    print(f"batched wide passes ({shared} shared): {T} tokens, worst vs decode {worst:.2e}", flush=True)
+

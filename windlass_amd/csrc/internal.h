@@ -267,7 +267,15 @@ struct NativeShared4 {
 // kBatchShared4: the shared expert is MXFP4 and runs as expert E of the pass
 // table (all T tokens, activations straight from norm3, outputs in the rows
 // [T*K, T*K + T) of mid3 and expout).
-enum : uint32_t { kBatchSkipUnbound = 1u, kBatchNoShared = 2u, kBatchShared4 = 4u };
+// kBatchWideSharedUp / Down (set by launch_batched): the bf16 shared
+// expert's gate/up (down) runs as 64-token units in the wide GEMM kernel.
+enum : uint32_t {
+    kBatchSkipUnbound = 1u,
+    kBatchNoShared = 2u,
+    kBatchShared4 = 4u,
+    kBatchWideSharedUp = 8u,
+    kBatchWideSharedDown = 16u
+};
 // launch_batched phases: routing (norm .. permute), the GEMMs, the combine.
 enum : uint32_t { kPhaseRoute = 1u, kPhaseGemm = 2u, kPhaseCombine = 4u, kPhaseAll = 7u };
 struct BatchArgs {

@@ -37,6 +37,9 @@ namespace wl {
 #define WL_MEM __device__ __forceinline__  // member functions
 
 constexpr uint32_t kMT = 32;         // tokens per pass: two MFMA row blocks of 16
+constexpr uint32_t kMTW = 64;        // tokens per wide pass (more than kMT tokens): four row blocks
+constexpr uint32_t kKCW = 128;       // activation columns staged per wide step
+constexpr uint32_t kMTR = 48;        // tokens per wide pass of a routed expert (three row blocks)
 constexpr uint32_t kKC = 256;        // activation columns staged per step
 constexpr uint32_t kTB = 8;          // tokens per routing work-group
 
@@ -373,17 +376,28 @@ __global__ void __launch_bounds__(256) bpermute_kernel(const BatchArgs b, uint32
 // passes. Units are numbered densely over the passes that exist (unit u =
 // pass j * parts + part), so the grid-stride loop visits live units only and
 // the passes of one expert sit next to each other.
+// With wide passes on, an expert of more than kMT tokens runs as passes of
+// kMTW tokens instead (their own prefix ppw, ppw[E] = all wide passes) and
+// has no kMT passes.
 struct PassTab {
     const uint32_t* cnt;
     const uint32_t* off;
     const uint32_t* pp;
-    uint32_t n;  // passes
+    const uint32_t* ppw;
+    uint32_t n;   // kMT passes
+    uint32_t nw;  // kMTW passes
 };
+WL_DEV uint32_t passes_of(uint32_t c, bool wide) { return wide && c > kMT ? 0u : cdiv(c, kMT); }
+WL_DEV uint32_t wide_passes_of(uint32_t c, bool wide) { return wide && c > kMT ? cdiv(c, kMTR) : 0u; }
 // E counts the MXFP4 shared pseudo-expert (index E - 1) when there is one:
 // all T tokens, compact rows from T*K on.
-WL_DEV PassTab load_pass_tab(const BatchArgs& b, uint32_t E, uint32_t K, uint32_t* s, const uint8_t* const* stab) {
+// wparts > 0: experts of more than kMT tokens run in wide passes if their
+// wparts units per pass fill the grid (fewer wide units than work-groups
+// leave the ones that hold one ending last: measured slower at T = 256).
+WL_DEV PassTab load_pass_tab(const BatchArgs& b, uint32_t E, uint32_t K, uint32_t* s, const uint8_t* const* stab,
+                             uint32_t wparts) {
     const uint32_t tid = threadIdx.x;
-    uint32_t *cnt = s, *off = s + E, *pp = s + 2u * E;
+    uint32_t *cnt = s, *off = s + E, *pp = s + 2u * E, *ppw = s + 3u * E + 1u;
     const bool skip = (b.flags & kBatchSkipUnbound) != 0u;
     const uint32_t esh = (b.flags & kBatchShared4) ? E - 1u : E;
     for (uint32_t f = tid; f < E; f += kThreads) {
@@ -399,25 +413,43 @@ WL_DEV PassTab load_pass_tab(const BatchArgs& b, uint32_t E, uint32_t K, uint32_
     lds_barrier();
     if (tid < 64u) {
         const uint32_t per = cdiv(E, 64u), e0 = tid * per;
-        uint32_t mine = 0;
+        // inclusive scans over the wave of the kMT passes with and without
+        // wide passes and of the wide passes; the wave then picks one form
+        uint32_t mine0 = 0, mine1 = 0, minew = 0;
         for (uint32_t i = 0; i < per; i++)
-            if (e0 + i < E) mine += cdiv(cnt[e0 + i], kMT);
-        uint32_t inc = mine;  // inclusive scan over the wave
+            if (e0 + i < E) {
+                mine0 += passes_of(cnt[e0 + i], false);
+                mine1 += passes_of(cnt[e0 + i], true);
+                minew += wide_passes_of(cnt[e0 + i], true);
+            }
+        uint32_t inc0 = mine0, inc1 = mine1, incw = minew;
 #pragma unroll
         for (uint32_t o = 1; o < 64u; o <<= 1) {
-            const uint32_t t = __shfl_up(inc, o, 64);
-            if (tid >= o) inc += t;
+            const uint32_t t0 = __shfl_up(inc0, o, 64), t1 = __shfl_up(inc1, o, 64), tw = __shfl_up(incw, o, 64);
+            if (tid >= o) {
+                inc0 += t0;
+                inc1 += t1;
+                incw += tw;
+            }
         }
-        uint32_t run = inc - mine;
+        const bool wide = wparts > 0u && __shfl(incw, 63, 64) * wparts >= gridDim.x;
+        if (!wide) minew = incw = 0u;
+        const uint32_t mine = wide ? mine1 : mine0, inc = wide ? inc1 : inc0;
+        uint32_t run = inc - mine, runw = incw - minew;
         for (uint32_t i = 0; i < per; i++)
             if (e0 + i < E) {
                 pp[e0 + i] = run;
-                run += cdiv(cnt[e0 + i], kMT);
+                ppw[e0 + i] = runw;
+                run += passes_of(cnt[e0 + i], wide);
+                runw += wide_passes_of(cnt[e0 + i], wide);
             }
-        if (tid == 63u) pp[E] = inc;
+        if (tid == 63u) {
+            pp[E] = inc;
+            ppw[E] = incw;
+        }
     }
     lds_barrier();
-    return PassTab{cnt, off, pp, uni(pp[E])};
+    return PassTab{cnt, off, pp, ppw, uni(pp[E]), uni(ppw[E])};
 }
 // Routed unit r (< n_passes * parts) -> (pass j, part). Units go in blocks
 // of 8 passes x parts, ordered so that unit r has j % 8 == r % 8 in full
@@ -438,15 +470,26 @@ WL_DEV PassPart pass_part(uint32_t r, uint32_t parts, uint32_t npass) {
 struct Pass {
     uint32_t e, nt, c0;
 };
-WL_DEV Pass pass_at(const PassTab& pt, uint32_t E, uint32_t j) {
+WL_DEV uint32_t expert_of_pass(const uint32_t* pp, uint32_t E, uint32_t j) {
     uint32_t lo = 0, hi = E;  // pp[lo] <= j < pp[hi]
     while (hi - lo > 1u) {
         const uint32_t mid = (lo + hi) >> 1;
-        if (uni(pt.pp[mid]) <= j) lo = mid;
+        if (uni(pp[mid]) <= j) lo = mid;
         else hi = mid;
     }
-    const uint32_t p = j - uni(pt.pp[lo]);
-    return Pass{lo, min(kMT, uni(pt.cnt[lo]) - p * kMT), uni(pt.off[lo]) + p * kMT};
+    return lo;
+}
+// kMT passes: full passes of kMT tokens, the remainder last.
+WL_DEV Pass pass_at(const PassTab& pt, uint32_t E, uint32_t j) {
+    const uint32_t e = expert_of_pass(pt.pp, E, j), p = j - uni(pt.pp[e]);
+    return Pass{e, min(kMT, uni(pt.cnt[e]) - p * kMT), uni(pt.off[e]) + p * kMT};
+}
+// Wide passes: an expert's tokens split evenly over its cdiv(count, kMTR)
+// passes (100 tokens: 34 + 33 + 33, not 48 + 48 + 4).
+WL_DEV Pass pass_at_w(const PassTab& pt, uint32_t E, uint32_t j) {
+    const uint32_t e = expert_of_pass(pt.ppw, E, j), p = j - uni(pt.ppw[e]);
+    const uint32_t c = uni(pt.cnt[e]), np = cdiv(c, kMTR), q = c / np, r = c % np;
+    return Pass{e, q + (p < r ? 1u : 0u), uni(pt.off[e]) + p * q + min(p, r)};
 }
 
 // ---- grouped GEMMs ------------------------------------------------------------
@@ -551,8 +594,6 @@ WL_DEV void a_issue(const AStream& A, uint32_t k0) {
 // 4j + 3 (j = v + kWaves k; lanes 16r .. 16r + 15 row 4j + r), so a lane's
 // rows are r0 + 32k with r0 = 4v + (lane >> 4) < 32: token r0 + 32 (k & 1),
 // piece k >> 1, R & 15 = r0 & 15.
-constexpr uint32_t kMTW = 64;
-constexpr uint32_t kKCW = 128;
 constexpr uint32_t kRowBW = 2u * kKCW;
 static_assert(3u * kMTW * kRowBW == kSlotB, "a wide step fills one slot");
 static_assert(3u * kMTW * kRowBW / 1024u / kWaves == kDma, "a wide step takes kDma DMAs per wave");
@@ -588,6 +629,9 @@ WL_DEV uint32_t aw_lane_off(uint32_t cg) {
     const uint32_t m = threadIdx.x & 15u;
     return m * kRowBW + 16u * (cg ^ m);
 }
+// When cg = c0 | d with c0 per lane and d uniform in bits c0 never uses,
+// aw_lane_off(cg) = aw_lane_off(c0) ^ 16 d: one base register per unit type
+// and a constant per k step.
 WL_DEV bf16x8 afragw(const uint8_t* sl, uint32_t pc, uint32_t tb, uint32_t lane_off) {
     return as_bf16x8(*(const u32x4*)(sl + (pc * kMTW + tb * 16u) * kRowBW + lane_off));
 }
@@ -597,20 +641,25 @@ template <uint32_t NB, class F>
 WL_DEV void tile_each_w(const f32x4 (&acc)[NB], uint32_t nt, uint32_t lane, F f) {
     const uint32_t g = lane >> 4;
 #pragma unroll
-    for (uint32_t tb = 0; tb < NB; tb++)
+    for (uint32_t tb = 0; tb < NB; tb++) {
 #pragma unroll
         for (uint32_t i = 0; i < 4; i++) {
             const uint32_t m = tb * 16u + 4u * g + i;
             if (m < nt) f(m, acc[tb][i]);
         }
+        __builtin_amdgcn_sched_barrier(0);
+    }
 }
 // SwiGLU epilogue of a gate/up tile (columns n < 8 gate rows, n + 8 the
 // matching up rows): put(m, n, value) for n < 8 and live tokens.
+// One token block at a time (sched_barrier): interleaved over the blocks
+// and tiles of a wide unit, the epilogue's temporaries do not fit beside the
+// pipeline's registers.
 template <uint32_t NB, class PutF>
 WL_DEV void swiglu_store_w(const f32x4 (&acc)[NB], uint32_t nt, uint32_t lane, PutF put) {
     const uint32_t n = lane & 15u, g = lane >> 4;
 #pragma unroll
-    for (uint32_t tb = 0; tb < NB; tb++)
+    for (uint32_t tb = 0; tb < NB; tb++) {
 #pragma unroll
         for (uint32_t i = 0; i < 4; i++) {
             const float v = acc[tb][i];
@@ -618,6 +667,16 @@ WL_DEV void swiglu_store_w(const f32x4 (&acc)[NB], uint32_t nt, uint32_t lane, P
             const uint32_t m = tb * 16u + 4u * g + i;
             if (n < 8u && m < nt) put(m, n, silu_mul(v, up));
         }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+}
+// A value the compiler must treat as produced here: keeps the conversions of
+// one k step in their iteration (pure conversions of a whole step are
+// otherwise hoisted together, and their 64 results do not fit beside the
+// wide units' accumulators).
+WL_DEV uint32_t pinned(uint32_t x) {
+    asm volatile("" : "+v"(x));
+    return x;
 }
 struct WBufW {
     u32x4 w[8];
@@ -723,7 +782,7 @@ WL_DEV const uint8_t* const* load_slot_tab(const DecodeArgs& a, uint32_t E, bool
     return s;  // visible after the barrier in load_pass_tab
 }
 // LDS of the tables for E experts and the MXFP4 shared pseudo-expert.
-__host__ __device__ inline size_t gemm_tab_bytes(uint32_t E) { return 8u * (E + 1u) + 4u * (3u * (E + 1u) + 1u); }
+__host__ __device__ inline size_t gemm_tab_bytes(uint32_t E) { return 8u * (E + 1u) + 4u * (4u * (E + 1u) + 2u); }
 
 // Splits x into its three bf16 pieces at p[0], p[stride], p[2 stride].
 WL_DEV void store3(uint16_t* p, uint32_t stride, float x) {
@@ -951,7 +1010,7 @@ struct SharedUpW {
     Cursor ca, cw, cc;
     rsrc_t wrs;
     uint32_t wpair, vbase;
-    uint32_t lo[4];  // A fragment lane offsets of k step k (cg = 4k + g)
+    uint32_t lob;  // A fragment lane offset of k step 0 (cg = g; k step k: ^ 64 k)
     uint32_t cpair, cnt, crow0, cnb;
     f32x4 acc[2][4];
 
@@ -1001,14 +1060,14 @@ struct SharedUpW {
     WL_MEM void comp(const uint8_t* sl, const WBufW& W) {
         bf16x8 af[2][NB];
 #pragma unroll
-        for (uint32_t tb = 0; tb < NB; tb++) af[0][tb] = afragw(sl, 0u, tb, lo[0]);
+        for (uint32_t tb = 0; tb < NB; tb++) af[0][tb] = afragw(sl, 0u, tb, lob);
 #pragma unroll
         for (uint32_t it = 0; it < 12u; it++) {
             const uint32_t k = it / 3u, c = it & 1u;
             if (it + 1u < 12u) {
                 const uint32_t nx = it + 1u;
 #pragma unroll
-                for (uint32_t tb = 0; tb < NB; tb++) af[c ^ 1u][tb] = afragw(sl, nx % 3u, tb, lo[nx / 3u]);
+                for (uint32_t tb = 0; tb < NB; tb++) af[c ^ 1u][tb] = afragw(sl, nx % 3u, tb, lob ^ (64u * (nx / 3u)));
             }
 #pragma unroll
             for (uint32_t t = 0; t < 2; t++) {
@@ -1040,35 +1099,198 @@ struct SharedUpW {
         }
     }
 };
-// The shared expert's wide-pass units run first when there are at least as
-// many as work-groups (the bf16 shared expert in this launch); returns their
-// count (0: the shared expert runs as kMT units among the routed ones). A
-// wide unit is about three routed units of work, so with fewer of them than
-// work-groups the ones that hold one end last (measured: T = 64 and 256
-// slower, T = 1024 3.8 % faster per call).
+// The shared expert's wide-pass units (kBatchWideSharedUp: launch_batched
+// sets it when there are at least as many as work-groups; a wide unit is
+// about three routed units of work, so with fewer of them than work-groups
+// the ones that hold one end last: measured slower at T = 64 and 256, 3.8 %
+// faster per call at T = 1024); returns their count.
+template <bool GLM>
 WL_DEV uint32_t run_shared_up_wide(const DecodeArgs& a, const BatchArgs& b) {
-    if ((b.flags & (kBatchNoShared | kBatchShared4)) ||
-        cdiv(b.T, kMTW) * cdiv(a.SI / kSlice, 2u) < gridDim.x)
-        return 0u;
+    if (!(b.flags & kBatchWideSharedUp)) return 0u;
+    const uint32_t H_ = GLM ? 6144u : a.H, I_ = GLM ? 2048u : a.I, SI_ = GLM ? 2048u : a.SI, K_ = GLM ? 8u : a.K;
+    (void)I_;
+    (void)K_;
     SharedUpW w{a, b};
-    w.H = a.H;
-    w.SI = a.SI;
-    w.nkt = a.H / 32u;
-    w.nsl = a.SI / kSlice;
+    w.H = H_;
+    w.SI = SI_;
+    w.nkt = H_ / 32u;
+    w.nsl = SI_ / kSlice;
     w.npair = cdiv(w.nsl, 2u);
     w.npass = cdiv(b.T, kMTW);
-    w.nst = a.H / kKCW;
+    w.nst = H_ / kKCW;
     const uint32_t U = w.npass * w.npair;
     w.nu = U > blockIdx.x ? cdiv(U - blockIdx.x, gridDim.x) : 0u;
     w.lane = threadIdx.x & 63u;
     w.v = uni(threadIdx.x >> 6);
     w.vbase = 16u * w.lane;
-#pragma unroll
-    for (uint32_t k = 0; k < 4; k++) w.lo[k] = aw_lane_off(4u * k + (w.lane >> 4));
+    w.lob = aw_lane_off(w.lane >> 4);
     run_steps(w);
-    pipeline_drain();
     return U;
 }
+// Routed gate/up in wide passes (an expert of more than kMT tokens): unit
+// (pass of kMTW tokens, slice group sg): wave v owns the tiles of a kMT unit,
+// 8 (kSG sg + i) + v (i < kSG); step s covers columns [128 s, +128): one
+// native gu chunk (tile, s) per tile and the batched scale word of the
+// 256-column step s / 2 (bytes 2i + (s & 1)). A work-group step moves 32 KB of
+// weights and 48 KB of activations for 1536 MFMAs (a kMT unit: 64 + 48 KB),
+// and an expert's weights are read once per 64 of its tokens.
+struct RoutedUpW {
+    using AS = AStreamW;
+    struct WB {
+        u32x4 w[kSG];
+        uint32_t s[2];
+    };
+    static constexpr uint32_t kLoads = kSG + 1u;
+    template <int S>
+    static __device__ __forceinline__ void issue_a(const AStreamW& A, uint32_t s) {
+        aw_issue<S>(A, s * kKCW);
+    }
+    const DecodeArgs& a;
+    const BatchArgs& b;
+    uint32_t H, I, E, K, nkg, S, NSG, nst, nst2, nu, v, lane, uoff;
+    PassTab pt;
+    const uint8_t* const* stab;
+    NativeLayout NL;
+    Cursor ca, cw, cc;
+    rsrc_t wrs;
+    uint32_t wpart, vgu, vgus;
+    uint32_t lob;  // A fragment lane offset of k step 0 (cg = 4g; k step jj: ^ 16 jj)
+    UnitInfo cu;
+    uint32_t cnb;
+    f32x4 acc[kSG][3];
+
+    WL_MEM UnitInfo unit(uint32_t i) const {
+        UnitInfo x{false, false, 0u, 0u, 0u, 0u};
+        if (i >= nu) return x;
+        const uint32_t r = (blockIdx.x + gridDim.x - uoff) % gridDim.x + gridDim.x * i;
+        const PassPart jp = pass_part(r, NSG, pt.nw);
+        const Pass ps = pass_at_w(pt, E, jp.j);
+        x.live = true;
+        x.part = jp.part;
+        x.e = ps.e;
+        x.nt = ps.nt;
+        x.row0 = ps.c0;
+        return x;
+    }
+    WL_MEM void bind_a(uint32_t i, AStreamW& A) const {
+        const UnitInfo x = unit(i);
+        if (!x.live) return aw_bind(A, nullptr, 0u, 0u, 0u, 0u);
+        if (x.e == a.E) aw_bind(A, b.norm3, (uint64_t)b.T * 6u * H, x.row0 - b.T * K, x.nt, H);  // MXFP4 shared
+        else aw_bind(A, b.xperm3, (uint64_t)b.T * K * 6u * H, x.row0, x.nt, H);
+    }
+    WL_MEM void bind_w(uint32_t i) {
+        const UnitInfo x = unit(i);
+        const uint8_t* blk = x.live ? uni_ptr(stab[x.e]) : nullptr;
+        wrs = make_rsrc(blk, blk ? (uint32_t)NL.total : 0u);
+        wpart = x.part;
+    }
+    WL_MEM void issue_w_one(uint32_t s, WB& W, uint32_t j) const {
+        if (j < kSG) {
+            const uint32_t sl = min(wpart * kSG + j, S - 1u);
+            W.w[j] = bld16_nt(wrs, vgu, sl * 8u * nkg * 1024u + s * 1024u);
+        } else {
+            bld8(wrs, vgus, (wpart * 8u * nst2 + s / 2u) * 512u, W.s);
+        }
+    }
+    WL_MEM void begin(uint32_t i) {
+        cu = unit(i);
+        cnb = cdiv(cu.nt, 16u);
+        if (stab[cu.e] == nullptr && threadIdx.x == 0) raise_error(a.sync, SyncMap::make(), E_NOT_RESIDENT, 0u);
+#pragma unroll
+        for (uint32_t t = 0; t < kSG; t++)
+#pragma unroll
+            for (uint32_t tb = 0; tb < 3; tb++) acc[t][tb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    // Iteration it = NH (3 jj + pc) + hp: plane pc of k step jj (columns
+    // 32 g + 8 jj of the step's k tile), token blocks 2 hp and 2 hp + 1,
+    // against the kSG tiles; the next iteration's two fragments are read while
+    // this one's MFMAs run (two at a time: four would not fit beside the 64
+    // accumulator registers).
+    template <uint32_t NB>
+    WL_MEM void comp(uint32_t s, const uint8_t* sl, const WB& W) {
+        constexpr uint32_t NH = (NB + 1u) / 2u, N = 12u * NH;
+        float sc[kSG];
+#pragma unroll
+        for (uint32_t i = 0; i < kSG; i++) sc[i] = e8m0f((W.s[i >> 1] >> (8u * (2u * (i & 1u) + (s & 1u)))) & 0xFFu);
+        auto frag = [&](uint32_t it, uint32_t t2) {
+            const uint32_t kp = it / NH, tb = 2u * (it % NH) + t2;
+            return afragw(sl, kp % 3u, tb < NB ? tb : NB - 1u, lob ^ (16u * (kp / 3u)));
+        };
+        bf16x8 af[2][2], bw[kSG];
+        af[0][0] = frag(0u, 0u);
+        af[0][1] = frag(0u, 1u);
+#pragma unroll
+        for (uint32_t it = 0; it < N; it++) {
+            const uint32_t kp = it / NH, hp = it % NH, jj = kp / 3u, pc = kp % 3u, c = it & 1u;
+            if (it + 1u < N) {
+                af[c ^ 1u][0] = frag(it + 1u, 0u);
+                af[c ^ 1u][1] = frag(it + 1u, 1u);
+            }
+            if (pc == 0u && hp == 0u) {
+#pragma unroll
+                for (uint32_t i = 0; i < kSG; i++) bw[i] = fp4x8_bf16(pinned(W.w[i][jj]), sc[i]);
+            }
+#pragma unroll
+            for (uint32_t i = 0; i < kSG; i++)
+#pragma unroll
+                for (uint32_t t2 = 0; t2 < 2; t2++)
+                    if (2u * hp + t2 < NB) acc[i][2u * hp + t2] = mma(af[c][t2], bw[i], acc[i][2u * hp + t2]);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    WL_MEM void compute(uint32_t s, const uint8_t* sl, const WB& W) {
+        switch (cnb) {
+            case 1: return comp<1>(s, sl, W);
+            case 2: return comp<2>(s, sl, W);
+            default: return comp<3>(s, sl, W);
+        }
+    }
+    WL_MEM void finish() {
+        const uint32_t ln = opaque_lane();
+#pragma unroll
+        for (uint32_t i = 0; i < kSG; i++) {
+            const uint32_t sl = cu.part * kSG + i;
+            if (sl >= S) continue;
+            swiglu_store_w(acc[i], cu.nt, ln, [&](uint32_t m, uint32_t n, float x) {
+                store3(b.mid3 + (size_t)(cu.row0 + m) * 3u * I + sl * kSlice + v * 8u + n, I, x);
+            });
+        }
+    }
+};
+// The wide passes of the routed experts, as one pipeline starting at work-group
+// uoff; returns their unit count.
+template <bool GLM>
+WL_DEV uint32_t run_routed_up_wide(const DecodeArgs& a, const BatchArgs& b, const PassTab& pt,
+                                   const uint8_t* const* stab, uint32_t E, uint32_t uoff) {
+    if (pt.nw == 0u) return 0u;
+    const uint32_t H_ = GLM ? 6144u : a.H, I_ = GLM ? 2048u : a.I, SI_ = GLM ? 2048u : a.SI, K_ = GLM ? 8u : a.K;
+    (void)I_;
+    (void)K_;
+    RoutedUpW w{a, b};
+    w.H = H_;
+    w.I = I_;
+    w.E = E;
+    w.K = K_;
+    w.nkg = H_ / 128u;
+    w.S = I_ / kSlice;
+    w.NSG = cdiv(w.S, kSG);
+    w.nst = w.nkg;
+    w.nst2 = cdiv(H_, kKC);
+    w.uoff = uoff;
+    const uint32_t U = pt.nw * w.NSG, b0 = (blockIdx.x + gridDim.x - uoff) % gridDim.x;
+    w.nu = U > b0 ? cdiv(U - b0, gridDim.x) : 0u;
+    w.lane = threadIdx.x & 63u;
+    w.v = uni(threadIdx.x >> 6);
+    w.pt = pt;
+    w.stab = stab;
+    w.NL = NativeLayout::make(H_, I_);
+    w.vgu = (uint32_t)w.NL.gu + w.v * w.nkg * 1024u + 16u * w.lane;
+    w.vgus = (uint32_t)w.NL.bgus + w.v * w.nst2 * 512u + 8u * w.lane;
+    w.lob = aw_lane_off(4u * (w.lane >> 4));
+    run_steps(w);
+    return U;
+}
+template <bool GLM>
 __global__ void __launch_bounds__(kThreads) bup_kernel(const DecodeArgs* __restrict__ pa, const BatchArgs b) {
     const DecodeArgs& a = *pa;
     extern __shared__ __align__(16) uint8_t dyn[];
@@ -1076,8 +1298,13 @@ __global__ void __launch_bounds__(kThreads) bup_kernel(const DecodeArgs* __restr
     const bool sh4 = (b.flags & kBatchShared4) != 0u;
     const uint32_t E = a.E + (sh4 ? 1u : 0u);  // experts in the pass table
     const uint8_t* const* stab = load_slot_tab(a, a.E, sh4, (const uint8_t**)dyn);
-    const PassTab pt = load_pass_tab(b, E, a.K, (uint32_t*)(dyn + 8u * E), stab);
-    const uint32_t Uw = run_shared_up_wide(a, b);
+    const PassTab pt = load_pass_tab(b, E, a.K, (uint32_t*)(dyn + 8u * E), stab, cdiv(I / kSlice, kSG));
+    // the wide units first (each a pipeline of its own), then the kMT units,
+    // which start on the work-groups after the wide units' last ones
+    const uint32_t Us = run_shared_up_wide<GLM>(a, b);
+    if (Us) pipeline_drain();
+    const uint32_t Ur = run_routed_up_wide<GLM>(a, b, pt, stab, E, Us % gridDim.x);
+    if (Ur) pipeline_drain();
     UpK k{a, b};
     k.H = H;
     k.I = I;
@@ -1089,10 +1316,10 @@ __global__ void __launch_bounds__(kThreads) bup_kernel(const DecodeArgs* __restr
     k.S = I / kSlice;
     k.NSG = cdiv(k.S, kSG);
     k.Ssh = a.SI / kSlice;
-    k.Us = (b.flags & (kBatchNoShared | kBatchShared4)) || Uw ? 0u : cdiv(b.T, kMT) * k.Ssh;
+    k.Us = (b.flags & (kBatchNoShared | kBatchShared4 | kBatchWideSharedUp)) ? 0u : cdiv(b.T, kMT) * k.Ssh;
     k.nst = cdiv(H, kKC);
     const uint32_t U = k.Us + pt.n * k.NSG;
-    k.uoff = Uw % gridDim.x;  // the work-groups after the wide units' last ones start
+    k.uoff = (Us + Ur) % gridDim.x;
     const uint32_t b0 = (blockIdx.x + gridDim.x - k.uoff) % gridDim.x;
     k.nu = U > b0 ? cdiv(U - b0, gridDim.x) : 0u;
     k.lane = threadIdx.x & 63u;
@@ -1337,7 +1564,7 @@ struct SharedDownW {
     Cursor ca, cw, cc;
     rsrc_t wrs;
     uint32_t wvoff[2];
-    uint32_t lo[4];
+    uint32_t lob;  // A fragment lane offset of k step 0 (cg = g; k step k: ^ 64 k)
     uint32_t crb, cnt, crow0, cnb;
     f32x4 d[2][4];
 
@@ -1385,14 +1612,14 @@ struct SharedDownW {
     WL_MEM void comp(const uint8_t* sl, const WBufW& W) {
         bf16x8 af[2][NB];
 #pragma unroll
-        for (uint32_t tb = 0; tb < NB; tb++) af[0][tb] = afragw(sl, 0u, tb, lo[0]);
+        for (uint32_t tb = 0; tb < NB; tb++) af[0][tb] = afragw(sl, 0u, tb, lob);
 #pragma unroll
         for (uint32_t it = 0; it < 12u; it++) {
             const uint32_t k = it / 3u, c = it & 1u;
             if (it + 1u < 12u) {
                 const uint32_t nx = it + 1u;
 #pragma unroll
-                for (uint32_t tb = 0; tb < NB; tb++) af[c ^ 1u][tb] = afragw(sl, nx % 3u, tb, lo[nx / 3u]);
+                for (uint32_t tb = 0; tb < NB; tb++) af[c ^ 1u][tb] = afragw(sl, nx % 3u, tb, lob ^ (64u * (nx / 3u)));
             }
 #pragma unroll
             for (uint32_t t = 0; t < 2; t++) {
@@ -1421,26 +1648,202 @@ struct SharedDownW {
         }
     }
 };
+template <bool GLM>
 WL_DEV uint32_t run_shared_down_wide(const DecodeArgs& a, const BatchArgs& b) {
-    if ((b.flags & (kBatchNoShared | kBatchShared4)) || cdiv(b.T, kMTW) * cdiv(a.H, 256u) < gridDim.x) return 0u;
+    if (!(b.flags & kBatchWideSharedDown)) return 0u;
+    const uint32_t H_ = GLM ? 6144u : a.H, I_ = GLM ? 2048u : a.I, SI_ = GLM ? 2048u : a.SI, K_ = GLM ? 8u : a.K;
+    (void)I_;
+    (void)K_;
     SharedDownW w{a, b};
-    w.H = a.H;
-    w.SI = a.SI;
-    w.nrb = cdiv(a.H, 256u);
+    w.H = H_;
+    w.SI = SI_;
+    w.nrb = cdiv(H_, 256u);
     w.npass = cdiv(b.T, kMTW);
-    w.nst = a.SI / kKCW;
+    w.nst = SI_ / kKCW;
     const uint32_t U = w.npass * w.nrb;
     w.nu = U > blockIdx.x ? cdiv(U - blockIdx.x, gridDim.x) : 0u;
     w.lane = threadIdx.x & 63u;
     w.n = w.lane & 15u;
     w.g = w.lane >> 4;
     w.v = uni(threadIdx.x >> 6);
-#pragma unroll
-    for (uint32_t k = 0; k < 4; k++) w.lo[k] = aw_lane_off(4u * k + w.g);
+    w.lob = aw_lane_off(w.g);
     run_steps(w);
-    pipeline_drain();
     return U;
 }
+// Routed down in wide passes (an expert of more than kMT tokens): unit (pass
+// of kMTW tokens, row block rb): wave v owns row pairs q = 16 rb + 2v + h
+// (h = 0, 1), as in a kMT unit; step st covers columns [128 st, +128) of I:
+// slices sj = 2 st + s4 (s4 = 0, 1), the native dn chunks (sj, q) and the
+// batched scale word of the 256-column step st / 2 (bytes 2 (2 (st & 1) + s4)
+// + h).
+struct RoutedDownW {
+    using AS = AStreamW;
+    struct WB {
+        u32x4 w[4];
+        uint32_t s;  // the step's dword of its scale word
+    };
+    static constexpr uint32_t kLoads = 5;
+    template <int S>
+    static __device__ __forceinline__ void issue_a(const AStreamW& A, uint32_t s) {
+        aw_issue<S>(A, s * kKCW);
+    }
+    const DecodeArgs& a;
+    const BatchArgs& b;
+    uint32_t H, I, E, nq, NS, RBr, nst, nstd, nu, v, lane, n, g, uoff;
+    PassTab pt;
+    const uint8_t* const* stab;
+    NativeLayout NL;
+    Cursor ca, cw, cc;
+    rsrc_t wrs;
+    uint32_t wpart, vdn, vdns;
+    uint32_t lob;  // A fragment lane offset of slice 0, half 0 (cg = 4 (g & 1) + (g >> 1); ^ 16 (8 s4 + 2 f))
+    UnitInfo cu;
+    uint32_t cnb;
+    f32x4 d[2][2][3];  // [row pair h][x rows / y rows][row block tb]
+
+    WL_MEM UnitInfo unit(uint32_t i) const {
+        UnitInfo x{false, false, 0u, 0u, 0u, 0u};
+        if (i >= nu) return x;
+        const uint32_t r = (blockIdx.x + gridDim.x - uoff) % gridDim.x + gridDim.x * i;
+        const PassPart jp = pass_part(r, RBr, pt.nw);
+        const Pass ps = pass_at_w(pt, E, jp.j);
+        x.live = true;
+        x.part = jp.part;
+        x.e = ps.e;
+        x.nt = ps.nt;
+        x.row0 = ps.c0;
+        return x;
+    }
+    WL_MEM void bind_a(uint32_t i, AStreamW& A) const {
+        const UnitInfo x = unit(i);
+        if (!x.live) return aw_bind(A, nullptr, 0u, 0u, 0u, 0u);
+        aw_bind(A, b.mid3, (uint64_t)b.T * (a.K + ((b.flags & kBatchShared4) ? 1u : 0u)) * 6u * I, x.row0, x.nt, I);
+    }
+    WL_MEM void bind_w(uint32_t i) {
+        const UnitInfo x = unit(i);
+        const uint8_t* blk = x.live ? uni_ptr(stab[x.e]) : nullptr;
+        wrs = make_rsrc(blk, blk ? (uint32_t)NL.total : 0u);
+        wpart = x.part;
+    }
+    WL_MEM void issue_w_one(uint32_t st, WB& W, uint32_t j) const {
+        if (j < 4u) {
+            const uint32_t sj = min(2u * st + j / 2u, NS - 1u), q = min(wpart * 16u + 2u * v + j % 2u, nq - 1u);
+            W.w[j] = bld16_nt(wrs, vdn, (sj * nq + q) * 1024u);
+        } else {
+            W.s = __builtin_amdgcn_raw_buffer_load_b32(wrs, (int)vdns, (int)((wpart * 8u * nstd + st / 2u) * 512u + 4u * (st & 1u)), 0);
+        }
+    }
+    WL_MEM void begin(uint32_t i) {
+        cu = unit(i);
+        cnb = cdiv(cu.nt, 16u);
+#pragma unroll
+        for (uint32_t h = 0; h < 2; h++)
+#pragma unroll
+            for (uint32_t xy = 0; xy < 2; xy++)
+#pragma unroll
+                for (uint32_t tb = 0; tb < 3; tb++) d[h][xy][tb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    // Iteration it = 3 NB (2 s4 + f) + 3 tb + pc runs the fragment of plane
+    // pc, block tb at column half f of slice s4 against both row pairs; the
+    // next iteration's fragment is read while this one's four MFMAs run.
+    template <uint32_t NB>
+    WL_MEM void comp(uint32_t st, const uint8_t* sl, const WB& W) {
+        constexpr uint32_t NI = NB * 3u, N = 4u * NI;
+        auto frag = [&](uint32_t it) {
+            const uint32_t o = it / NI, in = it % NI;
+            return afragw(sl, in % 3u, in / 3u, lob ^ (16u * (8u * (o / 2u) + 2u * (o % 2u))));
+        };
+        bf16x8 af[2];
+        af[0] = frag(0u);
+        float scx[2], scy[2];
+        bf16x8 bx[2], by[2];
+#pragma unroll
+        for (uint32_t it = 0; it < N; it++) {
+            const uint32_t o = it / NI, in = it % NI, s4 = o / 2u, f = o % 2u, tb = in / 3u;
+            if (it + 1u < N) af[(it + 1u) % 2u] = frag(it + 1u);
+            if (in == 0u) {
+                if (f == 0u) {
+                    const bool valid = 2u * st + s4 < NS;
+#pragma unroll
+                    for (uint32_t h = 0; h < 2; h++) {
+                        // decoded once, then swapped like the weight dwords
+                        const uint32_t sv = __float_as_uint(e8m0f((W.s >> (8u * (2u * s4 + h))) & 0xFFu));
+                        uint32_t sx, sy;
+                        swap32(sv, sv, sx, sy);
+                        scx[h] = valid ? __uint_as_float(sx) : 0.f;
+                        scy[h] = valid ? __uint_as_float(sy) : 0.f;
+                    }
+                }
+#pragma unroll
+                for (uint32_t h = 0; h < 2; h++) {
+                    const u32x4 w = W.w[2u * s4 + h];
+                    uint32_t x, y;
+                    swap32(pinned(w[2u * f]), w[2u * f + 1u], x, y);
+                    bx[h] = fp4x8_bf16(x, scx[h]);
+                    by[h] = fp4x8_bf16(y, scy[h]);
+                }
+            }
+            const bf16x8 av = af[it % 2u];
+#pragma unroll
+            for (uint32_t h = 0; h < 2; h++) {
+                d[h][0][tb] = mma(av, bx[h], d[h][0][tb]);
+                d[h][1][tb] = mma(av, by[h], d[h][1][tb]);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    WL_MEM void compute(uint32_t st, const uint8_t* sl, const WB& W) {
+        switch (cnb) {
+            case 1: return comp<1>(st, sl, W);
+            case 2: return comp<2>(st, sl, W);
+            default: return comp<3>(st, sl, W);
+        }
+    }
+    WL_MEM void finish() {
+        const uint32_t ln = opaque_lane(), nn = ln & 15u;
+#pragma unroll
+        for (uint32_t h = 0; h < 2; h++) {
+            const uint32_t q = cu.part * 16u + 2u * v + h;
+            if (q >= nq) continue;
+            float* o = b.expout + (size_t)cu.row0 * H + 32u * q + nn;
+            tile_each_w(d[h][0], cu.nt, ln, [&](uint32_t m, float x) { gst(o + (size_t)m * H, x); });
+            tile_each_w(d[h][1], cu.nt, ln, [&](uint32_t m, float x) { gst(o + (size_t)m * H + 16u, x); });
+        }
+    }
+};
+template <bool GLM>
+WL_DEV uint32_t run_routed_down_wide(const DecodeArgs& a, const BatchArgs& b, const PassTab& pt,
+                                     const uint8_t* const* stab, uint32_t E, uint32_t uoff) {
+    if (pt.nw == 0u) return 0u;
+    const uint32_t H_ = GLM ? 6144u : a.H, I_ = GLM ? 2048u : a.I, SI_ = GLM ? 2048u : a.SI, K_ = GLM ? 8u : a.K;
+    (void)I_;
+    (void)K_;
+    RoutedDownW w{a, b};
+    w.H = H_;
+    w.I = I_;
+    w.E = E;
+    w.nq = H_ / 32u;
+    w.NS = I_ / kSlice;
+    w.RBr = cdiv(w.nq, 16u);
+    w.nst = I_ / kKCW;
+    w.nstd = cdiv(I_, kKC);
+    w.uoff = uoff;
+    const uint32_t U = pt.nw * w.RBr, b0 = (blockIdx.x + gridDim.x - uoff) % gridDim.x;
+    w.nu = U > b0 ? cdiv(U - b0, gridDim.x) : 0u;
+    w.lane = threadIdx.x & 63u;
+    w.n = w.lane & 15u;
+    w.g = w.lane >> 4;
+    w.v = uni(threadIdx.x >> 6);
+    w.pt = pt;
+    w.stab = stab;
+    w.NL = NativeLayout::make(H_, I_);
+    w.vdn = (uint32_t)w.NL.dn + 16u * w.lane;
+    w.vdns = (uint32_t)w.NL.bdns + w.v * w.nstd * 512u + 8u * w.lane;
+    w.lob = aw_lane_off(4u * (w.g & 1u) + (w.g >> 1));
+    run_steps(w);
+    return U;
+}
+template <bool GLM>
 __global__ void __launch_bounds__(kThreads) bdown_kernel(const DecodeArgs* __restrict__ pa, const BatchArgs b) {
     const DecodeArgs& a = *pa;
     extern __shared__ __align__(16) uint8_t dyn[];
@@ -1448,8 +1851,11 @@ __global__ void __launch_bounds__(kThreads) bdown_kernel(const DecodeArgs* __res
     const bool sh4 = (b.flags & kBatchShared4) != 0u;
     const uint32_t E = a.E + (sh4 ? 1u : 0u);  // experts in the pass table
     const uint8_t* const* stab = load_slot_tab(a, a.E, sh4, (const uint8_t**)dyn);
-    const PassTab pt = load_pass_tab(b, E, a.K, (uint32_t*)(dyn + 8u * E), stab);
-    const uint32_t Uw = run_shared_down_wide(a, b);
+    const PassTab pt = load_pass_tab(b, E, a.K, (uint32_t*)(dyn + 8u * E), stab, cdiv(H / 32u, 16u));
+    const uint32_t Us = run_shared_down_wide<GLM>(a, b);
+    if (Us) pipeline_drain();
+    const uint32_t Ur = run_routed_down_wide<GLM>(a, b, pt, stab, E, Us % gridDim.x);
+    if (Ur) pipeline_drain();
     DownK k{a, b};
     k.H = H;
     k.I = I;
@@ -1460,10 +1866,10 @@ __global__ void __launch_bounds__(kThreads) bdown_kernel(const DecodeArgs* __res
     k.nks = a.SI / 32u;
     k.RBs = cdiv(H, 128u);
     k.RBr = cdiv(k.nq, 16u);
-    k.Us = (b.flags & (kBatchNoShared | kBatchShared4)) || Uw ? 0u : cdiv(b.T, kMT) * k.RBs;
+    k.Us = (b.flags & (kBatchNoShared | kBatchShared4 | kBatchWideSharedDown)) ? 0u : cdiv(b.T, kMT) * k.RBs;
     k.nst = cdiv(max(I, a.SI), kKC);  // the shorter kind's extra steps are masked
     const uint32_t U = k.Us + pt.n * k.RBr;
-    k.uoff = Uw % gridDim.x;  // the work-groups after the wide units' last ones start
+    k.uoff = (Us + Ur) % gridDim.x;
     const uint32_t b0 = (blockIdx.x + gridDim.x - k.uoff) % gridDim.x;
     k.nu = U > b0 ? cdiv(U - b0, gridDim.x) : 0u;
     k.lane = threadIdx.x & 63u;
@@ -1528,14 +1934,17 @@ uint32_t batched_max_experts() {
 
 int launch_batched(const DecodeArgs* d_args, const BatchArgs& b, uint32_t H, uint32_t I, uint32_t SI, uint32_t E,
                    uint32_t K, uint32_t n_cu, uint32_t phases, void* stream) {
-    (void)I;
-    (void)SI;
     hipStream_t s = (hipStream_t)stream;
     hipError_t e;
     const size_t topk_lds = 4u * (2u * E + 64u);
     const size_t gemm_lds = gemm_tab_bytes(E);
+    // the GEMM kernels' wide units take their shape parameters as constants
+    // at the GLM shape
+    const bool glm = H == 6144u && I == 2048u && SI == 2048u && K == 8u;
+    const void* up = glm ? (const void*)bup_kernel<true> : (const void*)bup_kernel<false>;
+    const void* down = glm ? (const void*)bdown_kernel<true> : (const void*)bdown_kernel<false>;
     const struct { const void* fn; size_t lds; } attrs[] = {
-        {(const void*)btopk_kernel, topk_lds}, {(const void*)bup_kernel, gemm_lds}, {(const void*)bdown_kernel, gemm_lds}};
+        {(const void*)btopk_kernel, topk_lds}, {up, gemm_lds}, {down, gemm_lds}};
     for (const auto& at : attrs)
         if ((e = hipFuncSetAttribute(at.fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)at.lds)) != hipSuccess)
             return (int)e;
@@ -1561,8 +1970,19 @@ int launch_batched(const DecodeArgs* d_args, const BatchArgs& b, uint32_t H, uin
         hipLaunchKernelGGL(bpermute_kernel, dim3(std::min((nperm + 255u) / 256u, 8u * n_cu)), dim3(256), 0, s, b, H, K);
     }
     if (phases & kPhaseGemm) {
-        hipLaunchKernelGGL(bup_kernel, dim3(resident((const void*)bup_kernel)), dim3(kThreads), gemm_lds, s, d_args, b);
-        hipLaunchKernelGGL(bdown_kernel, dim3(resident((const void*)bdown_kernel)), dim3(kThreads), gemm_lds, s, d_args, b);
+        // the shared expert's wide units when they fill the grid
+        BatchArgs bw = b;
+        const uint32_t gu = resident(up), gd = resident(down);
+        const bool bf16_sh = !(b.flags & (kBatchNoShared | kBatchShared4));
+        if (bf16_sh && (b.T + kMTW - 1u) / kMTW * ((SI / kSlice + 1u) / 2u) >= gu) bw.flags |= kBatchWideSharedUp;
+        if (bf16_sh && (b.T + kMTW - 1u) / kMTW * ((H + 255u) / 256u) >= gd) bw.flags |= kBatchWideSharedDown;
+        if (glm) {
+            hipLaunchKernelGGL(bup_kernel<true>, dim3(gu), dim3(kThreads), gemm_lds, s, d_args, bw);
+            hipLaunchKernelGGL(bdown_kernel<true>, dim3(gd), dim3(kThreads), gemm_lds, s, d_args, bw);
+        } else {
+            hipLaunchKernelGGL(bup_kernel<false>, dim3(gu), dim3(kThreads), gemm_lds, s, d_args, bw);
+            hipLaunchKernelGGL(bdown_kernel<false>, dim3(gd), dim3(kThreads), gemm_lds, s, d_args, bw);
+        }
     }
     if (phases & kPhaseCombine)
         hipLaunchKernelGGL(bcomb_kernel, dim3((H + 1023) / 1024, b.T), dim3(256), 0, s, b, H, K);
