@@ -135,10 +135,12 @@ wl_status wl_set_layer_dense(wl_ctx* ctx, uint32_t layer, const uint16_t* d_post
  * round-trip (src/glm_layer_runner.cuh:393-396) is needed when every expert
  * of the layer is bound.
  *
- * Bound blocks are in the NATIVE layout (wl_native_block_bytes bytes): the
- * same bytes as the reference's packed block, reordered so that each 16-byte
- * load of a GPU wave is one lane of a contiguous 1 KB chunk and the E8M0
- * scales of 16 k tiles of one lane are one 16-byte chunk. Convert a
+ * Bound blocks are in the NATIVE layout (wl_native_block_bytes bytes,
+ * 21,233,664 at the GLM shape): the same bytes as the reference's packed
+ * block, reordered so that each 16-byte load of a GPU wave is one lane of a
+ * contiguous 1 KB chunk and the E8M0 scales of 16 k tiles of one lane are
+ * one 16-byte chunk, plus a second copy of the scales in the batched
+ * kernels' order (one 8-byte word per lane and step). Convert a
  * reference-layout block with wl_expert_to_native (the conversion the
  * reference's loader would run when it fills a VRAM slot,
  * src/glm_expert_cache.cuh:394-433). */

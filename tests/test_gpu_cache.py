@@ -33,6 +33,13 @@ class _MappedSource:
         return self.base.get(*self.key(layer, expert))
 
 
+def _decode_bytes(cfg):
+    """The first regions of a native block (gu, gus, dn, dns): what a decode
+    call's cache miss copies."""
+    from oracle import native_layout
+    return sum(native_layout.native_sizes(cfg.hidden, cfg.moe_inter)[:4])
+
+
 def _pair(c, seed, L, capacity, n_host):
     zipf = synthdata.zipf_bias_offset(c["n_routed_experts"], seed)
     cm = CachedModel(c, seed=seed, n_layers=L, capacity=capacity, n_host=n_host, bias_offset=zipf)
@@ -69,7 +76,8 @@ def test_cached_layers_equal_resident_and_counters_match_replay(gpu):
     _, hits, misses, ev = OL.replay(20, keys, K)
     print(f"cache: {st}", flush=True)
     assert (st["hits"], st["misses"], st["evictions"]) == (hits, misses, ev)
-    assert st["used"] == 20 and st["bytes_h2d"] == misses * cm.nb
+    # a decode miss copies the decode kernel's regions of the native block only
+    assert st["used"] == 20 and st["bytes_h2d"] == misses * _decode_bytes(cm.cfg)
     cm.close()
     rm.close()
 

@@ -31,6 +31,13 @@ class _MappedSource:
         return self.base.get(*self.key(layer, expert))
 
 
+def _decode_bytes(cfg):
+    """The first regions of a native block (gu, gus, dn, dns): what a decode
+    call's cache miss copies."""
+    from oracle import native_layout
+    return sum(native_layout.native_sizes(cfg.hidden, cfg.moe_inter)[:4])
+
+
 def test_config4_scale_cached_equals_resident_and_counters_match_replay(gpu):
     hip = gpu
     H, E, K = GLM["hidden"], GLM["n_routed_experts"], GLM["n_experts_per_tok"]
@@ -69,6 +76,7 @@ def test_config4_scale_cached_equals_resident_and_counters_match_replay(gpu):
     print(f"cache: {st}", flush=True)
     assert len(set(keys)) > SLOTS  # the run evicted
     assert (st["hits"], st["misses"], st["evictions"]) == (hits, misses, ev)
-    assert st["used"] == SLOTS and st["bytes_h2d"] == misses * cm.nb
+    # a decode miss copies the decode kernel's regions of the native block only
+    assert st["used"] == SLOTS and st["bytes_h2d"] == misses * _decode_bytes(cm.cfg)
     cm.close()
     rm.close()

@@ -54,6 +54,12 @@ struct CacheState {
     std::vector<hipEvent_t> slot_ev;  // per slot: the last copy into it
     std::vector<uint8_t> has_ev;      // slot_ev recorded at least once
     std::vector<uint8_t> spec;        // filled by a speculative copy, not yet requested
+    // Decode calls read only a native block's decode regions (its first
+    // decode_bytes); while prefix_only is set (the decode path's own fetches)
+    // a miss copies just those and marks the slot partial; any other use of
+    // a partial slot copies the rest first.
+    std::vector<uint8_t> partial;
+    bool prefix_only = false;
     hipEvent_t gate = nullptr;        // compute-stream point that copies into reused slots wait for
     hipEvent_t cur_gate = nullptr;    // the gate recorded by the last real resolve (gate, or a ring entry)
     bool gate_recorded = false;
@@ -97,6 +103,7 @@ struct wl_ctx {
     wl_moe_config cfg{};
     wl_expert_layout lay{};
     size_t native_bytes = 0;
+    size_t decode_bytes = 0;  // the decode kernel's regions of a native block (its first bytes)
     uint32_t SI = 0;
     int device = 0;
     int n_cu = 0;
@@ -299,6 +306,7 @@ wl_status wl_create(const wl_moe_config* cfg, wl_ctx** out) {
     c->SI = cfg->moe_inter * cfg->n_shared;
     wl_expert_layout_of(cfg, 0, &c->lay);
     c->native_bytes = wl::NativeLayout::make(cfg->hidden, cfg->moe_inter).total;
+    c->decode_bytes = wl::NativeLayout::make(cfg->hidden, cfg->moe_inter).bgus;
     hipError_t e = hipGetDevice(&c->device);
     if (e != hipSuccess) { delete c; return WL_ERR_HIP; }
     hipDeviceProp_t prop;
@@ -665,6 +673,22 @@ static wl_status cache_resolve(wl_ctx* c, uint32_t layer, const int32_t* ids, ui
                 C.spec_hits++;
                 C.spec[r.slot] = 0;
             }
+            if (C.partial[r.slot] && !C.prefix_only && !speculative) {  // the rest of the block
+                const uint8_t* src = C.fn(C.user, layer, (uint32_t)ids[k]);
+                if (!src) return fail(c, WL_ERR_IO, "no host block for layer %u expert %d", layer, ids[k]);
+                hipStream_t cs = C.copy[C.next_copy++ & 1u];
+                const size_t db = c->decode_bytes;
+                if (C.gate_recorded && (e = hipStreamWaitEvent(cs, C.cur_gate, 0)) != hipSuccess)
+                    return hip_fail(c, e, "copy gate");
+                if (C.has_ev[r.slot] && (e = hipStreamWaitEvent(cs, C.slot_ev[r.slot], 0)) != hipSuccess)
+                    return hip_fail(c, e, "slot order");
+                if ((e = hipMemcpyAsync(dst + db, src + db, nb - db, hipMemcpyHostToDevice, cs)) != hipSuccess)
+                    return hip_fail(c, e, "expert copy");
+                if ((e = hipEventRecord(C.slot_ev[r.slot], cs)) != hipSuccess) return hip_fail(c, e, "copy event");
+                C.has_ev[r.slot] = 1;
+                C.partial[r.slot] = 0;
+                C.bytes_h2d += nb - db;
+            }
         } else if (C.files) {
             // a read still pending on this slot (its key was evicted before it
             // was waited for) lands first
@@ -696,6 +720,7 @@ static wl_status cache_resolve(wl_ctx* c, uint32_t layer, const int32_t* ids, ui
             }
             C.task_of[r.slot] = t;
             C.raw[r.slot] = 1;
+            C.partial[r.slot] = 0;  // the conversion writes the whole native block
             C.has_ev[r.slot] = 1;
             C.spec[r.slot] = speculative ? 1 : 0;
             C.bytes_h2d += C.files->ref_bytes();
@@ -710,12 +735,15 @@ static wl_status cache_resolve(wl_ctx* c, uint32_t layer, const int32_t* ids, ui
             if (C.gate_recorded && (e = hipStreamWaitEvent(cs, C.cur_gate, 0)) != hipSuccess) return hip_fail(c, e, "copy gate");
             if (C.has_ev[r.slot] && (e = hipStreamWaitEvent(cs, C.slot_ev[r.slot], 0)) != hipSuccess)
                 return hip_fail(c, e, "slot order");
-            if ((e = hipMemcpyAsync(dst, src, nb, hipMemcpyHostToDevice, cs)) != hipSuccess)
+            const bool part = C.prefix_only || speculative;  // speculation runs for decode only
+            const size_t n_copy = part ? c->decode_bytes : nb;
+            if ((e = hipMemcpyAsync(dst, src, n_copy, hipMemcpyHostToDevice, cs)) != hipSuccess)
                 return hip_fail(c, e, "expert copy");
             if ((e = hipEventRecord(C.slot_ev[r.slot], cs)) != hipSuccess) return hip_fail(c, e, "copy event");
             C.has_ev[r.slot] = 1;
             C.spec[r.slot] = speculative ? 1 : 0;
-            C.bytes_h2d += nb;
+            C.partial[r.slot] = part ? 1 : 0;
+            C.bytes_h2d += n_copy;
             if (speculative) C.spec_copies++;
         }
         // (file reads: the stream waits in wl_cache_get, once the read is issued)
@@ -823,6 +851,12 @@ static wl_status source_prepare(wl_ctx* c, uint32_t layer, const float* d_hidden
         return hip_fail(c, e, "routing read-back");
     if ((uint32_t)pin[PinMap::abort] == route_epoch)
         return fail(c, WL_ERR_DEVICE, "the routing kernel of layer %u reported an error (see wl_check_error)", layer);
+    // the built-in cache copies only the decode regions of a missing block
+    struct PrefixOnly {
+        CacheState& C;
+        PrefixOnly(CacheState& cs, bool on) : C(cs) { C.prefix_only = on; }
+        ~PrefixOnly() { C.prefix_only = false; }
+    } prefix_only(c->cache, c->src_cache);
     wl_status st = source_prefetch(c, layer, pin + PinMap::ids, K, s);
     if (st != WL_OK) return st;
     const uint8_t* ptrs[WL_MAX_TOPK];
@@ -1395,6 +1429,7 @@ static wl_status cache_init(wl_ctx* c, uint32_t capacity) {
         if ((e = hipEventCreateWithFlags(&ev, hipEventDisableTiming)) != hipSuccess) return hip_fail(c, e, "slot event");
     C.has_ev.assign(nslots, 0);
     C.spec.assign(nslots, 0);
+    C.partial.assign(nslots, 0);
     C.task_of.assign(nslots, nullptr);
     C.raw.assign(nslots, 0);
     C.blk.resize(nslots);
@@ -1621,6 +1656,7 @@ wl_status wl_cache_set_policy(wl_ctx* c, const wl_cache_policy* policy) {
     for (uint32_t k : C.pinned) C.lru->pin(k, true);
     C.policy = *policy;
     std::fill(C.spec.begin(), C.spec.end(), 0);
+    std::fill(C.partial.begin(), C.partial.end(), 0);
     std::fill(C.raw.begin(), C.raw.end(), 0);  // the keys are gone; a slot is read again before it is handed out
     C.resolved.clear();
     C.spec_pending = false;
