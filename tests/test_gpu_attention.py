@@ -227,7 +227,8 @@ def test_errors(gpu):
         moe.Attention(moe.make_attn_config(n_heads=24))
 
 
-@pytest.mark.parametrize("N,K", [(48, 256), (2048, 6144), (6144, 16384), (100, 24), (16384, 2048)])
+@pytest.mark.parametrize("N,K", [(48, 256), (2048, 6144), (6144, 16384), (100, 24), (16384, 2048), (1, 8), (7, 520),
+                                 (3000, 1032), (65536, 64)])
 def test_matvec_bf16(gpu, N, K):
     """wl_matvec_bf16 against an fp64 product of the same bf16 weights and f32
     input, within 1e-5 term-relative (the reference's matvec test bar,

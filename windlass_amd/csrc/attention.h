@@ -14,9 +14,12 @@ namespace attn {
 // makes x the RMSNorm of x over its K columns (x * (1/sqrt(mean(x^2) + eps))
 // * norm_w, norm_w bf16 [K]); x2 != null makes x silu(x) * x2 (SwiGLU).
 // x_out (optional, written by the job's first work-group): the transformed x.
-// y_raw (optional): W . x without add.
+// y_raw (optional): W . x without add. W2 (optional, bf16, the shape of W):
+// a paired product, y[r] = silu(W[r] . x) * (W2[r] . x) (a SwiGLU's gate and
+// up rows in one job; streaming kernel only).
 struct GemvJob {
     const void* W;
+    const void* W2;
     const float* x;
     const float* x2;
     const uint16_t* norm_w;
@@ -31,6 +34,7 @@ struct GemvJob {
     uint32_t tpr_log2;  // threads per row: 1 << tpr_log2 (<= 256), each 8 columns per step
     uint32_t wg0;       // first work-group of this job in the launch
     uint32_t rows_wg;   // rows per work-group: kGemvRows x (256 >> tpr_log2)
+    uint32_t nwg;       // streaming kernel: work-groups of this job (its rows split evenly over them)
 };
 constexpr int kMaxJobs = 4;
 #ifndef WL_GEMV_ROWS
@@ -87,7 +91,11 @@ struct AttnPtrs {
     float* ctx;            // [HN][L]
 };
 
+// Runs the jobs of l: on the streaming kernel when every job fits it (a
+// paired job must), else on the row-group kernel with n_wg work-groups.
 int launch_gemv(const GemvLaunch& l, uint32_t n_wg, void* stream);
+// Whether every job of l fits the streaming kernel.
+bool sgemv_fits(const GemvLaunch& l);
 // A dense SwiGLU MLP layer (the dense branch of run_moe,
 // src/glm_layer_runner.cuh:373-384): post_ln [H] bf16, gate / up [DI, H],
 // down [H, DI] bf16 row-major.

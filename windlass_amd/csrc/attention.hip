@@ -273,10 +273,12 @@ WL_DEV void rope(const float* in, uint32_t istride, float* out, uint32_t ostride
 
 static_assert(kGemvThreads == 256, "the prep and GEMV bodies share a launch of 256-thread work-groups");
 // Work-group blk (0: the KV rows, 1: the indexer key row) of the prep stage.
-WL_DEV void prep_body(const Shape& s, const AttnPtrs& p, uint32_t pos, uint32_t blk) {
-    __shared__ float red[4];
-    __shared__ float kbuf[1024];
-    __shared__ float cs[512];
+// LDS: kPrepLds floats (red [4] | kbuf [1024] | cs [512]).
+constexpr uint32_t kPrepLds = 4 + 1024 + 512;
+WL_DEV void prep_body(const Shape& s, const AttnPtrs& p, uint32_t pos, uint32_t blk, float* lds) {
+    float* red = lds;
+    float* kbuf = lds + 4;
+    float* cs = lds + 4 + 1024;
     const uint32_t tid = threadIdx.x;
     rope_table(cs, s.RP, pos, s.theta);
     __syncthreads();
@@ -314,8 +316,283 @@ WL_DEV void prep_body(const Shape& s, const AttnPtrs& p, uint32_t pos, uint32_t 
 // the same earlier stage only), so the prep needs no launch of its own.
 __global__ __launch_bounds__(kGemvThreads) void gemv_prep_kernel(GemvLaunch L, uint32_t n_gemv, Shape s, AttnPtrs p,
                                                                  uint32_t pos) {
+    __shared__ float lds[kPrepLds];
     if (blockIdx.x < n_gemv) gemv_body(L, blockIdx.x);
-    else prep_body(s, p, pos, blockIdx.x - n_gemv);
+    else prep_body(s, p, pos, blockIdx.x - n_gemv, lds);
+}
+
+// ---- streaming GEMV ------------------------------------------------------------
+// Work-group b of a job takes rows [rs, re) of an even split of the job's N
+// rows over its nwg work-groups. It stages its input once in LDS (DMA,
+// zero-padded to whole units, RMSNorm applied there), and runs its rows as one
+// flat sequence of 1 KB weight units (row vr, unit c: 512 bf16 or 256 f32
+// columns) split evenly over its four waves. A wave streams its units in
+// batches of kSgNB non-temporal 16-byte loads per lane, two batches in flight,
+// and sums a row's products in two f32 accumulators per lane; at a row change
+// the wave's sum goes to LDS slot [row][wave], and the four slots of a row are
+// added in wave order at the end. The weights of a work-group's first two
+// batches are requested right after its input DMAs, so both arrive while the
+// input is normalised. A paired job (W2) runs the rows of W, then those of W2,
+// and writes silu(W x) * (W2 x).
+#ifndef WL_SG_NB
+#define WL_SG_NB 4
+#endif
+constexpr uint32_t kSgNB = WL_SG_NB;  // 1 KB units per batch
+
+struct SgWG {
+    const uint8_t *w1, *w2;  // weight bytes of row wr0 (W, W2)
+    uint32_t wbytes;         // resource size: the rows [wr0, wr(re - 1)] of W
+    uint32_t rs, R, K, esz, epu, nL, Kp;
+    uint32_t G, GS, OFF, wr0, g0;
+};
+struct SgCursor {  // wave-uniform
+    uint32_t u, vr, c, roff;
+    uint32_t rr, gi;  // the row's index in its group, its group - g0
+};
+
+WL_DEV uint32_t sg_wrow(const SgWG& g, uint32_t r) { return g.GS ? (r / g.G) * g.GS + g.OFF + r % g.G : r; }
+WL_DEV void sg_row_start(const SgWG& g, SgCursor& cu) {
+    const uint32_t r = g.rs + (cu.vr < g.R ? cu.vr : cu.vr - g.R);
+    cu.roff = (sg_wrow(g, r) - g.wr0) * g.K * g.esz;
+    cu.rr = g.GS ? r % g.G : 0u;
+    cu.gi = g.GS ? r / g.G - g.g0 : 0u;
+}
+WL_DEV void sg_start(const SgWG& g, SgCursor& cu, uint32_t u) {
+    cu.u = u;
+    cu.vr = u / g.nL;
+    cu.c = u - cu.vr * g.nL;
+    sg_row_start(g, cu);
+}
+// The next unit; the next row without a division, except where a paired
+// job's W2 rows begin.
+WL_DEV void sg_next(const SgWG& g, SgCursor& cu) {
+    cu.u++;
+    if (++cu.c == g.nL) {
+        cu.c = 0;
+        if (++cu.vr == g.R) {
+            sg_row_start(g, cu);
+        } else {
+            cu.roff += g.K * g.esz;
+            if (g.GS && ++cu.rr == g.G) {
+                cu.rr = 0;
+                cu.gi++;
+                cu.roff += (g.GS - g.G) * g.K * g.esz;
+            }
+        }
+    }
+}
+// The load of the cursor's unit (lanes past K, and units past u1, read zeros
+// without a memory access).
+WL_DEV u32x4 sg_load(const SgWG& g, const SgCursor& cu, uint32_t u1, uint32_t lane) {
+    const uint32_t left = (g.K - cu.c * g.epu) * g.esz;  // bytes of the row from this unit on
+    const bool ok = cu.u < u1 && 16u * lane < left;
+    const rsrc_t r = make_rsrc(cu.vr < g.R ? g.w1 : g.w2, g.wbytes);
+    return bld16_nt(r, ok ? 16u * lane : kOOB, cu.roff + cu.c * 1024u);
+}
+template <int CTRL, int ROWS>
+WL_DEV float sum_step(float x) {
+    return x + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, ROWS, 0xF, false));
+}
+// Sum over the 64 lanes, returned uniform (DPP quad permutes, row shifts and
+// row broadcasts leave it in lane 63).
+WL_DEV float wave_sum(float x) {
+    x = sum_step<0xB1, 0xF>(x);   // quad_perm [1,0,3,2]
+    x = sum_step<0x4E, 0xF>(x);   // quad_perm [2,3,0,1]
+    x = sum_step<0x114, 0xF>(x);  // row_shr:4
+    x = sum_step<0x118, 0xF>(x);  // row_shr:8
+    x = sum_step<0x142, 0xA>(x);  // row_bcast:15
+    x = sum_step<0x143, 0xC>(x);  // row_bcast:31
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 63));
+}
+
+struct SgBatch {
+    u32x4 w[kSgNB];
+};
+WL_DEV void sg_issue(const SgWG& g, SgCursor& ci, uint32_t u1, SgBatch& X) {
+    const uint32_t lane = threadIdx.x & 63u;
+#pragma unroll
+    for (uint32_t i = 0; i < kSgNB; i++) {
+        X.w[i] = sg_load(g, ci, u1, lane);
+        sg_next(g, ci);
+    }
+}
+// The wave's units [u0, u1) of a work-group whose weights are ESZ-byte values;
+// batches A and B (the first two) are already issued, ci is two batches on.
+template <uint32_t NW, uint32_t ESZ>
+WL_DEV void sg_stream(const SgWG& g, uint32_t u0, uint32_t u1, SgCursor& ci, SgBatch& A, SgBatch& B,
+                      const float* xs, float* part) {
+    const uint32_t lane = threadIdx.x & 63u, v = uni(threadIdx.x >> 6);
+    SgCursor cc;
+    sg_start(g, cc, u0);
+    float a0 = 0.f, a1 = 0.f;
+    uint32_t cur = cc.vr, xoff = cc.gi * g.Kp;
+    auto flush = [&]() {
+        const float s = wave_sum(a0 + a1);
+        if (lane == 0) part[cur * NW + v] = s;
+        a0 = 0.f;
+        a1 = 0.f;
+    };
+    auto consume = [&](uint32_t, const SgBatch& X) {
+#pragma unroll
+        for (uint32_t i = 0; i < kSgNB; i++) {
+            if (cc.u < u1) {
+                if (cc.vr != cur) {
+                    flush();
+                    cur = cc.vr;
+                    xoff = cc.gi * g.Kp;
+                }
+                const u32x4 w = X.w[i];
+                if (ESZ == 2u) {
+                    const float* xp = xs + xoff + cc.c * 512u + 8u * lane;
+                    const f32x4 x0 = *(const f32x4*)xp, x1 = *(const f32x4*)(xp + 4);
+                    a0 += bf2f(w[0] & 0xFFFFu) * x0[0];
+                    a1 += bf2f(w[0] >> 16) * x0[1];
+                    a0 += bf2f(w[1] & 0xFFFFu) * x0[2];
+                    a1 += bf2f(w[1] >> 16) * x0[3];
+                    a0 += bf2f(w[2] & 0xFFFFu) * x1[0];
+                    a1 += bf2f(w[2] >> 16) * x1[1];
+                    a0 += bf2f(w[3] & 0xFFFFu) * x1[2];
+                    a1 += bf2f(w[3] >> 16) * x1[3];
+                } else {
+                    const f32x4 x0 = *(const f32x4*)(xs + xoff + cc.c * 256u + 4u * lane);
+                    a0 += __uint_as_float(w[0]) * x0[0];
+                    a1 += __uint_as_float(w[1]) * x0[1];
+                    a0 += __uint_as_float(w[2]) * x0[2];
+                    a1 += __uint_as_float(w[3]) * x0[3];
+                }
+            }
+            sg_next(g, cc);
+        }
+    };
+    auto issue = [&](uint32_t, SgBatch& X) { sg_issue(g, ci, u1, X); };
+    pingpong(at_least2(cdiv(u1 - u0, kSgNB)), A, B, issue, consume);
+    if (u1 > u0) flush();
+}
+
+// Work-group b (< the launch's GEMV work-groups) of a streaming launch.
+template <uint32_t NW>
+WL_DEV void sgemv_body(const GemvLaunch& L, uint32_t b, float* lds) {
+    GemvJob j = L.job[0];
+    if (L.n_jobs > 3 && b >= L.job[3].wg0) j = L.job[3];
+    else if (L.n_jobs > 2 && b >= L.job[2].wg0) j = L.job[2];
+    else if (L.n_jobs > 1 && b >= L.job[1].wg0) j = L.job[1];
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, v = uni(tid >> 6);
+    const uint32_t bj = b - j.wg0;
+    SgWG g;
+    g.rs = (uint32_t)((uint64_t)j.N * bj / j.nwg);
+    const uint32_t re = (uint32_t)((uint64_t)j.N * (bj + 1u) / j.nwg);
+    g.R = re - g.rs;
+    g.K = j.K;
+    g.esz = j.f32w ? 4u : 2u;
+    g.epu = 1024u / g.esz;
+    g.nL = cdiv(g.K, g.epu);
+    g.Kp = g.nL * g.epu;
+    g.G = j.G;
+    g.GS = j.GS;
+    g.OFF = j.OFF;
+    g.wr0 = sg_wrow(g, g.rs);
+    g.g0 = j.GS ? g.rs / j.G : 0u;
+    const uint32_t ng = j.GS ? (re - 1u) / j.G - g.g0 + 1u : 1u;
+    g.wbytes = (sg_wrow(g, re - 1u) - g.wr0 + 1u) * g.K * g.esz;
+    g.w1 = (const uint8_t*)j.W + (size_t)g.wr0 * g.K * g.esz;
+    g.w2 = j.W2 ? (const uint8_t*)j.W2 + (size_t)g.wr0 * g.K * g.esz : g.w1;
+    const uint32_t VR = j.W2 ? 2u * g.R : g.R;
+    // LDS: x [ng][Kp] f32 | norm weights (bf16, whole 1 KB units) | part [VR][4] | red [4]
+    float* xs = lds;
+    uint16_t* nw = (uint16_t*)(xs + (size_t)ng * g.Kp);
+    float* part = (float*)(nw + (j.norm_w ? cdiv(g.Kp, 512u) * 512u : 0u));
+    float* red = part + VR * NW;
+
+    // 1. input DMAs: group gi's x (f32, K columns, then zeros to Kp), the norm weights
+    {
+        const float* xb = j.x + (size_t)g.g0 * j.XS;
+        const rsrc_t xr = make_rsrc(xb, ((ng - 1u) * j.XS + g.K) * 4u);
+        const uint32_t cpg = g.Kp / 256u, nch = ng * cpg;
+        for (uint32_t ci = v; ci < nch; ci += NW) {
+            const uint32_t gi = ci / cpg, col = (ci - gi * cpg) * 256u + 4u * lane;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (__attribute__((address_space(3))) void*)(xs + ci * 256u), 16u,
+                                                     col < g.K ? (gi * j.XS + col) * 4u : kOOB, 0, 0, 0);
+        }
+        if (j.norm_w) {
+            const rsrc_t nr = make_rsrc(j.norm_w, g.K * 2u);
+            const uint32_t nchw = cdiv(g.Kp, 512u);
+            for (uint32_t ci = v; ci < nchw; ci += NW) {
+                const uint32_t col = ci * 512u + 8u * lane;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(nr, (__attribute__((address_space(3))) void*)(nw + ci * 512u),
+                                                         16u, col < g.K ? col * 2u : kOOB, 0, 0, 0);
+            }
+        }
+    }
+    // 2. the wave's units and its first two batches
+    const uint32_t n = VR * g.nL;
+    const uint32_t u0 = (uint32_t)((uint64_t)n * v / NW), u1 = (uint32_t)((uint64_t)n * (v + 1u) / NW);
+    SgCursor ci;  // the issue cursor
+    sg_start(g, ci, u0);
+    SgBatch A, B;
+    sg_issue(g, ci, u1, A);
+    sg_issue(g, ci, u1, B);
+    for (uint32_t i = tid; i < VR * NW; i += 64u * NW) part[i] = 0.f;
+    // 3. the input in LDS (the 2 kSgNB weight loads issued after the DMAs may
+    // stay in flight), then RMSNorm in place
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt((2u * kSgNB & 15u) | (((2u * kSgNB) >> 4) << 14) | 0x0F70u);
+    lds_barrier();
+    const uint32_t nx = ng * g.Kp;
+    if (j.norm_w) {  // ungrouped (ng = 1)
+        float ss = 0.f;
+        for (uint32_t k = 4u * tid; k < nx; k += 256u * NW) {
+            const f32x4 a = *(const f32x4*)(xs + k);
+            ss += a[0] * a[0] + a[1] * a[1] + a[2] * a[2] + a[3] * a[3];
+        }
+        ss = wave_sum(ss);
+        if (lane == 0) red[v] = ss;
+        lds_barrier();
+        float t = 0.f;
+#pragma unroll
+        for (uint32_t w = 0; w < NW; w++) t += red[w];
+        const float rsn = 1.0f / sqrtf(t / (float)g.K + j.eps);
+        for (uint32_t k = 4u * tid; k < nx; k += 256u * NW) {
+            f32x4 a = *(const f32x4*)(xs + k);
+            const uint2 wb = *(const uint2*)(nw + k);
+            a[0] = bf2f(wb.x & 0xFFFFu) * (a[0] * rsn);
+            a[1] = bf2f(wb.x >> 16) * (a[1] * rsn);
+            a[2] = bf2f(wb.y & 0xFFFFu) * (a[2] * rsn);
+            a[3] = bf2f(wb.y >> 16) * (a[3] * rsn);
+            *(f32x4*)(xs + k) = a;
+        }
+        lds_barrier();
+    }
+    if (j.x_out && bj == 0u)
+        for (uint32_t k = 4u * tid; k < g.K; k += 256u * NW) *(f32x4*)(j.x_out + k) = *(const f32x4*)(xs + k);
+    // 4. the stream
+    if (g.esz == 2u) sg_stream<NW, 2>(g, u0, u1, ci, A, B, xs, part);
+    else sg_stream<NW, 4>(g, u0, u1, ci, A, B, xs, part);
+    lds_barrier();
+    // 5. each row: its four wave slots in order (+ add)
+    for (uint32_t t = tid; t < g.R; t += 64u * NW) {
+        float y = 0.f;
+#pragma unroll
+        for (uint32_t w = 0; w < NW; w++) y += part[t * NW + w];
+        if (j.W2) {
+            float y2 = 0.f;
+#pragma unroll
+            for (uint32_t w = 0; w < NW; w++) y2 += part[(g.R + t) * NW + w];
+            y = silu(y) * y2;
+        }
+        const uint32_t row = g.rs + t;
+        if (j.y_raw) j.y_raw[row] = y;
+        j.y[row] = (j.add ? j.add[row] : 0.f) + y;
+    }
+}
+
+// Four waves per work-group, two work-groups per CU at the GLM shapes (one
+// eight-wave work-group per CU, staging the input once per CU, measured within
+// 1 % of it on every attention and MLP shape). Work-groups past n_gemv run
+// the prep stage.
+__global__ __launch_bounds__(256) void sgemv_kernel(GemvLaunch L, uint32_t n_gemv, Shape s, AttnPtrs p, uint32_t pos) {
+    extern __shared__ __align__(16) float sg_lds[];
+    if (blockIdx.x < n_gemv) sgemv_body<4>(L, blockIdx.x, sg_lds);
+    else prep_body(s, p, pos, blockIdx.x - n_gemv, sg_lds);
 }
 
 // q_abs[h][c] = sum_{d < NP} q[h][d] * kv_b[h (NP + VD) + d][c]: work-group
@@ -867,9 +1144,85 @@ uint32_t gemv_plan(GemvJob& j) {
     return (j.N + j.rows_wg - 1) / j.rows_wg;
 }
 
-int launch_gemv(const GemvLaunch& l, uint32_t n_wg, void* stream) {
-    hipLaunchKernelGGL(gemv_kernel, dim3(n_wg), dim3(kGemvThreads), 0, (hipStream_t)stream, l);
+#ifndef WL_SG_WGS
+#define WL_SG_WGS 512
+#endif
+constexpr uint32_t kSgTarget = WL_SG_WGS;  // work-groups of a streaming launch (two per CU at the GLM shapes)
+constexpr size_t kSgMaxLds = 160u * 1024u;  // dynamic LDS
+
+// Rows shorter than this run on the row-group kernel (measured on MI355X,
+// 16384 x 512: 7.2 us there against 7.6 for the streaming kernel, whose
+// staging of the input is one more round trip before the first product).
+constexpr uint32_t kSgMinK = 1024;
+// Streaming plan of l: every job's work-groups (in proportion to its weight
+// bytes, at least one, at most one per row) and the launch's dynamic LDS.
+// Returns the work-group count, 0 when a job does not fit the kernel (an x2
+// input, an LDS or resource size past its limits).
+uint32_t sgemv_plan(GemvLaunch& l, size_t& lds, uint32_t target, uint32_t nw) {
+    double total = 0;
+    for (uint32_t i = 0; i < l.n_jobs; i++) {
+        const GemvJob& j = l.job[i];
+        const uint32_t epu = j.f32w ? 256u : 512u;
+        total += (double)j.N * (j.W2 ? 2 : 1) * ((j.K + epu - 1) / epu);
+    }
+    uint32_t wg = 0;
+    lds = 0;
+    for (uint32_t i = 0; i < l.n_jobs; i++) {
+        GemvJob& j = l.job[i];
+        if (j.x2 || (j.W2 && (j.f32w || j.GS))) return 0;
+        if (!j.W2 && j.K < kSgMinK) return 0;
+        const uint32_t esz = j.f32w ? 4u : 2u, epu = 1024u / esz, nL = (j.K + epu - 1) / epu, Kp = nL * epu;
+        const double units = (double)j.N * (j.W2 ? 2 : 1) * nL;
+        uint32_t nwg = (uint32_t)(target * units / total + 0.5);
+        nwg = nwg < 1u ? 1u : nwg > j.N ? j.N : nwg;
+        const uint32_t R = (j.N + nwg - 1) / nwg;
+        const uint32_t ng = j.GS ? std::min((j.N + j.G - 1) / j.G, (R + j.G - 1) / j.G + 1u) : 1u;
+        if (j.norm_w && j.GS) return 0;
+        const size_t need = (size_t)ng * Kp * 4 + (j.norm_w ? (size_t)(Kp + 511) / 512 * 1024 : 0) +
+                            (size_t)(j.W2 ? 2 : 1) * R * nw * 4 + nw * 4;
+        const uint64_t span = (uint64_t)(j.GS ? ng * j.GS : R) * j.K * esz;
+        if (need > kSgMaxLds || span >= (1ull << 31) || (uint64_t)((ng - 1) * j.XS + j.K) * 4 >= (1ull << 31)) return 0;
+        lds = std::max(lds, need);
+        j.wg0 = wg;
+        j.nwg = nwg;
+        wg += nwg;
+    }
+    return wg;
+}
+
+int launch_sgemv(const GemvLaunch& l0, uint32_t n_wg, const Shape* s, const AttnPtrs* p, uint32_t pos,
+                 uint32_t n_prep, void* stream) {
+    GemvLaunch l = l0;
+    size_t lds = 0;
+    const uint32_t ns = sgemv_plan(l, lds, kSgTarget, 4);
+    if (ns == 0) {
+        if (n_prep) {
+            hipLaunchKernelGGL(gemv_prep_kernel, dim3(n_wg + n_prep), dim3(kGemvThreads), 0, (hipStream_t)stream, l0,
+                               n_wg, *s, *p, pos);
+        } else {
+            hipLaunchKernelGGL(gemv_kernel, dim3(n_wg), dim3(kGemvThreads), 0, (hipStream_t)stream, l0);
+        }
+        return (int)hipGetLastError();
+    }
+    hipError_t ae = hipFuncSetAttribute((const void*)sgemv_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                        (int)kSgMaxLds);
+    if (ae != hipSuccess) return (int)ae;
+    const Shape s0{};
+    const AttnPtrs p0{};
+    if (n_prep) lds = std::max(lds, (size_t)kPrepLds * 4);
+    hipLaunchKernelGGL(sgemv_kernel, dim3(ns + n_prep), dim3(256), lds, (hipStream_t)stream, l, ns, s ? *s : s0,
+                       p ? *p : p0, pos);
     return (int)hipGetLastError();
+}
+
+int launch_gemv(const GemvLaunch& l, uint32_t n_wg, void* stream) {
+    return launch_sgemv(l, n_wg, nullptr, nullptr, 0u, 0u, stream);
+}
+
+bool sgemv_fits(const GemvLaunch& l0) {
+    GemvLaunch l = l0;
+    size_t lds = 0;
+    return sgemv_plan(l, lds, kSgTarget, 4) != 0;
 }
 
 // Dynamic LDS of the index scores: q [IH][ID + 4], w [IH], k [kIdxKeys][ID + 4], RoPE table [RP].
@@ -879,9 +1232,7 @@ size_t index_score_lds(const Shape& s) {
 
 int launch_gemv_prep(const GemvLaunch& l, uint32_t n_wg, const Shape& s, const AttnPtrs& p, uint32_t pos, bool owner,
                      void* stream) {
-    hipLaunchKernelGGL(gemv_prep_kernel, dim3(n_wg + (owner ? 2u : 1u)), dim3(kGemvThreads), 0, (hipStream_t)stream, l,
-                       n_wg, s, p, pos);
-    return (int)hipGetLastError();
+    return launch_sgemv(l, n_wg, &s, &p, pos, owner ? 2u : 1u, stream);
 }
 
 int launch_attn_absorb(const Shape& s, const AttnPtrs& p, bool owner, uint32_t T, void* stream) {

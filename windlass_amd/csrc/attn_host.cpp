@@ -154,6 +154,23 @@ int launch_dense_mlp(const DenseMlp& m, const float* x, const float* add, float*
     j.norm_w = m.post_ln;
     j.eps = m.eps;
     j.x_out = x_norm;
+    {  // streaming kernel: gate and up rows as one paired job, g = silu(gate x') * up x'
+        GemvLaunch lp{};
+        uint32_t np = 0;
+        auto jp = j;
+        jp.W2 = m.up;
+        add_job(lp, np, jp);
+        GemvLaunch d{};
+        uint32_t nd = 0;
+        auto jd = job(m.down, g, y, m.H, m.DI);
+        jd.add = add;
+        jd.y_raw = y_raw;
+        add_job(d, nd, jd);
+        if (sgemv_fits(lp) && sgemv_fits(d)) {
+            int e = launch_gemv(lp, np, stream);
+            return e != 0 ? e : launch_gemv(d, nd, stream);
+        }
+    }
     add_job(l, n, j);
     j = job(m.up, x, u, m.DI, m.H);
     j.norm_w = m.post_ln;
