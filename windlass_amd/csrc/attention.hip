@@ -1090,12 +1090,25 @@ __global__ __launch_bounds__(kSplitThreads) void attn_split_kernel(Shape s, Attn
 }
 
 // ctx[h] = sum_s e^(m_s - M) ctx_s[h] / sum_s e^(m_s - M) l_s, M = max_s m_s:
-// work-group (head, 256 columns); the split weights once into LDS.
+// work-group (head, 64 columns); thread (column c, quarter q) sums the splits
+// q, q + 4, ... (all of its loads issued together, beside the split weights'
+// loads; S <= 64), and the four quarter sums of a column are added in order.
+constexpr uint32_t kCombCols = 64;
 __global__ __launch_bounds__(256) void attn_combine_kernel(Shape s, AttnPtrs p, uint32_t S) {
     __shared__ float w[64];
+    __shared__ float red[4][kCombCols];
     __shared__ float zz;
-    const uint32_t h = blockIdx.x / ((s.L + 255) / 256), c = (blockIdx.x % ((s.L + 255) / 256)) * 256 + threadIdx.x;
-    const uint32_t tid = threadIdx.x;
+    const uint32_t nb = (s.L + kCombCols - 1) / kCombCols;
+    const uint32_t h = blockIdx.x / nb, tid = threadIdx.x, cq = tid % kCombCols, q = tid / kCombCols;
+    const uint32_t c = (blockIdx.x % nb) * kCombCols + cq;
+    const bool col_ok = c < s.L;
+    float v[16];
+    const float* src = p.part_ctx + (size_t)h * s.L + (col_ok ? c : 0u);
+#pragma unroll
+    for (uint32_t i = 0; i < 16; i++) {
+        const uint32_t sp = q + 4u * i;
+        v[i] = sp < S ? src[(size_t)sp * s.HN * s.L] : 0.f;
+    }
     if (tid < 64) {
         const float m = tid < S ? p.part_m[(size_t)tid * s.HN + h] : -INFINITY;
         float M = m;
@@ -1107,13 +1120,12 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(Shape s, AttnPtrs p, 
         if (tid == 0) zz = z;
     }
     __syncthreads();
-    if (c < s.L) {
-        float t = 0.f;
-        const float* src = p.part_ctx + (size_t)h * s.L + c;
-#pragma unroll 8
-        for (uint32_t i = 0; i < S; i++) t += w[i] * src[(size_t)i * s.HN * s.L];
-        p.ctx[(size_t)h * s.L + c] = t / zz;
-    }
+    float t = 0.f;
+#pragma unroll
+    for (uint32_t i = 0; i < 16; i++) t += w[(q + 4u * i) & 63u] * v[i];
+    red[q][cq] = t;
+    __syncthreads();
+    if (q == 0 && col_ok) p.ctx[(size_t)h * s.L + c] = (((red[0][cq] + red[1][cq]) + red[2][cq]) + red[3][cq]) / zz;
 }
 
 }  // namespace
@@ -1291,8 +1303,8 @@ int launch_attn_core(const Shape& s, const AttnPtrs& p0, uint32_t T, uint32_t sp
                        (hipStream_t)stream, s, p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return (int)e;
-    hipLaunchKernelGGL(attn_combine_kernel, dim3(s.HN * ((s.L + 255) / 256)), dim3(256), 0, (hipStream_t)stream, s, p,
-                       S);
+    hipLaunchKernelGGL(attn_combine_kernel, dim3(s.HN * ((s.L + kCombCols - 1) / kCombCols)), dim3(256), 0,
+                       (hipStream_t)stream, s, p, S);
     return (int)hipGetLastError();
 }
 
