@@ -671,6 +671,9 @@ def main():
                     help="layer: config 1 (default); chain: config 2, 24 layers per step; "
                          "batched: config 3, --tokens positions per step; cache: config 4, 75 cache-backed layers per step")
     ap.add_argument("--tokens", type=int, default=256, help="batched workload: positions per layer call")
+    ap.add_argument("--noalloc", action="store_true",
+                    help="batched workload: through wl_run_moe_batched_noalloc (static scratch, token chunks of its "
+                         "capacity) instead of wl_run_moe_batched")
     ap.add_argument("--chain-layers", type=int, default=24)
     ap.add_argument("--cache-layers", type=int, default=75)
     ap.add_argument("--cache-slots", type=int, default=3094)
@@ -778,7 +781,10 @@ def main():
 
     def step(i):
         if batched:
-            dm.ctx.run_moe_batched(0, T, d_hb.ptr, None, d_ob.ptr, stream.handle)
+            if args.noalloc:
+                dm.ctx.run_moe_batched_noalloc(0, T, d_hb.ptr, None, d_ob.ptr, stream.handle)
+            else:
+                dm.ctx.run_moe_batched(0, T, d_hb.ptr, None, d_ob.ptr, stream.handle)
             return
         if chain:  # one token: its own start state, then h <- h + moe(h) through every layer
             hip.copy_d2d(d_h.ptr, d_hs.ptr + 4 * H * (i % n_h), 4 * H, stream.handle)
@@ -919,7 +925,8 @@ def main():
                   "mxfp4/bf16 weights, f32 activations and accumulation (bf16 MFMA on three exact bf16 pieces "
                   "of each f32 activation)"),
         "data": "synthetic",
-        "config": {"workload": (f"config3: one GLM MoE layer over {args.tokens} tokens (batched)" if batched else
+        "config": {"workload": (f"config3: one GLM MoE layer over {args.tokens} tokens (batched"
+                                f"{', allocation-free entry point' if args.noalloc else ''})" if batched else
                                 f"config4: {args.layers} GLM MoE layers behind a {args.cache_slots}-slot HBM expert "
                                 f"cache, misses from pinned host memory, bs=1" if cache else
                                 f"config2: chain of {args.layers} resident GLM MoE decode layers, bs=1, "
