@@ -165,6 +165,45 @@ def test_schedules_identical_and_stable(gpu, glm_model):
     assert np.array_equal(outs[0], outs[1]) and np.array_equal(outs[0], outs[2])
 
 
+def test_two_level_combine(gpu, glm_model):
+    """WL_DECODE_XL2=1: the partials are summed per XCD through that XCD's L2
+    first (plain stores, non-temporal loads), then over the 8 XCDs. Checked
+    against the oracle under both schedules (which must agree bit for bit)
+    and against the default one-level combine (a different summation order:
+    within the bar, not bit-equal)."""
+    hip = gpu
+    H = GLM["hidden"]
+    os.environ["WL_DECODE_XL2"] = "1"
+    try:
+        dm = DeviceModel(GLM, seed=1, n_layers=1)
+    finally:
+        del os.environ["WL_DECODE_XL2"]
+    try:
+        for step in range(3):
+            h = synth.hidden_state(H, 100 + step)
+            ref = O.moe_layer(h, dm.dense[0], O.ExpertSource(H, GLM["moe_inter"], dm.seed), 0, GLM)
+            outs = []
+            for sched in [moe.SCHED_FUSED, moe.SCHED_PHASED]:
+                dm.ctx.set_schedule(sched)
+                dh, dout = make_io(H)
+                dh.upload(h)
+                dm.ctx.run_moe(0, dh.ptr, dout.ptr)
+                dm.ctx.check_error()
+                outs.append(dout.download(np.float32))
+                r = _check_layer(ref, _taps(dm, hip), outs[-1], f"xl2 step{step} sched{sched}")
+            assert np.array_equal(outs[0], outs[1]), step
+            dh, dout = make_io(H)
+            dh.upload(h)
+            glm_model.ctx.run_moe(0, dh.ptr, dout.ptr)
+            glm_model.ctx.check_error()
+            one = dout.download(np.float32)
+            d = O.rel_to_scale(one, outs[0])
+            assert d < TOL, d
+            print(f"two-level combine step {step}: out rel_to_scale {r:.3e}, vs one-level {d:.3e}", flush=True)
+    finally:
+        dm.close()
+
+
 def _small():
     fx = np.load(os.path.join(GOLD, "moe_tf_small.npz"))
     return fx, json.loads(str(fx["config"])), [int(s) for s in fx["seeds"]]

@@ -25,8 +25,10 @@ COMMON = ["-O3", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-function", "-Wno-u
 
 
 def build(verbose: bool = False) -> str:
-    objs = []
-    for src in SOURCES:
+    """Compiles every source (in parallel, one hipcc per source), then links."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    def compile_one(src):
         path = os.path.join(CSRC, src)
         obj = os.path.join(CSRC, "_build", src + ".o")
         os.makedirs(os.path.dirname(obj), exist_ok=True)
@@ -39,7 +41,11 @@ def build(verbose: bool = False) -> str:
         if r.returncode != 0:
             sys.stderr.write(r.stdout + r.stderr)
             raise RuntimeError(f"hipcc failed on {src}")
-        objs.append(obj)
+        return obj
+
+    jobs = max(1, min(len(SOURCES), int(os.environ.get("MAX_JOBS", os.cpu_count() or 1))))
+    with ThreadPoolExecutor(max_workers=jobs) as pool:
+        objs = list(pool.map(compile_one, SOURCES))
     tmp = LIB + ".tmp"
     cmd = [HIPCC] + DEVICE_FLAGS + ["-shared", "-fPIC", "-o", tmp] + objs
     r = subprocess.run(cmd, capture_output=True, text=True)

@@ -36,6 +36,7 @@ constexpr uint32_t kLineWords = 32;
 enum : uint32_t {
     E_SPIN = 1u,          // a wait for another work-group's data exceeded its bound
     E_NOT_RESIDENT = 2u,  // a routed expert resolved to a null block
+    E_XCD = 4u,           // two-level combine: a work-group ran on another XCD than w mod 8
 };
 
 // Word offsets inside the uncached synchronisation block.
@@ -74,6 +75,11 @@ struct SyncMap {
 //                    (tickets in the order work-groups finish their own work)
 //                    combines blocks t, t + G, ...
 constexpr uint32_t kRowBlock = 32;  // rows per combine block (= rows per down item)
+// Words of each partial-sum array (part, tsh): [H/32][G][32] for the
+// one-level combine; the two-level combine uses the same H x G words as
+// [8 XCDs][H/32][G/8][32] and the 8 x H words after them as [H/32][8][32]
+// (each XCD's sum of its work-groups' partials).
+__host__ __device__ inline size_t part_words(uint32_t H, uint32_t G) { return (size_t)H * (G + 8u); }
 struct Plan {
     uint32_t G, S, U, NB;
     __host__ __device__ static Plan make(uint32_t H, uint32_t I, uint32_t SI, uint32_t K, uint32_t G) {
@@ -142,6 +148,8 @@ struct DecodeDyn {
     __host__ __device__ uint32_t seg_hi() const { return (seg >> 8) & 0xFFu; }
     __host__ __device__ int32_t taps() const { return (int32_t)((seg >> 16) & 1u); }
     __host__ __device__ uint32_t ptag() const { return (seg >> 24) & 3u; }
+    // bit 17: the two-level combine (partials summed per XCD through its L2 first)
+    __host__ __device__ bool xl2() const { return ((seg >> 17) & 1u) != 0u; }
 };
 // Dwords of kernel arguments the decode kernel preloads into SGPRs (the
 // record pointer, then hidden .. epoch).
@@ -167,6 +175,9 @@ struct LdsMap {
         m.pv = o;   // normalised input; this work-group's partial; combine staging
         uint32_t f32n = (p.G + 16u) * kRowBlock;
         if (f32n < H) f32n = H;
+        // the two-level combine stages all first-level blocks of a work-group
+        // at once: at most (H/32 + G/8) x 32 words
+        if (f32n < H + 4u * p.G) f32n = H + 4u * p.G;
         o += al(f32n * 4u);
         m.bytes = o;
         return m;
@@ -305,6 +316,9 @@ struct BatchArgs {
 int launch_decode(const DecodeArgs* d_args, const DecodeDyn& dyn, uint32_t H, uint32_t I, uint32_t SI,
                   uint32_t E, uint32_t K, uint32_t grid, bool sh4, void* stream);
 int decode_max_lds();
+// Whether work-group w of a grid-sized launch runs on XCD w mod 8 (every
+// work-group's XCC_ID register read back): *ok. Returns a hipError_t.
+int probe_xcd_map(uint32_t grid, bool* ok);
 // Work-groups of the decode / routing kernel one CU can hold at once
 // (hipOccupancyMaxActiveBlocksPerMultiprocessor at the kernel's LDS size).
 int decode_occupancy(uint32_t H, uint32_t I, uint32_t SI, uint32_t E, uint32_t K, uint32_t grid, int* per_cu);

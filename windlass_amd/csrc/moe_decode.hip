@@ -55,6 +55,7 @@
 // their contribution masked), so the compiler's wait counts stay exact.
 #include <hip/hip_runtime.h>
 #include <algorithm>
+#include <vector>
 #include "dev_common.h"
 #include "internal.h"
 
@@ -62,11 +63,15 @@ namespace wl {
 
 // Diagnostic builds (-DWL_TIMELINE) record a 100 MHz timestamp per work-group
 // at each phase boundary; product builds compile WL_TL to nothing.
+// A kernel names its record slot tl_slot (the decode kernel: its call's epoch
+// mod kTlCalls), so back-to-back calls keep their own records.
 #ifdef WL_TIMELINE
-__device__ uint64_t g_tl[kMaxGrid * 16];
+constexpr uint32_t kTlCalls = 64;
+__device__ uint64_t g_tl[kTlCalls * kMaxGrid * 16];
 #define WL_TL(i)                                                                                  \
     do {                                                                                          \
-        if (threadIdx.x == 0) g_tl[(size_t)blockIdx.x * 16 + (i)] = __builtin_amdgcn_s_memrealtime(); \
+        if (threadIdx.x == 0)                                                                     \
+            g_tl[((size_t)tl_slot * kMaxGrid + blockIdx.x) * 16 + (i)] = __builtin_amdgcn_s_memrealtime(); \
     } while (0)
 #else
 #define WL_TL(i) \
@@ -92,6 +97,21 @@ WL_DEV void st_part(uint32_t* p, uint32_t tag, float x) {
                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// The same tagged word for the first level of the two-level combine: a plain
+// store, which stays in the writer's XCD L2. The XCD's other work-groups read
+// it there with non-temporal loads (which never return a line kept in the
+// reader's L1). Measured on MI355X while 240 MB stream: 8 MB of agent-scope
+// (write-through) 4-byte stores cost 6.1 us, plain ones 1.7 us.
+WL_DEV void st_l1(uint32_t* p, uint32_t tag, float x) {
+    *(__attribute__((address_space(1))) uint32_t*)p = ((__float_as_uint(x) + 2u) & ~3u) | tag;
+}
+// This work-group's XCD (hardware register XCC_ID).
+WL_DEV uint32_t xcc_id() {
+    uint32_t x;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID, 0, 4)" : "=s"(x));
+    return x;
+}
+
 // ---- the decode kernel -------------------------------------------------------
 // GLM = true compiles the GLM shape (H 6144, I 2048, SI 2048, E 256, K 8) with
 // every shape constant known; GLM = false reads the shapes from the record.
@@ -106,6 +126,9 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const float* hidden, const 
                   const float* bias, const uint8_t* const* slot_tab, const float* resid, float* out) {
     const DecodeArgs& a = *pa;
     const DecodeDyn d{hidden, sh_native, router_w, ln_w, lslot, seg, epoch, bias, slot_tab, resid, out};
+#ifdef WL_TIMELINE
+    const uint32_t tl_slot = epoch % kTlCalls;
+#endif
     const uint32_t H = GLM ? 6144u : a.H, I = GLM ? 2048u : a.I, SI = GLM ? 2048u : a.SI,
                    E = GLM ? 256u : a.E, K = GLM ? 8u : a.K;
     const uint32_t G = gridDim.x, w = blockIdx.x, tid = threadIdx.x;
@@ -128,6 +151,16 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const float* hidden, const 
     const uint8_t** tk_blk = (const uint8_t**)(lds + L.slots);
     uint32_t* misc = (uint32_t*)(lds + L.misc);  // [0..8) vote flags, [8] barrier flag
     float* smf = (float*)(misc + 16);           // [8] this tile's shared SwiGLU values
+    // Two-level combine: work-group w writes its partial rows into slot w/8
+    // of XCD w mod 8's region ([8][H/32][G/8][32] words), which only that
+    // XCD's work-groups read. Work-groups are dispatched to the XCDs round
+    // robin; one that finds itself elsewhere raises E_XCD (checked below).
+    const bool xl2 = d.xl2();
+    // row r of block b of this work-group's partial: word b * pstride + r of
+    // a partial array (one-level: slot w of [H/32][G][32]; two-level: slot
+    // w/8 of XCD w mod 8's [H/32][G/8][32])
+    const uint32_t pstride = (xl2 ? G >> 3 : G) * kRowBlock;
+    const uint32_t pbase = (xl2 ? ((w & 7u) * P.NB * (G >> 3) + (w >> 3)) : w) * kRowBlock;
     // the next call's combine-ticket counter starts at zero: cleared first
     // thing by the launch that holds the combine (the counter was last used
     // two calls back, which has ended)
@@ -283,6 +316,7 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const float* hidden, const 
         const uint32_t tile0 = tile_of(0);
         sg_issue(tile0, 0, sA);
         sg_issue(tile0, 1, sB);
+        if (xl2 && tid == 0 && xcc_id() != (w & 7u)) raise_error(a.sync, SM, E_XCD, d.epoch);
 
         // RMSNorm: w * (x * (1/sqrt(mean(x^2) + eps))) in fp32
         // (tools/ref_glm_chain.py:63-80; src/glm_primitives.cuh:35-62)
@@ -375,11 +409,15 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const float* hidden, const 
             return true;
         };
 
-        // pv -> rows [32b, 32b+32) into block b, slot w of dst ([H/32][G][32]),
-        // tagged with this call's tag (each thread stores the rows it wrote)
+        // pv -> rows [32b, 32b+32) into block b, slot w of dst ([H/32][G][32];
+        // two-level: slot w/8 of XCD w mod 8's block b), tagged with this
+        // call's tag (each thread stores the rows it wrote)
         auto publish = [&](uint32_t* dst) {
-            for (uint32_t r = tid; r < H; r += kThreads)
-                st_part(dst + ((size_t)(r / kRowBlock) * G + w) * kRowBlock + r % kRowBlock, d.ptag(), pv[r]);
+            for (uint32_t r = tid; r < H; r += kThreads) {
+                uint32_t* const p = dst + pbase + (size_t)(r / kRowBlock) * pstride + r % kRowBlock;
+                if (xl2) st_l1(p, d.ptag(), pv[r]);
+                else st_part(p, d.ptag(), pv[r]);
+            }
         };
         // A work-group that leaves an aborted call still writes its words (pv
         // as it stands), so the arrays keep holding one call's tags.
@@ -504,6 +542,7 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const float* hidden, const 
         // items publish the partial rows directly
         const bool direct = P.U <= G && w < P.U;
         rsrc_t r_rs = make_rsrc(d.router_w, 16u);  // rebound per unit
+        const rsrc_t prs = make_rsrc(a.part, (uint32_t)(4u * part_words(H, G)));  // the partials (16-byte stores)
         uint32_t gu_voff = 0, gus_voff = 0, dn_voff = 0, dns_voff = 0;
         // Native block: the gate/up items of this wave are 1 KB chunks
         // [tile*(H/128) + kt], the down items [slice*(H/32) + q]; one 16-byte
@@ -588,13 +627,25 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const float* hidden, const 
                     d1 = mma(A1, fp4x8_bf16(y23, scy), d1);
                     const float s0 = sum3(d0);
                     const float s1 = __shfl(sum3(d1), (lane - 16u) & 63u, 64);
-                    // rows [32q, 32q+32): this unit's weighted contribution; with
-                    // one unit per work-group the rows are final and go straight
-                    // to block q of the partials
-                    if (valid && lane < 32) {
-                        const float x = pv[q * 32u + lane] + wk * (lane < 16 ? s0 : s1);
-                        if (direct) st_part(a.part + ((size_t)q * G + w) * kRowBlock + lane, d.ptag(), x);
-                        else pv[q * 32u + lane] = x;
+                    // rows [32q, 32q+32): this unit's weighted contribution
+                    if (valid && lane < 32) pv[q * 32u + lane] += wk * (lane < 16 ? s0 : s1);
+                }
+                if (direct) {
+                    // with one unit per work-group the batch's rows are final:
+                    // each lane publishes 4 consecutive rows of them with one
+                    // 16-byte store (a wave's LDS accesses complete in order).
+                    // Measured while 240 MB stream: 16-byte agent-scope stores
+                    // cost a third as much per byte as 4-byte ones.
+                    asm volatile("" ::: "memory");
+                    const uint32_t mq = m0 + lane / 8u, q = v * dq_per + mq, c4 = 4u * (lane % 8u);
+                    if (mq < dq_per && q < nq) {
+                        const float4 x4 = *(const float4*)(pv + 32u * q + c4);
+                        const uint32_t tag = d.ptag();
+                        const u32x4 t4 = {((__float_as_uint(x4.x) + 2u) & ~3u) | tag, ((__float_as_uint(x4.y) + 2u) & ~3u) | tag,
+                                          ((__float_as_uint(x4.z) + 2u) & ~3u) | tag, ((__float_as_uint(x4.w) + 2u) & ~3u) | tag};
+                        const int off = (int)(4u * (pbase + q * pstride + c4));
+                        if (xl2) __builtin_amdgcn_raw_buffer_store_b128(t4, prs, off, 0, 0);
+                        else __builtin_amdgcn_raw_buffer_store_b128(t4, prs, off, 0, kSC1);
                     }
                 }
             }
@@ -646,27 +697,34 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const float* hidden, const 
     // out[r] = sum over work-groups of their partials (fixed order), + resid.
     if (d.seg_hi() >= 1u) {
         constexpr uint32_t RB = kRowBlock;
+        const uint32_t Gx = G >> 3, xw = w & 7u, iw = w >> 3;
         float* fin = pv;                   // [G][32]
         float* f2 = fin + (size_t)G * RB;  // [16][32]
-        // sum of the G slots of block blkr of src; the result is in threads
-        // 0..31. Each thread reads 16-byte chunks (four tagged words) of the
-        // block with agent-scope loads: all at once first, then, for chunks
-        // whose writers have not finished (an older call's tag), again until
-        // this call's tag shows (bounded; the error word ends the wait too).
-        auto block_total = [&](const uint32_t* src, uint32_t blkr) -> float {
-            const uint32_t nchunk = G * RB / 4u, tag = d.ptag();
-            const rsrc_t rs = make_rsrc(src + (size_t)blkr * G * RB, G * RB * 4u);
+        // Stages n 16-byte chunks (four tagged words each) into fin (chunk c
+        // at fin + 4c): chunk c is read from byte offset off(c) of resource rs
+        // with cache policy aux. All of a thread's chunks are issued at once;
+        // a chunk whose words do not all carry this call's tag (their writers
+        // have not finished: an older call's tag) is read again, all of a
+        // thread's stale chunks in flight together, until the tag shows
+        // (bounded; the error word ends the wait too). Ends with a barrier.
+        auto gather = [&](rsrc_t rs, uint32_t n, auto off, int aux) {
+            const uint32_t tag = d.ptag();
             constexpr uint32_t kGrp = 4;
-            for (uint32_t c0 = 0; c0 < nchunk; c0 += kThreads * kGrp) {
+            auto ld = [&](uint32_t ch) -> u32x4 {
+                const uint32_t o = ch < n ? off(ch) : kOOB;
+                return aux == kNT ? __builtin_amdgcn_raw_buffer_load_b128(rs, (int)o, 0, kNT)
+                                  : __builtin_amdgcn_raw_buffer_load_b128(rs, (int)o, 0, kSC1);
+            };
+            for (uint32_t c0 = 0; c0 < n; c0 += kThreads * kGrp) {
                 u32x4 q[kGrp];
 #pragma unroll
-                for (uint32_t i = 0; i < kGrp; i++) q[i] = bld16_ag(rs, 16u * (c0 + tid + kThreads * i), 0u);
+                for (uint32_t i = 0; i < kGrp; i++) q[i] = ld(c0 + tid + kThreads * i);
                 uint32_t stale = 0;  // bit i: chunk i still holds an older call's tag
                 for (uint32_t spins = 0;; spins++) {
 #pragma unroll
                     for (uint32_t i = 0; i < kGrp; i++) {
                         const uint32_t ch = c0 + tid + kThreads * i;
-                        const bool mine = ch < nchunk && (spins == 0 || ((stale >> i) & 1u));
+                        const bool mine = ch < n && (spins == 0 || ((stale >> i) & 1u));
                         if (!mine) continue;
                         if (((q[i].x & 3u) == tag) & ((q[i].y & 3u) == tag) & ((q[i].z & 3u) == tag) &
                             ((q[i].w & 3u) == tag)) {
@@ -686,10 +744,16 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const float* hidden, const 
                     __builtin_amdgcn_s_sleep(2);
 #pragma unroll
                     for (uint32_t i = 0; i < kGrp; i++)  // every stale chunk again, all in flight together
-                        if ((stale >> i) & 1u) q[i] = bld16_ag(rs, 16u * (c0 + tid + kThreads * i), 0u);
+                        if ((stale >> i) & 1u) q[i] = ld(c0 + tid + kThreads * i);
                 }
             }
             lds_barrier();
+        };
+        // one-level: sum of the G slots of block blkr of src ([H/32][G][32]);
+        // the result is in threads 0..31
+        auto block_total = [&](const uint32_t* src, uint32_t blkr) -> float {
+            gather(make_rsrc(src + (size_t)blkr * G * RB, G * RB * 4u), G * RB / 4u,
+                   [](uint32_t ch) { return 16u * ch; }, kSC1);
             {  // 16 groups of work-groups, then the 16 group sums
                 const uint32_t rr = tid % RB, grp = tid / RB;
                 float sum = 0.f;
@@ -705,6 +769,43 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const float* hidden, const 
             lds_barrier();
             return o;
         };
+        // two-level, first level: this work-group sums blocks iw + Gx*j of its
+        // XCD (the G/8 slots of each, in slot order, read from the XCD's L2)
+        // and publishes each sum with agent-scope tagged stores into slot xw
+        // of the block's second-level words ([H/32][8][32] after the H x G
+        // first-level words)
+        auto xcd_level = [&](uint32_t* src) {
+            const uint32_t nb1 = iw < P.NB ? cdiv(P.NB - iw, Gx) : 0u, cpb = Gx * (RB / 4u);
+            const rsrc_t rs = make_rsrc(src + (size_t)xw * P.NB * Gx * RB, P.NB * Gx * RB * 4u);
+            gather(rs, nb1 * cpb, [&](uint32_t ch) { return ((iw + Gx * (ch / cpb)) * Gx * RB + 4u * (ch % cpb)) * 4u; },
+                   kNT);
+            for (uint32_t t = tid; t < nb1 * RB; t += kThreads) {
+                const uint32_t j = t / RB, rr = t % RB;
+                float sum = 0.f;
+                for (uint32_t sl = 0; sl < Gx; sl++) sum += fin[(j * Gx + sl) * RB + rr];
+                st_part(src + (size_t)H * G + ((size_t)(iw + Gx * j) * 8u + xw) * RB + rr, d.ptag(), sum);
+            }
+            lds_barrier();  // fin is staged again next
+        };
+        // two-level, second level: the 8 XCD sums of block blkr, in XCD order;
+        // the result is in threads 0..31
+        auto xcd_total = [&](const uint32_t* src, uint32_t blkr) -> float {
+            gather(make_rsrc(src + (size_t)H * G + (size_t)blkr * 8u * RB, 8u * RB * 4u), 8u * RB / 4u,
+                   [](uint32_t ch) { return 16u * ch; }, kSC1);
+            float o = 0.f;
+            if (tid < RB) {
+#pragma unroll
+                for (int x = 0; x < 8; x++) o += fin[x * RB + tid];
+            }
+            lds_barrier();
+            return o;
+        };
+        if (xl2) {
+            if (d.seg_lo() >= 1u && tid == 0 && xcc_id() != xw) raise_error(a.sync, SM, E_XCD, d.epoch);
+            xcd_level(a.part);
+            if (d.taps()) xcd_level(a.tsh);
+            WL_TL(6);
+        }
         // blocks go to work-groups in the order they get here (one ticket
         // each), so the work-groups that finish their own work last do not
         // also combine: with H/32 <= G they take no block
@@ -714,10 +815,10 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const float* hidden, const 
         WL_TL(11);
         for (uint32_t blkr = t0; blkr < P.NB; blkr += G) {
             const uint32_t r = blkr * RB + tid;
-            const float o = block_total(a.part, blkr);
+            const float o = xl2 ? xcd_total(a.part, blkr) : block_total(a.part, blkr);
             if (tid < RB) gst(d.out + r, d.resid ? __fadd_rn(gld(d.resid + r), o) : o);
             if (d.taps()) {
-                const float sh = block_total(a.tsh, blkr);
+                const float sh = xl2 ? xcd_total(a.tsh, blkr) : block_total(a.tsh, blkr);
                 if (tid < RB) gst(a.shared_out + r, sh);
             }
         }
@@ -1079,6 +1180,9 @@ __global__ void __launch_bounds__(kThreads) ffn1_kernel(FfnArgs a) {
     float* ms = xs + H;         // [I] the SwiGLU values
     uint32_t* flag = (uint32_t*)(ms + I);
     const SyncMap SM = SyncMap::make();
+#ifdef WL_TIMELINE
+    const uint32_t tl_slot = 0;
+#endif
     WL_TL(12);
     // x first (it returns first: a wave's loads complete in order), then
     // every weight load of the work-group
@@ -1290,6 +1394,27 @@ int launch_decode(const DecodeArgs* d_args, const DecodeDyn& dyn, uint32_t H, ui
     else hipLaunchKernelGGL((moe_decode_kernel<false, false>), gr, bl, lds, st, WL_DECODE_ARGS);
 #undef WL_DECODE_ARGS
     return (int)hipGetLastError();
+}
+
+__global__ void xcd_map_kernel(uint32_t* out) {
+    if (threadIdx.x == 0) out[blockIdx.x] = xcc_id();
+}
+
+int probe_xcd_map(uint32_t grid, bool* ok) {
+    *ok = false;
+    uint32_t* d = nullptr;
+    hipError_t e = hipMalloc(&d, 4 * (size_t)grid);
+    if (e != hipSuccess) return (int)e;
+    std::vector<uint32_t> h(grid, ~0u);
+    hipLaunchKernelGGL(xcd_map_kernel, dim3(grid), dim3(64), 0, 0, d);
+    e = hipGetLastError();
+    if (e == hipSuccess) e = hipMemcpy(h.data(), d, 4 * (size_t)grid, hipMemcpyDeviceToHost);
+    (void)hipFree(d);
+    if (e != hipSuccess) return (int)e;
+    bool all = true;
+    for (uint32_t w = 0; w < grid; w++) all = all && h[w] == (w & 7u);
+    *ok = all;
+    return 0;
 }
 
 #ifdef WL_TIMELINE

@@ -129,6 +129,7 @@ struct wl_ctx {
     uint32_t* part = nullptr;
     uint32_t* tsh = nullptr;
     uint32_t ptag = 0;  // the partials' tag of the last decode call: 1, 2, 3, 1, ...
+    bool xl2 = false;   // two-level combine (per-XCD sums through the XCDs' L2s first)
     bool stale_partials = false;  // a phased call's combine launch failed after its first segment ran
     uint32_t* sync = nullptr;   // barrier words (uncached)
     wl::SyncMap sm{};
@@ -362,8 +363,8 @@ wl_status wl_create(const wl_moe_config* cfg, wl_ctx** out) {
         (s = dalloc(c, &c->ffn_tag, 8 * (size_t)I)) != WL_OK ||
         (s = dalloc(c, &c->logits, 4 * (size_t)E)) != WL_OK ||
         (s = dalloc(c, &c->lslot, 8 * (size_t)E)) != WL_OK ||
-        (s = dalloc(c, &c->part, 4 * (size_t)H * grid)) != WL_OK ||
-        (s = dalloc(c, &c->tsh, 4 * (size_t)H * grid)) != WL_OK) {
+        (s = dalloc(c, &c->part, 4 * wl::part_words(H, grid))) != WL_OK ||
+        (s = dalloc(c, &c->tsh, 4 * wl::part_words(H, grid))) != WL_OK) {
         wl_destroy(c);
         return s;
     }
@@ -390,11 +391,22 @@ wl_status wl_create(const wl_moe_config* cfg, wl_ctx** out) {
     if (e == hipSuccess) e = hipMemset(c->lslot, 0, 8 * (size_t)E);
     if (e == hipSuccess) e = hipMemset(c->ffn_tag, 0, 8 * (size_t)I);
     // tag 0 is never a call's either
-    if (e == hipSuccess) e = hipMemset(c->part, 0, 4 * (size_t)H * grid);
-    if (e == hipSuccess) e = hipMemset(c->tsh, 0, 4 * (size_t)H * grid);
+    if (e == hipSuccess) e = hipMemset(c->part, 0, 4 * wl::part_words(H, grid));
+    if (e == hipSuccess) e = hipMemset(c->tsh, 0, 4 * wl::part_words(H, grid));
     if (e == hipSuccess) e = hipMemset(c->uc_block, 0, c->uc_bytes);
     if (e == hipSuccess) e = hipDeviceSynchronize();
     if (e != hipSuccess) { wl_destroy(c); return WL_ERR_HIP; }
+    // The two-level combine (WL_DECODE_XL2=1; off by default: at config 1
+    // its per-XCD first level takes as much time as it saves, see the
+    // kernel) needs work-group w on XCD w mod 8 (the dispatcher's round
+    // robin), checked here once with a probe launch of the decode grid and
+    // by every decode launch (E_XCD).
+    {
+        const char* env = getenv("WL_DECODE_XL2");
+        bool map_ok = false;
+        if (grid >= 8 && grid % 8 == 0 && env && env[0] == '1' && wl::probe_xcd_map(grid, &map_ok) == 0)
+            c->xl2 = map_ok;
+    }
     *out = c;
     return WL_OK;
 }
@@ -945,8 +957,8 @@ static wl_status run_layer(wl_ctx* c, uint32_t layer, const float* d_hidden, con
         // the next calls will use, and the next tag's ticket was not cleared
         hipError_t e = hipDeviceSynchronize();
         if (e == hipSuccess) e = hipMemset(c->sync + c->sm.ticket, 0, 4 * 3);
-        if (e == hipSuccess) e = hipMemset(c->part, 0, 4 * (size_t)H * c->grid);
-        if (e == hipSuccess) e = hipMemset(c->tsh, 0, 4 * (size_t)H * c->grid);
+        if (e == hipSuccess) e = hipMemset(c->part, 0, 4 * wl::part_words(H, c->grid));
+        if (e == hipSuccess) e = hipMemset(c->tsh, 0, 4 * wl::part_words(H, c->grid));
         if (e == hipSuccess) e = hipDeviceSynchronize();
         if (e != hipSuccess) return hip_fail(c, e, "partial-sum reset");
         c->stale_partials = false;
@@ -962,7 +974,7 @@ static wl_status run_layer(wl_ctx* c, uint32_t layer, const float* d_hidden, con
     dyn.resid = d_resid;
     dyn.out = d_out;
     auto launch = [&](uint32_t lo, uint32_t hi) -> wl_status {
-        dyn.seg = lo | (hi << 8) | ((c->taps ? 1u : 0u) << 16) | (ptag << 24);
+        dyn.seg = lo | (hi << 8) | ((c->taps ? 1u : 0u) << 16) | ((c->xl2 ? 1u : 0u) << 17) | (ptag << 24);
         int e = wl::launch_decode(c->d_largs + layer, dyn, H, I, SI, E, K, c->grid,
                                   L.shared_dtype == WL_SHARED_MXFP4, stream);
         if (e != 0) return hip_fail(c, (hipError_t)e, "decode launch");
@@ -1695,12 +1707,13 @@ wl_status wl_check_error(wl_ctx* c, void* stream) {
         // a launch that gave up may have left barrier counters mid-count, and
         // partial words of an older call whose tag a later call would reuse
         (void)hipMemset(c->sync, 0, 4 * (size_t)c->sm.words);
-        (void)hipMemset(c->part, 0, 4 * (size_t)c->cfg.hidden * c->grid);
-        (void)hipMemset(c->tsh, 0, 4 * (size_t)c->cfg.hidden * c->grid);
+        (void)hipMemset(c->part, 0, 4 * wl::part_words(c->cfg.hidden, c->grid));
+        (void)hipMemset(c->tsh, 0, 4 * wl::part_words(c->cfg.hidden, c->grid));
         (void)hipDeviceSynchronize();
-        return fail(c, WL_ERR_DEVICE, "device error bits 0x%x%s%s", flag,
+        return fail(c, WL_ERR_DEVICE, "device error bits 0x%x%s%s%s", flag,
                     (flag & wl::E_SPIN) ? " [dependency wait expired]" : "",
-                    (flag & wl::E_NOT_RESIDENT) ? " [routed expert not resident]" : "");
+                    (flag & wl::E_NOT_RESIDENT) ? " [routed expert not resident]" : "",
+                    (flag & wl::E_XCD) ? " [work-group not on XCD w mod 8: set WL_DECODE_XL2=0]" : "");
     }
     return WL_OK;
 }
