@@ -219,7 +219,9 @@ wl_status wl_make_resident(wl_ctx* ctx, uint32_t layer, void* stream);
  * round trip; a layer with none bound runs through the context's expert
  * source (wl_set_expert_source, or the built-in cache). Returns
  * WL_ERR_NOT_RESIDENT for a partly bound layer, or an unbound one without a
- * source. */
+ * source. A MoE decode layer cannot be captured into a HIP graph (each launch
+ * carries a new call epoch from the host): on a stream under capture this,
+ * wl_run_moe_residual and wl_run_chain return WL_ERR_STATE. */
 wl_status wl_run_moe(wl_ctx* ctx, uint32_t layer, const float* d_hidden, float* d_out,
                      void* stream);
 

@@ -73,3 +73,21 @@ def test_chain24_split_and_repeat_identical(gpu, chain_model):
     c, _, _ = _run(dm, None, 10, NL - 10, dh, dtmp)
     assert np.all(np.isfinite(a))
     assert np.array_equal(a, b) and np.array_equal(a, c)
+
+
+def test_chain24_one_launch_equals_per_layer_launches(gpu, chain_model):
+    """Under the fused schedule wl_run_chain runs all 24 resident layers in one
+    launch (each layer's output handed to the next as tagged words); under
+    the phased schedule it launches every layer on its own. Same arithmetic,
+    so the results must match bit for bit."""
+    from windlass_amd import moe
+    dm = chain_model
+    h0 = synth.hidden_state(GLM["hidden"], 33)
+    dm.ctx.set_schedule(moe.SCHED_PHASED)
+    try:
+        a, _, _ = _run(dm, h0, 0, NL)
+    finally:
+        dm.ctx.set_schedule(moe.SCHED_FUSED)
+    b, _, _ = _run(dm, h0, 0, NL)
+    assert np.all(np.isfinite(a))
+    assert np.array_equal(a, b)

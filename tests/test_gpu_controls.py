@@ -105,3 +105,41 @@ def test_bias_cast_to_bf16_changes_the_selection(gpu):
     bad = O.moe_layer(h, d16, src, 0, C)
     assert set(bad["topk_idx"].tolist()) != set(idx.tolist())
     assert O.rel_to_scale(bad["out"], out) > 1e-2
+
+
+def test_decode_layer_refuses_graph_capture(gpu):
+    """A MoE decode launch carries a new call epoch and partial tag from the
+    host, so a replayed capture could read an earlier call's logits or
+    partials as its own: under capture wl_run_moe, wl_run_moe_residual and
+    wl_run_chain return WL_ERR_STATE, enqueue nothing, and the context works
+    normally afterwards."""
+    from windlass_amd import hip as H_, moe
+    c = dict(hidden=384, moe_inter=256, n_routed_experts=48, n_experts_per_tok=6, n_shared=1,
+             routed_scaling=2.5, rms_eps=1e-5)
+    H = c["hidden"]
+    dm = DeviceModel(c, seed=3, n_layers=2)
+    try:
+        h = synth.hidden_state(H, 44)
+        dh, dout = make_io(H)
+        dh.upload(h)
+        st = H_.Stream()
+        for call in ("run_moe", "run_moe_residual", "run_chain"):
+            g = H_.Graph(st)
+            g.begin()
+            with pytest.raises(moe.WindlassError) as ei:
+                if call == "run_moe":
+                    dm.ctx.run_moe(0, dh.ptr, dout.ptr, st.handle)
+                elif call == "run_moe_residual":
+                    dm.ctx.run_moe_residual(0, dh.ptr, dh.ptr, dout.ptr, st.handle)
+                else:
+                    dm.ctx.run_chain(0, 2, dout.ptr, dh.ptr, st.handle)
+            g.end()
+            g.destroy()
+            assert ei.value.status == 5, call  # WL_ERR_STATE
+        dh.upload(h)
+        dm.ctx.run_moe(0, dh.ptr, dout.ptr, st.handle)
+        dm.ctx.check_error(st.handle)
+        ref = O.moe_layer(h, dm.dense[0], O.ExpertSource(H, c["moe_inter"], 3), 0, c)
+        assert O.rel_to_scale(ref["out"], dout.download(np.float32)) < 1e-5
+    finally:
+        dm.close()

@@ -315,6 +315,12 @@ struct BatchArgs {
 // Launchers (moe_decode.hip).
 int launch_decode(const DecodeArgs* d_args, const DecodeDyn& dyn, uint32_t H, uint32_t I, uint32_t SI,
                   uint32_t E, uint32_t K, uint32_t grid, bool sh4, void* stream);
+// n consecutive resident layers (records recs[0..n)) in one launch, in place
+// on d_h: epochs epoch0 .. epoch0 + n - 1, partial tags from seg0's; hx [H]
+// u64 carries each layer's output to the next (tagged words).
+int launch_chain(const DecodeArgs* recs, float* d_h, uint64_t* lslot, uint64_t* hx, uint32_t n, uint32_t epoch0,
+                 uint32_t seg0, uint32_t H, uint32_t I, uint32_t SI, uint32_t E, uint32_t K, uint32_t grid, bool sh4,
+                 void* stream);
 int decode_max_lds();
 // Whether work-group w of a grid-sized launch runs on XCD w mod 8 (every
 // work-group's XCC_ID register read back): *ok. Returns a hipError_t.

@@ -115,23 +115,36 @@ WL_DEV uint32_t xcc_id() {
 // ---- the decode kernel -------------------------------------------------------
 // GLM = true compiles the GLM shape (H 6144, I 2048, SI 2048, E 256, K 8) with
 // every shape constant known; GLM = false reads the shapes from the record.
-// The preloaded arguments: the record pointer, the five pointers up to lslot,
-// seg and epoch.
-static_assert(6 * sizeof(void*) / 4 + 2 == kPreloadDwords, "preloaded kernel arguments");
+// The hidden state of a layer inside one chain launch (moe_chain_kernel):
+// the previous layer's output arrives as epoch-tagged words (epoch << 32 |
+// f32 bits, agent scope) in hx, which is also the residual; a layer whose
+// output feeds the next writes it there the same way. A single-layer launch
+// passes {null, 0, null}: plain input d.hidden, plain output d.out.
+struct ChainIO {
+    const uint64_t* hx_in;  // tagged input (and residual), or null
+    uint32_t in_epoch;      // the epoch its words must carry
+    uint64_t* hx_out;       // tagged output, or null
+};
+
+// One layer on this work-group. Returns false when the work-group left an
+// aborted call (its partial words are written as they stand).
 // SH4 = true: the shared expert is MXFP4 (NativeShared4) instead of bf16.
-template <bool GLM, bool SH4>
-__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
-moe_decode_kernel(const DecodeArgs* __restrict__ pa, const float* hidden, const uint8_t* sh_native,
-                  const uint16_t* router_w, const uint16_t* ln_w, uint64_t* lslot, uint32_t seg, uint32_t epoch,
-                  const float* bias, const uint8_t* const* slot_tab, const float* resid, float* out) {
-    const DecodeArgs& a = *pa;
-    const DecodeDyn d{hidden, sh_native, router_w, ln_w, lslot, seg, epoch, bias, slot_tab, resid, out};
+// LOOP = true: the layer body of a multi-layer launch. Its work-group and
+// thread indices are re-read opaquely per layer, so that nothing derived
+// from them is computed once before the layer loop and held (spilled) across
+// the whole body.
+template <bool GLM, bool SH4, bool LOOP>
+__device__ __forceinline__ bool decode_layer(const DecodeArgs& a, const DecodeDyn& d, const ChainIO ch) {
 #ifdef WL_TIMELINE
-    const uint32_t tl_slot = epoch % kTlCalls;
+    const uint32_t tl_slot = d.epoch % kTlCalls;
 #endif
     const uint32_t H = GLM ? 6144u : a.H, I = GLM ? 2048u : a.I, SI = GLM ? 2048u : a.SI,
                    E = GLM ? 256u : a.E, K = GLM ? 8u : a.K;
-    const uint32_t G = gridDim.x, w = blockIdx.x, tid = threadIdx.x;
+    uint32_t G = gridDim.x, w = blockIdx.x, tid = threadIdx.x;
+    if constexpr (LOOP) {
+        asm volatile("" : "+s"(G), "+s"(w));
+        asm volatile("" : "+v"(tid));
+    }
     __builtin_assume(tid < (uint32_t)kThreads);
     const uint32_t v = uni(tid >> 6) & 7u, lane = tid & 63, n = lane & 15, g = lane >> 4;
     const Plan P = Plan::make(H, I, SI, K, G);
@@ -177,12 +190,28 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const float* hidden, const 
         constexpr int HV = kHV;
         float4 hv[HV];
         uint2 lv[HV];
-        const rsrc_t hid_rs = make_rsrc(d.hidden, H * 4u);
-        const rsrc_t ln_rs = make_rsrc(d.ln_w ? (const void*)d.ln_w : (const void*)d.hidden, H * 2u);
+        u32x4 hq[2 * HV];  // tagged input: the 8-byte words of float4 j at 32j, 32j + 16
+        // (no norm weight: the resource is empty and its loads read zeros)
+        const rsrc_t ln_rs = make_rsrc(d.ln_w ? (const void*)d.ln_w : (const void*)d.lslot, d.ln_w ? H * 2u : 0u);
+        if (ch.hx_in) {
+            const rsrc_t hx_rs = make_rsrc(ch.hx_in, H * 8u);
+#pragma unroll
+            for (int i = 0; i < HV; i++) {
+                const uint32_t j = tid + kThreads * i;
+                hq[2 * i] = bld16_ag(hx_rs, 32u * j, 0u);
+                hq[2 * i + 1] = bld16_ag(hx_rs, 32u * j + 16u, 0u);
+            }
+        } else {
+            const rsrc_t hid_rs = make_rsrc(d.hidden, H * 4u);
+#pragma unroll
+            for (int i = 0; i < HV; i++) {
+                const uint32_t j = tid + kThreads * i;  // float4 j = elements [4j, 4j+4)
+                hv[i] = __builtin_bit_cast(float4, bld16(hid_rs, 16u * j, 0u));
+            }
+        }
 #pragma unroll
         for (int i = 0; i < HV; i++) {
-            const uint32_t j = tid + kThreads * i;  // float4 j = elements [4j, 4j+4)
-            hv[i] = __builtin_bit_cast(float4, bld16(hid_rs, 16u * j, 0u));
+            const uint32_t j = tid + kThreads * i;
             lv[i] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(ln_rs, (int)(8u * j), 0, 0));
         }
         // the first router row of this work-group
@@ -318,6 +347,43 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const float* hidden, const 
         sg_issue(tile0, 1, sB);
         if (xl2 && tid == 0 && xcc_id() != (w & 7u)) raise_error(a.sync, SM, E_XCD, d.epoch);
 
+        if (ch.hx_in) {
+            // the previous layer's output: every word of this thread's float4s
+            // must carry its epoch; stale ones (its combine still running)
+            // are read again, bounded, the error word ending the wait too
+            const uint32_t e = ch.in_epoch;
+            auto fresh = [&](int i) {
+                return (hq[2 * i].y == e) & (hq[2 * i].w == e) & (hq[2 * i + 1].y == e) & (hq[2 * i + 1].w == e);
+            };
+            const rsrc_t hx_rs = make_rsrc(ch.hx_in, H * 8u);
+            uint32_t stale = 0;
+#pragma unroll
+            for (int i = 0; i < HV; i++)
+                if (tid + kThreads * i < H / 4u && !fresh(i)) stale |= 1u << i;
+            for (uint32_t spins = 0; stale != 0u; spins++) {
+                if (spins >= (1u << 20)) {
+                    raise_error(a.sync, SM, E_SPIN, d.epoch);
+                    break;
+                }
+                if ((spins & 63u) == 63u && aborted(a.sync, SM, d.epoch)) break;
+                __builtin_amdgcn_s_sleep(2);
+#pragma unroll
+                for (int i = 0; i < HV; i++) {
+                    if ((stale >> i) & 1u) {
+                        const uint32_t j = tid + kThreads * i;
+                        hq[2 * i] = bld16_ag(hx_rs, 32u * j, 0u);
+                        hq[2 * i + 1] = bld16_ag(hx_rs, 32u * j + 16u, 0u);
+                    }
+                }
+#pragma unroll
+                for (int i = 0; i < HV; i++)
+                    if (((stale >> i) & 1u) && fresh(i)) stale &= ~(1u << i);
+            }
+#pragma unroll
+            for (int i = 0; i < HV; i++)
+                hv[i] = make_float4(__uint_as_float(hq[2 * i].x), __uint_as_float(hq[2 * i].z),
+                                    __uint_as_float(hq[2 * i + 1].x), __uint_as_float(hq[2 * i + 1].z));
+        }
         // RMSNorm: w * (x * (1/sqrt(mean(x^2) + eps))) in fp32
         // (tools/ref_glm_chain.py:63-80; src/glm_primitives.cuh:35-62)
         const float rinv = norm_rinv(hv, red, H, a.eps);
@@ -487,7 +553,10 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const float* hidden, const 
             sd_issue(tile);
             if (lane < 16) red[v * 64 + n] = sum3(gacc);
             if (!routed) {
-                if (!route()) return leave();
+                if (!route()) {
+                    leave();
+                    return false;
+                }
                 routed = true;
             }
             lds_barrier();
@@ -510,7 +579,10 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const float* hidden, const 
                 sd_pending = true;
             }
         }
-        if (!routed && !route()) return leave();
+        if (!routed && !route()) {
+            leave();
+            return false;
+        }
         // the deferred down columns, then (taps on) the shared-expert
         // contribution alone, published for the tap
         bool tsh_pending = d.taps() != 0;
@@ -816,13 +888,66 @@ moe_decode_kernel(const DecodeArgs* __restrict__ pa, const float* hidden, const 
         for (uint32_t blkr = t0; blkr < P.NB; blkr += G) {
             const uint32_t r = blkr * RB + tid;
             const float o = xl2 ? xcd_total(a.part, blkr) : block_total(a.part, blkr);
-            if (tid < RB) gst(d.out + r, d.resid ? __fadd_rn(gld(d.resid + r), o) : o);
+            if (tid < RB) {
+                // + the residual: the layer's input (plain, or the tagged words it
+                // was read from, which only this block's combine overwrites)
+                float v = o;
+                if (d.resid) v = __fadd_rn(gld(d.resid + r), o);
+                else if (ch.hx_in)
+                    v = __fadd_rn(__uint_as_float((uint32_t)__hip_atomic_load(
+                                      (__attribute__((address_space(1))) const uint64_t*)(ch.hx_in + r),
+                                      __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)),
+                                  o);
+                if (d.out) gst(d.out + r, v);
+                if (ch.hx_out) st_tag(ch.hx_out + r, d.epoch, v);
+            }
             if (d.taps()) {
                 const float sh = xl2 ? xcd_total(a.tsh, blkr) : block_total(a.tsh, blkr);
                 if (tid < RB) gst(a.shared_out + r, sh);
             }
         }
         WL_TL(10);
+    }
+    return true;
+}
+
+// One layer per launch: the pointers its first loads need are preloaded
+// kernel arguments (the record pointer, the five pointers up to lslot, seg
+// and epoch).
+static_assert(6 * sizeof(void*) / 4 + 2 == kPreloadDwords, "preloaded kernel arguments");
+template <bool GLM, bool SH4>
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
+moe_decode_kernel(const DecodeArgs* __restrict__ pa, const float* hidden, const uint8_t* sh_native,
+                  const uint16_t* router_w, const uint16_t* ln_w, uint64_t* lslot, uint32_t seg, uint32_t epoch,
+                  const float* bias, const uint8_t* const* slot_tab, const float* resid, float* out) {
+    const DecodeDyn d{hidden, sh_native, router_w, ln_w, lslot, seg, epoch, bias, slot_tab, resid, out};
+    (void)decode_layer<GLM, SH4, false>(*pa, d, ChainIO{nullptr, 0u, nullptr});
+}
+
+// n consecutive resident layers in one launch, h <- h + moe(h) each: layer i
+// uses record recs[i], epoch epoch0 + i and partial tag (tag0 - 1 + i) mod 3
+// + 1. A work-group starts layer i + 1 as soon as it has finished its part
+// of layer i (its own work and the combine blocks it took), so the next
+// layer's weight loads overlap this layer's combine: the first layer reads h
+// from d_h, every layer hands its output to the next through hx as tagged
+// words (the reader polls), and the last writes d_h. Safe to reuse the
+// per-layer arrays: a work-group stores layer i + 1's partials only after
+// that layer's top-k, which needs every work-group's layer i + 1 logit, so
+// every work-group has left layer i by then.
+template <bool GLM, bool SH4>
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
+moe_chain_kernel(const DecodeArgs* __restrict__ recs, float* d_h, uint64_t* lslot, uint64_t* hx, uint32_t n,
+                 uint32_t epoch0, uint32_t seg0) {
+    const uint32_t tag0 = (seg0 >> 24) & 3u;
+    for (uint32_t i = 0; i < n; i++) {
+        const DecodeArgs& a = recs[i];
+        const uint32_t seg = (seg0 & 0x00FFFFFFu) | ((((tag0 - 1u + i) % 3u) + 1u) << 24);
+        const bool first = i == 0u, last = i + 1u == n;
+        const DecodeDyn d{first ? d_h : nullptr, a.sh_native, a.router_w, a.ln_w, lslot, seg, epoch0 + i,
+                          a.bias, a.slot_tab, first ? d_h : nullptr, last ? d_h : nullptr};
+        if (!decode_layer<GLM, SH4, true>(a, d, ChainIO{first ? nullptr : hx, epoch0 + i - 1u, last ? nullptr : hx}))
+            return;
+        lds_barrier();  // the next layer's LDS writes follow every wave's last reads
     }
 }
 
@@ -1415,6 +1540,29 @@ int probe_xcd_map(uint32_t grid, bool* ok) {
     for (uint32_t w = 0; w < grid; w++) all = all && h[w] == (w & 7u);
     *ok = all;
     return 0;
+}
+
+static const void* chain_fn(bool glm, bool sh4) {
+    return glm ? (sh4 ? (const void*)moe_chain_kernel<true, true> : (const void*)moe_chain_kernel<true, false>)
+               : (sh4 ? (const void*)moe_chain_kernel<false, true> : (const void*)moe_chain_kernel<false, false>);
+}
+
+int launch_chain(const DecodeArgs* recs, float* d_h, uint64_t* lslot, uint64_t* hx, uint32_t n, uint32_t epoch0,
+                 uint32_t seg0, uint32_t H, uint32_t I, uint32_t SI, uint32_t E, uint32_t K, uint32_t grid, bool sh4,
+                 void* stream) {
+    const Plan p = Plan::make(H, I, SI, K, grid);
+    const size_t lds = LdsMap::make(H, SI, E, K, p).bytes;
+    const bool glm = glm_shape(H, I, SI, E, K);
+    const void* fn = chain_fn(glm, sh4);
+    hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return (int)e;
+    const dim3 gr(grid), bl(kThreads);
+    hipStream_t st = (hipStream_t)stream;
+    if (glm && sh4) hipLaunchKernelGGL((moe_chain_kernel<true, true>), gr, bl, lds, st, recs, d_h, lslot, hx, n, epoch0, seg0);
+    else if (glm) hipLaunchKernelGGL((moe_chain_kernel<true, false>), gr, bl, lds, st, recs, d_h, lslot, hx, n, epoch0, seg0);
+    else if (sh4) hipLaunchKernelGGL((moe_chain_kernel<false, true>), gr, bl, lds, st, recs, d_h, lslot, hx, n, epoch0, seg0);
+    else hipLaunchKernelGGL((moe_chain_kernel<false, false>), gr, bl, lds, st, recs, d_h, lslot, hx, n, epoch0, seg0);
+    return (int)hipGetLastError();
 }
 
 #ifdef WL_TIMELINE

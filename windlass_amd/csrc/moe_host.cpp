@@ -128,6 +128,7 @@ struct wl_ctx {
     uint64_t* lslot = nullptr;
     uint32_t* part = nullptr;
     uint32_t* tsh = nullptr;
+    uint64_t* hx = nullptr;  // [H] a chain launch's layer outputs, epoch-tagged words
     uint32_t ptag = 0;  // the partials' tag of the last decode call: 1, 2, 3, 1, ...
     bool xl2 = false;   // two-level combine (per-XCD sums through the XCDs' L2s first)
     bool stale_partials = false;  // a phased call's combine launch failed after its first segment ran
@@ -364,7 +365,8 @@ wl_status wl_create(const wl_moe_config* cfg, wl_ctx** out) {
         (s = dalloc(c, &c->logits, 4 * (size_t)E)) != WL_OK ||
         (s = dalloc(c, &c->lslot, 8 * (size_t)E)) != WL_OK ||
         (s = dalloc(c, &c->part, 4 * wl::part_words(H, grid))) != WL_OK ||
-        (s = dalloc(c, &c->tsh, 4 * wl::part_words(H, grid))) != WL_OK) {
+        (s = dalloc(c, &c->tsh, 4 * wl::part_words(H, grid))) != WL_OK ||
+        (s = dalloc(c, &c->hx, 8 * (size_t)H)) != WL_OK) {
         wl_destroy(c);
         return s;
     }
@@ -393,6 +395,7 @@ wl_status wl_create(const wl_moe_config* cfg, wl_ctx** out) {
     // tag 0 is never a call's either
     if (e == hipSuccess) e = hipMemset(c->part, 0, 4 * wl::part_words(H, grid));
     if (e == hipSuccess) e = hipMemset(c->tsh, 0, 4 * wl::part_words(H, grid));
+    if (e == hipSuccess) e = hipMemset(c->hx, 0, 8 * (size_t)H);
     if (e == hipSuccess) e = hipMemset(c->uc_block, 0, c->uc_bytes);
     if (e == hipSuccess) e = hipDeviceSynchronize();
     if (e != hipSuccess) { wl_destroy(c); return WL_ERR_HIP; }
@@ -933,6 +936,14 @@ static wl_status run_layer(wl_ctx* c, uint32_t layer, const float* d_hidden, con
                  : (d_out == d_hidden || (d_resid && d_out == d_resid)))
         return fail(c, WL_ERR_INVALID, "d_out must not alias the inputs");
     if (L.dense) return run_dense(c, layer, d_hidden, d_resid, d_out, stream);
+    {
+        // Each decode launch carries a new epoch and partial tag from the
+        // host; a captured launch replayed would reuse them and could take an
+        // earlier call's logits or partials as this call's.
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        if (hipStreamIsCapturing((hipStream_t)stream, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone)
+            return fail(c, WL_ERR_STATE, "a MoE decode layer cannot be captured into a graph (per-call epochs)");
+    }
     const uint32_t H = c->cfg.hidden, I = c->cfg.moe_inter, E = c->cfg.n_routed_experts,
                    K = c->cfg.n_experts_per_tok, SI = c->SI;
     const bool cached = c->n_bound[layer] == 0 && c->src.get != nullptr;
@@ -1027,6 +1038,36 @@ wl_status wl_run_chain(wl_ctx* c, uint32_t first_layer, uint32_t n_layers, float
     if (first_layer + (uint64_t)n_layers > c->cfg.n_layers)
         return fail(c, WL_ERR_INVALID, "layers [%u,%u) exceed n_layers %u", first_layer,
                     first_layer + n_layers, c->cfg.n_layers);
+    if (n_layers == 0) return WL_OK;
+    // Resident MoE layers under the fused schedule run in one launch
+    // (moe_chain_kernel): a work-group starts layer l + 1 as soon as it has
+    // finished its part of layer l, so the next layer's weight loads overlap
+    // this layer's combine, with no launch boundary between layers. The
+    // arithmetic is the per-layer launch's, so results are bit-identical.
+    bool one_launch = c->sched == WL_SCHED_FUSED && c->hx != nullptr && !c->stale_partials;
+    for (uint32_t l = 0; one_launch && l < n_layers; l++) {
+        const LayerState& L = c->layers[first_layer + l];
+        one_launch = L.set && !L.dense && c->n_bound[first_layer + l] == c->cfg.n_routed_experts &&
+                     L.shared_dtype == c->layers[first_layer].shared_dtype;
+    }
+    if (one_launch) {
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        if (hipStreamIsCapturing((hipStream_t)stream, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone)
+            return fail(c, WL_ERR_STATE, "a MoE decode chain cannot be captured into a graph (per-call epochs)");
+        if ((uintptr_t)d_h % 16) return fail(c, WL_ERR_INVALID, "d_h must be 16-byte aligned");
+        // layer l takes epoch epoch0 + l and the l-th partial tag after the last call's
+        if (c->epoch + (uint64_t)n_layers >= 0x7FFFFFFFu) c->epoch = 0;
+        const uint32_t epoch0 = c->epoch + 1, ptag0 = c->ptag % 3u + 1u;
+        const uint32_t seg0 = 0u | (1u << 8) | ((c->taps ? 1u : 0u) << 16) | ((c->xl2 ? 1u : 0u) << 17) | (ptag0 << 24);
+        const int e = wl::launch_chain(c->d_largs + first_layer, d_h, c->lslot, c->hx, n_layers, epoch0, seg0,
+                                       c->cfg.hidden, c->cfg.moe_inter, c->SI, c->cfg.n_routed_experts,
+                                       c->cfg.n_experts_per_tok, c->grid,
+                                       c->layers[first_layer].shared_dtype == WL_SHARED_MXFP4, stream);
+        if (e != 0) return hip_fail(c, (hipError_t)e, "chain launch");
+        c->epoch += n_layers;
+        c->ptag = (ptag0 - 1u + n_layers - 1u) % 3u + 1u;
+        return WL_OK;
+    }
     // every layer in place (see run_layer); d_tmp is not written
     for (uint32_t l = 0; l < n_layers; l++) {
         const uint32_t next = l + 1 < n_layers ? first_layer + l + 1 : 0xFFFFFFFFu;
