@@ -947,7 +947,8 @@ def main():
                                         "scaled by a copy-kernel calibration)") if traffic is not None else None,
                      "algorithmic_bytes": nbytes,
                      "kernel": ("whole batched call (bup_kernel + bdown_kernel dominate)" if batched else
-                                "moe_decode_kernel")},
+                                f"moe_chain_kernel ({args.layers} layers per launch; per layer)"
+                                if args.workload == "chain" and args.sched == "fused" else "moe_decode_kernel")},
         "cpu_baseline": cpu,
         **({"batched": {"tokens": args.tokens, "unique_experts": uniq, "max_tokens_per_expert": int(cnt.max()),
                         "zipf": {"s": 1.1, "amplitude": args.zipf_amp}}} if batched else {}),
