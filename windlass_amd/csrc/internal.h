@@ -287,6 +287,11 @@ enum : uint32_t {
     kBatchWideSharedUp = 8u,
     kBatchWideSharedDown = 16u
 };
+// Routed experts of at most kSmallT tokens run their down projection in the
+// down GEMM kernel's streaming pipeline (run_small_down) when launch_batched
+// takes that kernel's small-expert instantiation; its pass table leaves them
+// out of the other pipelines.
+constexpr uint32_t kSmallT = 4;
 // launch_batched phases: routing (norm .. permute), the GEMMs, the combine.
 enum : uint32_t { kPhaseRoute = 1u, kPhaseGemm = 2u, kPhaseCombine = 4u, kPhaseAll = 7u };
 struct BatchArgs {

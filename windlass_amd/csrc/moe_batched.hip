@@ -394,8 +394,10 @@ WL_DEV uint32_t wide_passes_of(uint32_t c, bool wide) { return wide && c > kMT ?
 // wparts > 0: experts of more than kMT tokens run in wide passes if their
 // wparts units per pass fill the grid (fewer wide units than work-groups
 // leave the ones that hold one ending last: measured slower at T = 256).
+// small > 0: routed experts of 1..small tokens are left out (their down
+// projection runs in bdown_kernel's streaming pipeline, run_small_down).
 WL_DEV PassTab load_pass_tab(const BatchArgs& b, uint32_t E, uint32_t K, uint32_t* s, const uint8_t* const* stab,
-                             uint32_t wparts) {
+                             uint32_t wparts, uint32_t small = 0u) {
     const uint32_t tid = threadIdx.x;
     uint32_t *cnt = s, *off = s + E, *pp = s + 2u * E, *ppw = s + 3u * E + 1u;
     const bool skip = (b.flags & kBatchSkipUnbound) != 0u;
@@ -407,7 +409,8 @@ WL_DEV PassTab load_pass_tab(const BatchArgs& b, uint32_t E, uint32_t K, uint32_
             continue;
         }
         // stab[f] was written by this thread (load_slot_tab, same stride)
-        cnt[f] = skip && stab[f] == nullptr ? 0u : gld(b.counts + f);
+        const uint32_t c = skip && stab[f] == nullptr ? 0u : gld(b.counts + f);
+        cnt[f] = c <= small ? 0u : c;
         off[f] = gld(b.offsets + f);
     }
     lds_barrier();
@@ -1843,7 +1846,169 @@ WL_DEV uint32_t run_routed_down_wide(const DecodeArgs& a, const BatchArgs& b, co
     run_steps(w);
     return U;
 }
+// ---- routed down of small experts ---------------------------------------------
+// Experts with 1..kSmallT tokens (at small T most of them: 64 tokens x 8
+// slots over ~200 experts) run their down projection as streaming units,
+// like the decode kernel's down phase: unit (expert, row block of 16 row
+// pairs). The expert's SwiGLU pieces are staged once per unit in LDS, token
+// m's three pieces in rows 4m..4m+2 (rows 4m+3 zero), so one
+// v_mfma_f32_16x16x32_bf16 covers all of the expert's tokens; then each wave
+// streams its 2 row pairs x I/64 slices (native 1 KB dn chunks, the batched
+// scale words of bdns) two 256-column steps ahead, with no barrier between
+// steps (the GEMM kernel stages 48 KB of activation rows and meets a barrier
+// every step). The arithmetic per step is the GEMM kernel's (pieces in rows,
+// one row block). It is the last pipeline of bdown_kernel: its units are
+// 512 KB of weights each, so with the rotation (unit r on work-group (r +
+// uoff) mod grid, uoff the units of the earlier pipelines) the work-groups
+// end within about one unit of each other. LDS: the staged rows 0-7 in slot
+// 0, 8-15 in slot 1, the small-expert list in slot 2.
+// the shapes it runs: at least two 256-column steps, at most 2048 columns staged
+__host__ __device__ inline bool small_down_fits(uint32_t H, uint32_t I) {
+    return I % kKC == 0u && I >= 2u * kKC && I <= 2048u && H % 512u == 0u;
+}
 template <bool GLM>
+WL_DEV void run_small_down(const DecodeArgs& a, const BatchArgs& b, const uint8_t* const* stab, uint32_t uoff) {
+    const uint32_t H = GLM ? 6144u : a.H, I = GLM ? 2048u : a.I, E = GLM ? 256u : a.E;
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, v = uni(tid >> 6), n = lane & 15u, g = lane >> 4;
+    uint32_t* se = (uint32_t*)slot<2>();  // [E] the small experts, ascending; se[E] their count
+    const uint32_t RS = I + 8u;  // staged row stride (bf16): rows 16 bytes apart in the bank groups
+    // staged row R (token R / 4, piece R % 4) at xrow(R)
+    auto xrow = [&](uint32_t R) { return (uint16_t*)(R < 8u ? slot<0>() : slot<1>()) + (R % 8u) * RS; };
+    const bool skip = (b.flags & kBatchSkipUnbound) != 0u;
+    if (v == 0u) {
+        uint32_t run = 0;
+        for (uint32_t e0 = 0; e0 < E; e0 += 64u) {
+            const uint32_t e = e0 + lane;
+            const uint32_t c = e < E ? gld(b.counts + e) : 0u;
+            const bool sm = c >= 1u && c <= kSmallT && !(skip && stab[e] == nullptr);
+            const uint64_t bal = __ballot(sm);
+            if (sm) se[run + (uint32_t)__popcll(bal & ((1ull << lane) - 1ull))] = e;
+            run += (uint32_t)__popcll(bal);
+        }
+        if (lane == 0u) se[E] = run;
+    }
+    lds_barrier();
+    const uint32_t ns = uni(se[E]), nq = H / 32u, RBr = cdiv(nq, 16u), nstd = I / kKC;
+    const uint32_t U = ns * RBr, G = gridDim.x;
+    const NativeLayout NL = NativeLayout::make(H, I);
+    const uint32_t vdn = (uint32_t)NL.dn + 16u * lane, vdns = (uint32_t)NL.bdns + v * nstd * 512u + 8u * lane;
+    const rsrc_t mrs = make_rsrc(b.mid3, (uint32_t)((size_t)b.T * (a.K + ((b.flags & kBatchShared4) ? 1u : 0u)) * 6u * I));
+    // A fragment of lane (n, g): row n, columns 256 st + 64 s4 + 32 (g & 1) + 8 (g >> 1) + 16 f
+    const uint16_t* const arow = xrow(n) + 32u * (g & 1u) + 8u * (g >> 1);
+    struct WB {
+        u32x4 w[kWL];
+        uint32_t s[2];
+    };
+    constexpr uint32_t kAV = 8;  // 16-byte chunks of the staged rows per thread (I <= 2048)
+    const uint32_t cpr = I / 8u;  // 16-byte chunks per staged row
+    // the unit being loaded: its expert's tokens, first compact row, block, row block
+    uint32_t nt = 0, c0 = 0, part = 0;
+    rsrc_t wrs = make_rsrc(nullptr, 0u);
+    u32x4 av[kAV];
+    auto issue = [&](uint32_t st, WB& W) {
+#pragma unroll
+        for (uint32_t j = 0; j < kWL; j++) {
+            const uint32_t sj = 4u * st + j / 2u, q = min(16u * part + 2u * v + j % 2u, nq - 1u);
+            W.w[j] = bld16_nt(wrs, vdn, (sj * nq + q) * 1024u);
+        }
+        bld8(wrs, vdns, (part * 8u * nstd + st) * 512u, W.s);
+    };
+    // unit r's pieces (into av, issued first) and its first two steps
+    WB B0, B1;
+    auto start = [&](uint32_t r) {
+        const PassPart jp = pass_part(r, RBr, ns);
+        const uint32_t e = uni(se[jp.j]);
+        part = jp.part;
+        nt = uni(gld(b.counts + e));
+        c0 = uni(gld(b.offsets + e));
+        wrs = make_rsrc(uni_ptr(stab[e]), (uint32_t)NL.total);
+#pragma unroll
+        for (uint32_t k = 0; k < kAV; k++) {
+            const uint32_t idx = tid + kThreads * k, row = idx / cpr, c8 = idx % cpr, m = row / 4u, pc = row % 4u;
+            const bool ok = idx < 16u * cpr && m < nt && pc < 3u;
+            av[k] = __builtin_amdgcn_raw_buffer_load_b128(mrs, (int)(ok ? (((c0 + m) * 3u + pc) * I + 8u * c8) * 2u : kOOB), 0, 0);
+        }
+        issue(0u, B0);
+        issue(1u, B1);
+    };
+    f32x4 d[2][2];
+    auto consume = [&](uint32_t st, const WB& W) {
+        auto frag = [&](uint32_t o) {  // o = 2 s4 + f
+            return as_bf16x8(*(const u32x4*)(arow + 256u * st + 64u * (o / 2u) + 16u * (o % 2u)));
+        };
+        bf16x8 af[2];
+        af[0] = frag(0u);
+        float scx[2], scy[2];
+#pragma unroll
+        for (uint32_t o = 0; o < 8u; o++) {
+            const uint32_t s4 = o / 2u, f = o % 2u;
+            if (o + 1u < 8u) af[(o + 1u) % 2u] = frag(o + 1u);
+            if (f == 0u) {
+#pragma unroll
+                for (uint32_t h = 0; h < 2; h++) {
+                    // decoded once, then swapped like the weight dwords
+                    const uint32_t sv = __float_as_uint(e8m0f((W.s[s4 >> 1] >> (8u * (2u * (s4 & 1u) + h))) & 0xFFu));
+                    uint32_t sx, sy;
+                    swap32(sv, sv, sx, sy);
+                    scx[h] = __uint_as_float(sx);
+                    scy[h] = __uint_as_float(sy);
+                }
+            }
+            // column half f of slice s4: lane group g's columns 64 s4 + 32 (g & 1)
+            // + 8 (g >> 1) + 16 f, from dwords 2f, 2f + 1 of each row pair's chunk
+            bf16x8 bx[2], by[2];
+#pragma unroll
+            for (uint32_t h = 0; h < 2; h++) {
+                const u32x4 wv = W.w[2u * s4 + h];
+                uint32_t x, y;
+                swap32(wv[2u * f], wv[2u * f + 1u], x, y);
+                bx[h] = fp4x8_bf16(x, scx[h]);
+                by[h] = fp4x8_bf16(y, scy[h]);
+            }
+            const bf16x8 af_o = af[o % 2u];
+#pragma unroll
+            for (uint32_t h = 0; h < 2; h++) {
+                d[h][0] = mma(af_o, bx[h], d[h][0]);
+                d[h][1] = mma(af_o, by[h], d[h][1]);
+            }
+        }
+    };
+    const uint32_t r0 = (blockIdx.x + G - uoff % G) % G;
+    if (r0 < U) start(r0);
+    for (uint32_t r = r0; r < U; r += G) {
+#pragma unroll
+        for (uint32_t k = 0; k < kAV; k++) {
+            const uint32_t idx = tid + kThreads * k;
+            if (idx < 16u * cpr) *(u32x4*)(xrow(idx / cpr) + 8u * (idx % cpr)) = av[k];
+        }
+        lds_barrier();
+#pragma unroll
+        for (uint32_t h = 0; h < 2; h++) d[h][0] = d[h][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+        pingpong(nstd, B0, B1, issue, consume);
+        // the next unit's pieces and first steps go out before this unit's
+        // epilogue, so the stream does not stop between units
+        const uint32_t nt_u = nt, c0_u = c0, part_u = part;
+        if (r + G < U) start(r + G);
+        const uint32_t ln = opaque_lane(), nn = ln & 15u;
+#pragma unroll
+        for (uint32_t h = 0; h < 2; h++) {
+            const uint32_t q = 16u * part_u + 2u * v + h;
+            if (q >= nq) continue;
+            float* o = b.expout + (size_t)c0_u * H + 32u * q + nn;
+            const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+            const f32x4 ax[2] = {d[h][0], z}, ay[2] = {d[h][1], z};
+            tile_each(ax, nt_u, true, ln, [&](uint32_t m, float x) { gst(o + (size_t)m * H, x); });
+            tile_each(ay, nt_u, true, ln, [&](uint32_t m, float x) { gst(o + (size_t)m * H + 16u, x); });
+        }
+        lds_barrier();  // every wave is done with the staged rows before the next unit's pieces
+    }
+}
+
+// SMALL = true: the instantiation with the small-expert pipeline (launch_batched
+// takes it when the batch averages at most two tokens per expert); the other
+// keeps the GEMM pipelines' code as it was (with the small pipeline compiled
+// in, T = 256 and 1024 ran 2-4 % slower).
+template <bool GLM, bool SMALL>
 __global__ void __launch_bounds__(kThreads) bdown_kernel(const DecodeArgs* __restrict__ pa, const BatchArgs b) {
     const DecodeArgs& a = *pa;
     extern __shared__ __align__(16) uint8_t dyn[];
@@ -1851,7 +2016,8 @@ __global__ void __launch_bounds__(kThreads) bdown_kernel(const DecodeArgs* __res
     const bool sh4 = (b.flags & kBatchShared4) != 0u;
     const uint32_t E = a.E + (sh4 ? 1u : 0u);  // experts in the pass table
     const uint8_t* const* stab = load_slot_tab(a, a.E, sh4, (const uint8_t**)dyn);
-    const PassTab pt = load_pass_tab(b, E, a.K, (uint32_t*)(dyn + 8u * E), stab, cdiv(H / 32u, 16u));
+    const PassTab pt = load_pass_tab(b, E, a.K, (uint32_t*)(dyn + 8u * E), stab, cdiv(H / 32u, 16u),
+                                     SMALL ? kSmallT : 0u);
     const uint32_t Us = run_shared_down_wide<GLM>(a, b);
     if (Us) pipeline_drain();
     const uint32_t Ur = run_routed_down_wide<GLM>(a, b, pt, stab, E, Us % gridDim.x);
@@ -1888,6 +2054,10 @@ __global__ void __launch_bounds__(kThreads) bdown_kernel(const DecodeArgs* __res
         k.lo_s[j] = a_lane_off(4u * j + k.g);
     }
     run_steps(k);
+    if constexpr (SMALL) {
+        pipeline_drain();
+        run_small_down<GLM>(a, b, stab, k.uoff + U);
+    }
 }
 
 // out[t] = (resid[t] +) sum_k w[t][k] e_k[t] in slot order + shared[t]
@@ -1942,7 +2112,14 @@ int launch_batched(const DecodeArgs* d_args, const BatchArgs& b, uint32_t H, uin
     // at the GLM shape
     const bool glm = H == 6144u && I == 2048u && SI == 2048u && K == 8u;
     const void* up = glm ? (const void*)bup_kernel<true> : (const void*)bup_kernel<false>;
-    const void* down = glm ? (const void*)bdown_kernel<true> : (const void*)bdown_kernel<false>;
+    // routed experts of at most kSmallT tokens: their down projection as
+    // bdown_kernel's streaming pipeline, when the batch averages at most two
+    // tokens per expert (measured at the GLM shape: T = 64 about -3 % per
+    // call; at T = 256 and 1024, where few experts are that small, their
+    // units after the GEMM pipeline's made the call slower)
+    const bool small = small_down_fits(H, I) && (uint64_t)b.T * K <= 2ull * E;
+    const void* down = glm ? (small ? (const void*)bdown_kernel<true, true> : (const void*)bdown_kernel<true, false>)
+                           : (small ? (const void*)bdown_kernel<false, true> : (const void*)bdown_kernel<false, false>);
     const struct { const void* fn; size_t lds; } attrs[] = {
         {(const void*)btopk_kernel, topk_lds}, {up, gemm_lds}, {down, gemm_lds}};
     for (const auto& at : attrs)
@@ -1978,10 +2155,12 @@ int launch_batched(const DecodeArgs* d_args, const BatchArgs& b, uint32_t H, uin
         if (bf16_sh && (b.T + kMTW - 1u) / kMTW * ((H + 255u) / 256u) >= gd) bw.flags |= kBatchWideSharedDown;
         if (glm) {
             hipLaunchKernelGGL(bup_kernel<true>, dim3(gu), dim3(kThreads), gemm_lds, s, d_args, bw);
-            hipLaunchKernelGGL(bdown_kernel<true>, dim3(gd), dim3(kThreads), gemm_lds, s, d_args, bw);
+            if (small) hipLaunchKernelGGL((bdown_kernel<true, true>), dim3(gd), dim3(kThreads), gemm_lds, s, d_args, bw);
+            else hipLaunchKernelGGL((bdown_kernel<true, false>), dim3(gd), dim3(kThreads), gemm_lds, s, d_args, bw);
         } else {
             hipLaunchKernelGGL(bup_kernel<false>, dim3(gu), dim3(kThreads), gemm_lds, s, d_args, bw);
-            hipLaunchKernelGGL(bdown_kernel<false>, dim3(gd), dim3(kThreads), gemm_lds, s, d_args, bw);
+            if (small) hipLaunchKernelGGL((bdown_kernel<false, true>), dim3(gd), dim3(kThreads), gemm_lds, s, d_args, bw);
+            else hipLaunchKernelGGL((bdown_kernel<false, false>), dim3(gd), dim3(kThreads), gemm_lds, s, d_args, bw);
         }
     }
     if (phases & kPhaseCombine)
