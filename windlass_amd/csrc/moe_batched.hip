@@ -1367,7 +1367,12 @@ struct DownK {
     const uint8_t* const* stab;
     NativeLayout NL;
     Cursor ca, cw, cc;
-    rsrc_t wrs, srs;
+    // the weight stream's block and the scale stream's (null: none), kept as
+    // pointers: a buffer resource held in the struct went through scratch in
+    // one instantiation, and its loads became per-lane resource loops
+    const uint8_t* wbase;
+    const uint8_t* sbase;
+    uint32_t wbytes, sbytes;
     bool wsh;
     uint32_t wpart, wvoff, vdn, vdns;
     // A fragment lane offsets: routed slice s4, half f (cg = 8 s4 + 4 (g & 1)
@@ -1413,10 +1418,10 @@ struct DownK {
         wpart = x.part;
         const NativeShared NSh = NativeShared::make(H, SI);
         const uint8_t* blk = x.live && !x.sh ? uni_ptr(stab[x.e]) : nullptr;
-        wrs = !x.live ? make_rsrc(nullptr, 0u)
-              : x.sh  ? make_rsrc(a.sh_native + NSh.sdn, (uint32_t)(NSh.total - NSh.sdn))
-                      : make_rsrc(blk, blk ? (uint32_t)NL.total : 0u);
-        srs = x.live && !x.sh ? wrs : make_rsrc(nullptr, 0u);
+        wbase = !x.live ? nullptr : x.sh ? a.sh_native + NSh.sdn : blk;
+        wbytes = !x.live ? 0u : x.sh ? (uint32_t)(NSh.total - NSh.sdn) : blk ? (uint32_t)NL.total : 0u;
+        sbase = x.live && !x.sh ? blk : nullptr;
+        sbytes = x.live && !x.sh && blk ? (uint32_t)NL.total : 0u;
         // the lane's weight offset base, chosen here (a select between two
         // members at each load would take the members' addresses)
         wvoff = x.sh ? (g * H + min(x.part * 128u + 16u * v + n, H - 1u)) * 16u : vdn;
@@ -1427,9 +1432,9 @@ struct DownK {
             const uint32_t sj = min(st * 4u + j / 2u, NS - 1u), q = min(q0 + j % 2u, nq - 1u);
             const uint32_t ro = (sj * nq + q) * 1024u;
             const uint32_t so = min(8u * st + j, nks - 1u) * 4u * H * 16u;
-            W.w[j] = bld16_nt(wrs, wvoff, wsh ? so : ro);
+            W.w[j] = bld16_nt(make_rsrc(wbase, wbytes), wvoff, wsh ? so : ro);
         } else {
-            bld8(srs, vdns, (wpart * 8u * nstd + min(st, nstd - 1u)) * 512u, W.s);
+            bld8(make_rsrc(sbase, sbytes), vdns, (wpart * 8u * nstd + min(st, nstd - 1u)) * 512u, W.s);
         }
     }
     WL_MEM void begin(uint32_t i) {
