@@ -268,7 +268,7 @@ wl_status wl_run_moe_batched(wl_ctx* ctx, uint32_t layer, uint32_t n_tokens, con
  * (one per GPU, held until the process ends) instead of context memory that
  * wl_run_moe_batched grows on demand, so the call performs no hipMalloc,
  * hipFree or other allocation. Tokens run in chunks of as many as the array
- * holds (97 at hidden 6144 / inter 2048 / 8 of 256 experts); a shape whose
+ * holds (169 at hidden 6144 / inter 2048 / 8 of 256 experts); a shape whose
  * single token does not fit returns WL_ERR_INVALID. Every call on one GPU
  * shares that GPU's array, which keeps the last call's contents: calls that
  * overlap on one GPU (two streams, two contexts, two host threads) race.

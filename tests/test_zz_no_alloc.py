@@ -2,9 +2,9 @@
 allocating one (wl_run_moe_batched), through the C ABI (GPU; -m gpu).
 
 Both run the same kernels; the allocation-free one takes its scratch from the
-library's static 64 MiB device array and runs at most 97 GLM tokens per chunk.
+library's static 64 MiB device array and runs at most 169 GLM tokens per chunk.
 Two calls in a row, the second smaller, at a small shape and at the GLM shape;
-the GLM call of 130 tokens runs as two chunks (97 + 33)."""
+the GLM call of 200 tokens runs as two chunks (169 + 31)."""
 import numpy as np
 import pytest
 
@@ -20,7 +20,7 @@ SMALL = dict(hidden=384, moe_inter=256, n_routed_experts=48, n_experts_per_tok=6
              routed_scaling=2.5, rms_eps=1e-5)
 GLM = dict(hidden=6144, moe_inter=2048, n_routed_experts=256, n_experts_per_tok=8, n_shared=1,
            routed_scaling=2.5, rms_eps=1e-5)
-GLM_CHUNK = 97
+GLM_CHUNK = 169
 
 
 def _tokens(H, T, seed):
@@ -45,7 +45,7 @@ def test_noalloc_matches_batched(gpu, shape):
     H = c["hidden"]
     off = synthdata.zipf_bias_offset(c["n_routed_experts"], 21, amplitude=0.25) if shape == "glm" else None
     dm = DeviceModel(c, seed=21, n_layers=1, bias_offset=off)
-    sizes = [70, 5] if shape == "small" else [130, 20]
+    sizes = [70, 5] if shape == "small" else [200, 20]
     for call, T in enumerate(sizes):
         print(f"noalloc {shape}: call {call}, T={T}", flush=True)
         hs = _tokens(H, T, 900 + 10 * call)

@@ -37,6 +37,7 @@ enum : uint32_t {
     E_SPIN = 1u,          // a wait for another work-group's data exceeded its bound
     E_NOT_RESIDENT = 2u,  // a routed expert resolved to a null block
     E_XCD = 4u,           // two-level combine: a work-group ran on another XCD than w mod 8
+    E_TOKTAB = 8u,        // batched gate/up: a work-group's units needed more token-table entries than sized
 };
 
 // Word offsets inside the uncached synchronisation block.
@@ -302,7 +303,6 @@ struct BatchArgs {
     float* out;            // [T][H]
     float* norm;           // [T][H]
     uint16_t* norm3;       // [T][3][H] bf16 pieces of norm
-    uint16_t* xperm3;      // [T*K][3][H] norm3 rows in compact (expert-major) entry order
     float* logits;         // [T][E]
     int32_t* idx;          // [T][K]
     float* wts;            // [T][K]
@@ -315,6 +315,7 @@ struct BatchArgs {
     float* expout;         // [T*K (+T)][H] routed (and MXFP4 shared) expert outputs, compact rows
     uint16_t* smid3;       // [T][3][SI] shared SwiGLU outputs (pieces)
     float* shout;          // [T][H]
+    uint32_t tcap;         // token-table entries per work-group in bup_kernel's LDS (set by launch_batched)
 };
 
 // Launchers (moe_decode.hip).
@@ -364,6 +365,10 @@ int launch_expert_ffn(const uint8_t* blk, uint64_t gw_off, uint64_t gs_off, uint
 // The most routed experts the batched layer supports (its GEMM kernels keep
 // the expert tables in LDS beside the activation slots).
 uint32_t batched_max_experts();
+// Largest batched chunk (tokens per launch) whose gate/up token table fits in
+// LDS beside the activation slots and the expert tables, for a grid of at
+// least `grid` work-groups.
+uint32_t batched_max_tokens(uint32_t I, uint32_t SI, uint32_t E, uint32_t K, uint32_t grid);
 int launch_batched(const DecodeArgs* d_args, const BatchArgs& b, uint32_t H, uint32_t I, uint32_t SI, uint32_t E,
                    uint32_t K, uint32_t n_cu, uint32_t phases, void* stream);
 // The library's static device scratch (noalloc.hip): its device address on

@@ -12,9 +12,11 @@
 //   bcount   per expert: its entries (token*K + slot) in ascending order
 //            (wave ballots, deterministic) and their count
 //   bscatter per expert: its compact range (prefix of the counts), ent/pos
-//   bpermute norm3 rows gathered into expert-major order (xperm3)
 //   bup      gate/up + SwiGLU: shared expert (unit = token pass x 64 rows),
-//            routed experts (unit = expert pass x 4 x 64 rows)
+//            routed experts (unit = expert pass x 4 x 64 rows); a routed
+//            pass's activation DMAs read its tokens' norm3 rows in place,
+//            through a per-work-group table of its units' tokens in LDS, so
+//            no expert-major copy of the activations is made
 //   bdown    down: shared expert (unit = token pass x 128 rows), routed
 //            experts (unit = expert pass x 512 rows)
 //   bcomb    out[t] = (resid[t] +) sum_k w[t][k] e_k[t] (slot order) + shared[t]
@@ -355,21 +357,6 @@ __global__ void __launch_bounds__(256) bscatter_kernel(const BatchArgs b, uint32
     }
 }
 
-// Permute: the pieces of entry c's token into row c of b.xperm3, so each
-// expert's rows are contiguous for the grouped GEMM (the reference's permute
-// step). Grid-stride over (entry, 16-byte chunk).
-__global__ void __launch_bounds__(256) bpermute_kernel(const BatchArgs b, uint32_t H, uint32_t K) {
-    const uint32_t per = 3u * H / 8u;  // 16-byte chunks per row
-    const uint32_t n = b.T * K;
-    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < (uint64_t)n * per;
-         i += (uint64_t)gridDim.x * blockDim.x) {
-        const uint32_t c = (uint32_t)(i / per), q = (uint32_t)(i % per);
-        const uint32_t t = gld(b.ent + c) / K;
-        const u32x4 v = gld16((const uint8_t*)(b.norm3 + (size_t)t * 3u * H) + 16u * q);
-        *(__attribute__((address_space(1))) u32x4*)((uint8_t*)(b.xperm3 + (size_t)c * 3u * H) + 16u * q) = v;
-    }
-}
-
 // ---- pass table ----------------------------------------------------------------
 // Pass table of the routed GEMMs, in LDS: the experts' counts and offsets and
 // the exclusive prefix pp of their passes (cdiv(count, kMT)), pp[E] = all
@@ -495,6 +482,52 @@ WL_DEV Pass pass_at_w(const PassTab& pt, uint32_t E, uint32_t j) {
     return Pass{e, q + (p < r ? 1u : 0u), uni(pt.off[e]) + p * q + min(p, r)};
 }
 
+// ---- token table -------------------------------------------------------------
+// A routed pass's activations are its tokens' rows of norm3, read in place by
+// the DMAs. Before a gate/up pipeline runs, its work-group writes the tokens
+// of its units' passes into LDS, tt[W i + m] = the token of row m of its unit
+// i (W: the pipeline's largest pass), in one round of global loads for the
+// whole pipeline; a unit's bind then reads its lane's two tokens there. (A
+// prefetch into registers would cost a wait at every bind: the compiler does
+// not know how many steps lie between a load and its use.) The host sizes
+// the table (BatchArgs::tcap entries) for the most units a work-group can
+// get (batched_tok_entries); past it, tokens read as 0 and E_TOKTAB is raised.
+template <class Kn>
+WL_DEV void fill_tokens(const Kn& k, uint16_t* tt, uint32_t W) {
+    static_assert(kMT <= 64u && kMTR <= 64u, "one lane per pass row");
+    if (k.nu * W > k.b.tcap && threadIdx.x == 0u) raise_error(k.a.sync, SyncMap::make(), E_TOKTAB, 0u);
+    // wave v takes units v, v + kWaves, ...: unit() takes a uniform index (it
+    // reads the pass table through readfirstlane), lane m the pass row m
+    const uint32_t v = uni(threadIdx.x >> 6), m = threadIdx.x & 63u;
+    constexpr uint32_t R = 4;  // units per wave whose loads are in flight together
+    for (uint32_t i0 = 0; i0 < k.nu; i0 += R * kWaves) {
+        uint32_t ent[R];
+        bool has[R];
+#pragma unroll
+        for (uint32_t r = 0; r < R; r++) {
+            const uint32_t i = i0 + v + kWaves * r;
+            has[r] = false;
+            ent[r] = 0u;
+            if (i < k.nu) {
+                const auto x = k.unit(i);
+                has[r] = x.live && !x.sh && x.e != k.a.E && m < x.nt;
+                if (has[r]) ent[r] = k.b.ent[x.row0 + m];
+            }
+        }
+#pragma unroll
+        for (uint32_t r = 0; r < R; r++) {
+            const uint32_t i = i0 + v + kWaves * r;
+            if (i < k.nu && m < W && W * i + m < k.b.tcap) tt[W * i + m] = (uint16_t)(has[r] ? ent[r] / k.K : 0u);
+        }
+    }
+    lds_barrier();
+}
+// The token of row m (< nt) of this work-group's unit i.
+WL_DEV uint32_t table_token(const uint16_t* tt, uint32_t cap, uint32_t W, uint32_t i, uint32_t m, uint32_t nt) {
+    const uint32_t idx = W * i + min(m, nt - 1u);
+    return idx < cap ? (uint32_t)tt[idx] : 0u;
+}
+
 // ---- grouped GEMMs ------------------------------------------------------------
 // A unit is one token pass (up to kMT tokens: rows [row0, row0 + nt) of a
 // [rows][3][kdim] bf16 piece array) times a block of weight rows, run in nst
@@ -548,29 +581,49 @@ WL_DEV bf16x8 afrag(const uint8_t* sl, uint32_t pc, uint32_t tb, uint32_t hi, ui
     return as_bf16x8(*(const u32x4*)(sl + (pc * 32u + tb * 16u) * kRowB + 256u * hi + lane_off));
 }
 
-// Activation side of a unit: rows [row0, row0 + nt) of a piece array with
-// kdim columns (uniform values; dead: nt = 0). DMA instruction k of wave v
-// writes slot rows 2j and 2j + 1 (j = v + kWaves k; lanes 0-31 the first), so
-// every row a lane writes has R & 15 = x = 2v + (lane >> 5): its 16-byte
-// group (column group cg = p ^ x) and, per layout, its token and piece differ
-// between k only by uniform amounts:
-//   pieces in rows: R = 4m + pc -> m = (x >> 2) + 4k, pc = x & 3;
+// Activation side of a unit: tokens [0, nt) of a pass, each a row of three
+// pieces of kdim columns in a [rows][3][kdim] piece array (uniform values;
+// dead: nt = 0). DMA instruction k of wave v writes slot rows 2j and 2j + 1
+// (j = v + kWaves k; lanes 0-31 the first), so every row a lane writes has
+// R & 15 = x = 2v + (lane >> 5): its 16-byte group (column group cg = p ^ x)
+// is the same for every k, and per layout its token and piece are
+//   pieces in rows: R = 4m + pc -> m = (x >> 2) + 4k, pc = x & 3 (a pass of
+//                   at most kPR = 8 tokens: only k = 0, 1 have live rows);
 //   tokens in rows: R = 32 pc + m -> m = x + 16 (k & 1), pc = k >> 1.
-// So one lane offset per unit (base, at k = 0) plus a uniform offset per k.
+// Either way a lane's DMAs read two tokens' rows, at lane offsets base[k & 1]
+// (the token's row, at piece x & 3 or 0), plus the uniform piece offset
+// (k >> 1) kd2 with tokens in rows. The tokens' rows are consecutive rows of
+// the array (a_bind) or any rows (a_bind_rows: a routed pass's tokens' rows
+// of norm3, read in place).
 struct AStream {
     rsrc_t rs;
-    uint32_t base, nt, kd2;  // lane byte offset at k = 0, tokens, bytes per piece row
+    uint32_t base[2], nt, kd2;  // lane byte offsets of the two tokens' rows, tokens, bytes per piece row
     bool pr;
 };
 WL_DEV uint32_t a_x() { return 2u * uni(threadIdx.x >> 6) + ((threadIdx.x & 63u) >> 5); }
-WL_DEV void a_bind(AStream& A, const uint16_t* base, uint64_t bytes, uint32_t row0, uint32_t nt, bool pr,
-                   uint32_t kdim) {
+// The pass rows (tokens m0, m1 of the pass) this lane's DMAs write.
+WL_DEV void a_rows(bool pr, uint32_t& m0, uint32_t& m1) {
+    const uint32_t x = a_x();
+    m0 = pr ? x >> 2 : x;
+    m1 = pr ? (x >> 2) + 4u : x + 16u;
+}
+// row[j]: the array row of the lane's token m_j (a_rows).
+WL_DEV void a_bind_rows(AStream& A, const uint16_t* base, uint64_t bytes, const uint32_t (&row)[2], uint32_t nt,
+                        bool pr, uint32_t kdim) {
     A.rs = make_rsrc(base, (uint32_t)bytes);
     A.nt = nt;
     A.kd2 = 2u * kdim;
     A.pr = pr;
     const uint32_t x = a_x(), cg = (threadIdx.x & 31u) ^ x;
-    A.base = ((row0 + (pr ? x >> 2 : x)) * 3u + (pr ? x & 3u : 0u)) * A.kd2 + 16u * cg;
+#pragma unroll
+    for (uint32_t j = 0; j < 2; j++) A.base[j] = (row[j] * 3u + (pr ? x & 3u : 0u)) * A.kd2 + 16u * cg;
+}
+WL_DEV void a_bind(AStream& A, const uint16_t* base, uint64_t bytes, uint32_t row0, uint32_t nt, bool pr,
+                   uint32_t kdim) {
+    uint32_t m0, m1;
+    a_rows(pr, m0, m1);
+    const uint32_t row[2] = {row0 + m0, row0 + m1};
+    a_bind_rows(A, base, bytes, row, nt, pr, kdim);
 }
 WL_DEV void a_none(AStream& A) { a_bind(A, nullptr, 0u, 0u, 0u, true, 0u); }
 // DMA instruction k of one step (columns [k0, k0 + kKC)); absent rows
@@ -579,10 +632,10 @@ template <int S>
 WL_DEV void a_issue_one(const AStream& A, uint32_t k0, uint32_t k) {
     const uint32_t v = uni(threadIdx.x >> 6), x = a_x();
     const bool ok = A.pr ? (x >> 2) + 4u * k < A.nt && (x & 3u) < 3u : x + 16u * (k & 1u) < A.nt;
-    const uint32_t so = 2u * k0 + (A.pr ? 12u * k : 48u * (k & 1u) + (k >> 1)) * A.kd2;
+    const uint32_t so = 2u * k0 + (A.pr ? 0u : (k >> 1) * A.kd2);
     __builtin_amdgcn_raw_ptr_buffer_load_lds(
         A.rs, (__attribute__((address_space(3))) void*)(slot<S>() + (v + kWaves * k) * 2u * kRowB), 16u,
-        ok ? A.base : kOOBV, so, 0, 0);
+        ok ? A.base[k & 1u] : kOOBV, so, 0, 0);
 }
 template <int S>
 WL_DEV void a_issue(const AStream& A, uint32_t k0) {
@@ -600,17 +653,25 @@ WL_DEV void a_issue(const AStream& A, uint32_t k0) {
 constexpr uint32_t kRowBW = 2u * kKCW;
 static_assert(3u * kMTW * kRowBW == kSlotB, "a wide step fills one slot");
 static_assert(3u * kMTW * kRowBW / 1024u / kWaves == kDma, "a wide step takes kDma DMAs per wave");
+// A lane's two tokens r0 and r0 + 32 have lane offsets base[0], base[1]
+// (their rows at piece 0: consecutive rows of the array, or any rows).
 struct AStreamW {
     rsrc_t rs;
-    uint32_t base, nt, kd2;  // lane byte offset at k = 0, tokens, bytes per piece row
+    uint32_t base[2], nt, kd2;  // lane byte offsets of the two tokens' rows, tokens, bytes per piece row
 };
 WL_DEV uint32_t aw_r0() { return 4u * uni(threadIdx.x >> 6) + ((threadIdx.x & 63u) >> 4); }
-WL_DEV void aw_bind(AStreamW& A, const uint16_t* base, uint64_t bytes, uint32_t row0, uint32_t nt, uint32_t kdim) {
+WL_DEV void aw_bind_rows(AStreamW& A, const uint16_t* base, uint64_t bytes, const uint32_t (&row)[2], uint32_t nt,
+                         uint32_t kdim) {
     A.rs = make_rsrc(base, (uint32_t)bytes);
     A.nt = nt;
     A.kd2 = 2u * kdim;
     const uint32_t r0 = aw_r0(), cg = (threadIdx.x & 15u) ^ (r0 & 15u);
-    A.base = (row0 + r0) * 3u * A.kd2 + 16u * cg;
+#pragma unroll
+    for (uint32_t j = 0; j < 2; j++) A.base[j] = row[j] * 3u * A.kd2 + 16u * cg;
+}
+WL_DEV void aw_bind(AStreamW& A, const uint16_t* base, uint64_t bytes, uint32_t row0, uint32_t nt, uint32_t kdim) {
+    const uint32_t r0 = aw_r0(), row[2] = {row0 + r0, row0 + r0 + 32u};
+    aw_bind_rows(A, base, bytes, row, nt, kdim);
 }
 // The kDma DMAs of one wide step (columns [k0, k0 + kKCW)); absent rows land
 // as zeros.
@@ -620,10 +681,10 @@ WL_DEV void aw_issue(const AStreamW& A, uint32_t k0) {
 #pragma unroll
     for (uint32_t k = 0; k < kDma; k++) {
         const bool ok = r0 + 32u * (k & 1u) < A.nt;
-        const uint32_t so = 2u * k0 + (96u * (k & 1u) + (k >> 1)) * A.kd2;
+        const uint32_t so = 2u * k0 + (k >> 1) * A.kd2;
         __builtin_amdgcn_raw_ptr_buffer_load_lds(
             A.rs, (__attribute__((address_space(3))) void*)(slot<S>() + (v + kWaves * k) * 1024u), 16u,
-            ok ? A.base : kOOBV, so, 0, 0);
+            ok ? A.base[k & 1u] : kOOBV, so, 0, 0);
     }
 }
 // Lane (m, g) A fragment of row 64 pc + 16 tb + m at column group cg (< 16):
@@ -786,6 +847,13 @@ WL_DEV const uint8_t* const* load_slot_tab(const DecodeArgs& a, uint32_t E, bool
 }
 // LDS of the tables for E experts and the MXFP4 shared pseudo-expert.
 __host__ __device__ inline size_t gemm_tab_bytes(uint32_t E) { return 8u * (E + 1u) + 4u * (4u * (E + 1u) + 2u); }
+// The gate/up kernel's token table follows them (16-byte aligned).
+__host__ __device__ inline size_t tok_table_offset(uint32_t E) { return (gemm_tab_bytes(E) + 15u) & ~(size_t)15u; }
+// The dynamic LDS of the kernel (every extern __shared__ array starts there).
+WL_DEV uint8_t* dyn_lds() {
+    extern __shared__ __align__(16) uint8_t dyn_base[];
+    return dyn_base;
+}
 
 // Splits x into its three bf16 pieces at p[0], p[stride], p[2 stride].
 WL_DEV void store3(uint16_t* p, uint32_t stride, float x) {
@@ -828,8 +896,11 @@ struct UpK {
     const uint8_t* const* stab;
     NativeLayout NL;
     Cursor ca, cw, cc;
-    // weight stream
-    rsrc_t wrs, srs;
+    // weight stream: the block and the scale stream's (null: none), kept as
+    // pointers and sizes (see DownK)
+    const uint8_t* wbase;
+    const uint8_t* sbase;
+    uint32_t wbytes, sbytes;
     bool wsh;
     uint32_t wpart, wvoff, vgu, vgus, vsh;
     // A fragment lane offsets: routed k step jj (cg = 16 q + 4 g + jj), shared
@@ -840,6 +911,7 @@ struct UpK {
     PassShape cps;
     uint32_t cvar;  // compute variant: 0/1 pieces in rows, 1/2 blocks; 2/3 tokens in rows, 1/2 blocks
     f32x4 acc[kSG][2];
+    const uint16_t* tt;  // the token table (kMT entries per unit)
 
     WL_MEM UnitInfo unit(uint32_t i) const {
         UnitInfo x{false, false, 0u, 0u, 0u, 0u};
@@ -868,7 +940,12 @@ struct UpK {
         const bool pr = pass_shape(x.nt).pr;
         if (x.sh) a_bind(A, b.norm3, (uint64_t)b.T * 6u * H, x.row0, x.nt, pr, H);
         else if (x.e == a.E) a_bind(A, b.norm3, (uint64_t)b.T * 6u * H, x.row0 - b.T * K, x.nt, pr, H);  // MXFP4 shared
-        else a_bind(A, b.xperm3, (uint64_t)b.T * K * 6u * H, x.row0, x.nt, pr, H);
+        else {
+            uint32_t m0, m1;
+            a_rows(pr, m0, m1);
+            const uint32_t row[2] = {table_token(tt, b.tcap, kMT, i, m0, x.nt), table_token(tt, b.tcap, kMT, i, m1, x.nt)};
+            a_bind_rows(A, b.norm3, (uint64_t)b.T * 6u * H, row, x.nt, pr, H);
+        }
     }
     WL_MEM void bind_w(uint32_t i) {
         const UnitInfo x = unit(i);
@@ -876,10 +953,10 @@ struct UpK {
         wpart = x.part;
         const NativeShared NS = NativeShared::make(H, SI);
         const uint8_t* blk = x.live && !x.sh ? uni_ptr(stab[x.e]) : nullptr;
-        wrs = !x.live ? make_rsrc(nullptr, 0u)
-              : x.sh  ? make_rsrc(a.sh_native + NS.sgu, (uint32_t)(NS.sdn - NS.sgu))
-                      : make_rsrc(blk, blk ? (uint32_t)NL.total : 0u);
-        srs = x.live && !x.sh ? wrs : make_rsrc(nullptr, 0u);
+        wbase = !x.live ? nullptr : x.sh ? a.sh_native + NS.sgu : blk;
+        wbytes = !x.live ? 0u : x.sh ? (uint32_t)(NS.sdn - NS.sgu) : blk ? (uint32_t)NL.total : 0u;
+        sbase = x.live && !x.sh ? blk : nullptr;
+        sbytes = x.live && !x.sh && blk ? (uint32_t)NL.total : 0u;
         wvoff = x.sh ? vsh : vgu;  // chosen here, not per load (see DownK::bind_w)
     }
     WL_MEM void issue_w_one(uint32_t s, WBuf& W, uint32_t j) const {
@@ -887,9 +964,9 @@ struct UpK {
             const uint32_t sl = min(wpart * kSG + j / 2u, S - 1u);
             const uint32_t ro = sl * 8u * nkg * 1024u + min(2u * s + j % 2u, nkg - 1u) * 1024u;
             const uint32_t so = wpart * 8u * nkt * 1024u + min(8u * s + j, nkt - 1u) * 1024u;
-            W.w[j] = bld16_nt(wrs, wvoff, wsh ? so : ro);
+            W.w[j] = bld16_nt(make_rsrc(wbase, wbytes), wvoff, wsh ? so : ro);
         } else {
-            bld8(srs, vgus, (wpart * 8u * nst + s) * 512u, W.s);
+            bld8(make_rsrc(sbase, sbytes), vgus, (wpart * 8u * nst + s) * 512u, W.s);
         }
     }
     WL_MEM void begin(uint32_t i) {
@@ -1011,7 +1088,8 @@ struct SharedUpW {
     const BatchArgs& b;
     uint32_t H, SI, nkt, nsl, npair, npass, nst, nu, v, lane;
     Cursor ca, cw, cc;
-    rsrc_t wrs;
+    const uint8_t* wbase;  // the weight stream's block and size (see DownK)
+    uint32_t wbytes;
     uint32_t wpair, vbase;
     uint32_t lob;  // A fragment lane offset of k step 0 (cg = g; k step k: ^ 64 k)
     uint32_t cpair, cnt, crow0, cnb;
@@ -1039,12 +1117,13 @@ struct SharedUpW {
     WL_MEM void bind_w(uint32_t i) {
         const Unit x = unit(i);
         const NativeShared NS = NativeShared::make(H, SI);
-        wrs = x.live ? make_rsrc(a.sh_native + NS.sgu, (uint32_t)(NS.sdn - NS.sgu)) : make_rsrc(nullptr, 0u);
+        wbase = x.live ? a.sh_native + NS.sgu : nullptr;
+        wbytes = x.live ? (uint32_t)(NS.sdn - NS.sgu) : 0u;
         wpair = x.pair;
     }
     WL_MEM void issue_w_one(uint32_t s, WBufW& W, uint32_t j) const {
         const uint32_t T = 8u * min(2u * wpair + j / 4u, nsl - 1u) + v;
-        W.w[j] = bld16(wrs, vbase, (T * nkt + 4u * s + j % 4u) * 1024u);  // re-read by every pass: cached
+        W.w[j] = bld16(make_rsrc(wbase, wbytes), vbase, (T * nkt + 4u * s + j % 4u) * 1024u);  // re-read by every pass: cached
     }
     WL_MEM void begin(uint32_t i) {
         const Unit x = unit(i);
@@ -1155,12 +1234,14 @@ struct RoutedUpW {
     const uint8_t* const* stab;
     NativeLayout NL;
     Cursor ca, cw, cc;
-    rsrc_t wrs;
+    const uint8_t* wbase;  // the weight stream's block and size (see DownK)
+    uint32_t wbytes;
     uint32_t wpart, vgu, vgus;
     uint32_t lob;  // A fragment lane offset of k step 0 (cg = 4g; k step jj: ^ 16 jj)
     UnitInfo cu;
     uint32_t cnb;
     f32x4 acc[kSG][3];
+    const uint16_t* tt;  // the token table (kMTR entries per unit)
 
     WL_MEM UnitInfo unit(uint32_t i) const {
         UnitInfo x{false, false, 0u, 0u, 0u, 0u};
@@ -1179,20 +1260,26 @@ struct RoutedUpW {
         const UnitInfo x = unit(i);
         if (!x.live) return aw_bind(A, nullptr, 0u, 0u, 0u, 0u);
         if (x.e == a.E) aw_bind(A, b.norm3, (uint64_t)b.T * 6u * H, x.row0 - b.T * K, x.nt, H);  // MXFP4 shared
-        else aw_bind(A, b.xperm3, (uint64_t)b.T * K * 6u * H, x.row0, x.nt, H);
+        else {
+            const uint32_t r0 = aw_r0();
+            const uint32_t row[2] = {table_token(tt, b.tcap, kMTR, i, r0, x.nt),
+                                     table_token(tt, b.tcap, kMTR, i, r0 + 32u, x.nt)};
+            aw_bind_rows(A, b.norm3, (uint64_t)b.T * 6u * H, row, x.nt, H);
+        }
     }
     WL_MEM void bind_w(uint32_t i) {
         const UnitInfo x = unit(i);
         const uint8_t* blk = x.live ? uni_ptr(stab[x.e]) : nullptr;
-        wrs = make_rsrc(blk, blk ? (uint32_t)NL.total : 0u);
+        wbase = blk;
+        wbytes = blk ? (uint32_t)NL.total : 0u;
         wpart = x.part;
     }
     WL_MEM void issue_w_one(uint32_t s, WB& W, uint32_t j) const {
         if (j < kSG) {
             const uint32_t sl = min(wpart * kSG + j, S - 1u);
-            W.w[j] = bld16_nt(wrs, vgu, sl * 8u * nkg * 1024u + s * 1024u);
+            W.w[j] = bld16_nt(make_rsrc(wbase, wbytes), vgu, sl * 8u * nkg * 1024u + s * 1024u);
         } else {
-            bld8(wrs, vgus, (wpart * 8u * nst2 + s / 2u) * 512u, W.s);
+            bld8(make_rsrc(wbase, wbytes), vgus, (wpart * 8u * nst2 + s / 2u) * 512u, W.s);
         }
     }
     WL_MEM void begin(uint32_t i) {
@@ -1290,6 +1377,9 @@ WL_DEV uint32_t run_routed_up_wide(const DecodeArgs& a, const BatchArgs& b, cons
     w.vgu = (uint32_t)w.NL.gu + w.v * w.nkg * 1024u + 16u * w.lane;
     w.vgus = (uint32_t)w.NL.bgus + w.v * w.nst2 * 512u + 8u * w.lane;
     w.lob = aw_lane_off(4u * (w.lane >> 4));
+    uint16_t* tt = (uint16_t*)(dyn_lds() + tok_table_offset(a.E));
+    w.tt = tt;
+    fill_tokens(w, tt, kMTR);
     run_steps(w);
     return U;
 }
@@ -1339,6 +1429,9 @@ __global__ void __launch_bounds__(kThreads) bup_kernel(const DecodeArgs* __restr
         k.lo_r[j] = a_lane_off(4u * k.g + j);
         k.lo_s[j] = a_lane_off(4u * j + k.g);
     }
+    uint16_t* tt = (uint16_t*)(dyn + tok_table_offset(a.E));
+    k.tt = tt;
+    fill_tokens(k, tt, kMT);
     run_steps(k);
 }
 
@@ -2099,6 +2192,35 @@ __global__ void __launch_bounds__(256) bcomb_kernel(const BatchArgs b, uint32_t 
     *(float4*)(b.out + (size_t)t * H + r) = acc;
 }
 
+// Token-table entries a work-group of the gate/up kernel can need for T
+// tokens (an upper bound over every routing): the kMT pipeline's units are at
+// most the shared passes' cdiv(T, kMT) x SI / kSlice plus P x NSG for
+// P <= cdiv(T (K + 1), kMT) + E + 1 passes (each expert adds at most one
+// partial pass; K + 1 counts an MXFP4 shared expert's rows), the wide
+// pipeline's at most Pw x NSG for Pw <= R / kMTR + R / (kMT + 1) + 1 passes
+// (R = T (K + 1) rows; only experts of more than kMT rows have wide passes,
+// cdiv(c, kMTR) each); a work-group gets at most cdiv(units, grid).
+static uint32_t batched_tok_entries(uint32_t T, uint32_t I, uint32_t SI, uint32_t E, uint32_t K, uint32_t grid) {
+    auto cd = [](uint64_t a, uint64_t b) { return (a + b - 1u) / b; };
+    const uint64_t R = (uint64_t)T * (K + 1u), NSG = cd(I / kSlice, kSG);
+    const uint64_t units = cd(T, kMT) * (SI / kSlice) + (cd(R, kMT) + E + 1u) * NSG;
+    const uint64_t wunits = (R / kMTR + R / (kMT + 1u) + 1u) * NSG;
+    return (uint32_t)std::max(cd(units, grid) * kMT, cd(wunits, grid) * kMTR);
+}
+static size_t bup_lds(uint32_t T, uint32_t I, uint32_t SI, uint32_t E, uint32_t K, uint32_t grid) {
+    return tok_table_offset(E) + 2u * (size_t)batched_tok_entries(T, I, SI, E, K, grid);
+}
+uint32_t batched_max_tokens(uint32_t I, uint32_t SI, uint32_t E, uint32_t K, uint32_t grid) {
+    const size_t room = (size_t)decode_max_lds() - 3u * (size_t)kSlotB;
+    uint32_t lo = 0, hi = 1u << 16;
+    while (lo < hi) {
+        const uint32_t mid = (lo + hi + 1u) / 2u;
+        if (bup_lds(mid, I, SI, E, K, grid) <= room) lo = mid;
+        else hi = mid - 1u;
+    }
+    return lo;
+}
+
 uint32_t batched_max_experts() {
     // the GEMM kernels' LDS: the three activation slots and the expert tables
     const size_t lds = (size_t)decode_max_lds(), ring = 3u * (size_t)kSlotB;
@@ -2113,6 +2235,12 @@ int launch_batched(const DecodeArgs* d_args, const BatchArgs& b, uint32_t H, uin
     hipError_t e;
     const size_t topk_lds = 4u * (2u * E + 64u);
     const size_t gemm_lds = gemm_tab_bytes(E);
+    // the gate/up kernel's token table, sized for this call and a grid of
+    // n_cu or more work-groups
+    BatchArgs bt = b;
+    bt.tcap = batched_tok_entries(b.T, I, SI, E, K, n_cu);
+    const size_t up_lds = bup_lds(b.T, I, SI, E, K, n_cu);
+    if (up_lds + 3u * (size_t)kSlotB > (size_t)decode_max_lds()) return (int)hipErrorInvalidValue;
     // the GEMM kernels' wide units take their shape parameters as constants
     // at the GLM shape
     const bool glm = H == 6144u && I == 2048u && SI == 2048u && K == 8u;
@@ -2126,19 +2254,18 @@ int launch_batched(const DecodeArgs* d_args, const BatchArgs& b, uint32_t H, uin
     const void* down = glm ? (small ? (const void*)bdown_kernel<true, true> : (const void*)bdown_kernel<true, false>)
                            : (small ? (const void*)bdown_kernel<false, true> : (const void*)bdown_kernel<false, false>);
     const struct { const void* fn; size_t lds; } attrs[] = {
-        {(const void*)btopk_kernel, topk_lds}, {up, gemm_lds}, {down, gemm_lds}};
+        {(const void*)btopk_kernel, topk_lds}, {up, up_lds}, {down, gemm_lds}};
     for (const auto& at : attrs)
         if ((e = hipFuncSetAttribute(at.fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)at.lds)) != hipSuccess)
             return (int)e;
     // The GEMM kernels walk their units with a grid stride, so their grid is
     // what the chip holds at once (the LDS ring allows one work-group per CU);
     // a larger grid would leave its second part waiting for the first.
-    auto resident = [&](const void* fn) {
+    auto resident = [&](const void* fn, size_t lds) {
         int nb = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, fn, kThreads, gemm_lds) != hipSuccess || nb < 1) nb = 1;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, fn, kThreads, lds) != hipSuccess || nb < 1) nb = 1;
         return n_cu * (uint32_t)nb;
     };
-    const uint32_t nperm = b.T * K * (3u * H / 8u);
     if (phases & kPhaseRoute) {
         hipLaunchKernelGGL(bnorm_kernel, dim3(b.T), dim3(kThreads), 0, s, d_args, b);
         // router: ~one work-group per CU; each token block's rows split over gx
@@ -2149,21 +2276,20 @@ int launch_batched(const DecodeArgs* d_args, const BatchArgs& b, uint32_t H, uin
         hipLaunchKernelGGL(btopk_kernel, dim3(b.T), dim3(kThreads), topk_lds, s, d_args, b);
         hipLaunchKernelGGL(bcount_kernel, dim3(E), dim3(64), 0, s, b, K);
         hipLaunchKernelGGL(bscatter_kernel, dim3(E), dim3(256), 0, s, b, E);
-        hipLaunchKernelGGL(bpermute_kernel, dim3(std::min((nperm + 255u) / 256u, 8u * n_cu)), dim3(256), 0, s, b, H, K);
     }
     if (phases & kPhaseGemm) {
         // the shared expert's wide units when they fill the grid
-        BatchArgs bw = b;
-        const uint32_t gu = resident(up), gd = resident(down);
+        BatchArgs bw = bt;
+        const uint32_t gu = resident(up, up_lds), gd = resident(down, gemm_lds);
         const bool bf16_sh = !(b.flags & (kBatchNoShared | kBatchShared4));
         if (bf16_sh && (b.T + kMTW - 1u) / kMTW * ((SI / kSlice + 1u) / 2u) >= gu) bw.flags |= kBatchWideSharedUp;
         if (bf16_sh && (b.T + kMTW - 1u) / kMTW * ((H + 255u) / 256u) >= gd) bw.flags |= kBatchWideSharedDown;
         if (glm) {
-            hipLaunchKernelGGL(bup_kernel<true>, dim3(gu), dim3(kThreads), gemm_lds, s, d_args, bw);
+            hipLaunchKernelGGL(bup_kernel<true>, dim3(gu), dim3(kThreads), up_lds, s, d_args, bw);
             if (small) hipLaunchKernelGGL((bdown_kernel<true, true>), dim3(gd), dim3(kThreads), gemm_lds, s, d_args, bw);
             else hipLaunchKernelGGL((bdown_kernel<true, false>), dim3(gd), dim3(kThreads), gemm_lds, s, d_args, bw);
         } else {
-            hipLaunchKernelGGL(bup_kernel<false>, dim3(gu), dim3(kThreads), gemm_lds, s, d_args, bw);
+            hipLaunchKernelGGL(bup_kernel<false>, dim3(gu), dim3(kThreads), up_lds, s, d_args, bw);
             if (small) hipLaunchKernelGGL((bdown_kernel<false, true>), dim3(gd), dim3(kThreads), gemm_lds, s, d_args, bw);
             else hipLaunchKernelGGL((bdown_kernel<false, false>), dim3(gd), dim3(kThreads), gemm_lds, s, d_args, bw);
         }

@@ -1107,7 +1107,6 @@ static size_t batch_layout(const wl_ctx* c, uint32_t T, uint8_t* base, wl::Batch
     wl::BatchArgs& x = b ? *b : d;
     take(&x.norm, 4 * t * H);
     take(&x.norm3, 6 * t * H);
-    take(&x.xperm3, 6 * t * K * H);
     take(&x.logits, 4 * t * E);
     take(&x.idx, 4 * t * K);
     take(&x.wts, 4 * t * K);
@@ -1186,11 +1185,14 @@ static wl_status batched_check(wl_ctx* c, uint32_t layer, uint32_t n_tokens, con
 }
 
 // Chunk cap that keeps every piece array of the kernels under 2 GB (they
-// address them with 32-bit buffer offsets).
+// address them with 32-bit buffer offsets) and the gate/up kernel's token
+// table within its LDS.
 static uint32_t batch_offset_cap(const wl_ctx* c) {
     const uint64_t H = c->cfg.hidden, K = c->cfg.n_experts_per_tok + (c->any_sh4 ? 1u : 0u);
     const uint64_t row = 6ull * K * std::max<uint64_t>(std::max<uint64_t>(H, c->cfg.moe_inter), c->SI);
-    return (uint32_t)std::min<uint64_t>(kBatchChunk, ((1ull << 31) - 1) / row);
+    const uint32_t lds = wl::batched_max_tokens(c->cfg.moe_inter, c->SI, c->cfg.n_routed_experts,
+                                                c->cfg.n_experts_per_tok, (uint32_t)c->n_cu);
+    return (uint32_t)std::min<uint64_t>(std::min<uint64_t>(kBatchChunk, lds), ((1ull << 31) - 1) / row);
 }
 
 // The GEMMs of a source-backed batched chunk (routing already enqueued): read
@@ -1751,10 +1753,11 @@ wl_status wl_check_error(wl_ctx* c, void* stream) {
         (void)hipMemset(c->part, 0, 4 * wl::part_words(c->cfg.hidden, c->grid));
         (void)hipMemset(c->tsh, 0, 4 * wl::part_words(c->cfg.hidden, c->grid));
         (void)hipDeviceSynchronize();
-        return fail(c, WL_ERR_DEVICE, "device error bits 0x%x%s%s%s", flag,
+        return fail(c, WL_ERR_DEVICE, "device error bits 0x%x%s%s%s%s", flag,
                     (flag & wl::E_SPIN) ? " [dependency wait expired]" : "",
                     (flag & wl::E_NOT_RESIDENT) ? " [routed expert not resident]" : "",
-                    (flag & wl::E_XCD) ? " [work-group not on XCD w mod 8: set WL_DECODE_XL2=0]" : "");
+                    (flag & wl::E_XCD) ? " [work-group not on XCD w mod 8: set WL_DECODE_XL2=0]" : "",
+                    (flag & wl::E_TOKTAB) ? " [batched token table overflow]" : "");
     }
     return WL_OK;
 }

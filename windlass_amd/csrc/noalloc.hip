@@ -17,7 +17,7 @@
 
 namespace wl {
 
-// 64 MiB: the batched layer's scratch for 97 tokens per chunk at the GLM shape
+// 64 MiB: the batched layer's scratch for 169 tokens per chunk at the GLM shape
 // (hidden 6144, inter 2048, 8 of 256 experts).
 constexpr size_t kScratchBytes = 64ull << 20;
 
