@@ -293,7 +293,7 @@ enum : uint32_t {
 // takes that kernel's small-expert instantiation; its pass table leaves them
 // out of the other pipelines.
 constexpr uint32_t kSmallT = 4;
-// launch_batched phases: routing (norm .. permute), the GEMMs, the combine.
+// launch_batched phases: routing (norm .. scatter), the GEMMs, the combine.
 enum : uint32_t { kPhaseRoute = 1u, kPhaseGemm = 2u, kPhaseCombine = 4u, kPhaseAll = 7u };
 struct BatchArgs {
     uint32_t T;

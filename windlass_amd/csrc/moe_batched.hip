@@ -1383,7 +1383,248 @@ WL_DEV uint32_t run_routed_up_wide(const DecodeArgs& a, const BatchArgs& b, cons
     run_steps(w);
     return U;
 }
+// ---- routed gate/up of small experts -----------------------------------------
+// Experts with 1..kSmallT tokens run their gate/up as streaming units, like
+// the decode kernel's gate/up phase: unit (expert, part of kSG slices). The
+// three LDS slots hold the expert's tokens' pieces for the whole K = H =
+// 3 x 2048 columns, slot C columns [2048 C, +2048): stored row Rs = 3m + pc
+// (token m, piece pc; 4096 bytes), its 16-byte group p holding logical group
+// p ^ Rs (the 16 rows an A fragment reads at one column fall in different
+// bank groups). MFMA row n = 4m + pc reads stored row 3m + min(pc, 2) (rows
+// 4m + 3 and tokens past nt carry values no output reads). Each wave streams
+// its tiles of the unit's kSG slices (the GEMM kernel's native gu chunks and
+// batched scale words) two 256-column steps ahead with no barrier inside a
+// chunk; at each chunk boundary the waves meet once, and the slot the last
+// chunk used takes the next unit's rows (DMA), so a unit's pieces are in
+// LDS a chunk and more before its steps reach them:
+//   before chunk 0 of unit u: slot 2 <- unit u, chunk 2;
+//   before chunk 1:           slot 0 <- unit u + 1, chunk 0;
+//   before chunk 2:           slot 1 <- unit u + 1, chunk 1.
+// The per-step arithmetic is the GEMM kernel's for a pass of pieces in rows
+// (one row block). The small-expert list (expert, its tokens, first compact
+// entry, count) lives where the pass table was, after the GEMM pipelines.
+constexpr uint32_t kSUC = 2048;  // columns per slot (chunk)
+__host__ __device__ inline bool small_up_fits(uint32_t H, uint32_t I) {
+    return H == 3u * kSUC && I % (kSlice * kSG) == 0u && 12u * 2u * kSUC <= kSlotB;
+}
+struct SmallExp {
+    uint16_t tok[kSmallT];
+    uint16_t c0, nt;
+    uint32_t e;
+};
+static_assert(sizeof(SmallExp) == 16u, "16 bytes per small expert");
 template <bool GLM>
+WL_DEV uint32_t run_small_up(const DecodeArgs& a, const BatchArgs& b, const uint8_t* const* stab, uint32_t uoff,
+                             SmallExp* se, uint32_t* wcnt) {
+    const uint32_t H = GLM ? 6144u : a.H, I = GLM ? 2048u : a.I, E = a.E, K = GLM ? 8u : a.K;
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, v = uni(tid >> 6), n = lane & 15u, g = lane >> 4;
+    const bool skip = (b.flags & kBatchSkipUnbound) != 0u;
+    // the list: wave v takes experts v, v + 8, ... in blocks of 64 (ballot
+    // order within a block), the blocks' counts summed in LDS
+    {
+        uint32_t run = 0;
+        for (uint32_t e0 = 64u * v; e0 < E; e0 += 64u * kWaves) {
+            const uint32_t e = e0 + lane;
+            const uint32_t c = e < E ? gld(b.counts + e) : 0u;
+            const bool sm = c >= 1u && c <= kSmallT && !(skip && stab[e] == nullptr);
+            run += (uint32_t)__popcll(__ballot(sm));
+        }
+        if (lane == 0u) wcnt[v] = run;
+    }
+    lds_barrier();
+    uint32_t base = 0, ns = 0;
+    for (uint32_t w = 0; w < kWaves; w++) {
+        const uint32_t c = uni(wcnt[w]);
+        base += w < v ? c : 0u;
+        ns += c;
+    }
+    {
+        uint32_t run = base;
+        for (uint32_t e0 = 64u * v; e0 < E; e0 += 64u * kWaves) {
+            const uint32_t e = e0 + lane;
+            const uint32_t c = e < E ? gld(b.counts + e) : 0u;
+            const bool sm = c >= 1u && c <= kSmallT && !(skip && stab[e] == nullptr);
+            const uint64_t bal = __ballot(sm);
+            if (sm) {
+                SmallExp x;
+                const uint32_t c0 = gld(b.offsets + e);
+#pragma unroll
+                for (uint32_t m = 0; m < kSmallT; m++) x.tok[m] = (uint16_t)(gld(b.ent + c0 + min(m, c - 1u)) / K);
+                x.c0 = (uint16_t)c0;
+                x.nt = (uint16_t)c;
+                x.e = e;
+                se[run + (uint32_t)__popcll(bal & ((1ull << lane) - 1ull))] = x;
+            }
+            run += (uint32_t)__popcll(bal);
+        }
+    }
+    lds_barrier();
+    const uint32_t S = I / kSlice, NSG = cdiv(S, kSG), U = ns * NSG, G = gridDim.x;
+    const uint32_t nkg = H / 128u, nst = H / kKC;  // 128-column k tiles, 256-column steps
+    const NativeLayout NL = NativeLayout::make(H, I);
+    const uint32_t vgu = (uint32_t)NL.gu + v * nkg * 1024u + 16u * lane;
+    const uint32_t vgus = (uint32_t)NL.bgus + v * nst * 512u + 8u * lane;
+    const rsrc_t nrs = make_rsrc(b.norm3, b.T * 6u * H);
+    // A fragment of lane (n, g): stored row of MFMA row n, logical groups
+    // 32 s + 16 q + 4 g + jj of the chunk
+    const uint32_t rs_n = 3u * (n >> 2) + min(n & 3u, 2u);
+    uint32_t lo[4];
+#pragma unroll
+    for (uint32_t jj = 0; jj < 4; jj++) lo[jj] = rs_n * 4096u + 16u * ((4u * g + jj) ^ rs_n);
+    struct Unit {
+        const uint8_t* blk;
+        uint32_t part, c0, nt;
+        uint32_t tok[kSmallT];
+    };
+    auto unit = [&](uint32_t r, Unit& x) {
+        x.blk = nullptr;
+        x.part = 0u;
+        x.c0 = 0u;
+        x.nt = 0u;
+        if (r >= U) return;
+        const uint32_t j = r / NSG;
+        const SmallExp* q = se + j;
+        x.part = r % NSG;
+        x.blk = uni_ptr(stab[uni(q->e)]);
+        x.c0 = uni(q->c0);
+        x.nt = uni(q->nt);
+#pragma unroll
+        for (uint32_t m = 0; m < kSmallT; m++) x.tok[m] = uni(q->tok[m]);
+    };
+    // slot C (C a constant once inlined)
+    auto slot_c = [](uint32_t C) { return C == 0u ? slot<0>() : C == 1u ? slot<1>() : slot<2>(); };
+    // DMA of unit x's chunk C into slot C: instruction k of wave v writes
+    // segment q = v + kWaves k (stored row q / 4, its 1 KB quarter q % 4)
+    auto dma = [&](uint32_t C, const Unit& x) {
+#pragma unroll
+        for (uint32_t k = 0; k < 6u; k++) {
+            const uint32_t q = v + kWaves * k, rs = q >> 2, seg = q & 3u, m = rs / 3u, pc = rs % 3u;
+            const bool ok = x.blk != nullptr && m < x.nt;
+            const uint32_t t = m == 0u ? x.tok[0] : m == 1u ? x.tok[1] : m == 2u ? x.tok[2] : x.tok[3];
+            const uint32_t so = ((t * 3u + pc) * H + C * kSUC) * 2u + seg * 1024u;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                nrs, (__attribute__((address_space(3))) void*)(slot_c(C) + rs * 4096u + seg * 1024u), 16u,
+                ok ? 16u * (lane ^ rs) : kOOBV, ok ? so : 0u, 0, 0);
+        }
+    };
+    struct WB {
+        u32x4 w[kWL];
+        uint32_t s[2];
+    };
+    auto issue = [&](const Unit& x, uint32_t st, WB& W) {
+        const rsrc_t wr = make_rsrc(x.blk, x.blk ? (uint32_t)NL.total : 0u);
+#pragma unroll
+        for (uint32_t j = 0; j < kWL; j++) {
+            const uint32_t sl = min(x.part * kSG + j / 2u, S - 1u);
+            W.w[j] = bld16_nt(wr, vgu, sl * 8u * nkg * 1024u + (2u * st + j % 2u) * 1024u);
+        }
+        bld8(wr, vgus, (x.part * 8u * nst + st) * 512u, W.s);
+    };
+    f32x4 acc[kSG];
+    // step st (< 8) of chunk C: the GEMM kernel's routed step, A from slot C
+    auto consume = [&](uint32_t C, uint32_t st, const WB& W) {
+        float sc[2][kSG];
+#pragma unroll
+        for (uint32_t q = 0; q < 2; q++)
+#pragma unroll
+            for (uint32_t i = 0; i < kSG; i++) sc[q][i] = e8m0f((W.s[i >> 1] >> (8u * (2u * (i & 1u) + q))) & 0xFFu);
+        const uint8_t* sl = slot_c(C) + 512u * st;
+        bf16x8 af[2];
+        af[0] = as_bf16x8(*(const u32x4*)(sl + lo[0]));
+        bf16x8 bw[kSG];
+#pragma unroll
+        for (uint32_t it = 0; it < 8u; it++) {
+            const uint32_t q = it / 4u, jj = it % 4u, c = it % 2u;
+            if (it + 1u < 8u) {
+                const uint32_t n2 = it + 1u;
+                af[c ^ 1u] = as_bf16x8(*(const u32x4*)(sl + 256u * (n2 / 4u) + lo[n2 % 4u]));
+            }
+#pragma unroll
+            for (uint32_t i = 0; i < kSG; i++) bw[i] = fp4x8_bf16(W.w[2u * i + q][jj], sc[q][i]);
+#pragma unroll
+            for (uint32_t i = 0; i < kSG; i++) acc[i] = mma(af[c], bw[i], acc[i]);
+        }
+    };
+    // chunk boundary: this wave's DMAs older than the two steps of weights in
+    // flight have landed, then every wave's have and every wave is done with
+    // the slot the last chunk read
+    auto boundary = [&]() {
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_waitcnt((18u & 15u) | ((18u >> 4) << 14) | 0x0F70u);
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+    };
+    const uint32_t r0 = (blockIdx.x + G - uoff % G) % G;
+    if (r0 >= U) return U;
+    Unit cur, nxt, done;
+    unit(r0, cur);
+    unit(r0 + G, nxt);
+    done.blk = nullptr;
+    dma(0u, cur);
+    dma(1u, cur);
+    WB B0, B1;
+    issue(cur, 0u, B0);
+    issue(cur, 1u, B1);
+    static_assert(3u * kSUC / kKC == 24u, "three chunks of eight steps");
+    // SwiGLU of unit x's kSG slices (pieces in rows: token m = row block g),
+    // after the next unit's first boundary, so its stores do not count
+    // against that boundary's wait
+    auto epilogue = [&](const Unit& x) {
+        const uint32_t ln = opaque_lane();
+#pragma unroll
+        for (uint32_t i = 0; i < kSG; i++) {
+            const uint32_t sl = x.part * kSG + i;
+            if (sl >= S) continue;
+            const f32x4 two[2] = {acc[i], f32x4{0.f, 0.f, 0.f, 0.f}};
+            swiglu_store(two, x.nt, true, ln, [&](uint32_t m, uint32_t nn, float xv) {
+                store3(b.mid3 + (size_t)(x.c0 + m) * 3u * I + sl * kSlice + v * 8u + nn, I, xv);
+            });
+        }
+    };
+    for (uint32_t r = r0; r < U; r += G) {
+        if (cur.blk == nullptr && threadIdx.x == 0u) raise_error(a.sync, SyncMap::make(), E_NOT_RESIDENT, 0u);
+        // steps 0..23 of unit cur; steps z + 2 >= 24 load the next unit's
+        // first steps (dead units load nothing)
+#define WL_SU_STEP(C, z, BUF)                                                      \
+    consume(C, (z) % 8u, BUF);                                                      \
+    __builtin_amdgcn_sched_barrier(0);                                              \
+    if ((z) + 2u < 24u) issue(cur, (z) + 2u, BUF);                                  \
+    else issue(nxt, (z) + 2u - 24u, BUF);                                           \
+    __builtin_amdgcn_sched_barrier(0);
+#define WL_SU_CHUNK(C)                                                              \
+    WL_SU_STEP(C, 8u * C + 0u, B0)                                                  \
+    WL_SU_STEP(C, 8u * C + 1u, B1)                                                  \
+    WL_SU_STEP(C, 8u * C + 2u, B0)                                                  \
+    WL_SU_STEP(C, 8u * C + 3u, B1)                                                  \
+    WL_SU_STEP(C, 8u * C + 4u, B0)                                                  \
+    WL_SU_STEP(C, 8u * C + 5u, B1)                                                  \
+    WL_SU_STEP(C, 8u * C + 6u, B0)                                                  \
+    WL_SU_STEP(C, 8u * C + 7u, B1)
+        boundary();
+        dma(2u, cur);
+        if (done.blk != nullptr) epilogue(done);
+#pragma unroll
+        for (uint32_t i = 0; i < kSG; i++) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+        WL_SU_CHUNK(0u)
+        boundary();
+        dma(0u, nxt);
+        WL_SU_CHUNK(1u)
+        boundary();
+        dma(1u, nxt);
+        WL_SU_CHUNK(2u)
+#undef WL_SU_CHUNK
+#undef WL_SU_STEP
+        done = cur;
+        cur = nxt;
+        unit(r + 2u * G, nxt);
+    }
+    epilogue(done);
+    return U;
+}
+
+// SMALL = true (GLM shape only): the instantiation with the small-expert
+// pipeline, taken with bdown_kernel's (launch_batched).
+template <bool GLM, bool SMALL>
 __global__ void __launch_bounds__(kThreads) bup_kernel(const DecodeArgs* __restrict__ pa, const BatchArgs b) {
     const DecodeArgs& a = *pa;
     extern __shared__ __align__(16) uint8_t dyn[];
@@ -1391,7 +1632,8 @@ __global__ void __launch_bounds__(kThreads) bup_kernel(const DecodeArgs* __restr
     const bool sh4 = (b.flags & kBatchShared4) != 0u;
     const uint32_t E = a.E + (sh4 ? 1u : 0u);  // experts in the pass table
     const uint8_t* const* stab = load_slot_tab(a, a.E, sh4, (const uint8_t**)dyn);
-    const PassTab pt = load_pass_tab(b, E, a.K, (uint32_t*)(dyn + 8u * E), stab, cdiv(I / kSlice, kSG));
+    const PassTab pt =
+        load_pass_tab(b, E, a.K, (uint32_t*)(dyn + 8u * E), stab, cdiv(I / kSlice, kSG), SMALL ? kSmallT : 0u);
     // the wide units first (each a pipeline of its own), then the kMT units,
     // which start on the work-groups after the wide units' last ones
     const uint32_t Us = run_shared_up_wide<GLM>(a, b);
@@ -1433,6 +1675,12 @@ __global__ void __launch_bounds__(kThreads) bup_kernel(const DecodeArgs* __restr
     k.tt = tt;
     fill_tokens(k, tt, kMT);
     run_steps(k);
+    if constexpr (SMALL) {
+        pipeline_drain();
+        // the pass table's LDS holds the small-expert list now (16 bytes per
+        // expert: the table is 16 E + 8 bytes), the token table the wave counts
+        run_small_up<GLM>(a, b, stab, k.uoff + U, (SmallExp*)(dyn + 8u * E), (uint32_t*)tt);
+    }
 }
 
 // ---- down ---------------------------------------------------------------------
@@ -2244,7 +2492,8 @@ int launch_batched(const DecodeArgs* d_args, const BatchArgs& b, uint32_t H, uin
     // the GEMM kernels' wide units take their shape parameters as constants
     // at the GLM shape
     const bool glm = H == 6144u && I == 2048u && SI == 2048u && K == 8u;
-    const void* up = glm ? (const void*)bup_kernel<true> : (const void*)bup_kernel<false>;
+    // (decided below with the down kernel's small-expert instantiation)
+    const void* up = nullptr;
     // routed experts of at most kSmallT tokens: their down projection as
     // bdown_kernel's streaming pipeline, when the batch averages at most two
     // tokens per expert (measured at the GLM shape: T = 64 about -3 % per
@@ -2253,6 +2502,10 @@ int launch_batched(const DecodeArgs* d_args, const BatchArgs& b, uint32_t H, uin
     const bool small = small_down_fits(H, I) && (uint64_t)b.T * K <= 2ull * E;
     const void* down = glm ? (small ? (const void*)bdown_kernel<true, true> : (const void*)bdown_kernel<true, false>)
                            : (small ? (const void*)bdown_kernel<false, true> : (const void*)bdown_kernel<false, false>);
+    // the gate/up side of the same experts (GLM shape: K = 3 x 2048)
+    const bool small_up = small && glm && small_up_fits(H, I);
+    up = glm ? (small_up ? (const void*)bup_kernel<true, true> : (const void*)bup_kernel<true, false>)
+             : (const void*)bup_kernel<false, false>;
     const struct { const void* fn; size_t lds; } attrs[] = {
         {(const void*)btopk_kernel, topk_lds}, {up, up_lds}, {down, gemm_lds}};
     for (const auto& at : attrs)
@@ -2285,11 +2538,12 @@ int launch_batched(const DecodeArgs* d_args, const BatchArgs& b, uint32_t H, uin
         if (bf16_sh && (b.T + kMTW - 1u) / kMTW * ((SI / kSlice + 1u) / 2u) >= gu) bw.flags |= kBatchWideSharedUp;
         if (bf16_sh && (b.T + kMTW - 1u) / kMTW * ((H + 255u) / 256u) >= gd) bw.flags |= kBatchWideSharedDown;
         if (glm) {
-            hipLaunchKernelGGL(bup_kernel<true>, dim3(gu), dim3(kThreads), up_lds, s, d_args, bw);
+            if (small_up) hipLaunchKernelGGL((bup_kernel<true, true>), dim3(gu), dim3(kThreads), up_lds, s, d_args, bw);
+            else hipLaunchKernelGGL((bup_kernel<true, false>), dim3(gu), dim3(kThreads), up_lds, s, d_args, bw);
             if (small) hipLaunchKernelGGL((bdown_kernel<true, true>), dim3(gd), dim3(kThreads), gemm_lds, s, d_args, bw);
             else hipLaunchKernelGGL((bdown_kernel<true, false>), dim3(gd), dim3(kThreads), gemm_lds, s, d_args, bw);
         } else {
-            hipLaunchKernelGGL(bup_kernel<false>, dim3(gu), dim3(kThreads), up_lds, s, d_args, bw);
+            hipLaunchKernelGGL((bup_kernel<false, false>), dim3(gu), dim3(kThreads), up_lds, s, d_args, bw);
             if (small) hipLaunchKernelGGL((bdown_kernel<false, true>), dim3(gd), dim3(kThreads), gemm_lds, s, d_args, bw);
             else hipLaunchKernelGGL((bdown_kernel<false, false>), dim3(gd), dim3(kThreads), gemm_lds, s, d_args, bw);
         }
