@@ -2351,9 +2351,9 @@ WL_DEV void run_small_down(const DecodeArgs& a, const BatchArgs& b, const uint8_
 }
 
 // SMALL = true: the instantiation with the small-expert pipeline (launch_batched
-// takes it when the batch averages at most two tokens per expert); the other
-// keeps the GEMM pipelines' code as it was (with the small pipeline compiled
-// in, T = 256 and 1024 ran 2-4 % slower).
+// takes it at the shapes small_down_fits allows); the other keeps the GEMM
+// pipelines' code alone (with the small pipeline compiled into one kernel for
+// every shape, T = 256 and 1024 ran 2-4 % slower).
 template <bool GLM, bool SMALL>
 __global__ void __launch_bounds__(kThreads) bdown_kernel(const DecodeArgs* __restrict__ pa, const BatchArgs b) {
     const DecodeArgs& a = *pa;
@@ -2495,11 +2495,10 @@ int launch_batched(const DecodeArgs* d_args, const BatchArgs& b, uint32_t H, uin
     // (decided below with the down kernel's small-expert instantiation)
     const void* up = nullptr;
     // routed experts of at most kSmallT tokens: their down projection as
-    // bdown_kernel's streaming pipeline, when the batch averages at most two
-    // tokens per expert (measured at the GLM shape: T = 64 about -3 % per
-    // call; at T = 256 and 1024, where few experts are that small, their
-    // units after the GEMM pipeline's made the call slower)
-    const bool small = small_down_fits(H, I) && (uint64_t)b.T * K <= 2ull * E;
+    // bdown_kernel's streaming pipeline, for every batch the shape allows
+    // (measured at the GLM shape, per call: T = 64 -3 %, 128 -5 %, 512 -4 %,
+    // 1024 unchanged, where no expert is that small)
+    const bool small = small_down_fits(H, I);
     const void* down = glm ? (small ? (const void*)bdown_kernel<true, true> : (const void*)bdown_kernel<true, false>)
                            : (small ? (const void*)bdown_kernel<false, true> : (const void*)bdown_kernel<false, false>);
     // the gate/up side of the same experts (GLM shape: K = 3 x 2048)
