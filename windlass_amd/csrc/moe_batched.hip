@@ -1384,53 +1384,55 @@ WL_DEV uint32_t run_routed_up_wide(const DecodeArgs& a, const BatchArgs& b, cons
     return U;
 }
 // ---- routed gate/up of small experts -----------------------------------------
-// Experts with 1..kSmallT tokens run their gate/up as streaming units, like
-// the decode kernel's gate/up phase: unit (expert, part of kSG slices). The
-// three LDS slots hold the expert's tokens' pieces for the whole K = H =
-// 3 x 2048 columns, slot C columns [2048 C, +2048): stored row Rs = 3m + pc
-// (token m, piece pc; 4096 bytes), its 16-byte group p holding logical group
-// p ^ Rs (the 16 rows an A fragment reads at one column fall in different
-// bank groups). MFMA row n = 4m + pc reads stored row 3m + min(pc, 2) (rows
-// 4m + 3 and tokens past nt carry values no output reads). Each wave streams
-// its tiles of the unit's kSG slices (the GEMM kernel's native gu chunks and
-// batched scale words) two 256-column steps ahead with no barrier inside a
-// chunk; at each chunk boundary the waves meet once, and the slot the last
-// chunk used takes the next unit's rows (DMA), so a unit's pieces are in
-// LDS a chunk and more before its steps reach them:
-//   before chunk 0 of unit u: slot 2 <- unit u, chunk 2;
-//   before chunk 1:           slot 0 <- unit u + 1, chunk 0;
-//   before chunk 2:           slot 1 <- unit u + 1, chunk 1.
-// The per-step arithmetic is the GEMM kernel's for a pass of pieces in rows
-// (one row block). The small-expert list (expert, its tokens, first compact
-// entry, count) lives where the pass table was, after the GEMM pipelines.
-constexpr uint32_t kSUC = 2048;  // columns per slot (chunk)
+// Experts with 1..kSmallUpT tokens run their gate/up as streaming units, like
+// the decode kernel's gate/up phase: unit (expert, part of kSG slices), in two
+// pipelines, NB = 1 for 1-4 tokens and NB = 2 for 5-8 (MFMA row blocks of
+// pieces in rows: token m's pieces in rows 4m..4m+2). The three LDS slots
+// hold the unit's tokens' pieces for K = H = 6144 in NCH chunks of CW
+// columns, chunk c in slot c mod 3 (NB = 1: 3 chunks of 2048 columns, 12
+// stored rows of 4 KB; NB = 2: 6 chunks of 1024 columns, 24 rows of 2 KB;
+// either way 48 KB per slot). Stored row Rs = 3m + pc; its 16-byte group p
+// holds logical group p ^ (Rs & 15), so the 16 rows an A fragment reads at
+// one column fall in different bank groups. MFMA row 16 tb + n reads stored
+// row 3m + min(pc, 2) for m = 4 tb + n / 4, pc = n % 4 (rows 4m + 3 and
+// tokens past nt carry values no output reads). Each wave streams its tiles
+// of the unit's kSG slices (the GEMM kernel's native gu chunks and batched
+// scale words) two 256-column steps ahead with no barrier inside a chunk; at
+// each chunk boundary the waves meet once, and the slot the last chunk used
+// takes the chunk two ahead (of this unit or the next) by DMA, so a chunk's
+// rows are in LDS at least two chunks before its steps read them. The
+// per-step arithmetic is the GEMM kernel's for a pass of pieces in rows, so
+// the results are the same bits. The lists (expert, its tokens, first
+// compact entry, count) live where the pass table was, after the GEMM
+// pipelines.
+constexpr uint32_t kSmallUpT = 8;  // tokens of the largest expert the gate/up streaming units take
 __host__ __device__ inline bool small_up_fits(uint32_t H, uint32_t I) {
-    return H == 3u * kSUC && I % (kSlice * kSG) == 0u && 12u * 2u * kSUC <= kSlotB;
+    return H == 6144u && I % (kSlice * kSG) == 0u;
 }
 struct SmallExp {
-    uint16_t tok[kSmallT];
+    uint16_t tok[kSmallUpT];
     uint16_t c0, nt;
     uint32_t e;
 };
-static_assert(sizeof(SmallExp) == 16u, "16 bytes per small expert");
-template <bool GLM>
-WL_DEV uint32_t run_small_up(const DecodeArgs& a, const BatchArgs& b, const uint8_t* const* stab, uint32_t uoff,
-                             SmallExp* se, uint32_t* wcnt) {
-    const uint32_t H = GLM ? 6144u : a.H, I = GLM ? 2048u : a.I, E = a.E, K = GLM ? 8u : a.K;
-    const uint32_t tid = threadIdx.x, lane = tid & 63u, v = uni(tid >> 6), n = lane & 15u, g = lane >> 4;
+static_assert(sizeof(SmallExp) == 24u, "24 bytes per small expert");
+// LDS the small-expert list needs from the pass table's start (8 E bytes
+// into the dynamic LDS), for E routed experts.
+__host__ __device__ inline size_t small_list_end(uint32_t E) { return 8u * (E + 1u) + sizeof(SmallExp) * E + 64u; }
+// The experts with lo..hi tokens (ascending), into se; returns their count.
+// wcnt: kWaves words of LDS.
+WL_DEV uint32_t small_list(const DecodeArgs& a, const BatchArgs& b, const uint8_t* const* stab, uint32_t lo,
+                           uint32_t hi, uint32_t K, SmallExp* se, uint32_t* wcnt) {
+    const uint32_t E = a.E, lane = threadIdx.x & 63u, v = uni(threadIdx.x >> 6);
     const bool skip = (b.flags & kBatchSkipUnbound) != 0u;
-    // the list: wave v takes experts v, v + 8, ... in blocks of 64 (ballot
-    // order within a block), the blocks' counts summed in LDS
-    {
-        uint32_t run = 0;
-        for (uint32_t e0 = 64u * v; e0 < E; e0 += 64u * kWaves) {
-            const uint32_t e = e0 + lane;
-            const uint32_t c = e < E ? gld(b.counts + e) : 0u;
-            const bool sm = c >= 1u && c <= kSmallT && !(skip && stab[e] == nullptr);
-            run += (uint32_t)__popcll(__ballot(sm));
-        }
-        if (lane == 0u) wcnt[v] = run;
+    auto is_small = [&](uint32_t e, uint32_t c) { return c >= lo && c <= hi && !(skip && stab[e] == nullptr); };
+    // wave v takes experts v, v + 8, ... in blocks of 64 (ballot order within
+    // a block), the blocks' counts summed in LDS
+    uint32_t run = 0;
+    for (uint32_t e0 = 64u * v; e0 < E; e0 += 64u * kWaves) {
+        const uint32_t e = e0 + lane, c = e < E ? gld(b.counts + e) : 0u;
+        run += (uint32_t)__popcll(__ballot(e < E && is_small(e, c)));
     }
+    if (lane == 0u) wcnt[v] = run;
     lds_barrier();
     uint32_t base = 0, ns = 0;
     for (uint32_t w = 0; w < kWaves; w++) {
@@ -1438,43 +1440,54 @@ WL_DEV uint32_t run_small_up(const DecodeArgs& a, const BatchArgs& b, const uint
         base += w < v ? c : 0u;
         ns += c;
     }
-    {
-        uint32_t run = base;
-        for (uint32_t e0 = 64u * v; e0 < E; e0 += 64u * kWaves) {
-            const uint32_t e = e0 + lane;
-            const uint32_t c = e < E ? gld(b.counts + e) : 0u;
-            const bool sm = c >= 1u && c <= kSmallT && !(skip && stab[e] == nullptr);
-            const uint64_t bal = __ballot(sm);
-            if (sm) {
-                SmallExp x;
-                const uint32_t c0 = gld(b.offsets + e);
+    run = base;
+    for (uint32_t e0 = 64u * v; e0 < E; e0 += 64u * kWaves) {
+        const uint32_t e = e0 + lane, c = e < E ? gld(b.counts + e) : 0u;
+        const bool sm = e < E && is_small(e, c);
+        const uint64_t bal = __ballot(sm);
+        if (sm) {
+            SmallExp x;
+            const uint32_t c0 = gld(b.offsets + e);
 #pragma unroll
-                for (uint32_t m = 0; m < kSmallT; m++) x.tok[m] = (uint16_t)(gld(b.ent + c0 + min(m, c - 1u)) / K);
-                x.c0 = (uint16_t)c0;
-                x.nt = (uint16_t)c;
-                x.e = e;
-                se[run + (uint32_t)__popcll(bal & ((1ull << lane) - 1ull))] = x;
-            }
-            run += (uint32_t)__popcll(bal);
+            for (uint32_t m = 0; m < kSmallUpT; m++) x.tok[m] = (uint16_t)(gld(b.ent + c0 + min(m, c - 1u)) / K);
+            x.c0 = (uint16_t)c0;
+            x.nt = (uint16_t)c;
+            x.e = e;
+            se[run + (uint32_t)__popcll(bal & ((1ull << lane) - 1ull))] = x;
         }
+        run += (uint32_t)__popcll(bal);
     }
     lds_barrier();
+    return ns;
+}
+template <uint32_t NB>
+WL_DEV uint32_t run_small_up(const DecodeArgs& a, const BatchArgs& b, uint32_t uoff, const SmallExp* se, uint32_t ns,
+                             const uint8_t* const* stab) {
+    constexpr uint32_t H = 6144u, CW = NB == 1u ? 2048u : 1024u, NCH = H / CW, SPC = CW / kKC, RB = 2u * CW;
+    constexpr uint32_t ROWS = 12u * NB, SEGS = RB / 1024u;
+    static_assert(ROWS * RB == kSlotB && ROWS * SEGS == 6u * kWaves, "a chunk fills one slot in six DMAs per wave");
+    static_assert(NCH * SPC == 24u && NCH >= 3u, "24 steps of 256 columns, at least three chunks");
+    const uint32_t I = a.I;
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, v = uni(tid >> 6), n = lane & 15u, g = lane >> 4;
     const uint32_t S = I / kSlice, NSG = cdiv(S, kSG), U = ns * NSG, G = gridDim.x;
     const uint32_t nkg = H / 128u, nst = H / kKC;  // 128-column k tiles, 256-column steps
     const NativeLayout NL = NativeLayout::make(H, I);
     const uint32_t vgu = (uint32_t)NL.gu + v * nkg * 1024u + 16u * lane;
     const uint32_t vgus = (uint32_t)NL.bgus + v * nst * 512u + 8u * lane;
     const rsrc_t nrs = make_rsrc(b.norm3, b.T * 6u * H);
-    // A fragment of lane (n, g): stored row of MFMA row n, logical groups
-    // 32 s + 16 q + 4 g + jj of the chunk
-    const uint32_t rs_n = 3u * (n >> 2) + min(n & 3u, 2u);
-    uint32_t lo[4];
+    // A fragment of lane (n, g), row block tb: stored row of MFMA row
+    // 16 tb + n, logical groups 32 s + 16 q + 4 g + jj of the chunk
+    uint32_t lo[NB][4];
 #pragma unroll
-    for (uint32_t jj = 0; jj < 4; jj++) lo[jj] = rs_n * 4096u + 16u * ((4u * g + jj) ^ rs_n);
+    for (uint32_t tb = 0; tb < NB; tb++) {
+        const uint32_t rs = 3u * (4u * tb + (n >> 2)) + min(n & 3u, 2u);
+#pragma unroll
+        for (uint32_t jj = 0; jj < 4; jj++) lo[tb][jj] = rs * RB + 16u * ((4u * g + jj) ^ (rs & 15u));
+    }
     struct Unit {
         const uint8_t* blk;
         uint32_t part, c0, nt;
-        uint32_t tok[kSmallT];
+        uint32_t tok[4u * NB];
     };
     auto unit = [&](uint32_t r, Unit& x) {
         x.blk = nullptr;
@@ -1482,29 +1495,30 @@ WL_DEV uint32_t run_small_up(const DecodeArgs& a, const BatchArgs& b, const uint
         x.c0 = 0u;
         x.nt = 0u;
         if (r >= U) return;
-        const uint32_t j = r / NSG;
-        const SmallExp* q = se + j;
+        const SmallExp* q = se + r / NSG;
         x.part = r % NSG;
         x.blk = uni_ptr(stab[uni(q->e)]);
         x.c0 = uni(q->c0);
         x.nt = uni(q->nt);
 #pragma unroll
-        for (uint32_t m = 0; m < kSmallT; m++) x.tok[m] = uni(q->tok[m]);
+        for (uint32_t m = 0; m < 4u * NB; m++) x.tok[m] = uni(q->tok[m]);
     };
-    // slot C (C a constant once inlined)
     auto slot_c = [](uint32_t C) { return C == 0u ? slot<0>() : C == 1u ? slot<1>() : slot<2>(); };
-    // DMA of unit x's chunk C into slot C: instruction k of wave v writes
-    // segment q = v + kWaves k (stored row q / 4, its 1 KB quarter q % 4)
-    auto dma = [&](uint32_t C, const Unit& x) {
+    // DMA of unit x's chunk c into slot c mod 3: instruction k of wave v
+    // writes segment q = v + kWaves k (stored row q / SEGS, its 1 KB part
+    // q % SEGS)
+    auto dma = [&](uint32_t c, const Unit& x) {
 #pragma unroll
         for (uint32_t k = 0; k < 6u; k++) {
-            const uint32_t q = v + kWaves * k, rs = q >> 2, seg = q & 3u, m = rs / 3u, pc = rs % 3u;
+            const uint32_t q = v + kWaves * k, rs = q / SEGS, seg = q % SEGS, m = rs / 3u, pc = rs % 3u;
             const bool ok = x.blk != nullptr && m < x.nt;
-            const uint32_t t = m == 0u ? x.tok[0] : m == 1u ? x.tok[1] : m == 2u ? x.tok[2] : x.tok[3];
-            const uint32_t so = ((t * 3u + pc) * H + C * kSUC) * 2u + seg * 1024u;
+            uint32_t t = x.tok[0];
+#pragma unroll
+            for (uint32_t j = 1; j < 4u * NB; j++) t = m == j ? x.tok[j] : t;
+            const uint32_t so = ((t * 3u + pc) * H + c * CW) * 2u + seg * 1024u;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                nrs, (__attribute__((address_space(3))) void*)(slot_c(C) + rs * 4096u + seg * 1024u), 16u,
-                ok ? 16u * (lane ^ rs) : kOOBV, ok ? so : 0u, 0, 0);
+                nrs, (__attribute__((address_space(3))) void*)(slot_c(c % 3u) + rs * RB + seg * 1024u), 16u,
+                ok ? 16u * (lane ^ (rs & 15u)) : kOOBV, ok ? so : 0u, 0, 0);
         }
     };
     struct WB {
@@ -1520,29 +1534,34 @@ WL_DEV uint32_t run_small_up(const DecodeArgs& a, const BatchArgs& b, const uint
         }
         bld8(wr, vgus, (x.part * 8u * nst + st) * 512u, W.s);
     };
-    f32x4 acc[kSG];
-    // step st (< 8) of chunk C: the GEMM kernel's routed step, A from slot C
-    auto consume = [&](uint32_t C, uint32_t st, const WB& W) {
+    f32x4 acc[kSG][NB];
+    // step st (< SPC) of chunk c: the GEMM kernel's routed step, A from slot c mod 3
+    auto consume = [&](uint32_t c, uint32_t st, const WB& W) {
         float sc[2][kSG];
 #pragma unroll
         for (uint32_t q = 0; q < 2; q++)
 #pragma unroll
             for (uint32_t i = 0; i < kSG; i++) sc[q][i] = e8m0f((W.s[i >> 1] >> (8u * (2u * (i & 1u) + q))) & 0xFFu);
-        const uint8_t* sl = slot_c(C) + 512u * st;
-        bf16x8 af[2];
-        af[0] = as_bf16x8(*(const u32x4*)(sl + lo[0]));
+        const uint8_t* sl = slot_c(c % 3u) + 512u * st;
+        bf16x8 af[2][NB];
+#pragma unroll
+        for (uint32_t tb = 0; tb < NB; tb++) af[0][tb] = as_bf16x8(*(const u32x4*)(sl + lo[tb][0]));
         bf16x8 bw[kSG];
 #pragma unroll
         for (uint32_t it = 0; it < 8u; it++) {
-            const uint32_t q = it / 4u, jj = it % 4u, c = it % 2u;
+            const uint32_t q = it / 4u, jj = it % 4u, cc = it % 2u;
             if (it + 1u < 8u) {
                 const uint32_t n2 = it + 1u;
-                af[c ^ 1u] = as_bf16x8(*(const u32x4*)(sl + 256u * (n2 / 4u) + lo[n2 % 4u]));
+#pragma unroll
+                for (uint32_t tb = 0; tb < NB; tb++)
+                    af[cc ^ 1u][tb] = as_bf16x8(*(const u32x4*)(sl + 256u * (n2 / 4u) + lo[tb][n2 % 4u]));
             }
 #pragma unroll
             for (uint32_t i = 0; i < kSG; i++) bw[i] = fp4x8_bf16(W.w[2u * i + q][jj], sc[q][i]);
 #pragma unroll
-            for (uint32_t i = 0; i < kSG; i++) acc[i] = mma(af[c], bw[i], acc[i]);
+            for (uint32_t i = 0; i < kSG; i++)
+#pragma unroll
+                for (uint32_t tb = 0; tb < NB; tb++) acc[i][tb] = mma(af[cc][tb], bw[i], acc[i][tb]);
         }
     };
     // chunk boundary: this wave's DMAs older than the two steps of weights in
@@ -1565,8 +1584,7 @@ WL_DEV uint32_t run_small_up(const DecodeArgs& a, const BatchArgs& b, const uint
     WB B0, B1;
     issue(cur, 0u, B0);
     issue(cur, 1u, B1);
-    static_assert(3u * kSUC / kKC == 24u, "three chunks of eight steps");
-    // SwiGLU of unit x's kSG slices (pieces in rows: token m = row block g),
+    // SwiGLU of unit x's kSG slices (pieces in rows: token m = 4 tb + g),
     // after the next unit's first boundary, so its stores do not count
     // against that boundary's wait
     auto epilogue = [&](const Unit& x) {
@@ -1575,7 +1593,7 @@ WL_DEV uint32_t run_small_up(const DecodeArgs& a, const BatchArgs& b, const uint
         for (uint32_t i = 0; i < kSG; i++) {
             const uint32_t sl = x.part * kSG + i;
             if (sl >= S) continue;
-            const f32x4 two[2] = {acc[i], f32x4{0.f, 0.f, 0.f, 0.f}};
+            const f32x4 two[2] = {acc[i][0], NB == 2u ? acc[i][NB - 1u] : f32x4{0.f, 0.f, 0.f, 0.f}};
             swiglu_store(two, x.nt, true, ln, [&](uint32_t m, uint32_t nn, float xv) {
                 store3(b.mid3 + (size_t)(x.c0 + m) * 3u * I + sl * kSlice + v * 8u + nn, I, xv);
             });
@@ -1583,37 +1601,33 @@ WL_DEV uint32_t run_small_up(const DecodeArgs& a, const BatchArgs& b, const uint
     };
     for (uint32_t r = r0; r < U; r += G) {
         if (cur.blk == nullptr && threadIdx.x == 0u) raise_error(a.sync, SyncMap::make(), E_NOT_RESIDENT, 0u);
-        // steps 0..23 of unit cur; steps z + 2 >= 24 load the next unit's
-        // first steps (dead units load nothing)
-#define WL_SU_STEP(C, z, BUF)                                                      \
-    consume(C, (z) % 8u, BUF);                                                      \
-    __builtin_amdgcn_sched_barrier(0);                                              \
-    if ((z) + 2u < 24u) issue(cur, (z) + 2u, BUF);                                  \
-    else issue(nxt, (z) + 2u - 24u, BUF);                                           \
-    __builtin_amdgcn_sched_barrier(0);
-#define WL_SU_CHUNK(C)                                                              \
-    WL_SU_STEP(C, 8u * C + 0u, B0)                                                  \
-    WL_SU_STEP(C, 8u * C + 1u, B1)                                                  \
-    WL_SU_STEP(C, 8u * C + 2u, B0)                                                  \
-    WL_SU_STEP(C, 8u * C + 3u, B1)                                                  \
-    WL_SU_STEP(C, 8u * C + 4u, B0)                                                  \
-    WL_SU_STEP(C, 8u * C + 5u, B1)                                                  \
-    WL_SU_STEP(C, 8u * C + 6u, B0)                                                  \
-    WL_SU_STEP(C, 8u * C + 7u, B1)
-        boundary();
-        dma(2u, cur);
-        if (done.blk != nullptr) epilogue(done);
+        // chunk c of unit cur: at its boundary the slot (c + 2) mod 3 takes
+        // chunk c + 2 (of this unit, or the next unit's chunk c + 2 - NCH);
+        // steps z + 2 >= 24 load the next unit's first steps (dead units
+        // load nothing)
 #pragma unroll
-        for (uint32_t i = 0; i < kSG; i++) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-        WL_SU_CHUNK(0u)
-        boundary();
-        dma(0u, nxt);
-        WL_SU_CHUNK(1u)
-        boundary();
-        dma(1u, nxt);
-        WL_SU_CHUNK(2u)
-#undef WL_SU_CHUNK
-#undef WL_SU_STEP
+        for (uint32_t c = 0; c < NCH; c++) {
+            boundary();
+            if (c + 2u < NCH) dma(c + 2u, cur);
+            else dma(c + 2u - NCH, nxt);
+            if (c == 0u) {
+                if (done.blk != nullptr) epilogue(done);
+#pragma unroll
+                for (uint32_t i = 0; i < kSG; i++)
+#pragma unroll
+                    for (uint32_t tb = 0; tb < NB; tb++) acc[i][tb] = f32x4{0.f, 0.f, 0.f, 0.f};
+            }
+#pragma unroll
+            for (uint32_t st = 0; st < SPC; st++) {
+                const uint32_t z = SPC * c + st;
+                WB& BUF = (z % 2u) ? B1 : B0;
+                consume(c, st, BUF);
+                __builtin_amdgcn_sched_barrier(0);
+                if (z + 2u < 24u) issue(cur, z + 2u, BUF);
+                else issue(nxt, z + 2u - 24u, BUF);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
         done = cur;
         cur = nxt;
         unit(r + 2u * G, nxt);
@@ -1633,7 +1647,7 @@ __global__ void __launch_bounds__(kThreads) bup_kernel(const DecodeArgs* __restr
     const uint32_t E = a.E + (sh4 ? 1u : 0u);  // experts in the pass table
     const uint8_t* const* stab = load_slot_tab(a, a.E, sh4, (const uint8_t**)dyn);
     const PassTab pt =
-        load_pass_tab(b, E, a.K, (uint32_t*)(dyn + 8u * E), stab, cdiv(I / kSlice, kSG), SMALL ? kSmallT : 0u);
+        load_pass_tab(b, E, a.K, (uint32_t*)(dyn + 8u * E), stab, cdiv(I / kSlice, kSG), SMALL ? kSmallUpT : 0u);
     // the wide units first (each a pipeline of its own), then the kMT units,
     // which start on the work-groups after the wide units' last ones
     const uint32_t Us = run_shared_up_wide<GLM>(a, b);
@@ -1677,9 +1691,17 @@ __global__ void __launch_bounds__(kThreads) bup_kernel(const DecodeArgs* __restr
     run_steps(k);
     if constexpr (SMALL) {
         pipeline_drain();
-        // the pass table's LDS holds the small-expert list now (16 bytes per
-        // expert: the table is 16 E + 8 bytes), the token table the wave counts
-        run_small_up<GLM>(a, b, stab, k.uoff + U, (SmallExp*)(dyn + 8u * E), (uint32_t*)tt);
+        // the pass table's LDS (and on) holds the small-expert lists now
+        // (the host sizes the dynamic LDS for them: small_list_end)
+        SmallExp* se = (SmallExp*)(dyn + 8u * (a.E + 1u));
+        uint32_t* wcnt = (uint32_t*)(se + a.E);
+        const uint32_t K_ = GLM ? 8u : a.K;
+        uint32_t uo = k.uoff + U;
+        uint32_t ns = small_list(a, b, stab, 1u, kSmallT, K_, se, wcnt);
+        uo += run_small_up<1>(a, b, uo, se, ns, stab);
+        pipeline_drain();
+        ns = small_list(a, b, stab, kSmallT + 1u, kSmallUpT, K_, se, wcnt);
+        run_small_up<2>(a, b, uo, se, ns, stab);
     }
 }
 
@@ -2487,7 +2509,7 @@ int launch_batched(const DecodeArgs* d_args, const BatchArgs& b, uint32_t H, uin
     // n_cu or more work-groups
     BatchArgs bt = b;
     bt.tcap = batched_tok_entries(b.T, I, SI, E, K, n_cu);
-    const size_t up_lds = bup_lds(b.T, I, SI, E, K, n_cu);
+    size_t up_lds = bup_lds(b.T, I, SI, E, K, n_cu);
     if (up_lds + 3u * (size_t)kSlotB > (size_t)decode_max_lds()) return (int)hipErrorInvalidValue;
     // the GEMM kernels' wide units take their shape parameters as constants
     // at the GLM shape
@@ -2501,8 +2523,11 @@ int launch_batched(const DecodeArgs* d_args, const BatchArgs& b, uint32_t H, uin
     const bool small = small_down_fits(H, I);
     const void* down = glm ? (small ? (const void*)bdown_kernel<true, true> : (const void*)bdown_kernel<true, false>)
                            : (small ? (const void*)bdown_kernel<false, true> : (const void*)bdown_kernel<false, false>);
-    // the gate/up side of the same experts (GLM shape: K = 3 x 2048)
-    const bool small_up = small && glm && small_up_fits(H, I);
+    // the gate/up side (experts of up to kSmallUpT tokens; GLM shape, and
+    // the lists must fit the dynamic LDS)
+    const bool small_up = small && glm && small_up_fits(H, I) &&
+                          small_list_end(E) + 3u * (size_t)kSlotB <= (size_t)decode_max_lds();
+    if (small_up) up_lds = std::max(up_lds, small_list_end(E));
     up = glm ? (small_up ? (const void*)bup_kernel<true, true> : (const void*)bup_kernel<true, false>)
              : (const void*)bup_kernel<false, false>;
     const struct { const void* fn; size_t lds; } attrs[] = {
