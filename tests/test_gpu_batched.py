@@ -261,3 +261,28 @@ def test_calls_longer_than_a_chunk(gpu):
             assert O.rel_to_scale(ref, moe_t) < TOL, t
     print(f"T={T}: chunked call equals per-chunk calls; worst vs another split {worst:.2e}", flush=True)
     dm.close()
+
+
+@pytest.mark.parametrize("T", [64, 256])
+def test_small_expert_units_equal_grouped_passes(gpu, monkeypatch, T):
+    """At the GLM shape experts of up to 8 tokens run their gate/up, and of up
+    to 4 their down, as streaming units instead of grouped passes (the
+    kernels' small-expert instantiations). WL_BATCHED_SMALL=0 keeps every
+    expert in the grouped passes; both give the same outputs bit for bit,
+    with the bench's Zipf bias (T = 64: most experts hold 1-4 tokens; 256:
+    most hold 5-16)."""
+    c = GLM
+    H = c["hidden"]
+    zipf = synthdata.zipf_bias_offset(c["n_routed_experts"], 1, amplitude=0.25)
+    dm = DeviceModel(c, seed=1, n_layers=1, bias_offset=zipf)
+    hs = _tokens(H, T, 1600)
+    monkeypatch.delenv("WL_BATCHED_SMALL", raising=False)
+    units = _batched(dm, hs)
+    counts = dm.ctx.batched_counts()
+    monkeypatch.setenv("WL_BATCHED_SMALL", "0")
+    grouped = _batched(dm, hs)
+    small = int(((counts >= 1) & (counts <= 8)).sum())
+    print(f"T={T}: {small} experts of 1-8 tokens", flush=True)
+    assert small > 20
+    assert np.array_equal(units.view(np.uint32), grouped.view(np.uint32))
+    dm.close()

@@ -30,6 +30,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cstdlib>
 
 #include "dev_common.h"
 #include "internal.h"
@@ -2520,7 +2521,10 @@ int launch_batched(const DecodeArgs* d_args, const BatchArgs& b, uint32_t H, uin
     // bdown_kernel's streaming pipeline, for every batch the shape allows
     // (measured at the GLM shape, per call: T = 64 -3 %, 128 -5 %, 512 -4 %,
     // 1024 unchanged, where no expert is that small)
-    const bool small = small_down_fits(H, I);
+    // (WL_BATCHED_SMALL=0 keeps every expert in the grouped passes: the
+    // same results bit for bit, which a GPU test compares)
+    const char* small_env = getenv("WL_BATCHED_SMALL");
+    const bool small = small_down_fits(H, I) && !(small_env && small_env[0] == '0');
     const void* down = glm ? (small ? (const void*)bdown_kernel<true, true> : (const void*)bdown_kernel<true, false>)
                            : (small ? (const void*)bdown_kernel<false, true> : (const void*)bdown_kernel<false, false>);
     // the gate/up side (experts of up to kSmallUpT tokens; GLM shape, and
