@@ -317,7 +317,10 @@ struct BatchArgs {
     uint16_t* smid3;       // [T][3][SI] shared SwiGLU outputs (pieces)
     float* shout;          // [T][H]
     uint32_t tcap;         // token-table entries per work-group in bup_kernel's LDS (set by launch_batched)
+    uint32_t* wq;          // [kWqWords] work-queue counters of the streaming units: zero between launches
+                           // (zeroed once when the scratch is made, reset by each launch's last work-group)
 };
+constexpr uint32_t kWqWords = 8;
 
 // Launchers (moe_decode.hip).
 int launch_decode(const DecodeArgs* d_args, const DecodeDyn& dyn, uint32_t H, uint32_t I, uint32_t SI,

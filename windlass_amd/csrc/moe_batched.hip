@@ -1461,9 +1461,24 @@ WL_DEV uint32_t small_list(const DecodeArgs& a, const BatchArgs& b, const uint8_
     lds_barrier();
     return ns;
 }
+// Units are taken from a work queue (b.wq[NB - 1], an agent-scope counter
+// that every work-group increments): a work-group that ends its grouped
+// passes early takes more units. Wave 0 takes the next unit at the current
+// unit's first chunk boundary and publishes it in LDS (qs) at the boundary
+// where the next unit's first DMA goes out, so the take's round trip is
+// hidden behind a chunk of steps and no work-group holds more than one unit
+// ahead when the queue runs dry.
+// An agent-scope fetch-add through an address the compiler cannot tell is
+// uniform: a uniform one is rewritten into a wave-level atomic whose result
+// is waited for at once (vmcnt(0)), which would drain the weight stream.
+WL_DEV uint32_t take_next(uint32_t* p) {
+    uint32_t z = 0u;
+    asm volatile("" : "+v"(z));
+    return __hip_atomic_fetch_add((g_u32*)(p + z), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 template <uint32_t NB>
-WL_DEV uint32_t run_small_up(const DecodeArgs& a, const BatchArgs& b, uint32_t uoff, const SmallExp* se, uint32_t ns,
-                             const uint8_t* const* stab) {
+WL_DEV void run_small_up(const DecodeArgs& a, const BatchArgs& b, const SmallExp* se, uint32_t ns,
+                         const uint8_t* const* stab, uint32_t* qs) {
     constexpr uint32_t H = 6144u, CW = NB == 1u ? 2048u : 1024u, NCH = H / CW, SPC = CW / kKC, RB = 2u * CW;
     constexpr uint32_t ROWS = 12u * NB, SEGS = RB / 1024u;
     static_assert(ROWS * RB == kSlotB && ROWS * SEGS == 6u * kWaves, "a chunk fills one slot in six DMAs per wave");
@@ -1489,12 +1504,14 @@ WL_DEV uint32_t run_small_up(const DecodeArgs& a, const BatchArgs& b, uint32_t u
         const uint8_t* blk;
         uint32_t part, c0, nt;
         uint32_t tok[4u * NB];
+        bool live;
     };
     auto unit = [&](uint32_t r, Unit& x) {
         x.blk = nullptr;
         x.part = 0u;
         x.c0 = 0u;
         x.nt = 0u;
+        x.live = r < U;
         if (r >= U) return;
         const SmallExp* q = se + r / NSG;
         x.part = r % NSG;
@@ -1566,20 +1583,24 @@ WL_DEV uint32_t run_small_up(const DecodeArgs& a, const BatchArgs& b, uint32_t u
         }
     };
     // chunk boundary: this wave's DMAs older than the two steps of weights in
-    // flight have landed, then every wave's have and every wave is done with
-    // the slot the last chunk read
+    // flight have landed and its LDS writes are done, then every wave's are
+    // and every wave is done with the slot the last chunk read
     auto boundary = [&]() {
         __builtin_amdgcn_sched_barrier(0);
-        __builtin_amdgcn_s_waitcnt((18u & 15u) | ((18u >> 4) << 14) | 0x0F70u);
+        __builtin_amdgcn_s_waitcnt((18u & 15u) | ((18u >> 4) << 14) | 0x0070u);  // vmcnt(18) lgkmcnt(0)
         __builtin_amdgcn_s_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
     };
-    const uint32_t r0 = (blockIdx.x + G - uoff % G) % G;
-    if (r0 >= U) return U;
+    uint32_t* const q = b.wq + (NB - 1u);
+    const bool taker = tid == 0u;
+    if (taker) qs[0] = take_next(q);
+    lds_barrier();
     Unit cur, nxt, done;
-    unit(r0, cur);
-    unit(r0 + G, nxt);
+    unit(uni(qs[0]), cur);
+    unit(U, nxt);
     done.blk = nullptr;
+    done.live = false;
+    if (!cur.live) return;
     dma(0u, cur);
     dma(1u, cur);
     WB B0, B1;
@@ -1600,7 +1621,8 @@ WL_DEV uint32_t run_small_up(const DecodeArgs& a, const BatchArgs& b, uint32_t u
             });
         }
     };
-    for (uint32_t r = r0; r < U; r += G) {
+    uint32_t taken = 0u;  // wave 0: the next unit (in flight from chunk 0 on)
+    while (cur.live) {
         if (cur.blk == nullptr && threadIdx.x == 0u) raise_error(a.sync, SyncMap::make(), E_NOT_RESIDENT, 0u);
         // chunk c of unit cur: at its boundary the slot (c + 2) mod 3 takes
         // chunk c + 2 (of this unit, or the next unit's chunk c + 2 - NCH);
@@ -1608,11 +1630,14 @@ WL_DEV uint32_t run_small_up(const DecodeArgs& a, const BatchArgs& b, uint32_t u
         // load nothing)
 #pragma unroll
         for (uint32_t c = 0; c < NCH; c++) {
+            if (c == NCH - 2u && taker) qs[2] = taken;  // published by this boundary
             boundary();
+            if (c == 0u && taker) taken = take_next(q);
+            if (c == NCH - 2u) unit(uni(qs[2]), nxt);
             if (c + 2u < NCH) dma(c + 2u, cur);
             else dma(c + 2u - NCH, nxt);
             if (c == 0u) {
-                if (done.blk != nullptr) epilogue(done);
+                if (done.live && done.blk != nullptr) epilogue(done);
 #pragma unroll
                 for (uint32_t i = 0; i < kSG; i++)
 #pragma unroll
@@ -1631,10 +1656,16 @@ WL_DEV uint32_t run_small_up(const DecodeArgs& a, const BatchArgs& b, uint32_t u
         }
         done = cur;
         cur = nxt;
-        unit(r + 2u * G, nxt);
     }
-    epilogue(done);
-    return U;
+    if (done.blk != nullptr) epilogue(done);
+}
+// After the streaming pipelines: the last work-group to get here resets the
+// work-queue counters for the next launch (every other one has taken its
+// last unit by then).
+WL_DEV void wq_release(const BatchArgs& b) {
+    if (threadIdx.x != 0u) return;
+    if (rmw_inc(b.wq + kWqWords - 1u) != gridDim.x - 1u) return;
+    for (uint32_t i = 0; i < kWqWords; i++) __hip_atomic_store(b.wq + i, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // SMALL = true (GLM shape only): the instantiation with the small-expert
@@ -1697,12 +1728,12 @@ __global__ void __launch_bounds__(kThreads) bup_kernel(const DecodeArgs* __restr
         SmallExp* se = (SmallExp*)(dyn + 8u * (a.E + 1u));
         uint32_t* wcnt = (uint32_t*)(se + a.E);
         const uint32_t K_ = GLM ? 8u : a.K;
-        uint32_t uo = k.uoff + U;
         uint32_t ns = small_list(a, b, stab, 1u, kSmallT, K_, se, wcnt);
-        uo += run_small_up<1>(a, b, uo, se, ns, stab);
+        run_small_up<1>(a, b, se, ns, stab, wcnt);
         pipeline_drain();
         ns = small_list(a, b, stab, kSmallT + 1u, kSmallUpT, K_, se, wcnt);
-        run_small_up<2>(a, b, uo, se, ns, stab);
+        run_small_up<2>(a, b, se, ns, stab, wcnt);
+        wq_release(b);
     }
 }
 

@@ -1105,6 +1105,7 @@ static size_t batch_layout(const wl_ctx* c, uint32_t T, uint8_t* base, wl::Batch
     };
     wl::BatchArgs d{};
     wl::BatchArgs& x = b ? *b : d;
+    take(&x.wq, 4 * wl::kWqWords);  // first: the same offset in every layout of the shared static scratch
     take(&x.norm, 4 * t * H);
     take(&x.norm3, 6 * t * H);
     take(&x.logits, 4 * t * E);
@@ -1148,6 +1149,8 @@ static wl_status batch_reserve(wl_ctx* c, uint32_t T) {
         return fail(c, WL_ERR_OOM, "batched scratch for %u tokens (%zu B)", T, bytes);
     }
     batch_layout(c, T, (uint8_t*)B.buf, &B.b);
+    if ((e = hipMemset(B.b.wq, 0, 4 * wl::kWqWords)) != hipSuccess || (e = hipDeviceSynchronize()) != hipSuccess)
+        return hip_fail(c, e, "batched work-queue words");
     B.cap = T;
     B.sh4 = c->any_sh4;
     return WL_OK;
