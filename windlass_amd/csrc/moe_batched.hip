@@ -2590,12 +2590,17 @@ int launch_batched(const DecodeArgs* d_args, const BatchArgs& b, uint32_t H, uin
         hipLaunchKernelGGL(bscatter_kernel, dim3(E), dim3(256), 0, s, b, E);
     }
     if (phases & kPhaseGemm) {
-        // the shared expert's wide units when they fill the grid
+        // the shared expert's wide units when they fill the grid, and at the
+        // GLM shape from two wide passes on (measured, per call: T = 128
+        // -1 %, 256 and 512 -2 %; at T = 64, one pass, +2 %)
         BatchArgs bw = bt;
         const uint32_t gu = resident(up, up_lds), gd = resident(down, gemm_lds);
         const bool bf16_sh = !(b.flags & (kBatchNoShared | kBatchShared4));
-        if (bf16_sh && (b.T + kMTW - 1u) / kMTW * ((SI / kSlice + 1u) / 2u) >= gu) bw.flags |= kBatchWideSharedUp;
-        if (bf16_sh && (b.T + kMTW - 1u) / kMTW * ((H + 255u) / 256u) >= gd) bw.flags |= kBatchWideSharedDown;
+        const bool wide_sh = glm && b.T >= 2u * kMTW;
+        if (bf16_sh && (wide_sh || (b.T + kMTW - 1u) / kMTW * ((SI / kSlice + 1u) / 2u) >= gu))
+            bw.flags |= kBatchWideSharedUp;
+        if (bf16_sh && (wide_sh || (b.T + kMTW - 1u) / kMTW * ((H + 255u) / 256u) >= gd))
+            bw.flags |= kBatchWideSharedDown;
         if (glm) {
             if (small_up) hipLaunchKernelGGL((bup_kernel<true, true>), dim3(gu), dim3(kThreads), up_lds, s, d_args, bw);
             else hipLaunchKernelGGL((bup_kernel<true, false>), dim3(gu), dim3(kThreads), up_lds, s, d_args, bw);
