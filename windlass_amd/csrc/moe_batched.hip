@@ -1406,7 +1406,7 @@ WL_DEV uint32_t run_routed_up_wide(const DecodeArgs& a, const BatchArgs& b, cons
 // the results are the same bits. The lists (expert, its tokens, first
 // compact entry, count) live where the pass table was, after the GEMM
 // pipelines.
-constexpr uint32_t kSmallUpT = 8;  // tokens of the largest expert the gate/up streaming units take
+constexpr uint32_t kSmallUpT = 8;  // tokens of the largest expert the streaming units take (gate/up and down)
 __host__ __device__ inline bool small_up_fits(uint32_t H, uint32_t I) {
     return H == 6144u && I % (kSlice * kSG) == 0u;
 }
@@ -2247,12 +2247,15 @@ WL_DEV uint32_t run_routed_down_wide(const DecodeArgs& a, const BatchArgs& b, co
     return U;
 }
 // ---- routed down of small experts ---------------------------------------------
-// Experts with 1..kSmallT tokens (at small T most of them: 64 tokens x 8
+// Experts with 1..kSmallUpT tokens (at small T most of them: 64 tokens x 8
 // slots over ~200 experts) run their down projection as streaming units,
 // like the decode kernel's down phase: unit (expert, row block of 16 row
-// pairs). The expert's SwiGLU pieces are staged once per unit in LDS, token
-// m's three pieces in rows 4m..4m+2 (rows 4m+3 zero), so one
-// v_mfma_f32_16x16x32_bf16 covers all of the expert's tokens; then each wave
+// pairs), in two pipelines, NB = 1 for 1-4 tokens and NB = 2 for 5-8 (MFMA
+// row blocks of pieces in rows). The expert's SwiGLU pieces are staged once
+// per unit in LDS, token m's three pieces in stored rows 3m..3m+2 (MFMA row
+// 16 tb + n reads stored row 3m + min(n % 4, 2) for m = 4 tb + n / 4: rows
+// 4m + 3 carry values no output reads), so NB v_mfma_f32_16x16x32_bf16 cover
+// all of the expert's tokens; then each wave
 // streams its 2 row pairs x I/64 slices (native 1 KB dn chunks, the batched
 // scale words of bdns) two 256-column steps ahead, with no barrier between
 // steps (the GEMM kernel stages 48 KB of activation rows and meets a barrier
@@ -2260,27 +2263,33 @@ WL_DEV uint32_t run_routed_down_wide(const DecodeArgs& a, const BatchArgs& b, co
 // one row block). It is the last pipeline of bdown_kernel: its units are
 // 512 KB of weights each, so with the rotation (unit r on work-group (r +
 // uoff) mod grid, uoff the units of the earlier pipelines) the work-groups
-// end within about one unit of each other. LDS: the staged rows 0-7 in slot
-// 0, 8-15 in slot 1, the small-expert list in slot 2.
+// end within about one unit of each other. LDS: stored rows 8s..8s+7 in slot
+// s, the small-expert list where the pass table was.
 // the shapes it runs: at least two 256-column steps, at most 2048 columns staged
 __host__ __device__ inline bool small_down_fits(uint32_t H, uint32_t I) {
     return I % kKC == 0u && I >= 2u * kKC && I <= 2048u && H % 512u == 0u;
 }
-template <bool GLM>
-WL_DEV void run_small_down(const DecodeArgs& a, const BatchArgs& b, const uint8_t* const* stab, uint32_t uoff) {
+// Returns the pipeline's unit count (the next pipeline starts after it).
+template <bool GLM, uint32_t NB>
+WL_DEV uint32_t run_small_down(const DecodeArgs& a, const BatchArgs& b, const uint8_t* const* stab, uint32_t uoff,
+                               uint32_t* se) {
     const uint32_t H = GLM ? 6144u : a.H, I = GLM ? 2048u : a.I, E = GLM ? 256u : a.E;
     const uint32_t tid = threadIdx.x, lane = tid & 63u, v = uni(tid >> 6), n = lane & 15u, g = lane >> 4;
-    uint32_t* se = (uint32_t*)slot<2>();  // [E] the small experts, ascending; se[E] their count
+    // se: [E] the small experts, ascending; se[E] their count
     const uint32_t RS = I + 8u;  // staged row stride (bf16): rows 16 bytes apart in the bank groups
-    // staged row R (token R / 4, piece R % 4) at xrow(R)
-    auto xrow = [&](uint32_t R) { return (uint16_t*)(R < 8u ? slot<0>() : slot<1>()) + (R % 8u) * RS; };
+    constexpr uint32_t ROWS = 12u * NB;  // stored rows (token m, piece pc: 3m + pc)
+    static_assert(ROWS <= 24u, "three slots of eight rows");
+    auto xrow = [&](uint32_t R) {
+        return (uint16_t*)(R < 8u ? slot<0>() : R < 16u ? slot<1>() : slot<2>()) + (R % 8u) * RS;
+    };
+    const uint32_t lo_t = NB == 1u ? 1u : kSmallT + 1u, hi_t = NB == 1u ? kSmallT : kSmallUpT;
     const bool skip = (b.flags & kBatchSkipUnbound) != 0u;
     if (v == 0u) {
         uint32_t run = 0;
         for (uint32_t e0 = 0; e0 < E; e0 += 64u) {
             const uint32_t e = e0 + lane;
             const uint32_t c = e < E ? gld(b.counts + e) : 0u;
-            const bool sm = c >= 1u && c <= kSmallT && !(skip && stab[e] == nullptr);
+            const bool sm = c >= lo_t && c <= hi_t && !(skip && stab[e] == nullptr);
             const uint64_t bal = __ballot(sm);
             if (sm) se[run + (uint32_t)__popcll(bal & ((1ull << lane) - 1ull))] = e;
             run += (uint32_t)__popcll(bal);
@@ -2293,13 +2302,17 @@ WL_DEV void run_small_down(const DecodeArgs& a, const BatchArgs& b, const uint8_
     const NativeLayout NL = NativeLayout::make(H, I);
     const uint32_t vdn = (uint32_t)NL.dn + 16u * lane, vdns = (uint32_t)NL.bdns + v * nstd * 512u + 8u * lane;
     const rsrc_t mrs = make_rsrc(b.mid3, (uint32_t)((size_t)b.T * (a.K + ((b.flags & kBatchShared4) ? 1u : 0u)) * 6u * I));
-    // A fragment of lane (n, g): row n, columns 256 st + 64 s4 + 32 (g & 1) + 8 (g >> 1) + 16 f
-    const uint16_t* const arow = xrow(n) + 32u * (g & 1u) + 8u * (g >> 1);
+    // A fragment of lane (n, g), row block tb: its stored row, columns
+    // 256 st + 64 s4 + 32 (g & 1) + 8 (g >> 1) + 16 f
+    const uint16_t* arow[NB];
+#pragma unroll
+    for (uint32_t tb = 0; tb < NB; tb++)
+        arow[tb] = xrow(3u * (4u * tb + (n >> 2)) + min(n & 3u, 2u)) + 32u * (g & 1u) + 8u * (g >> 1);
     struct WB {
         u32x4 w[kWL];
         uint32_t s[2];
     };
-    constexpr uint32_t kAV = 8;  // 16-byte chunks of the staged rows per thread (I <= 2048)
+    constexpr uint32_t kAV = ROWS * 256u / kThreads;  // 16-byte chunks of the stored rows per thread (I <= 2048)
     const uint32_t cpr = I / 8u;  // 16-byte chunks per staged row
     // the unit being loaded: its expert's tokens, first compact row, block, row block
     uint32_t nt = 0, c0 = 0, part = 0;
@@ -2324,25 +2337,28 @@ WL_DEV void run_small_down(const DecodeArgs& a, const BatchArgs& b, const uint8_
         wrs = make_rsrc(uni_ptr(stab[e]), (uint32_t)NL.total);
 #pragma unroll
         for (uint32_t k = 0; k < kAV; k++) {
-            const uint32_t idx = tid + kThreads * k, row = idx / cpr, c8 = idx % cpr, m = row / 4u, pc = row % 4u;
-            const bool ok = idx < 16u * cpr && m < nt && pc < 3u;
+            const uint32_t idx = tid + kThreads * k, row = idx / cpr, c8 = idx % cpr, m = row / 3u, pc = row % 3u;
+            const bool ok = idx < ROWS * cpr && m < nt;
             av[k] = __builtin_amdgcn_raw_buffer_load_b128(mrs, (int)(ok ? (((c0 + m) * 3u + pc) * I + 8u * c8) * 2u : kOOB), 0, 0);
         }
         issue(0u, B0);
         issue(1u, B1);
     };
-    f32x4 d[2][2];
+    f32x4 d[2][2][NB];
     auto consume = [&](uint32_t st, const WB& W) {
-        auto frag = [&](uint32_t o) {  // o = 2 s4 + f
-            return as_bf16x8(*(const u32x4*)(arow + 256u * st + 64u * (o / 2u) + 16u * (o % 2u)));
+        auto frag = [&](uint32_t o, uint32_t tb) {  // o = 2 s4 + f
+            return as_bf16x8(*(const u32x4*)(arow[tb] + 256u * st + 64u * (o / 2u) + 16u * (o % 2u)));
         };
-        bf16x8 af[2];
-        af[0] = frag(0u);
+        bf16x8 af[2][NB];
+#pragma unroll
+        for (uint32_t tb = 0; tb < NB; tb++) af[0][tb] = frag(0u, tb);
         float scx[2], scy[2];
 #pragma unroll
         for (uint32_t o = 0; o < 8u; o++) {
             const uint32_t s4 = o / 2u, f = o % 2u;
-            if (o + 1u < 8u) af[(o + 1u) % 2u] = frag(o + 1u);
+            if (o + 1u < 8u)
+#pragma unroll
+                for (uint32_t tb = 0; tb < NB; tb++) af[(o + 1u) % 2u][tb] = frag(o + 1u, tb);
             if (f == 0u) {
 #pragma unroll
                 for (uint32_t h = 0; h < 2; h++) {
@@ -2365,12 +2381,13 @@ WL_DEV void run_small_down(const DecodeArgs& a, const BatchArgs& b, const uint8_
                 bx[h] = fp4x8_bf16(x, scx[h]);
                 by[h] = fp4x8_bf16(y, scy[h]);
             }
-            const bf16x8 af_o = af[o % 2u];
 #pragma unroll
-            for (uint32_t h = 0; h < 2; h++) {
-                d[h][0] = mma(af_o, bx[h], d[h][0]);
-                d[h][1] = mma(af_o, by[h], d[h][1]);
-            }
+            for (uint32_t h = 0; h < 2; h++)
+#pragma unroll
+                for (uint32_t tb = 0; tb < NB; tb++) {
+                    d[h][0][tb] = mma(af[o % 2u][tb], bx[h], d[h][0][tb]);
+                    d[h][1][tb] = mma(af[o % 2u][tb], by[h], d[h][1][tb]);
+                }
         }
     };
     const uint32_t r0 = (blockIdx.x + G - uoff % G) % G;
@@ -2379,11 +2396,13 @@ WL_DEV void run_small_down(const DecodeArgs& a, const BatchArgs& b, const uint8_
 #pragma unroll
         for (uint32_t k = 0; k < kAV; k++) {
             const uint32_t idx = tid + kThreads * k;
-            if (idx < 16u * cpr) *(u32x4*)(xrow(idx / cpr) + 8u * (idx % cpr)) = av[k];
+            if (idx < ROWS * cpr) *(u32x4*)(xrow(idx / cpr) + 8u * (idx % cpr)) = av[k];
         }
         lds_barrier();
 #pragma unroll
-        for (uint32_t h = 0; h < 2; h++) d[h][0] = d[h][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (uint32_t h = 0; h < 2; h++)
+#pragma unroll
+            for (uint32_t tb = 0; tb < NB; tb++) d[h][0][tb] = d[h][1][tb] = f32x4{0.f, 0.f, 0.f, 0.f};
         pingpong(nstd, B0, B1, issue, consume);
         // the next unit's pieces and first steps go out before this unit's
         // epilogue, so the stream does not stop between units
@@ -2396,12 +2415,14 @@ WL_DEV void run_small_down(const DecodeArgs& a, const BatchArgs& b, const uint8_
             if (q >= nq) continue;
             float* o = b.expout + (size_t)c0_u * H + 32u * q + nn;
             const f32x4 z = {0.f, 0.f, 0.f, 0.f};
-            const f32x4 ax[2] = {d[h][0], z}, ay[2] = {d[h][1], z};
+            const f32x4 ax[2] = {d[h][0][0], NB == 2u ? d[h][0][NB - 1u] : z};
+            const f32x4 ay[2] = {d[h][1][0], NB == 2u ? d[h][1][NB - 1u] : z};
             tile_each(ax, nt_u, true, ln, [&](uint32_t m, float x) { gst(o + (size_t)m * H, x); });
             tile_each(ay, nt_u, true, ln, [&](uint32_t m, float x) { gst(o + (size_t)m * H + 16u, x); });
         }
         lds_barrier();  // every wave is done with the staged rows before the next unit's pieces
     }
+    return U;
 }
 
 // SMALL = true: the instantiation with the small-expert pipeline (launch_batched
@@ -2416,8 +2437,10 @@ __global__ void __launch_bounds__(kThreads) bdown_kernel(const DecodeArgs* __res
     const bool sh4 = (b.flags & kBatchShared4) != 0u;
     const uint32_t E = a.E + (sh4 ? 1u : 0u);  // experts in the pass table
     const uint8_t* const* stab = load_slot_tab(a, a.E, sh4, (const uint8_t**)dyn);
+    // (5-8 token units at the GLM shape only: elsewhere the kernel's general
+    // shape code leaves no registers for their second row block)
     const PassTab pt = load_pass_tab(b, E, a.K, (uint32_t*)(dyn + 8u * E), stab, cdiv(H / 32u, 16u),
-                                     SMALL ? kSmallT : 0u);
+                                     SMALL ? (GLM ? kSmallUpT : kSmallT) : 0u);
     const uint32_t Us = run_shared_down_wide<GLM>(a, b);
     if (Us) pipeline_drain();
     const uint32_t Ur = run_routed_down_wide<GLM>(a, b, pt, stab, E, Us % gridDim.x);
@@ -2456,7 +2479,14 @@ __global__ void __launch_bounds__(kThreads) bdown_kernel(const DecodeArgs* __res
     run_steps(k);
     if constexpr (SMALL) {
         pipeline_drain();
-        run_small_down<GLM>(a, b, stab, k.uoff + U);
+        // the small-expert list where the pass table was (4 (E + 1) of its
+        // 16 E + 8 bytes)
+        uint32_t* se = (uint32_t*)(dyn + 8u * (a.E + 1u));
+        const uint32_t u1 = run_small_down<GLM, 1>(a, b, stab, k.uoff + U, se);
+        if constexpr (GLM) {
+            pipeline_drain();
+            run_small_down<GLM, 2>(a, b, stab, k.uoff + U + u1, se);
+        }
     }
 }
 
