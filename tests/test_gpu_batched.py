@@ -265,9 +265,9 @@ def test_calls_longer_than_a_chunk(gpu):
 
 @pytest.mark.parametrize("T", [64, 256])
 def test_small_expert_units_equal_grouped_passes(gpu, monkeypatch, T):
-    """At the GLM shape experts of up to 8 tokens run their gate/up, and of up
-    to 4 their down, as streaming units instead of grouped passes (the
-    kernels' small-expert instantiations). WL_BATCHED_SMALL=0 keeps every
+    """At the GLM shape experts of up to 8 tokens run their gate/up and down
+    as streaming units instead of grouped passes (the kernels' small-expert
+    instantiations). WL_BATCHED_SMALL=0 keeps every
     expert in the grouped passes; both give the same outputs bit for bit,
     with the bench's Zipf bias (T = 64: most experts hold 1-4 tokens; 256:
     most hold 5-16)."""
