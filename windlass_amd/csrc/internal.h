@@ -288,11 +288,12 @@ enum : uint32_t {
     kBatchWideSharedUp = 8u,
     kBatchWideSharedDown = 16u
 };
-// Routed experts of at most kSmallT tokens run their gate/up and down
-// projections in the GEMM kernels' streaming pipelines (run_small_up,
-// run_small_down) when launch_batched takes those kernels' small-expert
-// instantiations (at the shapes they fit); their pass tables leave them out
-// of the other pipelines.
+// Routed experts of few tokens run their gate/up and down projections in the
+// GEMM kernels' streaming pipelines (run_small_up, run_small_down) when
+// launch_batched takes those kernels' small-expert instantiations (at the
+// shapes they fit): 1..kSmallT tokens in one MFMA row block, and at the GLM
+// shape kSmallT+1..kSmallUpT (moe_batched.hip) in two; their pass tables leave
+// them out of the other pipelines.
 constexpr uint32_t kSmallT = 4;
 // launch_batched phases: routing (norm .. scatter), the GEMMs, the combine.
 enum : uint32_t { kPhaseRoute = 1u, kPhaseGemm = 2u, kPhaseCombine = 4u, kPhaseAll = 7u };

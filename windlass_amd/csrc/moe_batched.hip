@@ -2578,10 +2578,11 @@ int launch_batched(const DecodeArgs* d_args, const BatchArgs& b, uint32_t H, uin
     const bool glm = H == 6144u && I == 2048u && SI == 2048u && K == 8u;
     // (decided below with the down kernel's small-expert instantiation)
     const void* up = nullptr;
-    // routed experts of at most kSmallT tokens: their down projection as
-    // bdown_kernel's streaming pipeline, for every batch the shape allows
-    // (measured at the GLM shape, per call: T = 64 -3 %, 128 -5 %, 512 -4 %,
-    // 1024 unchanged, where no expert is that small)
+    // routed experts of few tokens (up to kSmallT; kSmallUpT at the GLM
+    // shape): their down projection as bdown_kernel's streaming pipelines,
+    // for every batch the shape allows (measured at the GLM shape, per call,
+    // with the 1-4 token units: T = 64 -3 %, 128 -5 %, 512 -4 %, 1024
+    // unchanged, where no expert is that small)
     // (WL_BATCHED_SMALL=0 keeps every expert in the grouped passes: the
     // same results bit for bit, which a GPU test compares)
     const char* small_env = getenv("WL_BATCHED_SMALL");
