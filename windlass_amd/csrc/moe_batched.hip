@@ -1728,11 +1728,14 @@ __global__ void __launch_bounds__(kThreads) bup_kernel(const DecodeArgs* __restr
         SmallExp* se = (SmallExp*)(dyn + 8u * (a.E + 1u));
         uint32_t* wcnt = (uint32_t*)(se + a.E);
         const uint32_t K_ = GLM ? 8u : a.K;
-        uint32_t ns = small_list(a, b, stab, 1u, kSmallT, K_, se, wcnt);
-        run_small_up<1>(a, b, se, ns, stab, wcnt);
-        pipeline_drain();
-        ns = small_list(a, b, stab, kSmallT + 1u, kSmallUpT, K_, se, wcnt);
+        // the larger units first: the queue then evens the work-groups out
+        // with the smaller ones (the other order left the work-groups that
+        // took one of the last, larger units ending most of a unit late)
+        uint32_t ns = small_list(a, b, stab, kSmallT + 1u, kSmallUpT, K_, se, wcnt);
         run_small_up<2>(a, b, se, ns, stab, wcnt);
+        pipeline_drain();
+        ns = small_list(a, b, stab, 1u, kSmallT, K_, se, wcnt);
+        run_small_up<1>(a, b, se, ns, stab, wcnt);
         wq_release(b);
     }
 }
@@ -2482,11 +2485,13 @@ __global__ void __launch_bounds__(kThreads) bdown_kernel(const DecodeArgs* __res
         // the small-expert list where the pass table was (4 (E + 1) of its
         // 16 E + 8 bytes)
         uint32_t* se = (uint32_t*)(dyn + 8u * (a.E + 1u));
-        const uint32_t u1 = run_small_down<GLM, 1>(a, b, stab, k.uoff + U, se);
+        // the larger units first, as in the gate/up kernel
+        uint32_t u2 = 0;
         if constexpr (GLM) {
+            u2 = run_small_down<GLM, 2>(a, b, stab, k.uoff + U, se);
             pipeline_drain();
-            run_small_down<GLM, 2>(a, b, stab, k.uoff + U + u1, se);
         }
+        run_small_down<GLM, 1>(a, b, stab, k.uoff + U + u2, se);
     }
 }
 
